@@ -1,0 +1,141 @@
+/*
+ * trident_hip.h -- C ABI of libtrident_hip.so, the MI355X (gfx950) lossless IVF query path.
+ *
+ * Plain pointers and sizes only; no torch types.  Every device pointer may also be a
+ * mapped pinned-host address (xb_sorted in the out-of-core mode).  Streams are passed as
+ * `void*` holding a hipStream_t.  All entry points return TRIDENT_OK (0) or an error
+ * code; trident_last_error() gives the message of the calling thread's last failure.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   trident_search          launch_trident_v4_search, src/trident_v4_kernels.cu:1172-1604
+ *                           (modes 2 and 10), bound in Python at :1606-1627
+ *   trident_coarse_probe    at::addmm_out coarse GEMM + trident_topk_centroids_kernel,
+ *                           src/trident_v4_kernels.cu:1233-1259 and :68-162
+ *   trident_group_pairs     trident_counting_sort_pairs_kernel, :168-263 (+ split :1264-1276)
+ *   trident_sq8_bounds      the per-vector SQ8 lower/upper bound arithmetic of Stage Y / X,
+ *                           :626-676 and :731-773 (exposed for bound-rigour tests)
+ *   trident_host_alloc_mapped / trident_host_free / trident_host_device_pointer
+ *                           the pinned host buffer of the out-of-core engine,
+ *                           benchmarks/phase8_ooc_100m_4080.py:501-507 (torch pin_memory)
+ */
+#ifndef TRIDENT_HIP_H
+#define TRIDENT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TRIDENT_ABI_VERSION 1
+
+enum TridentStatus {
+    TRIDENT_OK = 0,
+    TRIDENT_ERR_INVALID_ARGUMENT = 1,
+    TRIDENT_ERR_UNSUPPORTED = 2,
+    TRIDENT_ERR_WORKSPACE_TOO_SMALL = 3,
+    TRIDENT_ERR_HIP = 4,
+    TRIDENT_ERR_OUT_OF_MEMORY = 5
+};
+
+enum TridentMode {
+    TRIDENT_MODE_CASCADE = 2,   /* Stage X (optional) + Stage Y SQ8 LB cascade + Stage Z exact refine */
+    TRIDENT_MODE_CM_EXACT = 10  /* cluster-major exhaustive exact scan (reference CM-FP32 route) */
+};
+
+/* Device-resident index layout produced by trident_amd.TridentV4Index
+ * (reference layout: benchmarks/phase4a_suite.py:95-278). */
+typedef struct TridentIndexView {
+    int32_t N, D, D_pad, nlist;
+    int32_t tile_size;       /* vectors per tile, a multiple of 64 (64 or 256) */
+    int32_t total_tiles;
+    int32_t num_blocks;      /* SQ8 dimension blocks; blk_bounds4 holds num_blocks + 1 */
+    int32_t per_cluster_sq8; /* 1: vmin/delta/eps_dim are [nlist, D_pad]; 0: [1, D_pad] */
+    const float* W_combined; /* [D, ldw], ldw = nlist + D_pad: [-2 C^T | R | 0] */
+    const float* b_combined; /* [ldw]: [|c|^2 | b | 0], rotation x -> x R + b */
+    double rot_sq_min;       /* lower bound on the squared singular values of R */
+    double rot_sq_max;       /* upper bound on the squared singular values of R */
+    const uint32_t* sq8_packed;      /* [total_tiles, D_pad / 4, tile_size] */
+    const int32_t* tile_orig_ids;    /* [total_tiles, tile_size], -1 padded */
+    const float* tile_r_minmax;      /* [total_tiles, 2] residual-norm band, or NULL */
+    const int32_t* cluster_tile_off; /* [nlist + 1] */
+    const int32_t* cluster_vec_off;  /* [nlist + 1] */
+    const float* xb_sorted;          /* [N, D] cluster-sorted base (device or mapped host) */
+    const int32_t* orig_ids_sorted;  /* [N] */
+    const float* vmin;               /* [nlist or 1, D_pad] */
+    const float* delta;              /* [nlist or 1, D_pad] */
+    const float* eps_dim;            /* [nlist or 1, D_pad] rigorous |x_rot - x_hat| bound */
+    const int32_t* blk_bounds4;      /* [num_blocks + 1], device, in units of 4 dims */
+} TridentIndexView;
+
+typedef struct TridentSearchParams {
+    int32_t mode;    /* TRIDENT_MODE_CASCADE or TRIDENT_MODE_CM_EXACT */
+    int32_t B;       /* queries */
+    int32_t K;       /* 1..128 */
+    int32_t nprobe;  /* 1..min(nlist, 512) */
+    int32_t ub_seed; /* TRIDENT_UB_SEED semantics: 0 off, 1 pass 1, 2 both passes */
+    int32_t use_l1;  /* residual-norm tile band (needs tile_r_minmax) */
+    int32_t p_init;  /* pass-1 probes per query; -1 = reference rule */
+    int32_t reserved;
+} TridentSearchParams;
+
+typedef struct TridentSearchOutputs {
+    float* topk_d;        /* [B, K] squared L2 distances (float32), +inf if missing */
+    int64_t* topk_i;      /* [B, K] original ids, -1 if missing */
+    int32_t* probe_cids;  /* [B, probe_ld] probed clusters in (d, cid) order, or NULL */
+    float* probe_dqcs;    /* [B, probe_ld] |q - c| of each probe, or NULL */
+    int32_t probe_ld;     /* row stride of probe_cids / probe_dqcs (>= nprobe) */
+    int32_t reserved;
+    float* tau_sq;        /* [B] pass-1 threshold (squared, rounded up), or NULL */
+    int64_t* stats;       /* [4] candidates, scanned dims, survivors, refined-inserted; or NULL */
+} TridentSearchOutputs;
+
+/* Bytes of scratch trident_search needs for batches up to max_B x max_nprobe x max_K. */
+size_t trident_workspace_bytes(const TridentIndexView* ix, int32_t max_B, int32_t max_nprobe,
+                               int32_t max_K);
+
+/* Full batched query: front end, two-pass scan, merge.  Asynchronous on `stream`. */
+int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, const float* xq,
+                   void* workspace, size_t workspace_bytes, const TridentSearchOutputs* out,
+                   void* stream);
+
+/* Front end only: float64 coarse distances and the exact (d, cid) top-nprobe per query.
+ * workspace: >= trident_workspace_bytes(ix, B, nprobe, 1) bytes. */
+int trident_coarse_probe(const TridentIndexView* ix, const float* xq, int32_t B, int32_t nprobe,
+                         void* workspace, size_t workspace_bytes, int32_t* probe_cids,
+                         float* probe_dqcs, int32_t probe_ld, void* stream);
+
+/* Group (cluster, query) pairs by cluster for the two passes.  probe_cids: [B, probe_ld].
+ * Outputs pass p (0, 1): pair_cids[p] / pair_qids[p] of length B * (p ? nprobe - p_init :
+ * p_init), and seg_off[p][nlist + 1] cluster segment offsets.  counts_ws: 2 * (nlist + 1)
+ * int32 scratch. */
+int trident_group_pairs(const int32_t* probe_cids, int32_t probe_ld, int32_t B, int32_t nprobe,
+                        int32_t p_init, int32_t nlist, int32_t* p1_cids, int32_t* p1_qids,
+                        int32_t* p2_cids, int32_t* p2_qids, int32_t* seg_off,
+                        int32_t* counts_ws, void* stream);
+
+/* The reference two-pass split rule for mode 2 / 10 (src/trident_v4_kernels.cu:1264-1276). */
+int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe);
+
+/* Per-candidate SQ8 bounds exactly as Stage Y (lb) and Stage X (ub) evaluate them, scaled to
+ * bound the canonical float64 distance: lb[i] <= d64(q, x) <= ub[i] for the n (query,
+ * sorted-position) pairs.  cids/qids/spos are device arrays of length n. */
+int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
+                       const int32_t* qids, const int32_t* cids, const int64_t* spos, int32_t n,
+                       void* workspace, size_t workspace_bytes, double* lb, double* ub,
+                       void* stream);
+
+/* Pinned, device-mapped host memory for the out-of-core base. */
+int trident_host_alloc_mapped(size_t bytes, void** host_ptr);
+int trident_host_free(void* host_ptr);
+int trident_host_device_pointer(void* host_ptr, void** device_ptr);
+
+const char* trident_last_error(void);
+int trident_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIDENT_HIP_H */

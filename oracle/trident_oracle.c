@@ -1,0 +1,194 @@
+/*
+ * trident_oracle.c -- TEST INFRASTRUCTURE ONLY (the parity checker, never the product).
+ *
+ * CPU restatement of the reference's lossless-IVF query semantics, used by tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg.  The product path
+ * (trident_amd/) never links, loads or calls anything in this directory.
+ *
+ * Functions and the reference behaviour each one restates:
+ *
+ *   oracle_dist_f64        canonical float64 squared L2: t = (double)x_d - (double)q_d,
+ *                          acc = fma(t, t, acc) for d = 0..D-1 in order.  The float64
+ *                          audit computes sum((x64 - q64)^2)
+ *                          (benchmarks/phase3a_lossless_audit.py:56-58,
+ *                          benchmarks/phase4b_suite.py:211-213); fixing the summation
+ *                          order makes the GPU and this oracle bit-identical.
+ *   oracle_coarse_probe    float64 coarse distances to every centroid, nprobe smallest
+ *                          ordered by (d, cid): benchmarks/phase4b_suite.py:190-195
+ *                          (float64 coarse step) with the cid tie-break of
+ *                          src/trident_v4_kernels.cu:117-161.
+ *   oracle_ivf_exact       exhaustive float64 IVF over the probed lists, top-K by
+ *                          (d, id) lexicographic: benchmarks/phase4b_suite.py:197-219,
+ *                          tie-break of benchmarks/phase3a_lossless_audit.py:62 and
+ *                          insert_topk (src/trident_v4_kernels.cu:19-60).
+ *   oracle_ivfflat_f32     the reference CPU baseline omp_cpu_ivfflat_f32
+ *                          (benchmarks/phase8_ooc_100m_4080.py:141-204): FP32 direct
+ *                          sum with an OpenMP SIMD reduction and (d, id) insertion.
+ *
+ * Parity pins: see the checks in tests/test_oracle.py (brute force in numpy on tiny
+ * inputs, committed golden fixtures, integer-valued data where every summation order is
+ * exact, and planted-mistake checks).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+double oracle_dist_f64(const float* x, const float* q, int D) {
+    double acc = 0.0;
+    for (int d = 0; d < D; ++d) {
+        double t = (double)x[d] - (double)q[d];
+        acc = fma(t, t, acc);
+    }
+    return acc;
+}
+
+/* (d, id) strictly-less, the ordering contract of insert_topk. */
+static inline int lex_less(double da, int64_t ia, double db, int64_t ib) {
+    return (da < db) || (da == db && ia < ib);
+}
+
+/* Insert (d, id) into a list sorted ascending by (d, id) of length K; the list is
+ * pre-filled with (+inf, INT64_MAX) sentinels. */
+static inline void insert_sorted(double* ld, int64_t* li, int K, double d, int64_t id) {
+    if (!lex_less(d, id, ld[K - 1], li[K - 1])) return;
+    int j = K - 1;
+    while (j > 0 && lex_less(d, id, ld[j - 1], li[j - 1])) {
+        ld[j] = ld[j - 1];
+        li[j] = li[j - 1];
+        --j;
+    }
+    ld[j] = d;
+    li[j] = id;
+}
+
+int oracle_coarse_probe(const float* xq, int64_t B, int D, const float* centroids, int nlist,
+                        int nprobe, int32_t* out_cids, double* out_d, int nthreads) {
+    if (nprobe < 1 || nprobe > nlist || D < 1) return -1;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        double* ld = (double*)malloc(sizeof(double) * (size_t)nprobe);
+        int64_t* li = (int64_t*)malloc(sizeof(int64_t) * (size_t)nprobe);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 4)
+#endif
+        for (int64_t q = 0; q < B; ++q) {
+            const float* qv = xq + q * (int64_t)D;
+            for (int j = 0; j < nprobe; ++j) { ld[j] = INFINITY; li[j] = INT64_MAX; }
+            for (int c = 0; c < nlist; ++c) {
+                double d = oracle_dist_f64(centroids + (int64_t)c * D, qv, D);
+                insert_sorted(ld, li, nprobe, d, c);
+            }
+            for (int j = 0; j < nprobe; ++j) {
+                out_cids[q * nprobe + j] = (int32_t)li[j];
+                if (out_d) out_d[q * nprobe + j] = ld[j];
+            }
+        }
+        free(ld);
+        free(li);
+    }
+    return 0;
+}
+
+int oracle_ivf_exact(const float* xq, int64_t B, int D, const int32_t* probe_cids, int nprobe,
+                     const int32_t* vec_off, const float* xb_sorted, const int32_t* orig_ids,
+                     int K, double* out_d, int64_t* out_i, int nthreads) {
+    if (K < 1 || D < 1) return -1;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        double* ld = (double*)malloc(sizeof(double) * (size_t)K);
+        int64_t* li = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int64_t q = 0; q < B; ++q) {
+            const float* qv = xq + q * (int64_t)D;
+            for (int j = 0; j < K; ++j) { ld[j] = INFINITY; li[j] = INT64_MAX; }
+            for (int p = 0; p < nprobe; ++p) {
+                int32_t c = probe_cids[q * nprobe + p];
+                if (c < 0) continue;
+                for (int64_t v = vec_off[c]; v < vec_off[c + 1]; ++v) {
+                    double d = oracle_dist_f64(xb_sorted + v * D, qv, D);
+                    insert_sorted(ld, li, K, d, (int64_t)orig_ids[v]);
+                }
+            }
+            for (int j = 0; j < K; ++j) {
+                int valid = li[j] != INT64_MAX;
+                out_d[q * K + j] = valid ? ld[j] : INFINITY;
+                out_i[q * K + j] = valid ? li[j] : -1;
+            }
+        }
+        free(ld);
+        free(li);
+    }
+    return 0;
+}
+
+int oracle_ivfflat_f32(const float* xq, int64_t B, int D, const int32_t* probe_cids, int nprobe,
+                       const int32_t* vec_off, const float* xb_sorted, const int32_t* orig_ids,
+                       int K, float* out_d, int64_t* out_i, int nthreads) {
+    if (K < 1 || D < 1) return -1;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel for schedule(dynamic, 1)
+#endif
+    for (int64_t q = 0; q < B; ++q) {
+        const float* qr = xq + q * (int64_t)D;
+        float* td = out_d + q * K;
+        int64_t* ti = out_i + q * K;
+        for (int j = 0; j < K; ++j) { td[j] = INFINITY; ti[j] = -1; }
+        for (int p = 0; p < nprobe; ++p) {
+            int32_t c = probe_cids[q * nprobe + p];
+            if (c < 0) continue;
+            for (int64_t v = vec_off[c]; v < vec_off[c + 1]; ++v) {
+                const float* br = xb_sorted + v * D;
+                float sum = 0.0f;
+#ifdef _OPENMP
+#pragma omp simd reduction(+ : sum)
+#endif
+                for (int d = 0; d < D; ++d) {
+                    float diff = qr[d] - br[d];
+                    sum += diff * diff;
+                }
+                int64_t id = (int64_t)orig_ids[v];
+                /* insertion with the (d, id) tie-break; empty slots hold (+inf, -1) */
+                if (sum < td[K - 1] || (sum == td[K - 1] && id < ti[K - 1])) {
+                    td[K - 1] = sum;
+                    ti[K - 1] = id;
+                    for (int j = K - 1; j > 0; --j) {
+                        int swap = td[j] < td[j - 1] || (td[j] == td[j - 1] && ti[j] < ti[j - 1]);
+                        if (!swap) break;
+                        float tdv = td[j]; td[j] = td[j - 1]; td[j - 1] = tdv;
+                        int64_t tiv = ti[j]; ti[j] = ti[j - 1]; ti[j - 1] = tiv;
+                    }
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* Canonical float64 distances for an explicit list of (query, sorted-position) pairs. */
+int oracle_pair_dists(const float* xq, int D, const float* xb_sorted, const int32_t* qids,
+                      const int64_t* spos, int64_t n, double* out_d) {
+    for (int64_t i = 0; i < n; ++i)
+        out_d[i] = oracle_dist_f64(xb_sorted + spos[i] * D, xq + (int64_t)qids[i] * D, D);
+    return 0;
+}
+
+int oracle_max_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}

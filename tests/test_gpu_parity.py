@@ -1,0 +1,188 @@
+"""GPU parity: the HIP path against the float64 CPU oracle on the same seeded inputs.
+
+Bar: ids identical on every query and float32 distances equal to the oracle's float64 distances
+rounded to float32 (hence within 1e-5 relative).  Sizes keep the oracle to seconds.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import assert_exact, build_index, oracle_search, run_search
+from trident_amd import _lib, datagen, ext
+
+pytestmark = pytest.mark.gpu
+
+
+def _q(xq, dev):
+    return torch.as_tensor(np.ascontiguousarray(xq, np.float32)).to(dev).contiguous()
+
+
+@pytest.fixture(scope="module")
+def gmm(dev):
+    xb, xq = datagen.cfg1(N=30_000, D=128, B=200, n_centers=64, seed=1)
+    b = build_index(xb, 96, dev, max_batch=512)
+    return b, xq.numpy()
+
+
+@pytest.fixture(scope="module")
+def hist(dev):
+    xb, xq = datagen.cfg2(N=40_000, D=128, B=200, n_centers=128, seed=2)
+    b = build_index(xb, 128, dev, max_batch=512)
+    return b, xq.numpy()
+
+
+@pytest.fixture(scope="module")
+def aniso(dev):
+    xb, xq = datagen.cfg3(N=12_000, D=960, B=64, n_centers=64, seed=3)
+    b = build_index(xb, 64, dev, max_batch=128)
+    return b, xq.numpy()
+
+
+@pytest.fixture(scope="module")
+def norm96(dev):
+    xb, xq = datagen.cfg4(N=40_000, D=96, B=200, n_centers=256, seed=4)
+    b = build_index(xb, 256, dev, max_batch=512)
+    return b, xq.numpy()
+
+
+def test_coarse_probe_matches_oracle(gmm, dev):
+    b, xq = gmm
+    for nprobe in (1, 7, 16, 96):
+        b.ix.search(_q(xq, dev), nprobe, mode=10, k=10)
+        torch.cuda.synchronize()
+        got = b.ix.probe_cids_buf[: len(xq), :nprobe].cpu().numpy()
+        ref, _ = O.coarse_probe(xq, b.centroids_idx, nprobe)
+        assert np.array_equal(got, ref), f"nprobe={nprobe}"
+
+
+@pytest.mark.parametrize("mode", [10, 2])
+def test_gmm_k10(gmm, dev, mode):
+    b, xq = gmm
+    _, rd, ri = oracle_search(b, xq, 16, 10)
+    d, i = run_search(b, _q(xq, dev), 16, 10, mode=mode)
+    assert_exact(d, i, rd, ri, f"gmm mode={mode}")
+
+
+@pytest.mark.parametrize("ub", [0, 1, 2])
+def test_hist_ub_seed(hist, dev, ub):
+    b, xq = hist
+    _, rd, ri = oracle_search(b, xq, 24, 10)
+    d, i = run_search(b, _q(xq, dev), 24, 10, mode=2, ub=ub)
+    assert_exact(d, i, rd, ri, f"hist ub={ub}")
+
+
+@pytest.mark.parametrize("K", [1, 10, 50, 100, 128])
+def test_k_sweep_norm96(norm96, dev, K):
+    b, xq = norm96
+    _, rd, ri = oracle_search(b, xq, 16, K)
+    for mode in (2, 10):
+        d, i = run_search(b, _q(xq, dev), 16, K, mode=mode, ub=1)
+        assert_exact(d, i, rd, ri, f"norm96 K={K} mode={mode}")
+
+
+@pytest.mark.parametrize("K", [10, 100])
+def test_d960(aniso, dev, K):
+    b, xq = aniso
+    _, rd, ri = oracle_search(b, xq, 12, K)
+    for mode, ub in ((2, 0), (2, 1), (10, 0)):
+        d, i = run_search(b, _q(xq, dev), 12, K, mode=mode, ub=ub)
+        assert_exact(d, i, rd, ri, f"d960 K={K} mode={mode} ub={ub}")
+
+
+@pytest.mark.parametrize("nprobe", [1, 2, 3, 17, 128])
+def test_pass_split_edges(hist, dev, nprobe):
+    """nprobe 1 (single pass), 2 (pass 2 empty), 3 / 17 (p_init 2 / 3), all lists."""
+    b, xq = hist
+    _, rd, ri = oracle_search(b, xq[:50], nprobe, 10)
+    d, i = run_search(b, _q(xq[:50], dev), nprobe, 10, mode=2, ub=1)
+    assert_exact(d, i, rd, ri, f"nprobe={nprobe}")
+
+
+def test_single_query(hist, dev):
+    b, xq = hist
+    for K in (1, 10, 20):
+        _, rd, ri = oracle_search(b, xq[:1], 8, K)
+        d, i = run_search(b, _q(xq[:1], dev), 8, K, mode=2)
+        assert_exact(d, i, rd, ri, f"B=1 K={K}")
+
+
+def test_ties_duplicates_and_short_lists(dev):
+    """Integer data with duplicated rows (exact distance ties broken by id), a degenerate
+    dimension, empty lists and lists shorter than K (missing slots = (+inf, -1))."""
+    rng = np.random.default_rng(5)
+    base = rng.integers(0, 4, size=(600, 40)).astype(np.float32)
+    base[:, 7] = 3.0                                   # degenerate dimension
+    xb = np.concatenate([base, base[:300], base[:100]], 0)
+    nlist = 24
+    cen = rng.integers(0, 4, size=(nlist, 40)).astype(np.float32)
+    lid = np.argmin(((xb[:, None, :] - cen[None]) ** 2).sum(-1), 1).astype(np.int32)
+    lid[lid == 5] = 6                                  # list 5 empty
+    cen[9] = cen[2]                                    # duplicated centroid: coarse tie
+    xq = np.concatenate([rng.integers(0, 4, size=(60, 40)), base[:20]], 0).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=128)
+    for K, nprobe in ((10, 4), (64, 3), (128, 24)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        for mode, ub in ((2, 0), (2, 2), (10, 0)):
+            d, i = run_search(b, _q(xq, dev), nprobe, K, mode=mode, ub=ub)
+            assert_exact(d, i, rd, ri, f"ties K={K} nprobe={nprobe} mode={mode} ub={ub}")
+
+
+def test_stats_counters(hist, dev):
+    b, xq = hist
+    nprobe = 24
+    st = torch.zeros(4, dtype=torch.int64, device=dev)
+    run_search(b, _q(xq, dev), nprobe, 10, mode=2, stats=st)
+    tot, dims, surv, ins = st.tolist()
+    cids, _ = O.coarse_probe(xq, b.centroids_idx, nprobe)
+    sizes = np.diff(b.vec_off)
+    assert tot == int(sizes[cids].sum())
+    assert 0 < surv <= tot and ins <= surv
+    assert tot * 32 <= dims <= tot * b.ix.D_pad
+
+
+def test_sq8_bounds_bracket_exact_distance(aniso, hist, dev):
+    """lb <= d64 <= ub for every (query, candidate) of the probed lists (Stage Y / X rigour)."""
+    for b, xq in (aniso, hist):
+        xq = xq[:8]
+        cids, _ = O.coarse_probe(xq, b.centroids_idx, 4)
+        qids, pc, spos = [], [], []
+        for q in range(len(xq)):
+            for c in cids[q]:
+                for s in range(b.vec_off[c], b.vec_off[c + 1]):
+                    qids.append(q), pc.append(c), spos.append(s)
+        qids = np.array(qids, np.int32)
+        pc = np.array(pc, np.int32)
+        spos = np.array(spos, np.int64)
+        d64 = O.pair_dists(xq, b.xb_sorted, qids, spos)
+        ix = b.ix
+        view = ext.make_index_view(
+            N=ix.N, D=ix.D, D_pad=ix.D_pad, nlist=ix.nlist, tile_size=ix.tile_size,
+            per_cluster_sq8=ix.per_cluster_sq8, W_combined=ix.W_combined, b_combined=ix.b_combined,
+            rot_sq_min=ix.rot_sq_min, rot_sq_max=ix.rot_sq_max, sq8_packed=ix.sq8_packed,
+            tile_orig_ids=ix.tile_orig_ids, tile_r_minmax=ix.tile_r_minmax,
+            cluster_tile_off=ix.cluster_tile_off, cluster_vec_off=ix.storage.cluster_vec_off,
+            xb_sorted=ix.storage.xb_sorted, orig_ids_sorted=ix.storage.orig_ids_sorted,
+            vmin=ix.vmin_pad, delta=ix.delta_pad, eps_dim=ix.eps_pad, blk_bounds4=ix.blk_bounds4)
+        L = _lib.lib()
+        nbytes = L.trident_workspace_bytes(ctypes.byref(view), len(xq), 1, 1)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        tq, tc, ts = (torch.as_tensor(a).to(dev) for a in (qids, pc, spos))
+        lb = torch.empty(len(qids), dtype=torch.float64, device=dev)
+        ub = torch.empty_like(lb)
+        xqd = _q(xq, dev)
+        rc = L.trident_sq8_bounds(ctypes.byref(view), ctypes.c_void_p(xqd.data_ptr()), len(xq),
+                                  ctypes.c_void_p(tq.data_ptr()), ctypes.c_void_p(tc.data_ptr()),
+                                  ctypes.c_void_p(ts.data_ptr()), len(qids), ctypes.c_void_p(ws.data_ptr()),
+                                  ctypes.c_size_t(nbytes), ctypes.c_void_p(lb.data_ptr()),
+                                  ctypes.c_void_p(ub.data_ptr()),
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        _lib.check(rc, "trident_sq8_bounds")
+        torch.cuda.synchronize()
+        lb, ub = lb.cpu().numpy(), ub.cpu().numpy()
+        assert (lb <= d64).all(), f"lb > d64 by {(lb - d64).max()}"
+        assert (ub >= d64).all(), f"ub < d64 by {(d64 - ub).max()}"
+        # the bounds must also be useful: most of the distance is captured
+        assert np.median(lb / d64) > 0.5 and np.median(ub / d64) < 2.0

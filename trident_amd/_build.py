@@ -1,0 +1,63 @@
+"""Builds libtrident_hip.so in-tree with hipcc for gfx950.
+
+Each .hip source is compiled to an object in trident_amd/_build/ and linked into
+trident_amd/libtrident_hip.so.  Flags:
+  --offload-arch=gfx950                      MI355X only
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                                             no packed FP32 (v_pk_*_f32) instructions
+  -ffp-contract=off                          every fma in the kernels is written explicitly, so
+                                             the canonical float64 distance is reproduced bit
+                                             for bit by the CPU restatement
+"""
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+OUT_DIR = os.path.join(PKG, "_build")
+LIB = os.path.join(PKG, "libtrident_hip.so")
+SOURCES = ["frontend.hip", "scan.hip", "capi.hip"]
+HEADERS = ["common.hpp", "kernels.hpp"]
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"), "-Wall", "-Wno-unused-function",
+]
+
+
+def _compile(src: str, obj: str) -> None:
+    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    subprocess.run(cmd, check=True)
+
+
+def build(force: bool = True, jobs: int = 3) -> str:
+    """Compile every source (in parallel) and link the shared library; returns its path."""
+    os.makedirs(OUT_DIR, exist_ok=True)
+    deps = [os.path.join(CSRC, h) for h in HEADERS] + [os.path.join(ROOT, "include", "trident_hip.h")]
+    newest_dep = max(os.path.getmtime(d) for d in deps)
+    procs, objs = [], []
+    for s in SOURCES:
+        src = os.path.join(CSRC, s)
+        obj = os.path.join(OUT_DIR, s.replace(".hip", ".o"))
+        objs.append(obj)
+        fresh = (os.path.exists(obj) and os.path.getmtime(obj) >= max(os.path.getmtime(src), newest_dep))
+        if force or not fresh:
+            procs.append((s, subprocess.Popen([HIPCC, *CFLAGS, "-c", src, "-o", obj])))
+        while len([p for _, p in procs if p.poll() is None]) >= jobs:
+            procs[[p.poll() is None for _, p in procs].index(True)][1].wait()
+    for name, p in procs:
+        if p.wait() != 0:
+            raise RuntimeError(f"hipcc failed on {name}")
+    tmp = LIB + ".tmp"
+    subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], check=True)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(force="--lazy" not in sys.argv))

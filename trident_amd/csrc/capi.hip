@@ -1,0 +1,494 @@
+// C ABI of libtrident_hip.so (declared in include/trident_hip.h): argument validation,
+// workspace carving and the launch sequence of one batched lossless IVF query.
+//
+// Launch sequence of trident_search (reference launch_trident_v4_search,
+// src/trident_v4_kernels.cu:1172-1604):
+//   prep_queries -> coarse_dist -> select_probes           (front end, :1233-1259)
+//   p_init rule                                            (:1264-1276)
+//   fill / count / scan / scatter pairs                    (:1279-1289)
+//   pass 1: fill cand_cnt, pair_scan, merge  -> tau        (:1451-1512)
+//   pass 2: fill cand_cnt, pair_scan(tau), merge -> top-K  (:1514-1575)
+// Every launch goes on the caller's stream; no allocation, no host synchronisation.
+// Counters are cleared with a fill kernel (no memset nodes), so the sequence can be
+// captured in a graph.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/trident_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace trident;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(TRIDENT_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return TRIDENT_OK;
+}
+
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t x) { return (x + kAlign - 1) & ~(kAlign - 1); }
+
+struct Carver {
+    char* base;
+    size_t off = 0;
+    template <typename T>
+    T* take(size_t count) {
+        T* p = base ? reinterpret_cast<T*>(base + off) : nullptr;
+        off = align_up(off + count * sizeof(T));
+        return p;
+    }
+};
+
+struct Workspace {
+    double* xq64;
+    double* xrot64;
+    double* qerr;
+    double* cd64;
+    int32_t* probe_cids;
+    float* probe_dqcs;
+    int32_t* counts;
+    int32_t* seg_off;
+    int32_t* cursor;
+    int32_t* pair_cids;
+    int32_t* pair_qids;
+    float* pair_dqcs;
+    uint64_t* cand_key;
+    int32_t* cand_id;
+    int32_t* cand_cnt;
+    uint64_t* list_key;
+    int32_t* list_id;
+    double* tau64;
+    size_t bytes;
+};
+
+Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
+    Carver c{static_cast<char*>(base)};
+    Workspace w;
+    const int64_t KP = K <= 64 ? 64 : 128;
+    const int64_t cap = nprobe * K;
+    w.xq64 = c.take<double>(B * ix->D);
+    w.xrot64 = c.take<double>(B * ix->D_pad);
+    w.qerr = c.take<double>(B * ix->D_pad);
+    w.cd64 = c.take<double>(B * ix->nlist);
+    w.probe_cids = c.take<int32_t>(B * nprobe);
+    w.probe_dqcs = c.take<float>(B * nprobe);
+    w.counts = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
+    w.seg_off = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
+    w.cursor = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
+    w.pair_cids = c.take<int32_t>(B * nprobe);
+    w.pair_qids = c.take<int32_t>(B * nprobe);
+    w.pair_dqcs = c.take<float>(B * nprobe);
+    w.cand_key = c.take<uint64_t>(B * cap);
+    w.cand_id = c.take<int32_t>(B * cap);
+    w.cand_cnt = c.take<int32_t>(B);
+    w.list_key = c.take<uint64_t>(B * KP);
+    w.list_id = c.take<int32_t>(B * KP);
+    w.tau64 = c.take<double>(B);
+    w.bytes = c.off;
+    return w;
+}
+
+int validate_index(const TridentIndexView* ix) {
+    if (!ix) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "index view is NULL");
+    if (ix->N < 0 || ix->D < 1 || ix->nlist < 1)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad index sizes N=%d D=%d nlist=%d", ix->N,
+                    ix->D, ix->nlist);
+    if (ix->D_pad < ix->D || ix->D_pad % 32 != 0)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "D_pad=%d must be a multiple of 32 >= D=%d",
+                    ix->D_pad, ix->D);
+    if (ix->tile_size < 64 || ix->tile_size % 64 != 0)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "tile_size=%d must be a positive multiple of 64",
+                    ix->tile_size);
+    if (ix->num_blocks < 1 || ix->num_blocks > 64)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "num_blocks=%d outside [1, 64]", ix->num_blocks);
+    if (!ix->W_combined || !ix->b_combined || !ix->cluster_vec_off || !ix->cluster_tile_off ||
+        !ix->xb_sorted || !ix->tile_orig_ids)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "index view has NULL tensors");
+    if (!(ix->rot_sq_min > 0.0) || !(ix->rot_sq_max >= ix->rot_sq_min))
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad rotation bounds [%g, %g]", ix->rot_sq_min,
+                    ix->rot_sq_max);
+    if ((int64_t)ix->nlist * 8 > 150 * 1024)
+        return fail(TRIDENT_ERR_UNSUPPORTED, "nlist=%d exceeds the LDS probe selector", ix->nlist);
+    return TRIDENT_OK;
+}
+
+int validate_cascade_index(const TridentIndexView* ix) {
+    if (!ix->sq8_packed || !ix->vmin || !ix->delta || !ix->eps_dim || !ix->blk_bounds4)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "cascade route needs the SQ8 tensors");
+    return TRIDENT_OK;
+}
+
+double rho_of(int D_pad) { return (double)(D_pad + 4) * 0x1p-24; }
+
+ScanArgs make_scan_args(const TridentIndexView* ix, const Workspace& w, int K, int64_t cap,
+                        int use_l1, int64_t* stats) {
+    ScanArgs a{};
+    a.sq8 = ix->sq8_packed;
+    a.tile_oids = ix->tile_orig_ids;
+    a.tile_rmm = ix->tile_r_minmax;
+    a.tile_off = ix->cluster_tile_off;
+    a.vec_off = ix->cluster_vec_off;
+    a.xb = ix->xb_sorted;
+    a.vmin = ix->vmin;
+    a.delta = ix->delta;
+    a.eps = ix->eps_dim;
+    a.blk = ix->blk_bounds4;
+    a.D = ix->D;
+    a.D_pad = ix->D_pad;
+    a.T = ix->tile_size;
+    a.nb = ix->num_blocks;
+    a.per_cluster = ix->per_cluster_sq8;
+    a.use_l1 = use_l1;
+    a.xq64 = w.xq64;
+    a.xrot64 = w.xrot64;
+    a.qerr = w.qerr;
+    a.cand_key = w.cand_key;
+    a.cand_id = w.cand_id;
+    a.cand_cnt = w.cand_cnt;
+    a.cap = (int)cap;
+    a.K = K;
+    a.stats = reinterpret_cast<unsigned long long*>(stats);
+    const double rho = rho_of(ix->D_pad);
+    a.lb_scale = ix->rot_sq_max * (1.0 + rho) * (1.0 + 1e-12);
+    a.ub_scale = (1.0 + rho) * (1.0 + 1e-12) / ix->rot_sq_min;
+    return a;
+}
+
+template <int KP, bool CASCADE, bool UB>
+int launch_scan(const ScanArgs& a, hipStream_t st) {
+    if (a.M <= 0) return TRIDENT_OK;
+    const size_t dyn = scan_dyn_lds_bytes(a.D, a.D_pad);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)pair_scan_kernel<KP, CASCADE, UB>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e != hipSuccess)
+            return fail(TRIDENT_ERR_HIP, "hipFuncSetAttribute(pair_scan): %s", hipGetErrorString(e));
+        attr_set = true;
+    }
+    const unsigned nx = (unsigned)((a.M + 7) / 8);
+    pair_scan_kernel<KP, CASCADE, UB><<<dim3(nx * 8), dim3(kBlock), dyn, st>>>(a);
+    return check_launch("pair_scan_kernel");
+}
+
+template <int KP>
+int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
+    if (!cascade) return launch_scan<KP, false, false>(a, st);
+    if (ub) return launch_scan<KP, true, true>(a, st);
+    return launch_scan<KP, true, false>(a, st);
+}
+
+int launch_merge(const MergeArgs& m, int KP, hipStream_t st) {
+    const unsigned grid = (unsigned)((m.B + kWavesPerBlock - 1) / kWavesPerBlock);
+    if (KP == 64)
+        merge_kernel<64><<<grid, kBlock, 0, st>>>(m);
+    else
+        merge_kernel<128><<<grid, kBlock, 0, st>>>(m);
+    return check_launch("merge_kernel");
+}
+
+int fill(int32_t* p, int32_t v, int64_t n, hipStream_t st) {
+    if (n <= 0) return TRIDENT_OK;
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    fill_i32_kernel<<<(unsigned)blocks, 256, 0, st>>>(p, v, n);
+    return check_launch("fill_i32_kernel");
+}
+
+// Writes the probes to w.probe_cids / w.probe_dqcs (row stride nprobe) and, when non-null,
+// mirrors them into the caller's probe_cids / probe_dqcs (row stride ld).
+int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe, bool rotate,
+                  const Workspace& w, int32_t* probe_cids, float* probe_dqcs, int ld,
+                  hipStream_t st) {
+    const int ldw = ix->nlist + ix->D_pad;
+    const int cols = std::max(ix->D, rotate ? ix->D_pad : 0);
+    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 3) / 4), dim3(64, 4), 0, st>>>(
+        xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
+        w.xrot64, w.qerr, rotate ? 1 : 0);
+    int rc = check_launch("prep_queries_kernel");
+    if (rc) return rc;
+    coarse_dist_kernel<<<dim3((ix->nlist + 63) / 64, (B + 31) / 32), kBlock, 0, st>>>(
+        w.xq64, B, ix->D, ix->W_combined, ldw, ix->nlist, w.cd64);
+    if ((rc = check_launch("coarse_dist_kernel"))) return rc;
+    const size_t dyn = (size_t)ix->nlist * sizeof(uint64_t);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)select_probes_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 150 * 1024);
+        if (e != hipSuccess)
+            return fail(TRIDENT_ERR_HIP, "hipFuncSetAttribute(select): %s", hipGetErrorString(e));
+        attr_set = true;
+    }
+    select_probes_kernel<<<B, kBlock, dyn, st>>>(w.cd64, ix->nlist, nprobe, w.probe_cids,
+                                                 w.probe_dqcs, nprobe, probe_cids, probe_dqcs,
+                                                 ld);
+    return check_launch("select_probes_kernel");
+}
+
+int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int B, int nprobe,
+                int p_init, int nlist, int32_t* counts, int32_t* seg_off, int32_t* cursor,
+                int32_t* p1c, int32_t* p1q, float* p1d, int32_t* p2c, int32_t* p2q, float* p2d,
+                hipStream_t st) {
+    int rc = fill(counts, 0, 2 * ((int64_t)nlist + 1), st);
+    if (rc) return rc;
+    const int64_t total = (int64_t)B * nprobe;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    count_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, ld, B, nprobe, p_init, nlist, counts);
+    if ((rc = check_launch("count_pairs_kernel"))) return rc;
+    scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
+    if ((rc = check_launch("scan_pairs_kernel"))) return rc;
+    scatter_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, probe_dqcs, ld, B, nprobe, p_init,
+                                                 nlist, cursor, p1c, p1q, p1d, p2c, p2q, p2d);
+    return check_launch("scatter_pairs_kernel");
+}
+
+}  // namespace
+
+extern "C" {
+
+int trident_abi_version(void) { return TRIDENT_ABI_VERSION; }
+
+const char* trident_last_error(void) { return g_last_error.c_str(); }
+
+int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe) {
+    if (mode != TRIDENT_MODE_CASCADE) return 0;
+    if (nprobe <= 1) return 0;
+    if (B == 1 && K <= 10) return 1;
+    if (nprobe <= 16) return 2;
+    return 3;
+}
+
+size_t trident_workspace_bytes(const TridentIndexView* ix, int32_t max_B, int32_t max_nprobe,
+                               int32_t max_K) {
+    if (!ix || max_B < 0 || max_nprobe < 1 || max_K < 1) return 0;
+    return carve(ix, nullptr, max_B, max_nprobe, max_K).bytes;
+}
+
+int trident_coarse_probe(const TridentIndexView* ix, const float* xq, int32_t B, int32_t nprobe,
+                         void* workspace, size_t workspace_bytes, int32_t* probe_cids,
+                         float* probe_dqcs, int32_t probe_ld, void* stream) {
+    int rc = validate_index(ix);
+    if (rc) return rc;
+    if (B < 0 || nprobe < 1 || nprobe > ix->nlist || nprobe > 512 || probe_ld < nprobe ||
+        !probe_cids || (B > 0 && !xq))
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad probe arguments B=%d nprobe=%d ld=%d", B,
+                    nprobe, probe_ld);
+    if (B == 0) return TRIDENT_OK;
+    Workspace w = carve(ix, workspace, B, nprobe, 1);
+    if (!workspace || workspace_bytes < w.bytes)
+        return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu < %zu bytes", workspace_bytes,
+                    w.bytes);
+    return run_front_end(ix, xq, B, nprobe, false, w, probe_cids, probe_dqcs, probe_ld,
+                         static_cast<hipStream_t>(stream));
+}
+
+int trident_group_pairs(const int32_t* probe_cids, int32_t probe_ld, int32_t B, int32_t nprobe,
+                        int32_t p_init, int32_t nlist, int32_t* p1_cids, int32_t* p1_qids,
+                        int32_t* p2_cids, int32_t* p2_qids, int32_t* seg_off,
+                        int32_t* counts_ws, void* stream) {
+    if (B < 0 || nprobe < 1 || p_init < 0 || p_init > nprobe || nlist < 1 || probe_ld < nprobe ||
+        !seg_off || !counts_ws)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad group_pairs arguments");
+    if (B == 0) return TRIDENT_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // cursor reuses counts_ws after the scan has consumed the counts.
+    int rc = fill(counts_ws, 0, 2 * ((int64_t)nlist + 1), st);
+    if (rc) return rc;
+    const int64_t total = (int64_t)B * nprobe;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    count_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, probe_ld, B, nprobe, p_init, nlist,
+                                               counts_ws);
+    if ((rc = check_launch("count_pairs_kernel"))) return rc;
+    scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts_ws, nlist, seg_off, seg_off);
+    if ((rc = check_launch("scan_pairs_kernel"))) return rc;
+    // seg_off now doubles as the cursor; restore it from the counts afterwards.
+    scatter_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, nullptr, probe_ld, B, nprobe, p_init,
+                                                 nlist, seg_off, p1_cids, p1_qids, nullptr,
+                                                 p2_cids, p2_qids, nullptr);
+    if ((rc = check_launch("scatter_pairs_kernel"))) return rc;
+    scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts_ws, nlist, seg_off, seg_off);
+    return check_launch("scan_pairs_kernel");
+}
+
+int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, const float* xq,
+                   void* workspace, size_t workspace_bytes, const TridentSearchOutputs* out,
+                   void* stream) {
+    int rc = validate_index(ix);
+    if (rc) return rc;
+    if (!sp || !out) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "params/outputs are NULL");
+    const int mode = sp->mode, B = sp->B, K = sp->K, nprobe = sp->nprobe;
+    if (mode != TRIDENT_MODE_CASCADE && mode != TRIDENT_MODE_CM_EXACT)
+        return fail(TRIDENT_ERR_UNSUPPORTED,
+                    "mode %d is not supported (2 = cascade, 10 = cluster-major exact)", mode);
+    if (B < 0) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "B=%d", B);
+    if (K < 1 || K > 128) return fail(TRIDENT_ERR_UNSUPPORTED, "K=%d outside [1, 128]", K);
+    if (nprobe < 1 || nprobe > ix->nlist || nprobe > 512)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "nprobe=%d outside [1, min(nlist=%d, 512)]",
+                    nprobe, ix->nlist);
+    if (sp->ub_seed < 0 || sp->ub_seed > 2)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "ub_seed=%d outside {0,1,2}", sp->ub_seed);
+    if (!out->topk_d || !out->topk_i)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "topk outputs are NULL");
+    if ((out->probe_cids || out->probe_dqcs) && out->probe_ld < nprobe)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "probe_ld=%d < nprobe=%d", out->probe_ld, nprobe);
+    const bool cascade = mode == TRIDENT_MODE_CASCADE;
+    if (cascade && (rc = validate_cascade_index(ix))) return rc;
+    if (sp->use_l1 && cascade && !ix->tile_r_minmax)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "use_l1 needs tile_r_minmax");
+    if (B == 0) return TRIDENT_OK;
+    if (!xq) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "xq is NULL");
+
+    Workspace w = carve(ix, workspace, B, nprobe, K);
+    if (!workspace || workspace_bytes < w.bytes)
+        return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu < %zu bytes", workspace_bytes,
+                    w.bytes);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+
+    int p_init = sp->p_init >= 0 ? sp->p_init : trident_p_init_rule(mode, B, K, nprobe);
+    if (!cascade) p_init = 0;
+    if (p_init > nprobe) p_init = nprobe;
+
+    // Probes always land in the workspace (row stride nprobe); the caller's buffers, when
+    // given, receive a mirror copy from the same kernel.
+    int32_t* pc = w.probe_cids;
+    float* pd = w.probe_dqcs;
+    const int ld = nprobe;
+    if ((rc = run_front_end(ix, xq, B, nprobe, cascade, w, out->probe_cids, out->probe_dqcs,
+                            out->probe_ld, st)))
+        return rc;
+
+    const int64_t M1 = (int64_t)B * p_init, M2 = (int64_t)B * (nprobe - p_init);
+    int32_t *p1c = w.pair_cids, *p1q = w.pair_qids;
+    float* p1d = w.pair_dqcs;
+    int32_t *p2c = w.pair_cids + M1, *p2q = w.pair_qids + M1;
+    float* p2d = w.pair_dqcs + M1;
+    if ((rc = group_pairs(pc, pd, ld, B, nprobe, p_init, ix->nlist, w.counts, w.seg_off, w.cursor,
+                          p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, st)))
+        return rc;
+
+    const int KP = K <= 64 ? 64 : 128;
+    const int64_t cap = (int64_t)nprobe * K;
+    if (out->stats && (rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
+    ScanArgs a = make_scan_args(ix, w, K, cap, cascade ? sp->use_l1 : 0, out->stats);
+    MergeArgs m{};
+    m.B = B;
+    m.K = K;
+    m.cap = (int)cap;
+    m.cand_key = w.cand_key;
+    m.cand_id = w.cand_id;
+    m.cand_cnt = w.cand_cnt;
+    m.list_key = w.list_key;
+    m.list_id = w.list_id;
+    m.tau64 = w.tau64;
+
+    if (M1 > 0) {
+        if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
+        a.pair_cid = p1c;
+        a.pair_qid = p1q;
+        a.pair_dqc = pd ? p1d : nullptr;
+        a.M = (int)M1;
+        a.tau_in = nullptr;
+        const bool ub1 = cascade && sp->ub_seed != 0;
+        rc = KP == 64 ? dispatch_scan<64>(a, cascade, ub1, st) : dispatch_scan<128>(a, cascade, ub1, st);
+        if (rc) return rc;
+        m.use_prev = 0;
+        m.tau_sq_out = out->tau_sq;
+        const bool last = M2 == 0;
+        m.out_d = last ? out->topk_d : nullptr;
+        m.out_i = last ? out->topk_i : nullptr;
+        if ((rc = launch_merge(m, KP, st))) return rc;
+    }
+    if (M2 > 0) {
+        if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
+        a.pair_cid = p2c;
+        a.pair_qid = p2q;
+        a.pair_dqc = pd ? p2d : nullptr;
+        a.M = (int)M2;
+        a.tau_in = M1 > 0 ? w.tau64 : nullptr;
+        const bool ub2 = cascade && (sp->ub_seed == 2 || (sp->ub_seed == 1 && M1 == 0));
+        rc = KP == 64 ? dispatch_scan<64>(a, cascade, ub2, st) : dispatch_scan<128>(a, cascade, ub2, st);
+        if (rc) return rc;
+        m.use_prev = M1 > 0 ? 1 : 0;
+        m.tau_sq_out = M1 > 0 ? nullptr : out->tau_sq;
+        m.out_d = out->topk_d;
+        m.out_i = out->topk_i;
+        if ((rc = launch_merge(m, KP, st))) return rc;
+    }
+    return TRIDENT_OK;
+}
+
+int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
+                       const int32_t* qids, const int32_t* cids, const int64_t* spos, int32_t n,
+                       void* workspace, size_t workspace_bytes, double* lb, double* ub,
+                       void* stream) {
+    int rc = validate_index(ix);
+    if (rc) return rc;
+    if ((rc = validate_cascade_index(ix))) return rc;
+    if (B < 1 || n < 0 || !xq || !qids || !cids || !spos || !lb || !ub)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad sq8_bounds arguments");
+    Workspace w = carve(ix, workspace, B, 1, 1);
+    if (!workspace || workspace_bytes < w.bytes)
+        return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu < %zu bytes", workspace_bytes,
+                    w.bytes);
+    if (n == 0) return TRIDENT_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int ldw = ix->nlist + ix->D_pad;
+    const int cols = std::max(ix->D, ix->D_pad);
+    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 3) / 4), dim3(64, 4), 0, st>>>(
+        xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
+        w.xrot64, w.qerr, 1);
+    if ((rc = check_launch("prep_queries_kernel"))) return rc;
+    ScanArgs a = make_scan_args(ix, w, 1, 1, 0, nullptr);
+    sq8_bounds_kernel<<<(n + 255) / 256, 256, 0, st>>>(a, qids, cids, spos, n, lb, ub);
+    return check_launch("sq8_bounds_kernel");
+}
+
+int trident_host_alloc_mapped(size_t bytes, void** host_ptr) {
+    if (!host_ptr || bytes == 0) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad host alloc args");
+    void* p = nullptr;
+    hipError_t e = hipHostMalloc(&p, bytes, hipHostMallocMapped | hipHostMallocPortable);
+    if (e != hipSuccess)
+        return fail(TRIDENT_ERR_OUT_OF_MEMORY, "hipHostMalloc(%zu): %s", bytes,
+                    hipGetErrorString(e));
+    *host_ptr = p;
+    return TRIDENT_OK;
+}
+
+int trident_host_free(void* host_ptr) {
+    if (!host_ptr) return TRIDENT_OK;
+    hipError_t e = hipHostFree(host_ptr);
+    if (e != hipSuccess) return fail(TRIDENT_ERR_HIP, "hipHostFree: %s", hipGetErrorString(e));
+    return TRIDENT_OK;
+}
+
+int trident_host_device_pointer(void* host_ptr, void** device_ptr) {
+    if (!host_ptr || !device_ptr) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "NULL pointer");
+    hipError_t e = hipHostGetDevicePointer(device_ptr, host_ptr, 0);
+    if (e != hipSuccess)
+        return fail(TRIDENT_ERR_HIP, "hipHostGetDevicePointer: %s", hipGetErrorString(e));
+    return TRIDENT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,179 @@
+// Device helpers shared by the gfx950 kernels of the lossless IVF query path.
+//
+// Ordering contract: candidates are ordered lexicographically by (distance, id), the
+// tie-break of insert_topk (reference src/trident_v4_kernels.cu:19-60).  Distances are
+// non-negative float64 values, so their IEEE bit patterns order like the values and a
+// candidate is a (uint64 key, int32 id) pair.  Empty slots hold (kKeyInvalid, kIdInvalid)
+// and sort after every real candidate (NaN distances sort after +inf).
+//
+// Top-K lists live in registers of one wave64: a 64-entry list is one entry per lane, a
+// 128-entry list two entries per lane, both sorted ascending across lanes.  Inserting a
+// batch of up to 64 candidates is a register bitonic sort of the batch followed by a
+// bitonic merge with the list -- no LDS, no block barrier, no single-lane insertion loop.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace trident {
+
+constexpr int kWave = 64;
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr uint64_t kKeyInvalid = ~0ull;
+constexpr int32_t kIdInvalid = 0x7fffffff;
+
+__device__ __forceinline__ uint64_t key_of(double d) {
+    return (uint64_t)__double_as_longlong(d);
+}
+__device__ __forceinline__ double dist_of(uint64_t k) {
+    return __longlong_as_double((long long)k);
+}
+__device__ __forceinline__ bool ent_less(uint64_t ka, int32_t ia, uint64_t kb, int32_t ib) {
+    return ka < kb || (ka == kb && ia < ib);
+}
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+// Index of this lane among the set lanes of `mask` below it.
+__device__ __forceinline__ int mask_rank(uint64_t mask) {
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+    int lo = __shfl_xor((int)(uint32_t)v, m, kWave);
+    int hi = __shfl_xor((int)(uint32_t)(v >> 32), m, kWave);
+    return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+    uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Orders this wave's LDS accesses around the call (producer/consumer inside one wave).
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Compare-exchange with lane ^ j; keep the smaller entry when take_min.
+__device__ __forceinline__ void cmpx(uint64_t& k, int32_t& id, int j, bool take_min) {
+    uint64_t pk = shfl_xor_u64(k, j);
+    int32_t pi = __shfl_xor(id, j, kWave);
+    bool sw = take_min ? ent_less(pk, pi, k, id) : ent_less(k, id, pk, pi);
+    k = sw ? pk : k;
+    id = sw ? pi : id;
+}
+
+// Full bitonic sort of one entry per lane, ascending across lanes.
+__device__ __forceinline__ void wave_sort64(uint64_t& k, int32_t& id) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int s = 2; s <= kWave; s <<= 1) {
+#pragma unroll
+        for (int j = s >> 1; j > 0; j >>= 1) {
+            const bool up = (lane & s) == 0;
+            const bool lower = (lane & j) == 0;
+            cmpx(k, id, j, lower == up);
+        }
+    }
+}
+
+// Sorts a bitonic sequence held one entry per lane, ascending.
+__device__ __forceinline__ void wave_merge64(uint64_t& k, int32_t& id) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int j = kWave >> 1; j > 0; j >>= 1) cmpx(k, id, j, (lane & j) == 0);
+}
+
+template <int KP>
+struct WaveList;
+
+// Best 64 candidates seen, one per lane, sorted ascending.
+template <>
+struct WaveList<64> {
+    uint64_t k0;
+    int32_t i0;
+    __device__ __forceinline__ void init() {
+        k0 = kKeyInvalid;
+        i0 = kIdInvalid;
+    }
+    __device__ __forceinline__ void at(int idx, uint64_t& k, int32_t& i) const {
+        k = readlane_u64(k0, idx);
+        i = __builtin_amdgcn_readlane(i0, idx);
+    }
+    // Merge an unsorted batch (one entry per lane) into the list.
+    __device__ __forceinline__ void insert(uint64_t bk, int32_t bi) {
+        wave_sort64(bk, bi);
+        uint64_t rk = shfl_xor_u64(bk, kWave - 1);  // lane i <- batch[63 - i]
+        int32_t ri = __shfl_xor(bi, kWave - 1, kWave);
+        if (ent_less(rk, ri, k0, i0)) {
+            k0 = rk;
+            i0 = ri;
+        }
+        wave_merge64(k0, i0);
+    }
+};
+
+// Best 128 candidates seen: k0/i0 hold ranks 0..63, k1/i1 ranks 64..127.
+template <>
+struct WaveList<128> {
+    uint64_t k0, k1;
+    int32_t i0, i1;
+    __device__ __forceinline__ void init() {
+        k0 = k1 = kKeyInvalid;
+        i0 = i1 = kIdInvalid;
+    }
+    __device__ __forceinline__ void at(int idx, uint64_t& k, int32_t& i) const {
+        if (idx < kWave) {
+            k = readlane_u64(k0, idx);
+            i = __builtin_amdgcn_readlane(i0, idx);
+        } else {
+            k = readlane_u64(k1, idx - kWave);
+            i = __builtin_amdgcn_readlane(i1, idx - kWave);
+        }
+    }
+    __device__ __forceinline__ void insert(uint64_t bk, int32_t bi) {
+        wave_sort64(bk, bi);
+        uint64_t rk = shfl_xor_u64(bk, kWave - 1);
+        int32_t ri = __shfl_xor(bi, kWave - 1, kWave);
+        // Ranks 0..63 of the list always survive a 64-entry batch; the other 64 survivors are
+        // the smallest 64 of (upper half U, batch): min(U[i], batch[63-i]) is bitonic.
+        if (ent_less(rk, ri, k1, i1)) {
+            k1 = rk;
+            i1 = ri;
+        }
+        wave_merge64(k1, i1);
+        // Bitonic merge of (lower half, reversed new upper half), 128 entries.
+        uint64_t mk = shfl_xor_u64(k1, kWave - 1);
+        int32_t mi = __shfl_xor(i1, kWave - 1, kWave);
+        const bool m_lo = ent_less(mk, mi, k0, i0);
+        uint64_t lo_k = m_lo ? mk : k0, hi_k = m_lo ? k0 : mk;
+        int32_t lo_i = m_lo ? mi : i0, hi_i = m_lo ? i0 : mi;
+        wave_merge64(lo_k, lo_i);
+        wave_merge64(hi_k, hi_i);
+        k0 = lo_k;
+        i0 = lo_i;
+        k1 = hi_k;
+        i1 = hi_i;
+    }
+};
+
+// Offers one candidate per lane; only entries that beat the current K-th entry are merged.
+// Returns true (wave-uniform) when the list changed.
+template <int KP>
+__device__ __forceinline__ bool list_offer(WaveList<KP>& L, int K, uint64_t ck, int32_t ci) {
+    uint64_t tk;
+    int32_t ti;
+    L.at(K - 1, tk, ti);
+    const bool useful = ent_less(ck, ci, tk, ti);
+    if (__ballot(useful) == 0) return false;
+    L.insert(useful ? ck : kKeyInvalid, useful ? ci : kIdInvalid);
+    return true;
+}
+
+}  // namespace trident

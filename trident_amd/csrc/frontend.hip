@@ -1,0 +1,335 @@
+// Front end of the lossless IVF query path on gfx950: query preparation (float64 copy,
+// float64 PCA rotation with a rigorous error bound), float64 coarse distances, the exact
+// (d, cid) top-nprobe selection, and the cluster-major grouping of (cluster, query) pairs.
+//
+// Reference counterparts (src/trident_v4_kernels.cu): the fused coarse+rotation GEMM
+// at::addmm_out (:1233-1246), trident_topk_centroids_kernel (:68-162) and
+// trident_counting_sort_pairs_kernel (:168-263).  The reference forms coarse distances as
+// |c|^2 - 2<q,c> + |q|^2 in FP32, which can reorder near-tied centroids; here every
+// (query, centroid) distance is the canonical float64 sum of squared differences in
+// dimension order, so the probe set equals the float64 oracle's on every query.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace trident {
+
+__global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// grid (ceil(max(D, D_pad) / 64), ceil(B / 4)), block (64, 4).
+// xq64[b, d] = (double)xq[b, d]; xrot64[b, j] = sum_d xq[b, d] * R[d, j] + bvec[j] evaluated
+// in float64 (fma, dimension order) and qerr[b, j] bounds its distance from the exact value.
+__global__ __launch_bounds__(256) void prep_queries_kernel(
+    const float* __restrict__ xq, int B, int D, int D_pad, const float* __restrict__ W, int ldw,
+    int nlist, const float* __restrict__ bvec, double* __restrict__ xq64,
+    double* __restrict__ xrot64, double* __restrict__ qerr, int do_rot) {
+    const int j = blockIdx.x * 64 + threadIdx.x;
+    const int b = blockIdx.y * 4 + threadIdx.y;
+    if (b >= B) return;
+    const float* qr = xq + (size_t)b * D;
+    if (j < D) xq64[(size_t)b * D + j] = (double)qr[j];
+    if (!do_rot || j >= D_pad) return;
+    double acc = 0.0, mag = 0.0;
+    const float* wcol = W + nlist + j;
+    for (int d = 0; d < D; ++d) {
+        const double qd = (double)qr[d];
+        const double r = (double)wcol[(size_t)d * ldw];
+        acc = fma(qd, r, acc);
+        mag += fabs(qd * r);
+    }
+    const double bj = (double)bvec[nlist + j];
+    acc += bj;
+    xrot64[(size_t)b * D_pad + j] = acc;
+    // |fl(sum) - sum| <= (D + 1) 2^-53 sum|terms|; doubled to also cover the rounding of `mag`.
+    qerr[(size_t)b * D_pad + j] = (double)(D + 3) * 0x1p-52 * (mag + fabs(bj)) + 0x1p-1000;
+}
+
+// grid (ceil(nlist / 64), ceil(B / 32)), block 256: each wave owns 64 centroids (one per
+// lane) x 8 queries; query values are wave-uniform (scalar loads).  Centroid c, dim d is
+// -0.5f * W[d, c], exact because W_coarse_only = -2 C^T.
+__global__ __launch_bounds__(256) void coarse_dist_kernel(const double* __restrict__ xq64, int B,
+                                                          int D, const float* __restrict__ W,
+                                                          int ldw, int nlist,
+                                                          double* __restrict__ cd64) {
+    constexpr int QW = 8;
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = blockIdx.x * 64 + lane;
+    const int qb = blockIdx.y * (QW * kWavesPerBlock) + wid * QW;
+    if (qb >= B) return;
+    const int cc = c < nlist ? c : nlist - 1;
+    const double* qrow[QW];
+#pragma unroll
+    for (int i = 0; i < QW; ++i) qrow[i] = xq64 + (size_t)min(qb + i, B - 1) * D;
+    double acc[QW];
+#pragma unroll
+    for (int i = 0; i < QW; ++i) acc[i] = 0.0;
+    const float* wc = W + cc;
+    for (int d = 0; d < D; ++d) {
+        const double cv = (double)(-0.5f * wc[(size_t)d * ldw]);
+#pragma unroll
+        for (int i = 0; i < QW; ++i) {
+            const double t = qrow[i][d] - cv;
+            acc[i] = fma(t, t, acc[i]);
+        }
+    }
+    if (c < nlist) {
+#pragma unroll
+        for (int i = 0; i < QW; ++i)
+            if (qb + i < B) cd64[(size_t)(qb + i) * nlist + c] = acc[i];
+    }
+}
+
+// Block-wide exclusive scan of one uint32 per thread (256 threads).
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot,
+                                                         uint32_t* total) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
+        if (lane >= o) inc += t;
+    }
+    if (lane == kWave - 1) s_wave_tot[wid] = inc;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+        const uint32_t t = s_wave_tot[w];
+        if (w < wid) before += t;
+        all += t;
+    }
+    __syncthreads();
+    if (total) *total = all;
+    return before + inc - v;
+}
+
+// One block of 256 threads per query.  Radix-selects the exact nprobe-th smallest float64
+// key, takes every smaller key plus the smallest cids among the equal ones, then sorts the
+// selection by (d, cid).  Keys live in LDS (nlist * 8 bytes of dynamic LDS).  Results go to
+// out_* (stride ld) and, when non-null, are mirrored into out2_* (stride ld2).
+__global__ __launch_bounds__(256) void select_probes_kernel(const double* __restrict__ cd64,
+                                                            int nlist, int nprobe,
+                                                            int32_t* __restrict__ out_cids,
+                                                            float* __restrict__ out_dqcs, int ld,
+                                                            int32_t* __restrict__ out2_cids,
+                                                            float* __restrict__ out2_dqcs,
+                                                            int ld2) {
+    extern __shared__ uint64_t s_keys[];
+    __shared__ uint32_t s_hist[256];
+    __shared__ uint64_t s_sel_k[512];
+    __shared__ int32_t s_sel_c[512];
+    __shared__ uint32_t s_wtot[kWavesPerBlock];
+    __shared__ uint64_t s_red[2][kWavesPerBlock];
+    __shared__ uint32_t s_digit, s_need, s_nsel;
+
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int q = blockIdx.x;
+    const double* row = cd64 + (size_t)q * nlist;
+
+    uint64_t kmin = kKeyInvalid, kmax = 0;
+    for (int c = tid; c < nlist; c += kBlock) {
+        const uint64_t k = key_of(row[c]);
+        s_keys[c] = k;
+        kmin = k < kmin ? k : kmin;
+        kmax = k > kmax ? k : kmax;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint64_t a = shfl_xor_u64(kmin, o), b = shfl_xor_u64(kmax, o);
+        kmin = a < kmin ? a : kmin;
+        kmax = b > kmax ? b : kmax;
+    }
+    if (lane == 0) {
+        s_red[0][wid] = kmin;
+        s_red[1][wid] = kmax;
+    }
+    __syncthreads();
+    kmin = s_red[0][0];
+    kmax = s_red[1][0];
+#pragma unroll
+    for (int w = 1; w < kWavesPerBlock; ++w) {
+        kmin = s_red[0][w] < kmin ? s_red[0][w] : kmin;
+        kmax = s_red[1][w] > kmax ? s_red[1][w] : kmax;
+    }
+
+    // Radix select over the digits below the common prefix of all keys.
+    uint64_t prefix = kmin, mask = ~0ull;
+    uint32_t need = (uint32_t)nprobe;
+    const uint64_t diff = kmin ^ kmax;
+    if (diff != 0) {
+        const int top = 63 - __clzll((long long)diff);
+        const int start = (top >> 3) << 3;
+        mask = (start + 8 >= 64) ? 0ull : (~0ull << (start + 8));
+        prefix = kmin & mask;
+        for (int shift = start; shift >= 0; shift -= 8) {
+            s_hist[tid] = 0;
+            __syncthreads();
+            for (int c = tid; c < nlist; c += kBlock) {
+                const uint64_t k = s_keys[c];
+                if ((k & mask) == prefix) atomicAdd(&s_hist[(k >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (wid == 0) {
+                uint32_t h[4];
+                uint32_t loc = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    h[i] = s_hist[4 * lane + i];
+                    loc += h[i];
+                }
+                uint32_t inc = loc;
+#pragma unroll
+                for (int o = 1; o < kWave; o <<= 1) {
+                    uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
+                    if (lane >= o) inc += t;
+                }
+                const uint32_t exc = inc - loc;
+                if (exc < need && need <= inc) {
+                    uint32_t cum = exc;
+                    int bsel = 3;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (cum + h[i] >= need) {
+                            bsel = i;
+                            break;
+                        }
+                        cum += h[i];
+                    }
+                    s_digit = (uint32_t)(4 * lane + bsel);
+                    s_need = need - cum;
+                }
+            }
+            __syncthreads();
+            prefix |= (uint64_t)s_digit << shift;
+            mask |= 255ull << shift;
+            need = s_need;
+            __syncthreads();
+        }
+    }
+    const uint64_t kstar = prefix;
+
+    // Take all keys < kstar and the `need` smallest cids among keys == kstar.
+    const int chunk = (nlist + kBlock - 1) / kBlock;
+    const int c0 = min(nlist, tid * chunk), c1 = min(nlist, c0 + chunk);
+    uint32_t my_eq = 0;
+    for (int c = c0; c < c1; ++c) my_eq += s_keys[c] == kstar;
+    uint32_t rank = block_exclusive_scan(my_eq, s_wtot, nullptr);
+    if (tid == 0) s_nsel = 0;
+    __syncthreads();
+    for (int c = c0; c < c1; ++c) {
+        const uint64_t k = s_keys[c];
+        bool take = k < kstar;
+        if (k == kstar) {
+            take = rank < need;
+            ++rank;
+        }
+        if (take) {
+            const uint32_t slot = atomicAdd(&s_nsel, 1u);
+            s_sel_k[slot] = k;
+            s_sel_c[slot] = c;
+        }
+    }
+    int P2 = 1;
+    while (P2 < nprobe) P2 <<= 1;
+    __syncthreads();
+    for (int i = nprobe + tid; i < P2; i += kBlock) {
+        s_sel_k[i] = kKeyInvalid;
+        s_sel_c[i] = kIdInvalid;
+    }
+    __syncthreads();
+    for (int s = 2; s <= P2; s <<= 1) {
+        for (int j = s >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < (P2 >> 1); i += kBlock) {
+                const int lo = 2 * j * (i / j) + (i % j), hi = lo + j;
+                const bool up = (lo & s) == 0;
+                const uint64_t kl = s_sel_k[lo], kh = s_sel_k[hi];
+                const int32_t cl = s_sel_c[lo], ch = s_sel_c[hi];
+                const bool hi_less = ent_less(kh, ch, kl, cl);
+                if (hi_less == up) {
+                    s_sel_k[lo] = kh;
+                    s_sel_k[hi] = kl;
+                    s_sel_c[lo] = ch;
+                    s_sel_c[hi] = cl;
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = tid; i < nprobe; i += kBlock) {
+        const int32_t c = s_sel_c[i];
+        const float dq = (float)sqrt(dist_of(s_sel_k[i]));
+        out_cids[(size_t)q * ld + i] = c;
+        out_dqcs[(size_t)q * ld + i] = dq;
+        if (out2_cids) out2_cids[(size_t)q * ld2 + i] = c;
+        if (out2_dqcs) out2_dqcs[(size_t)q * ld2 + i] = dq;
+    }
+}
+
+// counts: [2, nlist + 1] (pass-1 row, pass-2 row), zeroed by the caller.
+__global__ void count_pairs_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
+                                   int nprobe, int p_init, int nlist, int32_t* counts) {
+    const int64_t total = (int64_t)B * nprobe;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int q = (int)(idx / nprobe), p = (int)(idx - (int64_t)q * nprobe);
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
+        atomicAdd(&counts[(p < p_init ? 0 : (nlist + 1)) + cid], 1);
+    }
+}
+
+// grid 2 (one block per pass), block 256: seg_off[pass] = exclusive scan of counts[pass];
+// cursor[pass] receives the same offsets for the scatter.
+__global__ __launch_bounds__(256) void scan_pairs_kernel(const int32_t* counts, int nlist,
+                                                         int32_t* seg_off, int32_t* cursor) {
+    __shared__ uint32_t s_wtot[kWavesPerBlock];
+    const int pass = blockIdx.x, tid = threadIdx.x;
+    const int32_t* cnt = counts + pass * (nlist + 1);
+    int32_t* off = seg_off + pass * (nlist + 1);
+    int32_t* cur = cursor + pass * (nlist + 1);
+    const int chunk = (nlist + kBlock - 1) / kBlock;
+    const int c0 = min(nlist, tid * chunk), c1 = min(nlist, c0 + chunk);
+    uint32_t local = 0;
+    for (int c = c0; c < c1; ++c) local += (uint32_t)cnt[c];
+    uint32_t total = 0;
+    uint32_t run = block_exclusive_scan(local, s_wtot, &total);
+    for (int c = c0; c < c1; ++c) {
+        const uint32_t v = (uint32_t)cnt[c];
+        off[c] = (int32_t)run;
+        cur[c] = (int32_t)run;
+        run += v;
+    }
+    if (tid == 0) {
+        off[nlist] = (int32_t)total;
+        cur[nlist] = (int32_t)total;
+    }
+}
+
+__global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
+                                     const float* __restrict__ probe_dqcs, int ld, int B,
+                                     int nprobe, int p_init, int nlist, int32_t* cursor,
+                                     int32_t* __restrict__ p1_cids, int32_t* __restrict__ p1_qids,
+                                     float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
+                                     int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs) {
+    const int64_t total = (int64_t)B * nprobe;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int q = (int)(idx / nprobe), p = (int)(idx - (int64_t)q * nprobe);
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
+        const bool first = p < p_init;
+        const int slot = atomicAdd(&cursor[(first ? 0 : (nlist + 1)) + cid], 1);
+        int32_t* oc = first ? p1_cids : p2_cids;
+        int32_t* oq = first ? p1_qids : p2_qids;
+        float* od = first ? p1_dqcs : p2_dqcs;
+        oc[slot] = cid;
+        oq[slot] = q;
+        if (od) od[slot] = probe_dqcs ? probe_dqcs[(size_t)q * ld + p] : 0.0f;
+    }
+}
+
+}  // namespace trident

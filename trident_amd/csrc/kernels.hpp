@@ -1,0 +1,105 @@
+// Kernel declarations and argument blocks of the gfx950 lossless IVF query path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace trident {
+
+// Everything one per-pair scan launch reads; passed by value as the kernel argument.
+struct ScanArgs {
+    // index layout
+    const uint32_t* sq8;        // [tiles, D4, T]
+    const int32_t* tile_oids;   // [tiles, T]
+    const float* tile_rmm;      // [tiles, 2] or null
+    const int32_t* tile_off;    // [nlist + 1]
+    const int32_t* vec_off;     // [nlist + 1]
+    const float* xb;            // [N, D] sorted base (device or mapped host)
+    const float* vmin;          // [nlist|1, D_pad]
+    const float* delta;
+    const float* eps;
+    const int32_t* blk;         // [nb + 1]
+    int D, D_pad, T, nb, per_cluster, use_l1;
+    // queries
+    const double* xq64;         // [B, D]
+    const double* xrot64;       // [B, D_pad]
+    const double* qerr;         // [B, D_pad]
+    // pairs of this pass, grouped by cluster
+    const int32_t* pair_cid;
+    const int32_t* pair_qid;
+    const float* pair_dqc;      // |q - c| per pair (use_l1) or null
+    int M;
+    // per-query threshold from the previous pass (float64), or null
+    const double* tau_in;
+    // per-query candidate lists
+    uint64_t* cand_key;
+    int32_t* cand_id;
+    int32_t* cand_cnt;
+    int cap, K;
+    unsigned long long* stats;  // [4] or null
+    double lb_scale;            // tau -> float32 Stage Y threshold factor
+    double ub_scale;            // Stage X sum -> float64 distance bound factor
+};
+
+struct MergeArgs {
+    int B, K, cap;
+    const uint64_t* cand_key;
+    const int32_t* cand_id;
+    const int32_t* cand_cnt;
+    uint64_t* list_key;   // [B, KP] per-query running top list
+    int32_t* list_id;
+    int use_prev;
+    double* tau64;        // [B] K-th distance after this merge (+inf if fewer than K)
+    float* out_d;         // [B, K] or null (final pass only)
+    int64_t* out_i;
+    float* tau_sq_out;    // [B] or null
+};
+
+__global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n);
+
+__global__ void prep_queries_kernel(const float* __restrict__ xq, int B, int D, int D_pad,
+                                    const float* __restrict__ W, int ldw, int nlist,
+                                    const float* __restrict__ bvec, double* __restrict__ xq64,
+                                    double* __restrict__ xrot64, double* __restrict__ qerr,
+                                    int do_rot);
+
+__global__ void coarse_dist_kernel(const double* __restrict__ xq64, int B, int D,
+                                   const float* __restrict__ W, int ldw, int nlist,
+                                   double* __restrict__ cd64);
+
+__global__ void select_probes_kernel(const double* __restrict__ cd64, int nlist, int nprobe,
+                                     int32_t* __restrict__ out_cids,
+                                     float* __restrict__ out_dqcs, int ld,
+                                     int32_t* __restrict__ out2_cids,
+                                     float* __restrict__ out2_dqcs, int ld2);
+
+__global__ void count_pairs_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
+                                   int nprobe, int p_init, int nlist, int32_t* counts);
+
+__global__ void scan_pairs_kernel(const int32_t* counts, int nlist, int32_t* seg_off,
+                                  int32_t* cursor);
+
+__global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
+                                     const float* __restrict__ probe_dqcs, int ld, int B,
+                                     int nprobe, int p_init, int nlist, int32_t* cursor,
+                                     int32_t* __restrict__ p1_cids, int32_t* __restrict__ p1_qids,
+                                     float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
+                                     int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs);
+
+template <int KP, bool CASCADE, bool UB>
+__global__ void pair_scan_kernel(ScanArgs a);
+
+template <int KP>
+__global__ void merge_kernel(MergeArgs a);
+
+__global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
+                                  const int32_t* __restrict__ cids,
+                                  const int64_t* __restrict__ spos, int n, double* lb,
+                                  double* ub);
+
+// Dynamic LDS bytes of pair_scan_kernel for a given D / D_pad.
+inline size_t scan_dyn_lds_bytes(int D, int D_pad) {
+    return (size_t)D * sizeof(double) + (size_t)3 * D_pad * sizeof(float);
+}
+
+}  // namespace trident

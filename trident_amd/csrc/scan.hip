@@ -1,0 +1,461 @@
+// Per-(cluster, query)-pair scan of the lossless IVF query path on gfx950, plus the
+// per-query merge.
+//
+// One 256-thread workgroup (4 independent waves) per pair; pairs arrive grouped by cluster
+// and are remapped so each XCD walks a contiguous run of clusters (its own L2 keeps the
+// cluster's codes).  Each wave takes 64-vector slices of the cluster, one vector per lane:
+//
+//   Stage X (UB)   : upper bound per vector from the SQ8 codes over all dims; the K-th
+//                    smallest over the cluster seeds the threshold
+//                    (reference src/trident_v4_kernels.cu:626-676).
+//   Stage Y        : SQ8 lower bound accumulated block by block; a lane dies once the bound
+//                    passes the threshold and the wave leaves the slice as soon as its 64-bit
+//                    ballot is empty -- no block barrier (reference :679-780, whose warp32
+//                    ballot is followed by a CTA barrier on every block).
+//   Stage Z        : survivors are compacted into a per-wave LDS queue with ballot/mbcnt
+//                    and refined 64 at a time: the wave copies the survivors' rows into LDS
+//                    with coalesced loads, then each lane sums its own row in float64, in
+//                    dimension order (the canonical distance) (reference :796-941).
+//   top-K          : each wave keeps a register bitonic top-K list; the four lists are
+//                    merged at the end and the pair emits at most K entries
+//                    (reference :943-961 emission, :19-60 ordering).
+//
+// CM route (CASCADE == false, reference mode 10, :268-374): no Stage X/Y, every vector is
+// refined exactly.
+//
+// Rigour.  Stage Y prunes x when  lb_f32(x) > round_up(tau * lb_scale)  with
+// lb_scale = rot_sq_max * (1 + rho) * (1 + 1e-12), rho = (D_pad + 4) * 2^-24.  Per dimension
+// the kernel evaluates a = fma(code, delta, base32) and l = max(|a| - e32, 0), where e32
+// (dim_params) bounds eps_dim plus every rounding between the exact rotated gap and a; so
+// l <= |x_rot - q_rot| (1 + 2^-24) and the float32 sum exceeds the exact rotated LB by at
+// most a factor (1 + rho).  |(x - q) R|^2 <= rot_sq_max |x - q|^2 then gives
+// lb_f32 > round_up(tau * lb_scale)  =>  d64(x) > tau.  Stage X mirrors this with
+// u = |a| + e32 and ub_scale = (1 + rho) (1 + 1e-12) / rot_sq_min.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace trident {
+
+constexpr int kStageCh = 32;    // dims per Stage Z staging chunk
+constexpr int kQueueCap = 128;  // per-wave survivor queue (64 pending + one slice)
+
+__device__ __forceinline__ void dim_params(double vm, float dl, float ep, double xr, double qe,
+                                           float& base32, float& e32) {
+    const double b64 = vm - xr;
+    const float b32 = (float)b64;
+    const double E = fabs((double)b32 - b64) + qe + 0x1p-52 * fabs(b64) +
+                     0x1p-24 * (255.0 * (double)dl + fabs((double)b32)) * (1.0 + 0x1p-20) +
+                     0x1p-126;
+    base32 = b32;
+    e32 = __double2float_ru(((double)ep + E) * (1.0 + 0x1p-50));
+}
+
+__device__ __forceinline__ float lb_step(uint32_t code, float dl, float bs, float ee, float acc) {
+    const float a = fmaf((float)code, dl, bs);
+    const float l = fmaxf(fabsf(a) - ee, 0.0f);
+    return fmaf(l, l, acc);
+}
+
+__device__ __forceinline__ float ub_step(uint32_t code, float dl, float bs, float ee, float acc) {
+    const float a = fmaf((float)code, dl, bs);
+    const float u = fabsf(a) + ee;
+    return fmaf(u, u, acc);
+}
+
+__device__ __forceinline__ uint32_t tau_bits_of(double tau, double lb_scale) {
+    return __float_as_uint(__double2float_ru(tau * lb_scale));
+}
+
+template <bool UB>
+__device__ __forceinline__ float sq8_accumulate(const uint32_t* cp, int T, int d4s, int d4e,
+                                                const float* s_base, const float* s_dlt,
+                                                const float* s_e, float acc) {
+#pragma unroll 4
+    for (int d4 = d4s; d4 < d4e; ++d4) {
+        const uint32_t w = cp[(size_t)d4 * T];
+        const float4 bs = *reinterpret_cast<const float4*>(s_base + 4 * d4);
+        const float4 dl = *reinterpret_cast<const float4*>(s_dlt + 4 * d4);
+        const float4 ee = *reinterpret_cast<const float4*>(s_e + 4 * d4);
+        if constexpr (UB) {
+            acc = ub_step(w & 0xffu, dl.x, bs.x, ee.x, acc);
+            acc = ub_step((w >> 8) & 0xffu, dl.y, bs.y, ee.y, acc);
+            acc = ub_step((w >> 16) & 0xffu, dl.z, bs.z, ee.z, acc);
+            acc = ub_step(w >> 24, dl.w, bs.w, ee.w, acc);
+        } else {
+            acc = lb_step(w & 0xffu, dl.x, bs.x, ee.x, acc);
+            acc = lb_step((w >> 8) & 0xffu, dl.y, bs.y, ee.y, acc);
+            acc = lb_step((w >> 16) & 0xffu, dl.z, bs.z, ee.z, acc);
+            acc = lb_step(w >> 24, dl.w, bs.w, ee.w, acc);
+        }
+    }
+    return acc;
+}
+
+// Canonical float64 distance of the first `nq` queued survivors (lane i <- survivor i).
+// Rows are staged through LDS 32 dims at a time with 128-byte coalesced row loads.
+__device__ __forceinline__ double refine_rows(const float* __restrict__ xb, int D,
+                                              const int32_t* q_spos, int nq,
+                                              float (*stage)[kWave + 1], const double* s_q64) {
+    const int lane = lane_id();
+    double acc = 0.0;
+    const int half = lane >> 5, kk = lane & 31;
+    for (int d0 = 0; d0 < D; d0 += kStageCh) {
+        const int ch = min(kStageCh, D - d0);
+        for (int r0 = 0; r0 < nq; r0 += 2) {
+            const int r = r0 + half;
+            float v = 0.0f;
+            if (r < nq && kk < ch) v = xb[(size_t)q_spos[r] * D + d0 + kk];
+            if (r < nq) stage[kk][r] = v;
+        }
+        wave_sync();
+        if (lane < nq) {
+            for (int k = 0; k < ch; ++k) {
+                const double t = (double)stage[k][lane] - s_q64[d0 + k];
+                acc = fma(t, t, acc);
+            }
+        }
+        wave_sync();
+    }
+    return acc;
+}
+
+template <int KP>
+__device__ __forceinline__ void list_store(const WaveList<KP>& L, uint64_t* k, int32_t* i) {
+    const int lane = lane_id();
+    k[lane] = L.k0;
+    i[lane] = L.i0;
+    if constexpr (KP == 128) {
+        k[kWave + lane] = L.k1;
+        i[kWave + lane] = L.i1;
+    }
+}
+
+template <int KP>
+__device__ __forceinline__ void list_absorb(WaveList<KP>& L, int K, const uint64_t* k,
+                                            const int32_t* i) {
+    const int lane = lane_id();
+    list_offer(L, K, k[lane], i[lane]);
+    if constexpr (KP == 128) list_offer(L, K, k[kWave + lane], i[kWave + lane]);
+}
+
+template <int KP, bool CASCADE, bool UB>
+__global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
+    extern __shared__ __align__(16) unsigned char dyn_smem[];
+    __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
+    __shared__ int32_t s_qspos[kWavesPerBlock][kQueueCap];
+    __shared__ int32_t s_qoid[kWavesPerBlock][kQueueCap];
+    __shared__ int32_t s_blk[68];
+    __shared__ uint32_t s_tau_bits;
+    __shared__ double s_thr;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // XCD-aware mapping: consecutive dispatch slots go to different XCDs, so XCD x walks
+    // the contiguous pair range [x * nx, (x + 1) * nx) of the cluster-sorted pair list.
+    const int nx = (a.M + 7) >> 3;
+    const int p = (int)(blockIdx.x & 7) * nx + (int)(blockIdx.x >> 3);
+    if (p >= a.M) return;
+    const int cid = a.pair_cid[p];
+    const int q = a.pair_qid[p];
+    const int v0 = a.vec_off[cid];
+    const int n = a.vec_off[cid + 1] - v0;
+    if (n <= 0) return;
+    const int t0 = a.tile_off[cid];
+    const int nslices = (n + kWave - 1) / kWave;
+    const int D = a.D, D_pad = a.D_pad, T = a.T, K = a.K;
+    const int D4 = D_pad >> 2;
+
+    double* s_q64 = reinterpret_cast<double*>(dyn_smem);
+    float* s_base = reinterpret_cast<float*>(s_q64 + D);
+    float* s_dlt = s_base + D_pad;
+    float* s_e = s_dlt + D_pad;
+
+    const double tau_init = a.tau_in ? a.tau_in[q] : (double)INFINITY;
+    for (int d = tid; d < D; d += kBlock) s_q64[d] = a.xq64[(size_t)q * D + d];
+    if constexpr (CASCADE) {
+        const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
+        const double* xr = a.xrot64 + (size_t)q * D_pad;
+        const double* qe = a.qerr + (size_t)q * D_pad;
+        for (int d = tid; d < D_pad; d += kBlock) {
+            float b32, e32;
+            dim_params((double)a.vmin[off + d], a.delta[off + d], a.eps[off + d], xr[d], qe[d],
+                       b32, e32);
+            s_base[d] = b32;
+            s_dlt[d] = a.delta[off + d];
+            s_e[d] = e32;
+        }
+        for (int b = tid; b <= a.nb; b += kBlock) s_blk[b] = a.blk[b];
+    }
+    if (tid == 0) {
+        s_thr = tau_init;
+        s_tau_bits = tau_bits_of(tau_init, a.lb_scale);
+    }
+    __syncthreads();
+
+    const uint32_t* sq8c = a.sq8 + (size_t)t0 * D4 * T;
+    uint64_t* s_ck = reinterpret_cast<uint64_t*>(&s_stage[0][0][0]);
+    int32_t* s_ci = reinterpret_cast<int32_t*>(s_ck + kWavesPerBlock * KP);
+
+    // ---------------- Stage X: SQ8 upper-bound threshold seeding ----------------
+    if constexpr (CASCADE && UB) {
+        WaveList<KP> U;
+        U.init();
+        for (int s = wid; s < nslices; s += kWavesPerBlock) {
+            const int li = s * kWave + lane;
+            const bool valid = li < n;
+            const uint32_t* cp = sq8c + (size_t)(s / (T / kWave)) * D4 * T +
+                                 (s % (T / kWave)) * kWave + lane;
+            float ub = 0.0f;
+            if (valid) ub = sq8_accumulate<true>(cp, T, 0, D4, s_base, s_dlt, s_e, 0.0f);
+            list_offer(U, K, valid ? key_of((double)ub) : kKeyInvalid, valid ? li : kIdInvalid);
+        }
+        list_store(U, s_ck + wid * KP, s_ci + wid * KP);
+        __syncthreads();
+        if (wid == 0) {
+            for (int w = 1; w < kWavesPerBlock; ++w) list_absorb(U, K, s_ck + w * KP, s_ci + w * KP);
+            uint64_t kk;
+            int32_t ki;
+            U.at(K - 1, kk, ki);
+            if (kk != kKeyInvalid && lane == 0) {
+                const double tub = dist_of(kk) * a.ub_scale;
+                if (tub < s_thr) {
+                    s_thr = tub;
+                    s_tau_bits = tau_bits_of(tub, a.lb_scale);
+                }
+            }
+        }
+        __syncthreads();
+    }
+
+    // ---------------- Stage Y / Z ----------------
+    WaveList<KP> L;
+    L.init();
+    double thr = s_thr;
+    int qn = 0;
+    unsigned long long st_cand = 0, st_dims = 0, st_surv = 0, st_ins = 0;
+    int32_t* my_qspos = s_qspos[wid];
+    int32_t* my_qoid = s_qoid[wid];
+    float(*my_stage)[kWave + 1] = s_stage[wid];
+
+    auto flush = [&](int cnt) {
+        const double d64 = refine_rows(a.xb, D, my_qspos, cnt, my_stage, s_q64);
+        const bool ok = lane < cnt && d64 <= thr;
+        if (a.stats) st_ins += __popcll(__ballot(ok));
+        if (list_offer(L, K, ok ? key_of(d64) : kKeyInvalid, ok ? my_qoid[lane] : kIdInvalid)) {
+            uint64_t kk;
+            int32_t ki;
+            L.at(K - 1, kk, ki);
+            if (kk != kKeyInvalid) {
+                const double kth = dist_of(kk);
+                if (kth < thr) {
+                    thr = kth;
+                    if (CASCADE && lane == 0) atomicMin(&s_tau_bits, tau_bits_of(kth, a.lb_scale));
+                }
+            }
+        }
+    };
+
+    for (int s = wid; s < nslices; s += kWavesPerBlock) {
+        const int li = s * kWave + lane;
+        const bool valid = li < n;
+        bool alive = valid;
+        if constexpr (CASCADE) {
+            const int tile = s / (T / kWave), sub = s % (T / kWave);
+            const float tau_s = __uint_as_float(__atomic_load_n(&s_tau_bits, __ATOMIC_RELAXED));
+            if (a.use_l1 && a.tile_rmm && a.pair_dqc) {
+                // Residual-norm band |d_qc - |x - c|| <= |q - x| (reference :686-695), with
+                // margins for the float32 storage of both norms.
+                const double tq = (double)__uint_as_float(
+                    __atomic_load_n(&s_tau_bits, __ATOMIC_RELAXED));
+                if (tq < (double)INFINITY) {
+                    const double dqc = (double)a.pair_dqc[p];
+                    const double rmin = (double)a.tile_rmm[(size_t)(t0 + tile) * 2];
+                    const double rmax = (double)a.tile_rmm[(size_t)(t0 + tile) * 2 + 1];
+                    const double tol = sqrt(tq) * (1.0 + 1e-6) + 1e-6 * (dqc + rmax) + 1e-30;
+                    if (rmax + tol < dqc || rmin - tol > dqc) alive = false;
+                }
+            }
+            const uint32_t* cp = sq8c + (size_t)tile * D4 * T + sub * kWave + lane;
+            float acc = 0.0f;
+            if (a.stats) st_cand += __popcll(__ballot(valid));
+            for (int b = 0; b < a.nb; ++b) {
+                const uint64_t m = __ballot(alive);
+                if (m == 0) break;
+                const int d4s = s_blk[b], d4e = s_blk[b + 1];
+                if (a.stats) st_dims += (unsigned long long)__popcll(m) * (unsigned)(4 * (d4e - d4s));
+                if (alive) {
+                    acc = sq8_accumulate<false>(cp, T, d4s, d4e, s_base, s_dlt, s_e, acc);
+                    alive = acc <= tau_s;
+                }
+            }
+        }
+        const uint64_t m = __ballot(alive);
+        const int cnt = __popcll(m);
+        if (CASCADE && a.stats) st_surv += (unsigned long long)cnt;
+        if (alive) {
+            const int pos = qn + mask_rank(m);
+            my_qspos[pos] = v0 + li;
+            my_qoid[pos] = a.tile_oids[(size_t)t0 * T + li];
+        }
+        qn += cnt;
+        if (qn >= kWave) {
+            wave_sync();
+            flush(kWave);
+            const int rest = qn - kWave;
+            int32_t sp = 0, oi = 0;
+            if (lane < rest) {
+                sp = my_qspos[kWave + lane];
+                oi = my_qoid[kWave + lane];
+            }
+            wave_sync();
+            if (lane < rest) {
+                my_qspos[lane] = sp;
+                my_qoid[lane] = oi;
+            }
+            qn = rest;
+            wave_sync();
+        }
+    }
+    if (qn > 0) {
+        wave_sync();
+        flush(qn);
+    }
+    if (a.stats && lane == 0) {
+        if (CASCADE) {
+            atomicAdd(&a.stats[0], st_cand);
+            atomicAdd(&a.stats[1], st_dims);
+            atomicAdd(&a.stats[2], st_surv);
+        }
+        atomicAdd(&a.stats[3], st_ins);
+    }
+
+    // ---------------- combine the four wave lists and emit <= K entries ----------------
+    __syncthreads();
+    list_store(L, s_ck + wid * KP, s_ci + wid * KP);
+    __syncthreads();
+    if (wid != 0) return;
+    for (int w = 1; w < kWavesPerBlock; ++w) list_absorb(L, K, s_ck + w * KP, s_ci + w * KP);
+    const bool e0 = lane < K && L.k0 != kKeyInvalid;
+    const uint64_t m0 = __ballot(e0);
+    int cnt = __popcll(m0);
+    bool e1 = false;
+    if constexpr (KP == 128) {
+        e1 = kWave + lane < K && L.k1 != kKeyInvalid;
+        cnt += __popcll(__ballot(e1));
+    }
+    if (cnt == 0) return;
+    int base = 0;
+    if (lane == 0) base = atomicAdd(&a.cand_cnt[q], cnt);
+    base = __builtin_amdgcn_readfirstlane(base);
+    if (base + cnt > a.cap) return;  // unreachable: cap = nprobe * K
+    uint64_t* ck = a.cand_key + (size_t)q * a.cap + base;
+    int32_t* ci = a.cand_id + (size_t)q * a.cap + base;
+    if (e0) {
+        ck[lane] = L.k0;
+        ci[lane] = L.i0;
+    }
+    if constexpr (KP == 128) {
+        if (e1) {
+            ck[kWave + lane] = L.k1;
+            ci[kWave + lane] = L.i1;
+        }
+    }
+}
+
+// One wave per query: merges the pass's candidates (and the previous pass's list) into
+// the query's top list; writes the K-th distance and, on the final pass, the outputs.
+template <int KP>
+__global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+    if (q >= a.B) return;
+    WaveList<KP> L;
+    L.init();
+    uint64_t* lk = a.list_key + (size_t)q * KP;
+    int32_t* li = a.list_id + (size_t)q * KP;
+    if (a.use_prev) {
+        L.k0 = lk[lane];
+        L.i0 = li[lane];
+        if constexpr (KP == 128) {
+            L.k1 = lk[kWave + lane];
+            L.i1 = li[kWave + lane];
+        }
+    }
+    const int cnt = min(a.cand_cnt[q], a.cap);
+    const uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+    const int32_t* ci = a.cand_id + (size_t)q * a.cap;
+    for (int b0 = 0; b0 < cnt; b0 += kWave) {
+        const int i = b0 + lane;
+        list_offer(L, a.K, i < cnt ? ck[i] : kKeyInvalid, i < cnt ? ci[i] : kIdInvalid);
+    }
+    list_store(L, lk, li);
+    uint64_t kk;
+    int32_t ki;
+    L.at(a.K - 1, kk, ki);
+    const bool full = kk != kKeyInvalid;
+    if (lane == 0) {
+        a.tau64[q] = full ? dist_of(kk) : (double)INFINITY;
+        if (a.tau_sq_out) a.tau_sq_out[q] = full ? __double2float_ru(dist_of(kk)) : INFINITY;
+    }
+    if (a.out_d) {
+        float* od = a.out_d + (size_t)q * a.K;
+        int64_t* oi = a.out_i + (size_t)q * a.K;
+        if (lane < a.K) {
+            const bool v = L.k0 != kKeyInvalid;
+            od[lane] = v ? (float)dist_of(L.k0) : INFINITY;
+            oi[lane] = v ? (int64_t)L.i0 : -1;
+        }
+        if constexpr (KP == 128) {
+            if (kWave + lane < a.K) {
+                const bool v = L.k1 != kKeyInvalid;
+                od[kWave + lane] = v ? (float)dist_of(L.k1) : INFINITY;
+                oi[kWave + lane] = v ? (int64_t)L.i1 : -1;
+            }
+        }
+    }
+}
+
+// One thread per (query, sorted position) pair: the Stage Y lower bound and the Stage X
+// upper bound over all dims, evaluated with exactly the scan kernel's arithmetic, then mapped
+// to bounds on the canonical float64 distance: lb = lb_f32 / lb_scale, ub = ub_f32 * ub_scale.
+__global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
+                                  const int32_t* __restrict__ cids,
+                                  const int64_t* __restrict__ spos, int n, double* lb,
+                                  double* ub) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int q = qids[i], cid = cids[i];
+    const int li = (int)(spos[i] - a.vec_off[cid]);
+    const int s = li / kWave, l = li % kWave;
+    const int D_pad = a.D_pad, T = a.T, D4 = D_pad >> 2;
+    const int tile = a.tile_off[cid] + s / (T / kWave), sub = s % (T / kWave);
+    const uint32_t* cp = a.sq8 + (size_t)tile * D4 * T + sub * kWave + l;
+    const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
+    float acc_l = 0.0f, acc_u = 0.0f;
+    for (int d4 = 0; d4 < D4; ++d4) {
+        const uint32_t w = cp[(size_t)d4 * T];
+        for (int j = 0; j < 4; ++j) {
+            const int d = 4 * d4 + j;
+            float b32, e32;
+            dim_params((double)a.vmin[off + d], a.delta[off + d], a.eps[off + d],
+                       a.xrot64[(size_t)q * D_pad + d], a.qerr[(size_t)q * D_pad + d], b32, e32);
+            const uint32_t c = (w >> (8 * j)) & 0xffu;
+            acc_l = lb_step(c, a.delta[off + d], b32, e32, acc_l);
+            acc_u = ub_step(c, a.delta[off + d], b32, e32, acc_u);
+        }
+    }
+    lb[i] = (double)acc_l / a.lb_scale;
+    ub[i] = (double)acc_u * a.ub_scale;
+}
+
+template __global__ void pair_scan_kernel<64, true, false>(ScanArgs);
+template __global__ void pair_scan_kernel<64, true, true>(ScanArgs);
+template __global__ void pair_scan_kernel<64, false, false>(ScanArgs);
+template __global__ void pair_scan_kernel<128, true, false>(ScanArgs);
+template __global__ void pair_scan_kernel<128, true, true>(ScanArgs);
+template __global__ void pair_scan_kernel<128, false, false>(ScanArgs);
+template __global__ void merge_kernel<64>(MergeArgs);
+template __global__ void merge_kernel<128>(MergeArgs);
+
+}  // namespace trident

@@ -1,0 +1,257 @@
+"""Drop-in search entry point with the reference's Python signature.
+
+``launch_trident_v4_search`` keeps the 41 positional arguments and 3 keywords of the
+reference PyBind11 export (src/trident_v4_kernels.cu:1606-1627, C++ body :1172-1604) and
+returns the kernel milliseconds when ``record_events`` is true, else 0.0.  It forwards to
+the C ABI ``trident_search`` of libtrident_hip.so on torch's current HIP stream.
+
+Differences from the reference, all stricter supersets:
+* shapes, dtypes and devices are validated and errors raise ``TridentError``;
+* K is read from ``topk_d.size(1)`` and honoured for every K <= 128 (the reference folds
+  the cascade and merge back to K = 10, src/trident_v4_kernels.cu:575-576, :984);
+* ``TRIDENT_UB_SEED`` is read here (once per call) and passed explicitly; the keyword
+  ``ub_seed`` overrides it;
+* the per-query candidate buffers are sized nprobe * K inside the library workspace, so
+  nothing is dropped (the reference silently drops past ``cand_buf_d.size(1)``, :955-958).
+  The reference workspace tensors (proj_buf, cdists_buf, p1_*/p2_*, topm_*, cand_*) are
+  accepted for signature compatibility; probe_cids_buf / probe_dqcs_buf receive the probes
+  and tau_sq the pass-1 threshold, as in the reference;
+* modes 0 (CM-SQ8+RR), 1 (K1) and 11 (Tribase) are comparison routes outside the lossless
+  path and raise NotImplementedError; ``warp_refine`` only selected a refinement schedule
+  and does not change results, so it is accepted and ignored.
+"""
+import ctypes
+import os
+import threading
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import TridentIndexView, TridentSearchOutputs, TridentSearchParams, check
+
+_ws_lock = threading.Lock()
+_ws_cache = {}
+_rot_cache = {}
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise _lib.TridentError(msg)
+
+
+def _check_tensor(name, t, dtype, device, dims=None, allow_host=False):
+    _need(isinstance(t, torch.Tensor), f"{name} must be a torch.Tensor")
+    _need(t.dtype == dtype, f"{name} must be {dtype}, got {t.dtype}")
+    _need(t.is_contiguous(), f"{name} must be contiguous")
+    if dims is not None:
+        _need(t.dim() == dims, f"{name} must be {dims}-D, got shape {tuple(t.shape)}")
+    if allow_host and t.device.type == "cpu":
+        _need(t.is_pinned(), f"{name} on the host must be pinned (hipHostMalloc) memory")
+    else:
+        _need(t.device == device, f"{name} must be on {device}, got {t.device}")
+
+
+def device_pointer(t: torch.Tensor) -> int:
+    """Device address of a tensor; pinned host tensors map through hipHostGetDevicePointer."""
+    if t.device.type != "cpu":
+        return t.data_ptr()
+    out = ctypes.c_void_p()
+    check(_lib.lib().trident_host_device_pointer(ctypes.c_void_p(t.data_ptr()), ctypes.byref(out)),
+          "trident_host_device_pointer")
+    return out.value
+
+
+def rotation_sq_bounds(W_combined: torch.Tensor, nlist: int, D: int):
+    """(min, max) squared singular values of the rotation block R = W_combined[:, nlist:nlist+D],
+    widened by 1e-12 relative; cached per tensor version."""
+    key = (W_combined.data_ptr(), tuple(W_combined.shape), W_combined._version, nlist, D)
+    hit = _rot_cache.get(key)
+    if hit is None:
+        R = W_combined[:, nlist:nlist + D].detach().to("cpu", torch.float64)
+        s = torch.linalg.svdvals(R)
+        hit = (float(s.min()) ** 2 * (1.0 - 1e-12), float(s.max()) ** 2 * (1.0 + 1e-12))
+        _rot_cache.clear()
+        _rot_cache[key] = hit
+    return hit
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Grow-only scratch buffer per device, reused across calls (the library itself never
+    allocates)."""
+    with _ws_lock:
+        buf = _ws_cache.get(device)
+        if buf is None or buf.numel() < nbytes:
+            buf = None
+            _ws_cache.pop(device, None)
+            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _ws_cache[device] = buf
+        return buf
+
+
+def release_workspaces() -> None:
+    with _ws_lock:
+        _ws_cache.clear()
+
+
+def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combined, b_combined,
+                    rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
+                    cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
+                    eps_dim, blk_bounds4) -> TridentIndexView:
+    v = TridentIndexView()
+    v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
+    v.tile_size = int(tile_size)
+    v.total_tiles = int(tile_orig_ids.shape[0]) if tile_orig_ids is not None else 0
+    v.num_blocks = int(blk_bounds4.numel() - 1) if blk_bounds4 is not None else 0
+    v.per_cluster_sq8 = int(per_cluster_sq8)
+    v.W_combined = _ptr(W_combined)
+    v.b_combined = _ptr(b_combined)
+    v.rot_sq_min, v.rot_sq_max = float(rot_sq_min), float(rot_sq_max)
+    v.sq8_packed = _ptr(sq8_packed)
+    v.tile_orig_ids = _ptr(tile_orig_ids)
+    v.tile_r_minmax = _ptr(tile_r_minmax) if tile_r_minmax is not None and tile_r_minmax.numel() >= 2 * v.total_tiles else None
+    v.cluster_tile_off = _ptr(cluster_tile_off)
+    v.cluster_vec_off = _ptr(cluster_vec_off)
+    v.xb_sorted = device_pointer(xb_sorted) if xb_sorted is not None else None
+    v.orig_ids_sorted = _ptr(orig_ids_sorted) if orig_ids_sorted is not None and orig_ids_sorted.device.type != "cpu" else None
+    v.vmin, v.delta, v.eps_dim = _ptr(vmin), _ptr(delta), _ptr(eps_dim)
+    v.blk_bounds4 = _ptr(blk_bounds4)
+    return v
+
+
+def env_ub_seed() -> int:
+    return int(os.environ.get("TRIDENT_UB_SEED", "0") or 0)
+
+
+def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: torch.Tensor,
+                topk_i: torch.Tensor, *, mode: int = 2, ub_seed: int = 0, use_l1: int = 0,
+                p_init: int = -1, probe_cids: Optional[torch.Tensor] = None,
+                probe_dqcs: Optional[torch.Tensor] = None, tau_sq: Optional[torch.Tensor] = None,
+                stats: Optional[torch.Tensor] = None, record_events: bool = False,
+                stream: Optional[torch.cuda.Stream] = None) -> float:
+    """Runs trident_search on an index view; all tensors already validated by the caller."""
+    B, K = int(xq.shape[0]), int(topk_d.shape[1])
+    L = _lib.lib()
+    nbytes = L.trident_workspace_bytes(ctypes.byref(view), max(B, 1), int(nprobe), K)
+    ws = workspace(xq.device, nbytes)
+    sp = TridentSearchParams(int(mode), B, K, int(nprobe), int(ub_seed), int(use_l1), int(p_init), 0)
+    out = TridentSearchOutputs()
+    out.topk_d, out.topk_i = topk_d.data_ptr(), topk_i.data_ptr()
+    out.probe_cids = _ptr(probe_cids)
+    out.probe_dqcs = _ptr(probe_dqcs)
+    ld = 0
+    if probe_cids is not None:
+        ld = int(probe_cids.shape[1])
+    elif probe_dqcs is not None:
+        ld = int(probe_dqcs.shape[1])
+    out.probe_ld = ld
+    out.tau_sq = _ptr(tau_sq)
+    out.stats = _ptr(stats)
+    st = stream if stream is not None else torch.cuda.current_stream(xq.device)
+    ev0 = ev1 = None
+    if record_events:
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(st)
+    rc = L.trident_search(ctypes.byref(view), ctypes.byref(sp), ctypes.c_void_p(xq.data_ptr()),
+                          ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()),
+                          ctypes.byref(out), ctypes.c_void_p(st.cuda_stream))
+    check(rc, "trident_search")
+    if record_events:
+        ev1.record(st)
+        ev1.synchronize()
+        return float(ev0.elapsed_time(ev1))
+    return 0.0
+
+
+def launch_trident_v4_search(
+    mode, tile_size, use_l1, per_cluster_sq8, rerank_m, nprobe,
+    xq_orig, W_combined, b_combined, W_coarse_only, b_coarse_only,
+    proj_buf, cdists_buf, probe_cids_buf, probe_dqcs_buf,
+    p1_cids_buf, p1_qids_buf, p1_dqcs_buf, p2_cids_buf, p2_qids_buf, p2_dqcs_buf,
+    sq8_packed, tile_orig_ids, tile_r_minmax, cluster_tile_off, cluster_vec_off,
+    xb_sorted, orig_ids_sorted, vmin, delta, eps_dim, blk_bounds4,
+    topk_d, topk_i, topm_buf_d, topm_buf_i, tau_sq,
+    cand_buf_d, cand_buf_i, cand_cnt, record_events,
+    warp_refine=1, stats_buf=None, r_vec_sorted=None,
+    *, ub_seed: Optional[int] = None, rot_sq_bounds=None, p_init: int = -1,
+):
+    """Batched lossless IVF search; signature of the reference extension (see module doc)."""
+    mode, nprobe = int(mode), int(nprobe)
+    if mode in (0, 1, 11):
+        raise NotImplementedError(
+            f"mode {mode} is a comparison route of the reference (CM-SQ8+RR / K1 / Tribase), "
+            "not part of the lossless path; use mode 2 (cascade) or 10 (cluster-major exact)")
+    _need(mode in (2, 10), f"unknown mode {mode}")
+    _need(int(rerank_m) == 0, "rerank_m applies to mode 0 only; must be 0 for modes 2 and 10")
+    dev = xq_orig.device
+    _need(dev.type == "cuda", "xq_orig must be a device tensor")
+    _check_tensor("xq_orig", xq_orig, torch.float32, dev, 2)
+    B, D = int(xq_orig.shape[0]), int(xq_orig.shape[1])
+    _check_tensor("W_coarse_only", W_coarse_only, torch.float32, dev, 2)
+    nlist = int(W_coarse_only.shape[1])
+    _check_tensor("W_combined", W_combined, torch.float32, dev, 2)
+    _need(W_combined.shape[0] == D, "W_combined rows must equal D")
+    D_pad = int(W_combined.shape[1]) - nlist
+    _need(D_pad >= D and D_pad % 32 == 0, f"W_combined implies D_pad={D_pad}; expected a multiple of 32 >= D")
+    _check_tensor("b_combined", b_combined, torch.float32, dev)
+    _need(b_combined.numel() == nlist + D_pad, "b_combined must have nlist + D_pad entries")
+    _check_tensor("topk_d", topk_d, torch.float32, dev, 2)
+    _check_tensor("topk_i", topk_i, torch.int64, dev, 2)
+    _need(topk_d.shape[0] == B and tuple(topk_i.shape) == tuple(topk_d.shape),
+          "topk_d / topk_i must be [B, K]")
+    K = int(topk_d.shape[1])
+    _check_tensor("cluster_vec_off", cluster_vec_off, torch.int32, dev, 1)
+    _check_tensor("cluster_tile_off", cluster_tile_off, torch.int32, dev, 1)
+    _need(cluster_vec_off.numel() == nlist + 1 and cluster_tile_off.numel() == nlist + 1,
+          "cluster offsets must have nlist + 1 entries")
+    _check_tensor("xb_sorted", xb_sorted, torch.float32, dev, 2, allow_host=True)
+    _need(xb_sorted.shape[1] == D, "xb_sorted must be [N, D]")
+    N = int(xb_sorted.shape[0])
+    _check_tensor("tile_orig_ids", tile_orig_ids, torch.int32, dev, 2)
+    _need(int(tile_orig_ids.shape[1]) == int(tile_size),
+          f"tile_size={tile_size} does not match the packed tiles ({tile_orig_ids.shape[1]})")
+    tiles = int(tile_orig_ids.shape[0])
+    if mode == 2:
+        _check_tensor("sq8_packed", sq8_packed, torch.int32, dev)
+        _need(sq8_packed.numel() == tiles * (D_pad // 4) * int(tile_size),
+              "sq8_packed must hold [tiles, D_pad/4, tile_size] words")
+        rows = nlist if int(per_cluster_sq8) else 1
+        for name, t in (("vmin", vmin), ("delta", delta), ("eps_dim", eps_dim)):
+            _check_tensor(name, t, torch.float32, dev)
+            _need(t.numel() == rows * D_pad, f"{name} must be [{rows}, D_pad]")
+        _check_tensor("blk_bounds4", blk_bounds4, torch.int32, dev, 1)
+    if stats_buf is not None:
+        _check_tensor("stats_buf", stats_buf, torch.int64, dev)
+        _need(stats_buf.numel() >= 4, "stats_buf needs 4 entries")
+    if probe_cids_buf is not None:
+        _check_tensor("probe_cids_buf", probe_cids_buf, torch.int32, dev, 2)
+        _need(probe_cids_buf.shape[0] >= B and probe_cids_buf.shape[1] >= nprobe, "probe_cids_buf too small")
+    if probe_dqcs_buf is not None:
+        _check_tensor("probe_dqcs_buf", probe_dqcs_buf, torch.float32, dev, 2)
+        _need(probe_dqcs_buf.shape[0] >= B and probe_dqcs_buf.shape[1] >= nprobe, "probe_dqcs_buf too small")
+        if probe_cids_buf is not None:
+            _need(probe_dqcs_buf.shape[1] == probe_cids_buf.shape[1], "probe buffers need one row stride")
+    if tau_sq is not None:
+        _check_tensor("tau_sq", tau_sq, torch.float32, dev)
+        _need(tau_sq.numel() >= B, "tau_sq needs B entries")
+
+    if rot_sq_bounds is None:
+        rot_sq_bounds = rotation_sq_bounds(W_combined, nlist, D)
+    view = make_index_view(
+        N=N, D=D, D_pad=D_pad, nlist=nlist, tile_size=tile_size, per_cluster_sq8=per_cluster_sq8,
+        W_combined=W_combined, b_combined=b_combined, rot_sq_min=rot_sq_bounds[0],
+        rot_sq_max=rot_sq_bounds[1], sq8_packed=sq8_packed if mode == 2 else None,
+        tile_orig_ids=tile_orig_ids, tile_r_minmax=tile_r_minmax,
+        cluster_tile_off=cluster_tile_off, cluster_vec_off=cluster_vec_off, xb_sorted=xb_sorted,
+        orig_ids_sorted=orig_ids_sorted, vmin=vmin if mode == 2 else None,
+        delta=delta if mode == 2 else None, eps_dim=eps_dim if mode == 2 else None,
+        blk_bounds4=blk_bounds4)
+    ub = env_ub_seed() if ub_seed is None else int(ub_seed)
+    return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
+                       use_l1=int(use_l1), p_init=p_init, probe_cids=probe_cids_buf,
+                       probe_dqcs=probe_dqcs_buf, tau_sq=tau_sq, stats=stats_buf,
+                       record_events=bool(record_events))

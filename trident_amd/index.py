@@ -1,0 +1,362 @@
+"""Index layout producer and search wrapper with the reference's Python API.
+
+``SharedClusterStorage`` and ``TridentV4Index`` mirror benchmarks/phase4a_suite.py:75-342
+(``choose_tile`` :61-62): same constructor arguments, same device tensors, same
+``search(...) -> (topk_d, topk_i, kern_ms)``.  The build runs as torch ops on the index
+device (the GPU at scale, in the manner of scripts/phase7_step2_gpu_build_verify.py:68-208)
+instead of per-cluster Python loops.
+
+What differs, and why:
+* Rotation map.  The query rotation the kernels apply is x -> x R + b with R and b exactly the
+  float32 values stored in W_combined / b_combined, evaluated in float64.  The base is rotated
+  with the same map (float64 GEMM), so base and query agree up to float64 rounding; the
+  orthogonality defect of the float32 R is measured once (``rot_sq_min``, ``rot_sq_max``,
+  squared extreme singular values) and enters the bounds as a factor.
+* eps is rigorous: eps[c, d] >= max over the cluster of |x_rot(exact) - (vmin + code delta)|,
+  computed in float64 and rounded up, plus the float64 rotation error bound.  The production
+  reference uses 0.5001 * delta (phase4a_suite.py:179), which does not bound the float32
+  rounding of the rotated coordinates; the strict variant it cites
+  (benchmarks/phase3a_benchmark.py:302) plays the same role as this one.
+* Codes follow the reference's closed form: code = clip(round_half_even((x32 - vmin) / delta),
+  0, 255) with delta = max((vmax - vmin) / 255, 1e-12) in float32 (phase4a_suite.py:163-176).
+* K is explicit (``k=``); output buffers are [max_batch, k].
+"""
+import math
+import time
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import ext as _ext
+
+_U53 = 2.0 ** -53
+
+
+def choose_tile(dim: int) -> int:
+    """Tile rule of benchmarks/phase4a_suite.py:61-62."""
+    return 256 if dim >= 256 else 64
+
+
+def _as_tensor(x, device, dtype):
+    if isinstance(x, torch.Tensor):
+        return x.to(device=device, dtype=dtype)
+    return torch.as_tensor(np.ascontiguousarray(x)).to(device=device, dtype=dtype)
+
+
+def round_up_f32(x64: torch.Tensor) -> torch.Tensor:
+    """Smallest float32 >= each float64 value."""
+    x32 = x64.to(torch.float32)
+    low = x32.to(torch.float64) < x64
+    if bool(low.any()):
+        x32 = torch.where(low, torch.nextafter(x32, torch.full_like(x32, math.inf)), x32)
+    return x32
+
+
+class PinnedHostBuffer:
+    """Device-mapped pinned host memory from ``hipHostMalloc`` (C ABI), viewed as a CPU tensor.
+
+    Replaces the torch ``pin_memory=True`` buffer of the out-of-core engine
+    (benchmarks/phase8_ooc_100m_4080.py:501-507): torch's caching host allocator rounds large
+    requests up, hipHostMalloc gives exactly the bytes asked for.
+    """
+
+    def __init__(self, shape, dtype=torch.float32):
+        import ctypes
+        from . import _lib
+        nbytes = int(np.prod(shape)) * torch.empty(0, dtype=dtype).element_size()
+        ptr = ctypes.c_void_p()
+        _lib.check(_lib.lib().trident_host_alloc_mapped(ctypes.c_size_t(max(nbytes, 1)), ctypes.byref(ptr)),
+                   "trident_host_alloc_mapped")
+        self._ptr = ptr.value
+        self.nbytes = nbytes
+        np_dtype = {torch.float32: np.float32, torch.int32: np.int32, torch.uint8: np.uint8}[dtype]
+        buf = (ctypes.c_char * max(nbytes, 1)).from_address(self._ptr)
+        arr = np.frombuffer(buf, dtype=np_dtype, count=int(np.prod(shape))).reshape(shape)
+        self.tensor = torch.from_numpy(arr)
+
+    def free(self):
+        if self._ptr:
+            from . import _lib
+            self.tensor = None
+            _lib.lib().trident_host_free(__import__("ctypes").c_void_p(self._ptr))
+            self._ptr = None
+
+
+class SharedClusterStorage:
+    """Cluster-sorted base (reference benchmarks/phase4a_suite.py:75-92).
+
+    ``xb_placement="device"`` keeps the FP32 base in HBM; ``"host"`` puts it in device-mapped
+    pinned host memory (the out-of-core mode) while ids and offsets stay on the device.
+    """
+
+    def __init__(self, xb_raw, list_ids, r_vec, nlist: int, device="cuda:0", xb_placement: str = "device"):
+        self.dev = torch.device(device)
+        lid = _as_tensor(list_ids, self.dev, torch.int64)
+        self.N = int(lid.numel())
+        self.nlist = int(nlist)
+        sort_perm = torch.argsort(lid, stable=True)
+        xb = xb_raw if isinstance(xb_raw, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(xb_raw))
+        self.D = int(xb.shape[1])
+        self.placement = xb_placement
+        self._host_buf = None
+        if xb_placement == "host":
+            self._host_buf = PinnedHostBuffer((self.N, self.D), torch.float32)
+            self.xb_sorted = self._host_buf.tensor
+            step = 1 << 22
+            perm_cpu = sort_perm.cpu()
+            for s in range(0, self.N, step):
+                idx = perm_cpu[s:s + step]
+                self.xb_sorted[s:s + step] = xb[idx.to(xb.device)].to("cpu", torch.float32)
+        else:
+            self.xb_sorted = xb.to(self.dev, torch.float32)[sort_perm].contiguous()
+        self.orig_ids_sorted = sort_perm.to(torch.int32).contiguous()
+        counts = torch.bincount(lid, minlength=nlist).to(torch.int32)
+        vec_off = torch.zeros(nlist + 1, dtype=torch.int32, device=self.dev)
+        vec_off[1:] = torch.cumsum(counts, 0).to(torch.int32)
+        self.cluster_vec_off = vec_off
+        self.counts = counts.cpu().numpy()
+        self.sort_perm = self.orig_ids_sorted.cpu().numpy()
+        self.list_ids_sorted = lid[sort_perm].to(torch.int32).contiguous()
+        self.r_vec_sorted = None if r_vec is None else _as_tensor(r_vec, self.dev, torch.float32)[sort_perm].contiguous()
+
+    def xb_sorted_host(self) -> np.ndarray:
+        return self.xb_sorted.cpu().numpy() if self.xb_sorted.device.type != "cpu" else self.xb_sorted.numpy()
+
+
+class TridentV4Index:
+    """PCA-rotated, per-cluster SQ8 index in the wave64 tile layout plus search buffers.
+
+    Layout (all on the index device; see the module docstring for the arithmetic):
+      sq8_packed   int32 [tiles, D_pad/4, T]: word [t, d4, s] packs dims 4*d4..4*d4+3 of slot
+                   s of tile t, byte 0 = dim 4*d4 (reference packing :221-228); for T = 64 a
+                   wave's 64 lanes read one contiguous 256-byte row per d4.
+      tile_orig_ids int32 [tiles, T] (-1 padded), tile_r_minmax f32 [tiles, 2]
+      cluster_tile_off int32 [nlist + 1]; vmin / delta / eps_pad f32 [nlist or 1, D_pad]
+      blk_bounds4  int32 [nb + 1] (32-dim blocks, or the variable scheme of :233-247)
+      W_combined [D, nlist + D_pad] = [-2 C^T | R | 0], b_combined = [|c|^2 | b | 0]
+    """
+
+    def __init__(self, storage: SharedClusterStorage, centroids, mean64, R64, tile_size: int = 256,
+                 per_cluster_sq8: int = 1, use_pca: int = 1, var_block: int = 0, max_batch: int = 1024,
+                 max_nprobe: int = 512, device="cuda:0", k: int = 10, chunk_rows: int = 1 << 20):
+        t_start = time.perf_counter()
+        self.storage = storage
+        self.dev = torch.device(device)
+        self.N, self.D, self.nlist = storage.N, storage.D, storage.nlist
+        self.tile_size = int(tile_size)
+        assert self.tile_size % 64 == 0, "tile_size must be a multiple of 64"
+        self.per_cluster_sq8 = int(per_cluster_sq8)
+        self.use_pca = int(use_pca)
+        self.var_block = int(var_block)
+        self.W_tile = self.tile_size // 32
+        self.D_pad = ((self.D + 31) // 32) * 32
+        self.D4 = self.D_pad // 4
+        self.k = int(k)
+        dev, N, D, D_pad, nlist, T = self.dev, self.N, self.D, self.D_pad, self.nlist, self.tile_size
+
+        # ---- rotation map x -> x R + b, R and b exactly the stored float32 values ----
+        if use_pca:
+            R32 = _as_tensor(R64, "cpu", torch.float64).to(torch.float32)
+            mean = _as_tensor(mean64, "cpu", torch.float64)
+        else:
+            R32 = torch.eye(D, dtype=torch.float32)
+            mean = torch.zeros(D, dtype=torch.float64)
+        b32 = (-(mean @ R32.to(torch.float64))).to(torch.float32)
+        s = torch.linalg.svdvals(R32.to(torch.float64))
+        self.rot_sq_min = float(s.min()) ** 2 * (1.0 - 1e-12)
+        self.rot_sq_max = float(s.max()) ** 2 * (1.0 + 1e-12)
+        R64d = R32.to(dev, torch.float64)
+        b64d = b32.to(dev, torch.float64)
+        colabs = R64d.abs().sum(0)                      # sum_j |R_jd|
+        rot_err_coef = (D + 2) * 2.0 * _U53             # generous float64 dot-product bound
+
+        # ---- coarse / fused projection matrices ----
+        cen = _as_tensor(centroids, dev, torch.float32).contiguous()
+        self.centroids = cen
+        c_norm_sq = (cen.double() ** 2).sum(1).to(torch.float32)
+        self.W_coarse_only = (-2.0 * cen.t()).contiguous()
+        self.b_coarse_only = c_norm_sq.unsqueeze(0).contiguous()
+        total_cols = nlist + D_pad
+        self.W_combined = torch.zeros((D, total_cols), device=dev, dtype=torch.float32)
+        self.b_combined = torch.zeros((1, total_cols), device=dev, dtype=torch.float32)
+        self.W_combined[:, :nlist] = self.W_coarse_only
+        self.W_combined[:, nlist:nlist + D] = R32.to(dev)
+        self.b_combined[0, :nlist] = c_norm_sq
+        self.b_combined[0, nlist:nlist + D] = b32.to(dev)
+
+        # ---- rotate, quantise, bound (chunked over sorted rows) ----
+        vec_off = storage.cluster_vec_off.to(torch.int64)
+        counts = (vec_off[1:] - vec_off[:-1])
+        lid_sorted = storage.list_ids_sorted.to(dev, torch.int64)
+        xb_src = storage.xb_sorted
+        rows_dev = lambda s, e: xb_src[s:e].to(dev, torch.float32)
+
+        def rotate(s, e):
+            x = rows_dev(s, e)
+            xr64 = torch.zeros((e - s, D_pad), device=dev, dtype=torch.float64)
+            xr64[:, :D] = x.double() @ R64d + b64d
+            err = torch.zeros_like(xr64)
+            err[:, :D] = rot_err_coef * (x.double().abs().amax(1, keepdim=True) * colabs + b64d.abs())
+            return xr64, err
+
+        rows = nlist if self.per_cluster_sq8 else 1
+        vmin = torch.full((rows, D_pad), math.inf, device=dev, dtype=torch.float32)
+        vmax = torch.full((rows, D_pad), -math.inf, device=dev, dtype=torch.float32)
+        for s in range(0, N, chunk_rows):
+            e = min(N, s + chunk_rows)
+            xr32 = rotate(s, e)[0].to(torch.float32)
+            if self.per_cluster_sq8:
+                idx = lid_sorted[s:e].unsqueeze(1).expand(-1, D_pad)
+                vmin.scatter_reduce_(0, idx, xr32, reduce="amin", include_self=True)
+                vmax.scatter_reduce_(0, idx, xr32, reduce="amax", include_self=True)
+            else:
+                vmin = torch.minimum(vmin, xr32.amin(0, keepdim=True))
+                vmax = torch.maximum(vmax, xr32.amax(0, keepdim=True))
+        empty = torch.isinf(vmin).all(1, keepdim=True)
+        vmin = torch.where(empty, torch.zeros_like(vmin), vmin)
+        vmax = torch.where(empty, torch.zeros_like(vmax), vmax)
+        delta = torch.clamp((vmax - vmin) / 255.0, min=1e-12)
+        delta = torch.where(empty, torch.ones_like(delta), delta)
+        codes = torch.empty((N, D_pad), device=dev, dtype=torch.uint8)
+        err_max = torch.zeros((rows, D_pad), device=dev, dtype=torch.float64)
+        for s in range(0, N, chunk_rows):
+            e = min(N, s + chunk_rows)
+            xr64, rerr = rotate(s, e)
+            xr32 = xr64.to(torch.float32)
+            ci = lid_sorted[s:e] if self.per_cluster_sq8 else torch.zeros(e - s, dtype=torch.int64, device=dev)
+            vm, dl = vmin[ci], delta[ci]
+            cd = torch.clamp(torch.round((xr32 - vm) / dl), 0.0, 255.0)
+            codes[s:e] = cd.to(torch.uint8)
+            xhat = vm.double() + cd.double() * dl.double()
+            err = (xr64 - xhat).abs() + rerr
+            idx = ci.unsqueeze(1).expand(-1, D_pad)
+            err_max.scatter_reduce_(0, idx, err, reduce="amax", include_self=True)
+        self.vmin_pad = vmin.contiguous()
+        self.delta_pad = delta.contiguous()
+        self.eps_pad = round_up_f32(err_max * (1.0 + 2.0 ** -20) + 1e-300).contiguous()
+
+        # ---- tiles (vectorised packing) ----
+        tile_counts = (counts + T - 1) // T
+        self.total_tiles = int(tile_counts.sum().item())
+        tile_off = torch.zeros(nlist + 1, dtype=torch.int64, device=dev)
+        tile_off[1:] = torch.cumsum(tile_counts, 0)
+        self.cluster_tile_off = tile_off.to(torch.int32).contiguous()
+        tiles = self.total_tiles
+        tile_cid = torch.repeat_interleave(torch.arange(nlist, device=dev), tile_counts)
+        tile_local = torch.arange(tiles, device=dev) - tile_off[tile_cid]
+        slot = torch.arange(T, device=dev).unsqueeze(0)
+        vidx = vec_off[tile_cid].unsqueeze(1) + tile_local.unsqueeze(1) * T + slot
+        valid = vidx < vec_off[tile_cid + 1].unsqueeze(1)
+        safe = torch.clamp(vidx, 0, max(N - 1, 0))
+        oids = storage.orig_ids_sorted.to(dev)
+        self.tile_orig_ids = torch.where(valid, oids[safe], torch.full_like(safe, -1).to(torch.int32)).to(torch.int32).contiguous()
+        codes32 = codes.view(torch.int32)                    # [N, D4], byte 0 = lowest dim
+        self.sq8_packed = torch.zeros((tiles, self.D4, T), device=dev, dtype=torch.int32)
+        tstep = max(1, (1 << 24) // max(T * self.D4, 1))
+        for ts in range(0, tiles, tstep):
+            te = min(tiles, ts + tstep)
+            g = codes32[safe[ts:te]]                         # [nt, T, D4]
+            g = torch.where(valid[ts:te].unsqueeze(-1), g, torch.zeros_like(g))
+            self.sq8_packed[ts:te] = g.permute(0, 2, 1)
+        self.tile_r_minmax = torch.zeros((tiles, 2), device=dev, dtype=torch.float32)
+        if storage.r_vec_sorted is not None:
+            r = storage.r_vec_sorted.to(dev)[safe]
+            self.tile_r_minmax[:, 0] = torch.where(valid, r, torch.full_like(r, math.inf)).amin(1)
+            self.tile_r_minmax[:, 1] = torch.where(valid, r, torch.full_like(r, -math.inf)).amax(1)
+        del codes, codes32
+
+        # ---- dimension blocks (reference :231-255) ----
+        if var_block:
+            if D_pad <= 128:
+                blk_dims = [16, 16, 32, 32, 32]
+            elif D_pad <= 256:
+                blk_dims = [16, 16, 32, 32, 64, 64, 32]
+            else:
+                blk_dims = [16, 16, 32, 32, 64, 64, 64, 128, 128, 256, 256]
+            bounds, cur = [0], 0
+            for bd in blk_dims:
+                cur += bd
+                if cur <= D_pad:
+                    bounds.append(cur // 4)
+            if bounds[-1] < self.D4:
+                bounds.append(self.D4)
+        else:
+            bounds = [0] + [d // 4 for d in range(32, D_pad + 1, 32)]
+            if bounds[-1] < self.D4:
+                bounds.append(self.D4)
+        self.blk_bounds4 = torch.tensor(bounds, device=dev, dtype=torch.int32)
+
+        # ---- search buffers (reference :257-278, K explicit) ----
+        self.max_batch, self.max_nprobe = int(max_batch), int(max_nprobe)
+        self._alloc_buffers()
+        self.build_time_s = time.perf_counter() - t_start
+
+    def _alloc_buffers(self):
+        dev, mb, mnp = self.dev, self.max_batch, self.max_nprobe
+        total_cols = self.nlist + self.D_pad
+        self.proj_buf = torch.zeros((1, total_cols), device=dev, dtype=torch.float32)
+        self.cdists_buf = torch.zeros((1, self.nlist), device=dev, dtype=torch.float32)
+        self.probe_cids_buf = torch.zeros((mb, mnp), device=dev, dtype=torch.int32)
+        self.probe_dqcs_buf = torch.zeros((mb, mnp), device=dev, dtype=torch.float32)
+        z32 = torch.zeros(1, device=dev, dtype=torch.int32)
+        zf = torch.zeros(1, device=dev, dtype=torch.float32)
+        self.p1_cids_buf = self.p2_cids_buf = self.p1_qids_buf = self.p2_qids_buf = z32
+        self.p1_dqcs_buf = self.p2_dqcs_buf = zf
+        self.topk_d_buf = torch.zeros((mb, self.k), device=dev, dtype=torch.float32)
+        self.topk_i_buf = torch.zeros((mb, self.k), device=dev, dtype=torch.int64)
+        self.topm_buf_d = torch.zeros((1, 1), device=dev, dtype=torch.float32)
+        self.topm_buf_i = torch.zeros((1, 1), device=dev, dtype=torch.int64)
+        self.tau_sq_buf = torch.zeros(mb, device=dev, dtype=torch.float32)
+        self.cand_buf_d = torch.zeros((1, 1), device=dev, dtype=torch.float32)
+        self.cand_buf_i = torch.zeros((1, 1), device=dev, dtype=torch.int64)
+        self.cand_cnt = torch.zeros(mb, device=dev, dtype=torch.int32)
+
+    def set_k(self, k: int):
+        if int(k) != self.k:
+            self.k = int(k)
+            self.topk_d_buf = torch.zeros((self.max_batch, self.k), device=self.dev, dtype=torch.float32)
+            self.topk_i_buf = torch.zeros((self.max_batch, self.k), device=self.dev, dtype=torch.int64)
+
+    def sq8_bytes(self) -> int:
+        return int(self.sq8_packed.numel() * 4)
+
+    def search(self, xq_gpu: torch.Tensor, nprobe: int, mode: int = 2, use_l1: int = 0, rerank_m: int = 0,
+               tile_override: int = 0, warp_refine: int = 1, stats_buf: Optional[torch.Tensor] = None,
+               record_kernel_ms: bool = False, k: Optional[int] = None, ub_seed: Optional[int] = None):
+        """Reference TridentV4Index.search (phase4a_suite.py:280-342) plus ``k=`` / ``ub_seed=``."""
+        if k is not None:
+            self.set_k(k)
+        B = int(xq_gpu.shape[0])
+        if B > self.max_batch:
+            raise ValueError(f"batch {B} exceeds max_batch={self.max_batch}")
+        if nprobe > self.max_nprobe:
+            raise ValueError(f"nprobe {nprobe} exceeds max_nprobe={self.max_nprobe}")
+        tsize = tile_override if tile_override > 0 else self.tile_size
+        topk_d = self.topk_d_buf[:B]
+        topk_i = self.topk_i_buf[:B]
+        st = self.storage
+        kern_ms = _ext.launch_trident_v4_search(
+            int(mode), int(tsize), int(use_l1), int(self.per_cluster_sq8), int(rerank_m), int(nprobe),
+            xq_gpu, self.W_combined, self.b_combined, self.W_coarse_only, self.b_coarse_only,
+            self.proj_buf, self.cdists_buf, self.probe_cids_buf, self.probe_dqcs_buf,
+            self.p1_cids_buf, self.p1_qids_buf, self.p1_dqcs_buf,
+            self.p2_cids_buf, self.p2_qids_buf, self.p2_dqcs_buf,
+            self.sq8_packed, self.tile_orig_ids, self.tile_r_minmax, self.cluster_tile_off,
+            st.cluster_vec_off, st.xb_sorted, st.orig_ids_sorted,
+            self.vmin_pad, self.delta_pad, self.eps_pad, self.blk_bounds4,
+            topk_d, topk_i, self.topm_buf_d, self.topm_buf_i, self.tau_sq_buf,
+            self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
+            bool(record_kernel_ms), int(warp_refine), stats_buf,
+            ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max))
+        return topk_d, topk_i, kern_ms
+
+    # ---- views used by tests / oracle (host copies) ----
+    def host_arrays(self):
+        st = self.storage
+        return dict(
+            xb_sorted=st.xb_sorted_host(),
+            orig_ids_sorted=st.orig_ids_sorted.cpu().numpy(),
+            vec_off=st.cluster_vec_off.cpu().numpy(),
+            centroids=self.centroids.cpu().numpy(),
+        )
