@@ -80,16 +80,34 @@ typedef struct TridentSearchParams {
     int32_t reserved;
 } TridentSearchParams;
 
+/* Stage boundaries at which trident_search records the caller's events (if given). */
+enum TridentStageEvent {
+    TRIDENT_EV_START = 0,       /* before the front end */
+    TRIDENT_EV_PROBED = 1,      /* rotation + coarse distances + top-nprobe done */
+    TRIDENT_EV_GROUPED = 2,     /* pairs grouped by cluster */
+    TRIDENT_EV_P1_SCAN = 3,     /* pass-1 pair scan done */
+    TRIDENT_EV_P1_MERGE = 4,    /* pass-1 merge (threshold) done */
+    TRIDENT_EV_P2_SCAN = 5,     /* pass-2 pair scan done */
+    TRIDENT_EV_END = 6,         /* final merge done */
+    TRIDENT_EV_COUNT = 7
+};
+
 typedef struct TridentSearchOutputs {
     float* topk_d;        /* [B, K] squared L2 distances (float32), +inf if missing */
     int64_t* topk_i;      /* [B, K] original ids, -1 if missing */
     int32_t* probe_cids;  /* [B, probe_ld] probed clusters in (d, cid) order, or NULL */
     float* probe_dqcs;    /* [B, probe_ld] |q - c| of each probe, or NULL */
     int32_t probe_ld;     /* row stride of probe_cids / probe_dqcs (>= nprobe) */
-    int32_t reserved;
+    int32_t n_events;     /* entries in `events` (<= TRIDENT_EV_COUNT) */
     float* tau_sq;        /* [B] pass-1 threshold (squared, rounded up), or NULL */
     int64_t* stats;       /* [4] candidates, scanned dims, survivors, refined-inserted; or NULL */
+    void* const* events;  /* hipEvent_t handles recorded at TridentStageEvent points, or NULL */
 } TridentSearchOutputs;
+
+/* Timing events for TridentSearchOutputs.events (hipEventCreate / Destroy / ElapsedTime). */
+int trident_event_create(void** event);
+int trident_event_destroy(void* event);
+int trident_event_elapsed_ms(void* start, void* stop, float* ms);
 
 /* Bytes of scratch trident_search needs for batches up to max_B x max_nprobe x max_K. */
 size_t trident_workspace_bytes(const TridentIndexView* ix, int32_t max_B, int32_t max_nprobe,

@@ -1,0 +1,192 @@
+"""Index layout producer (CPU torch): closed forms and invariants of the SQ8 layout.
+
+Reference layout: benchmarks/phase4a_suite.py:95-278.  Pinned here:
+  * W_combined / b_combined structure ([-2 C^T | R | 0], [|c|^2 | b | 0]) and exact centroid
+    recovery c = -0.5 W;
+  * rotation bounds bracket the squared singular values of the float32 rotation;
+  * codes equal the closed form clip(round_half_even((x32 - vmin) / delta), 0, 255);
+  * eps bounds the quantisation error of every vector against the float64 rotation;
+  * unpacking sq8_packed / tile_orig_ids recovers every code and id (the wave64 layout);
+  * block bounds (uniform and variable schemes);
+  * the Stage Y / Stage X bound arithmetic, restated in float32 numpy, brackets the float64
+    distance: lb <= d64 <= ub.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from trident_amd import clustering, datagen
+from trident_amd.index import SharedClusterStorage, TridentV4Index, choose_tile
+
+
+def build(xb, nlist, T=64, var_block=0, per_cluster=1, seed=0):
+    cen, lid, r, mean64, R64, _ = clustering.train_clustering(xb, nlist, seed=seed, niter=4)
+    st = SharedClusterStorage(xb.numpy(), lid, r, nlist, device="cpu")
+    ix = TridentV4Index(st, cen, mean64, R64, tile_size=T, per_cluster_sq8=per_cluster, var_block=var_block,
+                        device="cpu", max_batch=8, max_nprobe=8)
+    return ix, cen, lid
+
+
+@pytest.fixture(scope="module")
+def hist_ix():
+    xb, xq = datagen.cfg2(N=6000, D=128, B=16, n_centers=32, seed=3)
+    ix, cen, lid = build(xb, 24)
+    return ix, xb.numpy(), xq.numpy(), cen, lid
+
+
+@pytest.fixture(scope="module")
+def gmm_ix():
+    xb, xq = datagen.cfg1(N=5000, D=72, B=16, n_centers=16, seed=4)
+    ix, cen, lid = build(xb, 20)
+    return ix, xb.numpy(), xq.numpy(), cen, lid
+
+
+def test_choose_tile():
+    assert choose_tile(128) == 64 and choose_tile(96) == 64 and choose_tile(256) == 256 and choose_tile(960) == 256
+
+
+def test_fused_projection_layout(gmm_ix):
+    ix, _, _, cen, _ = gmm_ix
+    nlist, D, D_pad = ix.nlist, ix.D, ix.D_pad
+    W, b = ix.W_combined.numpy(), ix.b_combined.numpy()[0]
+    assert W.shape == (D, nlist + D_pad) and D_pad == 96
+    assert np.array_equal(-0.5 * W[:, :nlist].T, cen)          # exact centroid recovery
+    assert np.allclose(b[:nlist], (cen.astype(np.float64) ** 2).sum(1), rtol=1e-6)
+    assert np.all(W[:, nlist + D:] == 0) and np.all(b[nlist + D:] == 0)
+    R = W[:, nlist:nlist + D].astype(np.float64)
+    s = np.linalg.svd(R, compute_uv=False)
+    assert ix.rot_sq_min <= s.min() ** 2 <= s.max() ** 2 <= ix.rot_sq_max
+    assert abs(ix.rot_sq_max - 1) < 1e-5 and abs(1 - ix.rot_sq_min) < 1e-5
+    assert np.abs(R.T @ R - np.eye(D)).max() < 1e-5
+
+
+def rotated64(ix):
+    """Base rotated in float64 with the stored float32 map, in sorted order."""
+    W = ix.W_combined.numpy().astype(np.float64)
+    R = W[:, ix.nlist:ix.nlist + ix.D]
+    b = ix.b_combined.numpy()[0, ix.nlist:ix.nlist + ix.D].astype(np.float64)
+    xs = ix.storage.xb_sorted.numpy().astype(np.float64)
+    out = np.zeros((ix.N, ix.D_pad))
+    out[:, :ix.D] = xs @ R + b
+    return out
+
+
+def unpack_codes(ix):
+    """[N, D_pad] uint8 codes recovered from sq8_packed [tiles, D4, T] in sorted order."""
+    T, D4 = ix.tile_size, ix.D4
+    sq = ix.sq8_packed.numpy().view(np.uint32)            # [tiles, D4, T]
+    toff = ix.cluster_tile_off.numpy()
+    voff = ix.storage.cluster_vec_off.numpy()
+    codes = np.zeros((ix.N, ix.D_pad), np.uint8)
+    oids = np.zeros(ix.N, np.int64)
+    for c in range(ix.nlist):
+        for v in range(voff[c], voff[c + 1]):
+            li = v - voff[c]
+            t, s = toff[c] + li // T, li % T
+            words = sq[t, :, s]                           # word d4 packs dims 4*d4 .. 4*d4+3
+            codes[v] = np.stack([(words >> (8 * j)) & 0xFF for j in range(4)], 1).reshape(-1).astype(np.uint8)
+            oids[v] = ix.tile_orig_ids.numpy()[t, s]
+    return codes, oids
+
+
+def test_codes_closed_form_and_packing(hist_ix):
+    ix, xb, _, _, lid = hist_ix
+    xr64 = rotated64(ix)
+    xr32 = xr64.astype(np.float32)
+    lid_s = ix.storage.list_ids_sorted.numpy().astype(np.int64)
+    vmin, delta = ix.vmin_pad.numpy(), ix.delta_pad.numpy()
+    expect = np.clip(np.round((xr32 - vmin[lid_s]) / delta[lid_s]), 0, 255).astype(np.uint8)
+    codes, oids = unpack_codes(ix)
+    assert np.array_equal(codes, expect)
+    assert np.array_equal(oids, ix.storage.orig_ids_sorted.numpy())
+    # padded tile slots are -1
+    T = ix.tile_size
+    assert (ix.tile_orig_ids.numpy() >= 0).sum() == ix.N
+    assert ix.sq8_packed.shape == (ix.total_tiles, ix.D4, T)
+    # vmin/delta closed form per cluster
+    for c in range(ix.nlist):
+        m = lid_s == c
+        if m.any():
+            assert np.array_equal(vmin[c], xr32[m].min(0))
+            assert np.array_equal(delta[c], np.maximum((xr32[m].max(0) - xr32[m].min(0)) / np.float32(255.0),
+                                                       np.float32(1e-12)))
+
+
+@pytest.mark.parametrize("which", ["hist", "gmm"])
+def test_eps_bounds_quantisation_error(which, hist_ix, gmm_ix):
+    ix = (hist_ix if which == "hist" else gmm_ix)[0]
+    xr64 = rotated64(ix)
+    codes, _ = unpack_codes(ix)
+    lid_s = ix.storage.list_ids_sorted.numpy().astype(np.int64)
+    vmin = ix.vmin_pad.numpy().astype(np.float64)[lid_s]
+    dl = ix.delta_pad.numpy().astype(np.float64)[lid_s]
+    xhat = vmin + codes.astype(np.float64) * dl
+    err = np.abs(xr64 - xhat)
+    eps = ix.eps_pad.numpy().astype(np.float64)[lid_s]
+    assert (err <= eps).all()
+    # and eps is tight: about half a quantisation step where the dimension has spread
+    live = dl > 1e-6
+    assert np.median(eps[live] / dl[live]) < 0.51
+
+
+def test_block_bounds():
+    xb, _ = datagen.cfg1(N=600, D=128, B=4, n_centers=4, seed=5)
+    ix, _, _ = build(xb, 4, var_block=0)
+    assert ix.blk_bounds4.tolist() == [0, 8, 16, 24, 32]
+    ix, _, _ = build(xb, 4, var_block=1)
+    assert ix.blk_bounds4.tolist() == [0, 4, 8, 16, 24, 32]
+    xb, _ = datagen.cfg3(N=700, D=960, B=4, n_centers=4, seed=5)
+    ix, _, _ = build(xb, 4, T=256)
+    b = ix.blk_bounds4.tolist()
+    assert b[0] == 0 and b[-1] == 240 and len(b) == 31 and ix.sq8_packed.shape[2] == 256
+
+
+def fmaf(a, b, c):
+    return (a.astype(np.float64) * b.astype(np.float64) + c.astype(np.float64)).astype(np.float32)
+
+
+def test_bounds_bracket_distance_cpu_restatement(hist_ix, gmm_ix):
+    """float32 numpy restatement of the kernel's dim_params / lb_step / ub_step."""
+    for ix, xb, xq, cen, lid in (hist_ix, gmm_ix):
+        W = ix.W_combined.numpy().astype(np.float64)
+        R = W[:, ix.nlist:ix.nlist + ix.D]
+        bvec = ix.b_combined.numpy()[0, ix.nlist:].astype(np.float64)
+        codes, _ = unpack_codes(ix)
+        voff = ix.storage.cluster_vec_off.numpy()
+        xs = ix.storage.xb_sorted.numpy().astype(np.float64)
+        rho = (ix.D_pad + 4) * 2.0 ** -24
+        lb_scale = ix.rot_sq_max * (1 + rho) * (1 + 1e-12)
+        ub_scale = (1 + rho) * (1 + 1e-12) / ix.rot_sq_min
+        for qi in range(len(xq)):
+            q = xq[qi].astype(np.float64)
+            xr = np.zeros(ix.D_pad)
+            xr[:ix.D] = q @ R
+            xr += bvec
+            qe = (ix.D + 3) * 2.0 ** -52 * (np.abs(q[:, None] * np.pad(R, ((0, 0), (0, ix.D_pad - ix.D)))).sum(0) + np.abs(bvec))
+            for c in range(0, ix.nlist, 5):
+                s, e = voff[c], voff[c + 1]
+                if s == e:
+                    continue
+                vm = ix.vmin_pad.numpy()[c].astype(np.float64)
+                dl = ix.delta_pad.numpy()[c]
+                ep = ix.eps_pad.numpy()[c].astype(np.float64)
+                b64 = vm - xr
+                b32 = b64.astype(np.float32)
+                E = np.abs(b32.astype(np.float64) - b64) + qe + 2.0 ** -52 * np.abs(b64) + \
+                    2.0 ** -24 * (255.0 * dl.astype(np.float64) + np.abs(b32.astype(np.float64))) * (1 + 2.0 ** -20) + 2.0 ** -126
+                e32 = ((ep + E) * (1 + 2.0 ** -50)).astype(np.float32)
+                e32 = np.where(e32.astype(np.float64) < (ep + E), np.nextafter(e32, np.float32(np.inf)), e32)
+                cd = codes[s:e].astype(np.float32)
+                a = fmaf(cd, dl[None], b32[None])
+                lb = np.zeros(e - s, np.float32)
+                ub = np.zeros(e - s, np.float32)
+                for d in range(ix.D_pad):
+                    l = np.maximum(np.abs(a[:, d]) - e32[d], np.float32(0))
+                    lb = fmaf(l, l, lb)
+                    u = np.abs(a[:, d]) + e32[d]
+                    ub = fmaf(u, u, ub)
+                d64 = ((xs[s:e] - q) ** 2).sum(1)
+                assert (lb.astype(np.float64) / lb_scale <= d64 * (1 + 1e-12)).all()
+                assert (ub.astype(np.float64) * ub_scale >= d64 * (1 - 1e-12)).all()

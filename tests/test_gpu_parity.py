@@ -186,3 +186,59 @@ def test_sq8_bounds_bracket_exact_distance(aniso, hist, dev):
         assert (ub >= d64).all(), f"ub < d64 by {(d64 - ub).max()}"
         # the bounds must also be useful: most of the distance is captured
         assert np.median(lb / d64) > 0.5 and np.median(ub / d64) < 2.0
+
+
+def test_out_of_core_host_mapped_base(dev):
+    """FP32 base in hipHostMalloc-mapped host memory; Stage Z reads survivors over PCIe."""
+    xb, xq = datagen.cfg2(N=30_000, D=128, B=100, n_centers=64, seed=8)
+    b = build_index(xb, 64, dev, xb_placement="host", max_batch=128)
+    assert b.ix.storage.xb_sorted.device.type == "cpu"
+    xq = xq.numpy()
+    _, rd, ri = oracle_search(b, xq, 12, 10)
+    for mode, ub in ((2, 0), (2, 1), (10, 0)):
+        d, i = run_search(b, _q(xq, dev), 12, 10, mode=mode, ub=ub)
+        assert_exact(d, i, rd, ri, f"ooc mode={mode} ub={ub}")
+    b.ix.storage._host_buf.free()
+
+
+def test_group_pairs_entry_point(dev):
+    """trident_group_pairs: each pass holds exactly its (cluster, query) pairs, contiguous per
+    cluster at seg_off (reference counting sort, src/trident_v4_kernels.cu:168-263)."""
+    rng = np.random.default_rng(12)
+    B, nprobe, nlist, p_init, ld = 300, 20, 50, 3, 24
+    probes = np.stack([rng.choice(nlist, nprobe, replace=False) for _ in range(B)]).astype(np.int32)
+    pc = torch.zeros((B, ld), dtype=torch.int32, device=dev)
+    pc[:, :nprobe] = torch.as_tensor(probes).to(dev)
+    p1c = torch.full((B * p_init,), -7, dtype=torch.int32, device=dev)
+    p1q = torch.full_like(p1c, -7)
+    p2c = torch.full((B * (nprobe - p_init),), -7, dtype=torch.int32, device=dev)
+    p2q = torch.full_like(p2c, -7)
+    seg = torch.zeros(2 * (nlist + 1), dtype=torch.int32, device=dev)
+    cnt = torch.zeros_like(seg)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = _lib.lib().trident_group_pairs(P(pc), ld, B, nprobe, p_init, nlist, P(p1c), P(p1q), P(p2c), P(p2q),
+                                        P(seg), P(cnt), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, "trident_group_pairs")
+    torch.cuda.synchronize()
+    seg = seg.cpu().numpy().reshape(2, nlist + 1)
+    for pas, (cc, qq, lo, hi) in enumerate(((p1c, p1q, 0, p_init), (p2c, p2q, p_init, nprobe))):
+        cc, qq = cc.cpu().numpy(), qq.cpu().numpy()
+        want = sorted((int(probes[q, p]), q) for q in range(B) for p in range(lo, hi))
+        assert sorted(zip(cc.tolist(), qq.tolist())) == want
+        assert np.all(np.diff(cc) >= 0), "pairs not grouped by cluster"
+        for c in range(nlist):
+            assert np.all(cc[seg[pas, c]:seg[pas, c + 1]] == c)
+
+
+def test_router_calibration_and_routed_search(hist, dev):
+    from trident_amd import router
+    b, xq = hist
+    W0, rows = router.calibrate_w0(b.ix, _q(xq, dev), 16, batches=(1, 8, 64), warmup=1, iters=2)
+    assert len(rows) == 3 and all(r["ms_cm"] > 0 and r["ms_cascade"] > 0 for r in rows)
+    r = router.CostRouter(b.ix, W0=router.work_measure(8, 16, b.ix.N, b.ix.nlist, b.ix.D))
+    _, rd, ri = oracle_search(b, xq[:64], 16, 10)
+    for B, want in ((4, 10), (64, 2)):
+        d, i, _, mode = r.search(_q(xq[:B], dev), 16, k=10)
+        torch.cuda.synchronize()
+        assert mode == want
+        assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd[:B], ri[:B], f"routed B={B}")

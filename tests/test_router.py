@@ -1,0 +1,37 @@
+"""Cost router closed forms (reference benchmarks/phase4a_suite.py:1018, :1063-1079)."""
+import pytest
+
+from trident_amd import router
+
+
+def test_work_measure_closed_form():
+    # cfg 1: B=1000, nprobe=16, N=1e5, nlist=256, D=128 -> 8.0e8
+    assert router.work_measure(1000, 16, 100_000, 256, 128) == pytest.approx(8.0e8)
+    # cfg 5: B=1e4, nprobe=128, N=1e8, nlist=16384, D=128 -> ~1.0e12
+    assert router.work_measure(10_000, 128, 100_000_000, 16384, 128) == pytest.approx(1.0e12, rel=1e-3)
+
+
+def test_choose_mode_threshold():
+    W0 = router.W0_REFERENCE_A100
+    assert router.choose_mode(W0 - 1, W0) == 10
+    assert router.choose_mode(W0, W0) == 2
+    assert router.choose_mode(8.0e8, 9.0e8) == 10   # cfg 1 with the reference's README W0
+
+
+def test_router_uses_index_shape():
+    class Fake:
+        N, nlist, D, max_batch = 1_000_000, 1024, 128, 1024
+        calls = []
+
+        def search(self, xq, nprobe, mode, **kw):
+            self.calls.append(mode)
+            return (None, None, 0.0)
+
+    class Q:
+        shape = (1, 128)
+
+    f = Fake()
+    r = router.CostRouter(f, W0=1e9)
+    assert r.mode_for(1, 8) == 10          # 1 * 8 * 976.6 * 128 = 1e6 < 1e9
+    assert r.mode_for(10_000, 64) == 2
+    assert r.search(Q(), 8)[-1] == 10 and f.calls == [10]

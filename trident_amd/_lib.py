@@ -38,7 +38,12 @@ class TridentSearchParams(ctypes.Structure):
 
 class TridentSearchOutputs(ctypes.Structure):
     _fields_ = [("topk_d", _P), ("topk_i", _P), ("probe_cids", _P), ("probe_dqcs", _P),
-                ("probe_ld", _i32), ("reserved", _i32), ("tau_sq", _P), ("stats", _P)]
+                ("probe_ld", _i32), ("n_events", _i32), ("tau_sq", _P), ("stats", _P),
+                ("events", ctypes.POINTER(_P))]
+
+
+# Stage boundaries recorded into TridentSearchOutputs.events (enum TridentStageEvent).
+EV_START, EV_PROBED, EV_GROUPED, EV_P1_SCAN, EV_P1_MERGE, EV_P2_SCAN, EV_END, EV_COUNT = range(8)
 
 
 EXPORTS = {
@@ -54,6 +59,9 @@ EXPORTS = {
     "trident_host_alloc_mapped": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_P)]),
     "trident_host_free": (ctypes.c_int, [_P]),
     "trident_host_device_pointer": (ctypes.c_int, [_P, ctypes.POINTER(_P)]),
+    "trident_event_create": (ctypes.c_int, [ctypes.POINTER(_P)]),
+    "trident_event_destroy": (ctypes.c_int, [_P]),
+    "trident_event_elapsed_ms": (ctypes.c_int, [_P, _P, ctypes.POINTER(ctypes.c_float)]),
     "trident_last_error": (ctypes.c_char_p, []),
     "trident_abi_version": (ctypes.c_int, []),
 }
@@ -86,3 +94,26 @@ def check(rc: int, what: str) -> None:
     if rc != TRIDENT_OK:
         msg = lib().trident_last_error().decode(errors="replace")
         raise TridentError(f"{what} failed (code {rc}): {msg}")
+
+
+class StageEvents:
+    """One hipEvent_t per stage boundary, for timing the library's kernels on their stream."""
+
+    def __init__(self):
+        self.handles = (_P * EV_COUNT)()
+        for i in range(EV_COUNT):
+            h = _P()
+            check(lib().trident_event_create(ctypes.byref(h)), "trident_event_create")
+            self.handles[i] = h.value
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        ms = ctypes.c_float()
+        check(lib().trident_event_elapsed_ms(self.handles[a], self.handles[b], ctypes.byref(ms)),
+              "trident_event_elapsed_ms")
+        return float(ms.value)
+
+    def destroy(self):
+        for i in range(EV_COUNT):
+            if self.handles[i]:
+                lib().trident_event_destroy(self.handles[i])
+                self.handles[i] = None

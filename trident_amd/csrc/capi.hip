@@ -81,6 +81,7 @@ struct Workspace {
     uint64_t* list_key;
     int32_t* list_id;
     double* tau64;
+    unsigned long long* stat_slots;  // [kStatSlots, 4] telemetry partials
     size_t bytes;
 };
 
@@ -107,6 +108,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.list_key = c.take<uint64_t>(B * KP);
     w.list_id = c.take<int32_t>(B * KP);
     w.tau64 = c.take<double>(B);
+    w.stat_slots = c.take<unsigned long long>((size_t)kStatSlots * 4);
     w.bytes = c.off;
     return w;
 }
@@ -144,7 +146,7 @@ int validate_cascade_index(const TridentIndexView* ix) {
 double rho_of(int D_pad) { return (double)(D_pad + 4) * 0x1p-24; }
 
 ScanArgs make_scan_args(const TridentIndexView* ix, const Workspace& w, int K, int64_t cap,
-                        int use_l1, int64_t* stats) {
+                        int use_l1, unsigned long long* stats) {
     ScanArgs a{};
     a.sq8 = ix->sq8_packed;
     a.tile_oids = ix->tile_orig_ids;
@@ -170,7 +172,7 @@ ScanArgs make_scan_args(const TridentIndexView* ix, const Workspace& w, int K, i
     a.cand_cnt = w.cand_cnt;
     a.cap = (int)cap;
     a.K = K;
-    a.stats = reinterpret_cast<unsigned long long*>(stats);
+    a.stats = stats;
     const double rho = rho_of(ix->D_pad);
     a.lb_scale = ix->rot_sq_max * (1.0 + rho) * (1.0 + 1e-12);
     a.ub_scale = (1.0 + rho) * (1.0 + 1e-12) / ix->rot_sq_min;
@@ -375,9 +377,17 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     int32_t* pc = w.probe_cids;
     float* pd = w.probe_dqcs;
     const int ld = nprobe;
+    auto mark = [&](int ev) -> int {
+        if (!out->events || ev >= out->n_events || !out->events[ev]) return TRIDENT_OK;
+        hipError_t e = hipEventRecord(static_cast<hipEvent_t>(out->events[ev]), st);
+        return e == hipSuccess ? TRIDENT_OK
+                               : fail(TRIDENT_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(e));
+    };
+    if ((rc = mark(TRIDENT_EV_START))) return rc;
     if ((rc = run_front_end(ix, xq, B, nprobe, cascade, w, out->probe_cids, out->probe_dqcs,
                             out->probe_ld, st)))
         return rc;
+    if ((rc = mark(TRIDENT_EV_PROBED))) return rc;
 
     const int64_t M1 = (int64_t)B * p_init, M2 = (int64_t)B * (nprobe - p_init);
     int32_t *p1c = w.pair_cids, *p1q = w.pair_qids;
@@ -387,11 +397,16 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if ((rc = group_pairs(pc, pd, ld, B, nprobe, p_init, ix->nlist, w.counts, w.seg_off, w.cursor,
                           p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, st)))
         return rc;
+    if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
     const int KP = K <= 64 ? 64 : 128;
     const int64_t cap = (int64_t)nprobe * K;
-    if (out->stats && (rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
-    ScanArgs a = make_scan_args(ix, w, K, cap, cascade ? sp->use_l1 : 0, out->stats);
+    if (out->stats) {
+        if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
+        if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
+    }
+    ScanArgs a = make_scan_args(ix, w, K, cap, cascade ? sp->use_l1 : 0,
+                                out->stats ? w.stat_slots : nullptr);
     MergeArgs m{};
     m.B = B;
     m.K = K;
@@ -413,13 +428,17 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         const bool ub1 = cascade && sp->ub_seed != 0;
         rc = KP == 64 ? dispatch_scan<64>(a, cascade, ub1, st) : dispatch_scan<128>(a, cascade, ub1, st);
         if (rc) return rc;
+        if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
         m.use_prev = 0;
         m.tau_sq_out = out->tau_sq;
         const bool last = M2 == 0;
         m.out_d = last ? out->topk_d : nullptr;
         m.out_i = last ? out->topk_i : nullptr;
         if ((rc = launch_merge(m, KP, st))) return rc;
+    } else if ((rc = mark(TRIDENT_EV_P1_SCAN))) {
+        return rc;
     }
+    if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
     if (M2 > 0) {
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
         a.pair_cid = p2c;
@@ -430,11 +449,19 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         const bool ub2 = cascade && (sp->ub_seed == 2 || (sp->ub_seed == 1 && M1 == 0));
         rc = KP == 64 ? dispatch_scan<64>(a, cascade, ub2, st) : dispatch_scan<128>(a, cascade, ub2, st);
         if (rc) return rc;
+        if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
         m.use_prev = M1 > 0 ? 1 : 0;
         m.tau_sq_out = M1 > 0 ? nullptr : out->tau_sq;
         m.out_d = out->topk_d;
         m.out_i = out->topk_i;
         if ((rc = launch_merge(m, KP, st))) return rc;
+    } else if ((rc = mark(TRIDENT_EV_P2_SCAN))) {
+        return rc;
+    }
+    if ((rc = mark(TRIDENT_EV_END))) return rc;
+    if (out->stats) {
+        stats_fold_kernel<<<1, 64, 0, st>>>(w.stat_slots, out->stats);
+        if ((rc = check_launch("stats_fold_kernel"))) return rc;
     }
     return TRIDENT_OK;
 }
@@ -463,6 +490,29 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
     ScanArgs a = make_scan_args(ix, w, 1, 1, 0, nullptr);
     sq8_bounds_kernel<<<(n + 255) / 256, 256, 0, st>>>(a, qids, cids, spos, n, lb, ub);
     return check_launch("sq8_bounds_kernel");
+}
+
+int trident_event_create(void** event) {
+    if (!event) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "NULL event pointer");
+    hipEvent_t e;
+    hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) return fail(TRIDENT_ERR_HIP, "hipEventCreate: %s", hipGetErrorString(r));
+    *event = e;
+    return TRIDENT_OK;
+}
+
+int trident_event_destroy(void* event) {
+    if (!event) return TRIDENT_OK;
+    hipError_t r = hipEventDestroy(static_cast<hipEvent_t>(event));
+    return r == hipSuccess ? TRIDENT_OK
+                           : fail(TRIDENT_ERR_HIP, "hipEventDestroy: %s", hipGetErrorString(r));
+}
+
+int trident_event_elapsed_ms(void* start, void* stop, float* ms) {
+    if (!start || !stop || !ms) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "NULL event argument");
+    hipError_t r = hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(stop));
+    return r == hipSuccess ? TRIDENT_OK
+                           : fail(TRIDENT_ERR_HIP, "hipEventElapsedTime: %s", hipGetErrorString(r));
 }
 
 int trident_host_alloc_mapped(size_t bytes, void** host_ptr) {

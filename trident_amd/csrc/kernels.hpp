@@ -55,7 +55,11 @@ struct MergeArgs {
     float* tau_sq_out;    // [B] or null
 };
 
+constexpr int kStatSlots = 64;  // telemetry counters are spread over this many [4] slots
+
 __global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n);
+
+__global__ void stats_fold_kernel(const unsigned long long* slots, int64_t* out);
 
 __global__ void prep_queries_kernel(const float* __restrict__ xq, int B, int D, int D_pad,
                                     const float* __restrict__ W, int ldw, int nlist,

@@ -321,18 +321,26 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
         wave_sync();
         flush(qn);
     }
-    if (a.stats && lane == 0) {
-        if (CASCADE) {
-            atomicAdd(&a.stats[0], st_cand);
-            atomicAdd(&a.stats[1], st_dims);
-            atomicAdd(&a.stats[2], st_surv);
-        }
-        atomicAdd(&a.stats[3], st_ins);
-    }
-
     // ---------------- combine the four wave lists and emit <= K entries ----------------
     __syncthreads();
     list_store(L, s_ck + wid * KP, s_ci + wid * KP);
+    if (a.stats) {
+        // Telemetry: one atomic per counter per workgroup, spread over kStatSlots slots that
+        // stats_fold_kernel sums afterwards (a single address would serialise every workgroup).
+        unsigned long long* s_st = reinterpret_cast<unsigned long long*>(s_ci + kWavesPerBlock * KP);
+        if (lane == 0) {
+            s_st[wid * 4 + 0] = st_cand;
+            s_st[wid * 4 + 1] = st_dims;
+            s_st[wid * 4 + 2] = st_surv;
+            s_st[wid * 4 + 3] = st_ins;
+        }
+        __syncthreads();
+        if (tid < 4) {
+            unsigned long long v = 0;
+            for (int w = 0; w < kWavesPerBlock; ++w) v += s_st[w * 4 + tid];
+            if (v) atomicAdd(&a.stats[(blockIdx.x % kStatSlots) * 4 + tid], v);
+        }
+    }
     __syncthreads();
     if (wid != 0) return;
     for (int w = 1; w < kWavesPerBlock; ++w) list_absorb(L, K, s_ck + w * KP, s_ci + w * KP);
@@ -361,6 +369,15 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
             ci[kWave + lane] = L.i1;
         }
     }
+}
+
+// Sums the kStatSlots telemetry slots into the caller's int64[4] (added to its contents).
+__global__ void stats_fold_kernel(const unsigned long long* slots, int64_t* out) {
+    const int k = threadIdx.x;
+    if (k >= 4) return;
+    unsigned long long v = 0;
+    for (int s = 0; s < kStatSlots; ++s) v += slots[s * 4 + k];
+    out[k] += (int64_t)v;
 }
 
 // One wave per query: merges the pass's candidates (and the previous pass's list) into

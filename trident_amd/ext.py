@@ -51,7 +51,11 @@ def _check_tensor(name, t, dtype, device, dims=None, allow_host=False):
     if dims is not None:
         _need(t.dim() == dims, f"{name} must be {dims}-D, got shape {tuple(t.shape)}")
     if allow_host and t.device.type == "cpu":
-        _need(t.is_pinned(), f"{name} on the host must be pinned (hipHostMalloc) memory")
+        try:
+            device_pointer(t)
+        except _lib.TridentError as e:
+            raise _lib.TridentError(f"{name} on the host must be device-mapped pinned memory "
+                                    f"(hipHostMalloc): {e}") from None
     else:
         _need(t.device == device, f"{name} must be on {device}, got {t.device}")
 
@@ -132,7 +136,7 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
                 p_init: int = -1, probe_cids: Optional[torch.Tensor] = None,
                 probe_dqcs: Optional[torch.Tensor] = None, tau_sq: Optional[torch.Tensor] = None,
                 stats: Optional[torch.Tensor] = None, record_events: bool = False,
-                stream: Optional[torch.cuda.Stream] = None) -> float:
+                stream: Optional[torch.cuda.Stream] = None, stage_events=None) -> float:
     """Runs trident_search on an index view; all tensors already validated by the caller."""
     B, K = int(xq.shape[0]), int(topk_d.shape[1])
     L = _lib.lib()
@@ -151,6 +155,9 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
     out.probe_ld = ld
     out.tau_sq = _ptr(tau_sq)
     out.stats = _ptr(stats)
+    if stage_events is not None:
+        out.events = stage_events.handles
+        out.n_events = _lib.EV_COUNT
     st = stream if stream is not None else torch.cuda.current_stream(xq.device)
     ev0 = ev1 = None
     if record_events:
@@ -177,7 +184,7 @@ def launch_trident_v4_search(
     topk_d, topk_i, topm_buf_d, topm_buf_i, tau_sq,
     cand_buf_d, cand_buf_i, cand_cnt, record_events,
     warp_refine=1, stats_buf=None, r_vec_sorted=None,
-    *, ub_seed: Optional[int] = None, rot_sq_bounds=None, p_init: int = -1,
+    *, ub_seed: Optional[int] = None, rot_sq_bounds=None, p_init: int = -1, stage_events=None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -254,4 +261,4 @@ def launch_trident_v4_search(
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, probe_cids=probe_cids_buf,
                        probe_dqcs=probe_dqcs_buf, tau_sq=tau_sq, stats=stats_buf,
-                       record_events=bool(record_events))
+                       record_events=bool(record_events), stage_events=stage_events)

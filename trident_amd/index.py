@@ -323,7 +323,8 @@ class TridentV4Index:
 
     def search(self, xq_gpu: torch.Tensor, nprobe: int, mode: int = 2, use_l1: int = 0, rerank_m: int = 0,
                tile_override: int = 0, warp_refine: int = 1, stats_buf: Optional[torch.Tensor] = None,
-               record_kernel_ms: bool = False, k: Optional[int] = None, ub_seed: Optional[int] = None):
+               record_kernel_ms: bool = False, k: Optional[int] = None, ub_seed: Optional[int] = None,
+               stage_events=None):
         """Reference TridentV4Index.search (phase4a_suite.py:280-342) plus ``k=`` / ``ub_seed=``."""
         if k is not None:
             self.set_k(k)
@@ -348,7 +349,7 @@ class TridentV4Index:
             topk_d, topk_i, self.topm_buf_d, self.topm_buf_i, self.tau_sq_buf,
             self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
             bool(record_kernel_ms), int(warp_refine), stats_buf,
-            ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max))
+            ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events)
         return topk_d, topk_i, kern_ms
 
     # ---- views used by tests / oracle (host copies) ----
