@@ -35,3 +35,23 @@ def test_router_uses_index_shape():
     assert r.mode_for(1, 8) == 10          # 1 * 8 * 976.6 * 128 = 1e6 < 1e9
     assert r.mode_for(10_000, 64) == 2
     assert r.search(Q(), 8)[-1] == 10 and f.calls == [10]
+
+
+def test_eval_accuracy_v4_semantics():
+    import numpy as np
+    from trident_amd.metrics import eval_accuracy_v4, measure_latency_qps, measure_runs
+    gt = np.arange(20).reshape(2, 10)
+    cm_i = gt.copy()
+    cm_d = np.tile(np.arange(10, dtype=np.float32), (2, 1))
+    pred_i = cm_i.copy()
+    pred_i[1, 9] = 99                                  # different id, same distance -> still strict
+    pred_d = cm_d.copy()
+    rec, strict, full = eval_accuracy_v4(pred_i, pred_d, cm_i, cm_d, gt)
+    assert rec == 19 / 20 and strict == 100.0 and full == 100.0
+    pred_d[1, 9] = 10.0                                 # now the distance differs too
+    rec, strict, full = eval_accuracy_v4(pred_i, pred_d, cm_i, cm_d, gt)
+    assert strict == 95.0 and full == 50.0
+    calls = []
+    assert measure_latency_qps(lambda: calls.append(1), warmup=2, iters=3) >= 0 and len(calls) == 5
+    q, s = measure_runs(lambda: None, warmup=1, iters=3, b_size=10)
+    assert q > 0 and s >= 0
