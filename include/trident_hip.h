@@ -67,7 +67,16 @@ typedef struct TridentIndexView {
     const float* delta;              /* [nlist or 1, D_pad] */
     const float* eps_dim;            /* [nlist or 1, D_pad] rigorous |x_rot - x_hat| bound */
     const int32_t* blk_bounds4;      /* [num_blocks + 1], device, in units of 4 dims */
+    const double* vec_Ar;            /* [N, 2] sorted order: |code*delta|^2, residual-norm bound;
+                                        NULL disables the batched route */
 } TridentIndexView;
+
+/* How mode 2 is executed.  Both are exact; they differ in speed only. */
+enum TridentRoute {
+    TRIDENT_ROUTE_AUTO = 0,     /* batched when clusters are shared by enough queries */
+    TRIDENT_ROUTE_PAIR = 1,     /* one workgroup per (cluster, query): Stage X / Y / Z per pair */
+    TRIDENT_ROUTE_BATCHED = 2   /* one workgroup per (cluster, query block): int8 matrix-core bound */
+};
 
 typedef struct TridentSearchParams {
     int32_t mode;    /* TRIDENT_MODE_CASCADE or TRIDENT_MODE_CM_EXACT */
@@ -77,7 +86,7 @@ typedef struct TridentSearchParams {
     int32_t ub_seed; /* TRIDENT_UB_SEED semantics: 0 off, 1 pass 1, 2 both passes */
     int32_t use_l1;  /* residual-norm tile band (needs tile_r_minmax) */
     int32_t p_init;  /* pass-1 probes per query; -1 = reference rule */
-    int32_t reserved;
+    int32_t route;   /* TridentRoute (mode 2 only) */
 } TridentSearchParams;
 
 /* Stage boundaries at which trident_search records the caller's events (if given). */

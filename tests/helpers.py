@@ -59,7 +59,9 @@ def assert_exact(gpu_d, gpu_i, ref_d, ref_i, ctx=""):
     assert (rel <= 1e-5).all(), f"{ctx}: relative distance error {rel.max()} > 1e-5"
 
 
-def run_search(b, xq_dev, nprobe, K, mode=2, ub=0, use_l1=0, stats=None):
-    d, i, _ = b.ix.search(xq_dev, nprobe, mode=mode, use_l1=use_l1, k=K, ub_seed=ub, stats_buf=stats)
+def run_search(b, xq_dev, nprobe, K, mode=2, ub=0, use_l1=0, stats=None, route=1):
+    """route 1 = per-pair cascade (the default here, so each test pins one route), 2 = batched."""
+    d, i, _ = b.ix.search(xq_dev, nprobe, mode=mode, use_l1=use_l1, k=K, ub_seed=ub, stats_buf=stats,
+                          route=route)
     torch.cuda.synchronize()
     return d.cpu().numpy().copy(), i.cpu().numpy().copy()

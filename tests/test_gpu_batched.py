@@ -1,0 +1,95 @@
+"""GPU parity of the cluster-batched (int8 matrix-core) cascade against the float64 oracle.
+
+Same bar as test_gpu_parity.py: ids identical on every query, float32 distances equal to the
+oracle's float64 distances rounded to float32.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import assert_exact, build_index, oracle_search, run_search
+from trident_amd import datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _q(xq, dev):
+    return torch.as_tensor(np.ascontiguousarray(xq, np.float32)).to(dev).contiguous()
+
+
+@pytest.fixture(scope="module")
+def sets(dev):
+    out = {}
+    xb, xq = datagen.cfg2(N=60_000, D=128, B=400, n_centers=128, seed=21)
+    out["hist"] = (build_index(xb, 128, dev, max_batch=512), xq.numpy())
+    xb, xq = datagen.cfg4(N=50_000, D=96, B=400, n_centers=256, seed=22)
+    out["norm96"] = (build_index(xb, 200, dev, max_batch=512), xq.numpy())
+    xb, xq = datagen.cfg1(N=40_000, D=128, B=300, n_centers=64, seed=23)
+    out["gmm"] = (build_index(xb, 100, dev, max_batch=512), xq.numpy())
+    xb, xq = datagen.cfg1(N=20_000, D=200, B=200, n_centers=32, seed=24)
+    out["d200"] = (build_index(xb, 64, dev, max_batch=512, tile_size=256), xq.numpy())
+    return out
+
+
+@pytest.mark.parametrize("name", ["hist", "norm96", "gmm", "d200"])
+@pytest.mark.parametrize("K", [1, 10, 64])
+def test_batched_route_exact(sets, dev, name, K):
+    b, xq = sets[name]
+    for nprobe in (4, 24):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"batched {name} K={K} nprobe={nprobe}")
+
+
+def test_batched_matches_pair_route_and_auto(sets, dev):
+    b, xq = sets["hist"]
+    xqd = _q(xq, dev)
+    d1, i1 = run_search(b, xqd, 32, 10, mode=2, ub=1, route=1)
+    d2, i2 = run_search(b, xqd, 32, 10, mode=2, ub=1, route=2)
+    d0, i0 = run_search(b, xqd, 32, 10, mode=2, ub=1, route=0)
+    assert np.array_equal(i1, i2) and np.array_equal(d1, d2)
+    assert np.array_equal(i0, i2) and np.array_equal(d0, d2)
+
+
+@pytest.mark.parametrize("nprobe", [1, 2, 3])
+def test_batched_small_nprobe_and_single_query(sets, dev, nprobe):
+    """nprobe 1 has no seeding pass (every candidate survives, candidate lists overflow and the
+    merge rescans exactly); B = 1 exercises one-query chunks."""
+    b, xq = sets["hist"]
+    for B in (1, 33):
+        _, rd, ri = oracle_search(b, xq[:B], nprobe, 10)
+        d, i = run_search(b, _q(xq[:B], dev), nprobe, 10, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"batched nprobe={nprobe} B={B}")
+
+
+def test_batched_overflow_fallback_on_exact_ties(dev):
+    """40 copies of every row: all copies tie at the threshold, the per-query lists overflow
+    nprobe * K and the merge's exhaustive rescan must still return ids by (d, id)."""
+    rng = np.random.default_rng(31)
+    base = rng.integers(0, 3, size=(60, 16)).astype(np.float32)
+    xb = np.repeat(base, 40, axis=0)
+    nlist = 6
+    cen = rng.integers(0, 3, size=(nlist, 16)).astype(np.float32)
+    lid = np.argmin(((xb[:, None, :] - cen[None]) ** 2).sum(-1), 1).astype(np.int32)
+    xq = np.concatenate([base[:20], rng.integers(0, 3, size=(20, 16))]).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=64)
+    for K, nprobe in ((5, 2), (10, 4), (64, 6)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"ties K={K} nprobe={nprobe}")
+
+
+def test_batched_host_mapped_base(dev):
+    xb, xq = datagen.cfg2(N=30_000, D=128, B=200, n_centers=64, seed=25)
+    b = build_index(xb, 64, dev, xb_placement="host", max_batch=256)
+    _, rd, ri = oracle_search(b, xq.numpy(), 16, 10)
+    d, i = run_search(b, _q(xq.numpy(), dev), 16, 10, mode=2, ub=1, route=2)
+    assert_exact(d, i, rd, ri, "batched ooc")
+    b.ix.storage._host_buf.free()
+
+
+def test_batched_rejects_unsupported_k(sets, dev):
+    from trident_amd._lib import TridentError
+    b, xq = sets["hist"]
+    with pytest.raises(TridentError, match="batched route"):
+        run_search(b, _q(xq, dev), 8, 100, mode=2, route=2)

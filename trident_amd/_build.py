@@ -18,7 +18,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtrident_hip.so")
-SOURCES = ["frontend.hip", "scan.hip", "capi.hip"]
+SOURCES = ["frontend.hip", "scan.hip", "batch.hip", "capi.hip"]
 HEADERS = ["common.hpp", "kernels.hpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

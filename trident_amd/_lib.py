@@ -27,13 +27,16 @@ class TridentIndexView(ctypes.Structure):
         ("sq8_packed", _P), ("tile_orig_ids", _P), ("tile_r_minmax", _P),
         ("cluster_tile_off", _P), ("cluster_vec_off", _P),
         ("xb_sorted", _P), ("orig_ids_sorted", _P),
-        ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P),
+        ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P), ("vec_Ar", _P),
     ]
 
 
 class TridentSearchParams(ctypes.Structure):
     _fields_ = [("mode", _i32), ("B", _i32), ("K", _i32), ("nprobe", _i32),
-                ("ub_seed", _i32), ("use_l1", _i32), ("p_init", _i32), ("reserved", _i32)]
+                ("ub_seed", _i32), ("use_l1", _i32), ("p_init", _i32), ("route", _i32)]
+
+
+ROUTE_AUTO, ROUTE_PAIR, ROUTE_BATCHED = 0, 1, 2
 
 
 class TridentSearchOutputs(ctypes.Structure):

@@ -82,8 +82,16 @@ struct Workspace {
     int32_t* list_id;
     double* tau64;
     unsigned long long* stat_slots;  // [kStatSlots, 4] telemetry partials
+    int32_t* chunk_cid;              // [2, max_chunks] batched-route chunk tables
+    int32_t* chunk_start;
+    int32_t* chunk_cnt;
+    int32_t* n_chunks;               // [2]
+    int64_t max_chunks;
     size_t bytes;
 };
+
+// Upper bound on the chunks of one pass: every cluster rounds its pair count up to a chunk.
+inline int64_t max_chunks_of(int64_t pairs, int64_t nlist) { return (pairs + 63) / 64 + nlist; }
 
 Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
     Carver c{static_cast<char*>(base)};
@@ -109,6 +117,11 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.list_id = c.take<int32_t>(B * KP);
     w.tau64 = c.take<double>(B);
     w.stat_slots = c.take<unsigned long long>((size_t)kStatSlots * 4);
+    w.max_chunks = max_chunks_of(B * nprobe, ix->nlist);
+    w.chunk_cid = c.take<int32_t>(2 * w.max_chunks);
+    w.chunk_start = c.take<int32_t>(2 * w.max_chunks);
+    w.chunk_cnt = c.take<int32_t>(2 * w.max_chunks);
+    w.n_chunks = c.take<int32_t>(2);
     w.bytes = c.off;
     return w;
 }
@@ -201,6 +214,41 @@ int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
     if (!cascade) return launch_scan<KP, false, false>(a, st);
     if (ub) return launch_scan<KP, true, true>(a, st);
     return launch_scan<KP, true, false>(a, st);
+}
+
+// Route of a mode-2 search.  The batched route needs the per-vector scalars, K <= 64 (its
+// upper-bound seeding keeps 16 bounds per lane, 64 per query) and D_pad <= 256 (query
+// weights held in registers); AUTO takes it when clusters are shared by >= 8 queries on
+// average, where the contraction is dense enough for the matrix cores.
+int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
+                 int nprobe, int* route) {
+    const bool ok = ix->vec_Ar && K <= 64 && ix->D_pad <= 256;
+    switch (sp->route) {
+        case TRIDENT_ROUTE_PAIR:
+            *route = TRIDENT_ROUTE_PAIR;
+            return TRIDENT_OK;
+        case TRIDENT_ROUTE_BATCHED:
+            if (!ok)
+                return fail(TRIDENT_ERR_UNSUPPORTED,
+                            "batched route needs vec_Ar, K <= 64 and D_pad <= 256 (K=%d, D_pad=%d)",
+                            K, ix->D_pad);
+            *route = TRIDENT_ROUTE_BATCHED;
+            return TRIDENT_OK;
+        case TRIDENT_ROUTE_AUTO:
+            *route = (ok && (double)B * nprobe >= 8.0 * ix->nlist) ? TRIDENT_ROUTE_BATCHED
+                                                                 : TRIDENT_ROUTE_PAIR;
+            return TRIDENT_OK;
+        default:
+            return fail(TRIDENT_ERR_INVALID_ARGUMENT, "route=%d outside {0,1,2}", sp->route);
+    }
+}
+
+template <bool UB>
+int launch_batch(const BatchArgs& b, int64_t max_chunks, hipStream_t st) {
+    if (max_chunks <= 0) return TRIDENT_OK;
+    const unsigned grid = (unsigned)(((max_chunks + 7) / 8) * 8);
+    batch_scan_kernel<UB><<<grid, kBlock, 0, st>>>(b);
+    return check_launch("batch_scan_kernel");
 }
 
 int launch_merge(const MergeArgs& m, int KP, hipStream_t st) {
@@ -417,6 +465,90 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     m.list_key = w.list_key;
     m.list_id = w.list_id;
     m.tau64 = w.tau64;
+
+    int route = TRIDENT_ROUTE_PAIR;
+    if (cascade && (rc = choose_route(ix, sp, B, K, nprobe, &route))) return rc;
+    if (route == TRIDENT_ROUTE_BATCHED) {
+        BatchArgs b{};
+        b.sq8 = ix->sq8_packed;
+        b.tile_oids = ix->tile_orig_ids;
+        b.tile_off = ix->cluster_tile_off;
+        b.vec_off = ix->cluster_vec_off;
+        b.xb = ix->xb_sorted;
+        b.vmin = ix->vmin;
+        b.delta = ix->delta;
+        b.vec_Ar = ix->vec_Ar;
+        b.D = ix->D;
+        b.D_pad = ix->D_pad;
+        b.T = ix->tile_size;
+        b.per_cluster = ix->per_cluster_sq8;
+        b.xq = xq;
+        b.xrot64 = w.xrot64;
+        b.qerr = w.qerr;
+        b.tau = w.tau64;
+        b.cand_key = w.cand_key;
+        b.cand_id = w.cand_id;
+        b.cand_cnt = w.cand_cnt;
+        b.cap = (int)cap;
+        b.K = K;
+        b.stats = out->stats ? w.stat_slots : nullptr;
+        b.rot_sq_min = ix->rot_sq_min;
+        b.rot_sq_max = ix->rot_sq_max;
+        const int64_t mc = w.max_chunks;
+        build_chunks_kernel<<<2, kBlock, 0, st>>>(w.seg_off, ix->nlist, w.chunk_cid, w.chunk_start,
+                                                  w.chunk_cnt, w.n_chunks, (int)mc);
+        if ((rc = check_launch("build_chunks_kernel"))) return rc;
+        fill_u64_kernel<<<(unsigned)std::min<int64_t>((B + 255) / 256, 4096), 256, 0, st>>>(
+            reinterpret_cast<unsigned long long*>(w.tau64), 0x7ff0000000000000ull, B);
+        if ((rc = check_launch("fill_u64_kernel"))) return rc;
+        auto use_pass = [&](int p) {
+            b.chunk_cid = w.chunk_cid + p * mc;
+            b.chunk_start = w.chunk_start + p * mc;
+            b.chunk_cnt = w.chunk_cnt + p * mc;
+            b.n_chunks = w.n_chunks + p;
+            b.pair_qid = p ? p2q : p1q;
+        };
+        const int64_t mc1 = max_chunks_of(M1, ix->nlist), mc2 = max_chunks_of(M2, ix->nlist);
+        if (M1 > 0) {  // pass A: per-query upper-bound threshold from the first p_init probes
+            use_pass(0);
+            if ((rc = launch_batch<true>(b, mc1, st))) return rc;
+        }
+        if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
+        if (out->tau_sq) {
+            tau_to_f32_kernel<<<(B + 255) / 256, 256, 0, st>>>(w.tau64, out->tau_sq, B);
+            if ((rc = check_launch("tau_to_f32_kernel"))) return rc;
+        }
+        if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
+        if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
+        if (M1 > 0) {  // pass B over every probe: lower bound, exact refine, append <= tau
+            use_pass(0);
+            if ((rc = launch_batch<false>(b, mc1, st))) return rc;
+        }
+        if (M2 > 0) {
+            use_pass(1);
+            if ((rc = launch_batch<false>(b, mc2, st))) return rc;
+        }
+        if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
+        m.use_prev = 0;
+        m.out_d = out->topk_d;
+        m.out_i = out->topk_i;
+        m.probe_cids = w.probe_cids;
+        m.nprobe = nprobe;
+        m.vec_off = ix->cluster_vec_off;
+        m.xb = ix->xb_sorted;
+        m.xq64 = w.xq64;
+        m.tile_oids = ix->tile_orig_ids;
+        m.tile_off = ix->cluster_tile_off;
+        m.T = ix->tile_size;
+        m.D = ix->D;
+        if ((rc = launch_merge(m, KP, st))) return rc;
+        if ((rc = mark(TRIDENT_EV_END))) return rc;
+        if (out->stats) {
+            stats_fold_kernel<<<1, 64, 0, st>>>(w.stat_slots, out->stats);
+            if ((rc = check_launch("stats_fold_kernel"))) return rc;
+        }
+        return TRIDENT_OK;
+    }
 
     if (M1 > 0) {
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;

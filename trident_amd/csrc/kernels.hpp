@@ -53,6 +53,44 @@ struct MergeArgs {
     float* out_d;         // [B, K] or null (final pass only)
     int64_t* out_i;
     float* tau_sq_out;    // [B] or null
+    // Exhaustive fallback for a query whose candidate list overflowed `cap` (only the batched
+    // route appends without a per-pair cap): its probed lists are rescanned exactly.
+    const int32_t* probe_cids;  // [B, nprobe] or null (no fallback needed)
+    int nprobe;
+    const int32_t* vec_off;
+    const float* xb;
+    const double* xq64;   // [B, D]
+    const int32_t* tile_oids;
+    const int32_t* tile_off;
+    int T, D;
+};
+
+// Everything one cluster-batched scan launch reads (csrc/batch.hip).
+struct BatchArgs {
+    const uint32_t* sq8;
+    const int32_t* tile_oids;
+    const int32_t* tile_off;
+    const int32_t* vec_off;
+    const float* xb;
+    const float* vmin;
+    const float* delta;
+    const double* vec_Ar;       // [N, 2]
+    int D, D_pad, T, per_cluster;
+    const float* xq;            // [B, D] float32 queries
+    const double* xrot64;       // [B, D_pad]
+    const double* qerr;         // [B, D_pad]
+    const int32_t* chunk_cid;   // chunk table of this pass
+    const int32_t* chunk_start;
+    const int32_t* chunk_cnt;
+    const int32_t* n_chunks;    // device scalar
+    const int32_t* pair_qid;
+    double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
+    uint64_t* cand_key;
+    int32_t* cand_id;
+    int32_t* cand_cnt;
+    int cap, K;
+    unsigned long long* stats;  // [kStatSlots, 4] or null
+    double rot_sq_min, rot_sq_max;
 };
 
 constexpr int kStatSlots = 64;  // telemetry counters are spread over this many [4] slots
@@ -95,6 +133,17 @@ __global__ void pair_scan_kernel(ScanArgs a);
 
 template <int KP>
 __global__ void merge_kernel(MergeArgs a);
+
+__global__ void build_chunks_kernel(const int32_t* seg_off, int nlist, int32_t* chunk_cid,
+                                    int32_t* chunk_start, int32_t* chunk_cnt, int32_t* n_chunks,
+                                    int max_chunks);
+
+__global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
+
+__global__ void tau_to_f32_kernel(const double* tau, float* out, int B);
+
+template <bool UB_PASS>
+__global__ void batch_scan_kernel(BatchArgs a);
 
 __global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
                                   const int32_t* __restrict__ cids,

@@ -399,12 +399,39 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
             L.i1 = li[kWave + lane];
         }
     }
-    const int cnt = min(a.cand_cnt[q], a.cap);
-    const uint64_t* ck = a.cand_key + (size_t)q * a.cap;
-    const int32_t* ci = a.cand_id + (size_t)q * a.cap;
-    for (int b0 = 0; b0 < cnt; b0 += kWave) {
-        const int i = b0 + lane;
-        list_offer(L, a.K, i < cnt ? ck[i] : kKeyInvalid, i < cnt ? ci[i] : kIdInvalid);
+    const int raw = a.cand_cnt[q];
+    if (raw > a.cap && a.probe_cids) {
+        // Overflowed list: rescan every probed vector exactly (canonical float64 distance).
+        L.init();
+        const double* qv = a.xq64 + (size_t)q * a.D;
+        for (int p = 0; p < a.nprobe; ++p) {
+            const int c = a.probe_cids[(size_t)q * a.nprobe + p];
+            const int v0 = a.vec_off[c], n = a.vec_off[c + 1] - v0, t0 = a.tile_off[c];
+            for (int b0 = 0; b0 < n; b0 += kWave) {
+                const int li = b0 + lane;
+                uint64_t k = kKeyInvalid;
+                int32_t id = kIdInvalid;
+                if (li < n) {
+                    const float* xr = a.xb + (size_t)(v0 + li) * a.D;
+                    double acc = 0.0;
+                    for (int d = 0; d < a.D; ++d) {
+                        const double t = (double)xr[d] - qv[d];
+                        acc = fma(t, t, acc);
+                    }
+                    k = key_of(acc);
+                    id = a.tile_oids[(size_t)t0 * a.T + li];
+                }
+                list_offer(L, a.K, k, id);
+            }
+        }
+    } else {
+        const int cnt = min(raw, a.cap);
+        const uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+        const int32_t* ci = a.cand_id + (size_t)q * a.cap;
+        for (int b0 = 0; b0 < cnt; b0 += kWave) {
+            const int i = b0 + lane;
+            list_offer(L, a.K, i < cnt ? ck[i] : kKeyInvalid, i < cnt ? ci[i] : kIdInvalid);
+        }
     }
     list_store(L, lk, li);
     uint64_t kk;

@@ -105,7 +105,7 @@ def release_workspaces() -> None:
 def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combined, b_combined,
                     rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
-                    eps_dim, blk_bounds4) -> TridentIndexView:
+                    eps_dim, blk_bounds4, vec_Ar=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -124,6 +124,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.orig_ids_sorted = _ptr(orig_ids_sorted) if orig_ids_sorted is not None and orig_ids_sorted.device.type != "cpu" else None
     v.vmin, v.delta, v.eps_dim = _ptr(vmin), _ptr(delta), _ptr(eps_dim)
     v.blk_bounds4 = _ptr(blk_bounds4)
+    v.vec_Ar = _ptr(vec_Ar)
     return v
 
 
@@ -133,7 +134,7 @@ def env_ub_seed() -> int:
 
 def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: torch.Tensor,
                 topk_i: torch.Tensor, *, mode: int = 2, ub_seed: int = 0, use_l1: int = 0,
-                p_init: int = -1, probe_cids: Optional[torch.Tensor] = None,
+                p_init: int = -1, route: int = 0, probe_cids: Optional[torch.Tensor] = None,
                 probe_dqcs: Optional[torch.Tensor] = None, tau_sq: Optional[torch.Tensor] = None,
                 stats: Optional[torch.Tensor] = None, record_events: bool = False,
                 stream: Optional[torch.cuda.Stream] = None, stage_events=None) -> float:
@@ -142,7 +143,7 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
     L = _lib.lib()
     nbytes = L.trident_workspace_bytes(ctypes.byref(view), max(B, 1), int(nprobe), K)
     ws = workspace(xq.device, nbytes)
-    sp = TridentSearchParams(int(mode), B, K, int(nprobe), int(ub_seed), int(use_l1), int(p_init), 0)
+    sp = TridentSearchParams(int(mode), B, K, int(nprobe), int(ub_seed), int(use_l1), int(p_init), int(route))
     out = TridentSearchOutputs()
     out.topk_d, out.topk_i = topk_d.data_ptr(), topk_i.data_ptr()
     out.probe_cids = _ptr(probe_cids)
@@ -185,6 +186,7 @@ def launch_trident_v4_search(
     cand_buf_d, cand_buf_i, cand_cnt, record_events,
     warp_refine=1, stats_buf=None, r_vec_sorted=None,
     *, ub_seed: Optional[int] = None, rot_sq_bounds=None, p_init: int = -1, stage_events=None,
+    vec_Ar: Optional[torch.Tensor] = None, route: int = 0,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -231,6 +233,9 @@ def launch_trident_v4_search(
             _check_tensor(name, t, torch.float32, dev)
             _need(t.numel() == rows * D_pad, f"{name} must be [{rows}, D_pad]")
         _check_tensor("blk_bounds4", blk_bounds4, torch.int32, dev, 1)
+    if vec_Ar is not None:
+        _check_tensor("vec_Ar", vec_Ar, torch.float64, dev, 2)
+        _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float64")
     if stats_buf is not None:
         _check_tensor("stats_buf", stats_buf, torch.int64, dev)
         _need(stats_buf.numel() >= 4, "stats_buf needs 4 entries")
@@ -256,9 +261,9 @@ def launch_trident_v4_search(
         cluster_tile_off=cluster_tile_off, cluster_vec_off=cluster_vec_off, xb_sorted=xb_sorted,
         orig_ids_sorted=orig_ids_sorted, vmin=vmin if mode == 2 else None,
         delta=delta if mode == 2 else None, eps_dim=eps_dim if mode == 2 else None,
-        blk_bounds4=blk_bounds4)
+        blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
-                       use_l1=int(use_l1), p_init=p_init, probe_cids=probe_cids_buf,
+                       use_l1=int(use_l1), p_init=p_init, route=route, probe_cids=probe_cids_buf,
                        probe_dqcs=probe_dqcs_buf, tau_sq=tau_sq, stats=stats_buf,
                        record_events=bool(record_events), stage_events=stage_events)

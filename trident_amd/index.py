@@ -220,6 +220,10 @@ class TridentV4Index:
         delta = torch.where(empty, torch.ones_like(delta), delta)
         codes = torch.empty((N, D_pad), device=dev, dtype=torch.uint8)
         err_max = torch.zeros((rows, D_pad), device=dev, dtype=torch.float64)
+        # Per-vector scalars of the batched (matrix-core) bound, sorted order, float64 pairs:
+        #   vec_Ar[v, 0] = A_v = sum_d (code_d * delta_d)^2   (exact products, float64 sum)
+        #   vec_Ar[v, 1] = r_v >= |x_rot(exact) - x_hat|_2     (quantisation + rotation error)
+        self.vec_Ar = torch.empty((N, 2), device=dev, dtype=torch.float64)
         for s in range(0, N, chunk_rows):
             e = min(N, s + chunk_rows)
             xr64, rerr = rotate(s, e)
@@ -228,10 +232,14 @@ class TridentV4Index:
             vm, dl = vmin[ci], delta[ci]
             cd = torch.clamp(torch.round((xr32 - vm) / dl), 0.0, 255.0)
             codes[s:e] = cd.to(torch.uint8)
-            xhat = vm.double() + cd.double() * dl.double()
+            cdl = cd.double() * dl.double()
+            xhat = vm.double() + cdl
             err = (xr64 - xhat).abs() + rerr
             idx = ci.unsqueeze(1).expand(-1, D_pad)
             err_max.scatter_reduce_(0, idx, err, reduce="amax", include_self=True)
+            self.vec_Ar[s:e, 0] = (cdl * cdl).sum(1)
+            r_q = torch.sqrt(((xr64 - xhat) ** 2).sum(1)) + torch.sqrt((rerr ** 2).sum(1))
+            self.vec_Ar[s:e, 1] = r_q * (1.0 + 1e-12) + 1e-300
         self.vmin_pad = vmin.contiguous()
         self.delta_pad = delta.contiguous()
         self.eps_pad = round_up_f32(err_max * (1.0 + 2.0 ** -20) + 1e-300).contiguous()
@@ -324,8 +332,9 @@ class TridentV4Index:
     def search(self, xq_gpu: torch.Tensor, nprobe: int, mode: int = 2, use_l1: int = 0, rerank_m: int = 0,
                tile_override: int = 0, warp_refine: int = 1, stats_buf: Optional[torch.Tensor] = None,
                record_kernel_ms: bool = False, k: Optional[int] = None, ub_seed: Optional[int] = None,
-               stage_events=None):
-        """Reference TridentV4Index.search (phase4a_suite.py:280-342) plus ``k=`` / ``ub_seed=``."""
+               stage_events=None, route: int = 0):
+        """Reference TridentV4Index.search (phase4a_suite.py:280-342) plus ``k=``, ``ub_seed=`` and
+        ``route=`` (0 auto, 1 per-pair cascade, 2 cluster-batched matrix-core cascade)."""
         if k is not None:
             self.set_k(k)
         B = int(xq_gpu.shape[0])
@@ -349,7 +358,8 @@ class TridentV4Index:
             topk_d, topk_i, self.topm_buf_d, self.topm_buf_i, self.tau_sq_buf,
             self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
             bool(record_kernel_ms), int(warp_refine), stats_buf,
-            ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events)
+            ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events,
+            vec_Ar=self.vec_Ar, route=route)
         return topk_d, topk_i, kern_ms
 
     # ---- views used by tests / oracle (host copies) ----
