@@ -67,8 +67,9 @@ typedef struct TridentIndexView {
     const float* delta;              /* [nlist or 1, D_pad] */
     const float* eps_dim;            /* [nlist or 1, D_pad] rigorous |x_rot - x_hat| bound */
     const int32_t* blk_bounds4;      /* [num_blocks + 1], device, in units of 4 dims */
-    const double* vec_Ar;            /* [N, 2] sorted order: |code*delta|^2, residual-norm bound;
-                                        NULL disables the batched route */
+    const float* vec_Ar;             /* [N, 2] sorted order: |code*delta|^2 rounded down (margin
+                                        1e-13), residual-norm bound rounded up; NULL disables the
+                                        batched route */
 } TridentIndexView;
 
 /* How mode 2 is executed.  Both are exact; they differ in speed only. */

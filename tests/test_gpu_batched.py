@@ -88,6 +88,20 @@ def test_batched_host_mapped_base(dev):
     b.ix.storage._host_buf.free()
 
 
+@pytest.mark.parametrize("K", [1, 10, 64])
+def test_batched_large_clusters_split_into_slices(dev, K):
+    """~5000 vectors per cluster: every cluster is scanned as 5 vector slices (units of 16
+    queries x <= 1024 vectors), so seeding and the lower-bound pass cross slice boundaries."""
+    xb, xq = datagen.cfg1(N=40_000, D=64, B=300, n_centers=8, seed=26)
+    b = build_index(xb, 8, dev, max_batch=512)
+    sizes = np.diff(b.vec_off)
+    assert sizes.max() > 2048
+    for nprobe in (1, 3, 8):
+        _, rd, ri = oracle_search(b, xq.numpy(), nprobe, K)
+        d, i = run_search(b, _q(xq.numpy(), dev), nprobe, K, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"slices K={K} nprobe={nprobe}")
+
+
 def test_batched_rejects_unsupported_k(sets, dev):
     from trident_amd._lib import TridentError
     b, xq = sets["hist"]

@@ -20,17 +20,24 @@
 // canonical float64 distance.
 //
 // Pass A (UB):  for the first p_init probes of each query, the K-th smallest upper bound over
-//               the cluster -> atomicMin into tau[q] (the reference's Stage X seeding,
-//               src/trident_v4_kernels.cu:626-676, computed for a block of queries at once).
-// Pass B (LB):  for every probe, lanes whose lower bound passes tau[q] are compacted into a
-//               per-wave queue and refined exactly in float64 (canonical order); distances
-//               <= tau[q] are appended to the query's candidate list.
+//               a slice of the cluster -> atomicMin into tau[q] (the reference's Stage X
+//               seeding, src/trident_v4_kernels.cu:626-676, computed for 16 queries at once; the
+//               K-th smallest upper bound of any K vectors bounds the K-th distance).
+// Pass B (LB):  for every probe, vectors whose lower bound passes tau[q] are appended (sorted
+//               position) to the query's candidate list.  The test runs in float32 with an
+//               additive slack that bounds every rounding of it (see lb_slack below).
+// Refine:       one wave per query computes the canonical float64 distance of each listed
+//               survivor and keeps it iff <= tau[q] (the reference's Stage Z, :796-941).
 //
-// One workgroup per (cluster, block of <= 64 pairs); its 4 waves are independent and own 16
-// queries each (the MFMA N dimension).  Lane l = (i = l & 15, g = l >> 4) holds, for every
-// 64-dim step, bytes of dims step*64 + g*16 + [0, 16): vector i's codes in the A operand and
-// query i's weights in the B operand (any dim-to-byte assignment shared by A and B computes
-// the same contraction); the result row 4g + r, column i sits in lane l, register r.
+// Scheduling: a work unit is (cluster, 16 queries, slice of the cluster's vectors).  Units of
+// one launch are split into 8 contiguous ranges, one per XCD (blockIdx & 7), so a cluster's
+// codes are read from HBM once per XCD and then served by that XCD's L2; within a range every
+// wave takes the next unit from its XCD's counter (persistent grid, one atomic per unit).
+// Lane l = (i = l & 15, g = l >> 4) holds, for every 64-dim step, bytes of dims
+// step*64 + g*16 + [0, 16): vector i's codes in the A operand and query i's weights in the B
+// operand (any dim-to-byte assignment shared by A and B computes the same contraction); the
+// result row 4g + r, column i sits in lane l, register r.  The next 16-vector tile's codes and
+// per-vector scalars are loaded before the current tile's MFMAs and epilogue.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -38,32 +45,39 @@ namespace trident {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kQW = 16;                          // queries per wave
-constexpr int kChunkQ = kQW * kWavesPerBlock;    // pairs per workgroup chunk
-constexpr int kMaxKS = 4;                        // 64-dim steps held in registers (D_pad <= 256)
 constexpr int kUbList = 16;                      // per-lane upper-bound list (K <= 64)
-constexpr int kBStageCh = 32;
-constexpr int kBQueue = 128;
 
-// grid 2 (one block per pass): chunk table of the pass's cluster segments.
-__global__ __launch_bounds__(256) void build_chunks_kernel(const int32_t* seg_off, int nlist,
-                                                           int32_t* chunk_cid, int32_t* chunk_start,
-                                                           int32_t* chunk_cnt, int32_t* n_chunks,
-                                                           int max_chunks) {
+// Vector slices of a cluster in pass p.  Pass-1 segments (the seeding probes) keep whole
+// clusters: the K-th smallest upper bound over a slice is a much weaker threshold than over
+// the cluster.  Pass-2 segments are sliced so that no unit runs far longer than the others.
+__device__ __forceinline__ int splits_of(int n, int p) {
+    if (n <= 0) return 0;
+    return p ? min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec) : 1;
+}
+
+__device__ __forceinline__ int units_of_entry(const int32_t* seg_off, const int32_t* vec_off,
+                                              int nlist, int e) {
+    const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
+    const int32_t* so = seg_off + p * (nlist + 1);
+    const int q = so[c + 1] - so[c];
+    return q > 0 ? ((q + kUnitQ - 1) / kUnitQ) * splits_of(vec_off[c + 1] - vec_off[c], p) : 0;
+}
+
+// grid 1: exclusive scan of the unit counts of the 2 * nlist (pass, cluster) segments.
+__global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
+                                                        const int32_t* vec_off, int nlist,
+                                                        int32_t* unit_off) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
-    const int pass = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int32_t* off = seg_off + pass * (nlist + 1);
-    int32_t* cc = chunk_cid + pass * max_chunks;
-    int32_t* cs = chunk_start + pass * max_chunks;
-    int32_t* cn = chunk_cnt + pass * max_chunks;
-    const int per = (nlist + kBlock - 1) / kBlock;
-    const int c0 = min(nlist, tid * per), c1 = min(nlist, c0 + per);
+    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const int E = 2 * nlist;
+    const int per = (E + kBlock - 1) / kBlock;
+    const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
     uint32_t local = 0;
-    for (int c = c0; c < c1; ++c) local += (uint32_t)((off[c + 1] - off[c] + kChunkQ - 1) / kChunkQ);
+    for (int e = e0; e < e1; ++e) local += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
     uint32_t inc = local;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
-        uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
+        const uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
         if (lane >= o) inc += t;
     }
     if (lane == kWave - 1) s_wtot[wid] = inc;
@@ -73,17 +87,40 @@ __global__ __launch_bounds__(256) void build_chunks_kernel(const int32_t* seg_of
         if (w < wid) run += s_wtot[w];
         total += s_wtot[w];
     }
-    for (int c = c0; c < c1; ++c) {
-        for (int s = off[c]; s < off[c + 1]; s += kChunkQ) {
-            if ((int)run < max_chunks) {
-                cc[run] = c;
-                cs[run] = s;
-                cn[run] = min(kChunkQ, off[c + 1] - s);
-            }
-            ++run;
-        }
+    for (int e = e0; e < e1; ++e) {
+        unit_off[e] = (int32_t)run;
+        run += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
     }
-    if (tid == 0) n_chunks[pass] = (int32_t)min<uint32_t>(total, (uint32_t)max_chunks);
+    if (tid == 0) unit_off[E] = (int32_t)total;
+}
+
+// One thread per unit: locate its segment by binary search over unit_off, then its query block
+// and vector slice.  Slices are multiples of 16 vectors and never empty (n > 16 S (S - 1)).
+__global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
+                                                        const int32_t* vec_off, int nlist,
+                                                        const int32_t* unit_off, int M1,
+                                                        int4* units, int max_units) {
+    const int E = 2 * nlist;
+    const int total = min(unit_off[E], max_units);
+    for (int u = blockIdx.x * blockDim.x + threadIdx.x; u < total; u += gridDim.x * blockDim.x) {
+        int lo = 0, hi = E - 1;  // largest e with unit_off[e] <= u
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (unit_off[mid] <= u) lo = mid;
+            else hi = mid - 1;
+        }
+        const int p = lo >= nlist ? 1 : 0, c = lo - p * nlist;
+        const int32_t* so = seg_off + p * (nlist + 1);
+        const int n = vec_off[c + 1] - vec_off[c];
+        const int S = splits_of(n, p);
+        const int local = u - unit_off[lo];
+        const int qb = local / S, sp = local - qb * S;
+        const int q = so[c + 1] - so[c];
+        const int cnt = min(kUnitQ, q - qb * kUnitQ);
+        const int len = ((n + S - 1) / S + 15) & ~15;
+        const int vb = sp * len, ve = min(n, vb + len);
+        units[u] = make_int4(c | (cnt << 20), (p ? M1 : 0) + so[c] + qb * kUnitQ, vb, ve);
+    }
 }
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n) {
@@ -99,98 +136,133 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// Canonical float64 distance of queued survivors; lane s < cnt refines survivor s against its
-// own query row (float32 queries, widened exactly).  Base rows are staged through LDS with
-// 128-byte coalesced loads (the same pattern serves mapped host memory).
-__device__ __forceinline__ double refine_multi(const float* __restrict__ xb,
-                                               const float* __restrict__ xq, int D,
-                                               const int32_t* spos_of, int cnt, int my_q,
-                                               float (*stage)[kWave + 1]) {
-    const int lane = lane_id();
-    const int half = lane >> 5, kk = lane & 31;
-    double acc = 0.0;
-    const float* qrow = xq + (size_t)my_q * D;
-    for (int d0 = 0; d0 < D; d0 += kBStageCh) {
-        const int ch = min(kBStageCh, D - d0);
-        for (int r0 = 0; r0 < cnt; r0 += 2) {
-            const int r = r0 + half;
-            float v = 0.0f;
-            if (r < cnt && kk < ch) v = xb[(size_t)spos_of[r] * D + d0 + kk];
-            if (r < cnt) stage[kk][r] = v;
-        }
-        wave_sync();
-        if (lane < cnt) {
-            for (int k = 0; k < ch; ++k) {
-                const double t = (double)stage[k][lane] - (double)qrow[d0 + k];
+// Exact test of the listed survivors, in place: slot s of query q holds a sorted position on
+// entry and (key, original id) on exit, or (kKeyInvalid, kIdInvalid) when the canonical
+// float64 distance exceeds tau[q].  One wave per query, one survivor per lane; each lane walks
+// its own row in dimension order with 16-byte loads.  An overflowed list (count > cap) is left
+// alone: the merge rescans that query's probes exhaustively.
+__global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int B) {
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
+    if (q >= B) return;
+    const int cnt = a.cand_cnt[q];
+    if (cnt > a.cap) return;
+    const double tau = a.tau[q];
+    const int D = a.D;
+    const float* qr = a.xq + (size_t)q * D;
+    uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+    int32_t* ci = a.cand_id + (size_t)q * a.cap;
+    const bool vec4 = (D & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.xb) |
+                                         reinterpret_cast<uintptr_t>(a.xq)) & 15) == 0;
+    unsigned long long ins = 0;
+    for (int s = lane; s < cnt; s += kWave) {
+        const int pos = ci[s];
+        const float* xr = a.xb + (size_t)pos * D;
+        double acc = 0.0;
+        if (vec4) {
+#pragma unroll 4
+            for (int d = 0; d < D; d += 4) {
+                const float4 x = *reinterpret_cast<const float4*>(xr + d);
+                const float4 y = *reinterpret_cast<const float4*>(qr + d);
+                double t = (double)x.x - (double)y.x;
+                acc = fma(t, t, acc);
+                t = (double)x.y - (double)y.y;
+                acc = fma(t, t, acc);
+                t = (double)x.z - (double)y.z;
+                acc = fma(t, t, acc);
+                t = (double)x.w - (double)y.w;
+                acc = fma(t, t, acc);
+            }
+        } else {
+            for (int d = 0; d < D; ++d) {
+                const double t = (double)xr[d] - (double)qr[d];
                 acc = fma(t, t, acc);
             }
         }
-        wave_sync();
+        const bool ok = acc <= tau;
+        ck[s] = ok ? key_of(acc) : kKeyInvalid;
+        ci[s] = ok ? a.orig_ids[pos] : kIdInvalid;
+        if (a.stats) ins += __popcll(__ballot(ok));  // lane 0 is active in every round
     }
-    return acc;
+    if (a.stats && lane == 0 && ins)
+        atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
 }
 
-template <bool UB_PASS>
+template <bool UB_PASS, int KS>
 __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
-    __shared__ float s_stage[kWavesPerBlock][kBStageCh][kWave + 1];
-    __shared__ int32_t s_queue[kWavesPerBlock][kBQueue];
-    __shared__ int32_t s_spos[kWavesPerBlock][kWave];
+    __shared__ float s_ubl[UB_PASS ? kWavesPerBlock : 1][UB_PASS ? kUnitQ * kWave : 1];
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int total = a.n_chunks[0];
-    const int nx = (total + 7) >> 3;
-    const int ch = (int)(blockIdx.x & 7) * nx + (int)(blockIdx.x >> 3);
-    if ((int)(blockIdx.x >> 3) >= nx || ch >= total) return;
-    const int cid = a.chunk_cid[ch], start = a.chunk_start[ch], cnt = a.chunk_cnt[ch];
-    const int qb = wid * kQW;
-    if (qb >= cnt) return;
-    const int nq = min(kQW, cnt - qb);
     const int j = lane & 15, g = lane >> 4;
-    const bool hasq = j < nq;
-    const int q = a.pair_qid[start + qb + (hasq ? j : 0)];
-    const int v0 = a.vec_off[cid], n = a.vec_off[cid + 1] - v0;
-    if (n <= 0) return;
-    const int t0 = a.tile_off[cid];
+    const int total = min(a.unit_off[a.unit_end], a.max_units);
+    const int nx = (total + 7) >> 3;
+    const int xcd = (int)(blockIdx.x & 7);
+    const int rb = xcd * nx, re = min(total, rb + nx);
+    int32_t* ctr = a.ctr + xcd * kCtrStride;
     const int D_pad = a.D_pad, D4 = D_pad >> 2, T = a.T;
-    const int KS = (D_pad + 63) >> 6;
-    const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
-    const double* xr = a.xrot64 + (size_t)q * D_pad;
-    const double* qe = a.qerr + (size_t)q * D_pad;
+    unsigned long long st_cand = 0, st_surv = 0;
 
-    // ---- per-query weights for this lane's dims ----
-    double mx = 0.0, Qp = 0.0, ep = 0.0;
-    for (int ks = 0; ks < KS; ++ks) {
+    for (;;) {
+        int ui = 0;
+        if (lane == 0) ui = atomicAdd(ctr, 1);
+        ui = __builtin_amdgcn_readfirstlane(__shfl(ui, 0, kWave)) + rb;
+        if (ui >= re) break;
+        const int4 un = a.units[ui];
+        const int cid = un.x & 0xfffff, nq = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
+        const bool hasq = j < nq;
+        const int q = a.pair_qid[start + (hasq ? j : 0)];
+        const int v0 = a.vec_off[cid];
+        const int t0 = a.tile_off[cid];
+        const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
+        const double* xr = a.xrot64 + (size_t)q * D_pad;
+        const double* qe = a.qerr + (size_t)q * D_pad;
+
+        // ---- per-query weights for this lane's dims ----
+        // (dd, ee: sum of delta^2 and eps^2 over the cluster's dims, for the f32 slack)
+        double mx = 0.0, Qp = 0.0, ep = 0.0, dd = 0.0, ee = 0.0;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll 4
-        for (int t = 0; t < 16; ++t) {
-            const int d = ks * 64 + g * 16 + t;
-            if (d < D_pad) {
-                const double qp = xr[d] - (double)a.vmin[off + d];
-                const double w = (double)a.delta[off + d] * qp;
-                mx = fmax(mx, fabs(w));
-                Qp = fma(qp, qp, Qp);
-                ep = fma(qe[d], qe[d], ep);
+            for (int t = 0; t < 16; ++t) {
+                const int d = ks * 64 + g * 16 + t;
+                if (d < D_pad) {
+                    const double dl = (double)a.delta[off + d];
+                    const double qp = xr[d] - (double)a.vmin[off + d];
+                    const double w = dl * qp;
+                    mx = fmax(mx, fabs(w));
+                    Qp = fma(qp, qp, Qp);
+                    ep = fma(qe[d], qe[d], ep);
+                    if constexpr (!UB_PASS) {
+                        const double e = (double)a.eps[off + d];
+                        dd = fma(dl, dl, dd);
+                        ee = fma(e, e, ee);
+                    }
+                }
             }
         }
-    }
 #pragma unroll
-    for (int o = 16; o < 64; o <<= 1) {
-        mx = fmax(mx, shfl_f64(mx, lane ^ o));
-        Qp += shfl_f64(Qp, lane ^ o);
-        ep += shfl_f64(ep, lane ^ o);
-    }
-    double s = 1.0;
-    if (mx > 0.0) {
-        s = ldexp(1.0, ilogb(mx) - 14);
-        if (mx / s > 32639.0) s *= 2.0;
-    }
-    v4i bhi[kMaxKS], blo[kMaxKS];
-    double errs = 0.0;
-    int wsum = 0;
+        for (int o = 16; o < 64; o <<= 1) {
+            mx = fmax(mx, shfl_f64(mx, lane ^ o));
+            Qp += shfl_f64(Qp, lane ^ o);
+            ep += shfl_f64(ep, lane ^ o);
+            if constexpr (!UB_PASS) {
+                dd += shfl_f64(dd, lane ^ o);
+                ee += shfl_f64(ee, lane ^ o);
+            }
+        }
+        double s = 1.0;
+        if (mx > 0x1p-100) {
+            s = ldexp(1.0, ilogb(mx) - 14);
+            if (mx / s > 32639.0) s *= 2.0;
+        }
+        v4i bhi[KS], blo[KS];
+        double errs = 0.0;
+        int wsum = 0, wabs = 0;
 #pragma unroll
-    for (int ks = 0; ks < kMaxKS; ++ks) {
-        uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
-        if (ks < KS) {
+        for (int ks = 0; ks < KS; ++ks) {
+            uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
             for (int t = 0; t < 16; ++t) {
                 const int d = ks * 64 + g * 16 + t;
                 int wi = 0;
@@ -203,189 +275,205 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                 const int hi = (wi + 128) >> 8;
                 const int lo = wi - (hi << 8);
                 wsum += wi;
+                wabs += abs(wi);
                 hw[t >> 2] |= ((uint32_t)hi & 0xffu) << (8 * (t & 3));
                 lw[t >> 2] |= ((uint32_t)lo & 0xffu) << (8 * (t & 3));
             }
+            bhi[ks] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+            blo[ks] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
         }
-        bhi[ks] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
-        blo[ks] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
-    }
 #pragma unroll
-    for (int o = 16; o < 64; o <<= 1) {
-        errs += shfl_f64(errs, lane ^ o);
-        wsum += __shfl_xor(wsum, o, kWave);
-    }
-    const double err_q = 255.0 * errs * (1.0 + 0x1p-40);
-    const double e_q = sqrt(ep) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
-    const double cW = 128.0 * (double)wsum;
-    const double c1 = 2.0 * s;
+        for (int o = 16; o < 64; o <<= 1) {
+            errs += shfl_f64(errs, lane ^ o);
+            wsum += __shfl_xor(wsum, o, kWave);
+            wabs += __shfl_xor(wabs, o, kWave);
+        }
+        const double err_q = 255.0 * errs * (1.0 + 0x1p-40);
+        const double e_q = sqrt(ep) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
+        const double cW = 128.0 * (double)wsum;
+        const double c1 = 2.0 * s;
 
-    // thresholds
-    double tau = (double)INFINITY;
-    double G = 0.0, c2 = 0.0, AQ = 0.0;
-    bool pass_all = true;
-    if constexpr (UB_PASS) {
-        AQ = (Qp + 2.0 * err_q) * (1.0 + 1e-13);
-    } else {
-        tau = a.tau[q];
-        if (tau < (double)INFINITY) {
-            pass_all = false;
+        // thresholds
+        double AQ = 0.0;
+        bool pass_all = true;
+        float c1f = 0.0f, c2f = 0.0f, H32 = 0.0f;
+        if constexpr (UB_PASS) {
+            AQ = (Qp + 2.0 * err_q) * (1.0 + 1e-13);
+        } else {
+            const double tau = a.tau[q];
             const double tq = sqrt(tau * a.rot_sq_max) * (1.0 + 1e-12) + e_q;
-            G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
-            c2 = -2.0 * tq;
-        }
-    }
-
-    float ubl[kUbList];
-    if constexpr (UB_PASS) {
-#pragma unroll
-        for (int i = 0; i < kUbList; ++i) ubl[i] = INFINITY;
-    }
-    int qn = 0;
-    unsigned long long st_cand = 0, st_surv = 0, st_ins = 0;
-    int32_t* my_queue = s_queue[wid];
-    int32_t* my_spos = s_spos[wid];
-    float(*my_stage)[kWave + 1] = s_stage[wid];
-
-    auto flush = [&](int fcnt) {
-        int e = 0, my_sq = q;
-        double my_tau = tau;
-        if (lane < fcnt) e = my_queue[lane];
-        const int li = e >> 4, jj = e & 15;
-        my_sq = __shfl(q, jj, kWave);
-        my_tau = shfl_f64(tau, jj);
-        if (lane < fcnt) my_spos[lane] = v0 + li;
-        wave_sync();
-        const double d64 = refine_multi(a.xb, a.xq, a.D, my_spos, fcnt, my_sq, my_stage);
-        const bool ok = lane < fcnt && d64 <= my_tau;
-        if (a.stats) st_ins += __popcll(__ballot(ok));
-        if (ok) {
-            const int slot = atomicAdd(&a.cand_cnt[my_sq], 1);
-            if (slot < a.cap) {
-                a.cand_key[(size_t)my_sq * a.cap + slot] = key_of(d64);
-                a.cand_id[(size_t)my_sq * a.cap + slot] = a.tile_oids[(size_t)t0 * T + li];
+            if (tq < 1e30) {
+                // Survive iff A - r^2 - 2 tq r <= 2 s dot + 2 err - Q + tq^2 (the norm-form
+                // lower bound against sqrt(tau) scaled to the rotated space).  Evaluated as
+                //   L = fma(c2, r, fma(-r, r, A_lo)) <= R = fma(c1, float(acc), H32)
+                // with acc = dot - 128 sum(w_int) (exact int32), c1 = 2s (a power of two),
+                // c2 <= -2 tq and H32 >= 2 s 128 sum(w_int) + 2 err - Q + tq^2 + slack.  Each
+                // of the 4 f32 roundings is at most 2^-24 of a term bounded by
+                //   X = A_max + r_max^2 + 2 tq r_max + c1 acc_max + |H|,
+                // with A_max = 255^2 sum delta^2 (codes <= 255), r_max = 2 sqrt(sum eps^2)
+                // (r_x <= |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms) and
+                // |acc| <= acc_max = 128 sum |w_int|; slack = 2^-22 X covers them all.
+                pass_all = false;
+                const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
+                const double H = c1 * cW + G;
+                const double a_max = 65025.0 * dd * (1.0 + 1e-12);
+                const double r_max = 2.0 * sqrt(ee) * (1.0 + 1e-12);
+                const double X = a_max + r_max * r_max + 2.0 * tq * r_max +
+                                 c1 * 128.0 * (double)wabs + fabs(H);
+                const double slack = 0x1p-22 * X * (1.0 + 1e-6) + 1e-30;
+                H32 = __double2float_ru(H + slack);
+                c1f = (float)c1;
+                c2f = -__double2float_ru(2.0 * tq);
             }
         }
-        wave_sync();
-    };
 
-    const int ntl = (n + 15) >> 4;
-    for (int tt = 0; tt < ntl; ++tt) {
-        // A operand: codes of vector tt*16 + (lane & 15), dims ks*64 + g*16 + [0, 16)
-        const int lia = tt * 16 + j;
-        const bool va = lia < n;
-        const uint32_t* cp = a.sq8 + ((size_t)(t0 + lia / T) * D4) * T + (lia % T);
-        v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+        float ubl[kUbList];
+        if constexpr (UB_PASS) {
 #pragma unroll
-        for (int ks = 0; ks < kMaxKS; ++ks) {
-            if (ks < KS) {
-                v4i av;
+            for (int i = 0; i < kUbList; ++i) ubl[i] = INFINITY;
+        }
+
+        // A operand of the 16-vector tile starting at cluster vector li0 (T-tile ct, offset cw)
+        // and the per-vector scalars of this lane's 4 result rows.
+        auto load = [&](int ct, int cw, int li0, v4i (&A)[KS], float2 (&R)[4]) {
+            const uint32_t* cp = a.sq8 + ((size_t)(t0 + ct) * D4) * T + cw + j;
+            const bool va = li0 + j < ve;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
                 for (int t4 = 0; t4 < 4; ++t4) {
                     const int d4 = ks * 16 + g * 4 + t4;
-                    const uint32_t wv = (va && d4 < D4) ? cp[(size_t)d4 * T] : 0x80808080u;
-                    av[t4] = (int)(wv ^ 0x80808080u);
+                    uint32_t wv = 0x80808080u;
+                    if (va && d4 < D4) wv = cp[(size_t)d4 * T];
+                    A[ks][t4] = (int)(wv ^ 0x80808080u);
                 }
-                acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bhi[ks], acc_hi, 0, 0, 0);
-                acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, blo[ks], acc_lo, 0, 0, 0);
             }
-        }
-        // epilogue: rows 4g + r (vectors), column j (query)
-        uint32_t sbits = 0;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int li = tt * 16 + 4 * g + r;
-            const bool ok = hasq && li < n;
-            const double dot = (double)((acc_hi[r] << 8) + acc_lo[r]) + cW;
-            const double2 ar = ok ? *reinterpret_cast<const double2*>(a.vec_Ar + 2 * (size_t)(v0 + li))
-                                  : double2{0.0, 0.0};
-            if constexpr (UB_PASS) {
-                if (ok) {
-                    const double E = fmax(fma(-c1, dot, ar.x * (1.0 + 1e-13) + AQ), 0.0);
-                    const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
-                    const float u = (s32 + (float)ar.y + (float)e_q) * (1.0f + 0x1p-20f);
-                    if (u < ubl[kUbList - 1]) {
-#pragma unroll
-                        for (int i = kUbList - 1; i > 0; --i)
-                            ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
-                        ubl[0] = fminf(ubl[0], u);
-                    }
-                }
-            } else {
-                bool sv = ok;
-                if (ok && !pass_all) {
-                    const double lhs = fma(c2, ar.y, fma(-ar.y, ar.y, ar.x * (1.0 - 1e-13)));
-                    const double rhs = fma(c1, dot, G);
-                    sv = lhs <= rhs;
-                }
-                sbits |= (uint32_t)sv << r;
-            }
-        }
-        if (a.stats) st_cand += (unsigned long long)nq * (unsigned long long)min(16, n - tt * 16);
-        if constexpr (!UB_PASS) {
-            if (__ballot(sbits != 0) == 0) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const bool sv = (sbits >> r) & 1u;
-                const uint64_t m = __ballot(sv);
-                if (m == 0) continue;
-                if (sv) my_queue[qn + mask_rank(m)] = ((tt * 16 + 4 * g + r) << 4) | j;
-                qn += __popcll(m);
-                if (a.stats) st_surv += __popcll(m);
-                if (qn >= kWave) {
-                    wave_sync();
-                    flush(kWave);
-                    const int rest = qn - kWave;
-                    int32_t keep = 0;
-                    if (lane < rest) keep = my_queue[kWave + lane];
-                    wave_sync();
-                    if (lane < rest) my_queue[lane] = keep;
-                    qn = rest;
-                    wave_sync();
+                const int li = li0 + 4 * g + r;
+                float2 v = make_float2(0.0f, 0.0f);
+                if (hasq && li < ve) v = a.vec_Ar[v0 + li];
+                R[r] = v;
+            }
+        };
+
+        auto compute = [&](const v4i (&A)[KS], const float2 (&R)[4], int li0) {
+            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
+                acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
+            }
+            // epilogue: rows 4g + r (vectors), column j (query)
+            uint32_t sbits = 0;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int li = li0 + 4 * g + r;
+                const bool ok = hasq && li < ve;
+                const int acc = (acc_hi[r] << 8) + acc_lo[r];
+                if constexpr (UB_PASS) {
+                    if (ok) {
+                        const double dot = (double)acc + cW;
+                        const double Alo = (double)R[r].x, rr = (double)R[r].y;
+                        const double E = fmax(fma(-c1, dot, Alo * (1.0 + 0x1p-22) + AQ), 0.0);
+                        const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
+                        const float u = (s32 + (float)rr + (float)e_q) * (1.0f + 0x1p-20f);
+                        if (u < ubl[kUbList - 1]) {
+#pragma unroll
+                            for (int i = kUbList - 1; i > 0; --i)
+                                ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
+                            ubl[0] = fminf(ubl[0], u);
+                        }
+                    }
+                } else {
+                    const float rr = R[r].y;
+                    const float L = fmaf(c2f, rr, fmaf(-rr, rr, R[r].x));
+                    const float Rv = fmaf(c1f, (float)acc, H32);
+                    const bool sv = ok && (pass_all || L <= Rv);
+                    sbits |= (uint32_t)sv << r;
                 }
             }
+            if (a.stats) st_cand += (unsigned long long)nq * (unsigned long long)min(16, ve - li0);
+            if constexpr (!UB_PASS) {
+                if (__ballot(sbits != 0) == 0) return;
+                // rare: append survivors (sorted position) to the query's list
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if ((sbits >> r) & 1u) {
+                        const int slot = atomicAdd(&a.cand_cnt[q], 1);
+                        if (slot < a.cap) a.cand_id[(size_t)q * a.cap + slot] = v0 + li0 + 4 * g + r;
+                    }
+                }
+                if (a.stats) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) st_surv += __popcll(__ballot((sbits >> r) & 1u));
+                }
+            }
+        };
+
+        // ---- tiles of 16 vectors, two register sets in flight ----
+        const int tb = vb >> 4, te = (ve + 15) >> 4;
+        if (tb < te) {
+            v4i A0[KS], A1[KS];
+            float2 R0[4], R1[4];
+            int ct = (tb << 4) / T, cw = (tb << 4) - ct * T;
+            load(ct, cw, tb << 4, A0, R0);
+            for (int tt = tb; tt < te; tt += 2) {
+                int ct1 = ct, cw1 = cw + 16;
+                if (cw1 == T) { cw1 = 0; ++ct1; }
+                if (tt + 1 < te) load(ct1, cw1, (tt + 1) << 4, A1, R1);
+                compute(A0, R0, tt << 4);
+                if (tt + 1 >= te) break;
+                int ct2 = ct1, cw2 = cw1 + 16;
+                if (cw2 == T) { cw2 = 0; ++ct2; }
+                if (tt + 2 < te) load(ct2, cw2, (tt + 2) << 4, A0, R0);
+                compute(A1, R1, (tt + 1) << 4);
+                ct = ct2;
+                cw = cw2;
+            }
+        }
+
+        if constexpr (UB_PASS) {
+            // K-th smallest upper bound of each query: merge the 4 lanes' lists (64 values) by a
+            // register bitonic sort, then atomicMin into tau[q] (float64 bit pattern).
+            float* s_ub = s_ubl[UB_PASS ? wid : 0];
+            wave_sync();
+#pragma unroll
+            for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
+            wave_sync();
+            for (int jj = 0; jj < nq; ++jj) {
+                uint64_t k = key_of((double)s_ub[jj * 64 + lane]);
+                int32_t id = lane;
+                wave_sort64(k, id);
+                const uint64_t kk = readlane_u64(k, a.K - 1);
+                const int qq = __shfl(q, jj, kWave);
+                if (lane == 0 && dist_of(kk) < (double)INFINITY) {
+                    const double u = dist_of(kk);
+                    const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
+                    atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
+                              (unsigned long long)key_of(tub));
+                }
+            }
+            wave_sync();
         }
     }
 
-    if constexpr (UB_PASS) {
-        // K-th smallest upper bound of each query: merge the 4 lanes' lists (64 values) by a
-        // register bitonic sort, then atomicMin into tau[q] (float64 bit pattern).
-        float* s_ub = &my_stage[0][0];
-#pragma unroll
-        for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
-        wave_sync();
-        for (int jj = 0; jj < nq; ++jj) {
-            uint64_t k = key_of((double)s_ub[jj * 64 + lane]);
-            int32_t id = lane;
-            wave_sort64(k, id);
-            const uint64_t kk = readlane_u64(k, a.K - 1);
-            const int qq = __shfl(q, jj, kWave);
-            if (lane == 0 && dist_of(kk) < (double)INFINITY) {
-                const double u = dist_of(kk);
-                const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
-                          (unsigned long long)key_of(tub));
-            }
-        }
-    } else if (qn > 0) {
-        wave_sync();
-        flush(qn);
-    }
     if (a.stats && lane == 0) {
         const int slot = (int)(blockIdx.x % kStatSlots) * 4;
         atomicAdd(&a.stats[slot + 0], st_cand);
         atomicAdd(&a.stats[slot + 1], st_cand * (unsigned long long)D_pad);
         atomicAdd(&a.stats[slot + 2], st_surv);
-        atomicAdd(&a.stats[slot + 3], st_ins);
     }
 }
 
-template __global__ void batch_scan_kernel<true>(BatchArgs);
-template __global__ void batch_scan_kernel<false>(BatchArgs);
-
-}  // namespace trident
-
-namespace trident {
+template __global__ void batch_scan_kernel<true, 1>(BatchArgs);
+template __global__ void batch_scan_kernel<true, 2>(BatchArgs);
+template __global__ void batch_scan_kernel<true, 3>(BatchArgs);
+template __global__ void batch_scan_kernel<true, 4>(BatchArgs);
+template __global__ void batch_scan_kernel<false, 1>(BatchArgs);
+template __global__ void batch_scan_kernel<false, 2>(BatchArgs);
+template __global__ void batch_scan_kernel<false, 3>(BatchArgs);
+template __global__ void batch_scan_kernel<false, 4>(BatchArgs);
 
 // tau_sq output of the batched route: the seeded float64 threshold, rounded up to float32.
 __global__ void tau_to_f32_kernel(const double* tau, float* out, int B) {

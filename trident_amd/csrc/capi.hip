@@ -82,22 +82,23 @@ struct Workspace {
     int32_t* list_id;
     double* tau64;
     unsigned long long* stat_slots;  // [kStatSlots, 4] telemetry partials
-    int32_t* chunk_cid;              // [2, max_chunks] batched-route chunk tables
-    int32_t* chunk_start;
-    int32_t* chunk_cnt;
-    int32_t* n_chunks;               // [2]
-    int64_t max_chunks;
+    int4* units;                     // [max_units] batched-route work units (both passes)
+    int32_t* unit_off;               // [2 * nlist + 1]
+    int32_t* unit_ctr;               // [2, 8 * kCtrStride] per-launch, per-XCD counters
+    int64_t max_units;
     size_t bytes;
 };
 
-// Upper bound on the chunks of one pass: every cluster rounds its pair count up to a chunk.
-inline int64_t max_chunks_of(int64_t pairs, int64_t nlist) { return (pairs + 63) / 64 + nlist; }
+// Candidate-list slots per query.  The batched route stores every lower-bound survivor there
+// (before its exact test), so lists are at least 16 * nprobe deep; a longer list makes the
+// merge rescan that query's probes exhaustively.
+inline int64_t cand_cap(int64_t nprobe, int64_t K) { return nprobe * std::max<int64_t>(K, 16); }
 
 Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
     Carver c{static_cast<char*>(base)};
     Workspace w;
     const int64_t KP = K <= 64 ? 64 : 128;
-    const int64_t cap = nprobe * K;
+    const int64_t cap = cand_cap(nprobe, K);
     w.xq64 = c.take<double>(B * ix->D);
     w.xrot64 = c.take<double>(B * ix->D_pad);
     w.qerr = c.take<double>(B * ix->D_pad);
@@ -117,11 +118,10 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.list_id = c.take<int32_t>(B * KP);
     w.tau64 = c.take<double>(B);
     w.stat_slots = c.take<unsigned long long>((size_t)kStatSlots * 4);
-    w.max_chunks = max_chunks_of(B * nprobe, ix->nlist);
-    w.chunk_cid = c.take<int32_t>(2 * w.max_chunks);
-    w.chunk_start = c.take<int32_t>(2 * w.max_chunks);
-    w.chunk_cnt = c.take<int32_t>(2 * w.max_chunks);
-    w.n_chunks = c.take<int32_t>(2);
+    w.max_units = max_units_of(B * nprobe, ix->nlist);
+    w.units = c.take<int4>(w.max_units);
+    w.unit_off = c.take<int32_t>(2 * (int64_t)ix->nlist + 1);
+    w.unit_ctr = c.take<int32_t>(2 * 8 * kCtrStride);
     w.bytes = c.off;
     return w;
 }
@@ -222,7 +222,8 @@ int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
 // average, where the contraction is dense enough for the matrix cores.
 int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                  int nprobe, int* route) {
-    const bool ok = ix->vec_Ar && K <= 64 && ix->D_pad <= 256;
+    const bool ok = ix->vec_Ar && ix->orig_ids_sorted && K <= 64 && ix->D_pad <= 256 &&
+                    max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
         case TRIDENT_ROUTE_PAIR:
             *route = TRIDENT_ROUTE_PAIR;
@@ -243,12 +244,44 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
     }
 }
 
-template <bool UB>
-int launch_batch(const BatchArgs& b, int64_t max_chunks, hipStream_t st) {
-    if (max_chunks <= 0) return TRIDENT_OK;
-    const unsigned grid = (unsigned)(((max_chunks + 7) / 8) * 8);
-    batch_scan_kernel<UB><<<grid, kBlock, 0, st>>>(b);
+// Persistent grid of a batched-scan variant: as many workgroups as are resident at once (CUs x
+// the occupancy its registers and LDS allow), rounded to a multiple of 8 so every XCD gets the
+// same number; cached per device and variant.
+template <bool UB, int KS>
+unsigned persistent_grid() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!cached[dev]) {
+        int cu = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cu < 1)
+            cu = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void*>(&batch_scan_kernel<UB, KS>), kBlock, 0) !=
+                hipSuccess ||
+            per_cu < 1)
+            per_cu = 2;
+        cached[dev] = std::max(8, ((cu * per_cu + 7) / 8) * 8);
+    }
+    return (unsigned)cached[dev];
+}
+
+template <bool UB, int KS>
+int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
+    batch_scan_kernel<UB, KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
     return check_launch("batch_scan_kernel");
+}
+
+template <bool UB>
+int launch_batch(const BatchArgs& b, hipStream_t st) {
+    switch ((b.D_pad + 63) / 64) {
+        case 1: return launch_batch_ks<UB, 1>(b, st);
+        case 2: return launch_batch_ks<UB, 2>(b, st);
+        case 3: return launch_batch_ks<UB, 3>(b, st);
+        case 4: return launch_batch_ks<UB, 4>(b, st);
+        default: return fail(TRIDENT_ERR_UNSUPPORTED, "batched route needs D_pad <= 256");
+    }
 }
 
 int launch_merge(const MergeArgs& m, int KP, hipStream_t st) {
@@ -448,7 +481,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
     const int KP = K <= 64 ? 64 : 128;
-    const int64_t cap = (int64_t)nprobe * K;
+    const int64_t cap = cand_cap(nprobe, K);
     if (out->stats) {
         if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
         if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
@@ -477,7 +510,9 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.xb = ix->xb_sorted;
         b.vmin = ix->vmin;
         b.delta = ix->delta;
-        b.vec_Ar = ix->vec_Ar;
+        b.eps = ix->eps_dim;
+        b.orig_ids = ix->orig_ids_sorted;
+        b.vec_Ar = reinterpret_cast<const float2*>(ix->vec_Ar);
         b.D = ix->D;
         b.D_pad = ix->D_pad;
         b.T = ix->tile_size;
@@ -494,24 +529,25 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.stats = out->stats ? w.stat_slots : nullptr;
         b.rot_sq_min = ix->rot_sq_min;
         b.rot_sq_max = ix->rot_sq_max;
-        const int64_t mc = w.max_chunks;
-        build_chunks_kernel<<<2, kBlock, 0, st>>>(w.seg_off, ix->nlist, w.chunk_cid, w.chunk_start,
-                                                  w.chunk_cnt, w.n_chunks, (int)mc);
-        if ((rc = check_launch("build_chunks_kernel"))) return rc;
+        b.units = w.units;
+        b.unit_off = w.unit_off;
+        b.max_units = (int)w.max_units;
+        b.pair_qid = w.pair_qids;
+        unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
+                                               w.unit_off);
+        if ((rc = check_launch("unit_scan_kernel"))) return rc;
+        unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
+                           st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, w.unit_off, (int)M1,
+                                 w.units, (int)w.max_units);
+        if ((rc = check_launch("unit_fill_kernel"))) return rc;
         fill_u64_kernel<<<(unsigned)std::min<int64_t>((B + 255) / 256, 4096), 256, 0, st>>>(
             reinterpret_cast<unsigned long long*>(w.tau64), 0x7ff0000000000000ull, B);
         if ((rc = check_launch("fill_u64_kernel"))) return rc;
-        auto use_pass = [&](int p) {
-            b.chunk_cid = w.chunk_cid + p * mc;
-            b.chunk_start = w.chunk_start + p * mc;
-            b.chunk_cnt = w.chunk_cnt + p * mc;
-            b.n_chunks = w.n_chunks + p;
-            b.pair_qid = p ? p2q : p1q;
-        };
-        const int64_t mc1 = max_chunks_of(M1, ix->nlist), mc2 = max_chunks_of(M2, ix->nlist);
+        if ((rc = fill(w.unit_ctr, 0, 2 * 8 * kCtrStride, st))) return rc;
         if (M1 > 0) {  // pass A: per-query upper-bound threshold from the first p_init probes
-            use_pass(0);
-            if ((rc = launch_batch<true>(b, mc1, st))) return rc;
+            b.unit_end = ix->nlist;
+            b.ctr = w.unit_ctr;
+            if ((rc = launch_batch<true>(b, st))) return rc;
         }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
         if (out->tau_sq) {
@@ -520,15 +556,14 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
-        if (M1 > 0) {  // pass B over every probe: lower bound, exact refine, append <= tau
-            use_pass(0);
-            if ((rc = launch_batch<false>(b, mc1, st))) return rc;
-        }
-        if (M2 > 0) {
-            use_pass(1);
-            if ((rc = launch_batch<false>(b, mc2, st))) return rc;
-        }
+        // pass B over every probe: lower bound, exact refine, append <= tau
+        b.unit_end = 2 * ix->nlist;
+        b.ctr = w.unit_ctr + 8 * kCtrStride;
+        if ((rc = launch_batch<false>(b, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
+        refine_survivors_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
+                                  st>>>(b, B);
+        if ((rc = check_launch("refine_survivors_kernel"))) return rc;
         m.use_prev = 0;
         m.out_d = out->topk_d;
         m.out_i = out->topk_i;

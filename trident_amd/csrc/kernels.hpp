@@ -74,16 +74,19 @@ struct BatchArgs {
     const float* xb;
     const float* vmin;
     const float* delta;
-    const double* vec_Ar;       // [N, 2]
+    const float* eps;           // per-dim |x_rot - x_hat| bound (bounds r_x for the f32 slack)
+    const int32_t* orig_ids;    // [N] sorted position -> original id
+    const float2* vec_Ar;       // [N] (A rounded down, r rounded up)
     int D, D_pad, T, per_cluster;
     const float* xq;            // [B, D] float32 queries
     const double* xrot64;       // [B, D_pad]
     const double* qerr;         // [B, D_pad]
-    const int32_t* chunk_cid;   // chunk table of this pass
-    const int32_t* chunk_start;
-    const int32_t* chunk_cnt;
-    const int32_t* n_chunks;    // device scalar
-    const int32_t* pair_qid;
+    const int4* units;          // work units {cid | cnt << 20, pair start, v_begin, v_end}
+    const int32_t* unit_off;    // [2 * nlist + 1] unit offsets of the (pass, cluster) segments
+    int unit_end;               // this launch covers units [0, unit_off[unit_end])
+    int max_units;
+    int32_t* ctr;               // [8 * kCtrStride] per-XCD work counters, zero at launch
+    const int32_t* pair_qid;    // pass-1 pairs then pass-2 pairs
     double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
     uint64_t* cand_key;
     int32_t* cand_id;
@@ -134,16 +137,31 @@ __global__ void pair_scan_kernel(ScanArgs a);
 template <int KP>
 __global__ void merge_kernel(MergeArgs a);
 
-__global__ void build_chunks_kernel(const int32_t* seg_off, int nlist, int32_t* chunk_cid,
-                                    int32_t* chunk_start, int32_t* chunk_cnt, int32_t* n_chunks,
-                                    int max_chunks);
+// Batched-route work units: 16 queries of one cluster x one slice of <= kSplitVec-ish vectors
+// (at most kMaxSplit slices per cluster, so a pass has <= kMaxSplit * (pairs / 16 + 2 nlist)).
+constexpr int kUnitQ = 16;
+constexpr int kSplitVec = 1024;
+constexpr int kMaxSplit = 8;
+constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
+
+inline int64_t max_units_of(int64_t pairs, int64_t nlist) {
+    return (int64_t)kMaxSplit * ((pairs + kUnitQ - 1) / kUnitQ + 2 * nlist);
+}
+
+__global__ void unit_scan_kernel(const int32_t* seg_off, const int32_t* vec_off, int nlist,
+                                 int32_t* unit_off);
+
+__global__ void unit_fill_kernel(const int32_t* seg_off, const int32_t* vec_off, int nlist,
+                                 const int32_t* unit_off, int M1, int4* units, int max_units);
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
 
 __global__ void tau_to_f32_kernel(const double* tau, float* out, int B);
 
-template <bool UB_PASS>
+template <bool UB_PASS, int KS>
 __global__ void batch_scan_kernel(BatchArgs a);
+
+__global__ void refine_survivors_kernel(BatchArgs a, int B);
 
 __global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
                                   const int32_t* __restrict__ cids,

@@ -234,8 +234,8 @@ def launch_trident_v4_search(
             _need(t.numel() == rows * D_pad, f"{name} must be [{rows}, D_pad]")
         _check_tensor("blk_bounds4", blk_bounds4, torch.int32, dev, 1)
     if vec_Ar is not None:
-        _check_tensor("vec_Ar", vec_Ar, torch.float64, dev, 2)
-        _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float64")
+        _check_tensor("vec_Ar", vec_Ar, torch.float32, dev, 2)
+        _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float32")
     if stats_buf is not None:
         _check_tensor("stats_buf", stats_buf, torch.int64, dev)
         _need(stats_buf.numel() >= 4, "stats_buf needs 4 entries")

@@ -220,10 +220,12 @@ class TridentV4Index:
         delta = torch.where(empty, torch.ones_like(delta), delta)
         codes = torch.empty((N, D_pad), device=dev, dtype=torch.uint8)
         err_max = torch.zeros((rows, D_pad), device=dev, dtype=torch.float64)
-        # Per-vector scalars of the batched (matrix-core) bound, sorted order, float64 pairs:
-        #   vec_Ar[v, 0] = A_v = sum_d (code_d * delta_d)^2   (exact products, float64 sum)
-        #   vec_Ar[v, 1] = r_v >= |x_rot(exact) - x_hat|_2     (quantisation + rotation error)
-        self.vec_Ar = torch.empty((N, 2), device=dev, dtype=torch.float64)
+        # Per-vector scalars of the batched (matrix-core) bound, sorted order, float32 pairs:
+        #   vec_Ar[v, 0] <= A_v * (1 - 1e-13),  A_v = sum_d (code_d * delta_d)^2 (exact products;
+        #                   the float64 sum is within D * 2^-53 relative, far inside the margin)
+        #   vec_Ar[v, 1] >= r_v >= |x_rot(exact) - x_hat|_2   (quantisation + rotation error)
+        # The kernel uses vec_Ar[v, 0] * (1 + 2^-22) >= A_v as the upper value of A_v.
+        self.vec_Ar = torch.empty((N, 2), device=dev, dtype=torch.float32)
         for s in range(0, N, chunk_rows):
             e = min(N, s + chunk_rows)
             xr64, rerr = rotate(s, e)
@@ -237,9 +239,10 @@ class TridentV4Index:
             err = (xr64 - xhat).abs() + rerr
             idx = ci.unsqueeze(1).expand(-1, D_pad)
             err_max.scatter_reduce_(0, idx, err, reduce="amax", include_self=True)
-            self.vec_Ar[s:e, 0] = (cdl * cdl).sum(1)
+            a64 = (cdl * cdl).sum(1) * (1.0 - 1e-13)
+            self.vec_Ar[s:e, 0] = -round_up_f32(-a64)
             r_q = torch.sqrt(((xr64 - xhat) ** 2).sum(1)) + torch.sqrt((rerr ** 2).sum(1))
-            self.vec_Ar[s:e, 1] = r_q * (1.0 + 1e-12) + 1e-300
+            self.vec_Ar[s:e, 1] = round_up_f32(r_q * (1.0 + 1e-12) + 1e-300)
         self.vmin_pad = vmin.contiguous()
         self.delta_pad = delta.contiguous()
         self.eps_pad = round_up_f32(err_max * (1.0 + 2.0 ** -20) + 1e-300).contiguous()
