@@ -20,24 +20,26 @@
 // canonical float64 distance.
 //
 // Pass A (UB):  for the first p_init probes of each query, the K-th smallest upper bound over
-//               a slice of the cluster -> atomicMin into tau[q] (the reference's Stage X
-//               seeding, src/trident_v4_kernels.cu:626-676, computed for 16 queries at once; the
-//               K-th smallest upper bound of any K vectors bounds the K-th distance).
+//               the cluster -> atomicMin into tau[q] (the reference's Stage X seeding,
+//               src/trident_v4_kernels.cu:626-676, computed for 64 queries at once; the K-th
+//               smallest upper bound of any K vectors bounds the K-th distance).
 // Pass B (LB):  for every probe, vectors whose lower bound passes tau[q] are appended (sorted
 //               position) to the query's candidate list.  The test runs in float32 with an
-//               additive slack that bounds every rounding of it (see lb_slack below).
+//               additive slack that bounds every rounding of it.
 // Refine:       one wave per query computes the canonical float64 distance of each listed
 //               survivor and keeps it iff <= tau[q] (the reference's Stage Z, :796-941).
 //
-// Scheduling: a work unit is (cluster, 16 queries, slice of the cluster's vectors).  Units of
-// one launch are split into 8 contiguous ranges, one per XCD (blockIdx & 7), so a cluster's
-// codes are read from HBM once per XCD and then served by that XCD's L2; within a range every
-// wave takes the next unit from its XCD's counter (persistent grid, one atomic per unit).
-// Lane l = (i = l & 15, g = l >> 4) holds, for every 64-dim step, bytes of dims
-// step*64 + g*16 + [0, 16): vector i's codes in the A operand and query i's weights in the B
-// operand (any dim-to-byte assignment shared by A and B computes the same contraction); the
-// result row 4g + r, column i sits in lane l, register r.  The next 16-vector tile's codes and
-// per-vector scalars are loaded before the current tile's MFMAs and epilogue.
+// Scheduling: a work unit is (cluster, <= 64 queries, slice of the cluster's vectors); each of
+// the workgroup's 4 waves owns 16 of the queries (the MFMA N dimension).  Units of one launch
+// are split into 8 contiguous ranges, one per XCD (blockIdx & 7), so a cluster's codes are read
+// from HBM once per XCD and then served by that XCD's L2; within a range each workgroup takes
+// the next unit from its XCD's counter (persistent grid, one atomic per unit).  The unit's
+// vectors stream through LDS in 64-vector blocks, double-buffered: all 256 threads load block
+// b+1 (16-byte loads, D_pad/4 rows of 256 contiguous bytes) while the waves run block b from
+// LDS, one barrier per block.  Lane l = (i = l & 15, g = l >> 4) holds, for every 64-dim step,
+// bytes of dims step*64 + g*16 + [0, 16): vector i's codes in the A operand and query i's
+// weights in the B operand (any dim-to-byte assignment shared by A and B computes the same
+// contraction); the result row 4g + r, column i sits in lane l, register r.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -45,7 +47,9 @@ namespace trident {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kUbList = 16;                      // per-lane upper-bound list (K <= 64)
+constexpr int kUbList = 16;  // per-lane upper-bound list (K <= 64)
+constexpr int kBlkV = 64;    // vectors per LDS block
+constexpr int kWaveQ = 16;   // queries per wave
 
 // Vector slices of a cluster in pass p.  Pass-1 segments (the seeding probes) keep whole
 // clusters: the K-th smallest upper bound over a slice is a much weaker threshold than over
@@ -95,7 +99,8 @@ __global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
 }
 
 // One thread per unit: locate its segment by binary search over unit_off, then its query block
-// and vector slice.  Slices are multiples of 16 vectors and never empty (n > 16 S (S - 1)).
+// and vector slice.  Slices start on 64-vector blocks and are never empty (n > 64 S (S - 1)
+// whenever S = ceil(n / kSplitVec) > 1).
 __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
                                                         const int32_t* vec_off, int nlist,
                                                         const int32_t* unit_off, int M1,
@@ -117,7 +122,7 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
         const int qb = local / S, sp = local - qb * S;
         const int q = so[c + 1] - so[c];
         const int cnt = min(kUnitQ, q - qb * kUnitQ);
-        const int len = ((n + S - 1) / S + 15) & ~15;
+        const int len = ((n + S - 1) / S + kBlkV - 1) & ~(kBlkV - 1);
         const int vb = sp * len, ve = min(n, vb + len);
         units[u] = make_int4(c | (cnt << 20), (p ? M1 : 0) + so[c] + qb * kUnitQ, vb, ve);
     }
@@ -188,12 +193,23 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
         atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
 }
 
+// LDS word of (row d4, vector v) in a 64-vector code block: a row's four 16-vector groups are
+// rotated by (d4 >> 2) & 3, so the four lane groups g of one A-operand read (rows
+// ks*16 + g*4 + t4, same 16 vectors) land in four different 16-bank groups.
+__device__ __forceinline__ int blk_word(int d4, int v) {
+    return d4 * kBlkV + ((((v >> 4) ^ (d4 >> 2)) & 3) << 4) + (v & 15);
+}
+
 template <bool UB_PASS, int KS>
 __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
-    __shared__ float s_ubl[UB_PASS ? kWavesPerBlock : 1][UB_PASS ? kUnitQ * kWave : 1];
+    constexpr int kRows = KS * 16;  // code rows (4 dims each) held per block buffer
+    __shared__ uint4 s_codes[2][kRows * kBlkV / 4];
+    __shared__ __align__(16) float2 s_ar[2][kBlkV];
+    __shared__ float s_ubl[UB_PASS ? kWavesPerBlock : 1][UB_PASS ? kWaveQ * kWave : 1];
+    __shared__ int s_unit[2];
 
-    const int lane = threadIdx.x & 63;
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
     const int total = min(a.unit_off[a.unit_end], a.max_units);
     const int nx = (total + 7) >> 3;
@@ -203,127 +219,131 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
     const int D_pad = a.D_pad, D4 = D_pad >> 2, T = a.T;
     unsigned long long st_cand = 0, st_surv = 0;
 
-    for (;;) {
-        int ui = 0;
-        if (lane == 0) ui = atomicAdd(ctr, 1);
-        ui = __builtin_amdgcn_readfirstlane(__shfl(ui, 0, kWave)) + rb;
+    for (int it = 0;; ++it) {
+        // (s_unit alternates: slot it & 1 is rewritten two barriers after everyone read it)
+        if (tid == 0) s_unit[it & 1] = atomicAdd(ctr, 1);
+        __syncthreads();
+        const int ui = __builtin_amdgcn_readfirstlane(s_unit[it & 1]) + rb;
         if (ui >= re) break;
         const int4 un = a.units[ui];
-        const int cid = un.x & 0xfffff, nq = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
+        const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
+        const int nq = min(max(cnt - wid * kWaveQ, 0), kWaveQ);  // this wave's queries
+        const bool active = nq > 0;
         const bool hasq = j < nq;
-        const int q = a.pair_qid[start + (hasq ? j : 0)];
         const int v0 = a.vec_off[cid];
         const int t0 = a.tile_off[cid];
-        const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
-        const double* xr = a.xrot64 + (size_t)q * D_pad;
-        const double* qe = a.qerr + (size_t)q * D_pad;
+        int q = 0;
 
-        // ---- per-query weights for this lane's dims ----
-        // (dd, ee: sum of delta^2 and eps^2 over the cluster's dims, for the f32 slack)
-        double mx = 0.0, Qp = 0.0, ep = 0.0, dd = 0.0, ee = 0.0;
+        // ---- per-query weights for this lane's dims (active waves only) ----
+        v4i bhi[KS], blo[KS];
+        double e_q = 0.0, c1 = 0.0, cW = 0.0, AQ = 0.0;
+        bool pass_all = true;
+        float c1f = 0.0f, c2f = 0.0f, H32 = 0.0f;
+        if (active) {
+            q = a.pair_qid[start + wid * kWaveQ + (hasq ? j : 0)];
+            const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
+            const double* xr = a.xrot64 + (size_t)q * D_pad;
+            const double* qe = a.qerr + (size_t)q * D_pad;
+            // (dd, ee: sum of delta^2 and eps^2 over the cluster's dims, for the f32 slack)
+            double mx = 0.0, Qp = 0.0, ep = 0.0, dd = 0.0, ee = 0.0;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
+            for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll 4
-            for (int t = 0; t < 16; ++t) {
-                const int d = ks * 64 + g * 16 + t;
-                if (d < D_pad) {
-                    const double dl = (double)a.delta[off + d];
-                    const double qp = xr[d] - (double)a.vmin[off + d];
-                    const double w = dl * qp;
-                    mx = fmax(mx, fabs(w));
-                    Qp = fma(qp, qp, Qp);
-                    ep = fma(qe[d], qe[d], ep);
-                    if constexpr (!UB_PASS) {
-                        const double e = (double)a.eps[off + d];
-                        dd = fma(dl, dl, dd);
-                        ee = fma(e, e, ee);
+                for (int t = 0; t < 16; ++t) {
+                    const int d = ks * 64 + g * 16 + t;
+                    if (d < D_pad) {
+                        const double dl = (double)a.delta[off + d];
+                        const double qp = xr[d] - (double)a.vmin[off + d];
+                        const double w = dl * qp;
+                        mx = fmax(mx, fabs(w));
+                        Qp = fma(qp, qp, Qp);
+                        ep = fma(qe[d], qe[d], ep);
+                        if constexpr (!UB_PASS) {
+                            const double e = (double)a.eps[off + d];
+                            dd = fma(dl, dl, dd);
+                            ee = fma(e, e, ee);
+                        }
                     }
                 }
             }
-        }
 #pragma unroll
-        for (int o = 16; o < 64; o <<= 1) {
-            mx = fmax(mx, shfl_f64(mx, lane ^ o));
-            Qp += shfl_f64(Qp, lane ^ o);
-            ep += shfl_f64(ep, lane ^ o);
-            if constexpr (!UB_PASS) {
-                dd += shfl_f64(dd, lane ^ o);
-                ee += shfl_f64(ee, lane ^ o);
-            }
-        }
-        double s = 1.0;
-        if (mx > 0x1p-100) {
-            s = ldexp(1.0, ilogb(mx) - 14);
-            if (mx / s > 32639.0) s *= 2.0;
-        }
-        v4i bhi[KS], blo[KS];
-        double errs = 0.0;
-        int wsum = 0, wabs = 0;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-            uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int d = ks * 64 + g * 16 + t;
-                int wi = 0;
-                if (d < D_pad) {
-                    const double qp = xr[d] - (double)a.vmin[off + d];
-                    const double w = (double)a.delta[off + d] * qp;
-                    wi = (int)rint(w / s);
-                    errs += fabs(w - s * (double)wi) + 0x1p-52 * fabs(w);
+            for (int o = 16; o < 64; o <<= 1) {
+                mx = fmax(mx, shfl_f64(mx, lane ^ o));
+                Qp += shfl_f64(Qp, lane ^ o);
+                ep += shfl_f64(ep, lane ^ o);
+                if constexpr (!UB_PASS) {
+                    dd += shfl_f64(dd, lane ^ o);
+                    ee += shfl_f64(ee, lane ^ o);
                 }
-                const int hi = (wi + 128) >> 8;
-                const int lo = wi - (hi << 8);
-                wsum += wi;
-                wabs += abs(wi);
-                hw[t >> 2] |= ((uint32_t)hi & 0xffu) << (8 * (t & 3));
-                lw[t >> 2] |= ((uint32_t)lo & 0xffu) << (8 * (t & 3));
             }
-            bhi[ks] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
-            blo[ks] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
-        }
+            double s = 1.0;
+            if (mx > 0x1p-100) {
+                s = ldexp(1.0, ilogb(mx) - 14);
+                if (mx / s > 32639.0) s *= 2.0;
+            }
+            double errs = 0.0;
+            int wsum = 0, wabs = 0;
 #pragma unroll
-        for (int o = 16; o < 64; o <<= 1) {
-            errs += shfl_f64(errs, lane ^ o);
-            wsum += __shfl_xor(wsum, o, kWave);
-            wabs += __shfl_xor(wabs, o, kWave);
-        }
-        const double err_q = 255.0 * errs * (1.0 + 0x1p-40);
-        const double e_q = sqrt(ep) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
-        const double cW = 128.0 * (double)wsum;
-        const double c1 = 2.0 * s;
-
-        // thresholds
-        double AQ = 0.0;
-        bool pass_all = true;
-        float c1f = 0.0f, c2f = 0.0f, H32 = 0.0f;
-        if constexpr (UB_PASS) {
-            AQ = (Qp + 2.0 * err_q) * (1.0 + 1e-13);
-        } else {
-            const double tau = a.tau[q];
-            const double tq = sqrt(tau * a.rot_sq_max) * (1.0 + 1e-12) + e_q;
-            if (tq < 1e30) {
-                // Survive iff A - r^2 - 2 tq r <= 2 s dot + 2 err - Q + tq^2 (the norm-form
-                // lower bound against sqrt(tau) scaled to the rotated space).  Evaluated as
-                //   L = fma(c2, r, fma(-r, r, A_lo)) <= R = fma(c1, float(acc), H32)
-                // with acc = dot - 128 sum(w_int) (exact int32), c1 = 2s (a power of two),
-                // c2 <= -2 tq and H32 >= 2 s 128 sum(w_int) + 2 err - Q + tq^2 + slack.  Each
-                // of the 4 f32 roundings is at most 2^-24 of a term bounded by
-                //   X = A_max + r_max^2 + 2 tq r_max + c1 acc_max + |H|,
-                // with A_max = 255^2 sum delta^2 (codes <= 255), r_max = 2 sqrt(sum eps^2)
-                // (r_x <= |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms) and
-                // |acc| <= acc_max = 128 sum |w_int|; slack = 2^-22 X covers them all.
-                pass_all = false;
-                const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
-                const double H = c1 * cW + G;
-                const double a_max = 65025.0 * dd * (1.0 + 1e-12);
-                const double r_max = 2.0 * sqrt(ee) * (1.0 + 1e-12);
-                const double X = a_max + r_max * r_max + 2.0 * tq * r_max +
-                                 c1 * 128.0 * (double)wabs + fabs(H);
-                const double slack = 0x1p-22 * X * (1.0 + 1e-6) + 1e-30;
-                H32 = __double2float_ru(H + slack);
-                c1f = (float)c1;
-                c2f = -__double2float_ru(2.0 * tq);
+            for (int ks = 0; ks < KS; ++ks) {
+                uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const int d = ks * 64 + g * 16 + t;
+                    int wi = 0;
+                    if (d < D_pad) {
+                        const double qp = xr[d] - (double)a.vmin[off + d];
+                        const double w = (double)a.delta[off + d] * qp;
+                        wi = (int)rint(w / s);
+                        errs += fabs(w - s * (double)wi) + 0x1p-52 * fabs(w);
+                    }
+                    const int hi = (wi + 128) >> 8;
+                    const int lo = wi - (hi << 8);
+                    wsum += wi;
+                    wabs += abs(wi);
+                    hw[t >> 2] |= ((uint32_t)hi & 0xffu) << (8 * (t & 3));
+                    lw[t >> 2] |= ((uint32_t)lo & 0xffu) << (8 * (t & 3));
+                }
+                bhi[ks] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+                blo[ks] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+            }
+#pragma unroll
+            for (int o = 16; o < 64; o <<= 1) {
+                errs += shfl_f64(errs, lane ^ o);
+                wsum += __shfl_xor(wsum, o, kWave);
+                wabs += __shfl_xor(wabs, o, kWave);
+            }
+            const double err_q = 255.0 * errs * (1.0 + 0x1p-40);
+            e_q = sqrt(ep) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
+            cW = 128.0 * (double)wsum;
+            c1 = 2.0 * s;
+            if constexpr (UB_PASS) {
+                AQ = (Qp + 2.0 * err_q) * (1.0 + 1e-13);
+            } else {
+                const double tau = a.tau[q];
+                const double tq = sqrt(tau * a.rot_sq_max) * (1.0 + 1e-12) + e_q;
+                if (tq < 1e30) {
+                    // Survive iff A - r^2 - 2 tq r <= 2 s dot + 2 err - Q + tq^2 (the norm-form
+                    // lower bound against sqrt(tau) scaled to the rotated space).  Evaluated as
+                    //   L = fma(c2, r, fma(-r, r, A_lo)) <= R = fma(c1, float(acc), H32)
+                    // with acc = dot - 128 sum(w_int) (exact int32), c1 = 2s (a power of two),
+                    // c2 <= -2 tq and H32 >= 2 s 128 sum(w_int) + 2 err - Q + tq^2 + slack.
+                    // Each of the 4 f32 roundings is at most 2^-24 of a term bounded by
+                    //   X = A_max + r_max^2 + 2 tq r_max + c1 acc_max + |H|,
+                    // with A_max = 255^2 sum delta^2 (codes <= 255), r_max = 2 sqrt(sum eps^2)
+                    // (r_x <= |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms)
+                    // and |acc| <= acc_max = 128 sum |w_int|; slack = 2^-22 X covers them all.
+                    pass_all = false;
+                    const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
+                    const double H = c1 * cW + G;
+                    const double a_max = 65025.0 * dd * (1.0 + 1e-12);
+                    const double r_max = 2.0 * sqrt(ee) * (1.0 + 1e-12);
+                    const double X = a_max + r_max * r_max + 2.0 * tq * r_max +
+                                     c1 * 128.0 * (double)wabs + fabs(H);
+                    const double slack = 0x1p-22 * X * (1.0 + 1e-6) + 1e-30;
+                    H32 = __double2float_ru(H + slack);
+                    c1f = (float)c1;
+                    c2f = -__double2float_ru(2.0 * tq);
+                }
             }
         }
 
@@ -333,37 +353,27 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
             for (int i = 0; i < kUbList; ++i) ubl[i] = INFINITY;
         }
 
-        // A operand of the 16-vector tile starting at cluster vector li0 (T-tile ct, offset cw)
-        // and the per-vector scalars of this lane's 4 result rows.
-        auto load = [&](int ct, int cw, int li0, v4i (&A)[KS], float2 (&R)[4]) {
-            const uint32_t* cp = a.sq8 + ((size_t)(t0 + ct) * D4) * T + cw + j;
-            const bool va = li0 + j < ve;
+        // ---- one 16-vector tile of the block in LDS buffer buf ----
+        auto tile = [&](int buf, int t, int li0) {
+            const uint32_t* cw32 = reinterpret_cast<const uint32_t*>(s_codes[buf]);
+            v4i A[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4) {
-                    const int d4 = ks * 16 + g * 4 + t4;
-                    uint32_t wv = 0x80808080u;
-                    if (va && d4 < D4) wv = cp[(size_t)d4 * T];
-                    A[ks][t4] = (int)(wv ^ 0x80808080u);
-                }
+                for (int t4 = 0; t4 < 4; ++t4)
+                    A[ks][t4] = (int)(cw32[(ks * 16 + g * 4 + t4) * kBlkV + (((t ^ g) & 3) << 4) + j] ^
+                                      0x80808080u);
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int li = li0 + 4 * g + r;
-                float2 v = make_float2(0.0f, 0.0f);
-                if (hasq && li < ve) v = a.vec_Ar[v0 + li];
-                R[r] = v;
-            }
-        };
-
-        auto compute = [&](const v4i (&A)[KS], const float2 (&R)[4], int li0) {
             v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
                 acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
             }
+            const float4 ar01 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g]);
+            const float4 ar23 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g + 2]);
+            const float Ar[4][2] = {{ar01.x, ar01.y}, {ar01.z, ar01.w}, {ar23.x, ar23.y},
+                                    {ar23.z, ar23.w}};
             // epilogue: rows 4g + r (vectors), column j (query)
             uint32_t sbits = 0;
 #pragma unroll
@@ -374,7 +384,7 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                 if constexpr (UB_PASS) {
                     if (ok) {
                         const double dot = (double)acc + cW;
-                        const double Alo = (double)R[r].x, rr = (double)R[r].y;
+                        const double Alo = (double)Ar[r][0], rr = (double)Ar[r][1];
                         const double E = fmax(fma(-c1, dot, Alo * (1.0 + 0x1p-22) + AQ), 0.0);
                         const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
                         const float u = (s32 + (float)rr + (float)e_q) * (1.0f + 0x1p-20f);
@@ -386,8 +396,8 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                         }
                     }
                 } else {
-                    const float rr = R[r].y;
-                    const float L = fmaf(c2f, rr, fmaf(-rr, rr, R[r].x));
+                    const float rr = Ar[r][1];
+                    const float L = fmaf(c2f, rr, fmaf(-rr, rr, Ar[r][0]));
                     const float Rv = fmaf(c1f, (float)acc, H32);
                     const bool sv = ok && (pass_all || L <= Rv);
                     sbits |= (uint32_t)sv << r;
@@ -411,50 +421,76 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
             }
         };
 
-        // ---- tiles of 16 vectors, two register sets in flight ----
-        const int tb = vb >> 4, te = (ve + 15) >> 4;
-        if (tb < te) {
-            v4i A0[KS], A1[KS];
-            float2 R0[4], R1[4];
-            int ct = (tb << 4) / T, cw = (tb << 4) - ct * T;
-            load(ct, cw, tb << 4, A0, R0);
-            for (int tt = tb; tt < te; tt += 2) {
-                int ct1 = ct, cw1 = cw + 16;
-                if (cw1 == T) { cw1 = 0; ++ct1; }
-                if (tt + 1 < te) load(ct1, cw1, (tt + 1) << 4, A1, R1);
-                compute(A0, R0, tt << 4);
-                if (tt + 1 >= te) break;
-                int ct2 = ct1, cw2 = cw1 + 16;
-                if (cw2 == T) { cw2 = 0; ++ct2; }
-                if (tt + 2 < te) load(ct2, cw2, (tt + 2) << 4, A0, R0);
-                compute(A1, R1, (tt + 1) << 4);
-                ct = ct2;
-                cw = cw2;
+        // ---- stream the slice through LDS in 64-vector blocks ----
+        // Thread tid moves 16-byte pieces (jj * 256 + tid) of the block: row (piece >> 4) of
+        // D_pad / 4, vectors 4 * (piece & 15) .. + 3.  A block never crosses a T-tile (T and
+        // the block starts are multiples of 64).
+        uint4 stg[KS];
+        float2 stg_ar = make_float2(0.0f, 0.0f);
+        auto gload = [&](int blk0) {
+            const int ct = blk0 / T, cw = blk0 - ct * T;
+            const uint32_t* base = a.sq8 + ((size_t)(t0 + ct) * D4) * T + cw;
+#pragma unroll
+            for (int jj = 0; jj < KS; ++jj) {
+                const int piece = jj * kBlock + tid, row = piece >> 4;
+                if (row < D4)
+                    stg[jj] = *reinterpret_cast<const uint4*>(base + (size_t)row * T + (piece & 15) * 4);
+            }
+            if (tid < kBlkV) {
+                const int li = blk0 + tid;
+                stg_ar = li < ve ? a.vec_Ar[v0 + li] : make_float2(0.0f, 0.0f);
+            }
+        };
+        auto lstore = [&](int buf) {
+            uint32_t* cw32 = reinterpret_cast<uint32_t*>(s_codes[buf]);
+#pragma unroll
+            for (int jj = 0; jj < KS; ++jj) {
+                const int piece = jj * kBlock + tid, row = piece >> 4;
+                if (row < D4)
+                    *reinterpret_cast<uint4*>(cw32 + blk_word(row, (piece & 15) * 4)) = stg[jj];
+            }
+            if (tid < kBlkV) s_ar[buf][tid] = stg_ar;
+        };
+        const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
+        if (nblk > 0) gload(vb);
+        for (int b = 0; b < nblk; ++b) {
+            const int buf = b & 1;
+            lstore(buf);
+            __syncthreads();
+            if (b + 1 < nblk) gload(vb + (b + 1) * kBlkV);
+            if (active) {
+                const int blk0 = vb + b * kBlkV;
+#pragma unroll
+                for (int t = 0; t < kBlkV / 16; ++t) {
+                    if (blk0 + t * 16 >= ve) break;
+                    tile(buf, t, blk0 + t * 16);
+                }
             }
         }
 
         if constexpr (UB_PASS) {
-            // K-th smallest upper bound of each query: merge the 4 lanes' lists (64 values) by a
-            // register bitonic sort, then atomicMin into tau[q] (float64 bit pattern).
-            float* s_ub = s_ubl[UB_PASS ? wid : 0];
-            wave_sync();
+            if (active) {
+                // K-th smallest upper bound of each query: merge the 4 lanes' lists (64 values)
+                // by a register bitonic sort, then atomicMin into tau[q] (float64 bit pattern).
+                float* s_ub = s_ubl[wid];
 #pragma unroll
-            for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
-            wave_sync();
-            for (int jj = 0; jj < nq; ++jj) {
-                uint64_t k = key_of((double)s_ub[jj * 64 + lane]);
-                int32_t id = lane;
-                wave_sort64(k, id);
-                const uint64_t kk = readlane_u64(k, a.K - 1);
-                const int qq = __shfl(q, jj, kWave);
-                if (lane == 0 && dist_of(kk) < (double)INFINITY) {
-                    const double u = dist_of(kk);
-                    const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                    atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
-                              (unsigned long long)key_of(tub));
+                for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
+                wave_sync();
+                for (int jj = 0; jj < nq; ++jj) {
+                    uint64_t k = key_of((double)s_ub[jj * 64 + lane]);
+                    int32_t id = lane;
+                    wave_sort64(k, id);
+                    const uint64_t kk = readlane_u64(k, a.K - 1);
+                    const int qq = __shfl(q, jj, kWave);
+                    if (lane == 0 && dist_of(kk) < (double)INFINITY) {
+                        const double u = dist_of(kk);
+                        const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
+                        atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
+                                  (unsigned long long)key_of(tub));
+                    }
                 }
+                wave_sync();
             }
-            wave_sync();
         }
     }
 

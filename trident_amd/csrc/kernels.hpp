@@ -137,9 +137,9 @@ __global__ void pair_scan_kernel(ScanArgs a);
 template <int KP>
 __global__ void merge_kernel(MergeArgs a);
 
-// Batched-route work units: 16 queries of one cluster x one slice of <= kSplitVec-ish vectors
-// (at most kMaxSplit slices per cluster, so a pass has <= kMaxSplit * (pairs / 16 + 2 nlist)).
-constexpr int kUnitQ = 16;
+// Batched-route work units: <= 64 queries of one cluster x one slice of ~kSplitVec vectors
+// (at most kMaxSplit slices per cluster, so a pass has <= kMaxSplit * (pairs / 64 + 2 nlist)).
+constexpr int kUnitQ = 64;
 constexpr int kSplitVec = 1024;
 constexpr int kMaxSplit = 8;
 constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
