@@ -193,11 +193,158 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
         atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
 }
 
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) v += shfl_f64(v, lane_id() ^ o);
+    return v;
+}
+
+__device__ __forceinline__ double sum16_f64(double v) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v += shfl_f64(v, lane_id() ^ o);
+    return v;
+}
+
+// Waves [0, nlist): per-cluster bounds of the f32 slack, A_max = 255^2 sum delta^2 (>= A_x,
+// codes <= 255) and r_max = 2 sqrt(sum eps^2) (>= r_x = |a| + |b| <= 2 |a + b| for the
+// non-negative per-dim error terms bounded by eps).  Waves [nlist, nlist + B): per-query
+// sum of qerr^2 (the rotation error of q_rot, squared).
+__global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist, int B,
+                                                         double* cbound, double* qep) {
+    const int lane = threadIdx.x & 63;
+    const int wv = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
+    const int D_pad = a.D_pad;
+    if (wv < nlist) {
+        const size_t off = a.per_cluster ? (size_t)wv * D_pad : 0;
+        double dd = 0.0, ee = 0.0;
+        for (int d = lane; d < D_pad; d += kWave) {
+            const double dl = (double)a.delta[off + d], e = (double)a.eps[off + d];
+            dd = fma(dl, dl, dd);
+            ee = fma(e, e, ee);
+        }
+        dd = wave_sum_f64(dd);
+        ee = wave_sum_f64(ee);
+        if (lane == 0) {
+            cbound[2 * wv] = 65025.0 * dd * (1.0 + 1e-12);
+            cbound[2 * wv + 1] = 2.0 * sqrt(ee) * (1.0 + 1e-12);
+        }
+    } else if (wv < nlist + B) {
+        const double* qe = a.qerr + (size_t)(wv - nlist) * D_pad;
+        double ep = 0.0;
+        for (int d = lane; d < D_pad; d += kWave) ep = fma(qe[d], qe[d], ep);
+        ep = wave_sum_f64(ep);
+        if (lane == 0) qep[wv - nlist] = ep;
+    }
+}
+
+// 16 lanes per grouped pair p (4 pairs per wave): the query's int8 weight planes against its
+// cluster's SQ8 grid and the pair's threshold-independent scalars.  Lane l owns dims
+// 64 k + 4 l + [0, 4) (coalesced 32-byte row pieces, one packed 32-bit store per plane).
+//   w_d = delta_d * (q_rot,d - vmin_d);  s = 2^(ilogb(max |w|) - 14), doubled if max|w|/s >
+//   32639, so |w_int| <= 32639;  w_int = rint(w / s) = 256 hi + lo  (hi, lo in [-128, 127]).
+// Plane bytes past D_pad (up to DP) are zero, so the scan may read whole 64-dim steps.
+template <int KS>
+__global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
+    const int lane = threadIdx.x & 63, l = lane & 15;
+    const int p = (blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6)) * 4 + (lane >> 4);
+    const bool valid = p < a.M;
+    const int pp = valid ? p : a.M - 1;  // out-of-range groups redo the last pair, store nothing
+    const int c = a.pair_cid[pp], q = a.pair_qid[pp];
+    const int D_pad = a.D_pad, DP = a.DP;
+    const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
+    const double* xr = a.xrot64 + (size_t)q * D_pad;
+    double w[KS][4];
+    double mx = 0.0, Qp = 0.0;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        const int d0 = 64 * k + 4 * l;  // D_pad is a multiple of 4: all 4 dims or none
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[k][e] = 0.0;
+        if (d0 < D_pad) {
+            const double2 x01 = *reinterpret_cast<const double2*>(xr + d0);
+            const double2 x23 = *reinterpret_cast<const double2*>(xr + d0 + 2);
+            const double xv[4] = {x01.x, x01.y, x23.x, x23.y};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double qp = xv[e] - (double)a.vmin[off + d0 + e];
+                w[k][e] = (double)a.delta[off + d0 + e] * qp;
+                mx = fmax(mx, fabs(w[k][e]));
+                Qp = fma(qp, qp, Qp);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
+    Qp = sum16_f64(Qp);
+    double s = 1.0;
+    if (mx > 0x1p-100) {
+        s = ldexp(1.0, ilogb(mx) - 14);
+        if (mx / s > 32639.0) s *= 2.0;
+    }
+    double errs = 0.0;
+    int wsum = 0, wabs = 0;
+    int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        uint32_t hw = 0u, lw = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int wi = (int)rint(w[k][e] / s);  // 0 for dims >= D_pad
+            errs += fabs(w[k][e] - s * (double)wi) + 0x1p-52 * fabs(w[k][e]);
+            wsum += wi;
+            wabs += abs(wi);
+            const int hi = (wi + 128) >> 8;
+            hw |= ((uint32_t)hi & 0xffu) << (8 * e);
+            lw |= ((uint32_t)(wi - (hi << 8)) & 0xffu) << (8 * e);
+        }
+        if (valid) {
+            *reinterpret_cast<uint32_t*>(hi_p + 64 * k + 4 * l) = hw;
+            *reinterpret_cast<uint32_t*>(hi_p + DP + 64 * k + 4 * l) = lw;
+        }
+    }
+    errs = sum16_f64(errs);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+        wsum += __shfl_xor(wsum, o, kWave);
+        wabs += __shfl_xor(wabs, o, kWave);
+    }
+    if (valid && l == 0) {
+        PairRec r;
+        r.Qp = Qp;
+        r.err_q = 255.0 * errs * (1.0 + 0x1p-40);
+        r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
+        r.cW = 128.0 * (double)wsum;
+        r.c1 = 2.0 * s;
+        r.a_max = a.cbound[2 * c];
+        r.r_max = a.cbound[2 * c + 1];
+        r.acc_max = 128.0 * (double)wabs;
+        a.prec[pp] = r;
+    }
+}
+
+template __global__ void pair_prep_kernel<1>(BatchArgs);
+template __global__ void pair_prep_kernel<2>(BatchArgs);
+template __global__ void pair_prep_kernel<3>(BatchArgs);
+template __global__ void pair_prep_kernel<4>(BatchArgs);
+
 // LDS word of (row d4, vector v) in a 64-vector code block: a row's four 16-vector groups are
 // rotated by (d4 >> 2) & 3, so the four lane groups g of one A-operand read (rows
 // ks*16 + g*4 + t4, same 16 vectors) land in four different 16-bank groups.
 __device__ __forceinline__ int blk_word(int d4, int v) {
     return d4 * kBlkV + ((((v >> 4) ^ (d4 >> 2)) & 3) << 4) + (v & 15);
+}
+
+// 16-byte piece jj * 256 + tid of a 64-vector code block whose row 0 starts at base (rows T
+// words apart): row piece >> 4, vectors 4 (piece & 15) .. + 3.  Rows >= D4 are not read.
+__device__ __forceinline__ uint4 piece_load(const uint32_t* base, int jj, int tid, int D4, int T) {
+    const int piece = jj * kBlock + tid, row = piece >> 4;
+    if (row >= D4) return make_uint4(0u, 0u, 0u, 0u);
+    return *reinterpret_cast<const uint4*>(base + (size_t)row * T + (piece & 15) * 4);
+}
+
+__device__ __forceinline__ void piece_store(uint32_t* blk, uint4 v, int jj, int tid, int D4) {
+    const int piece = jj * kBlock + tid, row = piece >> 4;
+    if (row < D4) *reinterpret_cast<uint4*>(blk + blk_word(row, (piece & 15) * 4)) = v;
 }
 
 template <bool UB_PASS, int KS>
@@ -240,82 +387,21 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         bool pass_all = true;
         float c1f = 0.0f, c2f = 0.0f, H32 = 0.0f;
         if (active) {
-            q = a.pair_qid[start + wid * kWaveQ + (hasq ? j : 0)];
-            const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
-            const double* xr = a.xrot64 + (size_t)q * D_pad;
-            const double* qe = a.qerr + (size_t)q * D_pad;
-            // (dd, ee: sum of delta^2 and eps^2 over the cluster's dims, for the f32 slack)
-            double mx = 0.0, Qp = 0.0, ep = 0.0, dd = 0.0, ee = 0.0;
+            // Prepared by pair_prep_kernel: lane (j, g) takes bytes [ks*64 + g*16, +16) of
+            // query j's planes and the pair's scalars.
+            const int pj = start + wid * kWaveQ + (hasq ? j : 0);
+            q = a.pair_qid[pj];
+            const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll 4
-                for (int t = 0; t < 16; ++t) {
-                    const int d = ks * 64 + g * 16 + t;
-                    if (d < D_pad) {
-                        const double dl = (double)a.delta[off + d];
-                        const double qp = xr[d] - (double)a.vmin[off + d];
-                        const double w = dl * qp;
-                        mx = fmax(mx, fabs(w));
-                        Qp = fma(qp, qp, Qp);
-                        ep = fma(qe[d], qe[d], ep);
-                        if constexpr (!UB_PASS) {
-                            const double e = (double)a.eps[off + d];
-                            dd = fma(dl, dl, dd);
-                            ee = fma(e, e, ee);
-                        }
-                    }
-                }
+                bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
+                blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
             }
-#pragma unroll
-            for (int o = 16; o < 64; o <<= 1) {
-                mx = fmax(mx, shfl_f64(mx, lane ^ o));
-                Qp += shfl_f64(Qp, lane ^ o);
-                ep += shfl_f64(ep, lane ^ o);
-                if constexpr (!UB_PASS) {
-                    dd += shfl_f64(dd, lane ^ o);
-                    ee += shfl_f64(ee, lane ^ o);
-                }
-            }
-            double s = 1.0;
-            if (mx > 0x1p-100) {
-                s = ldexp(1.0, ilogb(mx) - 14);
-                if (mx / s > 32639.0) s *= 2.0;
-            }
-            double errs = 0.0;
-            int wsum = 0, wabs = 0;
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-                for (int t = 0; t < 16; ++t) {
-                    const int d = ks * 64 + g * 16 + t;
-                    int wi = 0;
-                    if (d < D_pad) {
-                        const double qp = xr[d] - (double)a.vmin[off + d];
-                        const double w = (double)a.delta[off + d] * qp;
-                        wi = (int)rint(w / s);
-                        errs += fabs(w - s * (double)wi) + 0x1p-52 * fabs(w);
-                    }
-                    const int hi = (wi + 128) >> 8;
-                    const int lo = wi - (hi << 8);
-                    wsum += wi;
-                    wabs += abs(wi);
-                    hw[t >> 2] |= ((uint32_t)hi & 0xffu) << (8 * (t & 3));
-                    lw[t >> 2] |= ((uint32_t)lo & 0xffu) << (8 * (t & 3));
-                }
-                bhi[ks] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
-                blo[ks] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
-            }
-#pragma unroll
-            for (int o = 16; o < 64; o <<= 1) {
-                errs += shfl_f64(errs, lane ^ o);
-                wsum += __shfl_xor(wsum, o, kWave);
-                wabs += __shfl_xor(wabs, o, kWave);
-            }
-            const double err_q = 255.0 * errs * (1.0 + 0x1p-40);
-            e_q = sqrt(ep) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
-            cW = 128.0 * (double)wsum;
-            c1 = 2.0 * s;
+            const PairRec pr = a.prec[pj];
+            const double Qp = pr.Qp, err_q = pr.err_q;
+            e_q = pr.e_q;
+            cW = pr.cW;
+            c1 = pr.c1;
             if constexpr (UB_PASS) {
                 AQ = (Qp + 2.0 * err_q) * (1.0 + 1e-13);
             } else {
@@ -335,10 +421,8 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                     pass_all = false;
                     const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
                     const double H = c1 * cW + G;
-                    const double a_max = 65025.0 * dd * (1.0 + 1e-12);
-                    const double r_max = 2.0 * sqrt(ee) * (1.0 + 1e-12);
-                    const double X = a_max + r_max * r_max + 2.0 * tq * r_max +
-                                     c1 * 128.0 * (double)wabs + fabs(H);
+                    const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max +
+                                     c1 * pr.acc_max + fabs(H);
                     const double slack = 0x1p-22 * X * (1.0 + 1e-6) + 1e-30;
                     H32 = __double2float_ru(H + slack);
                     c1f = (float)c1;
@@ -425,31 +509,30 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         // Thread tid moves 16-byte pieces (jj * 256 + tid) of the block: row (piece >> 4) of
         // D_pad / 4, vectors 4 * (piece & 15) .. + 3.  A block never crosses a T-tile (T and
         // the block starts are multiples of 64).
-        uint4 stg[KS];
-        float2 stg_ar = make_float2(0.0f, 0.0f);
+        // (The staging values are separate scalars filled by value: an array captured by
+        // reference lands in scratch memory and serialises every load.)
+        uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
+        float2 st_ar = make_float2(0.0f, 0.0f);
+        const uint32_t* sq8_c = a.sq8 + (size_t)t0 * D4 * T;  // cluster's first tile
         auto gload = [&](int blk0) {
             const int ct = blk0 / T, cw = blk0 - ct * T;
-            const uint32_t* base = a.sq8 + ((size_t)(t0 + ct) * D4) * T + cw;
-#pragma unroll
-            for (int jj = 0; jj < KS; ++jj) {
-                const int piece = jj * kBlock + tid, row = piece >> 4;
-                if (row < D4)
-                    stg[jj] = *reinterpret_cast<const uint4*>(base + (size_t)row * T + (piece & 15) * 4);
-            }
+            const uint32_t* base = sq8_c + (size_t)ct * D4 * T + cw;
+            st0 = piece_load(base, 0, tid, D4, T);
+            if constexpr (KS > 1) st1 = piece_load(base, 1, tid, D4, T);
+            if constexpr (KS > 2) st2 = piece_load(base, 2, tid, D4, T);
+            if constexpr (KS > 3) st3 = piece_load(base, 3, tid, D4, T);
             if (tid < kBlkV) {
                 const int li = blk0 + tid;
-                stg_ar = li < ve ? a.vec_Ar[v0 + li] : make_float2(0.0f, 0.0f);
+                st_ar = li < ve ? a.vec_Ar[v0 + li] : make_float2(0.0f, 0.0f);
             }
         };
         auto lstore = [&](int buf) {
             uint32_t* cw32 = reinterpret_cast<uint32_t*>(s_codes[buf]);
-#pragma unroll
-            for (int jj = 0; jj < KS; ++jj) {
-                const int piece = jj * kBlock + tid, row = piece >> 4;
-                if (row < D4)
-                    *reinterpret_cast<uint4*>(cw32 + blk_word(row, (piece & 15) * 4)) = stg[jj];
-            }
-            if (tid < kBlkV) s_ar[buf][tid] = stg_ar;
+            piece_store(cw32, st0, 0, tid, D4);
+            if constexpr (KS > 1) piece_store(cw32, st1, 1, tid, D4);
+            if constexpr (KS > 2) piece_store(cw32, st2, 2, tid, D4);
+            if constexpr (KS > 3) piece_store(cw32, st3, 3, tid, D4);
+            if (tid < kBlkV) s_ar[buf][tid] = st_ar;
         };
         const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
         if (nblk > 0) gload(vb);

@@ -86,8 +86,15 @@ struct Workspace {
     int32_t* unit_off;               // [2 * nlist + 1]
     int32_t* unit_ctr;               // [2, 8 * kCtrStride] per-launch, per-XCD counters
     int64_t max_units;
+    int8_t* pw;                      // [B * nprobe, 2, DP] batched-route weight planes
+    PairRec* prec;                   // [B * nprobe]
+    double* cbound;                  // [nlist, 2]
+    double* qep;                     // [B]
     size_t bytes;
 };
+
+// Bytes of one batched-route weight plane: whole 64-dim steps.
+inline int64_t plane_bytes(int D_pad) { return 64 * (int64_t)((D_pad + 63) / 64); }
 
 // Candidate-list slots per query.  The batched route stores every lower-bound survivor there
 // (before its exact test), so lists are at least 16 * nprobe deep; a longer list makes the
@@ -122,6 +129,10 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.units = c.take<int4>(w.max_units);
     w.unit_off = c.take<int32_t>(2 * (int64_t)ix->nlist + 1);
     w.unit_ctr = c.take<int32_t>(2 * 8 * kCtrStride);
+    w.pw = c.take<int8_t>(B * nprobe * 2 * plane_bytes(ix->D_pad));
+    w.prec = c.take<PairRec>(B * nprobe);
+    w.cbound = c.take<double>(2 * (int64_t)ix->nlist);
+    w.qep = c.take<double>(B);
     w.bytes = c.off;
     return w;
 }
@@ -271,6 +282,20 @@ template <bool UB, int KS>
 int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
     batch_scan_kernel<UB, KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
     return check_launch("batch_scan_kernel");
+}
+
+int launch_pair_prep(const BatchArgs& b, hipStream_t st) {
+    if (b.M <= 0) return TRIDENT_OK;
+    const int per_block = 4 * kWavesPerBlock;  // 16 lanes per pair
+    const unsigned grid = (unsigned)((b.M + per_block - 1) / per_block);
+    switch (b.DP / 64) {
+        case 1: pair_prep_kernel<1><<<grid, kBlock, 0, st>>>(b); break;
+        case 2: pair_prep_kernel<2><<<grid, kBlock, 0, st>>>(b); break;
+        case 3: pair_prep_kernel<3><<<grid, kBlock, 0, st>>>(b); break;
+        case 4: pair_prep_kernel<4><<<grid, kBlock, 0, st>>>(b); break;
+        default: return fail(TRIDENT_ERR_UNSUPPORTED, "batched route needs D_pad <= 256");
+    }
+    return check_launch("pair_prep_kernel");
 }
 
 template <bool UB>
@@ -533,6 +558,17 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.unit_off = w.unit_off;
         b.max_units = (int)w.max_units;
         b.pair_qid = w.pair_qids;
+        b.pair_cid = w.pair_cids;
+        b.M = (int)(M1 + M2);
+        b.DP = (int)plane_bytes(ix->D_pad);
+        b.pw = w.pw;
+        b.prec = w.prec;
+        b.cbound = w.cbound;
+        b.qep = w.qep;
+        aux_bounds_kernel<<<(unsigned)((ix->nlist + B + kWavesPerBlock - 1) / kWavesPerBlock),
+                            kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep);
+        if ((rc = check_launch("aux_bounds_kernel"))) return rc;
+        if ((rc = launch_pair_prep(b, st))) return rc;
         unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
                                                w.unit_off);
         if ((rc = check_launch("unit_scan_kernel"))) return rc;

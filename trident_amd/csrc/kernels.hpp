@@ -65,6 +65,18 @@ struct MergeArgs {
     int T, D;
 };
 
+// Per-(query, cluster) pair scalars of the batched bound (threshold-independent part).
+struct PairRec {
+    double Qp;       // |q_rot - vmin|^2
+    double err_q;    // 255 * sum |w - s w_int|  (bound on the weight quantisation error)
+    double e_q;      // >= |q_rot(float64) - q_rot(exact)|
+    double cW;       // 128 * sum w_int
+    double c1;       // 2 s
+    double a_max;    // >= A_x for every vector of the cluster
+    double r_max;    // >= r_x for every vector of the cluster
+    double acc_max;  // >= |sum c'_d w_int,d|
+};
+
 // Everything one cluster-batched scan launch reads (csrc/batch.hip).
 struct BatchArgs {
     const uint32_t* sq8;
@@ -87,6 +99,13 @@ struct BatchArgs {
     int max_units;
     int32_t* ctr;               // [8 * kCtrStride] per-XCD work counters, zero at launch
     const int32_t* pair_qid;    // pass-1 pairs then pass-2 pairs
+    const int32_t* pair_cid;
+    int M;                      // pairs (both passes)
+    int DP;                     // 64 * ceil(D_pad / 64): bytes per weight plane
+    int8_t* pw;                 // [M, 2, DP] int8 weight planes (hi, lo), natural dim order
+    PairRec* prec;              // [M]
+    const double* cbound;       // [nlist, 2] (A_max, r_max) per cluster
+    const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
     uint64_t* cand_key;
     int32_t* cand_id;
@@ -162,6 +181,11 @@ template <bool UB_PASS, int KS>
 __global__ void batch_scan_kernel(BatchArgs a);
 
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
+
+template <int KS>
+__global__ void pair_prep_kernel(BatchArgs a);
+
+__global__ void aux_bounds_kernel(BatchArgs a, int nlist, int B, double* cbound, double* qep);
 
 __global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
                                   const int32_t* __restrict__ cids,
