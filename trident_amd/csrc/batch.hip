@@ -64,7 +64,8 @@ __device__ __forceinline__ int units_of_entry(const int32_t* seg_off, const int3
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
     const int32_t* so = seg_off + p * (nlist + 1);
     const int q = so[c + 1] - so[c];
-    return q > 0 ? ((q + kUnitQ - 1) / kUnitQ) * splits_of(vec_off[c + 1] - vec_off[c], p) : 0;
+    const int uq = p ? kUnitQ : kUnitQ0;
+    return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c], p) : 0;
 }
 
 // grid 1: exclusive scan of the unit counts of the 2 * nlist (pass, cluster) segments.
@@ -121,10 +122,11 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
         const int local = u - unit_off[lo];
         const int qb = local / S, sp = local - qb * S;
         const int q = so[c + 1] - so[c];
-        const int cnt = min(kUnitQ, q - qb * kUnitQ);
+        const int uq = p ? kUnitQ : kUnitQ0;
+        const int cnt = min(uq, q - qb * uq);
         const int len = ((n + S - 1) / S + kBlkV - 1) & ~(kBlkV - 1);
         const int vb = sp * len, ve = min(n, vb + len);
-        units[u] = make_int4(c | (cnt << 20), (p ? M1 : 0) + so[c] + qb * kUnitQ, vb, ve);
+        units[u] = make_int4(c | (cnt << 20), (p ? M1 : 0) + so[c] + qb * uq, vb, ve);
     }
 }
 
@@ -327,24 +329,54 @@ template __global__ void pair_prep_kernel<2>(BatchArgs);
 template __global__ void pair_prep_kernel<3>(BatchArgs);
 template __global__ void pair_prep_kernel<4>(BatchArgs);
 
-// LDS word of (row d4, vector v) in a 64-vector code block: a row's four 16-vector groups are
-// rotated by (d4 >> 2) & 3, so the four lane groups g of one A-operand read (rows
-// ks*16 + g*4 + t4, same 16 vectors) land in four different 16-bank groups.
-__device__ __forceinline__ int blk_word(int d4, int v) {
-    return d4 * kBlkV + ((((v >> 4) ^ (d4 >> 2)) & 3) << 4) + (v & 15);
+// m <- the 16 smallest of two ascending 16-lists (m, o), ascending, all in registers:
+// min(m[i], o[15 - i]) is a bitonic sequence holding them; four half-cleaner stages sort it.
+__device__ __forceinline__ void merge16(float (&m)[16], const float (&o)[16]) {
+    float c[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) c[i] = fminf(m[i], o[15 - i]);
+#pragma unroll
+    for (int d = 8; d >= 1; d >>= 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            if ((i & d) == 0) {
+                const float lo = fminf(c[i], c[i + d]), hi = fmaxf(c[i], c[i + d]);
+                c[i] = lo;
+                c[i + d] = hi;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m[i] = c[i];
 }
 
-// 16-byte piece jj * 256 + tid of a 64-vector code block whose row 0 starts at base (rows T
-// words apart): row piece >> 4, vectors 4 (piece & 15) .. + 3.  Rows >= D4 are not read.
-__device__ __forceinline__ uint4 piece_load(const uint32_t* base, int jj, int tid, int D4, int T) {
-    const int piece = jj * kBlock + tid, row = piece >> 4;
-    if (row >= D4) return make_uint4(0u, 0u, 0u, 0u);
-    return *reinterpret_cast<const uint4*>(base + (size_t)row * T + (piece & 15) * 4);
+// Merge the lists of lanes l, l ^ 16, l ^ 32, l ^ 48 (one query's four lane groups).
+__device__ __forceinline__ void merge16_groups(float (&m)[16]) {
+#pragma unroll
+    for (int o = 16; o < kWave; o <<= 1) {
+        float other[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) other[i] = __shfl_xor(m[i], o, kWave);
+        merge16(m, other);
+    }
 }
 
-__device__ __forceinline__ void piece_store(uint32_t* blk, uint4 v, int jj, int tid, int D4) {
-    const int piece = jj * kBlock + tid, row = piece >> 4;
-    if (row < D4) *reinterpret_cast<uint4*>(blk + blk_word(row, (piece & 15) * 4)) = v;
+// A 64-vector code block in LDS: 16-byte cell rg * 64 + v holds vector v's codes of dims
+// 16 rg .. 16 rg + 15 (code rows 4 rg .. 4 rg + 3, one 32-bit row each) as c' = c - 128, so
+// the MFMA A operand of 64 dims is one 16-byte read.  Thread tid moves the cells of vector
+// tid & 63, row groups (tid >> 6) + 4 jj: four 4-byte loads, each coalesced over the wave (64
+// consecutive vectors of one code row).  D4 is a multiple of 8, so a row group is either
+// wholly inside D_pad or wholly past it (then zero).
+__device__ __forceinline__ uint4 cell_load(const uint32_t* base, int jj, int tid, int D4, int T) {
+    const int r0 = 4 * ((tid >> 6) + 4 * jj);
+    if (r0 >= D4) return make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+    const uint32_t* p = base + (size_t)r0 * T + (tid & 63);
+    return make_uint4(p[0], p[T], p[2 * T], p[3 * T]);
+}
+
+__device__ __forceinline__ void cell_store(uint4* blk, uint4 c, int jj, int tid) {
+    blk[((tid >> 6) + 4 * jj) * kBlkV + (tid & 63)] =
+        make_uint4(c.x ^ 0x80808080u, c.y ^ 0x80808080u, c.z ^ 0x80808080u, c.w ^ 0x80808080u);
 }
 
 template <bool UB_PASS, int KS>
@@ -374,8 +406,13 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         if (ui >= re) break;
         const int4 un = a.units[ui];
         const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
-        const int nq = min(max(cnt - wid * kWaveQ, 0), kWaveQ);  // this wave's queries
-        const bool active = nq > 0;
+        // The unit's queries form G groups of <= 16; each group gets R = 4 / G waves, which
+        // split every block's four 16-vector tiles (replica rr takes tiles rr, rr + R, ...).
+        const int G = (cnt + kWaveQ - 1) / kWaveQ;
+        const int R = kWavesPerBlock / G;
+        const int gq = wid / R, rr = wid - gq * R;
+        const bool active = gq < G;
+        const int nq = active ? min(kWaveQ, cnt - gq * kWaveQ) : 0;  // this wave's queries
         const bool hasq = j < nq;
         const int v0 = a.vec_off[cid];
         const int t0 = a.tile_off[cid];
@@ -384,12 +421,11 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         // ---- per-query weights for this lane's dims (active waves only) ----
         v4i bhi[KS], blo[KS];
         double e_q = 0.0, c1 = 0.0, cW = 0.0, AQ = 0.0;
-        bool pass_all = true;
-        float c1f = 0.0f, c2f = 0.0f, H32 = 0.0f;
+        float c1f = 0.0f, c2f = 0.0f, H32 = INFINITY;  // no threshold: every row passes
         if (active) {
             // Prepared by pair_prep_kernel: lane (j, g) takes bytes [ks*64 + g*16, +16) of
             // query j's planes and the pair's scalars.
-            const int pj = start + wid * kWaveQ + (hasq ? j : 0);
+            const int pj = start + gq * kWaveQ + (hasq ? j : 0);
             q = a.pair_qid[pj];
             const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
 #pragma unroll
@@ -418,7 +454,6 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                     // with A_max = 255^2 sum delta^2 (codes <= 255), r_max = 2 sqrt(sum eps^2)
                     // (r_x <= |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms)
                     // and |acc| <= acc_max = 128 sum |w_int|; slack = 2^-22 X covers them all.
-                    pass_all = false;
                     const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
                     const double H = c1 * cW + G;
                     const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max +
@@ -429,6 +464,7 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                     c2f = -__double2float_ru(2.0 * tq);
                 }
             }
+            if (!hasq) H32 = -INFINITY;  // lane has no query: nothing survives
         }
 
         float ubl[kUbList];
@@ -439,14 +475,14 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
 
         // ---- one 16-vector tile of the block in LDS buffer buf ----
         auto tile = [&](int buf, int t, int li0) {
-            const uint32_t* cw32 = reinterpret_cast<const uint32_t*>(s_codes[buf]);
+            // A operand: lane (i = j, g) reads vector 16t + i's 16 code bytes of dims
+            // ks*64 + g*16 + [0, 16) (row group ks*4 + g), already offset to c' = c - 128.
+            const uint4* blk = s_codes[buf];
             v4i A[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-#pragma unroll
-                for (int t4 = 0; t4 < 4; ++t4)
-                    A[ks][t4] = (int)(cw32[(ks * 16 + g * 4 + t4) * kBlkV + (((t ^ g) & 3) << 4) + j] ^
-                                      0x80808080u);
+                const uint4 v = blk[(ks * 4 + g) * kBlkV + t * 16 + j];
+                A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
             v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
 #pragma unroll
@@ -454,6 +490,16 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
                 acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
             }
+            // The matrix core does not interlock VALU reads of its results: keep 16 wait
+            // states (plus the compiler's own padding) between the last MFMA and the first
+            // accumulator read, fenced so the scheduler cannot move either side across.  (The
+            // compiler's padding alone fell short when a branch sat between the two: rows read
+            // the previous tile's sums.)
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7\n\ts_nop 7");
+            __builtin_amdgcn_sched_barrier(0);
+            // per-row scalars: (P = A_lo - r^2, r) in the lower-bound pass, (A_lo, r) in the
+            // upper-bound pass; rows past the slice hold (NaN, +inf), which neither test accepts
             const float4 ar01 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g]);
             const float4 ar23 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g + 2]);
             const float Ar[4][2] = {{ar01.x, ar01.y}, {ar01.z, ar01.w}, {ar23.x, ar23.y},
@@ -462,32 +508,27 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
             uint32_t sbits = 0;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int li = li0 + 4 * g + r;
-                const bool ok = hasq && li < ve;
                 const int acc = (acc_hi[r] << 8) + acc_lo[r];
                 if constexpr (UB_PASS) {
-                    if (ok) {
-                        const double dot = (double)acc + cW;
-                        const double Alo = (double)Ar[r][0], rr = (double)Ar[r][1];
-                        const double E = fmax(fma(-c1, dot, Alo * (1.0 + 0x1p-22) + AQ), 0.0);
-                        const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
-                        const float u = (s32 + (float)rr + (float)e_q) * (1.0f + 0x1p-20f);
-                        if (u < ubl[kUbList - 1]) {
+                    const double dot = (double)acc + cW;
+                    const double Alo = (double)Ar[r][0], rr = (double)Ar[r][1];
+                    const double E = fmax(fma(-c1, dot, Alo * (1.0 + 0x1p-22) + AQ), 0.0);
+                    const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
+                    const float u = (s32 + (float)rr + (float)e_q) * (1.0f + 0x1p-20f);
+                    if (u < ubl[kUbList - 1]) {
 #pragma unroll
-                            for (int i = kUbList - 1; i > 0; --i)
-                                ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
-                            ubl[0] = fminf(ubl[0], u);
-                        }
+                        for (int i = kUbList - 1; i > 0; --i)
+                            ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
+                        ubl[0] = fminf(ubl[0], u);
                     }
                 } else {
-                    const float rr = Ar[r][1];
-                    const float L = fmaf(c2f, rr, fmaf(-rr, rr, Ar[r][0]));
+                    // lanes without a query have H32 = -inf; a query with no threshold has
+                    // c1f = c2f = 0, H32 = +inf
+                    const float L = fmaf(c2f, Ar[r][1], Ar[r][0]);
                     const float Rv = fmaf(c1f, (float)acc, H32);
-                    const bool sv = ok && (pass_all || L <= Rv);
-                    sbits |= (uint32_t)sv << r;
+                    sbits |= (uint32_t)(L <= Rv) << r;
                 }
             }
-            if (a.stats) st_cand += (unsigned long long)nq * (unsigned long long)min(16, ve - li0);
             if constexpr (!UB_PASS) {
                 if (__ballot(sbits != 0) == 0) return;
                 // rare: append survivors (sorted position) to the query's list
@@ -506,9 +547,7 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         };
 
         // ---- stream the slice through LDS in 64-vector blocks ----
-        // Thread tid moves 16-byte pieces (jj * 256 + tid) of the block: row (piece >> 4) of
-        // D_pad / 4, vectors 4 * (piece & 15) .. + 3.  A block never crosses a T-tile (T and
-        // the block starts are multiples of 64).
+        // A block never crosses a T-tile (T and the block starts are multiples of 64).
         // (The staging values are separate scalars filled by value: an array captured by
         // reference lands in scratch memory and serialises every load.)
         uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
@@ -517,21 +556,27 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         auto gload = [&](int blk0) {
             const int ct = blk0 / T, cw = blk0 - ct * T;
             const uint32_t* base = sq8_c + (size_t)ct * D4 * T + cw;
-            st0 = piece_load(base, 0, tid, D4, T);
-            if constexpr (KS > 1) st1 = piece_load(base, 1, tid, D4, T);
-            if constexpr (KS > 2) st2 = piece_load(base, 2, tid, D4, T);
-            if constexpr (KS > 3) st3 = piece_load(base, 3, tid, D4, T);
+            st0 = cell_load(base, 0, tid, D4, T);
+            if constexpr (KS > 1) st1 = cell_load(base, 1, tid, D4, T);
+            if constexpr (KS > 2) st2 = cell_load(base, 2, tid, D4, T);
+            if constexpr (KS > 3) st3 = cell_load(base, 3, tid, D4, T);
             if (tid < kBlkV) {
                 const int li = blk0 + tid;
-                st_ar = li < ve ? a.vec_Ar[v0 + li] : make_float2(0.0f, 0.0f);
+                if (li < ve) {
+                    const float2 ar = a.vec_Ar[v0 + li];
+                    // lower-bound pass keeps P = A_lo - r^2 (its f32 rounding is inside the
+                    // slack), upper-bound pass keeps A_lo
+                    st_ar = UB_PASS ? ar : make_float2(fmaf(-ar.y, ar.y, ar.x), ar.y);
+                } else {
+                    st_ar = make_float2(__int_as_float(0x7fc00000), INFINITY);
+                }
             }
         };
         auto lstore = [&](int buf) {
-            uint32_t* cw32 = reinterpret_cast<uint32_t*>(s_codes[buf]);
-            piece_store(cw32, st0, 0, tid, D4);
-            if constexpr (KS > 1) piece_store(cw32, st1, 1, tid, D4);
-            if constexpr (KS > 2) piece_store(cw32, st2, 2, tid, D4);
-            if constexpr (KS > 3) piece_store(cw32, st3, 3, tid, D4);
+            cell_store(s_codes[buf], st0, 0, tid);
+            if constexpr (KS > 1) cell_store(s_codes[buf], st1, 1, tid);
+            if constexpr (KS > 2) cell_store(s_codes[buf], st2, 2, tid);
+            if constexpr (KS > 3) cell_store(s_codes[buf], st3, 3, tid);
             if (tid < kBlkV) s_ar[buf][tid] = st_ar;
         };
         const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
@@ -543,36 +588,77 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
             if (b + 1 < nblk) gload(vb + (b + 1) * kBlkV);
             if (active) {
                 const int blk0 = vb + b * kBlkV;
-#pragma unroll
-                for (int t = 0; t < kBlkV / 16; ++t) {
+                for (int t = rr; t < kBlkV / 16; t += R) {
                     if (blk0 + t * 16 >= ve) break;
                     tile(buf, t, blk0 + t * 16);
                 }
             }
         }
+        if (a.stats && active && rr == 0)
+            st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
 
         if constexpr (UB_PASS) {
-            if (active) {
-                // K-th smallest upper bound of each query: merge the 4 lanes' lists (64 values)
-                // by a register bitonic sort, then atomicMin into tau[q] (float64 bit pattern).
-                float* s_ub = s_ubl[wid];
+            // K-th smallest upper bound of each query -> atomicMin into tau[q] (float64 bit
+            // pattern).  Every lane holds the 16 smallest bounds of its rows.
+            //  K <= 16: the four lane groups' lists are merged in registers (exact top 16 of
+            //    the wave), replica waves exchange theirs through LDS and the group's first
+            //    wave merges them the same way: the K-th entry is the exact K-th smallest.
+            //  K > 16: all R x 64 kept values go through a register bitonic list; their K-th
+            //    smallest is >= the true K-th smallest bound, so still an upper bound.
+            if (a.K <= kUbList) {
+                if (active) {
+                    merge16_groups(ubl);
+                    if (R > 1 && g == 0) {
 #pragma unroll
-                for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
-                wave_sync();
-                for (int jj = 0; jj < nq; ++jj) {
-                    uint64_t k = key_of((double)s_ub[jj * 64 + lane]);
-                    int32_t id = lane;
-                    wave_sort64(k, id);
-                    const uint64_t kk = readlane_u64(k, a.K - 1);
-                    const int qq = __shfl(q, jj, kWave);
-                    if (lane == 0 && dist_of(kk) < (double)INFINITY) {
-                        const double u = dist_of(kk);
+                        for (int i = 0; i < kUbList; ++i) s_ubl[wid][j * kUbList + i] = ubl[i];
+                    }
+                }
+                if (R > 1) {
+                    __syncthreads();
+                    if (active && rr == 0) {
+#pragma unroll
+                        for (int i = 0; i < kUbList; ++i)
+                            ubl[i] = g < R ? s_ubl[wid + g][j * kUbList + i] : INFINITY;
+                        merge16_groups(ubl);
+                    }
+                }
+                if (active && rr == 0 && g == 0 && hasq) {
+                    float kth = INFINITY;
+#pragma unroll
+                    for (int i = 0; i < kUbList; ++i)
+                        if (i == a.K - 1) kth = ubl[i];
+                    if (kth < INFINITY) {
+                        const double u = (double)kth;
                         const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                        atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
+                        atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + q,
                                   (unsigned long long)key_of(tub));
                     }
                 }
-                wave_sync();
+            } else {
+                if (active) {
+                    float* s_ub = s_ubl[wid];
+#pragma unroll
+                    for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
+                }
+                __syncthreads();
+                if (active && rr == 0) {
+                    for (int jj = 0; jj < nq; ++jj) {
+                        WaveList<64> L;
+                        L.init();
+                        for (int r2 = 0; r2 < R; ++r2)
+                            L.insert(key_of((double)s_ubl[wid + r2][jj * 64 + lane]), lane);
+                        uint64_t kk;
+                        int32_t ki;
+                        L.at(a.K - 1, kk, ki);
+                        const int qq = __shfl(q, jj, kWave);
+                        if (lane == 0 && dist_of(kk) < (double)INFINITY) {
+                            const double u = dist_of(kk);
+                            const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
+                            atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
+                                      (unsigned long long)key_of(tub));
+                        }
+                    }
+                }
             }
         }
     }

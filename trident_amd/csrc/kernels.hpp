@@ -157,8 +157,10 @@ template <int KP>
 __global__ void merge_kernel(MergeArgs a);
 
 // Batched-route work units: <= 64 queries of one cluster x one slice of ~kSplitVec vectors
-// (at most kMaxSplit slices per cluster, so a pass has <= kMaxSplit * (pairs / 64 + 2 nlist)).
+// (at most kMaxSplit slices per cluster); units of the seeding pass hold <= 16 queries and a
+// whole cluster.  A launch has <= kMaxSplit * (pairs / 64 + 2 nlist) units.
 constexpr int kUnitQ = 64;
+constexpr int kUnitQ0 = 16;
 constexpr int kSplitVec = 1024;
 constexpr int kMaxSplit = 8;
 constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
