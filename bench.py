@@ -10,10 +10,13 @@ One step = one full batched search of B queries (front end + two-pass cascade + 
 inputs already resident in HBM.  W warmup steps, then exactly K timed steps between two
 torch.cuda.synchronize() calls.  Afterwards (untimed):
   * exactness: every query's ids and distances against the float64 CPU oracle;
-  * roofline of the dominant kernel (the pass-2 pair scan): algorithmic bytes per launch =
-    sum over its (cluster, query) pairs of n_c * D_pad * 1 byte (SQ8 codes at full depth, no
-    pruning credit), divided by the launch's average duration from HIP events recorded on
-    the library's stream around that launch;
+  * roofline of the dominant kernel.  Batched route (the default at this size): the pass-B
+    scan on the int8 matrix cores, algorithmic work per launch = 4 * D_pad int8 ops per
+    (query, vector) candidate over every probed cluster (multiply + add, two weight planes),
+    priced against the 5.0 POP/s dense int8 peak.  Per-pair route: the pass-2 pair scan,
+    algorithmic bytes = sum over its pairs of n_c * D_pad (SQ8 codes at full depth), priced
+    against 8 TB/s.  Either way divided by the launch's duration from HIP events recorded on
+    the library's stream around it;
   * cpu_baseline: the reference's CPU IVF-Flat (omp_cpu_ivfflat_f32 restated in oracle/,
     FP32, OpenMP) on the same probes, all B queries, warmup 1 + 3 timed rounds.
 """
@@ -28,9 +31,11 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
-METRIC = "QPS at 100% exact top-10, 1×MI355X; achieved HBM GB/s vs peak"
+METRIC = "QPS at 100% exact top-10, 1×MI355X; achieved HBM GB/s vs peak"  # BASELINE.json metric, verbatim
 HBM_PEAK_GBPS = 8000.0
-PROFILE_TRAFFIC = os.path.join(ROOT, "profiles", "pair_scan_cfg2_traffic.json")
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix throughput
+PROFILE_TRAFFIC = {1: os.path.join(ROOT, "profiles", "pair_scan_cfg2_traffic.json"),
+                   2: os.path.join(ROOT, "profiles", "batch_scan_cfg2_traffic.json")}
 
 
 def log(*a):
@@ -71,6 +76,7 @@ def main():
     ap.add_argument("--K", type=int, default=0, help="0 = the config's value")
     ap.add_argument("--ub", type=int, default=1, help="TRIDENT_UB_SEED for the timed runs")
     ap.add_argument("--mode", type=int, default=2, help="2 cascade, 10 CM exact")
+    ap.add_argument("--route", type=int, default=0, help="mode-2 route: 0 auto, 1 per-pair, 2 batched")
     ap.add_argument("--N", type=int, default=0)
     ap.add_argument("--B", type=int, default=0)
     ap.add_argument("--check", type=int, default=-1, help="queries checked against the oracle (-1 = all)")
@@ -114,7 +120,7 @@ def main():
     xq_d = xq.contiguous()
 
     def run(nprobe, mode, ub, events=None):
-        return ix.search(xq_d, nprobe, mode=mode, ub_seed=ub, stage_events=events)
+        return ix.search(xq_d, nprobe, mode=mode, ub_seed=ub, stage_events=events, route=args.route)
 
     # ---- timed region ----
     nprobe, mode, ub = cfg["nprobe"], args.mode, args.ub
@@ -147,7 +153,7 @@ def main():
 
     # ---- algorithmic bytes and pruning statistics (untimed) ----
     stats = torch.zeros(4, dtype=torch.int64, device=dev)
-    d_out, i_out, _ = ix.search(xq_d, nprobe, mode=mode, ub_seed=ub, stats_buf=stats)
+    d_out, i_out, _ = ix.search(xq_d, nprobe, mode=mode, ub_seed=ub, stats_buf=stats, route=args.route)
     torch.cuda.synchronize()
     gpu_d, gpu_i = d_out.cpu().numpy().copy(), i_out.cpu().numpy().copy()
     probes = ix.probe_cids_buf[:B, :nprobe].cpu().numpy()
@@ -160,9 +166,25 @@ def main():
         bytes_p2 = int(sizes[probes].sum()) * D * 4
         bytes_all = bytes_p2
     tot, dims, surv, ins = [int(v) for v in stats.tolist()]
-    achieved = bytes_p2 / (stage["pass2_scan_ms"] * 1e-3) / 1e9
-    log(f"pass-2 scan: {bytes_p2 / 1e9:.2f} GB algorithmic in {stage['pass2_scan_ms']:.3f} ms -> {achieved:,.0f} GB/s "
-        f"({achieved / HBM_PEAK_GBPS:.2f} of peak); survivors {surv}/{tot}")
+    route = ix.route_for(B, nprobe, K, args.route) if mode == 2 else _lib.ROUTE_PAIR
+    t_scan = stage["pass2_scan_ms"] * 1e-3
+    if route == _lib.ROUTE_BATCHED:
+        # pass B scans every probed (query, vector) pair: D_pad int8 MACs per weight plane
+        ops_alg = 4 * bytes_all
+        achieved = ops_alg / t_scan / 1e12
+        roof = {"bound": "mfma", "kernel": "batch_scan_kernel<false, KS> (pass B, int8 matrix cores)",
+                "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                "frac": round(achieved / INT8_PEAK_TOPS, 4), "ops_alg_per_launch": ops_alg}
+        log(f"pass-B scan: {ops_alg / 1e12:.2f} T int8 ops in {stage['pass2_scan_ms']:.3f} ms -> {achieved:,.1f} TOP/s "
+            f"({achieved / INT8_PEAK_TOPS:.3f} of peak); survivors {surv}/{tot}")
+    else:
+        achieved = bytes_p2 / t_scan / 1e9
+        roof = {"bound": "hbm", "kernel": "pair_scan_kernel (pass 2)" if mode == 2 else "pair_scan_kernel (CM)",
+                "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes_alg_per_launch": bytes_p2}
+        log(f"pass-2 scan: {bytes_p2 / 1e9:.2f} GB algorithmic in {stage['pass2_scan_ms']:.3f} ms -> {achieved:,.0f} GB/s "
+            f"({achieved / HBM_PEAK_GBPS:.2f} of peak); survivors {surv}/{tot}")
+    roof["launch_ms"] = round(stage["pass2_scan_ms"], 4)
 
     # ---- exactness against the float64 oracle ----
     from oracle import oracle as O
@@ -225,25 +247,24 @@ def main():
         w0 = {"W0": W0, "rows": rows}
         log(f"calibrated W0 = {W0:.3e}")
 
-    traffic = None
-    if args.cfg == 2 and os.path.exists(PROFILE_TRAFFIC):
-        with open(PROFILE_TRAFFIC) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary of
+    # the same workload (cfg 2, nprobe 64 only)
+    roof["traffic"] = None
+    prof = PROFILE_TRAFFIC.get(route)
+    if args.cfg == 2 and nprobe == 64 and mode == 2 and prof and os.path.exists(prof):
+        with open(prof) as f:
+            roof["traffic"] = json.load(f).get("hbm_bytes_per_launch")
 
     line = {
         "metric": METRIC, "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8 codes / f32 bounds / f64 exact distances", "data": "synthetic",
+        "dtype": "u8 codes x int8 weights (i32 MFMA) / f32 bounds / f64 exact distances", "data": "synthetic",
         "config": {"workload": f"BASELINE {cfg['desc']}, N={N}, D={D}, nlist={nlist}, nprobe={nprobe}, "
                                f"K={K}, B={B}",
-                   "route": "cascade" if mode == 2 else "cm_exact", "ub_seed": ub, "p_init": p_init,
-                   "tile_size": cfg["T"], "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "pair_scan_kernel (pass 2)",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "bytes_alg_per_launch": bytes_p2,
-                     "launch_ms": round(stage["pass2_scan_ms"], 4)},
+                   "route": ("batched" if route == _lib.ROUTE_BATCHED else "pair") if mode == 2 else "cm_exact",
+                   "ub_seed": ub, "p_init": p_init, "tile_size": cfg["T"], "parallelism": "single GPU"},
+        "roofline": roof,
         "cpu_baseline": cpu,
         "exact": {"queries_checked": nchk, "probes_identical": probe_same, "ids_identical": ids_same,
                   "distances_identical": dist_same},

@@ -146,6 +146,13 @@ int trident_group_pairs(const int32_t* probe_cids, int32_t probe_ld, int32_t B, 
 /* The reference two-pass split rule for mode 2 / 10 (src/trident_v4_kernels.cu:1264-1276). */
 int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe);
 
+/* The route (TRIDENT_ROUTE_PAIR or TRIDENT_ROUTE_BATCHED) a mode-2 trident_search with these
+ * sizes and requested route takes, or a negative error code when the request cannot run.
+ * No reference counterpart: the reference has a single per-pair kernel; this lets a caller
+ * (or a benchmark) know which kernels its search launches. */
+int32_t trident_route_for(const TridentIndexView* ix, int32_t B, int32_t K, int32_t nprobe,
+                          int32_t requested_route);
+
 /* Per-candidate SQ8 bounds exactly as Stage Y (lb) and Stage X (ub) evaluate them, scaled to
  * bound the canonical float64 distance: lb[i] <= d64(q, x) <= ub[i] for the n (query,
  * sorted-position) pairs.  cids/qids/spos are device arrays of length n. */

@@ -388,6 +388,16 @@ int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe) 
     return 3;
 }
 
+int32_t trident_route_for(const TridentIndexView* ix, int32_t B, int32_t K, int32_t nprobe,
+                          int32_t requested_route) {
+    if (!ix) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "index view is NULL");
+    TridentSearchParams sp{};
+    sp.route = requested_route;
+    int route = TRIDENT_ROUTE_PAIR;
+    const int rc = choose_route(ix, &sp, B, K, nprobe, &route);
+    return rc ? -rc : route;
+}
+
 size_t trident_workspace_bytes(const TridentIndexView* ix, int32_t max_B, int32_t max_nprobe,
                                int32_t max_K) {
     if (!ix || max_B < 0 || max_nprobe < 1 || max_K < 1) return 0;

@@ -28,6 +28,9 @@ from typing import Optional
 import numpy as np
 import torch
 
+import ctypes
+
+from . import _lib
 from . import ext as _ext
 
 _U53 = 2.0 ** -53
@@ -62,8 +65,6 @@ class PinnedHostBuffer:
     """
 
     def __init__(self, shape, dtype=torch.float32):
-        import ctypes
-        from . import _lib
         nbytes = int(np.prod(shape)) * torch.empty(0, dtype=dtype).element_size()
         ptr = ctypes.c_void_p()
         _lib.check(_lib.lib().trident_host_alloc_mapped(ctypes.c_size_t(max(nbytes, 1)), ctypes.byref(ptr)),
@@ -77,9 +78,8 @@ class PinnedHostBuffer:
 
     def free(self):
         if self._ptr:
-            from . import _lib
             self.tensor = None
-            _lib.lib().trident_host_free(__import__("ctypes").c_void_p(self._ptr))
+            _lib.lib().trident_host_free(ctypes.c_void_p(self._ptr))
             self._ptr = None
 
 
@@ -364,6 +364,22 @@ class TridentV4Index:
             ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events,
             vec_Ar=self.vec_Ar, route=route)
         return topk_d, topk_i, kern_ms
+
+    def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
+        """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a mode-2 search of B queries takes."""
+        st = self.storage
+        view = _ext.make_index_view(
+            N=st.N, D=self.D, D_pad=self.D_pad, nlist=self.nlist, tile_size=self.tile_size,
+            per_cluster_sq8=self.per_cluster_sq8, W_combined=self.W_combined, b_combined=self.b_combined,
+            rot_sq_min=self.rot_sq_min, rot_sq_max=self.rot_sq_max, sq8_packed=self.sq8_packed,
+            tile_orig_ids=self.tile_orig_ids, tile_r_minmax=self.tile_r_minmax,
+            cluster_tile_off=self.cluster_tile_off, cluster_vec_off=st.cluster_vec_off,
+            xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
+            delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar)
+        r = _lib.lib().trident_route_for(ctypes.byref(view), int(B), int(k or self.k), int(nprobe), int(route))
+        if r < 0:
+            _lib.check(-r, "trident_route_for")
+        return int(r)
 
     # ---- views used by tests / oracle (host copies) ----
     def host_arrays(self):
