@@ -337,7 +337,8 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
         w.xrot64, w.qerr, rotate ? 1 : 0);
     int rc = check_launch("prep_queries_kernel");
     if (rc) return rc;
-    coarse_dist_kernel<<<dim3((ix->nlist + 63) / 64, (B + 31) / 32), kBlock, 0, st>>>(
+    constexpr int qpb = kCoarseQW * kWavesPerBlock;
+    coarse_dist_kernel<<<dim3((ix->nlist + 63) / 64, (B + qpb - 1) / qpb), kBlock, 0, st>>>(
         w.xq64, B, ix->D, ix->W_combined, ldw, ix->nlist, w.cd64);
     if ((rc = check_launch("coarse_dist_kernel"))) return rc;
     const size_t dyn = (size_t)ix->nlist * sizeof(uint64_t);
@@ -355,21 +356,51 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
     return check_launch("select_probes_kernel");
 }
 
+// Pair counting and scattering: LDS-aggregated per chunk while the 2 (nlist + 1) counters fit
+// 64 KiB of LDS, one global atomic per pair otherwise.
+int launch_count_pairs(const int32_t* probe_cids, int ld, int B, int nprobe, int p_init,
+                       int nlist, int32_t* counts, hipStream_t st) {
+    const int64_t total = (int64_t)B * nprobe;
+    if (group_lds_bytes(nlist) <= 64 * 1024) {
+        const unsigned blocks = (unsigned)((total + kGroupChunk - 1) / kGroupChunk);
+        count_pairs_lds_kernel<<<blocks, kBlock, group_lds_bytes(nlist), st>>>(
+            probe_cids, ld, B, nprobe, p_init, nlist, counts);
+        return check_launch("count_pairs_lds_kernel");
+    }
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    count_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, ld, B, nprobe, p_init, nlist, counts);
+    return check_launch("count_pairs_kernel");
+}
+
+int launch_scatter_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int B,
+                         int nprobe, int p_init, int nlist, int32_t* cursor, int32_t* p1c,
+                         int32_t* p1q, float* p1d, int32_t* p2c, int32_t* p2q, float* p2d,
+                         hipStream_t st) {
+    const int64_t total = (int64_t)B * nprobe;
+    if (group_lds_bytes(nlist) <= 64 * 1024) {
+        const unsigned blocks = (unsigned)((total + kGroupChunk - 1) / kGroupChunk);
+        scatter_pairs_lds_kernel<<<blocks, kBlock, group_lds_bytes(nlist), st>>>(
+            probe_cids, probe_dqcs, ld, B, nprobe, p_init, nlist, cursor, p1c, p1q, p1d, p2c, p2q,
+            p2d);
+        return check_launch("scatter_pairs_lds_kernel");
+    }
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    scatter_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, probe_dqcs, ld, B, nprobe, p_init,
+                                                 nlist, cursor, p1c, p1q, p1d, p2c, p2q, p2d);
+    return check_launch("scatter_pairs_kernel");
+}
+
 int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int B, int nprobe,
                 int p_init, int nlist, int32_t* counts, int32_t* seg_off, int32_t* cursor,
                 int32_t* p1c, int32_t* p1q, float* p1d, int32_t* p2c, int32_t* p2q, float* p2d,
                 hipStream_t st) {
     int rc = fill(counts, 0, 2 * ((int64_t)nlist + 1), st);
     if (rc) return rc;
-    const int64_t total = (int64_t)B * nprobe;
-    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-    count_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, ld, B, nprobe, p_init, nlist, counts);
-    if ((rc = check_launch("count_pairs_kernel"))) return rc;
+    if ((rc = launch_count_pairs(probe_cids, ld, B, nprobe, p_init, nlist, counts, st))) return rc;
     scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
     if ((rc = check_launch("scan_pairs_kernel"))) return rc;
-    scatter_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, probe_dqcs, ld, B, nprobe, p_init,
-                                                 nlist, cursor, p1c, p1q, p1d, p2c, p2q, p2d);
-    return check_launch("scatter_pairs_kernel");
+    return launch_scatter_pairs(probe_cids, probe_dqcs, ld, B, nprobe, p_init, nlist, cursor, p1c,
+                                p1q, p1d, p2c, p2q, p2d, st);
 }
 
 }  // namespace
@@ -427,25 +458,21 @@ int trident_group_pairs(const int32_t* probe_cids, int32_t probe_ld, int32_t B, 
                         int32_t* p2_cids, int32_t* p2_qids, int32_t* seg_off,
                         int32_t* counts_ws, void* stream) {
     if (B < 0 || nprobe < 1 || p_init < 0 || p_init > nprobe || nlist < 1 || probe_ld < nprobe ||
-        !seg_off || !counts_ws)
+        !seg_off || !counts_ws || (int64_t)B * nprobe > 0x7fffffff)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad group_pairs arguments");
     if (B == 0) return TRIDENT_OK;
     hipStream_t st = static_cast<hipStream_t>(stream);
     // cursor reuses counts_ws after the scan has consumed the counts.
     int rc = fill(counts_ws, 0, 2 * ((int64_t)nlist + 1), st);
     if (rc) return rc;
-    const int64_t total = (int64_t)B * nprobe;
-    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-    count_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, probe_ld, B, nprobe, p_init, nlist,
-                                               counts_ws);
-    if ((rc = check_launch("count_pairs_kernel"))) return rc;
+    if ((rc = launch_count_pairs(probe_cids, probe_ld, B, nprobe, p_init, nlist, counts_ws, st)))
+        return rc;
     scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts_ws, nlist, seg_off, seg_off);
     if ((rc = check_launch("scan_pairs_kernel"))) return rc;
     // seg_off now doubles as the cursor; restore it from the counts afterwards.
-    scatter_pairs_kernel<<<blocks, 256, 0, st>>>(probe_cids, nullptr, probe_ld, B, nprobe, p_init,
-                                                 nlist, seg_off, p1_cids, p1_qids, nullptr,
-                                                 p2_cids, p2_qids, nullptr);
-    if ((rc = check_launch("scatter_pairs_kernel"))) return rc;
+    if ((rc = launch_scatter_pairs(probe_cids, nullptr, probe_ld, B, nprobe, p_init, nlist, seg_off,
+                                   p1_cids, p1_qids, nullptr, p2_cids, p2_qids, nullptr, st)))
+        return rc;
     scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts_ws, nlist, seg_off, seg_off);
     return check_launch("scan_pairs_kernel");
 }
@@ -465,6 +492,9 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if (nprobe < 1 || nprobe > ix->nlist || nprobe > 512)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "nprobe=%d outside [1, min(nlist=%d, 512)]",
                     nprobe, ix->nlist);
+    if ((int64_t)B * nprobe > 0x7fffffff)
+        return fail(TRIDENT_ERR_UNSUPPORTED, "B * nprobe = %lld exceeds 2^31 - 1",
+                    (long long)B * nprobe);
     if (sp->ub_seed < 0 || sp->ub_seed > 2)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "ub_seed=%d outside {0,1,2}", sp->ub_seed);
     if (!out->topk_d || !out->topk_i)

@@ -34,6 +34,7 @@ __global__ __launch_bounds__(256) void prep_queries_kernel(
     if (!do_rot || j >= D_pad) return;
     double acc = 0.0, mag = 0.0;
     const float* wcol = W + nlist + j;
+#pragma unroll 8
     for (int d = 0; d < D; ++d) {
         const double qd = (double)qr[d];
         const double r = (double)wcol[(size_t)d * ldw];
@@ -47,14 +48,15 @@ __global__ __launch_bounds__(256) void prep_queries_kernel(
     qerr[(size_t)b * D_pad + j] = (double)(D + 3) * 0x1p-52 * (mag + fabs(bj)) + 0x1p-1000;
 }
 
-// grid (ceil(nlist / 64), ceil(B / 32)), block 256: each wave owns 64 centroids (one per
-// lane) x 8 queries; query values are wave-uniform (scalar loads).  Centroid c, dim d is
-// -0.5f * W[d, c], exact because W_coarse_only = -2 C^T.
+// grid (ceil(nlist / 64), ceil(B / (kCoarseQW * 4))), block 256: each wave owns 64 centroids
+// (one per lane) x kCoarseQW queries; query values are wave-uniform (scalar loads, two dims at
+// a time when the rows allow it).  Centroid c, dim d is -0.5f * W[d, c], exact because
+// W_coarse_only = -2 C^T.  Each (query, centroid) sum is one fma chain in dimension order.
 __global__ __launch_bounds__(256) void coarse_dist_kernel(const double* __restrict__ xq64, int B,
                                                           int D, const float* __restrict__ W,
                                                           int ldw, int nlist,
                                                           double* __restrict__ cd64) {
-    constexpr int QW = 8;
+    constexpr int QW = kCoarseQW;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = blockIdx.x * 64 + lane;
@@ -68,7 +70,22 @@ __global__ __launch_bounds__(256) void coarse_dist_kernel(const double* __restri
 #pragma unroll
     for (int i = 0; i < QW; ++i) acc[i] = 0.0;
     const float* wc = W + cc;
-    for (int d = 0; d < D; ++d) {
+    int d = 0;
+    if ((D & 1) == 0) {  // rows are 16-byte aligned: xq64 is 256-byte aligned, D even
+        for (; d < D; d += 2) {
+            const double cv0 = (double)(-0.5f * wc[(size_t)d * ldw]);
+            const double cv1 = (double)(-0.5f * wc[(size_t)(d + 1) * ldw]);
+#pragma unroll
+            for (int i = 0; i < QW; ++i) {
+                const double2 qv = *reinterpret_cast<const double2*>(qrow[i] + d);
+                double t = qv.x - cv0;
+                acc[i] = fma(t, t, acc[i]);
+                t = qv.y - cv1;
+                acc[i] = fma(t, t, acc[i]);
+            }
+        }
+    }
+    for (; d < D; ++d) {
         const double cv = (double)(-0.5f * wc[(size_t)d * ldw]);
 #pragma unroll
         for (int i = 0; i < QW; ++i) {
@@ -323,6 +340,72 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
         if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
         const bool first = p < p_init;
         const int slot = atomicAdd(&cursor[(first ? 0 : (nlist + 1)) + cid], 1);
+        int32_t* oc = first ? p1_cids : p2_cids;
+        int32_t* oq = first ? p1_qids : p2_qids;
+        float* od = first ? p1_dqcs : p2_dqcs;
+        oc[slot] = cid;
+        oq[slot] = q;
+        if (od) od[slot] = probe_dqcs ? probe_dqcs[(size_t)q * ld + p] : 0.0f;
+    }
+}
+
+// Pair grouping with the histogram aggregated in LDS (used when 2 (nlist + 1) counters fit
+// the dynamic LDS): each block counts one chunk of kGroupChunk (query, probe) entries with LDS
+// atomics and adds its non-zero bins to the global counts -- one global atomic per (block,
+// cluster) instead of one per pair.
+__global__ __launch_bounds__(256) void count_pairs_lds_kernel(const int32_t* __restrict__ probe_cids,
+                                                              int ld, int B, int nprobe, int p_init,
+                                                              int nlist, int32_t* counts) {
+    extern __shared__ int32_t s_hist[];
+    const int H = 2 * (nlist + 1);
+    for (int i = threadIdx.x; i < H; i += blockDim.x) s_hist[i] = 0;
+    __syncthreads();
+    const int total = B * nprobe;
+    const int i0 = blockIdx.x * kGroupChunk, i1 = min(total, i0 + kGroupChunk);
+    for (int idx = i0 + (int)threadIdx.x; idx < i1; idx += blockDim.x) {
+        const int q = idx / nprobe, p = idx - q * nprobe;
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
+        atomicAdd(&s_hist[(p < p_init ? 0 : (nlist + 1)) + cid], 1);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const int v = s_hist[i];
+        if (v) atomicAdd(&counts[i], v);
+    }
+}
+
+// Same chunks as count_pairs_lds_kernel: the block reserves one range per non-empty bin
+// (a global atomicAdd on the cursor) and places its entries with LDS atomics.
+__global__ __launch_bounds__(256) void scatter_pairs_lds_kernel(
+    const int32_t* __restrict__ probe_cids, const float* __restrict__ probe_dqcs, int ld, int B,
+    int nprobe, int p_init, int nlist, int32_t* cursor, int32_t* __restrict__ p1_cids,
+    int32_t* __restrict__ p1_qids, float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
+    int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs) {
+    extern __shared__ int32_t s_hist[];
+    const int H = 2 * (nlist + 1);
+    for (int i = threadIdx.x; i < H; i += blockDim.x) s_hist[i] = 0;
+    __syncthreads();
+    const int total = B * nprobe;
+    const int i0 = blockIdx.x * kGroupChunk, i1 = min(total, i0 + kGroupChunk);
+    for (int idx = i0 + (int)threadIdx.x; idx < i1; idx += blockDim.x) {
+        const int q = idx / nprobe, p = idx - q * nprobe;
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;
+        atomicAdd(&s_hist[(p < p_init ? 0 : (nlist + 1)) + cid], 1);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < H; i += blockDim.x) {
+        const int v = s_hist[i];
+        if (v) s_hist[i] = atomicAdd(&cursor[i], v);
+    }
+    __syncthreads();
+    for (int idx = i0 + (int)threadIdx.x; idx < i1; idx += blockDim.x) {
+        const int q = idx / nprobe, p = idx - q * nprobe;
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;
+        const bool first = p < p_init;
+        const int slot = atomicAdd(&s_hist[(first ? 0 : (nlist + 1)) + cid], 1);
         int32_t* oc = first ? p1_cids : p2_cids;
         int32_t* oq = first ? p1_qids : p2_qids;
         float* od = first ? p1_dqcs : p2_dqcs;

@@ -150,6 +150,25 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
                                      int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs);
 
+constexpr int kGroupChunk = 8192;  // (query, probe) entries per block of the LDS grouping
+constexpr int kCoarseQW = 16;      // queries per wave of coarse_dist_kernel
+
+// Dynamic LDS bytes of the LDS grouping kernels; they are used while this is <= 64 KiB.
+inline size_t group_lds_bytes(int nlist) { return (size_t)2 * (nlist + 1) * sizeof(int32_t); }
+
+__global__ void count_pairs_lds_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
+                                       int nprobe, int p_init, int nlist, int32_t* counts);
+
+__global__ void scatter_pairs_lds_kernel(const int32_t* __restrict__ probe_cids,
+                                         const float* __restrict__ probe_dqcs, int ld, int B,
+                                         int nprobe, int p_init, int nlist, int32_t* cursor,
+                                         int32_t* __restrict__ p1_cids,
+                                         int32_t* __restrict__ p1_qids,
+                                         float* __restrict__ p1_dqcs,
+                                         int32_t* __restrict__ p2_cids,
+                                         int32_t* __restrict__ p2_qids,
+                                         float* __restrict__ p2_dqcs);
+
 template <int KP, bool CASCADE, bool UB>
 __global__ void pair_scan_kernel(ScanArgs a);
 
