@@ -58,6 +58,20 @@ def test_coarse_probe_matches_oracle(gmm, dev):
         assert np.array_equal(got, ref), f"nprobe={nprobe}"
 
 
+def test_coarse_probe_selectors_all_widths(dev):
+    """nprobe <= 64 and <= 128 use the one-wave register selector, larger ones the block radix
+    select; all must give the oracle's (d, cid) order, including at the 64 / 128 edges."""
+    xb, xq = datagen.cfg4(N=20_000, D=96, B=150, n_centers=256, seed=41)
+    b = build_index(xb, 256, dev, max_batch=256, max_nprobe=256)
+    xq = xq.numpy()
+    for nprobe in (63, 64, 65, 128, 129, 200, 256):
+        b.ix.search(_q(xq, dev), nprobe, mode=10, k=10)
+        torch.cuda.synchronize()
+        got = b.ix.probe_cids_buf[: len(xq), :nprobe].cpu().numpy()
+        ref, _ = O.coarse_probe(xq, b.centroids_idx, nprobe)
+        assert np.array_equal(got, ref), f"nprobe={nprobe}"
+
+
 @pytest.mark.parametrize("mode", [10, 2])
 def test_gmm_k10(gmm, dev, mode):
     b, xq = gmm

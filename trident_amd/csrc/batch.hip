@@ -278,11 +278,13 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
     Qp = sum16_f64(Qp);
-    double s = 1.0;
+    // s and 1/s are powers of two (|e| <= 1010 here), so w * (1/s) is exactly w / s
+    int es = 0;
     if (mx > 0x1p-100) {
-        s = ldexp(1.0, ilogb(mx) - 14);
-        if (mx / s > 32639.0) s *= 2.0;
+        es = ilogb(mx) - 14;
+        if (ldexp(mx, -es) > 32639.0) ++es;
     }
+    const double s = ldexp(1.0, es), inv_s = ldexp(1.0, -es);
     double errs = 0.0;
     int wsum = 0, wabs = 0;
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
@@ -291,7 +293,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         uint32_t hw = 0u, lw = 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int wi = (int)rint(w[k][e] / s);  // 0 for dims >= D_pad
+            const int wi = (int)rint(w[k][e] * inv_s);  // 0 for dims >= D_pad
             errs += fabs(w[k][e] - s * (double)wi) + 0x1p-52 * fabs(w[k][e]);
             wsum += wi;
             wabs += abs(wi);

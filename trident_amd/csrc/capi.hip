@@ -341,6 +341,18 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
     coarse_dist_kernel<<<dim3((ix->nlist + 63) / 64, (B + qpb - 1) / qpb), kBlock, 0, st>>>(
         w.xq64, B, ix->D, ix->W_combined, ldw, ix->nlist, w.cd64);
     if ((rc = check_launch("coarse_dist_kernel"))) return rc;
+    if (nprobe <= 128) {  // one wave per query, register list
+        const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
+        if (nprobe <= 64)
+            select_probes_wave_kernel<64><<<grid, kBlock, 0, st>>>(
+                w.cd64, B, ix->nlist, nprobe, w.probe_cids, w.probe_dqcs, nprobe, probe_cids,
+                probe_dqcs, ld);
+        else
+            select_probes_wave_kernel<128><<<grid, kBlock, 0, st>>>(
+                w.cd64, B, ix->nlist, nprobe, w.probe_cids, w.probe_dqcs, nprobe, probe_cids,
+                probe_dqcs, ld);
+        return check_launch("select_probes_wave_kernel");
+    }
     const size_t dyn = (size_t)ix->nlist * sizeof(uint64_t);
     static bool attr_set = false;
     if (!attr_set) {

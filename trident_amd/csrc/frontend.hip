@@ -349,6 +349,110 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
     }
 }
 
+// One wave per query (nprobe <= KP): the query's float64 centroid distances go through a
+// register list of the KP best (d, cid) entries, sorted across lanes.  Each chunk of 1024 keys
+// (16 per lane) is first cut at T0 = the largest over lanes of each lane's r-th smallest entry,
+// r = ceil(nprobe / 64): at least nprobe entries are <= T0, so nothing above T0 (or above the
+// list's current nprobe-th entry) can be selected.  The few entries below the cut are compacted
+// through LDS and merged in batches of 64.  Same (d, cid) order as the block radix select,
+// without barriers.
+template <int KP>
+__global__ __launch_bounds__(256) void select_probes_wave_kernel(
+    const double* __restrict__ cd64, int B, int nlist, int nprobe, int32_t* __restrict__ out_cids,
+    float* __restrict__ out_dqcs, int ld, int32_t* __restrict__ out2_cids,
+    float* __restrict__ out2_dqcs, int ld2) {
+    constexpr int kPer = 16;  // keys per lane per chunk
+    __shared__ uint64_t s_ck[kWavesPerBlock][kPer * kWave];
+    __shared__ int32_t s_ci[kWavesPerBlock][kPer * kWave];
+    const int lane = threadIdx.x & 63;
+    const int wid = (int)(threadIdx.x >> 6);
+    const int q = blockIdx.x * kWavesPerBlock + wid;
+    if (q >= B) return;
+    const double* row = cd64 + (size_t)q * nlist;
+    uint64_t* ck = s_ck[wid];
+    int32_t* ci = s_ci[wid];
+    WaveList<KP> L;
+    L.init();
+    for (int c0 = 0; c0 < nlist; c0 += kPer * kWave) {
+        uint64_t k[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int c = c0 + i * kWave + lane;
+            k[i] = c < nlist ? key_of(row[c]) : kKeyInvalid;
+        }
+        // this lane's smallest and second smallest (key, cid) of the chunk
+        uint64_t m1k = kKeyInvalid, m2k = kKeyInvalid;
+        int32_t m1i = kIdInvalid, m2i = kIdInvalid;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int32_t id = c0 + i * kWave + lane;
+            if (ent_less(k[i], id, m1k, m1i)) {
+                m2k = m1k;
+                m2i = m1i;
+                m1k = k[i];
+                m1i = id;
+            } else if (ent_less(k[i], id, m2k, m2i)) {
+                m2k = k[i];
+                m2i = id;
+            }
+        }
+        uint64_t tk = nprobe > kWave ? m2k : m1k;
+        int32_t ti = nprobe > kWave ? m2i : m1i;
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) {  // T0 = max over lanes
+            const uint64_t ok = shfl_xor_u64(tk, o);
+            const int32_t oi = __shfl_xor(ti, o, kWave);
+            if (ent_less(tk, ti, ok, oi)) {
+                tk = ok;
+                ti = oi;
+            }
+        }
+        uint64_t lk;
+        int32_t li;
+        L.at(nprobe - 1, lk, li);
+        if (ent_less(lk, li, tk, ti)) {
+            tk = lk;
+            ti = li;
+        }
+        // compact the entries <= (tk, ti)
+        int n = 0;
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int32_t id = c0 + i * kWave + lane;
+            const bool take = !ent_less(tk, ti, k[i], id) && k[i] != kKeyInvalid;
+            const uint64_t m = __ballot(take);
+            if (take) {
+                const int pos = n + mask_rank(m);
+                ck[pos] = k[i];
+                ci[pos] = id;
+            }
+            n += __popcll(m);
+        }
+        wave_sync();
+        for (int b0 = 0; b0 < n; b0 += kWave) {
+            const int i = b0 + lane;
+            list_offer(L, nprobe, i < n ? ck[i] : kKeyInvalid, i < n ? ci[i] : kIdInvalid);
+        }
+        wave_sync();
+    }
+    auto emit = [&](int rank, uint64_t key, int32_t cid) {
+        const float dq = (float)sqrt(dist_of(key));
+        out_cids[(size_t)q * ld + rank] = cid;
+        out_dqcs[(size_t)q * ld + rank] = dq;
+        if (out2_cids) out2_cids[(size_t)q * ld2 + rank] = cid;
+        if (out2_dqcs) out2_dqcs[(size_t)q * ld2 + rank] = dq;
+    };
+    if (lane < nprobe) emit(lane, L.k0, L.i0);
+    if constexpr (KP == 128) {
+        if (kWave + lane < nprobe) emit(kWave + lane, L.k1, L.i1);
+    }
+}
+
+template __global__ void select_probes_wave_kernel<64>(const double*, int, int, int, int32_t*,
+                                                       float*, int, int32_t*, float*, int);
+template __global__ void select_probes_wave_kernel<128>(const double*, int, int, int, int32_t*,
+                                                        float*, int, int32_t*, float*, int);
+
 // Pair grouping with the histogram aggregated in LDS (used when 2 (nlist + 1) counters fit
 // the dynamic LDS): each block counts one chunk of kGroupChunk (query, probe) entries with LDS
 // atomics and adds its non-zero bins to the global counts -- one global atomic per (block,

@@ -137,6 +137,13 @@ __global__ void select_probes_kernel(const double* __restrict__ cd64, int nlist,
                                      int32_t* __restrict__ out2_cids,
                                      float* __restrict__ out2_dqcs, int ld2);
 
+template <int KP>
+__global__ void select_probes_wave_kernel(const double* __restrict__ cd64, int B, int nlist,
+                                          int nprobe, int32_t* __restrict__ out_cids,
+                                          float* __restrict__ out_dqcs, int ld,
+                                          int32_t* __restrict__ out2_cids,
+                                          float* __restrict__ out2_dqcs, int ld2);
+
 __global__ void count_pairs_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
                                    int nprobe, int p_init, int nlist, int32_t* counts);
 
