@@ -19,6 +19,9 @@ CSRC = os.path.join(PKG, "csrc")
 OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtrident_hip.so")
 SOURCES = ["frontend.hip", "scan.hip", "batch.hip", "capi.hip"]
+# Per-source flags.  batch.hip: matrix-core results in VGPRs (no accumulator-register reads in
+# the per-tile epilogue).
+EXTRA = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HEADERS = ["common.hpp", "kernels.hpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -28,11 +31,6 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(ROOT, "include"), "-Wall", "-Wno-unused-function",
 ]
-
-
-def _compile(src: str, obj: str) -> None:
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
-    subprocess.run(cmd, check=True)
 
 
 def build(force: bool = True, jobs: int = 3) -> str:
@@ -47,7 +45,7 @@ def build(force: bool = True, jobs: int = 3) -> str:
         objs.append(obj)
         fresh = (os.path.exists(obj) and os.path.getmtime(obj) >= max(os.path.getmtime(src), newest_dep))
         if force or not fresh:
-            procs.append((s, subprocess.Popen([HIPCC, *CFLAGS, "-c", src, "-o", obj])))
+            procs.append((s, subprocess.Popen([HIPCC, *CFLAGS, *EXTRA.get(s, []), "-c", src, "-o", obj])))
         while len([p for _, p in procs if p.poll() is None]) >= jobs:
             procs[[p.poll() is None for _, p in procs].index(True)][1].wait()
     for name, p in procs:

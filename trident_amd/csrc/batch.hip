@@ -506,8 +506,9 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
             const float4 ar23 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g + 2]);
             const float Ar[4][2] = {{ar01.x, ar01.y}, {ar01.z, ar01.w}, {ar23.x, ar23.y},
                                     {ar23.z, ar23.w}};
-            // epilogue: rows 4g + r (vectors), column j (query)
-            uint32_t sbits = 0;
+            // epilogue: rows 4g + r (vectors), column j (query); the lower-bound pass keeps
+            // each row's survivors as the wave mask its compare produces
+            uint64_t sm[4] = {0ull, 0ull, 0ull, 0ull};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int acc = (acc_hi[r] << 8) + acc_lo[r];
@@ -528,22 +529,22 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                     // c1f = c2f = 0, H32 = +inf
                     const float L = fmaf(c2f, Ar[r][1], Ar[r][0]);
                     const float Rv = fmaf(c1f, (float)acc, H32);
-                    sbits |= (uint32_t)(L <= Rv) << r;
+                    sm[r] = __ballot(L <= Rv);
                 }
             }
             if constexpr (!UB_PASS) {
-                if (__ballot(sbits != 0) == 0) return;
+                if ((sm[0] | sm[1] | sm[2] | sm[3]) == 0ull) return;
                 // rare: append survivors (sorted position) to the query's list
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if ((sbits >> r) & 1u) {
+                    if ((sm[r] >> lane) & 1ull) {
                         const int slot = atomicAdd(&a.cand_cnt[q], 1);
                         if (slot < a.cap) a.cand_id[(size_t)q * a.cap + slot] = v0 + li0 + 4 * g + r;
                     }
                 }
                 if (a.stats) {
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) st_surv += __popcll(__ballot((sbits >> r) & 1u));
+                    for (int r = 0; r < 4; ++r) st_surv += __popcll(sm[r]);
                 }
             }
         };
