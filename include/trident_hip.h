@@ -70,6 +70,10 @@ typedef struct TridentIndexView {
     const float* vec_Ar;             /* [N, 2] sorted order: |code*delta|^2 rounded down (margin
                                         1e-13), residual-norm bound rounded up; NULL disables the
                                         batched route */
+    const uint32_t* sq8_cells;       /* [total_tiles, D_pad / 16, tile_size, 4]: the codes of
+                                        sq8_packed regrouped as 16-byte cells (dims 16 g ..
+                                        16 g + 15 of one slot), every byte c stored as c ^ 0x80
+                                        (c - 128 as int8); NULL disables the batched route */
 } TridentIndexView;
 
 /* How mode 2 is executed.  Both are exact; they differ in speed only. */

@@ -6,7 +6,8 @@ Reference layout: benchmarks/phase4a_suite.py:95-278.  Pinned here:
   * rotation bounds bracket the squared singular values of the float32 rotation;
   * codes equal the closed form clip(round_half_even((x32 - vmin) / delta), 0, 255);
   * eps bounds the quantisation error of every vector against the float64 rotation;
-  * unpacking sq8_packed / tile_orig_ids recovers every code and id (the wave64 layout);
+  * unpacking sq8_packed / tile_orig_ids recovers every code and id (the wave64 layout), and
+    the batched route's 16-byte cells (sq8_cells) decode to the same codes;
   * block bounds (uniform and variable schemes);
   * the Stage Y / Stage X bound arithmetic, restated in float32 numpy, brackets the float64
     distance: lb <= d64 <= ub.
@@ -112,6 +113,33 @@ def test_codes_closed_form_and_packing(hist_ix):
             assert np.array_equal(vmin[c], xr32[m].min(0))
             assert np.array_equal(delta[c], np.maximum((xr32[m].max(0) - xr32[m].min(0)) / np.float32(255.0),
                                                        np.float32(1e-12)))
+
+
+def unpack_cells(ix):
+    """[N, D_pad] uint8 codes recovered from sq8_cells [tiles, D_pad/16, T, 4] in sorted order."""
+    T = ix.tile_size
+    cells = ix.sq8_cells.numpy().view(np.uint8)           # [tiles, G16, T, 16] bytes c ^ 0x80
+    assert cells.shape == (ix.total_tiles, ix.D_pad // 16, T, 16)
+    toff = ix.cluster_tile_off.numpy()
+    voff = ix.storage.cluster_vec_off.numpy()
+    codes = np.zeros((ix.N, ix.D_pad), np.uint8)
+    for c in range(ix.nlist):
+        li = np.arange(voff[c + 1] - voff[c])
+        t, s = toff[c] + li // T, li % T
+        codes[voff[c]:voff[c + 1]] = (cells[t, :, s, :] ^ 0x80).reshape(len(li), -1)
+    return codes
+
+
+@pytest.mark.parametrize("which", ["hist", "gmm"])
+def test_cells_hold_the_packed_codes(which, hist_ix, gmm_ix):
+    """The batched route's 16-byte cells (dims 16 g .. 16 g + 15 of a slot, bytes c ^ 0x80)
+    decode to exactly the codes of sq8_packed, and padded slots hold code 0."""
+    ix = (hist_ix if which == "hist" else gmm_ix)[0]
+    codes, _ = unpack_codes(ix)
+    assert np.array_equal(unpack_cells(ix), codes)
+    cells = ix.sq8_cells.numpy().view(np.uint8)
+    pad = ix.tile_orig_ids.numpy() < 0                     # [tiles, T]
+    assert (cells[pad.nonzero()[0], :, pad.nonzero()[1], :] == 0x80).all()
 
 
 @pytest.mark.parametrize("which", ["hist", "gmm"])

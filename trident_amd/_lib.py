@@ -28,6 +28,7 @@ class TridentIndexView(ctypes.Structure):
         ("cluster_tile_off", _P), ("cluster_vec_off", _P),
         ("xb_sorted", _P), ("orig_ids_sorted", _P),
         ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P), ("vec_Ar", _P),
+        ("sq8_cells", _P),
     ]
 
 

@@ -7,25 +7,28 @@
 //
 //     |x_hat - q_rot|^2 = A_x - 2 sum_d c_d w_d + Q_q,   A_x = sum_d (c_d delta_d)^2,  Q_q = |q'|^2
 //
-// w is quantised per query to w = s * w_int + err (s a power of two, |w_int| <= 32639, split
-// w_int = 256 * hi + lo into two int8 planes); with c' = c - 128 the dot product
+// w is quantised to w = s * w_int + err (s a power of two shared by the 16 queries a wave
+// scans together, |w_int| <= 32639, split w_int = 256 * hi + lo into two int8 planes); with
+// c' = c - 128 the dot product
 //     sum_d c_d w_int,d = 256 * MFMA(c', hi) + MFMA(c', lo) + 128 * sum_d w_int,d
 // is computed EXACTLY by v_mfma_i32_16x16x64_i8 (two per 64 dims), and
 // |sum_d c_d w_d - s * dot| <= 255 * sum_d |w_d - s w_int,d| = err_q.  The triangle inequality
 // with r_x >= |x_rot - x_hat| (per vector) and e_q >= |q_rot(float64) - q_rot(exact)| gives
 //     lower bound:  |x_rot - q_rot| >= sqrt(A_x + Q_q - 2 s dot - 2 err_q) - r_x - e_q
 //     upper bound:  |x_rot - q_rot| <= sqrt(A_x + Q_q - 2 s dot + 2 err_q) + r_x + e_q
-// (this norm form keeps the per-dimension bound's selectivity: the same 0.006% survivors on
-// cfg-2 data).  Scaled by the rotation's squared singular-value bounds these bound the
-// canonical float64 distance.
+// Scaled by the rotation's squared singular-value bounds these bound the canonical float64
+// distance.
 //
 // Pass A (UB):  for the first p_init probes of each query, the K-th smallest upper bound over
 //               the cluster -> atomicMin into tau[q] (the reference's Stage X seeding,
 //               src/trident_v4_kernels.cu:626-676, computed for 64 queries at once; the K-th
 //               smallest upper bound of any K vectors bounds the K-th distance).
-// Pass B (LB):  for every probe, vectors whose lower bound passes tau[q] are appended (sorted
-//               position) to the query's candidate list.  The test runs in float32 with an
-//               additive slack that bounds every rounding of it.
+// Pass B (LB):  for every probe, vectors whose lower bound passes tau[q] are queued in LDS and
+//               appended (sorted position) to the query's candidate list.  The bulk test is
+//               one int32 compare per (vector, query), acc + kq >= thr_x, with per-query and
+//               per-vector constants rounded outward; rows that pass are re-tested in float32
+//               with an additive slack that bounds every rounding of it (0.07% of (vector,
+//               query) pairs survive on cfg-2 data).
 // Refine:       one wave per query computes the canonical float64 distance of each listed
 //               survivor and keeps it iff <= tau[q] (the reference's Stage Z, :796-941).
 //
@@ -35,8 +38,8 @@
 // from HBM once per XCD and then served by that XCD's L2; within a range each workgroup takes
 // the next unit from its XCD's counter (persistent grid, one atomic per unit).  The unit's
 // vectors stream through LDS in 64-vector blocks, double-buffered: all 256 threads load block
-// b+1 (16-byte loads, D_pad/4 rows of 256 contiguous bytes) while the waves run block b from
-// LDS, one barrier per block.  Lane l = (i = l & 15, g = l >> 4) holds, for every 64-dim step,
+// b+1 (16-byte code cells, 1 KiB contiguous per wave and load) while the waves run block b
+// from LDS, one barrier per block.  Lane l = (i = l & 15, g = l >> 4) holds, for every 64-dim step,
 // bytes of dims step*64 + g*16 + [0, 16): vector i's codes in the A operand and query i's
 // weights in the B operand (any dim-to-byte assignment shared by A and B computes the same
 // contraction); the result row 4g + r, column i sits in lane l, register r.
@@ -68,17 +71,16 @@ __device__ __forceinline__ int units_of_entry(const int32_t* seg_off, const int3
     return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c], p) : 0;
 }
 
-// grid 1: exclusive scan of the unit counts of the 2 * nlist (pass, cluster) segments.
-__global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
-                                                        const int32_t* vec_off, int nlist,
-                                                        int32_t* unit_off) {
-    __shared__ uint32_t s_wtot[kWavesPerBlock];
+__device__ __forceinline__ int groups_of_entry(const int32_t* seg_off, int nlist, int e) {
+    const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
+    const int32_t* so = seg_off + p * (nlist + 1);
+    return (so[c + 1] - so[c] + kGroupQ - 1) / kGroupQ;
+}
+
+// Block-wide exclusive scan of one count per thread (grid 1); returns the total.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t local, uint32_t& run,
+                                                    uint32_t* s_wtot) {
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const int E = 2 * nlist;
-    const int per = (E + kBlock - 1) / kBlock;
-    const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
-    uint32_t local = 0;
-    for (int e = e0; e < e1; ++e) local += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
     uint32_t inc = local;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -87,26 +89,72 @@ __global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
     }
     if (lane == kWave - 1) s_wtot[wid] = inc;
     __syncthreads();
-    uint32_t run = inc - local, total = 0;
+    uint32_t total = 0;
+    run = inc - local;
     for (int w = 0; w < kWavesPerBlock; ++w) {
         if (w < wid) run += s_wtot[w];
         total += s_wtot[w];
     }
+    __syncthreads();  // s_wtot is reused by the next scan
+    return total;
+}
+
+// grid 1: exclusive scans of the unit counts and of the weight-group counts of the 2 * nlist
+// (pass, cluster) segments.
+__global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
+                                                        const int32_t* vec_off, int nlist,
+                                                        int32_t* unit_off, int32_t* grp_off) {
+    __shared__ uint32_t s_wtot[kWavesPerBlock];
+    const int tid = threadIdx.x;
+    const int E = 2 * nlist;
+    const int per = (E + kBlock - 1) / kBlock;
+    const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+    uint32_t lu = 0, lg = 0;
     for (int e = e0; e < e1; ++e) {
-        unit_off[e] = (int32_t)run;
-        run += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
+        lu += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
+        lg += (uint32_t)groups_of_entry(seg_off, nlist, e);
     }
-    if (tid == 0) unit_off[E] = (int32_t)total;
+    uint32_t ru = 0, rg = 0;
+    const uint32_t tu = block_excl_scan(lu, ru, s_wtot);
+    const uint32_t tg = block_excl_scan(lg, rg, s_wtot);
+    for (int e = e0; e < e1; ++e) {
+        unit_off[e] = (int32_t)ru;
+        grp_off[e] = (int32_t)rg;
+        ru += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
+        rg += (uint32_t)groups_of_entry(seg_off, nlist, e);
+    }
+    if (tid == 0) {
+        unit_off[E] = (int32_t)tu;
+        grp_off[E] = (int32_t)tg;
+    }
 }
 
 // One thread per unit: locate its segment by binary search over unit_off, then its query block
 // and vector slice.  Slices start on 64-vector blocks and are never empty (n > 64 S (S - 1)
 // whenever S = ceil(n / kSplitVec) > 1).
+// Then one thread per weight group: {first pair, pair count}.
 __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
                                                         const int32_t* vec_off, int nlist,
                                                         const int32_t* unit_off, int M1,
-                                                        int4* units, int max_units) {
+                                                        int4* units, int max_units,
+                                                        const int32_t* grp_off, int2* groups,
+                                                        int max_groups) {
     const int E = 2 * nlist;
+    const int ngrp = min(grp_off[E], max_groups);
+    for (int gi = blockIdx.x * blockDim.x + threadIdx.x; gi < ngrp;
+         gi += gridDim.x * blockDim.x) {
+        int lo = 0, hi = E - 1;  // largest e with grp_off[e] <= gi
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (grp_off[mid] <= gi) lo = mid;
+            else hi = mid - 1;
+        }
+        const int p = lo >= nlist ? 1 : 0, c = lo - p * nlist;
+        const int32_t* so = seg_off + p * (nlist + 1);
+        const int k = gi - grp_off[lo];
+        groups[gi] = make_int2((p ? M1 : 0) + so[c] + k * kGroupQ,
+                               min(kGroupQ, so[c + 1] - so[c] - k * kGroupQ));
+    }
     const int total = min(unit_off[E], max_units);
     for (int u = blockIdx.x * blockDim.x + threadIdx.x; u < total; u += gridDim.x * blockDim.x) {
         int lo = 0, hi = E - 1;  // largest e with unit_off[e] <= u
@@ -209,8 +257,9 @@ __device__ __forceinline__ double sum16_f64(double v) {
 
 // Waves [0, nlist): per-cluster bounds of the f32 slack, A_max = 255^2 sum delta^2 (>= A_x,
 // codes <= 255) and r_max = 2 sqrt(sum eps^2) (>= r_x = |a| + |b| <= 2 |a + b| for the
-// non-negative per-dim error terms bounded by eps).  Waves [nlist, nlist + B): per-query
-// sum of qerr^2 (the rotation error of q_rot, squared).
+// non-negative per-dim error terms bounded by eps), and r_lo = the smallest stored r_x of the
+// cluster.  Waves [nlist, nlist + B): per-query sum of qerr^2 (the rotation error of q_rot,
+// squared).
 __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist, int B,
                                                          double* cbound, double* qep) {
     const int lane = threadIdx.x & 63;
@@ -226,9 +275,21 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
         }
         dd = wave_sum_f64(dd);
         ee = wave_sum_f64(ee);
+        float rlo = INFINITY;
+        const int vend = a.vec_off[wv + 1];
+        for (int v = a.vec_off[wv] + lane; v < vend; v += 4 * kWave) {  // 4 loads in flight
+            float r4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                r4[u] = v + u * kWave < vend ? a.vec_Ar[v + u * kWave].y : INFINITY;
+            rlo = fminf(rlo, fminf(fminf(r4[0], r4[1]), fminf(r4[2], r4[3])));
+        }
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) rlo = fminf(rlo, __shfl_xor(rlo, o, kWave));
         if (lane == 0) {
-            cbound[2 * wv] = 65025.0 * dd * (1.0 + 1e-12);
-            cbound[2 * wv + 1] = 2.0 * sqrt(ee) * (1.0 + 1e-12);
+            cbound[kCbStride * wv] = 65025.0 * dd * (1.0 + 1e-12);
+            cbound[kCbStride * wv + 1] = 2.0 * sqrt(ee) * (1.0 + 1e-12);
+            cbound[kCbStride * wv + 2] = rlo < INFINITY ? (double)rlo : 0.0;
         }
     } else if (wv < nlist + B) {
         const double* qe = a.qerr + (size_t)(wv - nlist) * D_pad;
@@ -239,18 +300,26 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
     }
 }
 
-// 16 lanes per grouped pair p (4 pairs per wave): the query's int8 weight planes against its
-// cluster's SQ8 grid and the pair's threshold-independent scalars.  Lane l owns dims
-// 64 k + 4 l + [0, 4) (coalesced 32-byte row pieces, one packed 32-bit store per plane).
-//   w_d = delta_d * (q_rot,d - vmin_d);  s = 2^(ilogb(max |w|) - 14), doubled if max|w|/s >
-//   32639, so |w_int| <= 32639;  w_int = rint(w / s) = 256 hi + lo  (hi, lo in [-128, 127]).
-// Plane bytes past D_pad (up to DP) are zero, so the scan may read whole 64-dim steps.
+// One weight group per workgroup (its <= 16 pairs share a cluster), 16 lanes per pair (wave w
+// takes pairs 4 w .. 4 w + 3): the queries' int8 weight planes against the cluster's SQ8 grid
+// and each pair's threshold-independent scalars.  Lane l owns dims 64 k + 4 l + [0, 4)
+// (coalesced 32-byte row pieces, one packed 32-bit store per plane).
+//   w_d = delta_d * (q_rot,d - vmin_d);  one scale for the group: s = 2^(ilogb(m) - 14),
+//   doubled if m / s > 32639, for m = the largest |w_d| of the group's pairs, so |w_int| <=
+//   32639;  w_int = rint(w / s) = 256 hi + lo  (hi, lo in [-128, 127]).
+// (A common scale lets the lower-bound scan compare a wave's 16 queries against one integer
+// threshold per vector.)  Plane bytes past D_pad (up to DP) are zero, so the scan may read
+// whole 64-dim steps.
 template <int KS>
 __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
+    __shared__ double s_mx[kGroupQ];
+    const int gi = blockIdx.x;
+    if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;
+    const int2 grp = a.groups[gi];
     const int lane = threadIdx.x & 63, l = lane & 15;
-    const int p = (blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6)) * 4 + (lane >> 4);
-    const bool valid = p < a.M;
-    const int pp = valid ? p : a.M - 1;  // out-of-range groups redo the last pair, store nothing
+    const int slot = (int)(threadIdx.x >> 6) * 4 + (lane >> 4);
+    const bool valid = slot < grp.y;
+    const int pp = grp.x + (valid ? slot : 0);  // idle slots redo the first pair, store nothing
     const int c = a.pair_cid[pp], q = a.pair_qid[pp];
     const int D_pad = a.D_pad, DP = a.DP;
     const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
@@ -278,6 +347,10 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
     Qp = sum16_f64(Qp);
+    if (l == 0) s_mx[slot] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kGroupQ; ++i) mx = fmax(mx, s_mx[i]);
     // s and 1/s are powers of two (|e| <= 1010 here), so w * (1/s) is exactly w / s
     int es = 0;
     if (mx > 0x1p-100) {
@@ -319,8 +392,8 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
         r.cW = 128.0 * (double)wsum;
         r.c1 = 2.0 * s;
-        r.a_max = a.cbound[2 * c];
-        r.r_max = a.cbound[2 * c + 1];
+        r.a_max = a.cbound[kCbStride * c];
+        r.r_max = a.cbound[kCbStride * c + 1];
         r.acc_max = 128.0 * (double)wabs;
         a.prec[pp] = r;
     }
@@ -363,30 +436,35 @@ __device__ __forceinline__ void merge16_groups(float (&m)[16]) {
     }
 }
 
-// A 64-vector code block in LDS: 16-byte cell rg * 64 + v holds vector v's codes of dims
-// 16 rg .. 16 rg + 15 (code rows 4 rg .. 4 rg + 3, one 32-bit row each) as c' = c - 128, so
-// the MFMA A operand of 64 dims is one 16-byte read.  Thread tid moves the cells of vector
-// tid & 63, row groups (tid >> 6) + 4 jj: four 4-byte loads, each coalesced over the wave (64
-// consecutive vectors of one code row).  D4 is a multiple of 8, so a row group is either
-// wholly inside D_pad or wholly past it (then zero).
-__device__ __forceinline__ uint4 cell_load(const uint32_t* base, int jj, int tid, int D4, int T) {
-    const int r0 = 4 * ((tid >> 6) + 4 * jj);
-    if (r0 >= D4) return make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-    const uint32_t* p = base + (size_t)r0 * T + (tid & 63);
-    return make_uint4(p[0], p[T], p[2 * T], p[3 * T]);
+// Integer lower-bound threshold of one vector for a wave: an int32 <= (A - r (r + 2 tq)) / c1
+// for the stored A (rounded down), r and tq (rounded up), computed in f32 with a margin m of
+// 2^-21 (A + y) / c1 + 1 over its three roundings (each <= 2^-24 of a term <= A + y); c1 is a
+// power of two, so the scaling is exact.  Out-of-range values saturate (a NaN from an
+// overflowed margin gives INT_MIN: every row passes); rows past the slice (r = +inf) get
+// INT_MAX, which acc + kq < 2^31 - 1 never reaches.
+__device__ __forceinline__ int lb_thr(float A, float r, float tq, float inv_c1) {
+    const float y = r * fmaf(2.0f, tq, r);
+    const float X = (A - y) * inv_c1;
+    const float m = fmaf(0x1p-21f * (A + y), inv_c1, 1.0f);
+    const float v = fminf(fmaxf(floorf(X - m), -2147483648.0f), 2147483520.0f);
+    return r <= 3.0e38f ? (int)v : INT_MAX;
 }
 
-__device__ __forceinline__ void cell_store(uint4* blk, uint4 c, int jj, int tid) {
-    blk[((tid >> 6) + 4 * jj) * kBlkV + (tid & 63)] =
-        make_uint4(c.x ^ 0x80808080u, c.y ^ 0x80808080u, c.z ^ 0x80808080u, c.w ^ 0x80808080u);
-}
-
+// (The lower-bound pass at KS <= 2 is held to 5 waves per SIMD: the compiler's own choice of
+// registers gives 4, and the scan is latency-bound.)
 template <bool UB_PASS, int KS>
-__global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_scan_kernel(
+    BatchArgs a) {
     constexpr int kRows = KS * 16;  // code rows (4 dims each) held per block buffer
     __shared__ uint4 s_codes[2][kRows * kBlkV / 4];
     __shared__ __align__(16) float2 s_ar[2][kBlkV];
+    __shared__ __align__(16) int s_thr[UB_PASS ? 1 : 2][UB_PASS ? 1 : kWavesPerBlock]
+                                      [UB_PASS ? 4 : kBlkV];
     __shared__ float s_ubl[UB_PASS ? kWavesPerBlock : 1][UB_PASS ? kWaveQ * kWave : 1];
+    constexpr int kLbW = UB_PASS ? 1 : kWavesPerBlock;  // per-wave survivor queues (pass B)
+    __shared__ uint32_t s_sq[kLbW][UB_PASS ? 1 : kSurvQ];
+    __shared__ int s_scnt[kLbW][kWaveQ], s_sbase[kLbW][kWaveQ], s_sqid[kLbW][kWaveQ];
     __shared__ int s_unit[2];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -397,8 +475,11 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
     const int xcd = (int)(blockIdx.x & 7);
     const int rb = xcd * nx, re = min(total, rb + nx);
     int32_t* ctr = a.ctr + xcd * kCtrStride;
-    const int D_pad = a.D_pad, D4 = D_pad >> 2, T = a.T;
+    const int D_pad = a.D_pad, T = a.T;
     unsigned long long st_cand = 0, st_surv = 0;
+    if constexpr (!UB_PASS) {
+        if (lane < kWaveQ) s_scnt[wid][lane] = 0;
+    }
 
     for (int it = 0;; ++it) {
         // (s_unit alternates: slot it & 1 is rewritten two barriers after everyone read it)
@@ -424,6 +505,12 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         v4i bhi[KS], blo[KS];
         double e_q = 0.0, c1 = 0.0, cW = 0.0, AQ = 0.0;
         float c1f = 0.0f, c2f = 0.0f, H32 = INFINITY;  // no threshold: every row passes
+        // integer test (lower-bound pass): kq of this lane's query, the wave's largest tq
+        // (rounded up) and 1 / c1 of its weight group
+        int kq = 0;
+        float tqw = 0.0f, inv_c1w = 0.0f;
+        double tq_l = 0.0, Kd = 0.0, mg = 0.0;
+        bool lane_int = true;
         if (active) {
             // Prepared by pair_prep_kernel: lane (j, g) takes bytes [ks*64 + g*16, +16) of
             // query j's planes and the pair's scalars.
@@ -464,16 +551,80 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                     H32 = __double2float_ru(H + slack);
                     c1f = (float)c1;
                     c2f = -__double2float_ru(2.0 * tq);
+                    tq_l = tq;
+                    Kd = cW + G / c1;  // G / c1 is exact: c1 is a power of two
+                    mg = 0x1p-50 * (fabs(Kd) + (2.0 * err_q + Qp + tq * tq) / c1);
+                    tqw = __double2float_ru(tq);
+                } else {
+                    lane_int = false;  // no threshold: every row passes (float test only)
                 }
             }
-            if (!hasq) H32 = -INFINITY;  // lane has no query: nothing survives
+            if (!hasq) {
+                H32 = -INFINITY;  // lane has no query: nothing survives
+                lane_int = true;
+            }
         }
+        // Integer form of the lower-bound test, exact in int32 (see the tile epilogue):
+        //   acc + kq >= thr_x,   thr_x <= (A_lo - r (r + 2 tq_w)) / c1   (per vector),
+        //   kq >= cW + G / c1 - 2 (tq_w - tq) r_lo / c1                 (per query),
+        // with tq_w the wave's largest tq and r_lo <= r_x over the cluster.  Since
+        // A - r^2 - 2 tq r >= A - r (r + 2 tq_w) + 2 (tq_w - tq) r_lo, the exact condition
+        // implies it.  mg covers the roundings of G and of the sums.  The wave takes the integer
+        // test iff every lane can: |kq| <= 2^30 (with |acc| < 2^30, acc + kq cannot overflow),
+        // every query has a threshold and all share one c1.
+        const double c1_0 = shfl_f64(c1, 0);
+        bool int_ok = !UB_PASS && active && __ballot(!lane_int || (hasq && c1 != c1_0)) == 0ull;
+        const uint64_t qmask = __ballot(hasq);
+        if (int_ok) {
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) tqw = fmaxf(tqw, __shfl_xor(tqw, o, kWave));
+            inv_c1w = (float)(1.0 / c1_0);  // a power of two in [2^-100, 2^100]: exact
+            const double r_lo = a.cbound[kCbStride * cid + 2];
+            const double corr = 2.0 * ((double)tqw - tq_l) * r_lo / c1_0 * (1.0 - 0x1p-50);
+            const double kd = ceil(Kd - corr + (mg + 0x1p-50 * fabs(corr)));
+            const bool ok = fabs(kd) <= 0x1p30 && c1_0 >= 0x1p-100 && c1_0 <= 0x1p100;
+            kq = hasq ? (int)(ok ? kd : 0.0) : -0x40000000;
+            int_ok = __ballot(hasq && !ok) == 0ull;
+        }
+        if (!int_ok) kq = 0;
 
         float ubl[kUbList];
         if constexpr (UB_PASS) {
 #pragma unroll
             for (int i = 0; i < kUbList; ++i) ubl[i] = INFINITY;
         }
+
+        // Lower-bound survivors wait in the wave's LDS queue (entries li << 4 | query slot) and
+        // are appended to the candidate lists here: one atomic per query of the wave reserves
+        // its slots, then every entry takes the next slot of its query.  Wave-local: LDS
+        // operations of one wave complete in order.
+        int nsq = 0;
+        if constexpr (!UB_PASS) {
+            if (active && lane < kWaveQ) s_sqid[wid][lane] = q;
+        }
+        auto flush = [&]() {
+            if constexpr (!UB_PASS) {
+                for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 15u], 1);
+                __builtin_amdgcn_wave_barrier();
+                if (lane < kWaveQ) {
+                    const int c = s_scnt[wid][lane];
+                    s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[q], c) : 0;
+                    s_scnt[wid][lane] = 0;
+                }
+                __builtin_amdgcn_wave_barrier();
+                for (int e = lane; e < nsq; e += kWave) {
+                    const uint32_t ent = s_sq[wid][e];
+                    const int jj = (int)(ent & 15u);
+                    const int slot = s_sbase[wid][jj] + atomicAdd(&s_scnt[wid][jj], 1);
+                    if (slot < a.cap)
+                        a.cand_id[(size_t)s_sqid[wid][jj] * a.cap + slot] = v0 + (int)(ent >> 4);
+                }
+                __builtin_amdgcn_wave_barrier();
+                if (lane < kWaveQ) s_scnt[wid][lane] = 0;
+                if (a.stats) st_surv += (unsigned long long)nsq;
+                nsq = 0;
+            }
+        };
 
         // ---- one 16-vector tile of the block in LDS buffer buf ----
         auto tile = [&](int buf, int t, int li0) {
@@ -486,7 +637,12 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                 const uint4 v = blk[(ks * 4 + g) * kBlkV + t * 16 + j];
                 A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
-            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+            // lower-bound pass: integer thresholds of rows 4g .. 4g + 3 (read ahead of the MFMAs)
+            int4 th = make_int4(0, 0, 0, 0);
+            if constexpr (!UB_PASS)
+                th = *reinterpret_cast<const int4*>(&s_thr[buf][wid][t * 16 + 4 * g]);
+            // the lower-bound pass starts the lo sums at kq (0 on the float test)
+            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {kq, kq, kq, kq};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
@@ -500,20 +656,26 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("s_nop 7\n\ts_nop 7");
             __builtin_amdgcn_sched_barrier(0);
-            // per-row scalars: (P = A_lo - r^2, r) in the lower-bound pass, (A_lo, r) in the
-            // upper-bound pass; rows past the slice hold (NaN, +inf), which neither test accepts
-            const float4 ar01 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g]);
-            const float4 ar23 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g + 2]);
-            const float Ar[4][2] = {{ar01.x, ar01.y}, {ar01.z, ar01.w}, {ar23.x, ar23.y},
-                                    {ar23.z, ar23.w}};
-            // epilogue: rows 4g + r (vectors), column j (query); the lower-bound pass keeps
-            // each row's survivors as the wave mask its compare produces
-            uint64_t sm[4] = {0ull, 0ull, 0ull, 0ull};
+            // epilogue: rows 4g + r (vectors), column j (query).  S = acc + kq, exact in int32
+            // (|acc| <= 128 * 256 * 32639 < 2^30, |kq| <= 2^30).
+            int S[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int acc = (acc_hi[r] << 8) + acc_lo[r];
-                if constexpr (UB_PASS) {
-                    const double dot = (double)acc + cW;
+            for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
+            // per-row scalars: (P = A_lo - r^2, r) in the lower-bound pass, (A_lo, r) in the
+            // upper-bound pass; rows past the slice hold (NaN, +inf), which no test accepts
+            auto row_scalars = [&](float (&Ar)[4][2]) {
+                const float4 ar01 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g]);
+                const float4 ar23 =
+                    *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g + 2]);
+                Ar[0][0] = ar01.x; Ar[0][1] = ar01.y; Ar[1][0] = ar01.z; Ar[1][1] = ar01.w;
+                Ar[2][0] = ar23.x; Ar[2][1] = ar23.y; Ar[3][0] = ar23.z; Ar[3][1] = ar23.w;
+            };
+            if constexpr (UB_PASS) {
+                float Ar[4][2];
+                row_scalars(Ar);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const double dot = (double)S[r] + cW;
                     const double Alo = (double)Ar[r][0], rr = (double)Ar[r][1];
                     const double E = fmax(fma(-c1, dot, Alo * (1.0 + 0x1p-22) + AQ), 0.0);
                     const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
@@ -524,63 +686,98 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
                             ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
                         ubl[0] = fminf(ubl[0], u);
                     }
+                }
+            } else {
+                // Survivor masks, one per row.  Integer test: acc + kq >= thr_x.  It and the
+                // float test are both implied by the exact lower-bound condition (thr_x uses
+                // the wave's largest tq and rounds down, kq rounds up; the float test carries
+                // its slack), so a row passing both is kept and no true survivor is lost.
+                uint64_t sm[4];
+                if (int_ok) {
+                    sm[0] = __ballot(S[0] >= th.x);
+                    sm[1] = __ballot(S[1] >= th.y);
+                    sm[2] = __ballot(S[2] >= th.z);
+                    sm[3] = __ballot(S[3] >= th.w);
                 } else {
                     // lanes without a query have H32 = -inf; a query with no threshold has
                     // c1f = c2f = 0, H32 = +inf
-                    const float L = fmaf(c2f, Ar[r][1], Ar[r][0]);
-                    const float Rv = fmaf(c1f, (float)acc, H32);
-                    sm[r] = __ballot(L <= Rv);
+                    float Ar[4][2];
+                    row_scalars(Ar);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        sm[r] = __ballot(fmaf(c2f, Ar[r][1], Ar[r][0]) <=
+                                         fmaf(c1f, (float)S[r], H32));
                 }
-            }
-            if constexpr (!UB_PASS) {
-                if ((sm[0] | sm[1] | sm[2] | sm[3]) == 0ull) return;
-                // rare: append survivors (sorted position) to the query's list
+                if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
+                // rare: the per-query float test
+                //   fma(c2, r, P) <= fma(c1, float(acc), H32),  acc = S - kq,
+                // then queue survivors (cluster index, query slot) in the wave's LDS queue
+                float Ar[4][2];
+                row_scalars(Ar);
+                if (nsq > kSurvQ - 4 * kWave) flush();
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    if ((sm[r] >> lane) & 1ull) {
-                        const int slot = atomicAdd(&a.cand_cnt[q], 1);
-                        if (slot < a.cap) a.cand_id[(size_t)q * a.cap + slot] = v0 + li0 + 4 * g + r;
+                    const bool pass = hasq && ((sm[r] >> lane) & 1ull) &&
+                                      fmaf(c2f, Ar[r][1], Ar[r][0]) <=
+                                          fmaf(c1f, (float)(S[r] - kq), H32);
+                    const uint64_t pm = __ballot(pass);
+                    if (pass) {
+                        const int idx = __builtin_amdgcn_mbcnt_hi(
+                            (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
+                        s_sq[wid][nsq + idx] = ((uint32_t)(li0 + 4 * g + r) << 4) | (uint32_t)j;
                     }
-                }
-                if (a.stats) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) st_surv += __popcll(sm[r]);
+                    nsq += __popcll(pm);
                 }
             }
         };
 
         // ---- stream the slice through LDS in 64-vector blocks ----
-        // A block never crosses a T-tile (T and the block starts are multiples of 64).
+        // A block is 64 slots of one T-tile (T and the block starts are multiples of 64): its
+        // cells (g, slot).  LDS cell g * 64 + v holds vector v's codes of dims 16 g .. 16 g + 15
+        // (already c - 128), so the MFMA A operand of 64 dims is one 16-byte read.  Thread tid
+        // moves vector tid & 63's cells g = (tid >> 6) + 4 jj: one 16-byte load each, 1 KiB
+        // contiguous per wave.  Cells past D_pad are not loaded: their weights are zero.
         // (The staging values are separate scalars filled by value: an array captured by
         // reference lands in scratch memory and serialises every load.)
         uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
         float2 st_ar = make_float2(0.0f, 0.0f);
-        const uint32_t* sq8_c = a.sq8 + (size_t)t0 * D4 * T;  // cluster's first tile
+        const int G16 = D_pad >> 4, g0 = wid;
+        const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
+        int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
         auto gload = [&](int blk0) {
-            const int ct = blk0 / T, cw = blk0 - ct * T;
-            const uint32_t* base = sq8_c + (size_t)ct * D4 * T + cw;
-            st0 = cell_load(base, 0, tid, D4, T);
-            if constexpr (KS > 1) st1 = cell_load(base, 1, tid, D4, T);
-            if constexpr (KS > 2) st2 = cell_load(base, 2, tid, D4, T);
-            if constexpr (KS > 3) st3 = cell_load(base, 3, tid, D4, T);
-            if (tid < kBlkV) {
-                const int li = blk0 + tid;
-                if (li < ve) {
-                    const float2 ar = a.vec_Ar[v0 + li];
-                    // lower-bound pass keeps P = A_lo - r^2 (its f32 rounding is inside the
-                    // slack), upper-bound pass keeps A_lo
-                    st_ar = UB_PASS ? ar : make_float2(fmaf(-ar.y, ar.y, ar.x), ar.y);
-                } else {
-                    st_ar = make_float2(__int_as_float(0x7fc00000), INFINITY);
-                }
+            // wave-uniform base, lane offset added per load
+            const uint4* base = cells_c + ((size_t)ct * G16 + g0) * T + cw;
+            if (g0 < G16) st0 = base[lane];
+            if constexpr (KS > 1) if (g0 + 4 < G16) st1 = (base + (size_t)4 * T)[lane];
+            if constexpr (KS > 2) if (g0 + 8 < G16) st2 = (base + (size_t)8 * T)[lane];
+            if constexpr (KS > 3) if (g0 + 12 < G16) st3 = (base + (size_t)12 * T)[lane];
+            cw += kBlkV;
+            if (cw == T) {
+                cw = 0;
+                ++ct;
+            }
+            // (A_lo, r) of row blk0 + lane: wave 0 publishes the rows' scalars, and each wave
+            // on the integer test derives its own thresholds from them
+            if (tid < kBlkV || int_ok) {
+                const int li = blk0 + lane;
+                st_ar = li < ve ? a.vec_Ar[v0 + li]
+                                : make_float2(__int_as_float(0x7fc00000), INFINITY);
             }
         };
         auto lstore = [&](int buf) {
-            cell_store(s_codes[buf], st0, 0, tid);
-            if constexpr (KS > 1) cell_store(s_codes[buf], st1, 1, tid);
-            if constexpr (KS > 2) cell_store(s_codes[buf], st2, 2, tid);
-            if constexpr (KS > 3) cell_store(s_codes[buf], st3, 3, tid);
-            if (tid < kBlkV) s_ar[buf][tid] = st_ar;
+            uint4* blk = s_codes[buf] + g0 * kBlkV + lane;
+            if (g0 < G16) blk[0] = st0;
+            if constexpr (KS > 1) if (g0 + 4 < G16) blk[4 * kBlkV] = st1;
+            if constexpr (KS > 2) if (g0 + 8 < G16) blk[8 * kBlkV] = st2;
+            if constexpr (KS > 3) if (g0 + 12 < G16) blk[12 * kBlkV] = st3;
+            // lower-bound pass keeps P = A_lo - r^2 (its f32 rounding is inside the float
+            // test's slack), upper-bound pass keeps A_lo
+            if (tid < kBlkV)
+                s_ar[buf][tid] =
+                    UB_PASS ? st_ar : make_float2(fmaf(-st_ar.y, st_ar.y, st_ar.x), st_ar.y);
+            if constexpr (!UB_PASS) {
+                if (int_ok) s_thr[buf][wid][lane] = lb_thr(st_ar.x, st_ar.y, tqw, inv_c1w);
+            }
         };
         const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
         if (nblk > 0) gload(vb);
@@ -599,6 +796,7 @@ __global__ __launch_bounds__(256) void batch_scan_kernel(BatchArgs a) {
         }
         if (a.stats && active && rr == 0)
             st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
+        if (nsq > 0) flush();
 
         if constexpr (UB_PASS) {
             // K-th smallest upper bound of each query -> atomicMin into tau[q] (float64 bit

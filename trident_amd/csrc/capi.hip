@@ -86,9 +86,12 @@ struct Workspace {
     int32_t* unit_off;               // [2 * nlist + 1]
     int32_t* unit_ctr;               // [2, 8 * kCtrStride] per-launch, per-XCD counters
     int64_t max_units;
+    int2* groups;                    // [max_groups] batched-route weight groups
+    int32_t* grp_off;                // [2 * nlist + 1]
+    int64_t max_groups;
     int8_t* pw;                      // [B * nprobe, 2, DP] batched-route weight planes
     PairRec* prec;                   // [B * nprobe]
-    double* cbound;                  // [nlist, 2]
+    double* cbound;                  // [nlist, kCbStride]
     double* qep;                     // [B]
     size_t bytes;
 };
@@ -129,9 +132,12 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.units = c.take<int4>(w.max_units);
     w.unit_off = c.take<int32_t>(2 * (int64_t)ix->nlist + 1);
     w.unit_ctr = c.take<int32_t>(2 * 8 * kCtrStride);
+    w.max_groups = max_groups_of(B * nprobe, ix->nlist);
+    w.groups = c.take<int2>(w.max_groups);
+    w.grp_off = c.take<int32_t>(2 * (int64_t)ix->nlist + 1);
     w.pw = c.take<int8_t>(B * nprobe * 2 * plane_bytes(ix->D_pad));
     w.prec = c.take<PairRec>(B * nprobe);
-    w.cbound = c.take<double>(2 * (int64_t)ix->nlist);
+    w.cbound = c.take<double>(kCbStride * (int64_t)ix->nlist);
     w.qep = c.take<double>(B);
     w.bytes = c.off;
     return w;
@@ -228,12 +234,15 @@ int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
 }
 
 // Route of a mode-2 search.  The batched route needs the per-vector scalars, K <= 64 (its
-// upper-bound seeding keeps 16 bounds per lane, 64 per query) and D_pad <= 256 (query
-// weights held in registers); AUTO takes it when clusters are shared by >= 8 queries on
-// average, where the contraction is dense enough for the matrix cores.
+// upper-bound seeding keeps 16 bounds per lane, 64 per query), D_pad <= 256 (query weights
+// held in registers) and N < 2^27 (a queued survivor packs its index within the cluster
+// into 28 bits); AUTO takes it when clusters are shared by >= 8 queries on average, where
+// the contraction is dense enough for the matrix cores.
 int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                  int nprobe, int* route) {
-    const bool ok = ix->vec_Ar && ix->orig_ids_sorted && K <= 64 && ix->D_pad <= 256 &&
+    const bool ok = ix->vec_Ar && ix->sq8_cells && ix->orig_ids_sorted && K <= 64 &&
+                    ix->D_pad <= 256 &&
+                    ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
         case TRIDENT_ROUTE_PAIR:
@@ -242,8 +251,10 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
         case TRIDENT_ROUTE_BATCHED:
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
-                            "batched route needs vec_Ar, K <= 64 and D_pad <= 256 (K=%d, D_pad=%d)",
-                            K, ix->D_pad);
+                            "batched route needs vec_Ar, sq8_cells, K <= 64, D_pad <= 256 and "
+                            "N < 2^27 "
+                            "(K=%d, D_pad=%d, N=%d)",
+                            K, ix->D_pad, ix->N);
             *route = TRIDENT_ROUTE_BATCHED;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_AUTO:
@@ -286,8 +297,8 @@ int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
 
 int launch_pair_prep(const BatchArgs& b, hipStream_t st) {
     if (b.M <= 0) return TRIDENT_OK;
-    const int per_block = 4 * kWavesPerBlock;  // 16 lanes per pair
-    const unsigned grid = (unsigned)((b.M + per_block - 1) / per_block);
+    static_assert(kGroupQ == 4 * kWavesPerBlock, "one weight group per workgroup, 16 lanes a pair");
+    const unsigned grid = (unsigned)b.max_groups;  // blocks past the group count return
     switch (b.DP / 64) {
         case 1: pair_prep_kernel<1><<<grid, kBlock, 0, st>>>(b); break;
         case 2: pair_prep_kernel<2><<<grid, kBlock, 0, st>>>(b); break;
@@ -580,7 +591,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if (cascade && (rc = choose_route(ix, sp, B, K, nprobe, &route))) return rc;
     if (route == TRIDENT_ROUTE_BATCHED) {
         BatchArgs b{};
-        b.sq8 = ix->sq8_packed;
+        b.cells = reinterpret_cast<const uint4*>(ix->sq8_cells);
         b.tile_oids = ix->tile_orig_ids;
         b.tile_off = ix->cluster_tile_off;
         b.vec_off = ix->cluster_vec_off;
@@ -617,17 +628,22 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.prec = w.prec;
         b.cbound = w.cbound;
         b.qep = w.qep;
+        b.nlist = ix->nlist;
+        b.groups = w.groups;
+        b.grp_off = w.grp_off;
+        b.max_groups = (int)w.max_groups;
         aux_bounds_kernel<<<(unsigned)((ix->nlist + B + kWavesPerBlock - 1) / kWavesPerBlock),
                             kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep);
         if ((rc = check_launch("aux_bounds_kernel"))) return rc;
-        if ((rc = launch_pair_prep(b, st))) return rc;
         unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
-                                               w.unit_off);
+                                               w.unit_off, w.grp_off);
         if ((rc = check_launch("unit_scan_kernel"))) return rc;
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, w.unit_off, (int)M1,
-                                 w.units, (int)w.max_units);
+                                 w.units, (int)w.max_units, w.grp_off, w.groups,
+                                 (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
+        if ((rc = launch_pair_prep(b, st))) return rc;
         fill_u64_kernel<<<(unsigned)std::min<int64_t>((B + 255) / 256, 4096), 256, 0, st>>>(
             reinterpret_cast<unsigned long long*>(w.tau64), 0x7ff0000000000000ull, B);
         if ((rc = check_launch("fill_u64_kernel"))) return rc;

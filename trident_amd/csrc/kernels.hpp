@@ -79,7 +79,7 @@ struct PairRec {
 
 // Everything one cluster-batched scan launch reads (csrc/batch.hip).
 struct BatchArgs {
-    const uint32_t* sq8;
+    const uint4* cells;         // [tiles, D_pad / 16, T] 16-byte code cells, bytes c ^ 0x80
     const int32_t* tile_oids;
     const int32_t* tile_off;
     const int32_t* vec_off;
@@ -101,10 +101,14 @@ struct BatchArgs {
     const int32_t* pair_qid;    // pass-1 pairs then pass-2 pairs
     const int32_t* pair_cid;
     int M;                      // pairs (both passes)
+    int nlist;
+    const int2* groups;        // weight groups {first pair, pair count}
+    const int32_t* grp_off;     // [2 * nlist + 1]; grp_off[2 * nlist] = number of groups
+    int max_groups;
     int DP;                     // 64 * ceil(D_pad / 64): bytes per weight plane
     int8_t* pw;                 // [M, 2, DP] int8 weight planes (hi, lo), natural dim order
     PairRec* prec;              // [M]
-    const double* cbound;       // [nlist, 2] (A_max, r_max) per cluster
+    const double* cbound;       // [nlist, kCbStride] (A_max, r_max, r_lo) per cluster
     const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
     uint64_t* cand_key;
@@ -191,15 +195,27 @@ constexpr int kSplitVec = 1024;
 constexpr int kMaxSplit = 8;
 constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
 
+// Weight groups: the 16 consecutive pairs of a segment that one wave scans together share one
+// weight scale (pairs 16 k .. 16 k + 15 of the segment; units start on such boundaries).
+constexpr int kGroupQ = 16;
+constexpr int kCbStride = 4;  // doubles per cluster in the per-cluster bound table
+// Survivors a lower-bound wave queues in LDS before appending them to the candidate lists.
+constexpr int kSurvQ = 512;
+
 inline int64_t max_units_of(int64_t pairs, int64_t nlist) {
     return (int64_t)kMaxSplit * ((pairs + kUnitQ - 1) / kUnitQ + 2 * nlist);
 }
 
+inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
+    return (pairs + kGroupQ - 1) / kGroupQ + 2 * nlist;
+}
+
 __global__ void unit_scan_kernel(const int32_t* seg_off, const int32_t* vec_off, int nlist,
-                                 int32_t* unit_off);
+                                 int32_t* unit_off, int32_t* grp_off);
 
 __global__ void unit_fill_kernel(const int32_t* seg_off, const int32_t* vec_off, int nlist,
-                                 const int32_t* unit_off, int M1, int4* units, int max_units);
+                                 const int32_t* unit_off, int M1, int4* units, int max_units,
+                                 const int32_t* grp_off, int2* groups, int max_groups);
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
 

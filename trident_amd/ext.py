@@ -105,7 +105,7 @@ def release_workspaces() -> None:
 def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combined, b_combined,
                     rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
-                    eps_dim, blk_bounds4, vec_Ar=None) -> TridentIndexView:
+                    eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -125,6 +125,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.vmin, v.delta, v.eps_dim = _ptr(vmin), _ptr(delta), _ptr(eps_dim)
     v.blk_bounds4 = _ptr(blk_bounds4)
     v.vec_Ar = _ptr(vec_Ar)
+    v.sq8_cells = _ptr(sq8_cells)
     return v
 
 
@@ -187,6 +188,7 @@ def launch_trident_v4_search(
     warp_refine=1, stats_buf=None, r_vec_sorted=None,
     *, ub_seed: Optional[int] = None, rot_sq_bounds=None, p_init: int = -1, stage_events=None,
     vec_Ar: Optional[torch.Tensor] = None, route: int = 0,
+    sq8_cells: Optional[torch.Tensor] = None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -236,6 +238,10 @@ def launch_trident_v4_search(
     if vec_Ar is not None:
         _check_tensor("vec_Ar", vec_Ar, torch.float32, dev, 2)
         _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float32")
+    if sq8_cells is not None:
+        _check_tensor("sq8_cells", sq8_cells, torch.int32, dev)
+        _need(sq8_cells.numel() == tiles * (D_pad // 16) * int(tile_size) * 4,
+              "sq8_cells must hold [tiles, D_pad/16, tile_size, 4] words")
     if stats_buf is not None:
         _check_tensor("stats_buf", stats_buf, torch.int64, dev)
         _need(stats_buf.numel() >= 4, "stats_buf needs 4 entries")
@@ -261,7 +267,8 @@ def launch_trident_v4_search(
         cluster_tile_off=cluster_tile_off, cluster_vec_off=cluster_vec_off, xb_sorted=xb_sorted,
         orig_ids_sorted=orig_ids_sorted, vmin=vmin if mode == 2 else None,
         delta=delta if mode == 2 else None, eps_dim=eps_dim if mode == 2 else None,
-        blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None)
+        blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
+        sq8_cells=sq8_cells if mode == 2 else None)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route, probe_cids=probe_cids_buf,

@@ -131,6 +131,8 @@ class TridentV4Index:
       sq8_packed   int32 [tiles, D_pad/4, T]: word [t, d4, s] packs dims 4*d4..4*d4+3 of slot
                    s of tile t, byte 0 = dim 4*d4 (reference packing :221-228); for T = 64 a
                    wave's 64 lanes read one contiguous 256-byte row per d4.
+      sq8_cells    int32 [tiles, D_pad/16, T, 4]: the same codes as 16-byte cells (16 dims of
+                   one slot), bytes XOR 0x80 -- the batched route's matrix-core operand layout.
       tile_orig_ids int32 [tiles, T] (-1 padded), tile_r_minmax f32 [tiles, 2]
       cluster_tile_off int32 [nlist + 1]; vmin / delta / eps_pad f32 [nlist or 1, D_pad]
       blk_bounds4  int32 [nb + 1] (32-dim blocks, or the variable scheme of :233-247)
@@ -270,7 +272,15 @@ class TridentV4Index:
             g = codes32[safe[ts:te]]                         # [nt, T, D4]
             g = torch.where(valid[ts:te].unsqueeze(-1), g, torch.zeros_like(g))
             self.sq8_packed[ts:te] = g.permute(0, 2, 1)
-        self.tile_r_minmax = torch.zeros((tiles, 2), device=dev, dtype=torch.float32)
+        # Batched-route copy: 16-byte cells, cell (t, g, s) = dims 16 g .. 16 g + 15 of slot s
+        # (words 4 g .. 4 g + 3 of sq8_packed[t, :, s]), every byte c stored as c ^ 0x80.
+        G16 = D_pad // 16
+        self.sq8_cells = torch.empty((tiles, G16, T, 4), device=dev, dtype=torch.int32)
+        flip = torch.tensor(-0x7f7f7f80, dtype=torch.int32, device=dev)  # 0x80808080
+        for ts in range(0, tiles, tstep):
+            te = min(tiles, ts + tstep)
+            self.sq8_cells[ts:te] = self.sq8_packed[ts:te].view(te - ts, G16, 4, T).permute(0, 1, 3, 2) ^ flip
+        self.tile_r_minmax =torch.zeros((tiles, 2), device=dev, dtype=torch.float32)
         if storage.r_vec_sorted is not None:
             r = storage.r_vec_sorted.to(dev)[safe]
             self.tile_r_minmax[:, 0] = torch.where(valid, r, torch.full_like(r, math.inf)).amin(1)
@@ -362,7 +372,7 @@ class TridentV4Index:
             self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
             bool(record_kernel_ms), int(warp_refine), stats_buf,
             ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events,
-            vec_Ar=self.vec_Ar, route=route)
+            vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells)
         return topk_d, topk_i, kern_ms
 
     def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
@@ -375,7 +385,8 @@ class TridentV4Index:
             tile_orig_ids=self.tile_orig_ids, tile_r_minmax=self.tile_r_minmax,
             cluster_tile_off=self.cluster_tile_off, cluster_vec_off=st.cluster_vec_off,
             xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
-            delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar)
+            delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
+            sq8_cells=self.sq8_cells)
         r = _lib.lib().trident_route_for(ctypes.byref(view), int(B), int(k or self.k), int(nprobe), int(route))
         if r < 0:
             _lib.check(-r, "trident_route_for")
