@@ -106,6 +106,18 @@ def test_batched_large_clusters_split_into_slices(dev, K):
         assert_exact(d, i, rd, ri, f"slices K={K} nprobe={nprobe}")
 
 
+def test_batched_many_units_per_workgroup(dev):
+    """~200k (query, probe) pairs in 256 clusters: thousands of work units, several per
+    persistent workgroup, so every workgroup hands the next unit's index to its waves through
+    LDS between units (a wave reading a stale index would scan the wrong unit)."""
+    xb, xq = datagen.cfg2(N=100_000, D=128, B=4096, n_centers=256, seed=27)
+    b = build_index(xb, 256, dev, max_batch=4096)
+    for rep in range(2):
+        _, rd, ri = oracle_search(b, xq.numpy(), 48, 10)
+        d, i = run_search(b, _q(xq.numpy(), dev), 48, 10, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"many units rep={rep}")
+
+
 def test_batched_rejects_unsupported_k(sets, dev):
     from trident_amd._lib import TridentError
     b, xq = sets["hist"]

@@ -481,12 +481,19 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
         if (lane < kWaveQ) s_scnt[wid][lane] = 0;
     }
 
+    // The next unit's counter value is taken two blocks before the current unit ends (its
+    // latency hides behind them) and published in s_unit at the end of the unit.  Slot
+    // (it + 1) & 1 is written at the end of unit it, after every wave read it at the start of
+    // unit it - 1 (the barrier at the top of unit it separates the two).
+    // The explicit LDS wait before the barrier keeps lane 0's s_unit write ahead of the other
+    // waves' reads (the compiler's own wait was missing on the loop's back edge).
+    if (tid == 0) s_unit[0] = atomicAdd(ctr, 1);
     for (int it = 0;; ++it) {
-        // (s_unit alternates: slot it & 1 is rewritten two barriers after everyone read it)
-        if (tid == 0) s_unit[it & 1] = atomicAdd(ctr, 1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
         const int ui = __builtin_amdgcn_readfirstlane(s_unit[it & 1]) + rb;
-        if (ui >= re) break;
+        if (ui < rb || ui >= re) break;
+        int nxt = 0;  // wave 0, lane 0: the next unit's counter value
         const int4 un = a.units[ui];
         const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
         // The unit's queries form G groups of <= 16; each group gets R = 4 / G waves, which
@@ -741,6 +748,7 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
         // reference lands in scratch memory and serialises every load.)
         uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
         float2 st_ar = make_float2(0.0f, 0.0f);
+        bool st_row_ok = false;
         const int G16 = D_pad >> 4, g0 = wid;
         const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
         int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
@@ -757,11 +765,12 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
                 ++ct;
             }
             // (A_lo, r) of row blk0 + lane: wave 0 publishes the rows' scalars, and each wave
-            // on the integer test derives its own thresholds from them
+            // on the integer test derives its own thresholds from them.  The load is
+            // unconditional (clamped row; ve > vb) so that nothing waits for it here; rows past
+            // the slice are replaced when stored.
             if (tid < kBlkV || int_ok) {
-                const int li = blk0 + lane;
-                st_ar = li < ve ? a.vec_Ar[v0 + li]
-                                : make_float2(__int_as_float(0x7fc00000), INFINITY);
+                st_row_ok = blk0 + lane < ve;
+                st_ar = a.vec_Ar[v0 + min(blk0 + lane, ve - 1)];
             }
         };
         auto lstore = [&](int buf) {
@@ -771,7 +780,8 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
             if constexpr (KS > 2) if (g0 + 8 < G16) blk[8 * kBlkV] = st2;
             if constexpr (KS > 3) if (g0 + 12 < G16) blk[12 * kBlkV] = st3;
             // lower-bound pass keeps P = A_lo - r^2 (its f32 rounding is inside the float
-            // test's slack), upper-bound pass keeps A_lo
+            // test's slack), upper-bound pass keeps A_lo; rows past the slice hold (NaN, +inf)
+            if (!st_row_ok) st_ar = make_float2(__int_as_float(0x7fc00000), INFINITY);
             if (tid < kBlkV)
                 s_ar[buf][tid] =
                     UB_PASS ? st_ar : make_float2(fmaf(-st_ar.y, st_ar.y, st_ar.x), st_ar.y);
@@ -785,6 +795,7 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
             const int buf = b & 1;
             lstore(buf);
             __syncthreads();
+            if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
             if (b + 1 < nblk) gload(vb + (b + 1) * kBlkV);
             if (active) {
                 const int blk0 = vb + b * kBlkV;
@@ -862,6 +873,7 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
                 }
             }
         }
+        if (tid == 0) s_unit[(it + 1) & 1] = nblk > 0 ? nxt : atomicAdd(ctr, 1);
     }
 
     if (a.stats && lane == 0) {
