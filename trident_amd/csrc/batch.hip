@@ -43,6 +43,8 @@
 // bytes of dims step*64 + g*16 + [0, 16): vector i's codes in the A operand and query i's
 // weights in the B operand (any dim-to-byte assignment shared by A and B computes the same
 // contraction); the result row 4g + r, column i sits in lane l, register r.
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -634,7 +636,10 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
         };
 
         // ---- one 16-vector tile of the block in LDS buffer buf ----
-        auto tile = [&](int buf, int t, int li0) {
+        // INT selects the lower-bound pass's integer test (a wave-uniform mode, so each mode gets
+        // its own loop rather than a branch per tile).
+        auto tile = [&](auto int_c, int buf, int t, int li0) {
+            constexpr bool INT = decltype(int_c)::value;
             // A operand: lane (i = j, g) reads vector 16t + i's 16 code bytes of dims
             // ks*64 + g*16 + [0, 16) (row group ks*4 + g), already offset to c' = c - 128.
             const uint4* blk = s_codes[buf];
@@ -700,7 +705,7 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
                 // the wave's largest tq and rounds down, kq rounds up; the float test carries
                 // its slack), so a row passing both is kept and no true survivor is lost.
                 uint64_t sm[4];
-                if (int_ok) {
+                if constexpr (INT) {
                     sm[0] = __ballot(S[0] >= th.x);
                     sm[1] = __ballot(S[1] >= th.y);
                     sm[2] = __ballot(S[2] >= th.z);
@@ -799,9 +804,18 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
             if (b + 1 < nblk) gload(vb + (b + 1) * kBlkV);
             if (active) {
                 const int blk0 = vb + b * kBlkV;
-                for (int t = rr; t < kBlkV / 16; t += R) {
-                    if (blk0 + t * 16 >= ve) break;
-                    tile(buf, t, blk0 + t * 16);
+                auto tiles = [&](auto int_c) {
+                    for (int t = rr; t < kBlkV / 16; t += R) {
+                        if (blk0 + t * 16 >= ve) break;
+                        tile(int_c, buf, t, blk0 + t * 16);
+                    }
+                };
+                if constexpr (UB_PASS) {
+                    tiles(std::false_type{});
+                } else if (int_ok) {
+                    tiles(std::true_type{});
+                } else {
+                    tiles(std::false_type{});
                 }
             }
         }
@@ -892,6 +906,332 @@ template __global__ void batch_scan_kernel<false, 1>(BatchArgs);
 template __global__ void batch_scan_kernel<false, 2>(BatchArgs);
 template __global__ void batch_scan_kernel<false, 3>(BatchArgs);
 template __global__ void batch_scan_kernel<false, 4>(BatchArgs);
+
+// ---------------------------------------------------------------------------------------------
+// Lower-bound pass.
+//
+// lb_prep_kernel: one 16-lane group per weight group, one lane per pair, after the seeding pass.
+// For pair (q, c) with t_q = sqrt(tau_q * rot_sq_max) (1 + 1e-12) + e_q the lower-bound
+// condition is (norm form against sqrt(tau) scaled to the rotated space)
+//     A - r^2 - 2 t_q r  <=  c1 (acc + cW) + G,   G = 2 err - Q + t_q^2,  c1 = 2 s,
+// with acc = sum (c - 128) w_int (exact int32).  Two forms of it are prepared:
+//   float:   fma(c2f, r, P) <= fma(c1f, float(acc), H32), P = A_lo - r^2 in float32,
+//            c2f <= -2 t_q, H32 >= c1 cW + G + slack; each of the 4 f32 roundings is at most
+//            2^-24 of a term bounded by X = A_max + r_max^2 + 2 t_q r_max + c1 acc_max + |H|
+//            (A_max = 255^2 sum delta^2, r_max = 2 sqrt(sum eps^2), acc_max = 128 sum |w_int|),
+//            so slack = 2^-22 X covers them all;
+//   integer: acc + kq >= thr_x with thr_x <= (A_lo - r (r + 2 t_w)) / c1 per vector (t_w the
+//            group's largest t_q) and kq >= cW + G / c1 - 2 (t_w - t_q) r_lo / c1 (r_lo <= r_x
+//            over the cluster): A - r^2 - 2 t_q r >= A - r (r + 2 t_w) + 2 (t_w - t_q) r_lo.
+//            G / c1 is exact (c1 is a power of two); mg covers the roundings of G and of the
+//            sums.  The group takes it iff every query has a threshold, all share c1 and
+//            |kq| <= 2^30 (with |acc| < 2^30 the int32 sum cannot overflow).
+__global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, slot = tid & 15;
+    const int gi = blockIdx.x * (kBlock / kGroupQ) + (tid >> 4);
+    if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;  // whole 16-lane groups
+    const int2 grp = a.groups[gi];
+    const bool valid = slot < grp.y;
+    const int p = grp.x + (valid ? slot : 0);
+    const int q = a.pair_qid[p], c = a.pair_cid[p];
+    const PairRec pr = a.prec[p];
+    const double Qp = pr.Qp, err_q = pr.err_q, cW = pr.cW, c1 = pr.c1;
+    const double tq = sqrt(a.tau[q] * a.rot_sq_max) * (1.0 + 1e-12) + pr.e_q;
+    const bool thr = tq < 1e30;
+    LbRec L;
+    L.kq = 0;
+    L.c1f = 0.0f;
+    L.c2f = 0.0f;
+    L.H32 = INFINITY;  // no threshold: every row passes
+    double Kd = 0.0, mg = 0.0;
+    float tqf = 0.0f;
+    if (thr) {
+        const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
+        const double H = c1 * cW + G;
+        const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max + c1 * pr.acc_max +
+                         fabs(H);
+        const double slack = 0x1p-22 * X * (1.0 + 1e-6) + 1e-30;
+        L.H32 = __double2float_ru(H + slack);
+        L.c1f = (float)c1;
+        L.c2f = -__double2float_ru(2.0 * tq);
+        Kd = cW + G / c1;
+        mg = 0x1p-50 * (fabs(Kd) + (2.0 * err_q + Qp + tq * tq) / c1);
+        tqf = __double2float_ru(tq);
+    }
+    // group reductions over the 16 lanes of this weight group
+    const double c1_0 = shfl_f64(c1, lane & ~15);
+    int bad = valid && (!thr || c1 != c1_0);
+    float tqw = valid ? tqf : 0.0f;
+#pragma unroll
+    for (int o = 1; o < kGroupQ; o <<= 1) {
+        bad |= __shfl_xor(bad, o, kWave);
+        tqw = fmaxf(tqw, __shfl_xor(tqw, o, kWave));
+    }
+    bool ok = !bad && c1_0 >= 0x1p-100 && c1_0 <= 0x1p100;
+    if (ok && valid) {
+        const double r_lo = a.cbound[kCbStride * c + 2];
+        const double corr = 2.0 * ((double)tqw - tq) * r_lo / c1_0 * (1.0 - 0x1p-50);
+        const double kd = ceil(Kd - corr + (mg + 0x1p-50 * fabs(corr)));
+        if (fabs(kd) <= 0x1p30) L.kq = (int)kd;
+        else ok = false;
+    }
+    int nok = valid && !ok;
+#pragma unroll
+    for (int o = 1; o < kGroupQ; o <<= 1) nok |= __shfl_xor(nok, o, kWave);
+    L.int_ok = !nok;
+    L.tqw = tqw;
+    L.inv_c1w = L.int_ok ? (float)(1.0 / c1_0) : 0.0f;  // a power of two in [2^-100, 2^100]
+    L.pad = 0;
+    if (valid) a.lbr[p] = L;
+}
+
+// Global -> LDS without registers: lane i's 16 (or 4) bytes land at lds + 16 i (4 i).
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// Pass B, every probe: units and wave mapping as in batch_scan_kernel.  Block b + 1's code
+// cells and row scalars (A_lo, r) move global -> LDS directly (no staging registers) while the
+// waves scan block b; each wave on the integer test turns the row scalars into its own int32
+// thresholds.  Survivors are queued per wave in LDS and appended with one atomic per query and
+// flush.
+template <int KS>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 6 : 1)))
+void lb_scan_kernel(BatchArgs a) {
+    __shared__ uint4 s_codes[2][KS * 4 * kBlkV];
+    __shared__ __align__(16) float s_A[2][kBlkV];
+    __shared__ __align__(16) float s_r[2][kBlkV];
+    __shared__ __align__(16) int s_thr[2][kWavesPerBlock][kBlkV];
+    __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
+    __shared__ int s_scnt[kWavesPerBlock][kWaveQ], s_sbase[kWavesPerBlock][kWaveQ],
+        s_sqid[kWavesPerBlock][kWaveQ];
+    __shared__ int s_unit[2];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, g = lane >> 4;
+    const int total = min(a.unit_off[a.unit_end], a.max_units);
+    const int nx = (total + 7) >> 3;
+    const int xcd = (int)(blockIdx.x & 7);
+    const int rb = xcd * nx, re = min(total, rb + nx);
+    int32_t* ctr = a.ctr + xcd * kCtrStride;
+    const int T = a.T, G16 = a.D_pad >> 4;
+    unsigned long long st_cand = 0, st_surv = 0;
+    if (lane < kWaveQ) s_scnt[wid][lane] = 0;
+
+    // Next unit's counter value: taken two blocks before the current unit ends, published in
+    // s_unit at its end (slot (it + 1) & 1, read at the start of unit it + 1; its previous read,
+    // at the start of unit it - 1, is separated from the write by the barrier at the top of
+    // unit it).  The explicit LDS wait keeps that write ahead of the barrier.
+    if (tid == 0) s_unit[0] = atomicAdd(ctr, 1);
+    for (int it = 0;; ++it) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int ui = __builtin_amdgcn_readfirstlane(s_unit[it & 1]) + rb;
+        if (ui < rb || ui >= re) break;
+        int nxt = 0;
+        const int4 un = a.units[ui];
+        const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
+        const int G = (cnt + kWaveQ - 1) / kWaveQ;
+        const int R = kWavesPerBlock / G;
+        const int gq = wid / R, rr = wid - gq * R;
+        const bool active = gq < G;
+        const int nq = active ? min(kWaveQ, cnt - gq * kWaveQ) : 0;
+        const bool hasq = j < nq;
+        const int v0 = a.vec_off[cid];
+        const int t0 = a.tile_off[cid];
+
+        // ---- this wave's queries: weight planes and the constants of lb_prep_kernel ----
+        v4i bhi[KS], blo[KS];
+        int q = 0, kq = 0;
+        float c1f = 0.0f, c2f = 0.0f, H32 = -INFINITY;  // lanes without a query: nothing passes
+        bool int_ok = false;
+        float tqw = 0.0f, inv_c1w = 0.0f;
+        if (active) {
+            const int pj = start + gq * kWaveQ + (hasq ? j : 0);
+            q = a.pair_qid[pj];
+            const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
+                blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
+            }
+            const LbRec L = a.lbr[pj];
+            int_ok = __builtin_amdgcn_readfirstlane(L.int_ok) != 0;  // lane 0 has a query
+            tqw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L.tqw)));
+            inv_c1w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L.inv_c1w)));
+            if (hasq) {
+                kq = int_ok ? L.kq : 0;
+                c1f = L.c1f;
+                c2f = L.c2f;
+                H32 = L.H32;
+            } else {
+                kq = int_ok ? -0x40000000 : 0;
+            }
+        }
+        const uint64_t qmask = __ballot(hasq);
+        if (active && lane < kWaveQ) s_sqid[wid][lane] = q;
+
+        // ---- survivor queue (entries li << 4 | query slot) ----
+        int nsq = 0;
+        auto flush = [&]() {
+            for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 15u], 1);
+            __builtin_amdgcn_wave_barrier();
+            if (lane < kWaveQ) {
+                const int c = s_scnt[wid][lane];
+                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[q], c) : 0;
+                s_scnt[wid][lane] = 0;
+            }
+            __builtin_amdgcn_wave_barrier();
+            for (int e = lane; e < nsq; e += kWave) {
+                const uint32_t ent = s_sq[wid][e];
+                const int jj = (int)(ent & 15u);
+                const int slot = s_sbase[wid][jj] + atomicAdd(&s_scnt[wid][jj], 1);
+                if (slot < a.cap)
+                    a.cand_id[(size_t)s_sqid[wid][jj] * a.cap + slot] = v0 + (int)(ent >> 4);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane < kWaveQ) s_scnt[wid][lane] = 0;
+            if (a.stats) st_surv += (unsigned long long)nsq;
+            nsq = 0;
+        };
+
+        // ---- one 16-vector tile: INT = the integer test (wave-uniform mode) ----
+        auto tile = [&](auto int_c, int buf, int t, int li0) {
+            constexpr bool INT = decltype(int_c)::value;
+            const uint4* blk = s_codes[buf];
+            v4i A[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint4 v = blk[(ks * 4 + g) * kBlkV + t * 16 + j];
+                A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+            int4 th = make_int4(0, 0, 0, 0);
+            if constexpr (INT) th = *reinterpret_cast<const int4*>(&s_thr[buf][wid][t * 16 + 4 * g]);
+            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {kq, kq, kq, kq};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
+                acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
+            }
+            // The matrix core does not interlock VALU reads of its results: 16 wait states (plus
+            // the compiler's own padding) between the last MFMA and the first accumulator read,
+            // fenced so that the scheduler cannot move either side across.
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7\n\ts_nop 7");
+            __builtin_amdgcn_sched_barrier(0);
+            // rows 4g + r (vectors), column j (query): S = acc + kq, exact in int32
+            int S[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
+            const int row0 = t * 16 + 4 * g;
+            uint64_t sm[4];
+            if constexpr (INT) {
+                sm[0] = __ballot(S[0] >= th.x);
+                sm[1] = __ballot(S[1] >= th.y);
+                sm[2] = __ballot(S[2] >= th.z);
+                sm[3] = __ballot(S[3] >= th.w);
+            } else {
+                const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
+                const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
+                const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sm[r] = __ballot(li0 + 4 * g + r < ve &&
+                                     fmaf(c2f, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
+                                         fmaf(c1f, (float)S[r], H32));
+            }
+            if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
+            // rare: the float test for the integer test's passes (rows past the slice never
+            // pass the integer test: thr = INT_MAX), then queue the survivors
+            const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
+            const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
+            const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool pass = hasq && ((sm[r] >> lane) & 1ull) &&
+                                  fmaf(c2f, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
+                                      fmaf(c1f, (float)(S[r] - kq), H32);
+                const uint64_t pm = __ballot(pass);
+                if (nsq + __popcll(pm) > kLbQ) flush();
+                if (pass) {
+                    const int idx = __builtin_amdgcn_mbcnt_hi(
+                        (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
+                    s_sq[wid][nsq + idx] = ((uint32_t)(li0 + 4 * g + r) << 4) | (uint32_t)j;
+                }
+                nsq += __popcll(pm);
+            }
+        };
+
+        // ---- stream the slice through LDS in 64-vector blocks (as batch_scan_kernel) ----
+        const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
+        int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
+        auto gload = [&](int buf, int blk0) {
+            const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
+#pragma unroll
+            for (int jj = 0; jj < KS; ++jj)
+                if (wid + 4 * jj < G16)
+                    load_lds16(base + (size_t)(4 * jj) * T + lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
+            cw += kBlkV;
+            if (cw == T) {
+                cw = 0;
+                ++ct;
+            }
+            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
+                const float* ar = reinterpret_cast<const float*>(a.vec_Ar + v0 + min(blk0 + lane, ve - 1));
+                load_lds4(ar, s_A[buf]);
+                load_lds4(ar + 1, s_r[buf]);
+            }
+        };
+        const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
+        if (nblk > 0) gload(0, vb);
+        for (int b = 0; b < nblk; ++b) {
+            const int buf = b & 1;
+            // this wave's direct loads of block b have landed; the barrier covers everyone's
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+            const int blk0 = vb + b * kBlkV;
+            if (b + 1 < nblk) gload(buf ^ 1, blk0 + kBlkV);
+            if (active) {
+                if (int_ok) {
+                    const float A = s_A[buf][lane], r = s_r[buf][lane];
+                    s_thr[buf][wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                    for (int t = rr; t < kBlkV / 16; t += R) {
+                        if (blk0 + t * 16 >= ve) break;
+                        tile(std::true_type{}, buf, t, blk0 + t * 16);
+                    }
+                } else {
+                    for (int t = rr; t < kBlkV / 16; t += R) {
+                        if (blk0 + t * 16 >= ve) break;
+                        tile(std::false_type{}, buf, t, blk0 + t * 16);
+                    }
+                }
+            }
+        }
+        if (a.stats && active && rr == 0)
+            st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
+        if (nsq > 0) flush();
+        if (tid == 0) s_unit[(it + 1) & 1] = nblk > 0 ? nxt : atomicAdd(ctr, 1);
+    }
+
+    if (a.stats && lane == 0) {
+        const int slot = (int)(blockIdx.x % kStatSlots) * 4;
+        atomicAdd(&a.stats[slot + 0], st_cand);
+        atomicAdd(&a.stats[slot + 1], st_cand * (unsigned long long)(a.D_pad));
+        atomicAdd(&a.stats[slot + 2], st_surv);
+    }
+}
+
+template __global__ void lb_scan_kernel<1>(BatchArgs);
+template __global__ void lb_scan_kernel<2>(BatchArgs);
+template __global__ void lb_scan_kernel<3>(BatchArgs);
+template __global__ void lb_scan_kernel<4>(BatchArgs);
 
 // tau_sq output of the batched route: the seeded float64 threshold, rounded up to float32.
 __global__ void tau_to_f32_kernel(const double* tau, float* out, int B) {

@@ -91,6 +91,7 @@ struct Workspace {
     int64_t max_groups;
     int8_t* pw;                      // [B * nprobe, 2, DP] batched-route weight planes
     PairRec* prec;                   // [B * nprobe]
+    LbRec* lbr;                      // [B * nprobe]
     double* cbound;                  // [nlist, kCbStride]
     double* qep;                     // [B]
     size_t bytes;
@@ -137,6 +138,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.grp_off = c.take<int32_t>(2 * (int64_t)ix->nlist + 1);
     w.pw = c.take<int8_t>(B * nprobe * 2 * plane_bytes(ix->D_pad));
     w.prec = c.take<PairRec>(B * nprobe);
+    w.lbr = c.take<LbRec>(B * nprobe);
     w.cbound = c.take<double>(kCbStride * (int64_t)ix->nlist);
     w.qep = c.take<double>(B);
     w.bytes = c.off;
@@ -270,6 +272,12 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
 // the occupancy its registers and LDS allow), rounded to a multiple of 8 so every XCD gets the
 // same number; cached per device and variant.
 template <bool UB, int KS>
+const void* batch_kernel_ptr() {
+    if constexpr (UB) return reinterpret_cast<const void*>(&batch_scan_kernel<true, KS>);
+    else return reinterpret_cast<const void*>(&lb_scan_kernel<KS>);
+}
+
+template <bool UB, int KS>
 unsigned persistent_grid() {
     static int cached[64] = {0};
     int dev = 0;
@@ -279,9 +287,8 @@ unsigned persistent_grid() {
         if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             cu < 1)
             cu = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &per_cu, reinterpret_cast<const void*>(&batch_scan_kernel<UB, KS>), kBlock, 0) !=
-                hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, batch_kernel_ptr<UB, KS>(), kBlock,
+                                                         0) != hipSuccess ||
             per_cu < 1)
             per_cu = 2;
         cached[dev] = std::max(8, ((cu * per_cu + 7) / 8) * 8);
@@ -289,10 +296,16 @@ unsigned persistent_grid() {
     return (unsigned)cached[dev];
 }
 
+// Upper-bound pass: batch_scan_kernel<true>; lower-bound pass: lb_scan_kernel.
 template <bool UB, int KS>
 int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
-    batch_scan_kernel<UB, KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
-    return check_launch("batch_scan_kernel");
+    if constexpr (UB) {
+        batch_scan_kernel<true, KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
+        return check_launch("batch_scan_kernel");
+    } else {
+        lb_scan_kernel<KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
+        return check_launch("lb_scan_kernel");
+    }
 }
 
 int launch_pair_prep(const BatchArgs& b, hipStream_t st) {
@@ -626,6 +639,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.DP = (int)plane_bytes(ix->D_pad);
         b.pw = w.pw;
         b.prec = w.prec;
+        b.lbr = w.lbr;
         b.cbound = w.cbound;
         b.qep = w.qep;
         b.nlist = ix->nlist;
@@ -660,6 +674,9 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
+        lb_prep_kernel<<<(unsigned)((w.max_groups + kBlock / kGroupQ - 1) / (kBlock / kGroupQ)),
+                         kBlock, 0, st>>>(b);
+        if ((rc = check_launch("lb_prep_kernel"))) return rc;
         // pass B over every probe: lower bound, exact refine, append <= tau
         b.unit_end = 2 * ix->nlist;
         b.ctr = w.unit_ctr + 8 * kCtrStride;

@@ -77,6 +77,18 @@ struct PairRec {
     double acc_max;  // >= |sum c'_d w_int,d|
 };
 
+// Per-pair constants of the batched lower-bound scan (they depend on tau, so they are computed
+// after the seeding pass).  int_ok, tqw and inv_c1w are shared by the pair's weight group.
+struct LbRec {
+    int32_t kq;        // integer test: acc + kq >= thr_x
+    float c1f, c2f;    // float test: fma(c2f, r, P) <= fma(c1f, float(acc), H32)
+    float H32;
+    float tqw;         // the group's largest tq, rounded up
+    float inv_c1w;     // 1 / c1 of the group (a power of two)
+    int32_t int_ok;    // the group takes the integer test
+    int32_t pad;
+};
+
 // Everything one cluster-batched scan launch reads (csrc/batch.hip).
 struct BatchArgs {
     const uint4* cells;         // [tiles, D_pad / 16, T] 16-byte code cells, bytes c ^ 0x80
@@ -108,6 +120,7 @@ struct BatchArgs {
     int DP;                     // 64 * ceil(D_pad / 64): bytes per weight plane
     int8_t* pw;                 // [M, 2, DP] int8 weight planes (hi, lo), natural dim order
     PairRec* prec;              // [M]
+    LbRec* lbr;                 // [M]
     const double* cbound;       // [nlist, kCbStride] (A_max, r_max, r_lo) per cluster
     const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
@@ -223,6 +236,14 @@ __global__ void tau_to_f32_kernel(const double* tau, float* out, int B);
 
 template <bool UB_PASS, int KS>
 __global__ void batch_scan_kernel(BatchArgs a);
+
+// Survivors a wave of lb_scan_kernel queues in LDS before appending them.
+constexpr int kLbQ = 128;
+
+__global__ void lb_prep_kernel(BatchArgs a);
+
+template <int KS>
+__global__ void lb_scan_kernel(BatchArgs a);
 
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
 
