@@ -1001,7 +1001,7 @@ __device__ __forceinline__ void load_lds4(const void* g, void* lds) {
 // thresholds.  Survivors are queued per wave in LDS and appended with one atomic per query and
 // flush.
 template <int KS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 6 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 7 : 1)))
 void lb_scan_kernel(BatchArgs a) {
     __shared__ uint4 s_codes[2][KS * 4 * kBlkV];
     __shared__ __align__(16) float s_A[2][kBlkV];
@@ -1010,6 +1010,7 @@ void lb_scan_kernel(BatchArgs a) {
     __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
     __shared__ int s_scnt[kWavesPerBlock][kWaveQ], s_sbase[kWavesPerBlock][kWaveQ],
         s_sqid[kWavesPerBlock][kWaveQ];
+    __shared__ float4 s_qf[kWavesPerBlock][kWaveQ];  // per query slot: (c1f, c2f, H32, -)
     __shared__ int s_unit[2];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1049,7 +1050,7 @@ void lb_scan_kernel(BatchArgs a) {
         // ---- this wave's queries: weight planes and the constants of lb_prep_kernel ----
         v4i bhi[KS], blo[KS];
         int q = 0, kq = 0;
-        float c1f = 0.0f, c2f = 0.0f, H32 = -INFINITY;  // lanes without a query: nothing passes
+        float4 qf = make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // no query: nothing passes
         bool int_ok = false;
         float tqw = 0.0f, inv_c1w = 0.0f;
         if (active) {
@@ -1067,15 +1068,17 @@ void lb_scan_kernel(BatchArgs a) {
             inv_c1w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L.inv_c1w)));
             if (hasq) {
                 kq = int_ok ? L.kq : 0;
-                c1f = L.c1f;
-                c2f = L.c2f;
-                H32 = L.H32;
+                qf = make_float4(L.c1f, L.c2f, L.H32, 0.0f);
             } else {
                 kq = int_ok ? -0x40000000 : 0;
             }
         }
         const uint64_t qmask = __ballot(hasq);
-        if (active && lane < kWaveQ) s_sqid[wid][lane] = q;
+        // the float test's constants and the query ids wait in LDS for the rare path and flush
+        if (active && lane < kWaveQ) {
+            s_sqid[wid][lane] = q;
+            s_qf[wid][lane] = qf;
+        }
 
         // ---- survivor queue (entries li << 4 | query slot) ----
         int nsq = 0;
@@ -1084,7 +1087,7 @@ void lb_scan_kernel(BatchArgs a) {
             __builtin_amdgcn_wave_barrier();
             if (lane < kWaveQ) {
                 const int c = s_scnt[wid][lane];
-                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[q], c) : 0;
+                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[s_sqid[wid][lane]], c) : 0;
                 s_scnt[wid][lane] = 0;
             }
             __builtin_amdgcn_wave_barrier();
@@ -1140,11 +1143,12 @@ void lb_scan_kernel(BatchArgs a) {
                 const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
                 const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
                 const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+                const float4 c = s_qf[wid][j];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
                     sm[r] = __ballot(li0 + 4 * g + r < ve &&
-                                     fmaf(c2f, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
-                                         fmaf(c1f, (float)S[r], H32));
+                                     fmaf(c.y, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
+                                         fmaf(c.x, (float)S[r], c.z));
             }
             if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
             // rare: the float test for the integer test's passes (rows past the slice never
@@ -1152,11 +1156,12 @@ void lb_scan_kernel(BatchArgs a) {
             const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
             const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
             const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+            const float4 c = s_qf[wid][j];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const bool pass = hasq && ((sm[r] >> lane) & 1ull) &&
-                                  fmaf(c2f, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
-                                      fmaf(c1f, (float)(S[r] - kq), H32);
+                                  fmaf(c.y, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
+                                      fmaf(c.x, (float)(S[r] - kq), c.z);
                 const uint64_t pm = __ballot(pass);
                 if (nsq + __popcll(pm) > kLbQ) flush();
                 if (pass) {

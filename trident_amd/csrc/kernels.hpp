@@ -238,7 +238,7 @@ template <bool UB_PASS, int KS>
 __global__ void batch_scan_kernel(BatchArgs a);
 
 // Survivors a wave of lb_scan_kernel queues in LDS before appending them.
-constexpr int kLbQ = 128;
+constexpr int kLbQ = 64;
 
 __global__ void lb_prep_kernel(BatchArgs a);
 
