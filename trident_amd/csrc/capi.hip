@@ -356,13 +356,16 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                   hipStream_t st) {
     const int ldw = ix->nlist + ix->D_pad;
     const int cols = std::max(ix->D, rotate ? ix->D_pad : 0);
-    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 3) / 4), dim3(64, 4), 0, st>>>(
+    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
+                          dim3(64, 4), 0, st>>>(
         xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
         w.xrot64, w.qerr, rotate ? 1 : 0);
     int rc = check_launch("prep_queries_kernel");
     if (rc) return rc;
     constexpr int qpb = kCoarseQW * kWavesPerBlock;
-    coarse_dist_kernel<<<dim3((ix->nlist + 63) / 64, (B + qpb - 1) / qpb), kBlock, 0, st>>>(
+    coarse_dist_kernel<<<dim3((ix->nlist + 64 * kCoarseNC - 1) / (64 * kCoarseNC),
+                                 (B + qpb - 1) / qpb),
+                            kBlock, 0, st>>>(
         w.xq64, B, ix->D, ix->W_combined, ldw, ix->nlist, w.cd64);
     if ((rc = check_launch("coarse_dist_kernel"))) return rc;
     if (nprobe <= 128) {  // one wave per query, register list
@@ -771,7 +774,8 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int ldw = ix->nlist + ix->D_pad;
     const int cols = std::max(ix->D, ix->D_pad);
-    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 3) / 4), dim3(64, 4), 0, st>>>(
+    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
+                          dim3(64, 4), 0, st>>>(
         xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
         w.xrot64, w.qerr, 1);
     if ((rc = check_launch("prep_queries_kernel"))) return rc;

@@ -19,84 +19,126 @@ __global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n) {
         p[i] = v;
 }
 
-// grid (ceil(max(D, D_pad) / 64), ceil(B / 4)), block (64, 4).
+// grid (ceil(max(D, D_pad) / 64), ceil(B / (4 kPrepQB))), block (64, 4): each wave takes
+// kPrepQB queries (wave-uniform rows, scalar loads) x 64 columns, so every loaded rotation value
+// feeds kPrepQB chains.
 // xq64[b, d] = (double)xq[b, d]; xrot64[b, j] = sum_d xq[b, d] * R[d, j] + bvec[j] evaluated
 // in float64 (fma, dimension order) and qerr[b, j] bounds its distance from the exact value.
 __global__ __launch_bounds__(256) void prep_queries_kernel(
     const float* __restrict__ xq, int B, int D, int D_pad, const float* __restrict__ W, int ldw,
     int nlist, const float* __restrict__ bvec, double* __restrict__ xq64,
     double* __restrict__ xrot64, double* __restrict__ qerr, int do_rot) {
+    constexpr int QB = kPrepQB;
     const int j = blockIdx.x * 64 + threadIdx.x;
-    const int b = blockIdx.y * 4 + threadIdx.y;
-    if (b >= B) return;
-    const float* qr = xq + (size_t)b * D;
-    if (j < D) xq64[(size_t)b * D + j] = (double)qr[j];
+    const int b0 = (blockIdx.y * 4 + threadIdx.y) * QB;
+    if (b0 >= B) return;
+    const float* qr[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) qr[i] = xq + (size_t)min(b0 + i, B - 1) * D;
+    if (j < D) {
+#pragma unroll
+        for (int i = 0; i < QB; ++i)
+            if (b0 + i < B) xq64[(size_t)(b0 + i) * D + j] = (double)qr[i][j];
+    }
     if (!do_rot || j >= D_pad) return;
-    double acc = 0.0, mag = 0.0;
+    double acc[QB], mag[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) acc[i] = mag[i] = 0.0;
     const float* wcol = W + nlist + j;
-#pragma unroll 8
+#pragma unroll 4
     for (int d = 0; d < D; ++d) {
-        const double qd = (double)qr[d];
         const double r = (double)wcol[(size_t)d * ldw];
-        acc = fma(qd, r, acc);
-        mag += fabs(qd * r);
+#pragma unroll
+        for (int i = 0; i < QB; ++i) {
+            const double qd = (double)qr[i][d];
+            acc[i] = fma(qd, r, acc[i]);
+            mag[i] += fabs(qd * r);
+        }
     }
     const double bj = (double)bvec[nlist + j];
-    acc += bj;
-    xrot64[(size_t)b * D_pad + j] = acc;
-    // |fl(sum) - sum| <= (D + 1) 2^-53 sum|terms|; doubled to also cover the rounding of `mag`.
-    qerr[(size_t)b * D_pad + j] = (double)(D + 3) * 0x1p-52 * (mag + fabs(bj)) + 0x1p-1000;
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+        if (b0 + i >= B) break;
+        xrot64[(size_t)(b0 + i) * D_pad + j] = acc[i] + bj;
+        // |fl(sum) - sum| <= (D + 1) 2^-53 sum|terms|; doubled to also cover the rounding of
+        // `mag`.
+        qerr[(size_t)(b0 + i) * D_pad + j] =
+            (double)(D + 3) * 0x1p-52 * (mag[i] + fabs(bj)) + 0x1p-1000;
+    }
 }
 
-// grid (ceil(nlist / 64), ceil(B / (kCoarseQW * 4))), block 256: each wave owns 64 centroids
-// (one per lane) x kCoarseQW queries; query values are wave-uniform (scalar loads, two dims at
-// a time when the rows allow it).  Centroid c, dim d is -0.5f * W[d, c], exact because
-// W_coarse_only = -2 C^T.  Each (query, centroid) sum is one fma chain in dimension order.
+// grid (ceil(nlist / (64 kCoarseNC)), ceil(B / (kCoarseQW * 4))), block 256: each wave owns
+// kCoarseQW queries x 64 kCoarseNC centroids, each lane kCoarseNC centroids (c = base + lane +
+// 64 k) x kCoarseQW queries in registers.  Query values are wave-uniform (scalar loads, two
+// dims at a time when the rows allow it), so every loaded value feeds kCoarseNC (queries) or
+// kCoarseQW (centroids) fma chains.  Centroid c, dim d is -0.5f * W[d, c], exact because
+// W_coarse_only = -2 C^T.  Each (query, centroid) sum is one fma chain in dimension order:
+// t = q_d - c_d, acc = fma(t, t, acc).
 __global__ __launch_bounds__(256) void coarse_dist_kernel(const double* __restrict__ xq64, int B,
                                                           int D, const float* __restrict__ W,
                                                           int ldw, int nlist,
                                                           double* __restrict__ cd64) {
-    constexpr int QW = kCoarseQW;
+    constexpr int QW = kCoarseQW, NC = kCoarseNC;
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int c = blockIdx.x * 64 + lane;
+    const int c0 = blockIdx.x * (64 * NC) + lane;
     const int qb = blockIdx.y * (QW * kWavesPerBlock) + wid * QW;
     if (qb >= B) return;
-    const int cc = c < nlist ? c : nlist - 1;
     const double* qrow[QW];
 #pragma unroll
     for (int i = 0; i < QW; ++i) qrow[i] = xq64 + (size_t)min(qb + i, B - 1) * D;
-    double acc[QW];
+    const float* wc[NC];
 #pragma unroll
-    for (int i = 0; i < QW; ++i) acc[i] = 0.0;
-    const float* wc = W + cc;
+    for (int k = 0; k < NC; ++k) wc[k] = W + min(c0 + 64 * k, nlist - 1);
+    double acc[QW][NC];
+#pragma unroll
+    for (int i = 0; i < QW; ++i)
+#pragma unroll
+        for (int k = 0; k < NC; ++k) acc[i][k] = 0.0;
     int d = 0;
     if ((D & 1) == 0) {  // rows are 16-byte aligned: xq64 is 256-byte aligned, D even
         for (; d < D; d += 2) {
-            const double cv0 = (double)(-0.5f * wc[(size_t)d * ldw]);
-            const double cv1 = (double)(-0.5f * wc[(size_t)(d + 1) * ldw]);
+            double cv0[NC], cv1[NC];
+#pragma unroll
+            for (int k = 0; k < NC; ++k) {
+                cv0[k] = (double)(-0.5f * wc[k][(size_t)d * ldw]);
+                cv1[k] = (double)(-0.5f * wc[k][(size_t)(d + 1) * ldw]);
+            }
 #pragma unroll
             for (int i = 0; i < QW; ++i) {
                 const double2 qv = *reinterpret_cast<const double2*>(qrow[i] + d);
-                double t = qv.x - cv0;
-                acc[i] = fma(t, t, acc[i]);
-                t = qv.y - cv1;
-                acc[i] = fma(t, t, acc[i]);
+#pragma unroll
+                for (int k = 0; k < NC; ++k) {
+                    double t = qv.x - cv0[k];
+                    acc[i][k] = fma(t, t, acc[i][k]);
+                    t = qv.y - cv1[k];
+                    acc[i][k] = fma(t, t, acc[i][k]);
+                }
             }
         }
     }
     for (; d < D; ++d) {
-        const double cv = (double)(-0.5f * wc[(size_t)d * ldw]);
+        double cv[NC];
+#pragma unroll
+        for (int k = 0; k < NC; ++k) cv[k] = (double)(-0.5f * wc[k][(size_t)d * ldw]);
 #pragma unroll
         for (int i = 0; i < QW; ++i) {
-            const double t = qrow[i][d] - cv;
-            acc[i] = fma(t, t, acc[i]);
+            const double qv = qrow[i][d];
+#pragma unroll
+            for (int k = 0; k < NC; ++k) {
+                const double t = qv - cv[k];
+                acc[i][k] = fma(t, t, acc[i][k]);
+            }
         }
     }
-    if (c < nlist) {
 #pragma unroll
-        for (int i = 0; i < QW; ++i)
-            if (qb + i < B) cd64[(size_t)(qb + i) * nlist + c] = acc[i];
+    for (int k = 0; k < NC; ++k) {
+        const int c = c0 + 64 * k;
+        if (c < nlist) {
+#pragma unroll
+            for (int i = 0; i < QW; ++i)
+                if (qb + i < B) cd64[(size_t)(qb + i) * nlist + c] = acc[i][k];
+        }
     }
 }
 

@@ -175,7 +175,9 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs);
 
 constexpr int kGroupChunk = 8192;  // (query, probe) entries per block of the LDS grouping
-constexpr int kCoarseQW = 16;      // queries per wave of coarse_dist_kernel
+constexpr int kCoarseQW = 4;       // queries per wave of coarse_dist_kernel
+constexpr int kCoarseNC = 2;       // centroids per lane of coarse_dist_kernel
+constexpr int kPrepQB = 2;         // queries per wave of prep_queries_kernel
 
 // Dynamic LDS bytes of the LDS grouping kernels; they are used while this is <= 64 KiB.
 inline size_t group_lds_bytes(int nlist) { return (size_t)2 * (nlist + 1) * sizeof(int32_t); }
