@@ -305,16 +305,19 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
 // One weight group per workgroup (its <= 16 pairs share a cluster), 16 lanes per pair (wave w
 // takes pairs 4 w .. 4 w + 3): the queries' int8 weight planes against the cluster's SQ8 grid
 // and each pair's threshold-independent scalars.  Lane l owns dims 64 k + 4 l + [0, 4)
-// (coalesced 32-byte row pieces, one packed 32-bit store per plane).
-//   w_d = delta_d * (q_rot,d - vmin_d);  one scale for the group: s = 2^(ilogb(m) - 14),
-//   doubled if m / s > 32639, for m = the largest |w_d| of the group's pairs, so |w_int| <=
-//   32639;  w_int = rint(w / s) = 256 hi + lo  (hi, lo in [-128, 127]).
+// (16-byte loads, one packed 32-bit store per plane).  All in float32, on the float32 rotated
+// query q32 (the bounds take q32 as the query point: e_q grows by |q32 - q64| <= 2^-24 |q32|
+// per dimension):
+//   w_d = delta_d * (q32_d - vmin_d) (two roundings, <= 2^-22 |w_d|, charged to err_q);  one
+//   scale for the group: s = 2^(ilogb(m) - 14), doubled if m / s > 32639, for m = the largest
+//   |w_d| of the group's pairs, so |w_int| <= 32639;  w_int = rint(w / s) = 256 hi + lo
+//   (hi, lo in [-128, 127]);  Q = sum (q32_d - vmin_d)^2 (relative error < 2^-15).
 // (A common scale lets the lower-bound scan compare a wave's 16 queries against one integer
 // threshold per vector.)  Plane bytes past D_pad (up to DP) are zero, so the scan may read
 // whole 64-dim steps.
 template <int KS>
 __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
-    __shared__ double s_mx[kGroupQ];
+    __shared__ float s_mx[kGroupQ];
     const int gi = blockIdx.x;
     if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;
     const int2 grp = a.groups[gi];
@@ -325,42 +328,49 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     const int c = a.pair_cid[pp], q = a.pair_qid[pp];
     const int D_pad = a.D_pad, DP = a.DP;
     const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
-    const double* xr = a.xrot64 + (size_t)q * D_pad;
-    double w[KS][4];
-    double mx = 0.0, Qp = 0.0;
+    const float* xr = a.xrot32 + (size_t)q * D_pad;
+    float w[KS][4];
+    float mx = 0.0f, Qp = 0.0f, qq = 0.0f;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
         const int d0 = 64 * k + 4 * l;  // D_pad is a multiple of 4: all 4 dims or none
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[k][e] = 0.0;
+        for (int e = 0; e < 4; ++e) w[k][e] = 0.0f;
         if (d0 < D_pad) {
-            const double2 x01 = *reinterpret_cast<const double2*>(xr + d0);
-            const double2 x23 = *reinterpret_cast<const double2*>(xr + d0 + 2);
-            const double xv[4] = {x01.x, x01.y, x23.x, x23.y};
+            const float4 x4 = *reinterpret_cast<const float4*>(xr + d0);
+            const float4 v4 = *reinterpret_cast<const float4*>(a.vmin + off + d0);
+            const float4 g4 = *reinterpret_cast<const float4*>(a.delta + off + d0);
+            const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w},
+                        gv[4] = {g4.x, g4.y, g4.z, g4.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const double qp = xv[e] - (double)a.vmin[off + d0 + e];
-                w[k][e] = (double)a.delta[off + d0 + e] * qp;
-                mx = fmax(mx, fabs(w[k][e]));
-                Qp = fma(qp, qp, Qp);
+                const float qp = xv[e] - vv[e];
+                w[k][e] = gv[e] * qp;
+                mx = fmaxf(mx, fabsf(w[k][e]));
+                Qp = fmaf(qp, qp, Qp);
+                qq = fmaf(xv[e], xv[e], qq);
             }
         }
     }
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
-    Qp = sum16_f64(Qp);
+    for (int o = 1; o < 16; o <<= 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+        Qp += __shfl_xor(Qp, o, kWave);
+        qq += __shfl_xor(qq, o, kWave);
+    }
     if (l == 0) s_mx[slot] = mx;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kGroupQ; ++i) mx = fmax(mx, s_mx[i]);
-    // s and 1/s are powers of two (|e| <= 1010 here), so w * (1/s) is exactly w / s
+    for (int i = 0; i < kGroupQ; ++i) mx = fmaxf(mx, s_mx[i]);
+    // s and 1/s are powers of two in [2^-114, 2^114], so w * (1/s) is exactly w / s and
+    // s * wi is exact
     int es = 0;
-    if (mx > 0x1p-100) {
-        es = ilogb(mx) - 14;
-        if (ldexp(mx, -es) > 32639.0) ++es;
+    if (mx > 0x1p-100f) {
+        es = ilogbf(mx) - 14;
+        if (ldexpf(mx, -es) > 32639.0f) ++es;
     }
-    const double s = ldexp(1.0, es), inv_s = ldexp(1.0, -es);
-    double errs = 0.0;
+    const float s = ldexpf(1.0f, es), inv_s = ldexpf(1.0f, -es);
+    float errs = 0.0f;
     int wsum = 0, wabs = 0;
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
 #pragma unroll
@@ -368,8 +378,9 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         uint32_t hw = 0u, lw = 0u;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int wi = (int)rint(w[k][e] * inv_s);  // 0 for dims >= D_pad
-            errs += fabs(w[k][e] - s * (double)wi) + 0x1p-52 * fabs(w[k][e]);
+            const int wi = (int)rintf(w[k][e] * inv_s);  // 0 for dims >= D_pad
+            // w - s wi is exact (Sterbenz, or wi = 0); 2^-22 |w| covers the two roundings of w
+            errs += fabsf(w[k][e] - s * (float)wi) + 0x1p-22f * fabsf(w[k][e]);
             wsum += wi;
             wabs += abs(wi);
             const int hi = (wi + 128) >> 8;
@@ -381,19 +392,23 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
             *reinterpret_cast<uint32_t*>(hi_p + DP + 64 * k + 4 * l) = lw;
         }
     }
-    errs = sum16_f64(errs);
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) {
+        errs += __shfl_xor(errs, o, kWave);
         wsum += __shfl_xor(wsum, o, kWave);
         wabs += __shfl_xor(wabs, o, kWave);
     }
     if (valid && l == 0) {
         PairRec r;
-        r.Qp = Qp;
-        r.err_q = 255.0 * errs * (1.0 + 0x1p-40);
-        r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-52 * sqrt(Qp) + 1e-300;
+        r.Qp = (double)Qp;
+        // float32 sums of <= 256 terms: relative error < 2^-15 (the (1 + 2^-15) factors here
+        // and the 2^-15 margins on Qp where it is used)
+        r.err_q = 255.0 * (double)errs * (1.0 + 0x1p-15);
+        // the query is the float32 rotation q32: |q32 - q_exact| <= e_q(float64) + 2^-23 |q32|
+        r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-23 * sqrt((double)qq) * (1.0 + 0x1p-15) +
+                1e-30;
         r.cW = 128.0 * (double)wsum;
-        r.c1 = 2.0 * s;
+        r.c1 = 2.0 * (double)s;
         r.a_max = a.cbound[kCbStride * c];
         r.r_max = a.cbound[kCbStride * c + 1];
         r.acc_max = 128.0 * (double)wabs;
@@ -537,7 +552,7 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
             cW = pr.cW;
             c1 = pr.c1;
             if constexpr (UB_PASS) {
-                AQ = (Qp + 2.0 * err_q) * (1.0 + 1e-13);
+                AQ = (Qp * (1.0 + 0x1p-15) + 1e-30 + 2.0 * err_q) * (1.0 + 1e-13);
             } else {
                 const double tau = a.tau[q];
                 const double tq = sqrt(tau * a.rot_sq_max) * (1.0 + 1e-12) + e_q;
@@ -552,7 +567,7 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
                     // with A_max = 255^2 sum delta^2 (codes <= 255), r_max = 2 sqrt(sum eps^2)
                     // (r_x <= |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms)
                     // and |acc| <= acc_max = 128 sum |w_int|; slack = 2^-22 X covers them all.
-                    const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
+                    const double G = 2.0 * err_q - Qp * (1.0 - 0x1p-15) + tq * tq;
                     const double H = c1 * cW + G;
                     const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max +
                                      c1 * pr.acc_max + fabs(H);
@@ -946,7 +961,7 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     double Kd = 0.0, mg = 0.0;
     float tqf = 0.0f;
     if (thr) {
-        const double G = 2.0 * err_q - Qp * (1.0 - 1e-13) + tq * tq;
+        const double G = 2.0 * err_q - Qp * (1.0 - 0x1p-15) + tq * tq;
         const double H = c1 * cW + G;
         const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max + c1 * pr.acc_max +
                          fabs(H);

@@ -65,6 +65,7 @@ struct Carver {
 struct Workspace {
     double* xq64;
     double* xrot64;
+    float* xrot32;
     double* qerr;
     double* cd64;
     int32_t* probe_cids;
@@ -112,6 +113,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     const int64_t cap = cand_cap(nprobe, K);
     w.xq64 = c.take<double>(B * ix->D);
     w.xrot64 = c.take<double>(B * ix->D_pad);
+    w.xrot32 = c.take<float>(B * ix->D_pad);
     w.qerr = c.take<double>(B * ix->D_pad);
     w.cd64 = c.take<double>(B * ix->nlist);
     w.probe_cids = c.take<int32_t>(B * nprobe);
@@ -359,7 +361,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
     prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
                           dim3(64, 4), 0, st>>>(
         xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
-        w.xrot64, w.qerr, rotate ? 1 : 0);
+        w.xrot64, w.xrot32, w.qerr, rotate ? 1 : 0);
     int rc = check_launch("prep_queries_kernel");
     if (rc) return rc;
     constexpr int qpb = kCoarseQW * kWavesPerBlock;
@@ -623,6 +625,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.per_cluster = ix->per_cluster_sq8;
         b.xq = xq;
         b.xrot64 = w.xrot64;
+        b.xrot32 = w.xrot32;
         b.qerr = w.qerr;
         b.tau = w.tau64;
         b.cand_key = w.cand_key;
@@ -777,7 +780,7 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
     prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
                           dim3(64, 4), 0, st>>>(
         xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
-        w.xrot64, w.qerr, 1);
+        w.xrot64, w.xrot32, w.qerr, 1);
     if ((rc = check_launch("prep_queries_kernel"))) return rc;
     ScanArgs a = make_scan_args(ix, w, 1, 1, 0, nullptr);
     sq8_bounds_kernel<<<(n + 255) / 256, 256, 0, st>>>(a, qids, cids, spos, n, lb, ub);

@@ -23,11 +23,13 @@ __global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n) {
 // kPrepQB queries (wave-uniform rows, scalar loads) x 64 columns, so every loaded rotation value
 // feeds kPrepQB chains.
 // xq64[b, d] = (double)xq[b, d]; xrot64[b, j] = sum_d xq[b, d] * R[d, j] + bvec[j] evaluated
-// in float64 (fma, dimension order) and qerr[b, j] bounds its distance from the exact value.
+// in float64 (fma, dimension order), xrot32 = xrot64 rounded to float32, and qerr[b, j] bounds
+// the distance of xrot64 from the exact value.
 __global__ __launch_bounds__(256) void prep_queries_kernel(
     const float* __restrict__ xq, int B, int D, int D_pad, const float* __restrict__ W, int ldw,
     int nlist, const float* __restrict__ bvec, double* __restrict__ xq64,
-    double* __restrict__ xrot64, double* __restrict__ qerr, int do_rot) {
+    double* __restrict__ xrot64, float* __restrict__ xrot32, double* __restrict__ qerr,
+    int do_rot) {
     constexpr int QB = kPrepQB;
     const int j = blockIdx.x * 64 + threadIdx.x;
     const int b0 = (blockIdx.y * 4 + threadIdx.y) * QB;
@@ -59,7 +61,9 @@ __global__ __launch_bounds__(256) void prep_queries_kernel(
 #pragma unroll
     for (int i = 0; i < QB; ++i) {
         if (b0 + i >= B) break;
-        xrot64[(size_t)(b0 + i) * D_pad + j] = acc[i] + bj;
+        const double xr = acc[i] + bj;
+        xrot64[(size_t)(b0 + i) * D_pad + j] = xr;
+        xrot32[(size_t)(b0 + i) * D_pad + j] = (float)xr;
         // |fl(sum) - sum| <= (D + 1) 2^-53 sum|terms|; doubled to also cover the rounding of
         // `mag`.
         qerr[(size_t)(b0 + i) * D_pad + j] =

@@ -104,6 +104,7 @@ struct BatchArgs {
     int D, D_pad, T, per_cluster;
     const float* xq;            // [B, D] float32 queries
     const double* xrot64;       // [B, D_pad]
+    const float* xrot32;        // [B, D_pad] xrot64 rounded to float32
     const double* qerr;         // [B, D_pad]
     const int4* units;          // work units {cid | cnt << 20, pair start, v_begin, v_end}
     const int32_t* unit_off;    // [2 * nlist + 1] unit offsets of the (pass, cluster) segments
@@ -141,8 +142,8 @@ __global__ void stats_fold_kernel(const unsigned long long* slots, int64_t* out)
 __global__ void prep_queries_kernel(const float* __restrict__ xq, int B, int D, int D_pad,
                                     const float* __restrict__ W, int ldw, int nlist,
                                     const float* __restrict__ bvec, double* __restrict__ xq64,
-                                    double* __restrict__ xrot64, double* __restrict__ qerr,
-                                    int do_rot);
+                                    double* __restrict__ xrot64, float* __restrict__ xrot32,
+                                    double* __restrict__ qerr, int do_rot);
 
 __global__ void coarse_dist_kernel(const double* __restrict__ xq64, int B, int D,
                                    const float* __restrict__ W, int ldw, int nlist,
