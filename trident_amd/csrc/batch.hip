@@ -467,21 +467,42 @@ __device__ __forceinline__ int lb_thr(float A, float r, float tq, float inv_c1) 
     return r <= 3.0e38f ? (int)v : INT_MAX;
 }
 
-// (The lower-bound pass at KS <= 2 is held to 5 waves per SIMD: the compiler's own choice of
-// registers gives 4, and the scan is latency-bound.)
-template <bool UB_PASS, int KS>
-__global__ __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_scan_kernel(
-    BatchArgs a) {
-    constexpr int kRows = KS * 16;  // code rows (4 dims each) held per block buffer
-    __shared__ uint4 s_codes[2][kRows * kBlkV / 4];
-    __shared__ __align__(16) float2 s_ar[2][kBlkV];
-    __shared__ __align__(16) int s_thr[UB_PASS ? 1 : 2][UB_PASS ? 1 : kWavesPerBlock]
-                                      [UB_PASS ? 4 : kBlkV];
-    __shared__ float s_ubl[UB_PASS ? kWavesPerBlock : 1][UB_PASS ? kWaveQ * kWave : 1];
-    constexpr int kLbW = UB_PASS ? 1 : kWavesPerBlock;  // per-wave survivor queues (pass B)
-    __shared__ uint32_t s_sq[kLbW][UB_PASS ? 1 : kSurvQ];
-    __shared__ int s_scnt[kLbW][kWaveQ], s_sbase[kLbW][kWaveQ], s_sqid[kLbW][kWaveQ];
+// Global -> LDS without registers: lane i's 16 (or 4) bytes land at lds + 16 i (4 i).
+__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
+                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// Pass A (seeding), the first p_init probes: for every query of a unit the K-th smallest upper
+// bound over the cluster -> atomicMin into tau[q] (float64 bit pattern).  Units (<= 16
+// queries, whole clusters) and wave mapping as in lb_scan_kernel; block b + 1's code cells and
+// row scalars (A_lo, r) move global -> LDS directly while the waves scan block b.
+//
+// Per row, in float32, with the per-query constants of the unit prologue:
+//     E = fma(-c1, float(acc), Cq) + A_lo (1 + 2^-21),   Cq >= A Q-part - c1 cW + slack,
+//     u = fma(sqrt(max(E, 0)), 1 + 2^-20, r + e_q) (1 + 2^-21)  >=  |x_rot - q_rot|,
+// where the exact E = A + Q + 2 err - c1 (acc + cW) (norm form of the upper bound) and the
+// slack 2^-22 (A_max + c1 acc_max + |Cq|) covers the roundings of float(acc), the fma and the
+// add (each <= 2^-24 of a term bounded by that sum); the (1 + 2^-20) factor covers sqrt's
+// error and (1 + 2^-21) the last two roundings (all terms non-negative).  A_lo (1 + 2^-21)
+// >= A: vec_Ar holds A rounded down by 1e-13 and then to float32.
+//
+// Each lane keeps the M smallest bounds of its rows (M = 4 when K <= 16: a query's rows are
+// spread over 16 lanes, and the merged lists' K-th entry is the exact K-th smallest unless one
+// lane held more than M of them, in which case it is still an upper bound of it).
+template <int KS, int M>
+__global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
+    // The code buffers double as the end-of-unit list exchange (after a barrier).
+    constexpr int kCodeU4 = 2 * KS * 4 * kBlkV, kUblU4 = kWavesPerBlock * kWaveQ * kWave / 4;
+    __shared__ uint4 s_big[kCodeU4 > kUblU4 ? kCodeU4 : kUblU4];
+    uint4(*s_codes)[KS * 4 * kBlkV] = reinterpret_cast<uint4(*)[KS * 4 * kBlkV]>(s_big);
+    float(*s_ubl)[kWaveQ * kWave] = reinterpret_cast<float(*)[kWaveQ * kWave]>(s_big);
+    __shared__ __align__(16) float s_A[2][kBlkV];
+    __shared__ __align__(16) float s_r[2][kBlkV];
     __shared__ int s_unit[2];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -492,52 +513,33 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
     const int xcd = (int)(blockIdx.x & 7);
     const int rb = xcd * nx, re = min(total, rb + nx);
     int32_t* ctr = a.ctr + xcd * kCtrStride;
-    const int D_pad = a.D_pad, T = a.T;
-    unsigned long long st_cand = 0, st_surv = 0;
-    if constexpr (!UB_PASS) {
-        if (lane < kWaveQ) s_scnt[wid][lane] = 0;
-    }
+    const int T = a.T, G16 = a.D_pad >> 4;
+    unsigned long long st_cand = 0;
 
-    // The next unit's counter value is taken two blocks before the current unit ends (its
-    // latency hides behind them) and published in s_unit at the end of the unit.  Slot
-    // (it + 1) & 1 is written at the end of unit it, after every wave read it at the start of
-    // unit it - 1 (the barrier at the top of unit it separates the two).
-    // The explicit LDS wait before the barrier keeps lane 0's s_unit write ahead of the other
-    // waves' reads (the compiler's own wait was missing on the loop's back edge).
+    // next unit index: as in lb_scan_kernel
     if (tid == 0) s_unit[0] = atomicAdd(ctr, 1);
     for (int it = 0;; ++it) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
         const int ui = __builtin_amdgcn_readfirstlane(s_unit[it & 1]) + rb;
         if (ui < rb || ui >= re) break;
-        int nxt = 0;  // wave 0, lane 0: the next unit's counter value
+        int nxt = 0;
         const int4 un = a.units[ui];
         const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
-        // The unit's queries form G groups of <= 16; each group gets R = 4 / G waves, which
-        // split every block's four 16-vector tiles (replica rr takes tiles rr, rr + R, ...).
         const int G = (cnt + kWaveQ - 1) / kWaveQ;
         const int R = kWavesPerBlock / G;
         const int gq = wid / R, rr = wid - gq * R;
         const bool active = gq < G;
-        const int nq = active ? min(kWaveQ, cnt - gq * kWaveQ) : 0;  // this wave's queries
+        const int nq = active ? min(kWaveQ, cnt - gq * kWaveQ) : 0;
         const bool hasq = j < nq;
         const int v0 = a.vec_off[cid];
         const int t0 = a.tile_off[cid];
-        int q = 0;
 
-        // ---- per-query weights for this lane's dims (active waves only) ----
+        // ---- this wave's queries: weight planes and float32 bound constants ----
         v4i bhi[KS], blo[KS];
-        double e_q = 0.0, c1 = 0.0, cW = 0.0, AQ = 0.0;
-        float c1f = 0.0f, c2f = 0.0f, H32 = INFINITY;  // no threshold: every row passes
-        // integer test (lower-bound pass): kq of this lane's query, the wave's largest tq
-        // (rounded up) and 1 / c1 of its weight group
-        int kq = 0;
-        float tqw = 0.0f, inv_c1w = 0.0f;
-        double tq_l = 0.0, Kd = 0.0, mg = 0.0;
-        bool lane_int = true;
+        int q = 0;
+        float nc1 = 0.0f, Cq = INFINITY, e_q = 0.0f;  // lanes without a query: u = +inf
         if (active) {
-            // Prepared by pair_prep_kernel: lane (j, g) takes bytes [ks*64 + g*16, +16) of
-            // query j's planes and the pair's scalars.
             const int pj = start + gq * kWaveQ + (hasq ? j : 0);
             q = a.pair_qid[pj];
             const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
@@ -546,117 +548,25 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
                 bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
                 blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
             }
-            const PairRec pr = a.prec[pj];
-            const double Qp = pr.Qp, err_q = pr.err_q;
-            e_q = pr.e_q;
-            cW = pr.cW;
-            c1 = pr.c1;
-            if constexpr (UB_PASS) {
-                AQ = (Qp * (1.0 + 0x1p-15) + 1e-30 + 2.0 * err_q) * (1.0 + 1e-13);
-            } else {
-                const double tau = a.tau[q];
-                const double tq = sqrt(tau * a.rot_sq_max) * (1.0 + 1e-12) + e_q;
-                if (tq < 1e30) {
-                    // Survive iff A - r^2 - 2 tq r <= 2 s dot + 2 err - Q + tq^2 (the norm-form
-                    // lower bound against sqrt(tau) scaled to the rotated space).  Evaluated as
-                    //   L = fma(c2, r, fma(-r, r, A_lo)) <= R = fma(c1, float(acc), H32)
-                    // with acc = dot - 128 sum(w_int) (exact int32), c1 = 2s (a power of two),
-                    // c2 <= -2 tq and H32 >= 2 s 128 sum(w_int) + 2 err - Q + tq^2 + slack.
-                    // Each of the 4 f32 roundings is at most 2^-24 of a term bounded by
-                    //   X = A_max + r_max^2 + 2 tq r_max + c1 acc_max + |H|,
-                    // with A_max = 255^2 sum delta^2 (codes <= 255), r_max = 2 sqrt(sum eps^2)
-                    // (r_x <= |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms)
-                    // and |acc| <= acc_max = 128 sum |w_int|; slack = 2^-22 X covers them all.
-                    const double G = 2.0 * err_q - Qp * (1.0 - 0x1p-15) + tq * tq;
-                    const double H = c1 * cW + G;
-                    const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max +
-                                     c1 * pr.acc_max + fabs(H);
-                    const double slack = 0x1p-22 * X * (1.0 + 1e-6) + 1e-30;
-                    H32 = __double2float_ru(H + slack);
-                    c1f = (float)c1;
-                    c2f = -__double2float_ru(2.0 * tq);
-                    tq_l = tq;
-                    Kd = cW + G / c1;  // G / c1 is exact: c1 is a power of two
-                    mg = 0x1p-50 * (fabs(Kd) + (2.0 * err_q + Qp + tq * tq) / c1);
-                    tqw = __double2float_ru(tq);
-                } else {
-                    lane_int = false;  // no threshold: every row passes (float test only)
-                }
-            }
-            if (!hasq) {
-                H32 = -INFINITY;  // lane has no query: nothing survives
-                lane_int = true;
+            if (hasq) {
+                const PairRec pr = a.prec[pj];
+                const double AQ = (pr.Qp * (1.0 + 0x1p-15) + 1e-30 + 2.0 * pr.err_q) * (1.0 + 1e-13);
+                const double C = AQ - pr.c1 * pr.cW;
+                const double slack =
+                    0x1p-22 * (pr.a_max * (1.0 + 0x1p-20) + pr.c1 * pr.acc_max + fabs(C)) *
+                        (1.0 + 1e-6) + 1e-30;
+                nc1 = -(float)pr.c1;  // a power of two: exact
+                Cq = __double2float_ru(C + slack);
+                e_q = __double2float_ru(pr.e_q);
             }
         }
-        // Integer form of the lower-bound test, exact in int32 (see the tile epilogue):
-        //   acc + kq >= thr_x,   thr_x <= (A_lo - r (r + 2 tq_w)) / c1   (per vector),
-        //   kq >= cW + G / c1 - 2 (tq_w - tq) r_lo / c1                 (per query),
-        // with tq_w the wave's largest tq and r_lo <= r_x over the cluster.  Since
-        // A - r^2 - 2 tq r >= A - r (r + 2 tq_w) + 2 (tq_w - tq) r_lo, the exact condition
-        // implies it.  mg covers the roundings of G and of the sums.  The wave takes the integer
-        // test iff every lane can: |kq| <= 2^30 (with |acc| < 2^30, acc + kq cannot overflow),
-        // every query has a threshold and all share one c1.
-        const double c1_0 = shfl_f64(c1, 0);
-        bool int_ok = !UB_PASS && active && __ballot(!lane_int || (hasq && c1 != c1_0)) == 0ull;
-        const uint64_t qmask = __ballot(hasq);
-        if (int_ok) {
-#pragma unroll
-            for (int o = 1; o < kWave; o <<= 1) tqw = fmaxf(tqw, __shfl_xor(tqw, o, kWave));
-            inv_c1w = (float)(1.0 / c1_0);  // a power of two in [2^-100, 2^100]: exact
-            const double r_lo = a.cbound[kCbStride * cid + 2];
-            const double corr = 2.0 * ((double)tqw - tq_l) * r_lo / c1_0 * (1.0 - 0x1p-50);
-            const double kd = ceil(Kd - corr + (mg + 0x1p-50 * fabs(corr)));
-            const bool ok = fabs(kd) <= 0x1p30 && c1_0 >= 0x1p-100 && c1_0 <= 0x1p100;
-            kq = hasq ? (int)(ok ? kd : 0.0) : -0x40000000;
-            int_ok = __ballot(hasq && !ok) == 0ull;
-        }
-        if (!int_ok) kq = 0;
 
         float ubl[kUbList];
-        if constexpr (UB_PASS) {
 #pragma unroll
-            for (int i = 0; i < kUbList; ++i) ubl[i] = INFINITY;
-        }
+        for (int i = 0; i < kUbList; ++i) ubl[i] = INFINITY;
 
-        // Lower-bound survivors wait in the wave's LDS queue (entries li << 4 | query slot) and
-        // are appended to the candidate lists here: one atomic per query of the wave reserves
-        // its slots, then every entry takes the next slot of its query.  Wave-local: LDS
-        // operations of one wave complete in order.
-        int nsq = 0;
-        if constexpr (!UB_PASS) {
-            if (active && lane < kWaveQ) s_sqid[wid][lane] = q;
-        }
-        auto flush = [&]() {
-            if constexpr (!UB_PASS) {
-                for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 15u], 1);
-                __builtin_amdgcn_wave_barrier();
-                if (lane < kWaveQ) {
-                    const int c = s_scnt[wid][lane];
-                    s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[q], c) : 0;
-                    s_scnt[wid][lane] = 0;
-                }
-                __builtin_amdgcn_wave_barrier();
-                for (int e = lane; e < nsq; e += kWave) {
-                    const uint32_t ent = s_sq[wid][e];
-                    const int jj = (int)(ent & 15u);
-                    const int slot = s_sbase[wid][jj] + atomicAdd(&s_scnt[wid][jj], 1);
-                    if (slot < a.cap)
-                        a.cand_id[(size_t)s_sqid[wid][jj] * a.cap + slot] = v0 + (int)(ent >> 4);
-                }
-                __builtin_amdgcn_wave_barrier();
-                if (lane < kWaveQ) s_scnt[wid][lane] = 0;
-                if (a.stats) st_surv += (unsigned long long)nsq;
-                nsq = 0;
-            }
-        };
-
-        // ---- one 16-vector tile of the block in LDS buffer buf ----
-        // INT selects the lower-bound pass's integer test (a wave-uniform mode, so each mode gets
-        // its own loop rather than a branch per tile).
-        auto tile = [&](auto int_c, int buf, int t, int li0) {
-            constexpr bool INT = decltype(int_c)::value;
-            // A operand: lane (i = j, g) reads vector 16t + i's 16 code bytes of dims
-            // ks*64 + g*16 + [0, 16) (row group ks*4 + g), already offset to c' = c - 128.
+        // ---- one 16-vector tile ----
+        auto tile = [&](int buf, int t, int li0) {
             const uint4* blk = s_codes[buf];
             v4i A[KS];
 #pragma unroll
@@ -664,240 +574,139 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
                 const uint4 v = blk[(ks * 4 + g) * kBlkV + t * 16 + j];
                 A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
-            // lower-bound pass: integer thresholds of rows 4g .. 4g + 3 (read ahead of the MFMAs)
-            int4 th = make_int4(0, 0, 0, 0);
-            if constexpr (!UB_PASS)
-                th = *reinterpret_cast<const int4*>(&s_thr[buf][wid][t * 16 + 4 * g]);
-            // the lower-bound pass starts the lo sums at kq (0 on the float test)
-            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {kq, kq, kq, kq};
+            const int row0 = t * 16 + 4 * g;
+            const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
+            const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
+            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
                 acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
             }
-            // The matrix core does not interlock VALU reads of its results: keep 16 wait
-            // states (plus the compiler's own padding) between the last MFMA and the first
-            // accumulator read, fenced so the scheduler cannot move either side across.  (The
-            // compiler's padding alone fell short when a branch sat between the two: rows read
-            // the previous tile's sums.)
+            // matrix-core results: 16 wait states (plus the compiler's padding) before the
+            // first read, fenced from the scheduler (see lb_scan_kernel)
             __builtin_amdgcn_sched_barrier(0);
             asm volatile("s_nop 7\n\ts_nop 7");
             __builtin_amdgcn_sched_barrier(0);
-            // epilogue: rows 4g + r (vectors), column j (query).  S = acc + kq, exact in int32
-            // (|acc| <= 128 * 256 * 32639 < 2^30, |kq| <= 2^30).
-            int S[4];
+            const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
 #pragma unroll
-            for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
-            // per-row scalars: (P = A_lo - r^2, r) in the lower-bound pass, (A_lo, r) in the
-            // upper-bound pass; rows past the slice hold (NaN, +inf), which no test accepts
-            auto row_scalars = [&](float (&Ar)[4][2]) {
-                const float4 ar01 = *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g]);
-                const float4 ar23 =
-                    *reinterpret_cast<const float4*>(&s_ar[buf][t * 16 + 4 * g + 2]);
-                Ar[0][0] = ar01.x; Ar[0][1] = ar01.y; Ar[1][0] = ar01.z; Ar[1][1] = ar01.w;
-                Ar[2][0] = ar23.x; Ar[2][1] = ar23.y; Ar[3][0] = ar23.z; Ar[3][1] = ar23.w;
-            };
-            if constexpr (UB_PASS) {
-                float Ar[4][2];
-                row_scalars(Ar);
+            for (int r = 0; r < 4; ++r) {
+                const int S = (acc_hi[r] << 8) + acc_lo[r];
+                const float E = fmaf(nc1, (float)S, Cq) + Av[r] * (1.0f + 0x1p-21f);
+                float u = fmaf(sqrtf(fmaxf(E, 0.0f)), 1.0f + 0x1p-20f, rv[r] + e_q) *
+                          (1.0f + 0x1p-21f);
+                if (li0 + 4 * g + r >= ve) u = INFINITY;  // rows past the slice
+                if constexpr (M <= 4) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const double dot = (double)S[r] + cW;
-                    const double Alo = (double)Ar[r][0], rr = (double)Ar[r][1];
-                    const double E = fmax(fma(-c1, dot, Alo * (1.0 + 0x1p-22) + AQ), 0.0);
-                    const float s32 = sqrtf((float)(E * (1.0 + 1e-12))) * (1.0f + 0x1p-20f);
-                    const float u = (s32 + (float)rr + (float)e_q) * (1.0f + 0x1p-20f);
-                    if (u < ubl[kUbList - 1]) {
+                    for (int i = M - 1; i > 0; --i)
+                        ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
+                    ubl[0] = fminf(ubl[0], u);
+                } else if (u < ubl[M - 1]) {
 #pragma unroll
-                        for (int i = kUbList - 1; i > 0; --i)
-                            ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
-                        ubl[0] = fminf(ubl[0], u);
-                    }
-                }
-            } else {
-                // Survivor masks, one per row.  Integer test: acc + kq >= thr_x.  It and the
-                // float test are both implied by the exact lower-bound condition (thr_x uses
-                // the wave's largest tq and rounds down, kq rounds up; the float test carries
-                // its slack), so a row passing both is kept and no true survivor is lost.
-                uint64_t sm[4];
-                if constexpr (INT) {
-                    sm[0] = __ballot(S[0] >= th.x);
-                    sm[1] = __ballot(S[1] >= th.y);
-                    sm[2] = __ballot(S[2] >= th.z);
-                    sm[3] = __ballot(S[3] >= th.w);
-                } else {
-                    // lanes without a query have H32 = -inf; a query with no threshold has
-                    // c1f = c2f = 0, H32 = +inf
-                    float Ar[4][2];
-                    row_scalars(Ar);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        sm[r] = __ballot(fmaf(c2f, Ar[r][1], Ar[r][0]) <=
-                                         fmaf(c1f, (float)S[r], H32));
-                }
-                if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
-                // rare: the per-query float test
-                //   fma(c2, r, P) <= fma(c1, float(acc), H32),  acc = S - kq,
-                // then queue survivors (cluster index, query slot) in the wave's LDS queue
-                float Ar[4][2];
-                row_scalars(Ar);
-                if (nsq > kSurvQ - 4 * kWave) flush();
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const bool pass = hasq && ((sm[r] >> lane) & 1ull) &&
-                                      fmaf(c2f, Ar[r][1], Ar[r][0]) <=
-                                          fmaf(c1f, (float)(S[r] - kq), H32);
-                    const uint64_t pm = __ballot(pass);
-                    if (pass) {
-                        const int idx = __builtin_amdgcn_mbcnt_hi(
-                            (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
-                        s_sq[wid][nsq + idx] = ((uint32_t)(li0 + 4 * g + r) << 4) | (uint32_t)j;
-                    }
-                    nsq += __popcll(pm);
+                    for (int i = M - 1; i > 0; --i)
+                        ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : fminf(ubl[i], u);
+                    ubl[0] = fminf(ubl[0], u);
                 }
             }
         };
 
-        // ---- stream the slice through LDS in 64-vector blocks ----
-        // A block is 64 slots of one T-tile (T and the block starts are multiples of 64): its
-        // cells (g, slot).  LDS cell g * 64 + v holds vector v's codes of dims 16 g .. 16 g + 15
-        // (already c - 128), so the MFMA A operand of 64 dims is one 16-byte read.  Thread tid
-        // moves vector tid & 63's cells g = (tid >> 6) + 4 jj: one 16-byte load each, 1 KiB
-        // contiguous per wave.  Cells past D_pad are not loaded: their weights are zero.
-        // (The staging values are separate scalars filled by value: an array captured by
-        // reference lands in scratch memory and serialises every load.)
-        uint4 st0 = make_uint4(0u, 0u, 0u, 0u), st1 = st0, st2 = st0, st3 = st0;
-        float2 st_ar = make_float2(0.0f, 0.0f);
-        bool st_row_ok = false;
-        const int G16 = D_pad >> 4, g0 = wid;
-        const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
-        int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
-        auto gload = [&](int blk0) {
-            // wave-uniform base, lane offset added per load
-            const uint4* base = cells_c + ((size_t)ct * G16 + g0) * T + cw;
-            if (g0 < G16) st0 = base[lane];
-            if constexpr (KS > 1) if (g0 + 4 < G16) st1 = (base + (size_t)4 * T)[lane];
-            if constexpr (KS > 2) if (g0 + 8 < G16) st2 = (base + (size_t)8 * T)[lane];
-            if constexpr (KS > 3) if (g0 + 12 < G16) st3 = (base + (size_t)12 * T)[lane];
+        // ---- stream the cluster through LDS in 64-vector blocks ----
+        const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;
+        int ct = vb / T, cw = vb - ct * T;
+        auto gload = [&](int buf, int blk0) {
+            const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
+#pragma unroll
+            for (int jj = 0; jj < KS; ++jj)
+                if (wid + 4 * jj < G16)
+                    load_lds16(base + (size_t)(4 * jj) * T + lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
             cw += kBlkV;
             if (cw == T) {
                 cw = 0;
                 ++ct;
             }
-            // (A_lo, r) of row blk0 + lane: wave 0 publishes the rows' scalars, and each wave
-            // on the integer test derives its own thresholds from them.  The load is
-            // unconditional (clamped row; ve > vb) so that nothing waits for it here; rows past
-            // the slice are replaced when stored.
-            if (tid < kBlkV || int_ok) {
-                st_row_ok = blk0 + lane < ve;
-                st_ar = a.vec_Ar[v0 + min(blk0 + lane, ve - 1)];
-            }
-        };
-        auto lstore = [&](int buf) {
-            uint4* blk = s_codes[buf] + g0 * kBlkV + lane;
-            if (g0 < G16) blk[0] = st0;
-            if constexpr (KS > 1) if (g0 + 4 < G16) blk[4 * kBlkV] = st1;
-            if constexpr (KS > 2) if (g0 + 8 < G16) blk[8 * kBlkV] = st2;
-            if constexpr (KS > 3) if (g0 + 12 < G16) blk[12 * kBlkV] = st3;
-            // lower-bound pass keeps P = A_lo - r^2 (its f32 rounding is inside the float
-            // test's slack), upper-bound pass keeps A_lo; rows past the slice hold (NaN, +inf)
-            if (!st_row_ok) st_ar = make_float2(__int_as_float(0x7fc00000), INFINITY);
-            if (tid < kBlkV)
-                s_ar[buf][tid] =
-                    UB_PASS ? st_ar : make_float2(fmaf(-st_ar.y, st_ar.y, st_ar.x), st_ar.y);
-            if constexpr (!UB_PASS) {
-                if (int_ok) s_thr[buf][wid][lane] = lb_thr(st_ar.x, st_ar.y, tqw, inv_c1w);
+            if (wid == 0) {
+                const float* ar = reinterpret_cast<const float*>(a.vec_Ar + v0 + min(blk0 + lane, ve - 1));
+                load_lds4(ar, s_A[buf]);
+                load_lds4(ar + 1, s_r[buf]);
             }
         };
         const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
-        if (nblk > 0) gload(vb);
+        if (nblk > 0) gload(0, vb);
         for (int b = 0; b < nblk; ++b) {
             const int buf = b & 1;
-            lstore(buf);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
-            if (b + 1 < nblk) gload(vb + (b + 1) * kBlkV);
+            const int blk0 = vb + b * kBlkV;
+            if (b + 1 < nblk) gload(buf ^ 1, blk0 + kBlkV);
             if (active) {
-                const int blk0 = vb + b * kBlkV;
-                auto tiles = [&](auto int_c) {
-                    for (int t = rr; t < kBlkV / 16; t += R) {
-                        if (blk0 + t * 16 >= ve) break;
-                        tile(int_c, buf, t, blk0 + t * 16);
-                    }
-                };
-                if constexpr (UB_PASS) {
-                    tiles(std::false_type{});
-                } else if (int_ok) {
-                    tiles(std::true_type{});
-                } else {
-                    tiles(std::false_type{});
+                for (int t = rr; t < kBlkV / 16; t += R) {
+                    if (blk0 + t * 16 >= ve) break;
+                    tile(buf, t, blk0 + t * 16);
                 }
             }
         }
         if (a.stats && active && rr == 0)
             st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
-        if (nsq > 0) flush();
 
-        if constexpr (UB_PASS) {
-            // K-th smallest upper bound of each query -> atomicMin into tau[q] (float64 bit
-            // pattern).  Every lane holds the 16 smallest bounds of its rows.
-            //  K <= 16: the four lane groups' lists are merged in registers (exact top 16 of
-            //    the wave), replica waves exchange theirs through LDS and the group's first
-            //    wave merges them the same way: the K-th entry is the exact K-th smallest.
-            //  K > 16: all R x 64 kept values go through a register bitonic list; their K-th
-            //    smallest is >= the true K-th smallest bound, so still an upper bound.
-            if (a.K <= kUbList) {
-                if (active) {
-                    merge16_groups(ubl);
-                    if (R > 1 && g == 0) {
+        // ---- K-th smallest upper bound per query -> atomicMin into tau[q] ----
+        //  K <= 16: the four lane groups' lists are merged in registers (exact top 16 of the
+        //    kept bounds), replica waves exchange theirs through LDS and the group's first
+        //    wave merges them the same way.
+        //  K > 16: all R x 64 lists go through a register bitonic list.
+        // Either way the K-th entry is an upper bound of the K-th smallest distance bound.
+        __syncthreads();  // every wave is done with the code buffers
+        if (a.K <= kUbList) {
+            if (active) {
+                merge16_groups(ubl);
+                if (R > 1 && g == 0) {
 #pragma unroll
-                        for (int i = 0; i < kUbList; ++i) s_ubl[wid][j * kUbList + i] = ubl[i];
-                    }
+                    for (int i = 0; i < kUbList; ++i) s_ubl[wid][j * kUbList + i] = ubl[i];
                 }
-                if (R > 1) {
-                    __syncthreads();
-                    if (active && rr == 0) {
-#pragma unroll
-                        for (int i = 0; i < kUbList; ++i)
-                            ubl[i] = g < R ? s_ubl[wid + g][j * kUbList + i] : INFINITY;
-                        merge16_groups(ubl);
-                    }
-                }
-                if (active && rr == 0 && g == 0 && hasq) {
-                    float kth = INFINITY;
-#pragma unroll
-                    for (int i = 0; i < kUbList; ++i)
-                        if (i == a.K - 1) kth = ubl[i];
-                    if (kth < INFINITY) {
-                        const double u = (double)kth;
-                        const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                        atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + q,
-                                  (unsigned long long)key_of(tub));
-                    }
-                }
-            } else {
-                if (active) {
-                    float* s_ub = s_ubl[wid];
-#pragma unroll
-                    for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
-                }
+            }
+            if (R > 1) {
                 __syncthreads();
                 if (active && rr == 0) {
-                    for (int jj = 0; jj < nq; ++jj) {
-                        WaveList<64> L;
-                        L.init();
-                        for (int r2 = 0; r2 < R; ++r2)
-                            L.insert(key_of((double)s_ubl[wid + r2][jj * 64 + lane]), lane);
-                        uint64_t kk;
-                        int32_t ki;
-                        L.at(a.K - 1, kk, ki);
-                        const int qq = __shfl(q, jj, kWave);
-                        if (lane == 0 && dist_of(kk) < (double)INFINITY) {
-                            const double u = dist_of(kk);
-                            const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                            atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
-                                      (unsigned long long)key_of(tub));
-                        }
+#pragma unroll
+                    for (int i = 0; i < kUbList; ++i)
+                        ubl[i] = g < R ? s_ubl[wid + g][j * kUbList + i] : INFINITY;
+                    merge16_groups(ubl);
+                }
+            }
+            if (active && rr == 0 && g == 0 && hasq) {
+                float kth = INFINITY;
+#pragma unroll
+                for (int i = 0; i < kUbList; ++i)
+                    if (i == a.K - 1) kth = ubl[i];
+                if (kth < INFINITY) {
+                    const double u = (double)kth;
+                    const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
+                    atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + q,
+                              (unsigned long long)key_of(tub));
+                }
+            }
+        } else {
+            if (active) {
+                float* s_ub = s_ubl[wid];
+#pragma unroll
+                for (int i = 0; i < kUbList; ++i) s_ub[j * 64 + g * kUbList + i] = ubl[i];
+            }
+            __syncthreads();
+            if (active && rr == 0) {
+                for (int jj = 0; jj < nq; ++jj) {
+                    WaveList<64> L;
+                    L.init();
+                    for (int r2 = 0; r2 < R; ++r2)
+                        L.insert(key_of((double)s_ubl[wid + r2][jj * 64 + lane]), lane);
+                    uint64_t kk;
+                    int32_t ki;
+                    L.at(a.K - 1, kk, ki);
+                    const int qq = __shfl(q, jj, kWave);
+                    if (lane == 0 && dist_of(kk) < (double)INFINITY) {
+                        const double u = dist_of(kk);
+                        const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
+                        atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
+                                  (unsigned long long)key_of(tub));
                     }
                 }
             }
@@ -908,19 +717,18 @@ __attribute__((amdgpu_waves_per_eu(!UB_PASS && KS <= 2 ? 5 : 1))) void batch_sca
     if (a.stats && lane == 0) {
         const int slot = (int)(blockIdx.x % kStatSlots) * 4;
         atomicAdd(&a.stats[slot + 0], st_cand);
-        atomicAdd(&a.stats[slot + 1], st_cand * (unsigned long long)D_pad);
-        atomicAdd(&a.stats[slot + 2], st_surv);
+        atomicAdd(&a.stats[slot + 1], st_cand * (unsigned long long)(a.D_pad));
     }
 }
 
-template __global__ void batch_scan_kernel<true, 1>(BatchArgs);
-template __global__ void batch_scan_kernel<true, 2>(BatchArgs);
-template __global__ void batch_scan_kernel<true, 3>(BatchArgs);
-template __global__ void batch_scan_kernel<true, 4>(BatchArgs);
-template __global__ void batch_scan_kernel<false, 1>(BatchArgs);
-template __global__ void batch_scan_kernel<false, 2>(BatchArgs);
-template __global__ void batch_scan_kernel<false, 3>(BatchArgs);
-template __global__ void batch_scan_kernel<false, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<1, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<2, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<3, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<4, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<1, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<2, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<3, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<4, 16>(BatchArgs);
 
 // ---------------------------------------------------------------------------------------------
 // Lower-bound pass.
@@ -1000,15 +808,6 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     if (valid) a.lbr[p] = L;
 }
 
-// Global -> LDS without registers: lane i's 16 (or 4) bytes land at lds + 16 i (4 i).
-__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
-}
 
 // Pass B, every probe: units and wave mapping as in batch_scan_kernel.  Block b + 1's code
 // cells and row scalars (A_lo, r) move global -> LDS directly (no staging registers) while the

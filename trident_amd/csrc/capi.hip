@@ -270,16 +270,18 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
     }
 }
 
-// Persistent grid of a batched-scan variant: as many workgroups as are resident at once (CUs x
-// the occupancy its registers and LDS allow), rounded to a multiple of 8 so every XCD gets the
-// same number; cached per device and variant.
-template <bool UB, int KS>
+// Seeding pass: ub_scan_kernel<KS, M> (M = per-lane list length, 4 when K <= 16);
+// lower-bound pass: lb_scan_kernel<KS>.
+template <bool UB, int KS, int M>
 const void* batch_kernel_ptr() {
-    if constexpr (UB) return reinterpret_cast<const void*>(&batch_scan_kernel<true, KS>);
+    if constexpr (UB) return reinterpret_cast<const void*>(&ub_scan_kernel<KS, M>);
     else return reinterpret_cast<const void*>(&lb_scan_kernel<KS>);
 }
 
-template <bool UB, int KS>
+// Persistent grid of a batched-scan variant: as many workgroups as are resident at once (CUs x
+// the occupancy its registers and LDS allow), rounded to a multiple of 8 so every XCD gets the
+// same number; cached per device and variant.
+template <bool UB, int KS, int M>
 unsigned persistent_grid() {
     static int cached[64] = {0};
     int dev = 0;
@@ -289,8 +291,8 @@ unsigned persistent_grid() {
         if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
             cu < 1)
             cu = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, batch_kernel_ptr<UB, KS>(), kBlock,
-                                                         0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, batch_kernel_ptr<UB, KS, M>(),
+                                                         kBlock, 0) != hipSuccess ||
             per_cu < 1)
             per_cu = 2;
         cached[dev] = std::max(8, ((cu * per_cu + 7) / 8) * 8);
@@ -298,14 +300,16 @@ unsigned persistent_grid() {
     return (unsigned)cached[dev];
 }
 
-// Upper-bound pass: batch_scan_kernel<true>; lower-bound pass: lb_scan_kernel.
 template <bool UB, int KS>
 int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
     if constexpr (UB) {
-        batch_scan_kernel<true, KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
-        return check_launch("batch_scan_kernel");
+        if (b.K <= 16)
+            ub_scan_kernel<KS, 4><<<persistent_grid<true, KS, 4>(), kBlock, 0, st>>>(b);
+        else
+            ub_scan_kernel<KS, 16><<<persistent_grid<true, KS, 16>(), kBlock, 0, st>>>(b);
+        return check_launch("ub_scan_kernel");
     } else {
-        lb_scan_kernel<KS><<<persistent_grid<UB, KS>(), kBlock, 0, st>>>(b);
+        lb_scan_kernel<KS><<<persistent_grid<false, KS, 0>(), kBlock, 0, st>>>(b);
         return check_launch("lb_scan_kernel");
     }
 }

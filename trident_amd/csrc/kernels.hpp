@@ -237,8 +237,8 @@ __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int
 
 __global__ void tau_to_f32_kernel(const double* tau, float* out, int B);
 
-template <bool UB_PASS, int KS>
-__global__ void batch_scan_kernel(BatchArgs a);
+template <int KS, int M>
+__global__ void ub_scan_kernel(BatchArgs a);
 
 // Survivors a wave of lb_scan_kernel queues in LDS before appending them.
 constexpr int kLbQ = 64;
