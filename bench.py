@@ -35,7 +35,7 @@ METRIC = "QPS at 100% exact top-10, 1×MI355X; achieved HBM GB/s vs peak"  # BAS
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix throughput
 PROFILE_TRAFFIC = {1: os.path.join(ROOT, "profiles", "pair_scan_cfg2_traffic.json"),
-                   2: os.path.join(ROOT, "profiles", "batch_scan_cfg2_traffic.json")}
+                   2: os.path.join(ROOT, "profiles", "lb_scan_cfg2_traffic.json")}
 
 
 def log(*a):
@@ -172,7 +172,7 @@ def main():
         # pass B scans every probed (query, vector) pair: D_pad int8 MACs per weight plane
         ops_alg = 4 * bytes_all
         achieved = ops_alg / t_scan / 1e12
-        roof = {"bound": "mfma", "kernel": "batch_scan_kernel<false, KS> (pass B, int8 matrix cores)",
+        roof = {"bound": "mfma", "kernel": "lb_scan_kernel<KS> (pass B, int8 matrix cores)",
                 "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": round(achieved / INT8_PEAK_TOPS, 4), "ops_alg_per_launch": ops_alg}
         log(f"pass-B scan: {ops_alg / 1e12:.2f} T int8 ops in {stage['pass2_scan_ms']:.3f} ms -> {achieved:,.1f} TOP/s "

@@ -682,11 +682,12 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
             tau_to_f32_kernel<<<(B + 255) / 256, 256, 0, st>>>(w.tau64, out->tau_sq, B);
             if ((rc = check_launch("tau_to_f32_kernel"))) return rc;
         }
-        if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
+        // the lower-bound constants follow from tau (part of the seeding pass's merge stage)
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
         lb_prep_kernel<<<(unsigned)((w.max_groups + kBlock / kGroupQ - 1) / (kBlock / kGroupQ)),
                          kBlock, 0, st>>>(b);
         if ((rc = check_launch("lb_prep_kernel"))) return rc;
+        if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
         // pass B over every probe: lower bound, exact refine, append <= tau
         b.unit_end = 2 * ix->nlist;
         b.ctr = w.unit_ctr + 8 * kCtrStride;
