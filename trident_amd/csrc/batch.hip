@@ -195,24 +195,29 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
 
 // Exact test of the listed survivors, in place: slot s of query q holds a sorted position on
 // entry and (key, original id) on exit, or (kKeyInvalid, kIdInvalid) when the canonical
-// float64 distance exceeds tau[q].  One wave per query, one survivor per lane; each lane walks
-// its own row in dimension order with 16-byte loads.  An overflowed list (count > cap) is left
-// alone: the merge rescans that query's probes exhaustively.
+// float64 distance exceeds tau[q].  One wave per (query, 64-slot chunk of its list), one
+// survivor per lane (a query with many survivors spreads over many waves); each lane walks its
+// own row in dimension order with 16-byte loads, against the query row staged in LDS (the
+// batched route has D <= 256).  An
+// overflowed list (count > cap) is left alone: the merge rescans that query's probes
+// exhaustively.
 __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int B) {
-    const int lane = threadIdx.x & 63;
-    const int q = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
+    __shared__ __align__(16) float s_q[kWavesPerBlock][256];
+    const int lane = threadIdx.x & 63, wid = (int)(threadIdx.x >> 6);
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + wid);
     if (q >= B) return;
     const int cnt = a.cand_cnt[q];
-    if (cnt > a.cap) return;
+    if (cnt > a.cap || (int)blockIdx.y * kWave >= cnt) return;
     const double tau = a.tau[q];
-    const int D = a.D;
-    const float* qr = a.xq + (size_t)q * D;
+    const int D = a.D;  // <= D_pad <= 256 on the batched route
+    for (int d = lane; d < D; d += kWave) s_q[wid][d] = a.xq[(size_t)q * D + d];
+    __builtin_amdgcn_wave_barrier();
+    const float* qr = s_q[wid];
     uint64_t* ck = a.cand_key + (size_t)q * a.cap;
     int32_t* ci = a.cand_id + (size_t)q * a.cap;
-    const bool vec4 = (D & 3) == 0 && ((reinterpret_cast<uintptr_t>(a.xb) |
-                                         reinterpret_cast<uintptr_t>(a.xq)) & 15) == 0;
+    const bool vec4 = (D & 3) == 0 && (reinterpret_cast<uintptr_t>(a.xb) & 15) == 0;
     unsigned long long ins = 0;
-    for (int s = lane; s < cnt; s += kWave) {
+    for (int s = (int)blockIdx.y * kWave + lane; s < cnt; s += kWave * (int)gridDim.y) {
         const int pos = ci[s];
         const float* xr = a.xb + (size_t)pos * D;
         double acc = 0.0;

@@ -693,8 +693,11 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.ctr = w.unit_ctr + 8 * kCtrStride;
         if ((rc = launch_batch<false>(b, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
-        refine_survivors_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
-                                  st>>>(b, B);
+        // one wave per (query, 64-slot chunk of its list): a query with many survivors spreads
+        // over many waves
+        refine_survivors_kernel<<<dim3((unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock),
+                                       (unsigned)((cap + kWave - 1) / kWave)),
+                                  kBlock, 0, st>>>(b, B);
         if ((rc = check_launch("refine_survivors_kernel"))) return rc;
         m.use_prev = 0;
         m.out_d = out->topk_d;
