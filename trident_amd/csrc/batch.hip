@@ -472,14 +472,30 @@ __device__ __forceinline__ int lb_thr(float A, float r, float tq, float inv_c1) 
     return r <= 3.0e38f ? (int)v : INT_MAX;
 }
 
-// Global -> LDS without registers: lane i's 16 (or 4) bytes land at lds + 16 i (4 i).
-__device__ __forceinline__ void load_lds16(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+// Global -> LDS without registers: lane i's 16 (or 4) bytes, read from base + off (base
+// wave-uniform, off per lane), land at lds + 16 i (4 i).  Written as inline asm on purpose:
+// the compiler tracks its own direct loads by LDS object and, when it cannot tell two halves
+// of one array apart, makes every LDS read wait for all loads in flight, which stalls each
+// block's first tile on the next block's loads.  It does not see these, so the callers wait
+// themselves (vmcnt(0) before the barrier that publishes a block); the compiler's waits for
+// its own global loads only grow more conservative (the counter retires in order).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
-__device__ __forceinline__ void load_lds4(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)g,
-                                     (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+// M0 (the LDS address of the load, latched at issue) is saved and restored around it.
+__device__ __forceinline__ void load_lds16(const void* base, uint32_t off, const void* lds) {
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
+}
+__device__ __forceinline__ void load_lds4(const void* base, uint32_t off, const void* lds) {
+    uint32_t keep;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
+        "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+        : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
 }
 
 // Pass A (seeding), the first p_init probes: for every query of a unit the K-th smallest upper
@@ -623,16 +639,16 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
 #pragma unroll
             for (int jj = 0; jj < KS; ++jj)
                 if (wid + 4 * jj < G16)
-                    load_lds16(base + (size_t)(4 * jj) * T + lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
+                    load_lds16(base + (size_t)(4 * jj) * T, 16u * lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
             cw += kBlkV;
             if (cw == T) {
                 cw = 0;
                 ++ct;
             }
-            if (wid == 0) {
-                const float* ar = reinterpret_cast<const float*>(a.vec_Ar + v0 + min(blk0 + lane, ve - 1));
-                load_lds4(ar, s_A[buf]);
-                load_lds4(ar + 1, s_r[buf]);
+            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
+                const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
+                load_lds4(a.vec_Ar + v0, off, s_A[buf]);
+                load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
             }
         };
         const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
@@ -970,18 +986,15 @@ void lb_scan_kernel(BatchArgs a) {
                                          fmaf(c.x, (float)S[r], c.z));
             }
             if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
-            // rare: the float test for the integer test's passes (rows past the slice never
-            // pass the integer test: thr = INT_MAX), then queue the survivors
-            const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
-            const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
-            const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
-            const float4 c = s_qf[wid][j];
+            // rare: queue the tile's survivors.  The integer test is implied by the exact
+            // condition, so nothing is lost, and it passes hardly more rows than the float test
+            // would (refinement decides); rows past the slice never pass (thr = INT_MAX, and
+            // |acc + kq| < 2^31 - 1), the row check below only makes that explicit.
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const bool pass = hasq && ((sm[r] >> lane) & 1ull) &&
-                                  fmaf(c.y, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
-                                      fmaf(c.x, (float)(S[r] - kq), c.z);
+                const bool pass = hasq && ((sm[r] >> lane) & 1ull) && li0 + 4 * g + r < ve;
                 const uint64_t pm = __ballot(pass);
+                if (pm == 0ull) continue;
                 if (nsq + __popcll(pm) > kLbQ) flush();
                 if (pass) {
                     const int idx = __builtin_amdgcn_mbcnt_hi(
@@ -1000,16 +1013,16 @@ void lb_scan_kernel(BatchArgs a) {
 #pragma unroll
             for (int jj = 0; jj < KS; ++jj)
                 if (wid + 4 * jj < G16)
-                    load_lds16(base + (size_t)(4 * jj) * T + lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
+                    load_lds16(base + (size_t)(4 * jj) * T, 16u * lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
             cw += kBlkV;
             if (cw == T) {
                 cw = 0;
                 ++ct;
             }
             if (wid == 0) {  // rows past the slice read the slice's last row (never used)
-                const float* ar = reinterpret_cast<const float*>(a.vec_Ar + v0 + min(blk0 + lane, ve - 1));
-                load_lds4(ar, s_A[buf]);
-                load_lds4(ar + 1, s_r[buf]);
+                const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
+                load_lds4(a.vec_Ar + v0, off, s_A[buf]);
+                load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
             }
         };
         const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
@@ -1026,9 +1039,14 @@ void lb_scan_kernel(BatchArgs a) {
                 if (int_ok) {
                     const float A = s_A[buf][lane], r = s_r[buf][lane];
                     s_thr[buf][wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
-                    for (int t = rr; t < kBlkV / 16; t += R) {
-                        if (blk0 + t * 16 >= ve) break;
-                        tile(std::true_type{}, buf, t, blk0 + t * 16);
+                    if (R == 1 && blk0 + kBlkV <= ve) {  // the common case: straight-line tiles
+#pragma unroll
+                        for (int t = 0; t < kBlkV / 16; ++t) tile(std::true_type{}, buf, t, blk0 + t * 16);
+                    } else {
+                        for (int t = rr; t < kBlkV / 16; t += R) {
+                            if (blk0 + t * 16 >= ve) break;
+                            tile(std::true_type{}, buf, t, blk0 + t * 16);
+                        }
                     }
                 } else {
                     for (int t = rr; t < kBlkV / 16; t += R) {
