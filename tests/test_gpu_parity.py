@@ -48,14 +48,41 @@ def norm96(dev):
     return b, xq.numpy()
 
 
+def _check_probes(b, xq, dev, nprobe):
+    b.ix.search(_q(xq, dev), nprobe, mode=10, k=10)
+    torch.cuda.synchronize()
+    got = b.ix.probe_cids_buf[: len(xq), :nprobe].cpu().numpy()
+    got_d = b.ix.probe_dqcs_buf[: len(xq), :nprobe].cpu().numpy()
+    ref, ref_d = O.coarse_probe(xq, b.centroids_idx, nprobe)
+    assert np.array_equal(got, ref), f"nprobe={nprobe}"
+    assert np.array_equal(got_d, np.sqrt(ref_d).astype(np.float32)), f"nprobe={nprobe}"
+
+
 def test_coarse_probe_matches_oracle(gmm, dev):
-    b, xq = gmm
     for nprobe in (1, 7, 16, 96):
-        b.ix.search(_q(xq, dev), nprobe, mode=10, k=10)
-        torch.cuda.synchronize()
-        got = b.ix.probe_cids_buf[: len(xq), :nprobe].cpu().numpy()
-        ref, _ = O.coarse_probe(xq, b.centroids_idx, nprobe)
-        assert np.array_equal(got, ref), f"nprobe={nprobe}"
+        _check_probes(*gmm, dev, nprobe)
+
+
+@pytest.mark.parametrize("nlist", [2048, 4096])
+def test_band_front_end_wide_nlist(dev, nlist):
+    """The matrix-core band front end with 32 and 64 approximations per lane."""
+    xb, xq = datagen.cfg4(N=3 * nlist, D=96, B=96, n_centers=nlist, seed=43)
+    b = build_index(xb, nlist, dev, max_batch=128, max_nprobe=128)
+    for nprobe in (1, 64, 100, 128):
+        _check_probes(b, xq.numpy(), dev, nprobe)
+
+
+def test_band_front_end_far_from_origin(dev):
+    """Data offset far from the origin: the float32 matrix-core approximation loses most of its
+    digits to cancellation, the band widens to many (or all) centroids, and the selection must
+    still be the float64 oracle's, ties included."""
+    xb, xq = datagen.cfg1(N=20_000, D=128, B=100, n_centers=128, seed=44)
+    b = build_index(xb + 3.0e4, 256, dev, max_batch=128, max_nprobe=128)
+    xq = (xq + 3.0e4).numpy()
+    dup = np.repeat(xq[:4], 2, axis=0)  # duplicated queries: identical rows
+    xq = np.concatenate([xq, dup]).astype(np.float32)
+    for nprobe in (5, 64, 128):
+        _check_probes(b, xq, dev, nprobe)
 
 
 def test_coarse_probe_selectors_all_widths(dev):

@@ -95,6 +95,12 @@ struct Workspace {
     LbRec* lbr;                      // [B * nprobe]
     double* cbound;                  // [nlist, kCbStride]
     double* qep;                     // [B]
+    float* qt32;                     // band front end: queries, matrix-core tile layout
+    float* qn32;                     // [B] their squared norms
+    float* cm32;                     // [nlist, Dq] centroid-major zero-padded centroids
+    float* cmt32;                    // the centroids in the matrix-core tile layout
+    float* cn32;                     // [nlist] their squared norms
+    unsigned long long* cmax2;       // largest centroid squared norm (float64 bits)
     size_t bytes;
 };
 
@@ -143,6 +149,13 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.lbr = c.take<LbRec>(B * nprobe);
     w.cbound = c.take<double>(kCbStride * (int64_t)ix->nlist);
     w.qep = c.take<double>(B);
+    const int64_t Dq = band_dq(ix->D);
+    w.qt32 = c.take<float>((B + 15) / 16 * 16 * Dq);
+    w.qn32 = c.take<float>(B);
+    w.cm32 = c.take<float>((int64_t)ix->nlist * Dq);
+    w.cmt32 = c.take<float>(((int64_t)ix->nlist + 15) / 16 * 16 * Dq);
+    w.cn32 = c.take<float>(ix->nlist);
+    w.cmax2 = c.take<unsigned long long>(1);
     w.bytes = c.off;
     return w;
 }
@@ -368,6 +381,39 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
         w.xrot64, w.xrot32, w.qerr, rotate ? 1 : 0);
     int rc = check_launch("prep_queries_kernel");
     if (rc) return rc;
+    if (nprobe <= 128 && ix->nlist <= kBandMaxNlist) {  // band front end
+        const int Dq = band_dq(ix->D);
+        fill_u64_kernel<<<1, 64, 0, st>>>(w.cmax2, 0ull, 1);
+        if ((rc = check_launch("fill_u64_kernel"))) return rc;
+        pad_centroids_kernel<<<(unsigned)((ix->nlist + 63) / 64), 256, 0, st>>>(
+            ix->W_combined, ldw, ix->nlist, ix->D, Dq, w.cm32, w.cmt32, w.cn32, w.cmax2);
+        if ((rc = check_launch("pad_centroids_kernel"))) return rc;
+        pad_queries_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
+                             st>>>(xq, B, ix->D, Dq, w.qt32, w.qn32);
+        if ((rc = check_launch("pad_queries_kernel"))) return rc;
+        float* a32 = reinterpret_cast<float*>(w.cd64);  // [B, nlist] approximations
+        coarse_gemm_kernel<<<dim3((unsigned)((B + 63) / 64), (unsigned)((ix->nlist + 255) / 256)),
+                             kBlock, 0, st>>>(w.qt32, w.qn32, B, w.cmt32, w.cn32, ix->nlist, Dq,
+                                              a32);
+        if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
+        const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
+        const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= 2048 ? 32 : 64;
+#define TRIDENT_BAND_LAUNCH(KPV, VV)                                                             \
+    select_band_kernel<KPV, VV><<<grid, kBlock, 0, st>>>(                                       \
+        a32, w.xq64, w.cm32, w.cmax2, B, ix->nlist, ix->D, Dq, nprobe, w.probe_cids,            \
+        w.probe_dqcs, nprobe, probe_cids, probe_dqcs, ld)
+        if (nprobe <= 64) {
+            if (V == 16) TRIDENT_BAND_LAUNCH(64, 16);
+            else if (V == 32) TRIDENT_BAND_LAUNCH(64, 32);
+            else TRIDENT_BAND_LAUNCH(64, 64);
+        } else {
+            if (V == 16) TRIDENT_BAND_LAUNCH(128, 16);
+            else if (V == 32) TRIDENT_BAND_LAUNCH(128, 32);
+            else TRIDENT_BAND_LAUNCH(128, 64);
+        }
+#undef TRIDENT_BAND_LAUNCH
+        return check_launch("select_band_kernel");
+    }
     constexpr int qpb = kCoarseQW * kWavesPerBlock;
     coarse_dist_kernel<<<dim3((ix->nlist + 64 * kCoarseNC - 1) / (64 * kCoarseNC),
                                  (B + qpb - 1) / qpb),

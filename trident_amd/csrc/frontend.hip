@@ -565,4 +565,395 @@ __global__ __launch_bounds__(256) void scatter_pairs_lds_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Band front end (nlist <= 4096, nprobe <= 128): approximate coarse distances on the matrix
+// cores with a rigorous error bound, then the canonical float64 distance for the band of
+// centroids that can still be among the nprobe nearest, and the exact (d, cid) selection.
+//
+// For float32 vectors q, c (exact reals) with d = |q - c|^2, nq = |q|^2, nc = |c|^2:
+//   s' = the matrix-core float32 dot product of q and c in any summation order, each product
+//        and addition with relative error <= 2^-23 (round-to-nearest gives 2^-24; the factor
+//        two also covers truncation): |s' - q.c| <= kappa sum |q_d c_d| <= kappa (nq + nc) / 2,
+//        kappa = (Dq + 2) 2^-23 (first-order bound of recursive summation over Dq terms);
+//   a  = fma(-2, s', fl(nq32 + nc32)) with nq32, nc32 the float64 norms rounded to float32:
+//        the three roundings add at most 2^-22 (nq + nc) (1 + 2^-20);
+//   d64, the canonical float64 chain, is within 2^-44 (nq + nc) of d.
+// So |a - d64| <= E = (kappa + 2^-21) (nq + nc_max) (1 + 2^-10) for every centroid.  If T is
+// any value with at least nprobe approximations a <= T, then at least nprobe centroids have
+// d64 <= T + E, so the nprobe-th smallest d64 is <= T + E and every centroid of the true
+// (d, cid) top-nprobe -- ties included -- has a <= T + 2E.  Those are the band; their exact d64
+// decide the selection, exactly as a full float64 pass would.
+
+// Matrix-core tile layout of zero-padded float32 rows (Dq = D rounded up to 16, S = Dq / 4):
+// for rows 16 t .. 16 t + 15, float4 number (t S/4 + j) 64 + lane holds, for row 16 t + lane % 16
+// and lane group g = lane / 16, dimensions g S + 4 j .. g S + 4 j + 3 -- the A (or B) operands
+// of four consecutive v_mfma_f32_16x16x4f32 steps, so one float4 load of a wave is 1 KiB
+// contiguous.
+__device__ __forceinline__ size_t mfma_tile_offset(int row, int d, int S) {
+    const int g = d / S, sd = d - g * S;
+    return ((((size_t)(row >> 4) * (S >> 2) + (sd >> 2)) * kWave + (row & 15) + 16 * g) << 2) +
+           (sd & 3);
+}
+
+// Queries in the tile layout (qt32) and their squared norms (float64 sum, float32 copy).
+__global__ __launch_bounds__(256) void pad_queries_kernel(const float* __restrict__ xq, int B,
+                                                          int D, int Dq,
+                                                          float* __restrict__ qt32,
+                                                          float* __restrict__ qn32) {
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
+    if (q >= B) return;
+    const int S = Dq >> 2;
+    double acc = 0.0;
+    for (int d = lane; d < Dq; d += kWave) {
+        const float v = d < D ? xq[(size_t)q * D + d] : 0.0f;
+        qt32[mfma_tile_offset(q, d, S)] = v;
+        acc = fma((double)v, (double)v, acc);
+    }
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) acc += __shfl_xor(acc, o, kWave);
+    if (lane == 0) qn32[q] = (float)acc;
+}
+
+// Centroids (c_d = -0.5f W[d, c], the same float32 values the float64 chains use) as
+// centroid-major zero-padded rows cm32 [nlist, Dq] and in the tile layout (cmt32), their
+// squared norms cn32 (float64 partial sums rounded to float32: only the error bound and the
+// approximations use them) and the largest squared norm (float64 bit pattern, atomicMax into a
+// cell the caller zeroes).  grid ceil(nlist / 64), block 256: 64 centroids per block,
+// transposed through LDS in 64-dim tiles (W rows read and cm32 rows written coalesced).
+__global__ __launch_bounds__(256) void pad_centroids_kernel(const float* __restrict__ W, int ldw,
+                                                            int nlist, int D, int Dq,
+                                                            float* __restrict__ cm32,
+                                                            float* __restrict__ cmt32,
+                                                            float* __restrict__ cn32,
+                                                            unsigned long long* __restrict__ cmax2) {
+    __shared__ float s_t[64][65];
+    __shared__ double s_n[4][64];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const int c0 = blockIdx.x * 64;
+    const int S = Dq >> 2;
+    double nrm = 0.0;  // centroid c0 + tx over dims ty, ty + 4, ...
+    for (int d0 = 0; d0 < Dq; d0 += 64) {
+#pragma unroll
+        for (int r = ty; r < 64; r += 4) {  // s_t[d][c] = centroid c0 + c, dim d0 + d
+            const int d = d0 + r, c = c0 + tx;
+            const float v = (d < D && c < nlist) ? -0.5f * W[(size_t)d * ldw + c] : 0.0f;
+            s_t[r][tx] = v;
+            nrm = fma((double)v, (double)v, nrm);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = ty; r < 64; r += 4) {  // centroid c0 + r, dim d0 + tx
+            const int c = c0 + r, d = d0 + tx;
+            if (c < nlist && d < Dq) {
+                const float v = s_t[tx][r];
+                cm32[(size_t)c * Dq + d] = v;
+                cmt32[mfma_tile_offset(c, d, S)] = v;
+            }
+        }
+        __syncthreads();
+    }
+    s_n[ty][tx] = nrm;
+    __syncthreads();
+    if (ty == 0) {
+        double n = 0.0;
+        if (c0 + tx < nlist) {
+            n = (s_n[0][tx] + s_n[1][tx]) + (s_n[2][tx] + s_n[3][tx]);
+            cn32[c0 + tx] = (float)n;
+        }
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) n = fmax(n, __shfl_xor(n, o, kWave));
+        // one atomic per block: same-address atomics serialise in L2
+        if (tx == 0) atomicMax(cmax2, (unsigned long long)__double_as_longlong(n));
+    }
+}
+
+// grid (ceil(B / 64), ceil(nlist / 256)), block 256: each wave 16 queries (one query tile), all
+// four waves the same 16 centroid tiles in the same order.  v_mfma_f32_16x16x4f32 with query
+// rows as A (16 x 4) and centroids as B (4 x 16), operands straight from the tile layouts: a
+// chunk of 32 k-steps is 8 + 8 coalesced float4 loads, issued whole before its 32 MFMAs; steps
+// past S are zero (clamped loads, no branch among the MFMAs).
+// a32[q, c] = fma(-2, dot, nq32 + nc32).
+__global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restrict__ qt32,
+                                                          const float* __restrict__ qn32, int B,
+                                                          const float* __restrict__ cmt32,
+                                                          const float* __restrict__ cn32,
+                                                          int nlist, int Dq,
+                                                          float* __restrict__ a32) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m = lane & 15, g = lane >> 4;
+    const int qtile = blockIdx.x * 4 + wid;
+    const int qb = qtile * 16;
+    if (qb >= B) return;
+    const int F = Dq >> 4;  // float4 per lane and row tile (= S / 4)
+    const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
+    const bool qv = qb + m < B;
+#pragma unroll 1
+    for (int t = 0; t < 16; ++t) {
+        const int n0 = blockIdx.y * 256 + t * 16;
+        if (n0 >= nlist) break;
+        const bool cv = n0 + m < nlist;
+        const float4* ct = reinterpret_cast<const float4*>(cmt32) + (size_t)(n0 >> 4) * F * kWave +
+                           lane;
+        // four independent accumulator chains (k-steps j mod 4), summed at the end: the error
+        // bound holds for any summation order
+        f4 acc4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 1
+        for (int f0 = 0; f0 < F; f0 += 8) {
+            float4 av[8], bv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool in = f0 + j < F;
+                const size_t o = (size_t)(in ? f0 + j : 0) * kWave;
+                av[j] = qt[o];
+                bv[j] = ct[o];
+                if (!in || !qv) av[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (!cv) bv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                f4& acc = acc4[j & 3];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, bv[j].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, bv[j].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, bv[j].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc, 0, 0, 0);
+            }
+        }
+        // matrix-core results: wait states before the first VALU read, fenced
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7");
+        __builtin_amdgcn_sched_barrier(0);
+        const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+        const int c = n0 + m;
+        if (c < nlist) {
+            const float ncv = cn32[c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = qb + 4 * g + i;
+                if (q < B) a32[(size_t)q * nlist + c] = fmaf(-2.0f, acc[i], qn32[q] + ncv);
+            }
+        }
+    }
+}
+
+// One wave per query: V approximations per lane (nlist <= 64 V).  T comes from a bisection on
+// the approximations (count(a <= hi) >= nprobe is kept invariant), and every centroid of the
+// band a <= T + 2E gets its canonical float64 distance (t = q_d - c_d, acc = fma(t, t, acc) in
+// dimension order -- the oracle's chain).  A band of <= 128 (the usual case: a few more than
+// nprobe) is ranked by counting, each entry against all others in (d, cid) order; a wider one
+// streams through the (d, cid) register list 64 centroids at a time.  Outputs as
+// select_probes_wave_kernel.
+template <int KP, int V>
+__global__ __launch_bounds__(256) void select_band_kernel(
+    const float* __restrict__ a32, const double* __restrict__ xq64, const float* __restrict__ cm32,
+    const unsigned long long* __restrict__ cmax2, int B, int nlist, int D, int Dq, int nprobe,
+    int32_t* __restrict__ out_cids, float* __restrict__ out_dqcs, int ld,
+    int32_t* __restrict__ out2_cids, float* __restrict__ out2_dqcs, int ld2) {
+    __shared__ int32_t s_band[kWavesPerBlock][2 * kWave];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int q = blockIdx.x * kWavesPerBlock + wid;
+    if (q >= B) return;
+    const double* qrow = xq64 + (size_t)q * D;
+    float v[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        const int c = i * kWave + lane;
+        v[i] = c < nlist ? a32[(size_t)q * nlist + c] : INFINITY;
+    }
+    // the error bound E (float64, then rounded up to float32)
+    double nq = 0.0;
+    for (int d = lane; d < D; d += kWave) nq = fma(qrow[d], qrow[d], nq);
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) nq += __shfl_xor(nq, o, kWave);
+    const double kappa = (double)(Dq + 2) * 0x1p-23;
+    const double E = (kappa + 0x1p-21) * (nq + __longlong_as_double((long long)*cmax2)) *
+                         (1.0 + 0x1p-10) + 1e-30;
+    const float Ef = __double2float_ru(E);
+    // bisection: count(a <= hi) >= nprobe throughout.  hi starts at the largest lane minimum
+    // when every lane holds a value and nprobe <= 64 (then >= 64 values lie at or below it),
+    // else at the largest value; counts come from ballots (no cross-lane shuffles).
+    float lmin = INFINITY, lmax = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        lmin = fminf(lmin, v[i]);
+        if (v[i] < INFINITY) lmax = fmaxf(lmax, v[i]);
+    }
+    float lo = lmin, hi = lmax, t0 = lmin;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        lo = fminf(lo, __shfl_xor(lo, o, kWave));
+        hi = fmaxf(hi, __shfl_xor(hi, o, kWave));
+        t0 = fmaxf(t0, __shfl_xor(t0, o, kWave));
+    }
+    if (nprobe <= kWave && t0 < INFINITY) hi = t0;
+    auto count_le = [&](float x) {
+        int n = 0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) n += __popcll(__ballot(v[i] <= x));
+        return n;
+    };
+    for (int it = 0; it < 40 && hi - lo > Ef; ++it) {
+        const float mid = lo + 0.5f * (hi - lo);
+        if (!(mid > lo && mid < hi)) break;
+        const int n = count_le(mid);
+        if (n >= nprobe) {
+            hi = mid;
+            if (n <= nprobe + 2) break;
+        } else {
+            lo = mid;
+        }
+    }
+    // E carries a 2^-10 relative margin, which covers the float64 rounding of this sum
+    const float thr = __double2float_ru((double)hi + 2.0 * E);
+    int32_t* band = s_band[wid];
+    auto emit = [&](int rank, uint64_t key, int32_t cid) {
+        const float dq = (float)sqrt(dist_of(key));
+        out_cids[(size_t)q * ld + rank] = cid;
+        out_dqcs[(size_t)q * ld + rank] = dq;
+        if (out2_cids) out2_cids[(size_t)q * ld2 + rank] = cid;
+        if (out2_dqcs) out2_dqcs[(size_t)q * ld2 + rank] = dq;
+    };
+    // canonical float64 distance of centroid c: dimension order, t = q_d - c_d, fma(t, t, acc).
+    // The row arrives in chunks of 64 (then 16) dims whose loads are all issued before their
+    // first use: one memory round trip per chunk instead of one per 4 dims.
+    auto exact = [&](int c) {
+        const float* crow = cm32 + (size_t)c * Dq;
+        double acc = 0.0;
+        int d = 0;
+        auto chunk = [&](auto nq4) {
+            constexpr int N4 = decltype(nq4)::value;
+            float4 cv[N4];
+#pragma unroll
+            for (int k = 0; k < N4; ++k) cv[k] = *reinterpret_cast<const float4*>(crow + d + 4 * k);
+#pragma unroll
+            for (int k = 0; k < N4; ++k) {
+                double t = qrow[d + 4 * k] - (double)cv[k].x;
+                acc = fma(t, t, acc);
+                t = qrow[d + 4 * k + 1] - (double)cv[k].y;
+                acc = fma(t, t, acc);
+                t = qrow[d + 4 * k + 2] - (double)cv[k].z;
+                acc = fma(t, t, acc);
+                t = qrow[d + 4 * k + 3] - (double)cv[k].w;
+                acc = fma(t, t, acc);
+            }
+            d += 4 * N4;
+        };
+        while (d + 64 <= D) chunk(std::integral_constant<int, 16>{});
+        while (d + 16 <= D) chunk(std::integral_constant<int, 4>{});
+        for (; d + 4 <= D; d += 4) {
+            const float4 cv = *reinterpret_cast<const float4*>(crow + d);
+            double t = qrow[d] - (double)cv.x;
+            acc = fma(t, t, acc);
+            t = qrow[d + 1] - (double)cv.y;
+            acc = fma(t, t, acc);
+            t = qrow[d + 2] - (double)cv.z;
+            acc = fma(t, t, acc);
+            t = qrow[d + 3] - (double)cv.w;
+            acc = fma(t, t, acc);
+        }
+        for (; d < D; ++d) {
+            const double t = qrow[d] - (double)crow[d];
+            acc = fma(t, t, acc);
+        }
+        return acc;
+    };
+    const int mband = thr < INFINITY ? count_le(thr) : nlist + 1;
+    if (mband <= 2 * kWave) {
+        // the common case: the band fits two entries per lane.  Compact it, compute the exact
+        // distances, and rank every entry by counting the entries before it in (d, cid) order.
+        int nb = 0;
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const bool take = v[i] <= thr;  // thr is finite: centroids past nlist hold +inf
+            const uint64_t mk = __ballot(take);
+            if (take) band[nb + mask_rank(mk)] = i * kWave + lane;
+            nb += __popcll(mk);
+        }
+        wave_sync();
+        const bool h0 = lane < nb, h1 = kWave + lane < nb;
+        const int c0 = band[h0 ? lane : 0], c1 = band[h1 ? kWave + lane : 0];
+        const uint64_t k0 = h0 ? key_of(exact(c0)) : kKeyInvalid;
+        const uint64_t k1 = h1 ? key_of(exact(c1)) : kKeyInvalid;
+        int r0 = 0, r1 = 0;
+        if (nb <= kWave) {
+            for (int jl = 0; jl < nb; ++jl) {
+                const uint64_t kj = readlane_u64(k0, jl);
+                r0 += ent_less(kj, __builtin_amdgcn_readlane(c0, jl), k0, c0) ? 1 : 0;
+            }
+        } else {
+            for (int jl = 0; jl < kWave; ++jl) {
+                const uint64_t kj = readlane_u64(k0, jl);
+                const int32_t cj = __builtin_amdgcn_readlane(c0, jl);
+                r0 += ent_less(kj, cj, k0, c0) ? 1 : 0;
+                r1 += ent_less(kj, cj, k1, c1) ? 1 : 0;
+            }
+        }
+        for (int jl = 0; jl < nb - kWave; ++jl) {
+            const uint64_t kj = readlane_u64(k1, jl);
+            const int32_t cj = __builtin_amdgcn_readlane(c1, jl);
+            r0 += ent_less(kj, cj, k0, c0) ? 1 : 0;
+            r1 += ent_less(kj, cj, k1, c1) ? 1 : 0;
+        }
+        if (h0 && r0 < nprobe) emit(r0, k0, c0);
+        if (h1 && r1 < nprobe) emit(r1, k1, c1);
+        return;
+    }
+    // a wide band (data far from the origin): 64 band centroids at a time into a register list
+    WaveList<KP> L;
+    L.init();
+    int nb = 0;
+    auto refine = [&](int n) {
+        const bool has = lane < n;
+        const int c = band[has ? lane : 0];
+        const double dd = exact(c);
+        list_offer(L, nprobe, has ? key_of(dd) : kKeyInvalid, has ? c : kIdInvalid);
+    };
+    // the band, from the approximations again (L2; a rolled loop keeps one copy of refine)
+    const float* arow = a32 + (size_t)q * nlist;
+#pragma unroll 1
+    for (int i = 0; i < V; ++i) {
+        const int c = i * kWave + lane;
+        const bool take = c < nlist && arow[c] <= thr;
+        const uint64_t mk = __ballot(take);
+        if (take) band[nb + mask_rank(mk)] = i * kWave + lane;
+        nb += __popcll(mk);
+        if (nb >= kWave) {
+            wave_sync();
+            refine(kWave);
+            wave_sync();
+            const int rest = nb - kWave;  // <= 63 entries move down
+            const int moved = lane < rest ? band[kWave + lane] : 0;
+            wave_sync();
+            if (lane < rest) band[lane] = moved;
+            wave_sync();
+            nb = rest;
+        }
+    }
+    if (nb > 0) {
+        wave_sync();
+        refine(nb);
+    }
+    if (lane < nprobe) emit(lane, L.k0, L.i0);
+    if constexpr (KP == 128) {
+        if (kWave + lane < nprobe) emit(kWave + lane, L.k1, L.i1);
+    }
+}
+
+#define TRIDENT_SELECT_BAND(KP, V)                                                              \
+    template __global__ void select_band_kernel<KP, V>(                                         \
+        const float*, const double*, const float*, const unsigned long long*, int, int, int, int, \
+        int, int32_t*, float*, int, int32_t*, float*, int);
+TRIDENT_SELECT_BAND(64, 16)
+TRIDENT_SELECT_BAND(64, 32)
+TRIDENT_SELECT_BAND(64, 64)
+TRIDENT_SELECT_BAND(128, 16)
+TRIDENT_SELECT_BAND(128, 32)
+TRIDENT_SELECT_BAND(128, 64)
+#undef TRIDENT_SELECT_BAND
+
 }  // namespace trident

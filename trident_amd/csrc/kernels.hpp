@@ -176,6 +176,28 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs);
 
 constexpr int kGroupChunk = 8192;  // (query, probe) entries per block of the LDS grouping
+// band front end (frontend.hip)
+__global__ void pad_queries_kernel(const float* __restrict__ xq, int B, int D, int Dq,
+                                   float* __restrict__ qt32, float* __restrict__ qn32);
+__global__ void pad_centroids_kernel(const float* __restrict__ W, int ldw, int nlist, int D,
+                                     int Dq, float* __restrict__ cm32, float* __restrict__ cmt32,
+                                     float* __restrict__ cn32,
+                                     unsigned long long* __restrict__ cmax2);
+__global__ void coarse_gemm_kernel(const float* __restrict__ qt32, const float* __restrict__ qn32,
+                                   int B, const float* __restrict__ cmt32,
+                                   const float* __restrict__ cn32, int nlist, int Dq,
+                                   float* __restrict__ a32);
+template <int KP, int V>
+__global__ void select_band_kernel(const float* __restrict__ a32, const double* __restrict__ xq64,
+                                   const float* __restrict__ cm32,
+                                   const unsigned long long* __restrict__ cmax2, int B, int nlist,
+                                   int D, int Dq, int nprobe, int32_t* __restrict__ out_cids,
+                                   float* __restrict__ out_dqcs, int ld,
+                                   int32_t* __restrict__ out2_cids,
+                                   float* __restrict__ out2_dqcs, int ld2);
+constexpr int kBandMaxNlist = 4096;  // band front end: nlist <= 64 x 64 approximations per lane
+inline int band_dq(int D) { return (D + 15) & ~15; }
+
 constexpr int kCoarseQW = 4;       // queries per wave of coarse_dist_kernel
 constexpr int kCoarseNC = 2;       // centroids per lane of coarse_dist_kernel
 constexpr int kPrepQB = 2;         // queries per wave of prep_queries_kernel
