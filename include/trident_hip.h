@@ -74,6 +74,16 @@ typedef struct TridentIndexView {
                                         sq8_packed regrouped as 16-byte cells (dims 16 g ..
                                         16 g + 15 of one slot), every byte c stored as c ^ 0x80
                                         (c - 128 as int8); NULL disables the batched route */
+    /* Centroids for the matrix-core coarse pass, Dq = D rounded up to 16, c_d = -W_combined[d, c]
+     * / 2.  Optional (all or none): when cent_rows is NULL every search derives them from
+     * W_combined into its workspace.  No counterpart in the reference (its coarse GEMM reads
+     * W_coarse_only directly). */
+    const float* cent_rows;          /* [nlist, Dq] zero-padded rows */
+    const float* cent_tiles;         /* [ceil(nlist / 16) * 16 * Dq] matrix-core tile layout: float4
+                                        (t Dq/16 + j) 64 + l holds dims (l / 16) Dq/4 + 4 j .. + 3
+                                        of centroid 16 t + l % 16 */
+    const float* cent_norms;         /* [nlist] float32(sum_d c_d^2) */
+    double cent_norm_max;            /* max_c sum_d c_d^2 (float64) */
 } TridentIndexView;
 
 /* How mode 2 is executed.  Both are exact; they differ in speed only. */

@@ -218,3 +218,27 @@ def test_bounds_bracket_distance_cpu_restatement(hist_ix, gmm_ix):
                 d64 = ((xs[s:e] - q) ** 2).sum(1)
                 assert (lb.astype(np.float64) / lb_scale <= d64 * (1 + 1e-12)).all()
                 assert (ub.astype(np.float64) * ub_scale >= d64 * (1 - 1e-12)).all()
+
+
+def test_centroid_band_layouts_positions():
+    """The matrix-core tile layout of the centroids: float4 (t Dq/16 + j) 64 + l holds dims
+    (l / 16) Dq/4 + 4 j .. + 3 of centroid 16 t + l % 16 (zero past D and past nlist)."""
+    from trident_amd import ext as E
+    g = torch.Generator().manual_seed(5)
+    for D, nlist in ((96, 40), (128, 64), (20, 17)):
+        W = torch.randn((D, nlist + 32), generator=g)
+        rows, tiles, norms, nmax = E.centroid_band_layouts(W, nlist)
+        Dq = E.band_dq(D)
+        S = Dq // 4
+        cen = (-0.5 * W[:, :nlist]).t()
+        assert torch.equal(rows[:, :D], cen) and not rows[:, D:].any()
+        t4 = tiles.view(-1, 4)
+        for c in range(0, (nlist + 15) // 16 * 16, 3):
+            for d in range(0, Dq, 5):
+                gq, sd = divmod(d, S)
+                f = ((c // 16) * (S // 4) + sd // 4) * 64 + (c % 16) + 16 * gq
+                want = float(cen[c, d]) if c < nlist and d < D else 0.0
+                assert float(t4[f, sd % 4]) == want, (D, nlist, c, d)
+        n64 = (cen.double() ** 2).sum(1)  # summation order may differ in the last bit
+        assert torch.allclose(norms.double(), n64, rtol=1e-6, atol=0)
+        assert abs(nmax - float(n64.max())) <= 1e-12 * float(n64.max())

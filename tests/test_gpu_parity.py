@@ -63,6 +63,19 @@ def test_coarse_probe_matches_oracle(gmm, dev):
         _check_probes(*gmm, dev, nprobe)
 
 
+def test_band_front_end_derived_centroids(gmm, dev):
+    """Without the index's centroid layouts (view fields cent_*) each search derives them into
+    its workspace; the probes must be the oracle's either way."""
+    b, xq = gmm
+    keep = b.ix.cent_band
+    try:
+        b.ix.cent_band = None
+        for nprobe in (7, 64):
+            _check_probes(b, xq, dev, nprobe)
+    finally:
+        b.ix.cent_band = keep
+
+
 @pytest.mark.parametrize("nlist", [2048, 4096])
 def test_band_front_end_wide_nlist(dev, nlist):
     """The matrix-core band front end with 32 and 64 approximations per lane."""

@@ -29,6 +29,7 @@ class TridentIndexView(ctypes.Structure):
         ("xb_sorted", _P), ("orig_ids_sorted", _P),
         ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P), ("vec_Ar", _P),
         ("sq8_cells", _P),
+        ("cent_rows", _P), ("cent_tiles", _P), ("cent_norms", _P), ("cent_norm_max", _f64),
     ]
 
 

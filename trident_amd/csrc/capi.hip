@@ -179,6 +179,10 @@ int validate_index(const TridentIndexView* ix) {
     if (!(ix->rot_sq_min > 0.0) || !(ix->rot_sq_max >= ix->rot_sq_min))
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad rotation bounds [%g, %g]", ix->rot_sq_min,
                     ix->rot_sq_max);
+    if (ix->cent_rows && (!ix->cent_tiles || !ix->cent_norms || !(ix->cent_norm_max >= 0.0) ||
+                          !(ix->cent_norm_max < INFINITY)))
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT,
+                    "cent_rows needs cent_tiles, cent_norms and a finite cent_norm_max >= 0");
     if ((int64_t)ix->nlist * 8 > 150 * 1024)
         return fail(TRIDENT_ERR_UNSUPPORTED, "nlist=%d exceeds the LDS probe selector", ix->nlist);
     return TRIDENT_OK;
@@ -383,24 +387,33 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
     if (rc) return rc;
     if (nprobe <= 128 && ix->nlist <= kBandMaxNlist) {  // band front end
         const int Dq = band_dq(ix->D);
-        fill_u64_kernel<<<1, 64, 0, st>>>(w.cmax2, 0ull, 1);
-        if ((rc = check_launch("fill_u64_kernel"))) return rc;
-        pad_centroids_kernel<<<(unsigned)((ix->nlist + 63) / 64), 256, 0, st>>>(
-            ix->W_combined, ldw, ix->nlist, ix->D, Dq, w.cm32, w.cmt32, w.cn32, w.cmax2);
-        if ((rc = check_launch("pad_centroids_kernel"))) return rc;
+        const float *cm = ix->cent_rows, *cmt = ix->cent_tiles, *cn = ix->cent_norms;
+        const unsigned long long* cmax_dev = nullptr;
+        if (!cm) {  // derive the centroid layouts into the workspace
+            fill_u64_kernel<<<1, 64, 0, st>>>(w.cmax2, 0ull, 1);
+            if ((rc = check_launch("fill_u64_kernel"))) return rc;
+            pad_centroids_kernel<<<(unsigned)((ix->nlist + 63) / 64), 256, 0, st>>>(
+                ix->W_combined, ldw, ix->nlist, ix->D, Dq, w.cm32, w.cmt32, w.cn32, w.cmax2);
+            if ((rc = check_launch("pad_centroids_kernel"))) return rc;
+            cm = w.cm32;
+            cmt = w.cmt32;
+            cn = w.cn32;
+            cmax_dev = w.cmax2;
+        }
         pad_queries_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
                              st>>>(xq, B, ix->D, Dq, w.qt32, w.qn32);
         if ((rc = check_launch("pad_queries_kernel"))) return rc;
         float* a32 = reinterpret_cast<float*>(w.cd64);  // [B, nlist] approximations
         coarse_gemm_kernel<<<dim3((unsigned)((B + 63) / 64), (unsigned)((ix->nlist + 255) / 256)),
-                             kBlock, 0, st>>>(w.qt32, w.qn32, B, w.cmt32, w.cn32, ix->nlist, Dq,
+                             kBlock, 0, st>>>(w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq,
                                               a32);
         if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
         const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
         const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= 2048 ? 32 : 64;
 #define TRIDENT_BAND_LAUNCH(KPV, VV)                                                             \
     select_band_kernel<KPV, VV><<<grid, kBlock, 0, st>>>(                                       \
-        a32, w.xq64, w.cm32, w.cmax2, B, ix->nlist, ix->D, Dq, nprobe, w.probe_cids,            \
+        a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, nprobe,          \
+        w.probe_cids,                                                                           \
         w.probe_dqcs, nprobe, probe_cids, probe_dqcs, ld)
         if (nprobe <= 64) {
             if (V == 16) TRIDENT_BAND_LAUNCH(64, 16);

@@ -635,16 +635,16 @@ __global__ __launch_bounds__(256) void pad_centroids_kernel(const float* __restr
     double nrm = 0.0;  // centroid c0 + tx over dims ty, ty + 4, ...
     for (int d0 = 0; d0 < Dq; d0 += 64) {
 #pragma unroll
-        for (int r = ty; r < 64; r += 4) {  // s_t[d][c] = centroid c0 + c, dim d0 + d
-            const int d = d0 + r, c = c0 + tx;
+        for (int k = 0; k < 16; ++k) {  // s_t[d][c] = centroid c0 + c, dim d0 + d
+            const int r = ty + 4 * k, d = d0 + r, c = c0 + tx;
             const float v = (d < D && c < nlist) ? -0.5f * W[(size_t)d * ldw + c] : 0.0f;
             s_t[r][tx] = v;
             nrm = fma((double)v, (double)v, nrm);
         }
         __syncthreads();
 #pragma unroll
-        for (int r = ty; r < 64; r += 4) {  // centroid c0 + r, dim d0 + tx
-            const int c = c0 + r, d = d0 + tx;
+        for (int k = 0; k < 16; ++k) {  // centroid c0 + r, dim d0 + tx
+            const int r = ty + 4 * k, c = c0 + r, d = d0 + tx;
             if (c < nlist && d < Dq) {
                 const float v = s_t[tx][r];
                 cm32[(size_t)c * Dq + d] = v;
@@ -690,6 +690,68 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
     const int F = Dq >> 4;  // float4 per lane and row tile (= S / 4)
     const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
     const bool qv = qb + m < B;
+    const int ntile = min(16, (nlist - blockIdx.y * 256 + 15) / 16);  // tiles of this block
+    auto store = [&](int n0, const f4 (&acc4)[4]) {
+        // matrix-core results: wait states before the first VALU read, fenced
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7");
+        __builtin_amdgcn_sched_barrier(0);
+        const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+        const int c = n0 + m;
+        if (c < nlist) {
+            const float ncv = cn32[c];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int q = qb + 4 * g + i;
+                if (q < B) a32[(size_t)q * nlist + c] = fmaf(-2.0f, acc[i], qn32[q] + ncv);
+            }
+        }
+    };
+    if (F <= 8) {
+        // Dq <= 128: the wave's A operands stay in registers for all its tiles, and the next
+        // tile's B operands load while the current tile's MFMAs run
+        float4 av[8], b0[8], b1[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            av[j] = qt[(size_t)(j < F ? j : 0) * kWave];
+            if (j >= F || !qv) av[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+        auto loadB = [&](int t, float4 (&bv)[8]) {
+            const int n0 = blockIdx.y * 256 + min(t, ntile - 1) * 16;
+            const bool cv = n0 + m < nlist;
+            const float4* ct = reinterpret_cast<const float4*>(cmt32) +
+                               (size_t)(n0 >> 4) * F * kWave + lane;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                bv[j] = ct[(size_t)(j < F ? j : 0) * kWave];
+                if (j >= F || !cv) bv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        };
+        auto tile = [&](int t, const float4 (&bv)[8]) {
+            f4 acc4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                f4& acc = acc4[j & 3];
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, bv[j].x, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, bv[j].y, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, bv[j].z, acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc, 0, 0, 0);
+            }
+            store(blockIdx.y * 256 + t * 16, acc4);
+        };
+        loadB(0, b0);
+#pragma unroll 1
+        for (int t = 0; t < ntile; t += 2) {
+            loadB(t + 1, b1);
+            tile(t, b0);
+            if (t + 1 >= ntile) break;
+            loadB(t + 2, b0);
+            tile(t + 1, b1);
+        }
+        return;
+    }
 #pragma unroll 1
     for (int t = 0; t < 16; ++t) {
         const int n0 = blockIdx.y * 256 + t * 16;
@@ -723,20 +785,7 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc, 0, 0, 0);
             }
         }
-        // matrix-core results: wait states before the first VALU read, fenced
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_nop 7\n\ts_nop 7");
-        __builtin_amdgcn_sched_barrier(0);
-        const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-        const int c = n0 + m;
-        if (c < nlist) {
-            const float ncv = cn32[c];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int q = qb + 4 * g + i;
-                if (q < B) a32[(size_t)q * nlist + c] = fmaf(-2.0f, acc[i], qn32[q] + ncv);
-            }
-        }
+        store(n0, acc4);
     }
 }
 
@@ -750,7 +799,8 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
 template <int KP, int V>
 __global__ __launch_bounds__(256) void select_band_kernel(
     const float* __restrict__ a32, const double* __restrict__ xq64, const float* __restrict__ cm32,
-    const unsigned long long* __restrict__ cmax2, int B, int nlist, int D, int Dq, int nprobe,
+    const unsigned long long* __restrict__ cmax_dev, double cmax_host, int B, int nlist, int D,
+    int Dq, int nprobe,
     int32_t* __restrict__ out_cids, float* __restrict__ out_dqcs, int ld,
     int32_t* __restrict__ out2_cids, float* __restrict__ out2_dqcs, int ld2) {
     __shared__ int32_t s_band[kWavesPerBlock][2 * kWave];
@@ -771,7 +821,8 @@ __global__ __launch_bounds__(256) void select_band_kernel(
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) nq += __shfl_xor(nq, o, kWave);
     const double kappa = (double)(Dq + 2) * 0x1p-23;
-    const double E = (kappa + 0x1p-21) * (nq + __longlong_as_double((long long)*cmax2)) *
+    const double cmax2 = cmax_dev ? __longlong_as_double((long long)*cmax_dev) : cmax_host;
+    const double E = (kappa + 0x1p-21) * (nq + cmax2) *
                          (1.0 + 0x1p-10) + 1e-30;
     const float Ef = __double2float_ru(E);
     // bisection: count(a <= hi) >= nprobe throughout.  hi starts at the largest lane minimum
@@ -946,8 +997,8 @@ __global__ __launch_bounds__(256) void select_band_kernel(
 
 #define TRIDENT_SELECT_BAND(KP, V)                                                              \
     template __global__ void select_band_kernel<KP, V>(                                         \
-        const float*, const double*, const float*, const unsigned long long*, int, int, int, int, \
-        int, int32_t*, float*, int, int32_t*, float*, int);
+        const float*, const double*, const float*, const unsigned long long*, double, int, int,  \
+        int, int, int, int32_t*, float*, int, int32_t*, float*, int);
 TRIDENT_SELECT_BAND(64, 16)
 TRIDENT_SELECT_BAND(64, 32)
 TRIDENT_SELECT_BAND(64, 64)

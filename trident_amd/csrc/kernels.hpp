@@ -190,8 +190,9 @@ __global__ void coarse_gemm_kernel(const float* __restrict__ qt32, const float* 
 template <int KP, int V>
 __global__ void select_band_kernel(const float* __restrict__ a32, const double* __restrict__ xq64,
                                    const float* __restrict__ cm32,
-                                   const unsigned long long* __restrict__ cmax2, int B, int nlist,
-                                   int D, int Dq, int nprobe, int32_t* __restrict__ out_cids,
+                                   const unsigned long long* __restrict__ cmax_dev,
+                                   double cmax_host, int B, int nlist, int D, int Dq, int nprobe,
+                                   int32_t* __restrict__ out_cids,
                                    float* __restrict__ out_dqcs, int ld,
                                    int32_t* __restrict__ out2_cids,
                                    float* __restrict__ out2_dqcs, int ld2);

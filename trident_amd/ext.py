@@ -105,7 +105,8 @@ def release_workspaces() -> None:
 def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combined, b_combined,
                     rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
-                    eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None) -> TridentIndexView:
+                    eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
+                    cent_band=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -126,7 +127,35 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.blk_bounds4 = _ptr(blk_bounds4)
     v.vec_Ar = _ptr(vec_Ar)
     v.sq8_cells = _ptr(sq8_cells)
+    if cent_band is not None:
+        rows, tiles, norms, nmax = cent_band
+        v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
+        v.cent_norm_max = float(nmax)
     return v
+
+
+def band_dq(D: int) -> int:
+    """Row length of the matrix-core coarse layouts: D rounded up to 16."""
+    return (int(D) + 15) & ~15
+
+
+def centroid_band_layouts(W_combined: torch.Tensor, nlist: int):
+    """(rows [nlist, Dq], tiles, norms [nlist], max norm) of the centroids c_d = -W[d, c] / 2,
+    the optional TridentIndexView fields cent_*: built once per index instead of per search."""
+    D = int(W_combined.shape[0])
+    Dq = band_dq(D)
+    dev = W_combined.device
+    cen = (-0.5 * W_combined[:, :nlist]).t().contiguous()          # exact: power-of-two scale
+    rows = torch.zeros((nlist, Dq), device=dev, dtype=torch.float32)
+    rows[:, :D] = cen
+    nl16 = (nlist + 15) // 16 * 16
+    pad = torch.zeros((nl16, Dq), device=dev, dtype=torch.float32)
+    pad[:nlist] = rows
+    S = Dq // 4
+    # [t, m, g, j, e] -> [t, j, g, m, e]: float4 (t S/4 + j) 64 + (m + 16 g) = dims g S + 4 j + e
+    tiles = pad.view(nl16 // 16, 16, 4, S // 4, 4).permute(0, 3, 2, 1, 4).contiguous().view(-1)
+    n64 = (rows.double() ** 2).sum(1)
+    return rows, tiles, n64.to(torch.float32), float(n64.max()) if nlist else 0.0
 
 
 def env_ub_seed() -> int:
@@ -189,6 +218,7 @@ def launch_trident_v4_search(
     *, ub_seed: Optional[int] = None, rot_sq_bounds=None, p_init: int = -1, stage_events=None,
     vec_Ar: Optional[torch.Tensor] = None, route: int = 0,
     sq8_cells: Optional[torch.Tensor] = None,
+    cent_band=None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -242,6 +272,14 @@ def launch_trident_v4_search(
         _check_tensor("sq8_cells", sq8_cells, torch.int32, dev)
         _need(sq8_cells.numel() == tiles * (D_pad // 16) * int(tile_size) * 4,
               "sq8_cells must hold [tiles, D_pad/16, tile_size, 4] words")
+    if cent_band is not None:
+        Dq = band_dq(D)
+        rows_t, tiles_t, norms_t, _ = cent_band
+        for name, t, numel in (("cent_band rows", rows_t, nlist * Dq),
+                               ("cent_band tiles", tiles_t, (nlist + 15) // 16 * 16 * Dq),
+                               ("cent_band norms", norms_t, nlist)):
+            _check_tensor(name, t, torch.float32, dev)
+            _need(t.numel() == numel, f"{name} must hold {numel} floats")
     if stats_buf is not None:
         _check_tensor("stats_buf", stats_buf, torch.int64, dev)
         _need(stats_buf.numel() >= 4, "stats_buf needs 4 entries")
@@ -268,7 +306,7 @@ def launch_trident_v4_search(
         orig_ids_sorted=orig_ids_sorted, vmin=vmin if mode == 2 else None,
         delta=delta if mode == 2 else None, eps_dim=eps_dim if mode == 2 else None,
         blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
-        sq8_cells=sq8_cells if mode == 2 else None)
+        sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route, probe_cids=probe_cids_buf,

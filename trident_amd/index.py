@@ -137,6 +137,8 @@ class TridentV4Index:
       cluster_tile_off int32 [nlist + 1]; vmin / delta / eps_pad f32 [nlist or 1, D_pad]
       blk_bounds4  int32 [nb + 1] (32-dim blocks, or the variable scheme of :233-247)
       W_combined [D, nlist + D_pad] = [-2 C^T | R | 0], b_combined = [|c|^2 | b | 0]
+      cent_band    the centroids for the matrix-core coarse pass (rows, tile layout, norms,
+                   max norm; ext.centroid_band_layouts)
     """
 
     def __init__(self, storage: SharedClusterStorage, centroids, mean64, R64, tile_size: int = 256,
@@ -186,6 +188,7 @@ class TridentV4Index:
         self.W_combined[:, nlist:nlist + D] = R32.to(dev)
         self.b_combined[0, :nlist] = c_norm_sq
         self.b_combined[0, nlist:nlist + D] = b32.to(dev)
+        self.cent_band = _ext.centroid_band_layouts(self.W_combined, nlist)
 
         # ---- rotate, quantise, bound (chunked over sorted rows) ----
         vec_off = storage.cluster_vec_off.to(torch.int64)
@@ -372,7 +375,7 @@ class TridentV4Index:
             self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
             bool(record_kernel_ms), int(warp_refine), stats_buf,
             ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events,
-            vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells)
+            vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band)
         return topk_d, topk_i, kern_ms
 
     def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
@@ -386,7 +389,7 @@ class TridentV4Index:
             cluster_tile_off=self.cluster_tile_off, cluster_vec_off=st.cluster_vec_off,
             xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
             delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
-            sq8_cells=self.sq8_cells)
+            sq8_cells=self.sq8_cells, cent_band=self.cent_band)
         r = _lib.lib().trident_route_for(ctypes.byref(view), int(B), int(k or self.k), int(nprobe), int(route))
         if r < 0:
             _lib.check(-r, "trident_route_for")
