@@ -307,66 +307,72 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
     }
 }
 
-// One weight group per workgroup (its <= 16 pairs share a cluster), 16 lanes per pair (wave w
-// takes pairs 4 w .. 4 w + 3): the queries' int8 weight planes against the cluster's SQ8 grid
-// and each pair's threshold-independent scalars.  Lane l owns dims 64 k + 4 l + [0, 4)
-// (16-byte loads, one packed 32-bit store per plane).  All in float32, on the float32 rotated
-// query q32 (the bounds take q32 as the query point: e_q grows by |q32 - q64| <= 2^-24 |q32|
-// per dimension):
+// One weight group per wave (its <= 16 pairs share a cluster), 4 lanes per pair: lane l =
+// lane % 4 of pair slot lane / 4 owns dims 64 k + 16 l + [0, 16) (16-byte loads, one 16-byte
+// store per plane and 64-dim step), so the group's scale is a wave reduction (no LDS, no
+// barrier) and the per-pair sums take two shuffle levels.  The queries' int8 weight planes
+// against the cluster's SQ8 grid and each pair's threshold-independent scalars, all in float32
+// on the float32 rotated query q32 (the bounds take q32 as the query point: e_q grows by
+// |q32 - q64| <= 2^-24 |q32| per dimension):
 //   w_d = delta_d * (q32_d - vmin_d) (two roundings, <= 2^-22 |w_d|, charged to err_q);  one
 //   scale for the group: s = 2^(ilogb(m) - 14), doubled if m / s > 32639, for m = the largest
 //   |w_d| of the group's pairs, so |w_int| <= 32639;  w_int = rint(w / s) = 256 hi + lo
 //   (hi, lo in [-128, 127]);  Q = sum (q32_d - vmin_d)^2 (relative error < 2^-15).
+// The quantisation error is charged by its bound, |w - s w_int| <= s / 2 per dimension:
+//   err_q = 255 (D_pad s / 2 + 2^-22 sum |w|),  and |w_int| <= |w| / s + 1 / 2 gives
+//   acc_max = 128 (sum |w| / s + D_pad / 2) >= |sum (c - 128) w_int|
+// (per-dimension sums of the exact residuals would tighten err_q by ~2x, a 2^-16-relative
+// change of the bounds, for four more instructions per dimension).
 // (A common scale lets the lower-bound scan compare a wave's 16 queries against one integer
 // threshold per vector.)  Plane bytes past D_pad (up to DP) are zero, so the scan may read
 // whole 64-dim steps.
 template <int KS>
 __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
-    __shared__ float s_mx[kGroupQ];
-    const int gi = blockIdx.x;
+    const int lane = threadIdx.x & 63, l = lane & 3, slot = lane >> 2;
+    const int gi = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
     if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;
     const int2 grp = a.groups[gi];
-    const int lane = threadIdx.x & 63, l = lane & 15;
-    const int slot = (int)(threadIdx.x >> 6) * 4 + (lane >> 4);
     const bool valid = slot < grp.y;
     const int pp = grp.x + (valid ? slot : 0);  // idle slots redo the first pair, store nothing
     const int c = a.pair_cid[pp], q = a.pair_qid[pp];
     const int D_pad = a.D_pad, DP = a.DP;
     const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
     const float* xr = a.xrot32 + (size_t)q * D_pad;
-    float w[KS][4];
-    float mx = 0.0f, Qp = 0.0f, qq = 0.0f;
+    float w[KS][16];
+    float mx = 0.0f, Qp = 0.0f, qq = 0.0f, wl1 = 0.0f;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-        const int d0 = 64 * k + 4 * l;  // D_pad is a multiple of 4: all 4 dims or none
+        const int d0 = 64 * k + 16 * l;  // D_pad is a multiple of 32: all 16 dims or none
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[k][e] = 0.0f;
+        for (int e = 0; e < 16; ++e) w[k][e] = 0.0f;
         if (d0 < D_pad) {
-            const float4 x4 = *reinterpret_cast<const float4*>(xr + d0);
-            const float4 v4 = *reinterpret_cast<const float4*>(a.vmin + off + d0);
-            const float4 g4 = *reinterpret_cast<const float4*>(a.delta + off + d0);
-            const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w},
-                        gv[4] = {g4.x, g4.y, g4.z, g4.w};
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float qp = xv[e] - vv[e];
-                w[k][e] = gv[e] * qp;
-                mx = fmaxf(mx, fabsf(w[k][e]));
-                Qp = fmaf(qp, qp, Qp);
-                qq = fmaf(xv[e], xv[e], qq);
+            for (int h = 0; h < 4; ++h) {
+                const float4 x4 = *reinterpret_cast<const float4*>(xr + d0 + 4 * h);
+                const float4 v4 = *reinterpret_cast<const float4*>(a.vmin + off + d0 + 4 * h);
+                const float4 g4 = *reinterpret_cast<const float4*>(a.delta + off + d0 + 4 * h);
+                const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w},
+                            gv[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float qp = xv[e] - vv[e];
+                    w[k][4 * h + e] = gv[e] * qp;
+                    mx = fmaxf(mx, fabsf(w[k][4 * h + e]));
+                    wl1 += fabsf(w[k][4 * h + e]);
+                    Qp = fmaf(qp, qp, Qp);
+                    qq = fmaf(xv[e], xv[e], qq);
+                }
             }
         }
     }
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, o, kWave));
+    for (int o = 1; o < kWave; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));  // the group
+#pragma unroll
+    for (int o = 1; o < 4; o <<= 1) {  // the pair
         Qp += __shfl_xor(Qp, o, kWave);
         qq += __shfl_xor(qq, o, kWave);
+        wl1 += __shfl_xor(wl1, o, kWave);
     }
-    if (l == 0) s_mx[slot] = mx;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kGroupQ; ++i) mx = fmaxf(mx, s_mx[i]);
     // s and 1/s are powers of two in [2^-114, 2^114], so w * (1/s) is exactly w / s and
     // s * wi is exact
     int es = 0;
@@ -375,40 +381,43 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         if (ldexpf(mx, -es) > 32639.0f) ++es;
     }
     const float s = ldexpf(1.0f, es), inv_s = ldexpf(1.0f, -es);
-    float errs = 0.0f;
-    int wsum = 0, wabs = 0;
+    int wsum = 0;
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
 #pragma unroll
     for (int k = 0; k < KS; ++k) {
-        uint32_t hw = 0u, lw = 0u;
+        uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int wi = (int)rintf(w[k][e] * inv_s);  // 0 for dims >= D_pad
-            // w - s wi is exact (Sterbenz, or wi = 0); 2^-22 |w| covers the two roundings of w
-            errs += fabsf(w[k][e] - s * (float)wi) + 0x1p-22f * fabsf(w[k][e]);
-            wsum += wi;
-            wabs += abs(wi);
-            const int hi = (wi + 128) >> 8;
-            hw |= ((uint32_t)hi & 0xffu) << (8 * e);
-            lw |= ((uint32_t)(wi - (hi << 8)) & 0xffu) << (8 * e);
+        for (int h = 0; h < 4; ++h) {
+            int wi[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                wi[e] = (int)rintf(w[k][4 * h + e] * inv_s);  // 0 for dims >= D_pad
+                wsum += wi[e];
+            }
+            // lo = the low byte of wi as int8, hi = (wi - lo) / 256 = the second byte of
+            // wi + 128
+            lw[h] = ((uint32_t)wi[0] & 0xffu) | (((uint32_t)wi[1] & 0xffu) << 8) |
+                    (((uint32_t)wi[2] & 0xffu) << 16) | ((uint32_t)wi[3] << 24);
+            hw[h] = (((uint32_t)(wi[0] + 128) >> 8) & 0xffu) |
+                    ((uint32_t)(wi[1] + 128) & 0xff00u) |
+                    ((((uint32_t)(wi[2] + 128) >> 8) & 0xffu) << 16) |
+                    ((uint32_t)(wi[3] + 128) >> 8 << 24);
         }
         if (valid) {
-            *reinterpret_cast<uint32_t*>(hi_p + 64 * k + 4 * l) = hw;
-            *reinterpret_cast<uint32_t*>(hi_p + DP + 64 * k + 4 * l) = lw;
+            *reinterpret_cast<uint4*>(hi_p + 64 * k + 16 * l) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+            *reinterpret_cast<uint4*>(hi_p + DP + 64 * k + 16 * l) =
+                make_uint4(lw[0], lw[1], lw[2], lw[3]);
         }
     }
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) {
-        errs += __shfl_xor(errs, o, kWave);
-        wsum += __shfl_xor(wsum, o, kWave);
-        wabs += __shfl_xor(wabs, o, kWave);
-    }
+    for (int o = 1; o < 4; o <<= 1) wsum += __shfl_xor(wsum, o, kWave);
     if (valid && l == 0) {
         PairRec r;
         r.Qp = (double)Qp;
         // float32 sums of <= 256 terms: relative error < 2^-15 (the (1 + 2^-15) factors here
         // and the 2^-15 margins on Qp where it is used)
-        r.err_q = 255.0 * (double)errs * (1.0 + 0x1p-15);
+        const double l1 = (double)wl1 * (1.0 + 0x1p-15);
+        r.err_q = 255.0 * (0.5 * (double)D_pad * (double)s + 0x1p-22 * l1);
         // the query is the float32 rotation q32: |q32 - q_exact| <= e_q(float64) + 2^-23 |q32|
         r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-23 * sqrt((double)qq) * (1.0 + 0x1p-15) +
                 1e-30;
@@ -416,7 +425,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         r.c1 = 2.0 * (double)s;
         r.a_max = a.cbound[kCbStride * c];
         r.r_max = a.cbound[kCbStride * c + 1];
-        r.acc_max = 128.0 * (double)wabs;
+        r.acc_max = 128.0 * (l1 * (double)inv_s + 0.5 * (double)D_pad);
         a.prec[pp] = r;
     }
 }

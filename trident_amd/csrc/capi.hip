@@ -333,8 +333,9 @@ int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
 
 int launch_pair_prep(const BatchArgs& b, hipStream_t st) {
     if (b.M <= 0) return TRIDENT_OK;
-    static_assert(kGroupQ == 4 * kWavesPerBlock, "one weight group per workgroup, 16 lanes a pair");
-    const unsigned grid = (unsigned)b.max_groups;  // blocks past the group count return
+    static_assert(kGroupQ * 4 == kWave, "one weight group per wave, 4 lanes a pair");
+    // one group per wave; waves past the group count return
+    const unsigned grid = (unsigned)((b.max_groups + kWavesPerBlock - 1) / kWavesPerBlock);
     switch (b.DP / 64) {
         case 1: pair_prep_kernel<1><<<grid, kBlock, 0, st>>>(b); break;
         case 2: pair_prep_kernel<2><<<grid, kBlock, 0, st>>>(b); break;
