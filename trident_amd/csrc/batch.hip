@@ -953,6 +953,26 @@ void lb_scan_kernel(BatchArgs a) {
             nsq = 0;
         };
 
+        // ---- rare: queue a tile's passes (rows row0 + r of this lane, r < 4).  The integer
+        // test is implied by the exact condition, so nothing is lost, and it passes hardly more
+        // rows than the float test would (refinement decides); rows past the slice never pass
+        // (thr = INT_MAX, and |acc + kq| < 2^31 - 1), the row check only makes that explicit.
+        auto queue = [&](const uint64_t (&sm)[4], int row0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool pass = hasq && ((sm[r] >> lane) & 1ull) && row0 + r < ve;
+                const uint64_t pm = __ballot(pass);
+                if (pm == 0ull) continue;
+                if (nsq + __popcll(pm) > kLbQ) flush();
+                if (pass) {
+                    const int idx = __builtin_amdgcn_mbcnt_hi(
+                        (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
+                    s_sq[wid][nsq + idx] = ((uint32_t)(row0 + r) << 4) | (uint32_t)j;
+                }
+                nsq += __popcll(pm);
+            }
+        };
+
         // ---- one 16-vector tile: INT = the integer test (wave-uniform mode) ----
         auto tile = [&](auto int_c, int buf, int t, int li0) {
             constexpr bool INT = decltype(int_c)::value;
@@ -1000,23 +1020,7 @@ void lb_scan_kernel(BatchArgs a) {
                                          fmaf(c.x, (float)S[r], c.z));
             }
             if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
-            // rare: queue the tile's survivors.  The integer test is implied by the exact
-            // condition, so nothing is lost, and it passes hardly more rows than the float test
-            // would (refinement decides); rows past the slice never pass (thr = INT_MAX, and
-            // |acc + kq| < 2^31 - 1), the row check below only makes that explicit.
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const bool pass = hasq && ((sm[r] >> lane) & 1ull) && li0 + 4 * g + r < ve;
-                const uint64_t pm = __ballot(pass);
-                if (pm == 0ull) continue;
-                if (nsq + __popcll(pm) > kLbQ) flush();
-                if (pass) {
-                    const int idx = __builtin_amdgcn_mbcnt_hi(
-                        (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
-                    s_sq[wid][nsq + idx] = ((uint32_t)(li0 + 4 * g + r) << 4) | (uint32_t)j;
-                }
-                nsq += __popcll(pm);
-            }
+            queue(sm, li0 + 4 * g);
         };
 
         // ---- stream the slice through LDS in 64-vector blocks (as batch_scan_kernel) ----

@@ -380,7 +380,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                   hipStream_t st) {
     const int ldw = ix->nlist + ix->D_pad;
     const int cols = std::max(ix->D, rotate ? ix->D_pad : 0);
-    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
+    prep_queries_kernel<<<dim3((cols + 127) / 128, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
                           dim3(64, 4), 0, st>>>(
         xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
         w.xrot64, w.xrot32, w.qerr, rotate ? 1 : 0);
@@ -845,7 +845,7 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int ldw = ix->nlist + ix->D_pad;
     const int cols = std::max(ix->D, ix->D_pad);
-    prep_queries_kernel<<<dim3((cols + 63) / 64, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
+    prep_queries_kernel<<<dim3((cols + 127) / 128, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
                           dim3(64, 4), 0, st>>>(
         xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
         w.xrot64, w.xrot32, w.qerr, 1);

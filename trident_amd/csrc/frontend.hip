@@ -19,56 +19,82 @@ __global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n) {
         p[i] = v;
 }
 
-// grid (ceil(max(D, D_pad) / 64), ceil(B / (4 kPrepQB))), block (64, 4): each wave takes
-// kPrepQB queries (wave-uniform rows, scalar loads) x 64 columns, so every loaded rotation value
-// feeds kPrepQB chains.
+// grid (ceil(max(D, D_pad) / 128), ceil(B / (4 kPrepQB))), block (64, 4): each wave takes
+// kPrepQB queries (wave-uniform rows, scalar loads) x 128 columns (two per lane), so every
+// converted query value feeds two chains and every rotation value kPrepQB.
 // xq64[b, d] = (double)xq[b, d]; xrot64[b, j] = sum_d xq[b, d] * R[d, j] + bvec[j] evaluated
 // in float64 (fma, dimension order), xrot32 = xrot64 rounded to float32, and qerr[b, j] bounds
-// the distance of xrot64 from the exact value.
+// the distance of xrot64 from the exact value: |fl(sum) - sum| <= (D + 1) 2^-53 sum_d |x_d R_dj|
+// <= (D + 1) 2^-53 |x| |R_j| (Cauchy-Schwarz; both norms from float64 sums), taken with a
+// factor two (and the bias) for the roundings of the norms.
 __global__ __launch_bounds__(256) void prep_queries_kernel(
     const float* __restrict__ xq, int B, int D, int D_pad, const float* __restrict__ W, int ldw,
     int nlist, const float* __restrict__ bvec, double* __restrict__ xq64,
     double* __restrict__ xrot64, float* __restrict__ xrot32, double* __restrict__ qerr,
     int do_rot) {
     constexpr int QB = kPrepQB;
-    const int j = blockIdx.x * 64 + threadIdx.x;
+    const int lane = threadIdx.x;
+    const int j0 = blockIdx.x * 128 + lane, j1 = j0 + 64;
     const int b0 = (blockIdx.y * 4 + threadIdx.y) * QB;
     if (b0 >= B) return;
     const float* qr[QB];
 #pragma unroll
     for (int i = 0; i < QB; ++i) qr[i] = xq + (size_t)min(b0 + i, B - 1) * D;
-    if (j < D) {
-#pragma unroll
-        for (int i = 0; i < QB; ++i)
-            if (b0 + i < B) xq64[(size_t)(b0 + i) * D + j] = (double)qr[i][j];
-    }
-    if (!do_rot || j >= D_pad) return;
-    double acc[QB], mag[QB];
-#pragma unroll
-    for (int i = 0; i < QB; ++i) acc[i] = mag[i] = 0.0;
-    const float* wcol = W + nlist + j;
-#pragma unroll 4
-    for (int d = 0; d < D; ++d) {
-        const double r = (double)wcol[(size_t)d * ldw];
-#pragma unroll
-        for (int i = 0; i < QB; ++i) {
-            const double qd = (double)qr[i][d];
-            acc[i] = fma(qd, r, acc[i]);
-            mag[i] += fabs(qd * r);
-        }
-    }
-    const double bj = (double)bvec[nlist + j];
 #pragma unroll
     for (int i = 0; i < QB; ++i) {
         if (b0 + i >= B) break;
-        const double xr = acc[i] + bj;
-        xrot64[(size_t)(b0 + i) * D_pad + j] = xr;
-        xrot32[(size_t)(b0 + i) * D_pad + j] = (float)xr;
-        // |fl(sum) - sum| <= (D + 1) 2^-53 sum|terms|; doubled to also cover the rounding of
-        // `mag`.
-        qerr[(size_t)(b0 + i) * D_pad + j] =
-            (double)(D + 3) * 0x1p-52 * (mag[i] + fabs(bj)) + 0x1p-1000;
+        if (j0 < D) xq64[(size_t)(b0 + i) * D + j0] = (double)qr[i][j0];
+        if (j1 < D) xq64[(size_t)(b0 + i) * D + j1] = (double)qr[i][j1];
     }
+    if (!do_rot || j0 >= D_pad) return;
+    // squared norms of the wave's queries, dims split over the lanes
+    double nx[QB];
+#pragma unroll
+    for (int i = 0; i < QB; ++i) {
+        double t = 0.0;
+        for (int d = lane; d < D; d += kWave) {
+            const double v = (double)qr[i][d];
+            t = fma(v, v, t);
+        }
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) t += __shfl_xor(t, o, kWave);
+        nx[i] = t;
+    }
+    double acc0[QB], acc1[QB], rn0 = 0.0, rn1 = 0.0;
+#pragma unroll
+    for (int i = 0; i < QB; ++i) acc0[i] = acc1[i] = 0.0;
+    const bool h1 = j1 < D_pad;
+    const float* wc0 = W + nlist + j0;
+    const float* wc1 = W + nlist + (h1 ? j1 : j0);
+#pragma unroll 4
+    for (int d = 0; d < D; ++d) {
+        const double r0 = (double)wc0[(size_t)d * ldw];
+        const double r1 = (double)wc1[(size_t)d * ldw];
+        rn0 = fma(r0, r0, rn0);
+        rn1 = fma(r1, r1, rn1);
+#pragma unroll
+        for (int i = 0; i < QB; ++i) {
+            const double qd = (double)qr[i][d];
+            acc0[i] = fma(qd, r0, acc0[i]);
+            acc1[i] = fma(qd, r1, acc1[i]);
+        }
+    }
+    auto out = [&](int j, const double (&acc)[QB], double rn) {
+        const double bj = (double)bvec[nlist + j];
+        const double sr = sqrt(rn);
+#pragma unroll
+        for (int i = 0; i < QB; ++i) {
+            if (b0 + i >= B) break;
+            const double xr = acc[i] + bj;
+            xrot64[(size_t)(b0 + i) * D_pad + j] = xr;
+            xrot32[(size_t)(b0 + i) * D_pad + j] = (float)xr;
+            qerr[(size_t)(b0 + i) * D_pad + j] =
+                (double)(D + 3) * 0x1p-52 * (sqrt(nx[i]) * sr * (1.0 + 1e-12) + fabs(bj)) +
+                0x1p-1000;
+        }
+    };
+    out(j0, acc0, rn0);
+    if (h1) out(j1, acc1, rn1);
 }
 
 // grid (ceil(nlist / (64 kCoarseNC)), ceil(B / (kCoarseQW * 4))), block 256: each wave owns

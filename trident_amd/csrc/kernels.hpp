@@ -201,7 +201,7 @@ inline int band_dq(int D) { return (D + 15) & ~15; }
 
 constexpr int kCoarseQW = 4;       // queries per wave of coarse_dist_kernel
 constexpr int kCoarseNC = 2;       // centroids per lane of coarse_dist_kernel
-constexpr int kPrepQB = 2;         // queries per wave of prep_queries_kernel
+constexpr int kPrepQB = 4;         // queries per wave of prep_queries_kernel
 
 // Dynamic LDS bytes of the LDS grouping kernels; they are used while this is <= 64 KiB.
 inline size_t group_lds_bytes(int nlist) { return (size_t)2 * (nlist + 1) * sizeof(int32_t); }
