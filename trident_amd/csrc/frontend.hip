@@ -537,13 +537,23 @@ __global__ __launch_bounds__(256) void count_pairs_lds_kernel(const int32_t* __r
     for (int i = threadIdx.x; i < H; i += blockDim.x) s_hist[i] = 0;
     __syncthreads();
     const int total = B * nprobe;
-    const int i0 = blockIdx.x * kGroupChunk, i1 = min(total, i0 + kGroupChunk);
-    for (int idx = i0 + (int)threadIdx.x; idx < i1; idx += blockDim.x) {
-        const int q = idx / nprobe, p = idx - q * nprobe;
-        const int cid = probe_cids[(size_t)q * ld + p];
-        if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
-        atomicAdd(&s_hist[(p < p_init ? 0 : (nlist + 1)) + cid], 1);
+    const int i0 = blockIdx.x * kGroupChunk;
+    constexpr int kPer = kGroupChunk / 256;  // entries per thread, loads issued together
+    int bin[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int idx = i0 + k * 256 + (int)threadIdx.x;
+        bin[k] = -1;
+        if (idx < total) {
+            const int q = idx / nprobe, p = idx - q * nprobe;
+            const int cid = probe_cids[(size_t)q * ld + p];
+            // invalid caller input: never index
+            if ((unsigned)cid < (unsigned)nlist) bin[k] = (p < p_init ? 0 : (nlist + 1)) + cid;
+        }
     }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+        if (bin[k] >= 0) atomicAdd(&s_hist[bin[k]], 1);
     __syncthreads();
     for (int i = threadIdx.x; i < H; i += blockDim.x) {
         const int v = s_hist[i];
@@ -563,31 +573,45 @@ __global__ __launch_bounds__(256) void scatter_pairs_lds_kernel(
     for (int i = threadIdx.x; i < H; i += blockDim.x) s_hist[i] = 0;
     __syncthreads();
     const int total = B * nprobe;
-    const int i0 = blockIdx.x * kGroupChunk, i1 = min(total, i0 + kGroupChunk);
-    for (int idx = i0 + (int)threadIdx.x; idx < i1; idx += blockDim.x) {
-        const int q = idx / nprobe, p = idx - q * nprobe;
-        const int cid = probe_cids[(size_t)q * ld + p];
-        if ((unsigned)cid >= (unsigned)nlist) continue;
-        atomicAdd(&s_hist[(p < p_init ? 0 : (nlist + 1)) + cid], 1);
+    const int i0 = blockIdx.x * kGroupChunk;
+    constexpr int kPer = kGroupChunk / 256;  // entries per thread, loads issued together
+    int bin[kPer], qq[kPer];
+    float dq[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        const int idx = i0 + k * 256 + (int)threadIdx.x;
+        bin[k] = -1;
+        qq[k] = 0;
+        dq[k] = 0.0f;
+        if (idx < total) {
+            const int q = idx / nprobe, p = idx - q * nprobe;
+            const int cid = probe_cids[(size_t)q * ld + p];
+            if ((unsigned)cid < (unsigned)nlist) bin[k] = (p < p_init ? 0 : (nlist + 1)) + cid;
+            qq[k] = q;
+            if (probe_dqcs) dq[k] = probe_dqcs[(size_t)q * ld + p];
+        }
     }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+        if (bin[k] >= 0) atomicAdd(&s_hist[bin[k]], 1);
     __syncthreads();
     for (int i = threadIdx.x; i < H; i += blockDim.x) {
         const int v = s_hist[i];
         if (v) s_hist[i] = atomicAdd(&cursor[i], v);
     }
     __syncthreads();
-    for (int idx = i0 + (int)threadIdx.x; idx < i1; idx += blockDim.x) {
-        const int q = idx / nprobe, p = idx - q * nprobe;
-        const int cid = probe_cids[(size_t)q * ld + p];
-        if ((unsigned)cid >= (unsigned)nlist) continue;
-        const bool first = p < p_init;
-        const int slot = atomicAdd(&s_hist[(first ? 0 : (nlist + 1)) + cid], 1);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        if (bin[k] < 0) continue;
+        const bool first = bin[k] <= nlist;
+        const int cid = first ? bin[k] : bin[k] - (nlist + 1);
+        const int slot = atomicAdd(&s_hist[bin[k]], 1);
         int32_t* oc = first ? p1_cids : p2_cids;
         int32_t* oq = first ? p1_qids : p2_qids;
         float* od = first ? p1_dqcs : p2_dqcs;
         oc[slot] = cid;
-        oq[slot] = q;
-        if (od) od[slot] = probe_dqcs ? probe_dqcs[(size_t)q * ld + p] : 0.0f;
+        oq[slot] = qq[k];
+        if (od) od[slot] = dq[k];
     }
 }
 

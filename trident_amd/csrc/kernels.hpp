@@ -175,7 +175,7 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
                                      int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs);
 
-constexpr int kGroupChunk = 8192;  // (query, probe) entries per block of the LDS grouping
+constexpr int kGroupChunk = 2048;  // (query, probe) entries per block of the LDS grouping
 // band front end (frontend.hip)
 __global__ void pad_queries_kernel(const float* __restrict__ xq, int B, int D, int Dq,
                                    float* __restrict__ qt32, float* __restrict__ qn32);
