@@ -222,19 +222,29 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
         const float* xr = a.xb + (size_t)pos * D;
         double acc = 0.0;
         if (vec4) {
-#pragma unroll 4
-            for (int d = 0; d < D; d += 4) {
-                const float4 x = *reinterpret_cast<const float4*>(xr + d);
-                const float4 y = *reinterpret_cast<const float4*>(qr + d);
-                double t = (double)x.x - (double)y.x;
-                acc = fma(t, t, acc);
-                t = (double)x.y - (double)y.y;
-                acc = fma(t, t, acc);
-                t = (double)x.z - (double)y.z;
-                acc = fma(t, t, acc);
-                t = (double)x.w - (double)y.w;
-                acc = fma(t, t, acc);
-            }
+            // the row arrives 64 dims at a time, all 16 loads issued before their first use
+            int d = 0;
+            auto chunk = [&](auto n4c) {
+                constexpr int N4 = decltype(n4c)::value;
+                float4 xv[N4];
+#pragma unroll
+                for (int k = 0; k < N4; ++k) xv[k] = *reinterpret_cast<const float4*>(xr + d + 4 * k);
+#pragma unroll
+                for (int k = 0; k < N4; ++k) {
+                    const float4 y = *reinterpret_cast<const float4*>(qr + d + 4 * k);
+                    double t = (double)xv[k].x - (double)y.x;
+                    acc = fma(t, t, acc);
+                    t = (double)xv[k].y - (double)y.y;
+                    acc = fma(t, t, acc);
+                    t = (double)xv[k].z - (double)y.z;
+                    acc = fma(t, t, acc);
+                    t = (double)xv[k].w - (double)y.w;
+                    acc = fma(t, t, acc);
+                }
+                d += 4 * N4;
+            };
+            while (d + 64 <= D) chunk(std::integral_constant<int, 16>{});
+            while (d + 4 <= D) chunk(std::integral_constant<int, 1>{});
         } else {
             for (int d = 0; d < D; ++d) {
                 const double t = (double)xr[d] - (double)qr[d];
