@@ -278,10 +278,15 @@ __device__ __forceinline__ double sum16_f64(double v) {
 // cluster.  Waves [nlist, nlist + B): per-query sum of qerr^2 (the rotation error of q_rot,
 // squared).
 __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist, int B,
-                                                         double* cbound, double* qep) {
+                                                         double* cbound, double* qep,
+                                                         int32_t* unit_ctr) {
     const int lane = threadIdx.x & 63;
     const int wv = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
     const int D_pad = a.D_pad;
+    // the per-launch state of both passes starts here (one launch instead of three fills):
+    // work counters, tau = +inf (pass A takes atomicMin), empty survivor lists (pass B)
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < 2 * 8 * kCtrStride; i += blockDim.x) unit_ctr[i] = 0;
     if (wv < nlist) {
         const size_t off = a.per_cluster ? (size_t)wv * D_pad : 0;
         double dd = 0.0, ee = 0.0;
@@ -309,11 +314,16 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
             cbound[kCbStride * wv + 2] = rlo < INFINITY ? (double)rlo : 0.0;
         }
     } else if (wv < nlist + B) {
-        const double* qe = a.qerr + (size_t)(wv - nlist) * D_pad;
+        const int q = wv - nlist;
+        const double* qe = a.qerr + (size_t)q * D_pad;
         double ep = 0.0;
         for (int d = lane; d < D_pad; d += kWave) ep = fma(qe[d], qe[d], ep);
         ep = wave_sum_f64(ep);
-        if (lane == 0) qep[wv - nlist] = ep;
+        if (lane == 0) {
+            qep[q] = ep;
+            a.tau[q] = INFINITY;
+            a.cand_cnt[q] = 0;
+        }
     }
 }
 
@@ -797,6 +807,9 @@ template __global__ void ub_scan_kernel<4, 16>(BatchArgs);
 __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, slot = tid & 15;
     const int gi = blockIdx.x * (kBlock / kGroupQ) + (tid >> 4);
+    if (a.tau_sq_out)  // the seeded thresholds, rounded up to float32, for the caller
+        for (int q = blockIdx.x * kBlock + tid; q < a.B; q += gridDim.x * kBlock)
+            a.tau_sq_out[q] = __double2float_ru(a.tau[q]);
     if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;  // whole 16-lane groups
     const int2 grp = a.groups[gi];
     const bool valid = slot < grp.y;

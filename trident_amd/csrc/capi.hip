@@ -692,6 +692,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.xrot32 = w.xrot32;
         b.qerr = w.qerr;
         b.tau = w.tau64;
+        b.tau_sq_out = nullptr;
+        b.B = B;
         b.cand_key = w.cand_key;
         b.cand_id = w.cand_id;
         b.cand_cnt = w.cand_cnt;
@@ -717,7 +719,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.grp_off = w.grp_off;
         b.max_groups = (int)w.max_groups;
         aux_bounds_kernel<<<(unsigned)((ix->nlist + B + kWavesPerBlock - 1) / kWavesPerBlock),
-                            kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep);
+                            kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep, w.unit_ctr);
         if ((rc = check_launch("aux_bounds_kernel"))) return rc;
         unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
                                                w.unit_off, w.grp_off);
@@ -728,23 +730,17 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                                  (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if ((rc = launch_pair_prep(b, st))) return rc;
-        fill_u64_kernel<<<(unsigned)std::min<int64_t>((B + 255) / 256, 4096), 256, 0, st>>>(
-            reinterpret_cast<unsigned long long*>(w.tau64), 0x7ff0000000000000ull, B);
-        if ((rc = check_launch("fill_u64_kernel"))) return rc;
-        if ((rc = fill(w.unit_ctr, 0, 2 * 8 * kCtrStride, st))) return rc;
         if (M1 > 0) {  // pass A: per-query upper-bound threshold from the first p_init probes
             b.unit_end = ix->nlist;
             b.ctr = w.unit_ctr;
             if ((rc = launch_batch<true>(b, st))) return rc;
         }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
-        if (out->tau_sq) {
-            tau_to_f32_kernel<<<(B + 255) / 256, 256, 0, st>>>(w.tau64, out->tau_sq, B);
-            if ((rc = check_launch("tau_to_f32_kernel"))) return rc;
-        }
-        // the lower-bound constants follow from tau (part of the seeding pass's merge stage)
-        if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
-        lb_prep_kernel<<<(unsigned)((w.max_groups + kBlock / kGroupQ - 1) / (kBlock / kGroupQ)),
+        // the lower-bound constants follow from tau (part of the seeding pass's merge stage);
+        // the same launch hands the caller its float32 copy of tau
+        b.tau_sq_out = out->tau_sq;
+        lb_prep_kernel<<<(unsigned)std::max<int64_t>(
+                             (w.max_groups + kBlock / kGroupQ - 1) / (kBlock / kGroupQ), 1),
                          kBlock, 0, st>>>(b);
         if ((rc = check_launch("lb_prep_kernel"))) return rc;
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;

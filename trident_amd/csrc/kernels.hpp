@@ -125,6 +125,8 @@ struct BatchArgs {
     const double* cbound;       // [nlist, kCbStride] (A_max, r_max, r_lo) per cluster
     const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
+    float* tau_sq_out;          // [B] caller's float32 copy of the seeded tau, or null
+    int B;
     uint64_t* cand_key;
     int32_t* cand_id;
     int32_t* cand_cnt;
@@ -276,7 +278,8 @@ __global__ void refine_survivors_kernel(BatchArgs a, int B);
 template <int KS>
 __global__ void pair_prep_kernel(BatchArgs a);
 
-__global__ void aux_bounds_kernel(BatchArgs a, int nlist, int B, double* cbound, double* qep);
+__global__ void aux_bounds_kernel(BatchArgs a, int nlist, int B, double* cbound, double* qep,
+                                  int32_t* unit_ctr);
 
 __global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
                                   const int32_t* __restrict__ cids,
