@@ -718,8 +718,8 @@ __global__ __launch_bounds__(256) void pad_centroids_kernel(const float* __restr
     }
 }
 
-// grid (ceil(B / 64), ceil(nlist / 256)), block 256: each wave 16 queries (one query tile), all
-// four waves the same 16 centroid tiles in the same order.  v_mfma_f32_16x16x4f32 with query
+// grid (ceil(B / 64), ceil(nlist / (16 kGemmTiles))), block 256: each wave 16 queries (one query
+// tile), all four waves the same kGemmTiles centroid tiles in the same order.  v_mfma_f32_16x16x4f32 with query
 // rows as A (16 x 4) and centroids as B (4 x 16), operands straight from the tile layouts: a
 // chunk of 32 k-steps is 8 + 8 coalesced float4 loads, issued whole before its 32 MFMAs; steps
 // past S are zero (clamped loads, no branch among the MFMAs).
@@ -734,13 +734,14 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, g = lane >> 4;
-    const int qtile = blockIdx.x * 4 + wid;
-    const int qb = qtile * 16;
-    if (qb >= B) return;
+    const int qb0 = blockIdx.x * 64 + wid * 16;
+    const bool wave_live = qb0 < B;  // waves past the last query still help with the LDS copy
+    const int qtile = wave_live ? qb0 / 16 : 0;
+    const int qb = wave_live ? qb0 : 0;
     const int F = Dq >> 4;  // float4 per lane and row tile (= S / 4)
     const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
-    const bool qv = qb + m < B;
-    const int ntile = min(16, (nlist - blockIdx.y * 256 + 15) / 16);  // tiles of this block
+    const bool qv = wave_live && qb + m < B;
+    const int ntile = min(kGemmTiles, (nlist - blockIdx.y * 16 * kGemmTiles + 15) / 16);
     auto store = [&](int n0, const f4 (&acc4)[4]) {
         // matrix-core results: wait states before the first VALU read, fenced
         __builtin_amdgcn_sched_barrier(0);
@@ -757,60 +758,82 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
             }
         }
     };
-    if (F <= 8) {
-        // Dq <= 128: the wave's A operands stay in registers for all its tiles, and the next
-        // tile's B operands load while the current tile's MFMAs run
-        float4 av[8], b0[8], b1[8];
+    // centroids as A and queries as B: lane (m, g) then holds centroids n0 + 4 g .. + 3 of
+    // query qb + m, one 16-byte store (16-byte aligned when nlist % 4 == 0)
+    auto store_t = [&](int n0, const f4 (&acc4)[4]) {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_nop 7\n\ts_nop 7");
+        __builtin_amdgcn_sched_barrier(0);
+        const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+        const int q = qb + m, c0 = n0 + 4 * g;
+        if (q >= B) return;
+        const float nq = qn32[q];
+        float* dst = a32 + (size_t)q * nlist + c0;
+        if ((nlist & 3) == 0 && c0 + 4 <= nlist) {
+            const float4 nc = *reinterpret_cast<const float4*>(cn32 + c0);
+            *reinterpret_cast<float4*>(dst) =
+                make_float4(fmaf(-2.0f, acc[0], nq + nc.x), fmaf(-2.0f, acc[1], nq + nc.y),
+                            fmaf(-2.0f, acc[2], nq + nc.z), fmaf(-2.0f, acc[3], nq + nc.w));
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            av[j] = qt[(size_t)(j < F ? j : 0) * kWave];
-            if (j >= F || !qv) av[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            for (int i = 0; i < 4; ++i)
+                if (c0 + i < nlist) dst[i] = fmaf(-2.0f, acc[i], nq + cn32[c0 + i]);
         }
-        auto loadB = [&](int t, float4 (&bv)[8]) {
-            const int n0 = blockIdx.y * 256 + min(t, ntile - 1) * 16;
-            const bool cv = n0 + m < nlist;
-            const float4* ct = reinterpret_cast<const float4*>(cmt32) +
-                               (size_t)(n0 >> 4) * F * kWave + lane;
+    };
+    if (F <= 8) {
+        // Dq <= 128: the block's kGemmTiles centroid tiles are copied to LDS once (one
+        // contiguous run of the tile layout) and shared by the four waves; each wave's query
+        // operands stay in registers for all tiles
+        __shared__ float4 s_b[kGemmTiles * 8 * kWave];
+        const float4* cb = reinterpret_cast<const float4*>(cmt32) +
+                           (size_t)(blockIdx.y * kGemmTiles) * F * kWave;
+        for (int i = threadIdx.x; i < ntile * F * kWave; i += blockDim.x) s_b[i] = cb[i];
+        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 av[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                bv[j] = ct[(size_t)(j < F ? j : 0) * kWave];
-                if (j >= F || !cv) bv[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-        };
-        auto tile = [&](int t, const float4 (&bv)[8]) {
+        for (int j = 0; j < 8; ++j) av[j] = qt[(size_t)(j < F ? j : 0) * kWave];
+        if (F < 8) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (j >= F) av[j] = z4;
+        }
+        if (qb + 16 > B && !qv) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) av[j] = z4;
+        }
+        __syncthreads();
+        if (!wave_live) return;  // after the barrier
+#pragma unroll 1
+        for (int t = 0; t < ntile; ++t) {
+            float4 bv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bv[j] = s_b[(t * F + (j < F ? j : 0)) * kWave + lane];
             f4 acc4[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+            // consecutive MFMAs go to different accumulators (k-step 4 j + u -> chain u);
+            // centroids are the A operand, queries the B operand
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                f4& acc = acc4[j & 3];
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, bv[j].x, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, bv[j].y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, bv[j].z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc, 0, 0, 0);
+            for (int j = 0; j < 8; ++j) {  // av[j] is zero for j >= F
+                acc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].x, av[j].x, acc4[0], 0, 0, 0);
+                acc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].y, av[j].y, acc4[1], 0, 0, 0);
+                acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, av[j].z, acc4[2], 0, 0, 0);
+                acc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].w, av[j].w, acc4[3], 0, 0, 0);
             }
-            store(blockIdx.y * 256 + t * 16, acc4);
-        };
-        loadB(0, b0);
-#pragma unroll 1
-        for (int t = 0; t < ntile; t += 2) {
-            loadB(t + 1, b1);
-            tile(t, b0);
-            if (t + 1 >= ntile) break;
-            loadB(t + 2, b0);
-            tile(t + 1, b1);
+            store_t(blockIdx.y * 16 * kGemmTiles + t * 16, acc4);
         }
         return;
     }
+    if (!wave_live) return;
 #pragma unroll 1
-    for (int t = 0; t < 16; ++t) {
-        const int n0 = blockIdx.y * 256 + t * 16;
+    for (int t = 0; t < kGemmTiles; ++t) {
+        const int n0 = blockIdx.y * 16 * kGemmTiles + t * 16;
         if (n0 >= nlist) break;
         const bool cv = n0 + m < nlist;
         const float4* ct = reinterpret_cast<const float4*>(cmt32) + (size_t)(n0 >> 4) * F * kWave +
                            lane;
-        // four independent accumulator chains (k-steps j mod 4), summed at the end: the error
-        // bound holds for any summation order
+        // four independent accumulator chains (k-step 4 j + u -> chain u), summed at the end:
+        // the error bound holds for any summation order
         f4 acc4[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
@@ -828,11 +851,10 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                f4& acc = acc4[j & 3];
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, bv[j].x, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, bv[j].y, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, bv[j].z, acc, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc, 0, 0, 0);
+                acc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].x, bv[j].x, acc4[0], 0, 0, 0);
+                acc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].y, bv[j].y, acc4[1], 0, 0, 0);
+                acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].z, bv[j].z, acc4[2], 0, 0, 0);
+                acc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j].w, bv[j].w, acc4[3], 0, 0, 0);
             }
         }
         store(n0, acc4);

@@ -198,6 +198,7 @@ __global__ void select_band_kernel(const float* __restrict__ a32, const double* 
                                    float* __restrict__ out_dqcs, int ld,
                                    int32_t* __restrict__ out2_cids,
                                    float* __restrict__ out2_dqcs, int ld2);
+constexpr int kGemmTiles = 4;  // coarse_gemm_kernel: 16-centroid tiles per wave
 constexpr int kBandMaxNlist = 4096;  // band front end: nlist <= 64 x 64 approximations per lane
 inline int band_dq(int D) { return (D + 15) & ~15; }
 
