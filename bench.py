@@ -63,6 +63,9 @@ CONFIGS = {
             desc="configs[2]: anisotropic power-law Gaussian, D=960"),
     4: dict(N=10_000_000, D=96, nlist=4096, nprobe=64, K=10, B=10_000, T=64, n_centers=4096,
             desc="configs[3]: L2-normalised 4096-centre mixture, D=96"),
+    # configs[4] (out of core, 1e8 rows): run with --xb-host, usually with a smaller --N
+    5: dict(N=100_000_000, D=128, nlist=16384, nprobe=128, K=10, B=10_000, T=64, n_centers=1024,
+            desc="configs[4]: histogram-like descriptors, out of core"),
 }
 
 
@@ -82,6 +85,8 @@ def main():
     ap.add_argument("--check", type=int, default=-1, help="queries checked against the oracle (-1 = all)")
     ap.add_argument("--cpu-queries", type=int, default=-1, help="CPU-baseline sample (-1 = all B)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--xb-host", action="store_true",
+                    help="out of core: the FP32 base in mapped pinned host memory (Stage Z over PCIe)")
     ap.add_argument("--sweep", action="store_true", help="also time other nprobe / ub values and the CM route")
     ap.add_argument("--calibrate-w0", action="store_true", help="router crossover sweep over batch sizes")
     args = ap.parse_args()
@@ -110,7 +115,8 @@ def main():
     t1 = time.perf_counter()
     cen, lid, r, mean64, R64, t_train = clustering.train_clustering(
         xb, nlist, seed=0, niter=20, max_train=min(N, max(64 * nlist, 256 * 1024)), device=dev)
-    st = SharedClusterStorage(xb, lid, r, nlist, device=dev)
+    st = SharedClusterStorage(xb, lid, r, nlist, device=dev,
+                              xb_placement="host" if args.xb_host else "device")
     ix = TridentV4Index(st, cen, mean64, R64, tile_size=cfg["T"], device=dev, max_batch=B,
                         max_nprobe=max(128, cfg["nprobe"]), k=K)
     del xb
@@ -263,7 +269,8 @@ def main():
         "config": {"workload": f"BASELINE {cfg['desc']}, N={N}, D={D}, nlist={nlist}, nprobe={nprobe}, "
                                f"K={K}, B={B}",
                    "route": ("batched" if route == _lib.ROUTE_BATCHED else "pair") if mode == 2 else "cm_exact",
-                   "ub_seed": ub, "p_init": p_init, "tile_size": cfg["T"], "parallelism": "single GPU"},
+                   "ub_seed": ub, "p_init": p_init, "tile_size": cfg["T"], "parallelism": "single GPU",
+                   "xb_placement": "host (mapped, out of core)" if args.xb_host else "device"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "exact": {"queries_checked": nchk, "probes_identical": probe_same, "ids_identical": ids_same,

@@ -201,6 +201,7 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
 // batched route has D <= 256).  An
 // overflowed list (count > cap) is left alone: the merge rescans that query's probes
 // exhaustively.
+template <bool HOST>
 __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int B) {
     __shared__ __align__(16) float s_q[kWavesPerBlock][256];
     const int lane = threadIdx.x & 63, wid = (int)(threadIdx.x >> 6);
@@ -217,6 +218,31 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
     int32_t* ci = a.cand_id + (size_t)q * a.cap;
     const bool vec4 = (D & 3) == 0 && (reinterpret_cast<uintptr_t>(a.xb) & 15) == 0;
     unsigned long long ins = 0;
+    if constexpr (HOST) {
+        // base in mapped host memory: rows cross PCIe, so they are read as 128-byte row
+        // segments (all of a 32-dim chunk's loads in flight) and staged through LDS
+        __shared__ int32_t s_pos[kWavesPerBlock][kWave];
+        __shared__ double s_q64[kWavesPerBlock][256];
+        __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
+        for (int d = lane; d < D; d += kWave) s_q64[wid][d] = (double)qr[d];
+        for (int s0 = (int)blockIdx.y * kWave; s0 < cnt; s0 += kWave * (int)gridDim.y) {
+            const int s = s0 + lane, n = min(kWave, cnt - s0);
+            const int pos = s < cnt ? ci[s] : 0;
+            s_pos[wid][lane] = pos;
+            wave_sync();
+            const double acc = refine_rows_mlp(a.xb, D, s_pos[wid], n, s_stage[wid], s_q64[wid]);
+            wave_sync();
+            if (s < cnt) {
+                const bool ok = acc <= tau;
+                ck[s] = ok ? key_of(acc) : kKeyInvalid;
+                ci[s] = ok ? a.orig_ids[pos] : kIdInvalid;
+                if (a.stats) ins += __popcll(__ballot(ok));
+            }
+        }
+        if (a.stats && lane == 0 && ins)
+            atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
+        return;
+    }
     for (int s = (int)blockIdx.y * kWave + lane; s < cnt; s += kWave * (int)gridDim.y) {
         const int pos = ci[s];
         const float* xr = a.xb + (size_t)pos * D;
@@ -259,6 +285,9 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
     if (a.stats && lane == 0 && ins)
         atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
 }
+
+template __global__ void refine_survivors_kernel<false>(BatchArgs, int);
+template __global__ void refine_survivors_kernel<true>(BatchArgs, int);
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll

@@ -108,9 +108,10 @@ struct Workspace {
 inline int64_t plane_bytes(int D_pad) { return 64 * (int64_t)((D_pad + 63) / 64); }
 
 // Candidate-list slots per query.  The batched route stores every lower-bound survivor there
-// (before its exact test), so lists are at least 16 * nprobe deep; a longer list makes the
-// merge rescan that query's probes exhaustively.
-inline int64_t cand_cap(int64_t nprobe, int64_t K) { return nprobe * std::max<int64_t>(K, 16); }
+// (before its exact test), so lists are at least 64 * nprobe deep (12 bytes a slot; only used
+// slots are touched): a longer list makes the merge rescan that query's probes exhaustively,
+// which with the base in host memory crosses PCIe for every probed row.
+inline int64_t cand_cap(int64_t nprobe, int64_t K) { return nprobe * std::max<int64_t>(K, 64); }
 
 Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
     Carver c{static_cast<char*>(base)};
@@ -695,6 +696,12 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.tau = w.tau64;
         b.tau_sq_out = nullptr;
         b.B = B;
+        {
+            hipPointerAttribute_t pa;
+            b.xb_host = hipPointerGetAttributes(&pa, ix->xb_sorted) == hipSuccess &&
+                        pa.type == hipMemoryTypeHost;
+            (void)hipGetLastError();  // an unregistered pointer is not an error here
+        }
         b.cand_key = w.cand_key;
         b.cand_id = w.cand_id;
         b.cand_cnt = w.cand_cnt;
@@ -752,9 +759,13 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
         // one wave per (query, 64-slot chunk of its list): a query with many survivors spreads
         // over many waves
-        refine_survivors_kernel<<<dim3((unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock),
-                                       (unsigned)((cap + kWave - 1) / kWave)),
-                                  kBlock, 0, st>>>(b, B);
+        // the chunk dimension stops at 16: waves loop over further chunks
+        const dim3 rgrid((unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock),
+                         (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
+        if (b.xb_host)
+            refine_survivors_kernel<true><<<rgrid, kBlock, 0, st>>>(b, B);
+        else
+            refine_survivors_kernel<false><<<rgrid, kBlock, 0, st>>>(b, B);
         if ((rc = check_launch("refine_survivors_kernel"))) return rc;
         m.use_prev = 0;
         m.out_d = out->topk_d;

@@ -126,6 +126,7 @@ struct BatchArgs {
     const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
     float* tau_sq_out;          // [B] caller's float32 copy of the seeded tau, or null
+    int xb_host;                // xb is mapped host memory (Stage Z reads cross PCIe)
     int B;
     uint64_t* cand_key;
     int32_t* cand_id;
@@ -274,6 +275,7 @@ __global__ void lb_prep_kernel(BatchArgs a);
 template <int KS>
 __global__ void lb_scan_kernel(BatchArgs a);
 
+template <bool HOST>
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
 
 template <int KS>

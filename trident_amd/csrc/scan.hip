@@ -36,7 +36,6 @@
 
 namespace trident {
 
-constexpr int kStageCh = 32;    // dims per Stage Z staging chunk
 constexpr int kQueueCap = 128;  // per-wave survivor queue (64 pending + one slice)
 
 __device__ __forceinline__ void dim_params(double vm, float dl, float ep, double xr, double qe,
@@ -87,34 +86,6 @@ __device__ __forceinline__ float sq8_accumulate(const uint32_t* cp, int T, int d
             acc = lb_step((w >> 16) & 0xffu, dl.z, bs.z, ee.z, acc);
             acc = lb_step(w >> 24, dl.w, bs.w, ee.w, acc);
         }
-    }
-    return acc;
-}
-
-// Canonical float64 distance of the first `nq` queued survivors (lane i <- survivor i).
-// Rows are staged through LDS 32 dims at a time with 128-byte coalesced row loads.
-__device__ __forceinline__ double refine_rows(const float* __restrict__ xb, int D,
-                                              const int32_t* q_spos, int nq,
-                                              float (*stage)[kWave + 1], const double* s_q64) {
-    const int lane = lane_id();
-    double acc = 0.0;
-    const int half = lane >> 5, kk = lane & 31;
-    for (int d0 = 0; d0 < D; d0 += kStageCh) {
-        const int ch = min(kStageCh, D - d0);
-        for (int r0 = 0; r0 < nq; r0 += 2) {
-            const int r = r0 + half;
-            float v = 0.0f;
-            if (r < nq && kk < ch) v = xb[(size_t)q_spos[r] * D + d0 + kk];
-            if (r < nq) stage[kk][r] = v;
-        }
-        wave_sync();
-        if (lane < nq) {
-            for (int k = 0; k < ch; ++k) {
-                const double t = (double)stage[k][lane] - s_q64[d0 + k];
-                acc = fma(t, t, acc);
-            }
-        }
-        wave_sync();
     }
     return acc;
 }
