@@ -123,3 +123,45 @@ def test_batched_rejects_unsupported_k(sets, dev):
     b, xq = sets["hist"]
     with pytest.raises(TridentError, match="batched route"):
         run_search(b, _q(xq, dev), 8, 100, mode=2, route=2)
+
+
+@pytest.fixture(scope="module")
+def wide_sets(dev):
+    """D_pad > 256: the scans stage 16-vector blocks and keep up to 16 steps of weights."""
+    out = {}
+    xb, xq = datagen.cfg3(N=24_000, D=960, B=300, n_centers=64, seed=41)
+    out["d960"] = (build_index(xb, 40, dev, max_batch=512), xq.numpy())
+    xb, xq = datagen.cfg1(N=20_000, D=288, B=300, n_centers=32, seed=42)  # last step half-full
+    out["d288"] = (build_index(xb, 48, dev, max_batch=512), xq.numpy())
+    return out
+
+
+@pytest.mark.parametrize("name", ["d960", "d288"])
+@pytest.mark.parametrize("K", [1, 10, 64])
+def test_batched_wide_route_exact(wide_sets, dev, name, K):
+    b, xq = wide_sets[name]
+    assert b.ix.D_pad > 256
+    for nprobe in (3, 16):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"batched {name} K={K} nprobe={nprobe}")
+
+
+def test_batched_wide_matches_pair_route_and_auto(wide_sets, dev):
+    b, xq = wide_sets["d960"]
+    xqd = _q(xq, dev)
+    assert b.ix.route_for(len(xq), 16, 10) == 2  # AUTO takes the batched route at D = 960
+    d1, i1 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=1)
+    d2, i2 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=2)
+    d0, i0 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=0)
+    assert np.array_equal(i1, i2) and np.array_equal(d1, d2)
+    assert np.array_equal(i0, i2) and np.array_equal(d0, d2)
+
+
+def test_batched_wide_host_mapped_base(dev):
+    xb, xq = datagen.cfg3(N=12_000, D=960, B=120, n_centers=32, seed=43)
+    b = build_index(xb, 24, dev, xb_placement="host", max_batch=128)
+    _, rd, ri = oracle_search(b, xq.numpy(), 6, 10)
+    d, i = run_search(b, _q(xq.numpy(), dev), 6, 10, mode=2, ub=1, route=2)
+    assert_exact(d, i, rd, ri, "batched wide ooc")
+    b.ix.storage._host_buf.free()

@@ -53,7 +53,7 @@ namespace trident {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kUbList = 16;  // per-lane upper-bound list (K <= 64)
-constexpr int kBlkV = 64;    // vectors per LDS block
+constexpr int kBlkV = 64;    // slices start on multiples of 64 vectors (whole LDS blocks)
 constexpr int kWaveQ = 16;   // queries per wave
 
 // Vector slices of a cluster in pass p.  Pass-1 segments (the seeding probes) keep whole
@@ -197,22 +197,23 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
 // entry and (key, original id) on exit, or (kKeyInvalid, kIdInvalid) when the canonical
 // float64 distance exceeds tau[q].  One wave per (query, 64-slot chunk of its list), one
 // survivor per lane (a query with many survivors spreads over many waves); each lane walks its
-// own row in dimension order with 16-byte loads, against the query row staged in LDS (the
-// batched route has D <= 256).  An
-// overflowed list (count > cap) is left alone: the merge rescans that query's probes
-// exhaustively.
-template <bool HOST>
+// own row in dimension order with 16-byte loads, against the query row staged in LDS (DQ >= D
+// floats per wave: 256, or 1024 for the wide batched route).  An overflowed list
+// (count > cap) is left alone: the merge rescans that query's probes exhaustively.
+template <bool HOST, int DQ>
 __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int B) {
-    __shared__ __align__(16) float s_q[kWavesPerBlock][256];
+    __shared__ __align__(16) float s_q[kWavesPerBlock][HOST ? 1 : DQ];  // host: float64 copy below
     const int lane = threadIdx.x & 63, wid = (int)(threadIdx.x >> 6);
     const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + wid);
     if (q >= B) return;
     const int cnt = a.cand_cnt[q];
     if (cnt > a.cap || (int)blockIdx.y * kWave >= cnt) return;
     const double tau = a.tau[q];
-    const int D = a.D;  // <= D_pad <= 256 on the batched route
-    for (int d = lane; d < D; d += kWave) s_q[wid][d] = a.xq[(size_t)q * D + d];
-    __builtin_amdgcn_wave_barrier();
+    const int D = a.D;  // <= DQ (the launch picks DQ from D)
+    if constexpr (!HOST) {
+        for (int d = lane; d < D; d += kWave) s_q[wid][d] = a.xq[(size_t)q * D + d];
+        __builtin_amdgcn_wave_barrier();
+    }
     const float* qr = s_q[wid];
     uint64_t* ck = a.cand_key + (size_t)q * a.cap;
     int32_t* ci = a.cand_id + (size_t)q * a.cap;
@@ -222,9 +223,9 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
         // base in mapped host memory: rows cross PCIe, so they are read as 128-byte row
         // segments (all of a 32-dim chunk's loads in flight) and staged through LDS
         __shared__ int32_t s_pos[kWavesPerBlock][kWave];
-        __shared__ double s_q64[kWavesPerBlock][256];
+        __shared__ double s_q64[kWavesPerBlock][DQ];
         __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
-        for (int d = lane; d < D; d += kWave) s_q64[wid][d] = (double)qr[d];
+        for (int d = lane; d < D; d += kWave) s_q64[wid][d] = (double)a.xq[(size_t)q * D + d];
         for (int s0 = (int)blockIdx.y * kWave; s0 < cnt; s0 += kWave * (int)gridDim.y) {
             const int s = s0 + lane, n = min(kWave, cnt - s0);
             const int pos = s < cnt ? ci[s] : 0;
@@ -286,8 +287,10 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
         atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
 }
 
-template __global__ void refine_survivors_kernel<false>(BatchArgs, int);
-template __global__ void refine_survivors_kernel<true>(BatchArgs, int);
+template __global__ void refine_survivors_kernel<false, 256>(BatchArgs, int);
+template __global__ void refine_survivors_kernel<true, 256>(BatchArgs, int);
+template __global__ void refine_survivors_kernel<false, 1024>(BatchArgs, int);
+template __global__ void refine_survivors_kernel<true, 1024>(BatchArgs, int);
 
 __device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
@@ -387,13 +390,17 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     const int D_pad = a.D_pad, DP = a.DP;
     const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
     const float* xr = a.xrot32 + (size_t)q * D_pad;
-    float w[KS][16];
+    // Up to 256 dims the weights stay in registers between the group scale and the
+    // quantisation; wider, the second loop recomputes them (the same operations, so the same
+    // values).
+    constexpr bool KEEP = KS <= 4;
+    float w[KEEP ? KS : 1][16];
     float mx = 0.0f, Qp = 0.0f, qq = 0.0f, wl1 = 0.0f;
-#pragma unroll
-    for (int k = 0; k < KS; ++k) {
+    auto weights = [&](int k, float (&wk)[16], auto sums_c) {
+        constexpr bool SUMS = decltype(sums_c)::value;
         const int d0 = 64 * k + 16 * l;  // D_pad is a multiple of 32: all 16 dims or none
 #pragma unroll
-        for (int e = 0; e < 16; ++e) w[k][e] = 0.0f;
+        for (int e = 0; e < 16; ++e) wk[e] = 0.0f;
         if (d0 < D_pad) {
 #pragma unroll
             for (int h = 0; h < 4; ++h) {
@@ -405,13 +412,27 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float qp = xv[e] - vv[e];
-                    w[k][4 * h + e] = gv[e] * qp;
-                    mx = fmaxf(mx, fabsf(w[k][4 * h + e]));
-                    wl1 += fabsf(w[k][4 * h + e]);
-                    Qp = fmaf(qp, qp, Qp);
-                    qq = fmaf(xv[e], xv[e], qq);
+                    wk[4 * h + e] = gv[e] * qp;
+                    if constexpr (SUMS) {
+                        mx = fmaxf(mx, fabsf(wk[4 * h + e]));
+                        wl1 += fabsf(wk[4 * h + e]);
+                        Qp = fmaf(qp, qp, Qp);
+                        qq = fmaf(xv[e], xv[e], qq);
+                    }
                 }
             }
+        }
+    };
+    if constexpr (KEEP) {
+#pragma unroll
+        for (int k = 0; k < KS; ++k) weights(k, w[k], std::true_type{});
+    } else {
+        // rolled loops: unrolled, the compiler would keep every step's weights live into the
+        // second loop instead of recomputing them
+#pragma unroll 1
+        for (int k = 0; k < KS; ++k) {
+            float wk[16];
+            weights(k, wk, std::true_type{});
         }
     }
 #pragma unroll
@@ -432,15 +453,18 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     const float s = ldexpf(1.0f, es), inv_s = ldexpf(1.0f, -es);
     int wsum = 0;
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
-#pragma unroll
+#pragma unroll KEEP ? KS : 1
     for (int k = 0; k < KS; ++k) {
+        float wre[16];
+        if constexpr (!KEEP) weights(k, wre, std::false_type{});
+        const float(&wk)[16] = KEEP ? w[KEEP ? k : 0] : wre;
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
             int wi[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                wi[e] = (int)rintf(w[k][4 * h + e] * inv_s);  // 0 for dims >= D_pad
+                wi[e] = (int)rintf(wk[4 * h + e] * inv_s);  // 0 for dims >= D_pad
                 wsum += wi[e];
             }
             // lo = the low byte of wi as int8, hi = (wi - lo) / 256 = the second byte of
@@ -483,6 +507,18 @@ template __global__ void pair_prep_kernel<1>(BatchArgs);
 template __global__ void pair_prep_kernel<2>(BatchArgs);
 template __global__ void pair_prep_kernel<3>(BatchArgs);
 template __global__ void pair_prep_kernel<4>(BatchArgs);
+template __global__ void pair_prep_kernel<5>(BatchArgs);
+template __global__ void pair_prep_kernel<6>(BatchArgs);
+template __global__ void pair_prep_kernel<7>(BatchArgs);
+template __global__ void pair_prep_kernel<8>(BatchArgs);
+template __global__ void pair_prep_kernel<9>(BatchArgs);
+template __global__ void pair_prep_kernel<10>(BatchArgs);
+template __global__ void pair_prep_kernel<11>(BatchArgs);
+template __global__ void pair_prep_kernel<12>(BatchArgs);
+template __global__ void pair_prep_kernel<13>(BatchArgs);
+template __global__ void pair_prep_kernel<14>(BatchArgs);
+template __global__ void pair_prep_kernel<15>(BatchArgs);
+template __global__ void pair_prep_kernel<16>(BatchArgs);
 
 // m <- the 16 smallest of two ascending 16-lists (m, o), ascending, all in registers:
 // min(m[i], o[15 - i]) is a bitonic sequence holding them; four half-cleaner stages sort it.
@@ -541,6 +577,14 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
 // M0 (the LDS address of the load, latched at issue) is saved and restored around it.
+// A wave-uniform base pointer kept in SGPRs: inside lane-divergent branches the compiler may
+// otherwise materialise it in VGPRs, which the direct loads' saddr operand cannot take.
+__device__ __forceinline__ const void* sgpr_ptr(const void* p) {
+    const uint64_t v = (uint64_t)(size_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return (const void*)(size_t)(((uint64_t)hi << 32) | lo);
+}
 __device__ __forceinline__ void load_lds16(const void* base, uint32_t off, const void* lds) {
     uint32_t keep;
     asm volatile(
@@ -554,6 +598,38 @@ __device__ __forceinline__ void load_lds4(const void* base, uint32_t off, const 
         "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
         "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
         : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
+}
+
+// Vectors per LDS block of the scan kernels: 64 while D_pad <= 256 (16 KiB of codes a block),
+// 16 for D_pad up to 1024 (at most 16 KiB a block, so two blocks and four waves' weights in
+// registers still leave room for several workgroups per CU).
+__host__ __device__ constexpr int block_vectors(int KS) { return KS <= 4 ? 64 : 16; }
+
+// Direct loads of one 16-vector block (the wide layout, D_pad > 256) of a tile's code cells
+// (cells [g][T] of 16 bytes, g < G16 = D_pad / 16, starting at slot cw) into an LDS buffer
+// laid out [g][16], plus the block's row scalars (A_lo, r) into sA / sr.  One wave-load moves
+// 64 cells = 4 groups (one 64-dim step) of 16 vectors; the workgroup's waves take every 4th
+// step.  Groups past G16 (the last step when D_pad is an odd multiple of 32) are not loaded:
+// their weights are zero.  Rows past the slice read the slice's last row (never used).
+template <int KS>
+__device__ __forceinline__ void load_code_block16(const uint4* tile_cells, int cw, int T,
+                                                  int G16, int wid, int lane, uint4* lds,
+                                                  const float2* rows_Ar, int row0,
+                                                  int row_last, float* sA, float* sr) {
+    const uint4* base = static_cast<const uint4*>(sgpr_ptr(tile_cells + cw));
+    const int grp_l = lane >> 4, v = lane & 15;
+#pragma unroll
+    for (int jj = 0; jj < (KS + kWavesPerBlock - 1) / kWavesPerBlock; ++jj) {
+        const int L = wid + kWavesPerBlock * jj;
+        if (L < KS && 4 * L + grp_l < G16)
+            load_lds16(base, 16u * (uint32_t)((4 * L + grp_l) * T + v), lds + L * kWave);
+    }
+    if (wid == 0 && lane < 16) {
+        const void* rb = sgpr_ptr(rows_Ar);
+        const uint32_t off = 8u * (uint32_t)min(row0 + lane, row_last);
+        load_lds4(rb, off, sA);
+        load_lds4(rb, off + 4u, sr);
+    }
 }
 
 // Pass A (seeding), the first p_init probes: for every query of a unit the K-th smallest upper
@@ -580,12 +656,13 @@ __device__ __forceinline__ void load_lds4(const void* base, uint32_t off, const 
 template <int KS, int M>
 __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
     // The code buffers double as the end-of-unit list exchange (after a barrier).
-    constexpr int kCodeU4 = 2 * KS * 4 * kBlkV, kUblU4 = kWavesPerBlock * kWaveQ * kWave / 4;
+    constexpr int BV = block_vectors(KS);
+    constexpr int kCodeU4 = 2 * KS * 4 * BV, kUblU4 = kWavesPerBlock * kWaveQ * kWave / 4;
     __shared__ uint4 s_big[kCodeU4 > kUblU4 ? kCodeU4 : kUblU4];
-    uint4(*s_codes)[KS * 4 * kBlkV] = reinterpret_cast<uint4(*)[KS * 4 * kBlkV]>(s_big);
+    uint4(*s_codes)[KS * 4 * BV] = reinterpret_cast<uint4(*)[KS * 4 * BV]>(s_big);
     float(*s_ubl)[kWaveQ * kWave] = reinterpret_cast<float(*)[kWaveQ * kWave]>(s_big);
-    __shared__ __align__(16) float s_A[2][kBlkV];
-    __shared__ __align__(16) float s_r[2][kBlkV];
+    __shared__ __align__(16) float s_A[2][BV];
+    __shared__ __align__(16) float s_r[2][BV];
     __shared__ int s_unit[2];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -654,7 +731,7 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
             v4i A[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const uint4 v = blk[(ks * 4 + g) * kBlkV + t * 16 + j];
+                const uint4 v = blk[(ks * 4 + g) * BV + t * 16 + j];
                 A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
             const int row0 = t * 16 + 4 * g;
@@ -698,33 +775,40 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
         const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;
         int ct = vb / T, cw = vb - ct * T;
         auto gload = [&](int buf, int blk0) {
-            const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
+            if constexpr (BV == 64) {
+                const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
 #pragma unroll
-            for (int jj = 0; jj < KS; ++jj)
-                if (wid + 4 * jj < G16)
-                    load_lds16(base + (size_t)(4 * jj) * T, 16u * lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
-            cw += kBlkV;
+                for (int jj = 0; jj < KS; ++jj)
+                    if (wid + 4 * jj < G16)
+                        load_lds16(base + (size_t)(4 * jj) * T, 16u * lane,
+                                   &s_codes[buf][(wid + 4 * jj) * BV]);
+                if (wid == 0) {  // rows past the slice read the slice's last row (never used)
+                    const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
+                    load_lds4(a.vec_Ar + v0, off, s_A[buf]);
+                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
+                }
+            } else {
+                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T, cw, T, G16, wid, lane,
+                                      s_codes[buf], a.vec_Ar + v0, blk0, ve - 1, s_A[buf],
+                                      s_r[buf]);
+            }
+            cw += BV;
             if (cw == T) {
                 cw = 0;
                 ++ct;
             }
-            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
-                const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
-                load_lds4(a.vec_Ar + v0, off, s_A[buf]);
-                load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
-            }
         };
-        const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
+        const int nblk = (ve - vb + BV - 1) / BV;
         if (nblk > 0) gload(0, vb);
         for (int b = 0; b < nblk; ++b) {
             const int buf = b & 1;
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
-            const int blk0 = vb + b * kBlkV;
-            if (b + 1 < nblk) gload(buf ^ 1, blk0 + kBlkV);
+            const int blk0 = vb + b * BV;
+            if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
             if (active) {
-                for (int t = rr; t < kBlkV / 16; t += R) {
+                for (int t = rr; t < BV / 16; t += R) {
                     if (blk0 + t * 16 >= ve) break;
                     tile(buf, t, blk0 + t * 16);
                 }
@@ -813,6 +897,30 @@ template __global__ void ub_scan_kernel<1, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<2, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<3, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<4, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<5, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<6, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<7, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<8, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<9, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<10, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<11, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<12, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<13, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<14, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<15, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<16, 4>(BatchArgs);
+template __global__ void ub_scan_kernel<5, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<6, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<7, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<8, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<9, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<10, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<11, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<12, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<13, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<14, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<15, 16>(BatchArgs);
+template __global__ void ub_scan_kernel<16, 16>(BatchArgs);
 
 // ---------------------------------------------------------------------------------------------
 // Lower-bound pass.
@@ -904,10 +1012,11 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
 template <int KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 7 : 1)))
 void lb_scan_kernel(BatchArgs a) {
-    __shared__ uint4 s_codes[2][KS * 4 * kBlkV];
-    __shared__ __align__(16) float s_A[2][kBlkV];
-    __shared__ __align__(16) float s_r[2][kBlkV];
-    __shared__ __align__(16) int s_thr[2][kWavesPerBlock][kBlkV];
+    constexpr int BV = block_vectors(KS);
+    __shared__ uint4 s_codes[2][KS * 4 * BV];
+    __shared__ __align__(16) float s_A[2][BV];
+    __shared__ __align__(16) float s_r[2][BV];
+    __shared__ __align__(16) int s_thr[2][kWavesPerBlock][BV];
     __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
     __shared__ int s_scnt[kWavesPerBlock][kWaveQ], s_sbase[kWavesPerBlock][kWaveQ],
         s_sqid[kWavesPerBlock][kWaveQ];
@@ -1032,7 +1141,7 @@ void lb_scan_kernel(BatchArgs a) {
             v4i A[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const uint4 v = blk[(ks * 4 + g) * kBlkV + t * 16 + j];
+                const uint4 v = blk[(ks * 4 + g) * BV + t * 16 + j];
                 A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
             int4 th = make_int4(0, 0, 0, 0);
@@ -1079,23 +1188,30 @@ void lb_scan_kernel(BatchArgs a) {
         const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
         int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
         auto gload = [&](int buf, int blk0) {
-            const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
+            if constexpr (BV == 64) {
+                const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
 #pragma unroll
-            for (int jj = 0; jj < KS; ++jj)
-                if (wid + 4 * jj < G16)
-                    load_lds16(base + (size_t)(4 * jj) * T, 16u * lane, &s_codes[buf][(wid + 4 * jj) * kBlkV]);
-            cw += kBlkV;
+                for (int jj = 0; jj < KS; ++jj)
+                    if (wid + 4 * jj < G16)
+                        load_lds16(base + (size_t)(4 * jj) * T, 16u * lane,
+                                   &s_codes[buf][(wid + 4 * jj) * BV]);
+                if (wid == 0) {  // rows past the slice read the slice's last row (never used)
+                    const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
+                    load_lds4(a.vec_Ar + v0, off, s_A[buf]);
+                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
+                }
+            } else {
+                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T, cw, T, G16, wid, lane,
+                                      s_codes[buf], a.vec_Ar + v0, blk0, ve - 1, s_A[buf],
+                                      s_r[buf]);
+            }
+            cw += BV;
             if (cw == T) {
                 cw = 0;
                 ++ct;
             }
-            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
-                const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
-                load_lds4(a.vec_Ar + v0, off, s_A[buf]);
-                load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
-            }
         };
-        const int nblk = (ve - vb + kBlkV - 1) / kBlkV;
+        const int nblk = (ve - vb + BV - 1) / BV;
         if (nblk > 0) gload(0, vb);
         for (int b = 0; b < nblk; ++b) {
             const int buf = b & 1;
@@ -1103,23 +1219,26 @@ void lb_scan_kernel(BatchArgs a) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
-            const int blk0 = vb + b * kBlkV;
-            if (b + 1 < nblk) gload(buf ^ 1, blk0 + kBlkV);
+            const int blk0 = vb + b * BV;
+            if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
             if (active) {
                 if (int_ok) {
-                    const float A = s_A[buf][lane], r = s_r[buf][lane];
-                    s_thr[buf][wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
-                    if (R == 1 && blk0 + kBlkV <= ve) {  // the common case: straight-line tiles
+                    if (BV == kWave || lane < BV) {
+                        const float A = s_A[buf][lane], r = s_r[buf][lane];
+                        s_thr[buf][wid][lane] =
+                            blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                    }
+                    if (R == 1 && blk0 + BV <= ve) {  // the common case: straight-line tiles
 #pragma unroll
-                        for (int t = 0; t < kBlkV / 16; ++t) tile(std::true_type{}, buf, t, blk0 + t * 16);
+                        for (int t = 0; t < BV / 16; ++t) tile(std::true_type{}, buf, t, blk0 + t * 16);
                     } else {
-                        for (int t = rr; t < kBlkV / 16; t += R) {
+                        for (int t = rr; t < BV / 16; t += R) {
                             if (blk0 + t * 16 >= ve) break;
                             tile(std::true_type{}, buf, t, blk0 + t * 16);
                         }
                     }
                 } else {
-                    for (int t = rr; t < kBlkV / 16; t += R) {
+                    for (int t = rr; t < BV / 16; t += R) {
                         if (blk0 + t * 16 >= ve) break;
                         tile(std::false_type{}, buf, t, blk0 + t * 16);
                     }
@@ -1144,6 +1263,18 @@ template __global__ void lb_scan_kernel<1>(BatchArgs);
 template __global__ void lb_scan_kernel<2>(BatchArgs);
 template __global__ void lb_scan_kernel<3>(BatchArgs);
 template __global__ void lb_scan_kernel<4>(BatchArgs);
+template __global__ void lb_scan_kernel<5>(BatchArgs);
+template __global__ void lb_scan_kernel<6>(BatchArgs);
+template __global__ void lb_scan_kernel<7>(BatchArgs);
+template __global__ void lb_scan_kernel<8>(BatchArgs);
+template __global__ void lb_scan_kernel<9>(BatchArgs);
+template __global__ void lb_scan_kernel<10>(BatchArgs);
+template __global__ void lb_scan_kernel<11>(BatchArgs);
+template __global__ void lb_scan_kernel<12>(BatchArgs);
+template __global__ void lb_scan_kernel<13>(BatchArgs);
+template __global__ void lb_scan_kernel<14>(BatchArgs);
+template __global__ void lb_scan_kernel<15>(BatchArgs);
+template __global__ void lb_scan_kernel<16>(BatchArgs);
 
 // tau_sq output of the batched route: the seeded float64 threshold, rounded up to float32.
 __global__ void tau_to_f32_kernel(const double* tau, float* out, int B) {

@@ -19,6 +19,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "../../include/trident_hip.h"
 #include "common.hpp"
@@ -256,14 +257,14 @@ int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
 }
 
 // Route of a mode-2 search.  The batched route needs the per-vector scalars, K <= 64 (its
-// upper-bound seeding keeps 16 bounds per lane, 64 per query), D_pad <= 256 (query weights
-// held in registers) and N < 2^27 (a queued survivor packs its index within the cluster
+// upper-bound seeding keeps 16 bounds per lane, 64 per query), D_pad <= 1024 (query weights
+// held in registers: 8 VGPRs per 64 dims) and N < 2^27 (a queued survivor packs its index within the cluster
 // into 28 bits); AUTO takes it when clusters are shared by >= 8 queries on average, where
 // the contraction is dense enough for the matrix cores.
 int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                  int nprobe, int* route) {
     const bool ok = ix->vec_Ar && ix->sq8_cells && ix->orig_ids_sorted && K <= 64 &&
-                    ix->D_pad <= 256 &&
+                    ix->D_pad <= 1024 &&
                     ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
@@ -273,7 +274,7 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
         case TRIDENT_ROUTE_BATCHED:
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
-                            "batched route needs vec_Ar, sq8_cells, K <= 64, D_pad <= 256 and "
+                            "batched route needs vec_Ar, sq8_cells, K <= 64, D_pad <= 1024 and "
                             "N < 2^27 "
                             "(K=%d, D_pad=%d, N=%d)",
                             K, ix->D_pad, ix->N);
@@ -332,30 +333,40 @@ int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
     }
 }
 
+// Calls f(std::integral_constant<int, KS>) for the 64-dim step count KS in [1, 16] (D_pad up
+// to 1024); false for any other count.
+template <int KS = 1, class F>
+bool with_ks(int ks, F&& f) {
+    if constexpr (KS > 16) {
+        return false;
+    } else {
+        if (ks == KS) {
+            f(std::integral_constant<int, KS>{});
+            return true;
+        }
+        return with_ks<KS + 1>(ks, f);
+    }
+}
+
 int launch_pair_prep(const BatchArgs& b, hipStream_t st) {
     if (b.M <= 0) return TRIDENT_OK;
     static_assert(kGroupQ * 4 == kWave, "one weight group per wave, 4 lanes a pair");
     // one group per wave; waves past the group count return
     const unsigned grid = (unsigned)((b.max_groups + kWavesPerBlock - 1) / kWavesPerBlock);
-    switch (b.DP / 64) {
-        case 1: pair_prep_kernel<1><<<grid, kBlock, 0, st>>>(b); break;
-        case 2: pair_prep_kernel<2><<<grid, kBlock, 0, st>>>(b); break;
-        case 3: pair_prep_kernel<3><<<grid, kBlock, 0, st>>>(b); break;
-        case 4: pair_prep_kernel<4><<<grid, kBlock, 0, st>>>(b); break;
-        default: return fail(TRIDENT_ERR_UNSUPPORTED, "batched route needs D_pad <= 256");
-    }
+    const bool ok = with_ks(b.DP / 64, [&](auto ks_c) {
+        pair_prep_kernel<decltype(ks_c)::value><<<grid, kBlock, 0, st>>>(b);
+    });
+    if (!ok) return fail(TRIDENT_ERR_UNSUPPORTED, "batched route needs D_pad <= 1024");
     return check_launch("pair_prep_kernel");
 }
 
 template <bool UB>
 int launch_batch(const BatchArgs& b, hipStream_t st) {
-    switch ((b.D_pad + 63) / 64) {
-        case 1: return launch_batch_ks<UB, 1>(b, st);
-        case 2: return launch_batch_ks<UB, 2>(b, st);
-        case 3: return launch_batch_ks<UB, 3>(b, st);
-        case 4: return launch_batch_ks<UB, 4>(b, st);
-        default: return fail(TRIDENT_ERR_UNSUPPORTED, "batched route needs D_pad <= 256");
-    }
+    int rc = TRIDENT_OK;
+    const bool ok = with_ks((b.D_pad + 63) / 64, [&](auto ks_c) {
+        rc = launch_batch_ks<UB, decltype(ks_c)::value>(b, st);
+    });
+    return ok ? rc : fail(TRIDENT_ERR_UNSUPPORTED, "batched route needs D_pad <= 1024");
 }
 
 int launch_merge(const MergeArgs& m, int KP, hipStream_t st) {
@@ -762,10 +773,17 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         // the chunk dimension stops at 16: waves loop over further chunks
         const dim3 rgrid((unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock),
                          (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
-        if (b.xb_host)
-            refine_survivors_kernel<true><<<rgrid, kBlock, 0, st>>>(b, B);
-        else
-            refine_survivors_kernel<false><<<rgrid, kBlock, 0, st>>>(b, B);
+        if (ix->D <= 256) {
+            if (b.xb_host)
+                refine_survivors_kernel<true, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+            else
+                refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+        } else {
+            if (b.xb_host)
+                refine_survivors_kernel<true, 1024><<<rgrid, kBlock, 0, st>>>(b, B);
+            else
+                refine_survivors_kernel<false, 1024><<<rgrid, kBlock, 0, st>>>(b, B);
+        }
         if ((rc = check_launch("refine_survivors_kernel"))) return rc;
         m.use_prev = 0;
         m.out_d = out->topk_d;

@@ -275,7 +275,7 @@ __global__ void lb_prep_kernel(BatchArgs a);
 template <int KS>
 __global__ void lb_scan_kernel(BatchArgs a);
 
-template <bool HOST>
+template <bool HOST, int DQ>
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
 
 template <int KS>
