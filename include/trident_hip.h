@@ -70,10 +70,12 @@ typedef struct TridentIndexView {
     const float* vec_Ar;             /* [N, 2] sorted order: |code*delta|^2 rounded down (margin
                                         1e-13), residual-norm bound rounded up; NULL disables the
                                         batched route */
-    const uint32_t* sq8_cells;       /* [total_tiles, D_pad / 16, tile_size, 4]: the codes of
+    const uint32_t* sq8_cells;       /* [total_tiles, tile_size / V, D_pad / 16, V, 4] with
+                                        V = 64 for D_pad <= 256, else 16: the codes of
                                         sq8_packed regrouped as 16-byte cells (dims 16 g ..
                                         16 g + 15 of one slot), every byte c stored as c ^ 0x80
-                                        (c - 128 as int8); NULL disables the batched route */
+                                        (c - 128 as int8), each V-slot block contiguous; NULL
+                                        disables the batched route */
     /* Centroids for the matrix-core coarse pass, Dq = D rounded up to 16, c_d = -W_combined[d, c]
      * / 2.  Optional (all or none): when cent_rows is NULL every search derives them from
      * W_combined into its workspace.  No counterpart in the reference (its coarse GEMM reads

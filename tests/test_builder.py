@@ -116,30 +116,44 @@ def test_codes_closed_form_and_packing(hist_ix):
 
 
 def unpack_cells(ix):
-    """[N, D_pad] uint8 codes recovered from sq8_cells [tiles, D_pad/16, T, 4] in sorted order."""
-    T = ix.tile_size
-    cells = ix.sq8_cells.numpy().view(np.uint8)           # [tiles, G16, T, 16] bytes c ^ 0x80
-    assert cells.shape == (ix.total_tiles, ix.D_pad // 16, T, 16)
+    """[N, D_pad] uint8 codes recovered from sq8_cells [tiles, T/V, D_pad/16, V, 4] in sorted
+    order (V = 64 up to 256 dims, else 16)."""
+    T, V = ix.tile_size, (64 if ix.D_pad <= 256 else 16)
+    cells = ix.sq8_cells.numpy().view(np.uint8)           # [tiles, T/V, G16, V, 16] bytes c ^ 0x80
+    assert cells.shape == (ix.total_tiles, T // V, ix.D_pad // 16, V, 16)
     toff = ix.cluster_tile_off.numpy()
     voff = ix.storage.cluster_vec_off.numpy()
     codes = np.zeros((ix.N, ix.D_pad), np.uint8)
     for c in range(ix.nlist):
         li = np.arange(voff[c + 1] - voff[c])
         t, s = toff[c] + li // T, li % T
-        codes[voff[c]:voff[c + 1]] = (cells[t, :, s, :] ^ 0x80).reshape(len(li), -1)
+        codes[voff[c]:voff[c + 1]] = (cells[t, s // V, :, s % V, :] ^ 0x80).reshape(len(li), -1)
     return codes
 
 
-@pytest.mark.parametrize("which", ["hist", "gmm"])
-def test_cells_hold_the_packed_codes(which, hist_ix, gmm_ix):
-    """The batched route's 16-byte cells (dims 16 g .. 16 g + 15 of a slot, bytes c ^ 0x80)
-    decode to exactly the codes of sq8_packed, and padded slots hold code 0."""
-    ix = (hist_ix if which == "hist" else gmm_ix)[0]
+@pytest.fixture(scope="module")
+def wide_ix():
+    """D = 300 (D_pad 320 > 256): 16-slot cell blocks, tile 256."""
+    xb, xq = datagen.cfg1(N=3000, D=300, B=16, n_centers=8, seed=5)
+    ix, cen, lid = build(xb, 6, T=256)
+    return ix, xb.numpy(), xq.numpy(), cen, lid
+
+
+@pytest.mark.parametrize("which", ["hist", "gmm", "wide"])
+def test_cells_hold_the_packed_codes(which, hist_ix, gmm_ix, wide_ix):
+    """The batched route's 16-byte cells (dims 16 g .. 16 g + 15 of a slot, bytes c ^ 0x80,
+    block-major) decode to exactly the codes of sq8_packed, and padded slots hold code 0."""
+    ix = {"hist": hist_ix, "gmm": gmm_ix, "wide": wide_ix}[which][0]
     codes, _ = unpack_codes(ix)
     assert np.array_equal(unpack_cells(ix), codes)
+    V = 64 if ix.D_pad <= 256 else 16
     cells = ix.sq8_cells.numpy().view(np.uint8)
     pad = ix.tile_orig_ids.numpy() < 0                     # [tiles, T]
-    assert (cells[pad.nonzero()[0], :, pad.nonzero()[1], :] == 0x80).all()
+    t, s = pad.nonzero()
+    assert len(t) > 0
+    assert (cells[t, s // V, :, s % V, :] == 0x80).all()
+    # one scan block of V slots is one contiguous run of D_pad / 16 * V cells
+    assert cells.shape[1:] == (ix.tile_size // V, ix.D_pad // 16, V, 16)
 
 
 @pytest.mark.parametrize("which", ["hist", "gmm"])

@@ -165,3 +165,24 @@ def test_batched_wide_host_mapped_base(dev):
     d, i = run_search(b, _q(xq.numpy(), dev), 6, 10, mode=2, ub=1, route=2)
     assert_exact(d, i, rd, ri, "batched wide ooc")
     b.ix.storage._host_buf.free()
+
+
+def test_batched_wide_exact_ties_and_replicas(dev):
+    """D = 300 (wide layout, last 64-dim step half-full), 40 copies of every row: ties at the
+    threshold everywhere.  Units of few queries make replica waves split the 64-dim steps and
+    finish each block from their summed partials one block later; an early accumulator read
+    or a partial summed twice changes the answer."""
+    rng = np.random.default_rng(44)
+    base = rng.integers(0, 3, size=(60, 300)).astype(np.float32)
+    xb = np.repeat(base, 40, axis=0)
+    nlist = 6
+    cen = rng.integers(0, 3, size=(nlist, 300)).astype(np.float32)
+    lid = np.argmin(((xb[:, None, :] - cen[None]) ** 2).sum(-1), 1).astype(np.int32)
+    xq = np.concatenate([base[:20], rng.integers(0, 3, size=(20, 300))]).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=64)
+    assert b.ix.D_pad == 320
+    for rep in range(2):
+        for K, nprobe in ((5, 2), (10, 4), (64, 6)):
+            _, rd, ri = oracle_search(b, xq, nprobe, K)
+            d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
+            assert_exact(d, i, rd, ri, f"wide ties rep={rep} K={K} nprobe={nprobe}")

@@ -56,12 +56,13 @@ constexpr int kUbList = 16;  // per-lane upper-bound list (K <= 64)
 constexpr int kBlkV = 64;    // slices start on multiples of 64 vectors (whole LDS blocks)
 constexpr int kWaveQ = 16;   // queries per wave
 
-// Vector slices of a cluster in pass p.  Pass-1 segments (the seeding probes) keep whole
-// clusters: the K-th smallest upper bound over a slice is a much weaker threshold than over
-// the cluster.  Pass-2 segments are sliced so that no unit runs far longer than the others.
+// Vector slices of a cluster (both passes), so that no unit runs far longer than the others.
+// The seeding pass loses nothing by slicing: every unit hands its K smallest bounds to the
+// query's list, and the threshold is the K-th smallest over all of them.
 __device__ __forceinline__ int splits_of(int n, int p) {
+    (void)p;
     if (n <= 0) return 0;
-    return p ? min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec) : 1;
+    return min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec);
 }
 
 __device__ __forceinline__ int units_of_entry(const int32_t* seg_off, const int32_t* vec_off,
@@ -131,8 +132,8 @@ __global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
     }
 }
 
-// One thread per unit: locate its segment by binary search over unit_off, then its query block
-// and vector slice.  Slices start on 64-vector blocks and are never empty (n > 64 S (S - 1)
+// One thread per unit: locate its segment by binary search over unit_off, then its vector slice
+// and query block.  Slices start on 64-vector blocks and are never empty (n > 64 S (S - 1)
 // whenever S = ceil(n / kSplitVec) > 1).
 // Then one thread per weight group: {first pair, pair count}.
 __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
@@ -170,9 +171,12 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
         const int n = vec_off[c + 1] - vec_off[c];
         const int S = splits_of(n, p);
         const int local = u - unit_off[lo];
-        const int qb = local / S, sp = local - qb * S;
         const int q = so[c + 1] - so[c];
         const int uq = p ? kUnitQ : kUnitQ0;
+        // slice-major: a slice's query blocks are consecutive units, so the workgroups that
+        // take them together read the slice's codes while they are in the XCD's L2
+        const int QB = (q + uq - 1) / uq;
+        const int sp = local / QB, qb = local - sp * QB;
         const int cnt = min(uq, q - qb * uq);
         const int len = ((n + S - 1) / S + kBlkV - 1) & ~(kBlkV - 1);
         const int vb = sp * len, ve = min(n, vb + len);
@@ -355,6 +359,7 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
             qep[q] = ep;
             a.tau[q] = INFINITY;
             a.cand_cnt[q] = 0;
+            a.ub_cnt[q] = 0;
         }
     }
 }
@@ -443,12 +448,21 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         qq += __shfl_xor(qq, o, kWave);
         wl1 += __shfl_xor(wl1, o, kWave);
     }
+    float l1g = wl1;  // the group's largest sum |w|
+#pragma unroll
+    for (int o = 4; o < kWave; o <<= 1) l1g = fmaxf(l1g, __shfl_xor(l1g, o, kWave));
     // s and 1/s are powers of two in [2^-114, 2^114], so w * (1/s) is exactly w / s and
-    // s * wi is exact
+    // s * wi is exact.  Two limits: |w_int| <= 32639 (the hi / lo split), and, for every pair,
+    // sum |w_int| <= sum |w| / s + D_pad / 2 <= 2^23 - 1, so that |acc| <= 128 sum |w_int| <
+    // 2^30 and the lower-bound test's acc + kq (|kq| <= 2^30) stays inside int32.  The second
+    // follows from the first while D_pad <= 256; it binds only for wider weights.
     int es = 0;
     if (mx > 0x1p-100f) {
         es = ilogbf(mx) - 14;
         if (ldexpf(mx, -es) > 32639.0f) ++es;
+        const float lim = 8388607.0f - 0.5f * (float)D_pad;
+        const float l1u = l1g * (1.0f + (float)a.sum_rel);
+        for (int i = 0; i < 8 && ldexpf(l1u, -es) > lim; ++i) ++es;
     }
     const float s = ldexpf(1.0f, es), inv_s = ldexpf(1.0f, -es);
     int wsum = 0;
@@ -487,12 +501,12 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     if (valid && l == 0) {
         PairRec r;
         r.Qp = (double)Qp;
-        // float32 sums of <= 256 terms: relative error < 2^-15 (the (1 + 2^-15) factors here
-        // and the 2^-15 margins on Qp where it is used)
-        const double l1 = (double)wl1 * (1.0 + 0x1p-15);
+        // float32 sums of D_pad non-negative terms: relative error < sum_rel (the
+        // (1 + sum_rel) factors here and the sum_rel margins on Qp where it is used)
+        const double l1 = (double)wl1 * (1.0 + a.sum_rel);
         r.err_q = 255.0 * (0.5 * (double)D_pad * (double)s + 0x1p-22 * l1);
         // the query is the float32 rotation q32: |q32 - q_exact| <= e_q(float64) + 2^-23 |q32|
-        r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-23 * sqrt((double)qq) * (1.0 + 0x1p-15) +
+        r.e_q = sqrt(a.qep[q]) * (1.0 + 1e-12) + 0x1p-23 * sqrt((double)qq) * (1.0 + a.sum_rel) +
                 1e-30;
         r.cW = 128.0 * (double)wsum;
         r.c1 = 2.0 * (double)s;
@@ -605,24 +619,45 @@ __device__ __forceinline__ void load_lds4(const void* base, uint32_t off, const 
 // registers still leave room for several workgroups per CU).
 __host__ __device__ constexpr int block_vectors(int KS) { return KS <= 4 ? 64 : 16; }
 
-// Direct loads of one 16-vector block (the wide layout, D_pad > 256) of a tile's code cells
-// (cells [g][T] of 16 bytes, g < G16 = D_pad / 16, starting at slot cw) into an LDS buffer
-// laid out [g][16], plus the block's row scalars (A_lo, r) into sA / sr.  One wave-load moves
-// 64 cells = 4 groups (one 64-dim step) of 16 vectors; the workgroup's waves take every 4th
-// step.  Groups past G16 (the last step when D_pad is an odd multiple of 32) are not loaded:
-// their weights are zero.  Rows past the slice read the slice's last row (never used).
+// Wide layout: blocks in flight ahead of the one being scanned (a ring of kWideAhead + 1 code
+// buffers).  With ~200 VGPRs a CU holds two workgroups, so one block in flight each leaves the
+// loop waiting on load latency; the row scalars use a ring of 8 (the deferred replica finish
+// reads the previous block's).
+constexpr int kWideAhead = 2;
+
+// s_waitcnt vmcnt(n) for a wave-uniform n (the count is an instruction immediate); counts
+// above 15 wait for everything.
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    switch (n) {
+#define TRIDENT_VMCNT_CASE(k) \
+    case k: asm volatile("s_waitcnt vmcnt(" #k ")" ::: "memory"); break;
+        TRIDENT_VMCNT_CASE(1) TRIDENT_VMCNT_CASE(2) TRIDENT_VMCNT_CASE(3) TRIDENT_VMCNT_CASE(4)
+        TRIDENT_VMCNT_CASE(5) TRIDENT_VMCNT_CASE(6) TRIDENT_VMCNT_CASE(7) TRIDENT_VMCNT_CASE(8)
+        TRIDENT_VMCNT_CASE(9) TRIDENT_VMCNT_CASE(10) TRIDENT_VMCNT_CASE(11)
+        TRIDENT_VMCNT_CASE(12) TRIDENT_VMCNT_CASE(13) TRIDENT_VMCNT_CASE(14)
+        TRIDENT_VMCNT_CASE(15)
+#undef TRIDENT_VMCNT_CASE
+        default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
+// Direct loads of one 16-vector block (the wide layout, D_pad > 256) of code cells -- one
+// contiguous run [g][16] of 16-byte cells, g < G16 = D_pad / 16, in the block-major sq8_cells
+// -- into an LDS buffer of the same layout, plus the block's row scalars (A_lo, r) into sA /
+// sr.  One wave-load moves 1 KiB = 4 groups (one 64-dim step); the workgroup's waves take
+// every 4th step.  Groups past G16 (the last step when D_pad is an odd multiple of 32) are not
+// loaded: their weights are zero.  Rows past the slice read the slice's last row (never used).
 template <int KS>
-__device__ __forceinline__ void load_code_block16(const uint4* tile_cells, int cw, int T,
-                                                  int G16, int wid, int lane, uint4* lds,
-                                                  const float2* rows_Ar, int row0,
-                                                  int row_last, float* sA, float* sr) {
-    const uint4* base = static_cast<const uint4*>(sgpr_ptr(tile_cells + cw));
-    const int grp_l = lane >> 4, v = lane & 15;
+__device__ __forceinline__ void load_code_block16(const uint4* block_cells, int G16, int wid,
+                                                  int lane, uint4* lds, const float2* rows_Ar,
+                                                  int row0, int row_last, float* sA,
+                                                  float* sr) {
+    const uint4* base = static_cast<const uint4*>(sgpr_ptr(block_cells));
 #pragma unroll
     for (int jj = 0; jj < (KS + kWavesPerBlock - 1) / kWavesPerBlock; ++jj) {
         const int L = wid + kWavesPerBlock * jj;
-        if (L < KS && 4 * L + grp_l < G16)
-            load_lds16(base, 16u * (uint32_t)((4 * L + grp_l) * T + v), lds + L * kWave);
+        if (L < KS && 4 * L + (lane >> 4) < G16)
+            load_lds16(base, 16u * (uint32_t)(L * kWave + lane), lds + L * kWave);
     }
     if (wid == 0 && lane < 16) {
         const void* rb = sgpr_ptr(rows_Ar);
@@ -657,12 +692,18 @@ template <int KS, int M>
 __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
     // The code buffers double as the end-of-unit list exchange (after a barrier).
     constexpr int BV = block_vectors(KS);
-    constexpr int kCodeU4 = 2 * KS * 4 * BV, kUblU4 = kWavesPerBlock * kWaveQ * kWave / 4;
+    constexpr int NBC = BV == 64 ? 2 : kWideAhead + 1;  // code buffers
+    constexpr int kCodeU4 = NBC * KS * 4 * BV, kUblU4 = kWavesPerBlock * kWaveQ * kWave / 4;
     __shared__ uint4 s_big[kCodeU4 > kUblU4 ? kCodeU4 : kUblU4];
     uint4(*s_codes)[KS * 4 * BV] = reinterpret_cast<uint4(*)[KS * 4 * BV]>(s_big);
     float(*s_ubl)[kWaveQ * kWave] = reinterpret_cast<float(*)[kWaveQ * kWave]>(s_big);
-    __shared__ __align__(16) float s_A[2][BV];
-    __shared__ __align__(16) float s_r[2][BV];
+    // Row scalars: double-buffered with the codes, or (wide layout) a ring of 8 that also
+    // holds the block its replica waves finish one block late.  s_part: the replicas' partial
+    // sums.
+    constexpr int NAB = BV == 64 ? 2 : 8, NP = BV == 64 ? 1 : 2;
+    __shared__ __align__(16) float s_A[NAB][BV];
+    __shared__ __align__(16) float s_r[NAB][BV];
+    __shared__ int4 s_part[NP][NP > 1 ? kWavesPerBlock : 1][NP > 1 ? kWave : 1];
     __shared__ int s_unit[2];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -703,14 +744,25 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
             const int pj = start + gq * kWaveQ + (hasq ? j : 0);
             q = a.pair_qid[pj];
             const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
+            if (BV == 64 || R == 1) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
-                blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
+                for (int ks = 0; ks < KS; ++ks) {
+                    bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
+                    blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
+                }
+            } else {
+                // wide layout with R replicas: slot i holds step rr + i R (zero past KS)
+#pragma unroll
+                for (int i = 0; i < KS; ++i) {
+                    const int ks = rr + i * R;
+                    bhi[i] = ks < KS ? *reinterpret_cast<const v4i*>(hp + ks * 64) : v4i{0, 0, 0, 0};
+                    blo[i] = ks < KS ? *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64)
+                                     : v4i{0, 0, 0, 0};
+                }
             }
             if (hasq) {
                 const PairRec pr = a.prec[pj];
-                const double AQ = (pr.Qp * (1.0 + 0x1p-15) + 1e-30 + 2.0 * pr.err_q) * (1.0 + 1e-13);
+                const double AQ = (pr.Qp * (1.0 + a.sum_rel) + 1e-30 + 2.0 * pr.err_q) * (1.0 + 1e-13);
                 const double C = AQ - pr.c1 * pr.cW;
                 const double slack =
                     0x1p-22 * (pr.a_max * (1.0 + 0x1p-20) + pr.c1 * pr.acc_max + fabs(C)) *
@@ -771,26 +823,88 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
             }
         };
 
+        // ---- wide layout (D_pad > 256, one 16-vector tile per block): this wave's share of
+        // the 64-dim steps (all of them, or steps rr, rr + R, ... when R replica waves share
+        // the tile: each replica's partial sum is exact in int32 like the whole; R is 1, 2 or
+        // 4 and a compile-time constant here, so the weight slots stay in registers) ----
+        auto wide_partial = [&](int buf, int (&S)[4], auto r_c) {
+            constexpr int RC = decltype(r_c)::value, NS = (KS + RC - 1) / RC;
+            const uint4* blk = s_codes[buf];
+            // every A operand of the wave's steps first (its weight slots past KS are zero, so
+            // a clamped step contributes nothing), then the MFMA chains
+            v4i A[NS];
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                const int ks = RC == 1 ? i : min(rr + i * RC, KS - 1);
+                const uint4 v = blk[(ks * 4 + g) * BV + j];
+                A[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], bhi[i], acc_hi, 0, 0, 0);
+                acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], blo[i], acc_lo, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7\n\ts_nop 7");
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
+        };
+        // the block's rows from whole sums (rows 4 g + r of the tile, query column j)
+        auto wide_rows = [&](const int (&S)[4], int abuf, int li0) {
+            const float4 A4 = *reinterpret_cast<const float4*>(&s_A[abuf][4 * g]);
+            const float4 r4 = *reinterpret_cast<const float4*>(&s_r[abuf][4 * g]);
+            const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float E = fmaf(nc1, (float)S[r], Cq) + Av[r] * (1.0f + 0x1p-21f);
+                float u = fmaf(__builtin_amdgcn_sqrtf(fmaxf(E, 0x1p-126f)), 1.0f + 0x1p-20f,
+                               rv[r] + e_q) * (1.0f + 0x1p-21f);
+                if (li0 + 4 * g + r >= ve) u = INFINITY;
+                if (u < ubl[M - 1]) {
+#pragma unroll
+                    for (int i = M - 1; i > 0; --i)
+                        ubl[i] = (u < ubl[i - 1]) ? ubl[i - 1] : (u < ubl[i] ? u : ubl[i]);
+                    ubl[0] = u < ubl[0] ? u : ubl[0];
+                }
+            }
+        };
+        // replica (b mod R) of the group finishes block b from the R partial sums
+        auto wide_finish = [&](int b, int abuf) {
+            if (((b & (R - 1)) != rr)) return;
+            int S[4] = {0, 0, 0, 0};
+            for (int r2 = 0; r2 < R; ++r2) {
+                const int4 p = s_part[b & 1][gq * R + r2][lane];
+                S[0] += p.x;
+                S[1] += p.y;
+                S[2] += p.z;
+                S[3] += p.w;
+            }
+            wide_rows(S, abuf, vb + b * BV);
+        };
+
         // ---- stream the cluster through LDS in 64-vector blocks ----
         const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;
         int ct = vb / T, cw = vb - ct * T;
-        auto gload = [&](int buf, int blk0) {
+        auto gload = [&](int buf, int abuf, int blk0) {
             if constexpr (BV == 64) {
-                const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
+                // block-major cells: the block's groups are consecutive runs of 64 cells
+                const uint4* base = cells_c + (size_t)ct * G16 * T + (size_t)cw * G16 + wid * BV;
 #pragma unroll
                 for (int jj = 0; jj < KS; ++jj)
                     if (wid + 4 * jj < G16)
-                        load_lds16(base + (size_t)(4 * jj) * T, 16u * lane,
+                        load_lds16(base + (size_t)(4 * jj) * BV, 16u * lane,
                                    &s_codes[buf][(wid + 4 * jj) * BV]);
                 if (wid == 0) {  // rows past the slice read the slice's last row (never used)
                     const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
-                    load_lds4(a.vec_Ar + v0, off, s_A[buf]);
-                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
+                    load_lds4(a.vec_Ar + v0, off, s_A[abuf]);
+                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[abuf]);
                 }
             } else {
-                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T, cw, T, G16, wid, lane,
-                                      s_codes[buf], a.vec_Ar + v0, blk0, ve - 1, s_A[buf],
-                                      s_r[buf]);
+                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T + (size_t)cw * G16, G16,
+                                      wid, lane, s_codes[buf], a.vec_Ar + v0, blk0, ve - 1,
+                                      s_A[abuf], s_r[abuf]);
             }
             cw += BV;
             if (cw == T) {
@@ -799,19 +913,57 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
             }
         };
         const int nblk = (ve - vb + BV - 1) / BV;
-        if (nblk > 0) gload(0, vb);
-        for (int b = 0; b < nblk; ++b) {
-            const int buf = b & 1;
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
-            const int blk0 = vb + b * BV;
-            if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
-            if (active) {
-                for (int t = rr; t < BV / 16; t += R) {
-                    if (blk0 + t * 16 >= ve) break;
-                    tile(buf, t, blk0 + t * 16);
+        if constexpr (BV == 64) {
+            if (nblk > 0) gload(0, 0, vb);
+            for (int b = 0; b < nblk; ++b) {
+                const int buf = b & 1;
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+                const int blk0 = vb + b * BV;
+                if (b + 1 < nblk) gload(buf ^ 1, buf ^ 1, blk0 + BV);
+                if (active) {
+                    for (int t = rr; t < BV / 16; t += R) {
+                        if (blk0 + t * 16 >= ve) break;
+                        tile(buf, t, blk0 + t * 16);
+                    }
                 }
+            }
+        } else {
+            // Ring: block b in code buffer b % NBC and row-scalar slot b % 8, with blocks b + 1 ..
+            // b + kWideAhead in flight.  A wave waits only for its own loads of block b: the
+            // nload per block it issued later may still be outstanding (vector memory
+            // operations retire in issue order).  Replicas (R > 1) leave their partial sums of
+            // block b in s_part[b & 1]; after the next barrier replica (b mod R) adds them and
+            // finishes the rows.
+            const int nload = (KS - wid + 3) / 4 + (wid == 0 ? 2 : 0);
+            for (int p = 0; p < kWideAhead && p < nblk; ++p) gload(p, p, vb + p * BV);
+            int cs = 0;  // b % NBC
+            for (int b = 0; b < nblk; ++b) {
+                wait_vmcnt(min(kWideAhead - 1, nblk - 1 - b) * nload);
+                __syncthreads();
+                if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+                const int blk0 = vb + b * BV;
+                if (b + kWideAhead < nblk)  // into the buffer block b - 1 used
+                    gload(cs == 0 ? NBC - 1 : cs - 1, (b + kWideAhead) & 7,
+                          blk0 + kWideAhead * BV);
+                if (active) {
+                    int S[4];
+                    if (R == 1) {
+                        wide_partial(cs, S, std::integral_constant<int, 1>{});
+                        wide_rows(S, b & 7, blk0);
+                    } else {
+                        if (R == 2) wide_partial(cs, S, std::integral_constant<int, 2>{});
+                        else wide_partial(cs, S, std::integral_constant<int, 4>{});
+                        s_part[b & 1][wid][lane] = make_int4(S[0], S[1], S[2], S[3]);
+                        if (b > 0) wide_finish(b - 1, (b - 1) & 7);
+                    }
+                }
+                cs = cs + 1 == NBC ? 0 : cs + 1;
+            }
+            if (R > 1 && nblk > 0) {
+                __syncthreads();
+                if (active) wide_finish(nblk - 1, (nblk - 1) & 7);
             }
         }
         if (a.stats && active && rr == 0)
@@ -842,16 +994,12 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 }
             }
             if (active && rr == 0 && g == 0 && hasq) {
-                float kth = INFINITY;
+                // the unit's K smallest kept bounds (K distinct rows) join the query's list
+                const int base = atomicAdd(&a.ub_cnt[q], a.K);
+                float* dst = a.ub_list + (size_t)q * a.ub_cap;
 #pragma unroll
                 for (int i = 0; i < kUbList; ++i)
-                    if (i == a.K - 1) kth = ubl[i];
-                if (kth < INFINITY) {
-                    const double u = (double)kth;
-                    const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                    atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + q,
-                              (unsigned long long)key_of(tub));
-                }
+                    if (i < a.K && base + i < a.ub_cap) dst[base + i] = ubl[i];
             }
         } else {
             if (active) {
@@ -866,16 +1014,15 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                     L.init();
                     for (int r2 = 0; r2 < R; ++r2)
                         L.insert(key_of((double)s_ubl[wid + r2][jj * 64 + lane]), lane);
-                    uint64_t kk;
-                    int32_t ki;
-                    L.at(a.K - 1, kk, ki);
+                    // lane i holds the unit's i-th smallest kept bound: the first K join the
+                    // query's list
                     const int qq = __shfl(q, jj, kWave);
-                    if (lane == 0 && dist_of(kk) < (double)INFINITY) {
-                        const double u = dist_of(kk);
-                        const double tub = u * u / a.rot_sq_min * (1.0 + 1e-6);
-                        atomicMin(reinterpret_cast<unsigned long long*>(a.tau) + qq,
-                                  (unsigned long long)key_of(tub));
-                    }
+                    int base = 0;
+                    if (lane == 0) base = atomicAdd(&a.ub_cnt[qq], a.K);
+                    base = __shfl(base, 0, kWave);
+                    if (lane < a.K && base + lane < a.ub_cap)
+                        a.ub_list[(size_t)qq * a.ub_cap + base + lane] =
+                            L.k0 == kKeyInvalid ? INFINITY : (float)dist_of(L.k0);
                 }
             }
         }
@@ -922,6 +1069,33 @@ template __global__ void ub_scan_kernel<14, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<15, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<16, 16>(BatchArgs);
 
+// Seeding threshold, one wave per query: tau[q] = the K-th smallest bound u of its list
+// (each seeding unit's K smallest, all of distinct rows, so K rows have distance <= that u),
+// squared and mapped back through the rotation (u^2 / sigma_min^2, margin 1e-6 as the
+// reference's Stage X).  Fewer than K listed bounds leave tau = +inf.  A list longer than
+// ub_cap keeps its first ub_cap entries: the K-th smallest of a subset is still a bound.
+__global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
+    if (q >= a.B) return;
+    const int n = min(a.ub_cnt[q], a.ub_cap);
+    if (n < a.K) return;
+    const float* lst = a.ub_list + (size_t)q * a.ub_cap;
+    WaveList<64> L;
+    L.init();
+    for (int i0 = 0; i0 < n; i0 += kWave) {
+        const int i = i0 + lane;
+        L.insert(i < n ? key_of((double)lst[i]) : kKeyInvalid, i < n ? i : kIdInvalid);
+    }
+    uint64_t kk;
+    int32_t ki;
+    L.at(a.K - 1, kk, ki);
+    if (lane == 0 && kk != kKeyInvalid) {
+        const double u = dist_of(kk);
+        if (u < (double)INFINITY) a.tau[q] = u * u / a.rot_sq_min * (1.0 + 1e-6);
+    }
+}
+
 // ---------------------------------------------------------------------------------------------
 // Lower-bound pass.
 //
@@ -940,7 +1114,8 @@ template __global__ void ub_scan_kernel<16, 16>(BatchArgs);
 //            over the cluster): A - r^2 - 2 t_q r >= A - r (r + 2 t_w) + 2 (t_w - t_q) r_lo.
 //            G / c1 is exact (c1 is a power of two); mg covers the roundings of G and of the
 //            sums.  The group takes it iff every query has a threshold, all share c1 and
-//            |kq| <= 2^30 (with |acc| < 2^30 the int32 sum cannot overflow).
+//            |kq| <= 2^30 (pair_prep_kernel keeps |acc| < 2^30, so the int32 sum cannot
+//            overflow).
 __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, slot = tid & 15;
     const int gi = blockIdx.x * (kBlock / kGroupQ) + (tid >> 4);
@@ -964,7 +1139,7 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     double Kd = 0.0, mg = 0.0;
     float tqf = 0.0f;
     if (thr) {
-        const double G = 2.0 * err_q - Qp * (1.0 - 0x1p-15) + tq * tq;
+        const double G = 2.0 * err_q - Qp * (1.0 - a.sum_rel) + tq * tq;
         const double H = c1 * cW + G;
         const double X = pr.a_max + pr.r_max * pr.r_max + 2.0 * tq * pr.r_max + c1 * pr.acc_max +
                          fabs(H);
@@ -1013,9 +1188,13 @@ template <int KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 7 : 1)))
 void lb_scan_kernel(BatchArgs a) {
     constexpr int BV = block_vectors(KS);
-    __shared__ uint4 s_codes[2][KS * 4 * BV];
-    __shared__ __align__(16) float s_A[2][BV];
-    __shared__ __align__(16) float s_r[2][BV];
+    // code buffers, row scalars and replica partial sums as in ub_scan_kernel
+    constexpr int NBC = BV == 64 ? 2 : kWideAhead + 1;
+    __shared__ uint4 s_codes[NBC][KS * 4 * BV];
+    constexpr int NAB = BV == 64 ? 2 : 8, NP = BV == 64 ? 1 : 2;
+    __shared__ __align__(16) float s_A[NAB][BV];
+    __shared__ __align__(16) float s_r[NAB][BV];
+    __shared__ int4 s_part[NP][NP > 1 ? kWavesPerBlock : 1][NP > 1 ? kWave : 1];
     __shared__ __align__(16) int s_thr[2][kWavesPerBlock][BV];
     __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
     __shared__ int s_scnt[kWavesPerBlock][kWaveQ], s_sbase[kWavesPerBlock][kWaveQ],
@@ -1067,10 +1246,21 @@ void lb_scan_kernel(BatchArgs a) {
             const int pj = start + gq * kWaveQ + (hasq ? j : 0);
             q = a.pair_qid[pj];
             const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
+            if (BV == 64 || R == 1) {
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
-                blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
+                for (int ks = 0; ks < KS; ++ks) {
+                    bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
+                    blo[ks] = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
+                }
+            } else {
+                // wide layout with R replicas: slot i holds step rr + i R (zero past KS)
+#pragma unroll
+                for (int i = 0; i < KS; ++i) {
+                    const int ks = rr + i * R;
+                    bhi[i] = ks < KS ? *reinterpret_cast<const v4i*>(hp + ks * 64) : v4i{0, 0, 0, 0};
+                    blo[i] = ks < KS ? *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64)
+                                     : v4i{0, 0, 0, 0};
+                }
             }
             const LbRec L = a.lbr[pj];
             int_ok = __builtin_amdgcn_readfirstlane(L.int_ok) != 0;  // lane 0 has a query
@@ -1112,6 +1302,8 @@ void lb_scan_kernel(BatchArgs a) {
             if (lane < kWaveQ) s_scnt[wid][lane] = 0;
             if (a.stats) st_surv += (unsigned long long)nsq;
             nsq = 0;
+            // wide ring: the block waits count only the ring's loads, so the stores drain here
+            if constexpr (BV != 64) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         };
 
         // ---- rare: queue a tile's passes (rows row0 + r of this lane, r < 4).  The integer
@@ -1184,26 +1376,90 @@ void lb_scan_kernel(BatchArgs a) {
             queue(sm, li0 + 4 * g);
         };
 
+        // ---- wide layout (D_pad > 256), as in ub_scan_kernel: this wave's share of the
+        // 64-dim steps of the block's one tile; the replica with rr = 0 carries kq, so the
+        // partial sums add up to acc + kq ----
+        auto wide_partial = [&](int buf, int (&S)[4], auto r_c) {
+            constexpr int RC = decltype(r_c)::value, NS = (KS + RC - 1) / RC;
+            const uint4* blk = s_codes[buf];
+            v4i A[NS];
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                const int ks = RC == 1 ? i : min(rr + i * RC, KS - 1);
+                const uint4 v = blk[(ks * 4 + g) * BV + j];
+                A[i] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+            const int k0 = (RC == 1 || rr == 0) ? kq : 0;
+            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {k0, k0, k0, k0};
+#pragma unroll
+            for (int i = 0; i < NS; ++i) {
+                acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], bhi[i], acc_hi, 0, 0, 0);
+                acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], blo[i], acc_lo, 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7\n\ts_nop 7");
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
+        };
+        // the tests of the tile lambda's epilogue on whole sums: thresholds of block buffer
+        // tb, row scalars of buffer abuf
+        auto wide_judge = [&](const int (&S)[4], int tb, int abuf, int li0) {
+            uint64_t sm[4];
+            if (int_ok) {
+                const int4 th = *reinterpret_cast<const int4*>(&s_thr[tb][wid][4 * g]);
+                sm[0] = __ballot(S[0] >= th.x);
+                sm[1] = __ballot(S[1] >= th.y);
+                sm[2] = __ballot(S[2] >= th.z);
+                sm[3] = __ballot(S[3] >= th.w);
+            } else {
+                const float4 A4 = *reinterpret_cast<const float4*>(&s_A[abuf][4 * g]);
+                const float4 r4 = *reinterpret_cast<const float4*>(&s_r[abuf][4 * g]);
+                const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
+                const float4 c = s_qf[wid][j];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    sm[r] = __ballot(li0 + 4 * g + r < ve &&
+                                     fmaf(c.y, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
+                                         fmaf(c.x, (float)S[r], c.z));
+            }
+            if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
+            queue(sm, li0 + 4 * g);
+        };
+        auto wide_finish = [&](int b, int abuf) {
+            if (((b & (R - 1)) != rr)) return;
+            int S[4] = {0, 0, 0, 0};
+            for (int r2 = 0; r2 < R; ++r2) {
+                const int4 p = s_part[b & 1][gq * R + r2][lane];
+                S[0] += p.x;
+                S[1] += p.y;
+                S[2] += p.z;
+                S[3] += p.w;
+            }
+            wide_judge(S, b & 1, abuf, vb + b * BV);
+        };
+
         // ---- stream the slice through LDS in 64-vector blocks (as batch_scan_kernel) ----
         const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
         int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
-        auto gload = [&](int buf, int blk0) {
+        auto gload = [&](int buf, int abuf, int blk0) {
             if constexpr (BV == 64) {
-                const uint4* base = cells_c + ((size_t)ct * G16 + wid) * T + cw;
+                // block-major cells: the block's groups are consecutive runs of 64 cells
+                const uint4* base = cells_c + (size_t)ct * G16 * T + (size_t)cw * G16 + wid * BV;
 #pragma unroll
                 for (int jj = 0; jj < KS; ++jj)
                     if (wid + 4 * jj < G16)
-                        load_lds16(base + (size_t)(4 * jj) * T, 16u * lane,
+                        load_lds16(base + (size_t)(4 * jj) * BV, 16u * lane,
                                    &s_codes[buf][(wid + 4 * jj) * BV]);
                 if (wid == 0) {  // rows past the slice read the slice's last row (never used)
                     const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
-                    load_lds4(a.vec_Ar + v0, off, s_A[buf]);
-                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
+                    load_lds4(a.vec_Ar + v0, off, s_A[abuf]);
+                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[abuf]);
                 }
             } else {
-                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T, cw, T, G16, wid, lane,
-                                      s_codes[buf], a.vec_Ar + v0, blk0, ve - 1, s_A[buf],
-                                      s_r[buf]);
+                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T + (size_t)cw * G16, G16,
+                                      wid, lane, s_codes[buf], a.vec_Ar + v0, blk0, ve - 1,
+                                      s_A[abuf], s_r[abuf]);
             }
             cw += BV;
             if (cw == T) {
@@ -1212,37 +1468,73 @@ void lb_scan_kernel(BatchArgs a) {
             }
         };
         const int nblk = (ve - vb + BV - 1) / BV;
-        if (nblk > 0) gload(0, vb);
-        for (int b = 0; b < nblk; ++b) {
-            const int buf = b & 1;
-            // this wave's direct loads of block b have landed; the barrier covers everyone's
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-            if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
-            const int blk0 = vb + b * BV;
-            if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
-            if (active) {
-                if (int_ok) {
-                    if (BV == kWave || lane < BV) {
+        if constexpr (BV == 64) {
+            if (nblk > 0) gload(0, 0, vb);
+            for (int b = 0; b < nblk; ++b) {
+                const int buf = b & 1;
+                // this wave's direct loads of block b have landed; the barrier covers everyone's
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+                const int blk0 = vb + b * BV;
+                if (b + 1 < nblk) gload(buf ^ 1, buf ^ 1, blk0 + BV);
+                if (active) {
+                    if (int_ok) {
                         const float A = s_A[buf][lane], r = s_r[buf][lane];
                         s_thr[buf][wid][lane] =
                             blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
-                    }
-                    if (R == 1 && blk0 + BV <= ve) {  // the common case: straight-line tiles
+                        if (R == 1 && blk0 + BV <= ve) {  // the common case: straight-line tiles
 #pragma unroll
-                        for (int t = 0; t < BV / 16; ++t) tile(std::true_type{}, buf, t, blk0 + t * 16);
+                            for (int t = 0; t < BV / 16; ++t) tile(std::true_type{}, buf, t, blk0 + t * 16);
+                        } else {
+                            for (int t = rr; t < BV / 16; t += R) {
+                                if (blk0 + t * 16 >= ve) break;
+                                tile(std::true_type{}, buf, t, blk0 + t * 16);
+                            }
+                        }
                     } else {
                         for (int t = rr; t < BV / 16; t += R) {
                             if (blk0 + t * 16 >= ve) break;
-                            tile(std::true_type{}, buf, t, blk0 + t * 16);
+                            tile(std::false_type{}, buf, t, blk0 + t * 16);
                         }
                     }
-                } else {
-                    for (int t = rr; t < BV / 16; t += R) {
-                        if (blk0 + t * 16 >= ve) break;
-                        tile(std::false_type{}, buf, t, blk0 + t * 16);
+                }
+            }
+        } else {
+            // ring and replica finish as in ub_scan_kernel
+            const int nload = (KS - wid + 3) / 4 + (wid == 0 ? 2 : 0);
+            for (int p = 0; p < kWideAhead && p < nblk; ++p) gload(p, p, vb + p * BV);
+            int cs = 0;  // b % NBC
+            for (int b = 0; b < nblk; ++b) {
+                wait_vmcnt(min(kWideAhead - 1, nblk - 1 - b) * nload);
+                __syncthreads();
+                if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+                const int blk0 = vb + b * BV;
+                if (b + kWideAhead < nblk)
+                    gload(cs == 0 ? NBC - 1 : cs - 1, (b + kWideAhead) & 7,
+                          blk0 + kWideAhead * BV);
+                if (active) {
+                    if (int_ok && lane < BV) {
+                        const float A = s_A[b & 7][lane], r = s_r[b & 7][lane];
+                        s_thr[b & 1][wid][lane] =
+                            blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                    }
+                    int S[4];
+                    if (R == 1) {
+                        wide_partial(cs, S, std::integral_constant<int, 1>{});
+                        wide_judge(S, b & 1, b & 7, blk0);
+                    } else {
+                        if (R == 2) wide_partial(cs, S, std::integral_constant<int, 2>{});
+                        else wide_partial(cs, S, std::integral_constant<int, 4>{});
+                        s_part[b & 1][wid][lane] = make_int4(S[0], S[1], S[2], S[3]);
+                        if (b > 0) wide_finish(b - 1, (b - 1) & 7);
                     }
                 }
+                cs = cs + 1 == NBC ? 0 : cs + 1;
+            }
+            if (R > 1 && nblk > 0) {
+                __syncthreads();
+                if (active) wide_finish(nblk - 1, (nblk - 1) & 7);
             }
         }
         if (a.stats && active && rr == 0)

@@ -96,6 +96,9 @@ struct Workspace {
     LbRec* lbr;                      // [B * nprobe]
     double* cbound;                  // [nlist, kCbStride]
     double* qep;                     // [B]
+    float* ub_list;                  // [B, ub_cap] seeding bounds (batched route)
+    int32_t* ub_cnt;                 // [B]
+    int64_t ub_cap;
     float* qt32;                     // band front end: queries, matrix-core tile layout
     float* qn32;                     // [B] their squared norms
     float* cm32;                     // [nlist, Dq] centroid-major zero-padded centroids
@@ -151,6 +154,9 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.lbr = c.take<LbRec>(B * nprobe);
     w.cbound = c.take<double>(kCbStride * (int64_t)ix->nlist);
     w.qep = c.take<double>(B);
+    w.ub_cap = ub_cap_of(std::min<int64_t>(K, 64));
+    w.ub_list = c.take<float>(B * w.ub_cap);
+    w.ub_cnt = c.take<int32_t>(B);
     const int64_t Dq = band_dq(ix->D);
     w.qt32 = c.take<float>((B + 15) / 16 * 16 * Dq);
     w.qn32 = c.take<float>(B);
@@ -721,6 +727,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.stats = out->stats ? w.stat_slots : nullptr;
         b.rot_sq_min = ix->rot_sq_min;
         b.rot_sq_max = ix->rot_sq_max;
+        b.sum_rel = sum_rel_of(ix->D_pad);
         b.units = w.units;
         b.unit_off = w.unit_off;
         b.max_units = (int)w.max_units;
@@ -733,6 +740,9 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.lbr = w.lbr;
         b.cbound = w.cbound;
         b.qep = w.qep;
+        b.ub_list = w.ub_list;
+        b.ub_cnt = w.ub_cnt;
+        b.ub_cap = (int)w.ub_cap;
         b.nlist = ix->nlist;
         b.groups = w.groups;
         b.grp_off = w.grp_off;
@@ -753,6 +763,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
             b.unit_end = ix->nlist;
             b.ctr = w.unit_ctr;
             if ((rc = launch_batch<true>(b, st))) return rc;
+            ub_kth_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0, st>>>(b);
+            if ((rc = check_launch("ub_kth_kernel"))) return rc;
         }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
         // the lower-bound constants follow from tau (part of the seeding pass's merge stage);

@@ -91,7 +91,8 @@ struct LbRec {
 
 // Everything one cluster-batched scan launch reads (csrc/batch.hip).
 struct BatchArgs {
-    const uint4* cells;         // [tiles, D_pad / 16, T] 16-byte code cells, bytes c ^ 0x80
+    const uint4* cells;         // [tiles, T / V, D_pad / 16, V] 16-byte code cells (V-slot
+                                // blocks contiguous, V = block_vectors), bytes c ^ 0x80
     const int32_t* tile_oids;
     const int32_t* tile_off;
     const int32_t* vec_off;
@@ -124,7 +125,10 @@ struct BatchArgs {
     LbRec* lbr;                 // [M]
     const double* cbound;       // [nlist, kCbStride] (A_max, r_max, r_lo) per cluster
     const double* qep;          // [B] sum of qerr^2 per query
-    double* tau;                // [B] float64 thresholds (UB pass: atomicMin target)
+    double* tau;                // [B] float64 thresholds (set from the seeding lists)
+    float* ub_list;             // [B, ub_cap] seeding bounds: each seeding unit's K smallest
+    int32_t* ub_cnt;            // [B] entries appended to ub_list (may exceed ub_cap)
+    int ub_cap;
     float* tau_sq_out;          // [B] caller's float32 copy of the seeded tau, or null
     int xb_host;                // xb is mapped host memory (Stage Z reads cross PCIe)
     int B;
@@ -134,6 +138,7 @@ struct BatchArgs {
     int cap, K;
     unsigned long long* stats;  // [kStatSlots, 4] or null
     double rot_sq_min, rot_sq_max;
+    double sum_rel;             // relative error bound of the per-pair float32 sums (sum_rel_of)
 };
 
 constexpr int kStatSlots = 64;  // telemetry counters are spread over this many [4] slots
@@ -241,6 +246,12 @@ constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte 
 // Weight groups: the 16 consecutive pairs of a segment that one wave scans together share one
 // weight scale (pairs 16 k .. 16 k + 15 of the segment; units start on such boundaries).
 constexpr int kGroupQ = 16;
+// Relative error bound of the batched route's per-pair float32 sums over D_pad terms (Q = sum
+// (q - vmin)^2, sum |w|, |q|^2): n - 1 additions in any order, each rounding by <= 2^-24 of a
+// partial sum of non-negative terms, give (n - 1) 2^-24 (1 + n 2^-24); the rounded difference
+// q - vmin inside Q's terms adds 2^-23 (1 + 2^-24).  (D_pad + 4) 2^-24 covers both for
+// D_pad <= 1024.
+inline double sum_rel_of(int D_pad) { return (double)(D_pad + 4) * 0x1p-24; }
 constexpr int kCbStride = 4;  // doubles per cluster in the per-cluster bound table
 // Survivors a lower-bound wave queues in LDS before appending them to the candidate lists.
 constexpr int kSurvQ = 512;
@@ -271,6 +282,12 @@ __global__ void ub_scan_kernel(BatchArgs a);
 constexpr int kLbQ = 64;
 
 __global__ void lb_prep_kernel(BatchArgs a);
+
+__global__ void ub_kth_kernel(BatchArgs a);
+
+// Seeding-list slots per query: at most 3 seeding probes (trident_p_init_rule) x kMaxSplit
+// slices, K bounds each.
+inline int64_t ub_cap_of(int64_t K) { return 3 * kMaxSplit * K; }
 
 template <int KS>
 __global__ void lb_scan_kernel(BatchArgs a);

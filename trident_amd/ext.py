@@ -271,7 +271,7 @@ def launch_trident_v4_search(
     if sq8_cells is not None:
         _check_tensor("sq8_cells", sq8_cells, torch.int32, dev)
         _need(sq8_cells.numel() == tiles * (D_pad // 16) * int(tile_size) * 4,
-              "sq8_cells must hold [tiles, D_pad/16, tile_size, 4] words")
+              "sq8_cells must hold [tiles, tile_size/V, D_pad/16, V, 4] words")
     if cent_band is not None:
         Dq = band_dq(D)
         rows_t, tiles_t, norms_t, _ = cent_band

@@ -36,6 +36,12 @@ from . import ext as _ext
 _U53 = 2.0 ** -53
 
 
+def cell_block(D_pad: int) -> int:
+    """Slots per contiguous block of sq8_cells: the batched route's scan block (64 vectors up to
+    256 dims, 16 beyond)."""
+    return 64 if D_pad <= 256 else 16
+
+
 def choose_tile(dim: int) -> int:
     """Tile rule of benchmarks/phase4a_suite.py:61-62."""
     return 256 if dim >= 256 else 64
@@ -131,8 +137,10 @@ class TridentV4Index:
       sq8_packed   int32 [tiles, D_pad/4, T]: word [t, d4, s] packs dims 4*d4..4*d4+3 of slot
                    s of tile t, byte 0 = dim 4*d4 (reference packing :221-228); for T = 64 a
                    wave's 64 lanes read one contiguous 256-byte row per d4.
-      sq8_cells    int32 [tiles, D_pad/16, T, 4]: the same codes as 16-byte cells (16 dims of
-                   one slot), bytes XOR 0x80 -- the batched route's matrix-core operand layout.
+      sq8_cells    int32 [tiles, T/V, D_pad/16, V, 4], V = cell_block(D_pad) (64, or 16 past
+                   256 dims): the same codes as 16-byte cells (16 dims of one slot), bytes XOR
+                   0x80, every V-slot block contiguous -- the batched route's matrix-core operand
+                   layout (one scan block is one contiguous run).
       tile_orig_ids int32 [tiles, T] (-1 padded), tile_r_minmax f32 [tiles, 2]
       cluster_tile_off int32 [nlist + 1]; vmin / delta / eps_pad f32 [nlist or 1, D_pad]
       blk_bounds4  int32 [nb + 1] (32-dim blocks, or the variable scheme of :233-247)
@@ -275,14 +283,16 @@ class TridentV4Index:
             g = codes32[safe[ts:te]]                         # [nt, T, D4]
             g = torch.where(valid[ts:te].unsqueeze(-1), g, torch.zeros_like(g))
             self.sq8_packed[ts:te] = g.permute(0, 2, 1)
-        # Batched-route copy: 16-byte cells, cell (t, g, s) = dims 16 g .. 16 g + 15 of slot s
-        # (words 4 g .. 4 g + 3 of sq8_packed[t, :, s]), every byte c stored as c ^ 0x80.
-        G16 = D_pad // 16
-        self.sq8_cells = torch.empty((tiles, G16, T, 4), device=dev, dtype=torch.int32)
+        # Batched-route copy: 16-byte cells, cell (t, b, g, v) = dims 16 g .. 16 g + 15 of slot
+        # s = b V + v (words 4 g .. 4 g + 3 of sq8_packed[t, :, s]), every byte c stored as
+        # c ^ 0x80; the V slots of a scan block are one contiguous run.
+        G16, V = D_pad // 16, cell_block(D_pad)
+        self.sq8_cells = torch.empty((tiles, T // V, G16, V, 4), device=dev, dtype=torch.int32)
         flip = torch.tensor(-0x7f7f7f80, dtype=torch.int32, device=dev)  # 0x80808080
         for ts in range(0, tiles, tstep):
             te = min(tiles, ts + tstep)
-            self.sq8_cells[ts:te] = self.sq8_packed[ts:te].view(te - ts, G16, 4, T).permute(0, 1, 3, 2) ^ flip
+            self.sq8_cells[ts:te] = (self.sq8_packed[ts:te].view(te - ts, G16, 4, T // V, V)
+                                     .permute(0, 3, 1, 4, 2) ^ flip)
         self.tile_r_minmax =torch.zeros((tiles, 2), device=dev, dtype=torch.float32)
         if storage.r_vec_sorted is not None:
             r = storage.r_vec_sorted.to(dev)[safe]
