@@ -186,3 +186,27 @@ def test_batched_wide_exact_ties_and_replicas(dev):
             _, rd, ri = oracle_search(b, xq, nprobe, K)
             d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
             assert_exact(d, i, rd, ri, f"wide ties rep={rep} K={K} nprobe={nprobe}")
+
+
+def test_batched_wide_integer_range_guard(dev):
+    """D = 960, identity rotation: a cluster spanning [0, 1]^960 (the all-zeros and all-ones rows
+    included) and queries near 3 * ones make every weight of a pair equal and maximal, and the
+    all-ones row (every code 255) is the nearest neighbour.  Without the weight scale's L1
+    limit its int32 sum would be 127 * 960 * 32639 ~ 4e9 (wrapped, so the row's bounds would be
+    wrong); with it the answer is exact."""
+    rng = np.random.default_rng(45)
+    D = 960
+    c0 = rng.random((400, D), dtype=np.float32)
+    c0[0], c0[1] = 0.0, 1.0
+    c1 = (rng.random((400, D), dtype=np.float32) - 10.0)
+    xb = np.concatenate([c0, c1])
+    lid = np.repeat(np.arange(2, dtype=np.int32), 400)
+    cen = np.stack([c0.mean(0), c1.mean(0)]).astype(np.float32)
+    xq = (3.0 + 0.01 * rng.standard_normal((24, D))).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), 2, dev, list_ids=lid, centroids=cen, max_batch=32,
+                    use_pca=0)
+    for K, nprobe in ((10, 2), (1, 1), (64, 2)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        assert (ri[:, 0] == 1).all()  # the all-ones row
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"range guard K={K} nprobe={nprobe}")
