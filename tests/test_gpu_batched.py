@@ -32,7 +32,7 @@ def sets(dev):
 
 
 @pytest.mark.parametrize("name", ["hist", "norm96", "gmm", "d200"])
-@pytest.mark.parametrize("K", [1, 10, 64])
+@pytest.mark.parametrize("K", [1, 10, 64, 100, 128])
 def test_batched_route_exact(sets, dev, name, K):
     b, xq = sets[name]
     for nprobe in (4, 24):
@@ -118,11 +118,21 @@ def test_batched_many_units_per_workgroup(dev):
         assert_exact(d, i, rd, ri, f"many units rep={rep}")
 
 
-def test_batched_rejects_unsupported_k(sets, dev):
+def test_batched_rejects_k_above_128(sets, dev):
     from trident_amd._lib import TridentError
     b, xq = sets["hist"]
-    with pytest.raises(TridentError, match="batched route"):
-        run_search(b, _q(xq, dev), 8, 100, mode=2, route=2)
+    with pytest.raises(TridentError, match="outside"):
+        run_search(b, _q(xq, dev), 8, 129, mode=2, route=2)
+
+
+def test_batched_k100_matches_pair_route(sets, dev):
+    """K > 64: seeding units list their 64 smallest bounds, the threshold is the K-th over all
+    of a query's units; both routes return the same lists."""
+    b, xq = sets["hist"]
+    xqd = _q(xq, dev)
+    d1, i1 = run_search(b, xqd, 32, 100, mode=2, ub=1, route=1)
+    d2, i2 = run_search(b, xqd, 32, 100, mode=2, ub=1, route=2)
+    assert np.array_equal(i1, i2) and np.array_equal(d1, d2)
 
 
 @pytest.fixture(scope="module")
@@ -137,7 +147,7 @@ def wide_sets(dev):
 
 
 @pytest.mark.parametrize("name", ["d960", "d288"])
-@pytest.mark.parametrize("K", [1, 10, 64])
+@pytest.mark.parametrize("K", [1, 10, 64, 100])
 def test_batched_wide_route_exact(wide_sets, dev, name, K):
     b, xq = wide_sets[name]
     assert b.ix.D_pad > 256
@@ -151,6 +161,7 @@ def test_batched_wide_matches_pair_route_and_auto(wide_sets, dev):
     b, xq = wide_sets["d960"]
     xqd = _q(xq, dev)
     assert b.ix.route_for(len(xq), 16, 10) == 2  # AUTO takes the batched route at D = 960
+    assert b.ix.route_for(len(xq), 16, 100) == 1  # ... but not for K > 64 past 256 dims
     d1, i1 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=1)
     d2, i2 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=2)
     d0, i0 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=0)

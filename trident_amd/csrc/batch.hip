@@ -52,7 +52,7 @@ namespace trident {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kUbList = 16;  // per-lane upper-bound list (K <= 64)
+constexpr int kUbList = 16;  // per-lane upper-bound list
 constexpr int kBlkV = 64;    // slices start on multiples of 64 vectors (whole LDS blocks)
 constexpr int kWaveQ = 16;   // queries per wave
 
@@ -1017,10 +1017,11 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                     // lane i holds the unit's i-th smallest kept bound: the first K join the
                     // query's list
                     const int qq = __shfl(q, jj, kWave);
+                    const int nl = ub_per_unit(a.K);
                     int base = 0;
-                    if (lane == 0) base = atomicAdd(&a.ub_cnt[qq], a.K);
+                    if (lane == 0) base = atomicAdd(&a.ub_cnt[qq], nl);
                     base = __shfl(base, 0, kWave);
-                    if (lane < a.K && base + lane < a.ub_cap)
+                    if (lane < nl && base + lane < a.ub_cap)
                         a.ub_list[(size_t)qq * a.ub_cap + base + lane] =
                             L.k0 == kKeyInvalid ? INFINITY : (float)dist_of(L.k0);
                 }
@@ -1069,11 +1070,13 @@ template __global__ void ub_scan_kernel<14, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<15, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<16, 16>(BatchArgs);
 
-// Seeding threshold, one wave per query: tau[q] = the K-th smallest bound u of its list
-// (each seeding unit's K smallest, all of distinct rows, so K rows have distance <= that u),
+// Seeding threshold, one wave per query: tau[q] = the K-th smallest bound u of its list (each
+// seeding unit's min(K, 64) smallest, all of distinct rows, so K rows have distance <= that u;
+// KP >= K entries are kept while selecting),
 // squared and mapped back through the rotation (u^2 / sigma_min^2, margin 1e-6 as the
 // reference's Stage X).  Fewer than K listed bounds leave tau = +inf.  A list longer than
 // ub_cap keeps its first ub_cap entries: the K-th smallest of a subset is still a bound.
+template <int KP>
 __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
     const int lane = threadIdx.x & 63;
     const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
@@ -1081,7 +1084,7 @@ __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
     const int n = min(a.ub_cnt[q], a.ub_cap);
     if (n < a.K) return;
     const float* lst = a.ub_list + (size_t)q * a.ub_cap;
-    WaveList<64> L;
+    WaveList<KP> L;
     L.init();
     for (int i0 = 0; i0 < n; i0 += kWave) {
         const int i = i0 + lane;
@@ -1095,6 +1098,9 @@ __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
         if (u < (double)INFINITY) a.tau[q] = u * u / a.rot_sq_min * (1.0 + 1e-6);
     }
 }
+
+template __global__ void ub_kth_kernel<64>(BatchArgs);
+template __global__ void ub_kth_kernel<128>(BatchArgs);
 
 // ---------------------------------------------------------------------------------------------
 // Lower-bound pass.

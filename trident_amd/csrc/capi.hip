@@ -262,14 +262,15 @@ int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
     return launch_scan<KP, true, false>(a, st);
 }
 
-// Route of a mode-2 search.  The batched route needs the per-vector scalars, K <= 64 (its
-// upper-bound seeding keeps 16 bounds per lane, 64 per query), D_pad <= 1024 (query weights
+// Route of a mode-2 search.  The batched route needs the per-vector scalars, K <= 128 (a
+// seeding unit lists at most 64 bounds per query; the threshold is the K-th over all of a
+// query's units and the merge keeps 128), D_pad <= 1024 (query weights
 // held in registers: 8 VGPRs per 64 dims) and N < 2^27 (a queued survivor packs its index within the cluster
 // into 28 bits); AUTO takes it when clusters are shared by >= 8 queries on average, where
 // the contraction is dense enough for the matrix cores.
 int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                  int nprobe, int* route) {
-    const bool ok = ix->vec_Ar && ix->sq8_cells && ix->orig_ids_sorted && K <= 64 &&
+    const bool ok = ix->vec_Ar && ix->sq8_cells && ix->orig_ids_sorted && K <= 128 &&
                     ix->D_pad <= 1024 &&
                     ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
@@ -280,15 +281,20 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
         case TRIDENT_ROUTE_BATCHED:
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
-                            "batched route needs vec_Ar, sq8_cells, K <= 64, D_pad <= 1024 and "
+                            "batched route needs vec_Ar, sq8_cells, K <= 128, D_pad <= 1024 and "
                             "N < 2^27 "
                             "(K=%d, D_pad=%d, N=%d)",
                             K, ix->D_pad, ix->N);
             *route = TRIDENT_ROUTE_BATCHED;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_AUTO:
-            *route = (ok && (double)B * nprobe >= 8.0 * ix->nlist) ? TRIDENT_ROUTE_BATCHED
-                                                                 : TRIDENT_ROUTE_PAIR;
+            // K > 64 only up to 256 dims: at D = 960 (cfg 3) a K = 100 threshold lets ~1 % of
+            // candidates through, the longest candidate lists overflow and the merge's
+            // exhaustive rescans dominate (the per-pair route keeps register top-K lists)
+            *route = (ok && (double)B * nprobe >= 8.0 * ix->nlist &&
+                      (K <= 64 || ix->D_pad <= 256))
+                         ? TRIDENT_ROUTE_BATCHED
+                         : TRIDENT_ROUTE_PAIR;
             return TRIDENT_OK;
         default:
             return fail(TRIDENT_ERR_INVALID_ARGUMENT, "route=%d outside {0,1,2}", sp->route);
@@ -763,7 +769,11 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
             b.unit_end = ix->nlist;
             b.ctr = w.unit_ctr;
             if ((rc = launch_batch<true>(b, st))) return rc;
-            ub_kth_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0, st>>>(b);
+            const unsigned kg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
+            if (K <= 64)
+                ub_kth_kernel<64><<<kg, kBlock, 0, st>>>(b);
+            else
+                ub_kth_kernel<128><<<kg, kBlock, 0, st>>>(b);
             if ((rc = check_launch("ub_kth_kernel"))) return rc;
         }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;

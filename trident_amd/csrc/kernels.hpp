@@ -283,11 +283,15 @@ constexpr int kLbQ = 64;
 
 __global__ void lb_prep_kernel(BatchArgs a);
 
+template <int KP>
 __global__ void ub_kth_kernel(BatchArgs a);
 
+// Bounds a seeding unit lists per query: its K smallest, at most 64.
+__host__ __device__ constexpr int ub_per_unit(int K) { return K < 64 ? K : 64; }
+
 // Seeding-list slots per query: at most 3 seeding probes (trident_p_init_rule) x kMaxSplit
-// slices, K bounds each.
-inline int64_t ub_cap_of(int64_t K) { return 3 * kMaxSplit * K; }
+// slices, ub_per_unit(K) bounds each.
+inline int64_t ub_cap_of(int64_t K) { return 3 * kMaxSplit * (int64_t)ub_per_unit((int)K); }
 
 template <int KS>
 __global__ void lb_scan_kernel(BatchArgs a);
