@@ -76,9 +76,10 @@ def test_band_front_end_derived_centroids(gmm, dev):
         b.ix.cent_band = keep
 
 
-@pytest.mark.parametrize("nlist", [2048, 4096])
+@pytest.mark.parametrize("nlist", [2048, 4096, 5000])
 def test_band_front_end_wide_nlist(dev, nlist):
-    """The matrix-core band front end with 32 and 64 approximations per lane."""
+    """The matrix-core band front end with 32 and 64 approximations per lane, and past 4096
+    centroids with each lane streaming its share of the row (8 smallest in registers)."""
     xb, xq = datagen.cfg4(N=3 * nlist, D=96, B=96, n_centers=nlist, seed=43)
     b = build_index(xb, nlist, dev, max_batch=128, max_nprobe=128)
     for nprobe in (1, 64, 100, 128):

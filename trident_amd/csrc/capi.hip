@@ -410,7 +410,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
         w.xrot64, w.xrot32, w.qerr, rotate ? 1 : 0);
     int rc = check_launch("prep_queries_kernel");
     if (rc) return rc;
-    if (nprobe <= 128 && ix->nlist <= kBandMaxNlist) {  // band front end
+    if (nprobe <= 128) {  // band front end
         const int Dq = band_dq(ix->D);
         const float *cm = ix->cent_rows, *cmt = ix->cent_tiles, *cn = ix->cent_norms;
         const unsigned long long* cmax_dev = nullptr;
@@ -435,20 +435,22 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                                               a32);
         if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
         const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
-        const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= 2048 ? 32 : 64;
-#define TRIDENT_BAND_LAUNCH(KPV, VV)                                                             \
-    select_band_kernel<KPV, VV><<<grid, kBlock, 0, st>>>(                                       \
+        const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= 2048 ? 32 : ix->nlist <= kBandMaxNlist ? 64 : 0;
+#define TRIDENT_BAND_LAUNCH(KPV, VV, SS)                                                         \
+    select_band_kernel<KPV, VV, SS><<<grid, kBlock, 0, st>>>(                                   \
         a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, nprobe,          \
         w.probe_cids,                                                                           \
         w.probe_dqcs, nprobe, probe_cids, probe_dqcs, ld)
         if (nprobe <= 64) {
-            if (V == 16) TRIDENT_BAND_LAUNCH(64, 16);
-            else if (V == 32) TRIDENT_BAND_LAUNCH(64, 32);
-            else TRIDENT_BAND_LAUNCH(64, 64);
+            if (V == 16) TRIDENT_BAND_LAUNCH(64, 16, false);
+            else if (V == 32) TRIDENT_BAND_LAUNCH(64, 32, false);
+            else if (V == 64) TRIDENT_BAND_LAUNCH(64, 64, false);
+            else TRIDENT_BAND_LAUNCH(64, 8, true);
         } else {
-            if (V == 16) TRIDENT_BAND_LAUNCH(128, 16);
-            else if (V == 32) TRIDENT_BAND_LAUNCH(128, 32);
-            else TRIDENT_BAND_LAUNCH(128, 64);
+            if (V == 16) TRIDENT_BAND_LAUNCH(128, 16, false);
+            else if (V == 32) TRIDENT_BAND_LAUNCH(128, 32, false);
+            else if (V == 64) TRIDENT_BAND_LAUNCH(128, 64, false);
+            else TRIDENT_BAND_LAUNCH(128, 8, true);
         }
 #undef TRIDENT_BAND_LAUNCH
         return check_launch("select_band_kernel");

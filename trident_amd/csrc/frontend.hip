@@ -861,14 +861,15 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
     }
 }
 
-// One wave per query: V approximations per lane (nlist <= 64 V).  T comes from a bisection on
-// the approximations (count(a <= hi) >= nprobe is kept invariant), and every centroid of the
-// band a <= T + 2E gets its canonical float64 distance (t = q_d - c_d, acc = fma(t, t, acc) in
-// dimension order -- the oracle's chain).  A band of <= 128 (the usual case: a few more than
-// nprobe) is ranked by counting, each entry against all others in (d, cid) order; a wider one
-// streams through the (d, cid) register list 64 centroids at a time.  Outputs as
-// select_probes_wave_kernel.
-template <int KP, int V>
+// One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM, each lane's V
+// smallest of its nlist / 64 (any nlist >= 64 V).  T comes from a bisection on the register
+// values (count(a <= hi) >= nprobe is kept invariant: counted over a subset of the row, it
+// never exceeds the row's count), and every centroid of the band a <= T + 2E gets its
+// canonical float64 distance (t = q_d - c_d, acc = fma(t, t, acc) in dimension order -- the
+// oracle's chain).  A band of <= 128 (the usual case: a few more than nprobe) is ranked by
+// counting, each entry against all others in (d, cid) order; a wider one streams through the
+// (d, cid) register list 64 centroids at a time.  Outputs as select_probes_wave_kernel.
+template <int KP, int V, bool STREAM>
 __global__ __launch_bounds__(256) void select_band_kernel(
     const float* __restrict__ a32, const double* __restrict__ xq64, const float* __restrict__ cm32,
     const unsigned long long* __restrict__ cmax_dev, double cmax_host, int B, int nlist, int D,
@@ -881,11 +882,22 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     const int q = blockIdx.x * kWavesPerBlock + wid;
     if (q >= B) return;
     const double* qrow = xq64 + (size_t)q * D;
+    const float* arow = a32 + (size_t)q * nlist;
     float v[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) {
         const int c = i * kWave + lane;
-        v[i] = c < nlist ? a32[(size_t)q * nlist + c] : INFINITY;
+        v[i] = !STREAM && c < nlist ? arow[c] : INFINITY;
+    }
+    if constexpr (STREAM) {  // the lane's V smallest, ascending (selects: no NaN here)
+        for (int c = lane; c < nlist; c += kWave) {
+            const float x = arow[c];
+            if (x < v[V - 1]) {
+#pragma unroll
+                for (int i = V - 1; i > 0; --i) v[i] = x < v[i - 1] ? v[i - 1] : (x < v[i] ? x : v[i]);
+                v[0] = x < v[0] ? x : v[0];
+            }
+        }
     }
     // the error bound E (float64, then rounded up to float32)
     double nq = 0.0;
@@ -914,6 +926,14 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         t0 = fmaxf(t0, __shfl_xor(t0, o, kWave));
     }
     if (nprobe <= kWave && t0 < INFINITY) hi = t0;
+    // STREAM: every lane holds V values (nlist >= 64 V), so >= 64 V >= nprobe lie at or below
+    // the largest lane's V-th smallest
+    if (STREAM && lmax < INFINITY) {
+        float tv = v[V - 1];
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) tv = fmaxf(tv, __shfl_xor(tv, o, kWave));
+        if (kWave * V >= nprobe) hi = fminf(hi, tv);
+    }
     auto count_le = [&](float x) {
         int n = 0;
 #pragma unroll
@@ -985,17 +1005,33 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         }
         return acc;
     };
-    const int mband = thr < INFINITY ? count_le(thr) : nlist + 1;
+    // the band's size over the whole row (STREAM: the registers hold part of it)
+    auto count_row = [&](float x) {
+        int n = 0;
+        for (int c0 = 0; c0 < nlist; c0 += kWave)
+            n += __popcll(__ballot(c0 + lane < nlist && arow[c0 + lane] <= x));
+        return n;
+    };
+    const int mband = thr < INFINITY ? (STREAM ? count_row(thr) : count_le(thr)) : nlist + 1;
     if (mband <= 2 * kWave) {
         // the common case: the band fits two entries per lane.  Compact it, compute the exact
         // distances, and rank every entry by counting the entries before it in (d, cid) order.
         int nb = 0;
+        if constexpr (STREAM) {
+            for (int c0 = 0; c0 < nlist; c0 += kWave) {
+                const bool take = c0 + lane < nlist && arow[c0 + lane] <= thr;
+                const uint64_t mk = __ballot(take);
+                if (take) band[nb + mask_rank(mk)] = c0 + lane;
+                nb += __popcll(mk);
+            }
+        } else {
 #pragma unroll
-        for (int i = 0; i < V; ++i) {
-            const bool take = v[i] <= thr;  // thr is finite: centroids past nlist hold +inf
-            const uint64_t mk = __ballot(take);
-            if (take) band[nb + mask_rank(mk)] = i * kWave + lane;
-            nb += __popcll(mk);
+            for (int i = 0; i < V; ++i) {
+                const bool take = v[i] <= thr;  // thr is finite: centroids past nlist hold +inf
+                const uint64_t mk = __ballot(take);
+                if (take) band[nb + mask_rank(mk)] = i * kWave + lane;
+                nb += __popcll(mk);
+            }
         }
         wave_sync();
         const bool h0 = lane < nb, h1 = kWave + lane < nb;
@@ -1037,9 +1073,9 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         list_offer(L, nprobe, has ? key_of(dd) : kKeyInvalid, has ? c : kIdInvalid);
     };
     // the band, from the approximations again (L2; a rolled loop keeps one copy of refine)
-    const float* arow = a32 + (size_t)q * nlist;
+    const int nch = (nlist + kWave - 1) / kWave;
 #pragma unroll 1
-    for (int i = 0; i < V; ++i) {
+    for (int i = 0; i < nch; ++i) {
         const int c = i * kWave + lane;
         const bool take = c < nlist && arow[c] <= thr;
         const uint64_t mk = __ballot(take);
@@ -1067,16 +1103,18 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     }
 }
 
-#define TRIDENT_SELECT_BAND(KP, V)                                                              \
-    template __global__ void select_band_kernel<KP, V>(                                         \
+#define TRIDENT_SELECT_BAND(KP, V, S)                                                           \
+    template __global__ void select_band_kernel<KP, V, S>(                                      \
         const float*, const double*, const float*, const unsigned long long*, double, int, int,  \
         int, int, int, int32_t*, float*, int, int32_t*, float*, int);
-TRIDENT_SELECT_BAND(64, 16)
-TRIDENT_SELECT_BAND(64, 32)
-TRIDENT_SELECT_BAND(64, 64)
-TRIDENT_SELECT_BAND(128, 16)
-TRIDENT_SELECT_BAND(128, 32)
-TRIDENT_SELECT_BAND(128, 64)
+TRIDENT_SELECT_BAND(64, 16, false)
+TRIDENT_SELECT_BAND(64, 32, false)
+TRIDENT_SELECT_BAND(64, 64, false)
+TRIDENT_SELECT_BAND(128, 16, false)
+TRIDENT_SELECT_BAND(128, 32, false)
+TRIDENT_SELECT_BAND(128, 64, false)
+TRIDENT_SELECT_BAND(64, 8, true)
+TRIDENT_SELECT_BAND(128, 8, true)
 #undef TRIDENT_SELECT_BAND
 
 }  // namespace trident

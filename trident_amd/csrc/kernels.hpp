@@ -195,7 +195,7 @@ __global__ void coarse_gemm_kernel(const float* __restrict__ qt32, const float* 
                                    int B, const float* __restrict__ cmt32,
                                    const float* __restrict__ cn32, int nlist, int Dq,
                                    float* __restrict__ a32);
-template <int KP, int V>
+template <int KP, int V, bool STREAM>
 __global__ void select_band_kernel(const float* __restrict__ a32, const double* __restrict__ xq64,
                                    const float* __restrict__ cm32,
                                    const unsigned long long* __restrict__ cmax_dev,
@@ -205,7 +205,9 @@ __global__ void select_band_kernel(const float* __restrict__ a32, const double* 
                                    int32_t* __restrict__ out2_cids,
                                    float* __restrict__ out2_dqcs, int ld2);
 constexpr int kGemmTiles = 4;  // coarse_gemm_kernel: 16-centroid tiles per wave
-constexpr int kBandMaxNlist = 4096;  // band front end: nlist <= 64 x 64 approximations per lane
+// band front end: up to 64 x 64 approximations per lane in registers; past that each lane
+// streams its share of the row and keeps its 8 smallest
+constexpr int kBandMaxNlist = 4096;
 inline int band_dq(int D) { return (D + 15) & ~15; }
 
 constexpr int kCoarseQW = 4;       // queries per wave of coarse_dist_kernel
