@@ -280,6 +280,15 @@ def main():
                     "survivors_frac": round(surv / max(tot, 1), 5), "refined_inserted": ins},
         "bytes_alg_total": bytes_all,
     }
+    if args.xb_host:
+        # Stage Z reads every survivor's FP32 row from mapped host memory once (128-byte
+        # segments); a query whose candidate list overflowed would add an exhaustive rescan of
+        # its probed rows, which this count leaves out
+        pcie = surv * D * 4
+        line["out_of_core"] = {"stage_z_rows": surv, "row_bytes": D * 4, "pcie_bytes": pcie,
+                               "pcie_bytes_per_query": round(pcie / B, 1),
+                               "stage_z_ms": round(stage["pass2_merge_ms"], 4),
+                               "pcie_GBps": round(pcie / max(stage["pass2_merge_ms"], 1e-9) / 1e6, 1)}
     if sweep:
         line["sweep"] = sweep
     if w0 is not None:
