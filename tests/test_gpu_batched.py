@@ -161,7 +161,7 @@ def test_batched_wide_matches_pair_route_and_auto(wide_sets, dev):
     b, xq = wide_sets["d960"]
     xqd = _q(xq, dev)
     assert b.ix.route_for(len(xq), 16, 10) == 2  # AUTO takes the batched route at D = 960
-    assert b.ix.route_for(len(xq), 16, 100) == 1  # ... but not for K > 64 past 256 dims
+    assert b.ix.route_for(len(xq), 16, 100) == 2  # ... for every K <= 128
     d1, i1 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=1)
     d2, i2 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=2)
     d0, i0 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=0)

@@ -114,14 +114,19 @@ inline int64_t plane_bytes(int D_pad) { return 64 * (int64_t)((D_pad + 63) / 64)
 // Candidate-list slots per query.  The batched route stores every lower-bound survivor there
 // (before its exact test), so lists are at least 64 * nprobe deep (12 bytes a slot; only used
 // slots are touched): a longer list makes the merge rescan that query's probes exhaustively,
-// which with the base in host memory crosses PCIe for every probed row.
-inline int64_t cand_cap(int64_t nprobe, int64_t K) { return nprobe * std::max<int64_t>(K, 64); }
+// which with the base in host memory crosses PCIe for every probed row.  Past 64 neighbours in
+// more than 256 dims the K-th distance sits in the bulk of the distance distribution (cfg 3,
+// K = 100: ~1 % of candidates pass, ~2,300 per query with a long tail), so those lists are 8x
+// deeper.
+inline int64_t cand_cap(int64_t nprobe, int64_t K, int64_t D_pad) {
+    return nprobe * std::max<int64_t>(K, 64) * (K > 64 && D_pad > 256 ? 8 : 1);
+}
 
 Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
     Carver c{static_cast<char*>(base)};
     Workspace w;
     const int64_t KP = K <= 64 ? 64 : 128;
-    const int64_t cap = cand_cap(nprobe, K);
+    const int64_t cap = cand_cap(nprobe, K, ix->D_pad);
     w.xq64 = c.take<double>(B * ix->D);
     w.xrot64 = c.take<double>(B * ix->D_pad);
     w.xrot32 = c.take<float>(B * ix->D_pad);
@@ -288,13 +293,8 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
             *route = TRIDENT_ROUTE_BATCHED;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_AUTO:
-            // K > 64 only up to 256 dims: at D = 960 (cfg 3) a K = 100 threshold lets ~1 % of
-            // candidates through, the longest candidate lists overflow and the merge's
-            // exhaustive rescans dominate (the per-pair route keeps register top-K lists)
-            *route = (ok && (double)B * nprobe >= 8.0 * ix->nlist &&
-                      (K <= 64 || ix->D_pad <= 256))
-                         ? TRIDENT_ROUTE_BATCHED
-                         : TRIDENT_ROUTE_PAIR;
+            *route = (ok && (double)B * nprobe >= 8.0 * ix->nlist) ? TRIDENT_ROUTE_BATCHED
+                                                                 : TRIDENT_ROUTE_PAIR;
             return TRIDENT_OK;
         default:
             return fail(TRIDENT_ERR_INVALID_ARGUMENT, "route=%d outside {0,1,2}", sp->route);
@@ -678,7 +678,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
     const int KP = K <= 64 ? 64 : 128;
-    const int64_t cap = cand_cap(nprobe, K);
+    const int64_t cap = cand_cap(nprobe, K, ix->D_pad);
     if (out->stats) {
         if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
         if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
