@@ -890,12 +890,23 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         v[i] = !STREAM && c < nlist ? arow[c] : INFINITY;
     }
     if constexpr (STREAM) {  // the lane's V smallest, ascending (selects: no NaN here)
-        for (int c = lane; c < nlist; c += kWave) {
-            const float x = arow[c];
-            if (x < v[V - 1]) {
+        // eight of the lane's values per round, all loaded before the first insertion
+        for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
+            float xs[8];
 #pragma unroll
-                for (int i = V - 1; i > 0; --i) v[i] = x < v[i - 1] ? v[i - 1] : (x < v[i] ? x : v[i]);
-                v[0] = x < v[0] ? x : v[0];
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * kWave + lane;
+                xs[u] = c < nlist ? arow[c] : INFINITY;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const float x = xs[u];
+                if (x < v[V - 1]) {
+#pragma unroll
+                    for (int i = V - 1; i > 0; --i)
+                        v[i] = x < v[i - 1] ? v[i - 1] : (x < v[i] ? x : v[i]);
+                    v[0] = x < v[0] ? x : v[0];
+                }
             }
         }
     }
@@ -1005,25 +1016,38 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         }
         return acc;
     };
-    // the band's size over the whole row (STREAM: the registers hold part of it)
-    auto count_row = [&](float x) {
-        int n = 0;
-        for (int c0 = 0; c0 < nlist; c0 += kWave)
-            n += __popcll(__ballot(c0 + lane < nlist && arow[c0 + lane] <= x));
-        return n;
-    };
-    const int mband = thr < INFINITY ? (STREAM ? count_row(thr) : count_le(thr)) : nlist + 1;
+    // STREAM: the band is compacted from the row in one pass (eight values per lane loaded
+    // per round), counting past the 128 slots without writing; the registers hold part of it
+    int mband = nlist + 1, nb_stream = 0;
+    if (thr < INFINITY) {
+        if constexpr (STREAM) {
+            for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
+                float xs[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int c = c0 + u * kWave + lane;
+                    xs[u] = c < nlist ? arow[c] : INFINITY;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const bool take = xs[u] <= thr;  // +inf past nlist never passes
+                    const uint64_t mk = __ballot(take);
+                    const int at = nb_stream + mask_rank(mk);
+                    if (take && at < 2 * kWave) band[at] = c0 + u * kWave + lane;
+                    nb_stream += __popcll(mk);
+                }
+            }
+            mband = nb_stream;
+        } else {
+            mband = count_le(thr);
+        }
+    }
     if (mband <= 2 * kWave) {
         // the common case: the band fits two entries per lane.  Compact it, compute the exact
         // distances, and rank every entry by counting the entries before it in (d, cid) order.
         int nb = 0;
         if constexpr (STREAM) {
-            for (int c0 = 0; c0 < nlist; c0 += kWave) {
-                const bool take = c0 + lane < nlist && arow[c0 + lane] <= thr;
-                const uint64_t mk = __ballot(take);
-                if (take) band[nb + mask_rank(mk)] = c0 + lane;
-                nb += __popcll(mk);
-            }
+            nb = nb_stream;  // compacted above
         } else {
 #pragma unroll
             for (int i = 0; i < V; ++i) {
