@@ -59,8 +59,7 @@ constexpr int kWaveQ = 16;   // queries per wave
 // Vector slices of a cluster (both passes), so that no unit runs far longer than the others.
 // The seeding pass loses nothing by slicing: every unit hands its K smallest bounds to the
 // query's list, and the threshold is the K-th smallest over all of them.
-__device__ __forceinline__ int splits_of(int n, int p) {
-    (void)p;
+__device__ __forceinline__ int splits_of(int n) {
     if (n <= 0) return 0;
     return min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec);
 }
@@ -71,7 +70,7 @@ __device__ __forceinline__ int units_of_entry(const int32_t* seg_off, const int3
     const int32_t* so = seg_off + p * (nlist + 1);
     const int q = so[c + 1] - so[c];
     const int uq = p ? kUnitQ : kUnitQ0;
-    return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c], p) : 0;
+    return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c]) : 0;
 }
 
 __device__ __forceinline__ int groups_of_entry(const int32_t* seg_off, int nlist, int e) {
@@ -169,7 +168,7 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
         const int p = lo >= nlist ? 1 : 0, c = lo - p * nlist;
         const int32_t* so = seg_off + p * (nlist + 1);
         const int n = vec_off[c + 1] - vec_off[c];
-        const int S = splits_of(n, p);
+        const int S = splits_of(n);
         const int local = u - unit_off[lo];
         const int q = so[c + 1] - so[c];
         const int uq = p ? kUnitQ : kUnitQ0;
