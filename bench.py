@@ -97,7 +97,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build's path runs on a "
-              "single MI355X; sharding across GPUs is design-only (see DESIGN.md).", file=sys.stderr)
+              "single MI355X; sharding across GPUs is a design, not part of this build.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
@@ -280,6 +280,18 @@ def main():
                     "survivors_frac": round(surv / max(tot, 1), 5), "refined_inserted": ins},
         "bytes_alg_total": bytes_all,
     }
+    # the metric's HBM view of the same launch: algorithmic code bytes (every probed vector at
+    # full depth, no pruning credit; above 1.0 only through on-chip reuse) and the
+    # physical traffic the committed rocprofv3 summary measured for this workload
+    t_l = roof["launch_ms"] * 1e-3
+    alg = bytes_all if mode == 2 else bytes_p2
+    hv = {"bytes_alg_per_launch": alg, "alg_GBps": round(alg / t_l / 1e9, 1),
+          "alg_frac_of_peak": round(alg / t_l / 1e9 / HBM_PEAK_GBPS, 3)}
+    if roof.get("traffic"):
+        hv.update({"physical_bytes_per_launch": roof["traffic"],
+                   "physical_GBps": round(roof["traffic"] / t_l / 1e9, 1),
+                   "physical_frac_of_peak": round(roof["traffic"] / t_l / 1e9 / HBM_PEAK_GBPS, 3)})
+    line["hbm_view"] = hv
     if args.xb_host:
         # Stage Z reads every survivor's FP32 row from mapped host memory once (128-byte
         # segments); a query whose candidate list overflowed would add an exhaustive rescan of
