@@ -221,3 +221,24 @@ def test_batched_wide_integer_range_guard(dev):
         assert (ri[:, 0] == 1).all()  # the all-ones row
         d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
         assert_exact(d, i, rd, ri, f"range guard K={K} nprobe={nprobe}")
+
+
+@pytest.mark.parametrize("D", [64, 320])
+def test_batched_short_and_empty_lists(dev, D):
+    """Probed lists with fewer than K vectors in total (the missing slots must be (+inf, -1)
+    as in the oracle) and probed lists that are empty (centroids nobody was assigned to), on
+    the narrow and the wide layout."""
+    rng = np.random.default_rng(46 + D)
+    nlist = 24
+    cen = (rng.standard_normal((nlist, D)) * 10.0).astype(np.float32)
+    used = np.arange(0, nlist, 3)                       # lists 1, 2, 4, 5, ... stay empty
+    lid = rng.choice(used, size=180).astype(np.int32)   # ~22 vectors per used list
+    xb = (cen[lid] + rng.standard_normal((180, D)).astype(np.float32)).astype(np.float32)
+    xq = (cen[rng.integers(0, nlist, 40)] + rng.standard_normal((40, D))).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=64)
+    assert (np.diff(b.vec_off) == 0).sum() > 0
+    for K, nprobe in ((64, 2), (100, 3), (10, 5), (128, 12)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
+        assert_exact(d, i, rd, ri, f"short/empty D={D} K={K} nprobe={nprobe}")
+        assert (ri == -1).any()  # some query really has fewer than K candidates
