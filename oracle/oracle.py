@@ -153,17 +153,30 @@ def np_ivf_exact(xq, xb, list_ids, probe_cids, K):
 
 
 def audit(pred_ids, ref_ids, xb, xq):
-    """Classify every differing slot: exact tie, f32 rounding (<= 1e-5 rel) or true miss."""
-    res = dict(diff_slots=0, exact_tie=0, f32_rounding=0, true_miss=0, max_rel=0.0)
-    for q in range(len(ref_ids)):
+    """Float64 audit of a predicted id list against the reference list (restates
+    audit_predictions, benchmarks/phase3a_lossless_audit.py:76-129, for any K).
+
+    Per query, the ids in only one of the two lists are paired in order of their float64
+    distance and each pair is classified as an exact tie (|dp - dr| <= 1e-12 max(1, dr)), an
+    FP32 rounding difference (relative <= 1e-5) or a true miss; ids that cannot be paired (a
+    list shorter than the other, -1 slots) count as true misses.  ``xb`` is indexed by id."""
+    Q = len(ref_ids)
+    K = int(np.asarray(ref_ids).shape[1]) if Q else 0
+    res = dict(diff_slots=0, exact_tie=0, f32_rounding=0, true_miss=0, max_rel=0.0,
+               total_slots=Q * K, strict_id_hits=0, queries_strict=0, queries_no_miss=0)
+    for q in range(Q):
         sp = set(int(i) for i in pred_ids[q] if i >= 0)
         sr = set(int(i) for i in ref_ids[q] if i >= 0)
+        res["strict_id_hits"] += len(sp & sr)
         if sp == sr:
+            res["queries_strict"] += 1
+            res["queries_no_miss"] += 1
             continue
         qv = xq[q].astype(np.float64)
         dist = lambda i: float(((xb[i].astype(np.float64) - qv) ** 2).sum())
         miss = sorted(sr - sp, key=dist)
         extra = sorted(sp - sr, key=dist)
+        q_miss = abs(len(miss) - len(extra))
         for r, p in zip(miss, extra):
             dr, dp = dist(r), dist(p)
             rel = abs(dp - dr) / max(dr, 1e-12)
@@ -174,6 +187,10 @@ def audit(pred_ids, ref_ids, xb, xq):
             elif rel <= 1e-5:
                 res["f32_rounding"] += 1
             else:
-                res["true_miss"] += 1
-        res["true_miss"] += abs(len(miss) - len(extra))
+                q_miss += 1
+        res["true_miss"] += q_miss
+        res["queries_no_miss"] += q_miss == 0
+    slots = max(res["total_slots"], 1)
+    res["strict_id_overlap_pct"] = 100.0 * res["strict_id_hits"] / slots
+    res["lossless_no_miss_pct"] = 100.0 * res["queries_no_miss"] / max(Q, 1)
     return res

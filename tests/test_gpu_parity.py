@@ -185,17 +185,24 @@ def test_ties_duplicates_and_short_lists(dev):
             assert_exact(d, i, rd, ri, f"ties K={K} nprobe={nprobe} mode={mode} ub={ub}")
 
 
-def test_stats_counters(hist, dev):
+@pytest.mark.parametrize("route", [1, 2])
+def test_stats_counters(hist, dev, route):
+    """candidates = sum over the probed pairs of the list sizes, each pair counted once on both
+    routes (the batched route's seeding pass does not count: its lower-bound pass rescans
+    every probe); survivors and insertions are bounded by it."""
     b, xq = hist
     nprobe = 24
     st = torch.zeros(4, dtype=torch.int64, device=dev)
-    run_search(b, _q(xq, dev), nprobe, 10, mode=2, stats=st)
+    run_search(b, _q(xq, dev), nprobe, 10, mode=2, ub=1, stats=st, route=route)
     tot, dims, surv, ins = st.tolist()
     cids, _ = O.coarse_probe(xq, b.centroids_idx, nprobe)
     sizes = np.diff(b.vec_off)
     assert tot == int(sizes[cids].sum())
-    assert 0 < surv <= tot and ins <= surv
-    assert tot * 32 <= dims <= tot * b.ix.D_pad
+    assert 0 < surv <= tot and 0 < ins <= surv
+    if route == 2:
+        assert dims == tot * b.ix.D_pad   # the matrix-core bound always reads every dimension
+    else:
+        assert tot * 32 <= dims <= tot * b.ix.D_pad
 
 
 def test_sq8_bounds_bracket_exact_distance(aniso, hist, dev):

@@ -137,6 +137,27 @@ def test_fp32_baseline_matches_on_integer_and_audits_on_float():
     np.testing.assert_allclose(d32, d64, rtol=1e-5)
 
 
+def test_audit_known_answers():
+    """oracle.audit on hand-built lists (reference audit_predictions,
+    benchmarks/phase3a_lossless_audit.py:76-129): one exact tie, one FP32-rounding pair and one
+    true miss on query 0, an identical list on query 1, and two unfilled (-1) slots on query 2."""
+    xb = np.array([[1, 0], [0, 1], [2, 0], [2.000002, 0], [3, 0], [4, 0]], np.float32)
+    xq = np.zeros((3, 2), np.float32)
+    ref = np.array([[0, 2, 4], [0, 2, 4], [0, 2, 4]])
+    pred = np.array([[1, 3, 5], [4, 0, 2], [0, -1, -1]])
+    a = O.audit(pred, ref, xb, xq)
+    d3 = float(xb[3, 0]) ** 2
+    assert 1e-12 < (d3 - 4.0) / 4.0 <= 1e-5
+    assert (a["diff_slots"], a["exact_tie"], a["f32_rounding"], a["true_miss"]) == (3, 1, 1, 3)
+    assert (a["queries_strict"], a["queries_no_miss"], a["strict_id_hits"], a["total_slots"]) == (1, 1, 4, 9)
+    assert a["max_rel"] == pytest.approx(7.0 / 9.0, rel=1e-12)
+    assert a["strict_id_overlap_pct"] == pytest.approx(400.0 / 9.0)
+    assert a["lossless_no_miss_pct"] == pytest.approx(100.0 / 3.0)
+    # the same lists in the other role: the classification is symmetric in the paired ids
+    b = O.audit(ref[:1], pred[:1], xb, xq[:1])
+    assert (b["exact_tie"], b["f32_rounding"], b["true_miss"]) == (1, 1, 1)
+
+
 # ---- planted mistakes: each mutated oracle must fail the checks above ----
 
 def _mut_no_tiebreak(xq, xb, lid, probes, K):

@@ -308,9 +308,10 @@ __device__ __forceinline__ double sum16_f64(double v) {
 }
 
 // Waves [0, nlist): per-cluster bounds of the f32 slack, A_max = 255^2 sum delta^2 (>= A_x,
-// codes <= 255) and r_max = 2 sqrt(sum eps^2) (>= r_x = |a| + |b| <= 2 |a + b| for the
-// non-negative per-dim error terms bounded by eps), and r_lo = the smallest stored r_x of the
-// cluster.  Waves [nlist, nlist + B): per-query sum of qerr^2 (the rotation error of q_rot,
+// codes <= 255) and r_max = max(2 sqrt(sum eps^2), the largest stored r_x) (the first term
+// bounds r_x = |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms when eps bounds
+// them; the second holds for any eps, e.g. an index built with the reference's 0.5001 delta),
+// and r_lo = the smallest stored r_x of the cluster.  Waves [nlist, nlist + B): per-query sum of qerr^2 (the rotation error of q_rot,
 // squared).
 __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist, int B,
                                                          double* cbound, double* qep,
@@ -332,7 +333,7 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
         }
         dd = wave_sum_f64(dd);
         ee = wave_sum_f64(ee);
-        float rlo = INFINITY;
+        float rlo = INFINITY, rhi = 0.0f;
         const int vend = a.vec_off[wv + 1];
         for (int v = a.vec_off[wv] + lane; v < vend; v += 4 * kWave) {  // 4 loads in flight
             float r4[4];
@@ -340,12 +341,18 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
             for (int u = 0; u < 4; ++u)
                 r4[u] = v + u * kWave < vend ? a.vec_Ar[v + u * kWave].y : INFINITY;
             rlo = fminf(rlo, fminf(fminf(r4[0], r4[1]), fminf(r4[2], r4[3])));
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (v + u * kWave < vend) rhi = fmaxf(rhi, r4[u]);
         }
 #pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) rlo = fminf(rlo, __shfl_xor(rlo, o, kWave));
+        for (int o = 1; o < kWave; o <<= 1) {
+            rlo = fminf(rlo, __shfl_xor(rlo, o, kWave));
+            rhi = fmaxf(rhi, __shfl_xor(rhi, o, kWave));
+        }
         if (lane == 0) {
             cbound[kCbStride * wv] = 65025.0 * dd * (1.0 + 1e-12);
-            cbound[kCbStride * wv + 1] = 2.0 * sqrt(ee) * (1.0 + 1e-12);
+            cbound[kCbStride * wv + 1] = fmax(2.0 * sqrt(ee), (double)rhi) * (1.0 + 1e-12);
             cbound[kCbStride * wv + 2] = rlo < INFINITY ? (double)rlo : 0.0;
         }
     } else if (wv < nlist + B) {
@@ -714,7 +721,6 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
     const int rb = xcd * nx, re = min(total, rb + nx);
     int32_t* ctr = a.ctr + xcd * kCtrStride;
     const int T = a.T, G16 = a.D_pad >> 4;
-    unsigned long long st_cand = 0;
 
     // next unit index: as in lb_scan_kernel
     if (tid == 0) s_unit[0] = atomicAdd(ctr, 1);
@@ -965,8 +971,6 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 if (active) wide_finish(nblk - 1, (nblk - 1) & 7);
             }
         }
-        if (a.stats && active && rr == 0)
-            st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
 
         // ---- K-th smallest upper bound per query -> atomicMin into tau[q] ----
         //  K <= 16: the four lane groups' lists are merged in registers (exact top 16 of the
@@ -1028,12 +1032,7 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
         }
         if (tid == 0) s_unit[(it + 1) & 1] = nblk > 0 ? nxt : atomicAdd(ctr, 1);
     }
-
-    if (a.stats && lane == 0) {
-        const int slot = (int)(blockIdx.x % kStatSlots) * 4;
-        atomicAdd(&a.stats[slot + 0], st_cand);
-        atomicAdd(&a.stats[slot + 1], st_cand * (unsigned long long)(a.D_pad));
-    }
+    // telemetry is counted by the lower-bound pass alone, which scans every probed pair once
 }
 
 template __global__ void ub_scan_kernel<1, 4>(BatchArgs);

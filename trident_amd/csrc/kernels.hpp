@@ -237,8 +237,10 @@ template <int KP>
 __global__ void merge_kernel(MergeArgs a);
 
 // Batched-route work units: <= 64 queries of one cluster x one slice of ~kSplitVec vectors
-// (at most kMaxSplit slices per cluster); units of the seeding pass hold <= 16 queries and a
-// whole cluster.  A launch has <= kMaxSplit * (pairs / 64 + 2 nlist) units.
+// (at most kMaxSplit slices per cluster); units of the seeding pass hold <= 16 queries.  Pass p
+// with M_p pairs has at most kMaxSplit * sum_c ceil(q_c / uq_p) <= kMaxSplit * (M_p / uq_p +
+// nlist) units, so both passes together stay within kMaxSplit * (ceil(M / 16) + 2 nlist) for
+// M = M_1 + M_2 pairs, whatever the split (max_units_of).
 constexpr int kUnitQ = 64;
 constexpr int kUnitQ0 = 16;
 constexpr int kSplitVec = 1024;
@@ -258,8 +260,11 @@ constexpr int kCbStride = 4;  // doubles per cluster in the per-cluster bound ta
 // Survivors a lower-bound wave queues in LDS before appending them to the candidate lists.
 constexpr int kSurvQ = 512;
 
+// Units of both passes for `pairs` (query, probe) pairs: bounded with the seeding pass's
+// smaller units (16 queries) for every pair, since the split between the passes (p_init) is a
+// search parameter that the workspace size does not know.
 inline int64_t max_units_of(int64_t pairs, int64_t nlist) {
-    return (int64_t)kMaxSplit * ((pairs + kUnitQ - 1) / kUnitQ + 2 * nlist);
+    return (int64_t)kMaxSplit * ((pairs + kUnitQ0 - 1) / kUnitQ0 + 2 * nlist);
 }
 
 inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {

@@ -84,21 +84,52 @@ def rotation_sq_bounds(W_combined: torch.Tensor, nlist: int, D: int):
     return hit
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Grow-only scratch buffer per device, reused across calls (the library itself never
-    allocates)."""
+class _Workspace:
+    """One grow-only scratch buffer for the searches enqueued on one (device, stream).
+
+    The buffer is allocated while its stream is current, so the caching allocator orders its
+    reuse after the work queued on that stream when it is replaced by a larger one; ``lock`` is
+    held from taking the buffer until the search is enqueued, so two host threads that share a
+    stream cannot interleave their launches over the same scratch memory."""
+
+    __slots__ = ("buf", "lock")
+
+    def __init__(self):
+        self.buf = None
+        self.lock = threading.Lock()
+
+
+def _workspace_slot(device: torch.device, stream) -> _Workspace:
+    key = (device, int(stream.cuda_stream))
     with _ws_lock:
-        buf = _ws_cache.get(device)
-        if buf is None or buf.numel() < nbytes:
-            buf = None
-            _ws_cache.pop(device, None)
-            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-            _ws_cache[device] = buf
-        return buf
+        slot = _ws_cache.get(key)
+        if slot is None:
+            slot = _ws_cache[key] = _Workspace()
+        return slot
+
+
+def workspace(device: torch.device, nbytes: int, stream=None) -> torch.Tensor:
+    """Grow-only scratch buffer of at least ``nbytes`` for searches on ``stream`` (default:
+    the device's current stream); the library itself never allocates.  The caller must hold
+    the slot's lock while the buffer is in use from the host (``search_view`` does)."""
+    st = stream if stream is not None else torch.cuda.current_stream(device)
+    slot = _workspace_slot(device, st)
+    return _grow(slot, device, nbytes, st)
+
+
+def _grow(slot: _Workspace, device, nbytes: int, st) -> torch.Tensor:
+    if slot.buf is None or slot.buf.numel() < nbytes:
+        slot.buf = None
+        with torch.cuda.stream(st):
+            slot.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    return slot.buf
 
 
 def release_workspaces() -> None:
     with _ws_lock:
+        for slot in _ws_cache.values():
+            with slot.lock:
+                slot.buf = None
         _ws_cache.clear()
 
 
@@ -118,7 +149,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.rot_sq_min, v.rot_sq_max = float(rot_sq_min), float(rot_sq_max)
     v.sq8_packed = _ptr(sq8_packed)
     v.tile_orig_ids = _ptr(tile_orig_ids)
-    v.tile_r_minmax = _ptr(tile_r_minmax) if tile_r_minmax is not None and tile_r_minmax.numel() >= 2 * v.total_tiles else None
+    v.tile_r_minmax = _ptr(tile_r_minmax) if tile_r_minmax is not None and tile_r_minmax.numel() > 0 else None
     v.cluster_tile_off = _ptr(cluster_tile_off)
     v.cluster_vec_off = _ptr(cluster_vec_off)
     v.xb_sorted = device_pointer(xb_sorted) if xb_sorted is not None else None
@@ -172,7 +203,8 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
     B, K = int(xq.shape[0]), int(topk_d.shape[1])
     L = _lib.lib()
     nbytes = L.trident_workspace_bytes(ctypes.byref(view), max(B, 1), int(nprobe), K)
-    ws = workspace(xq.device, nbytes)
+    st = stream if stream is not None else torch.cuda.current_stream(xq.device)
+    slot = _workspace_slot(xq.device, st)
     sp = TridentSearchParams(int(mode), B, K, int(nprobe), int(ub_seed), int(use_l1), int(p_init), int(route))
     out = TridentSearchOutputs()
     out.topk_d, out.topk_i = topk_d.data_ptr(), topk_i.data_ptr()
@@ -189,14 +221,15 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
     if stage_events is not None:
         out.events = stage_events.handles
         out.n_events = _lib.EV_COUNT
-    st = stream if stream is not None else torch.cuda.current_stream(xq.device)
     ev0 = ev1 = None
     if record_events:
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record(st)
-    rc = L.trident_search(ctypes.byref(view), ctypes.byref(sp), ctypes.c_void_p(xq.data_ptr()),
-                          ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()),
-                          ctypes.byref(out), ctypes.c_void_p(st.cuda_stream))
+    with slot.lock:
+        ws = _grow(slot, xq.device, nbytes, st)
+        rc = L.trident_search(ctypes.byref(view), ctypes.byref(sp), ctypes.c_void_p(xq.data_ptr()),
+                              ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws.numel()),
+                              ctypes.byref(out), ctypes.c_void_p(st.cuda_stream))
     check(rc, "trident_search")
     if record_events:
         ev1.record(st)
@@ -256,6 +289,14 @@ def launch_trident_v4_search(
     _need(int(tile_orig_ids.shape[1]) == int(tile_size),
           f"tile_size={tile_size} does not match the packed tiles ({tile_orig_ids.shape[1]})")
     tiles = int(tile_orig_ids.shape[0])
+    _check_tensor("orig_ids_sorted", orig_ids_sorted, torch.int32, dev, 1)
+    _need(orig_ids_sorted.numel() == N, f"orig_ids_sorted must hold N={N} int32 ids")
+    if tile_r_minmax is not None and tile_r_minmax.numel() > 0:
+        _check_tensor("tile_r_minmax", tile_r_minmax, torch.float32, dev)
+        _need(tile_r_minmax.numel() == 2 * tiles, f"tile_r_minmax must be [tiles={tiles}, 2] float32")
+    else:
+        tile_r_minmax = None
+    _need(not (int(use_l1) and mode == 2 and tile_r_minmax is None), "use_l1 needs tile_r_minmax")
     if mode == 2:
         _check_tensor("sq8_packed", sq8_packed, torch.int32, dev)
         _need(sq8_packed.numel() == tiles * (D_pad // 4) * int(tile_size),

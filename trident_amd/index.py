@@ -70,7 +70,8 @@ class PinnedHostBuffer:
     requests up, hipHostMalloc gives exactly the bytes asked for.
     """
 
-    def __init__(self, shape, dtype=torch.float32):
+    def __init__(self, shape, dtype=torch.float32, owner=None):
+        self._owner = owner  # object whose xb_sorted is this buffer's tensor (cleared by free)
         nbytes = int(np.prod(shape)) * torch.empty(0, dtype=dtype).element_size()
         ptr = ctypes.c_void_p()
         _lib.check(_lib.lib().trident_host_alloc_mapped(ctypes.c_size_t(max(nbytes, 1)), ctypes.byref(ptr)),
@@ -83,7 +84,12 @@ class PinnedHostBuffer:
         self.tensor = torch.from_numpy(arr)
 
     def free(self):
+        """Releases the host memory.  The owning storage's ``xb_sorted`` (a view of it) is
+        cleared first, so nothing keeps a tensor over freed memory; every search using that
+        storage must have completed (synchronise its stream before freeing)."""
         if self._ptr:
+            if self._owner is not None and getattr(self._owner, "xb_sorted", None) is self.tensor:
+                self._owner.xb_sorted = None
             self.tensor = None
             _lib.lib().trident_host_free(ctypes.c_void_p(self._ptr))
             self._ptr = None
@@ -107,7 +113,7 @@ class SharedClusterStorage:
         self.placement = xb_placement
         self._host_buf = None
         if xb_placement == "host":
-            self._host_buf = PinnedHostBuffer((self.N, self.D), torch.float32)
+            self._host_buf = PinnedHostBuffer((self.N, self.D), torch.float32, owner=self)
             self.xb_sorted = self._host_buf.tensor
             step = 1 << 22
             perm_cpu = sort_perm.cpu()
