@@ -144,6 +144,21 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                    void* workspace, size_t workspace_bytes, const TridentSearchOutputs* out,
                    void* stream);
 
+/* Bytes of the fixed scratch array behind trident_search_noalloc (one per GPU, 64 MiB). */
+#define TRIDENT_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* trident_search without a workspace argument, and without any allocation: its scratch memory
+ * is a fixed device array of TRIDENT_NOALLOC_SCRATCH_BYTES compiled into the library (one copy
+ * per GPU, kept until the process ends).  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under graph capture, tight serving loops, hosts that
+ * forbid hipMalloc).  Batches whose trident_workspace_bytes exceeds the array fail with
+ * TRIDENT_ERR_WORKSPACE_TOO_SMALL.  The stream's device must be the current device.  Every call
+ * on one GPU shares that GPU's array (each call initialises what it reads), so calls that
+ * overlap on one GPU -- on different streams or host threads -- race and must be serialised by
+ * the caller; calls in one stream are ordered and safe. */
+int trident_search_noalloc(const TridentIndexView* ix, const TridentSearchParams* sp,
+                           const float* xq, const TridentSearchOutputs* out, void* stream);
+
 /* Front end only: float64 coarse distances and the exact (d, cid) top-nprobe per query.
  * workspace: >= trident_workspace_bytes(ix, B, nprobe, 1) bytes. */
 int trident_coarse_probe(const TridentIndexView* ix, const float* xq, int32_t B, int32_t nprobe,

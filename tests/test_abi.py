@@ -84,6 +84,24 @@ def test_host_validation_errors_without_gpu():
     assert L.trident_workspace_bytes(None, 1, 1, 1) == 0
 
 
+def test_noalloc_refuses_oversized_batches_without_touching_the_device():
+    """trident_search_noalloc checks the batch against its fixed scratch before any HIP call
+    (the view's pointers are never dereferenced here)."""
+    L = _lib.lib()
+    v = TridentIndexView()
+    v.N, v.D, v.D_pad, v.nlist, v.tile_size, v.num_blocks = 1_000_000, 128, 128, 1024, 64, 4
+    v.rot_sq_min = v.rot_sq_max = 1.0
+    for f in ("W_combined", "b_combined", "cluster_vec_off", "cluster_tile_off", "xb_sorted",
+              "tile_orig_ids"):
+        setattr(v, f, 256)
+    out = TridentSearchOutputs()
+    sp = TridentSearchParams(2, 10_000, 10, 64, 1, 0, -1, 0)
+    need = L.trident_workspace_bytes(ctypes.byref(v), 10_000, 64, 10)
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    rc = L.trident_search_noalloc(ctypes.byref(v), ctypes.byref(sp), None, ctypes.byref(out), None)
+    assert rc == 3 and str(need).encode() in L.trident_last_error()
+
+
 def test_workspace_size_scales_with_batch():
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = 1000, 128, 128, 64

@@ -17,6 +17,8 @@ _P = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _f64 = ctypes.c_double
 
+NOALLOC_SCRATCH_BYTES = 64 << 20  # TRIDENT_NOALLOC_SCRATCH_BYTES
+
 
 class TridentIndexView(ctypes.Structure):
     _fields_ = [
@@ -55,6 +57,8 @@ EXPORTS = {
     "trident_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(TridentIndexView), _i32, _i32, _i32]),
     "trident_search": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), ctypes.POINTER(TridentSearchParams),
                                       _P, _P, ctypes.c_size_t, ctypes.POINTER(TridentSearchOutputs), _P]),
+    "trident_search_noalloc": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), ctypes.POINTER(TridentSearchParams),
+                                              _P, ctypes.POINTER(TridentSearchOutputs), _P]),
     "trident_coarse_probe": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _i32, _P,
                                             ctypes.c_size_t, _P, _P, _i32, _P]),
     "trident_group_pairs": (ctypes.c_int, [_P, _i32, _i32, _i32, _i32, _i32, _P, _P, _P, _P, _P, _P, _P]),

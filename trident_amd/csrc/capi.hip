@@ -18,6 +18,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -26,6 +27,12 @@
 #include "kernels.hpp"
 
 using namespace trident;
+
+// Scratch memory of trident_search_noalloc, for callers that cannot allocate: one copy of this
+// array on every GPU the library runs on, held until the process ends.  Host code never uses
+// the array's name as an address (on the host it is only a stand-in for the symbol): the
+// device address comes from hipGetSymbolAddress, once per device, with that device current.
+static __device__ __align__(256) unsigned char scratch[TRIDENT_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -40,6 +47,30 @@ int fail(int code, const char* fmt, ...) {
     va_end(ap);
     g_last_error = buf;
     return code;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // device address of `scratch` per device, once looked up
+
+// The current device's copy of `scratch` (looked up on the first call on that device).
+int scratch_of_current_device(void** ptr) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(TRIDENT_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(TRIDENT_ERR_UNSUPPORTED, "device %d outside [0, %d)", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(TRIDENT_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return TRIDENT_OK;
 }
 
 int check_launch(const char* what) {
@@ -876,6 +907,38 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         if ((rc = check_launch("stats_fold_kernel"))) return rc;
     }
     return TRIDENT_OK;
+}
+
+int trident_search_noalloc(const TridentIndexView* ix, const TridentSearchParams* sp,
+                           const float* xq, const TridentSearchOutputs* out, void* stream) {
+    int rc = validate_index(ix);
+    if (rc) return rc;
+    if (!sp || !out) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "params/outputs are NULL");
+    if (sp->B < 0 || sp->K < 1 || sp->nprobe < 1)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad sizes B=%d K=%d nprobe=%d", sp->B, sp->K,
+                    sp->nprobe);
+    // the size check comes before any HIP call, so an oversized request fails without touching
+    // the device
+    const size_t need = carve(ix, nullptr, sp->B, sp->nprobe, sp->K).bytes;
+    if (need > (size_t)TRIDENT_NOALLOC_SCRATCH_BYTES)
+        return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL,
+                    "trident_search_noalloc: B=%d nprobe=%d K=%d needs %zu bytes of scratch, more "
+                    "than the fixed %zu (use trident_search with a caller-owned workspace)",
+                    sp->B, sp->nprobe, sp->K, need, (size_t)TRIDENT_NOALLOC_SCRATCH_BYTES);
+    if (stream) {
+        int sdev = -1, cur = -1;
+        hipError_t e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+        if (e == hipSuccess) e = hipGetDevice(&cur);
+        if (e != hipSuccess)
+            return fail(TRIDENT_ERR_HIP, "stream device: %s", hipGetErrorString(e));
+        if (sdev != cur)
+            return fail(TRIDENT_ERR_INVALID_ARGUMENT,
+                        "trident_search_noalloc: the stream is on device %d, make it current (current "
+                        "device %d)", sdev, cur);
+    }
+    void* ws = nullptr;
+    if ((rc = scratch_of_current_device(&ws))) return rc;
+    return trident_search(ix, sp, xq, ws, (size_t)TRIDENT_NOALLOC_SCRATCH_BYTES, out, stream);
 }
 
 int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
