@@ -1,32 +1,45 @@
 #!/usr/bin/env python3
-"""QPS at 100% exact top-10 on one MI355X, with the scan kernel's roofline and the CPU baseline.
+"""QPS at 100% exact top-10 on one MI355X, with the dominant kernel's roofline and the CPU
+baseline.
 
-Workload (the config the metric is quoted on): N = 1,000,000
-histogram-like descriptors, D = 128 (integer values 0-255 stored as float32), nlist = 1024,
-nprobe = 64 (headline; --nprobe 32 / 128 for the other points), K = 10, B = 10,000 queries.
-Synthetic data and index are built on the GPU first (untimed).
+Workload (default): BASELINE.json configs[4], the largest single-GPU configuration -- N = 1e8
+histogram-like descriptors, D = 128 (integer values 0-255 stored as float32), nlist = 16,384,
+nprobe = 128, K = 10, B = 10,000 queries; SQ8 codes (12.8 GB) and the batched route's code
+cells in HBM, the 51.2 GB FP32 base in hipHostMalloc-mapped pinned host memory (read over PCIe
+by Stage Z only).  Data and index are generated and built on the GPU first (untimed).
+``--cfg 1..4`` selects the in-HBM configurations instead; after the configs[4] line the bench
+also times configs[1] (cfg 2, N = 1e6 in HBM) and reports it under ``extra.cfg2``.
 
-One step = one full batched search of B queries (front end + two-pass cascade + merge) on
-inputs already resident in HBM.  W warmup steps, then exactly K timed steps between two
-torch.cuda.synchronize() calls.  Afterwards (untimed):
-  * exactness: every query's ids and distances against the float64 CPU oracle;
-  * roofline of the dominant kernel.  Batched route (the default at this size): the pass-B
-    scan on the int8 matrix cores, algorithmic work per launch = 4 * D_pad int8 ops per
-    (query, vector) candidate over every probed cluster (multiply + add, two weight planes),
-    priced against the 5.0 POP/s dense int8 peak.  Per-pair route: the pass-2 pair scan,
-    algorithmic bytes = sum over its pairs of n_c * D_pad (SQ8 codes at full depth), priced
-    against 8 TB/s.  Either way divided by the launch's duration from HIP events recorded on
-    the library's stream around it;
-  * cpu_baseline: the reference's CPU IVF-Flat (omp_cpu_ivfflat_f32 restated in oracle/,
-    FP32, OpenMP) on the same probes, all B queries, warmup 1 + 3 timed rounds.
+One step = one full batched search of B queries (front end + seeding pass + lower-bound pass +
+exact refine + merge) with the queries already resident in HBM.  W warmup steps, then exactly K
+timed steps in R rounds (K / R steps each, bracketed by torch.cuda.synchronize()); ``value`` is
+B * K / (total timed seconds), ``rounds`` gives the per-round mean and standard deviation.
+Afterwards (untimed):
+  * exactness: ids and distances of the checked queries against the float64 CPU oracle;
+  * roofline of the dominant kernel (batched route: the lower-bound pass on the int8 matrix
+    cores, 4 * D_pad int8 ops per probed (query, vector) pair -- multiply + add over two
+    weight planes -- against the 5.0 POP/s dense int8 peak; per-pair route: SQ8 code bytes at
+    full depth against 8 TB/s), its duration from HIP events on the library's stream, and its
+    HBM bytes per launch from the committed rocprofv3 PMC summary of the same workload;
+  * out of core: PCIe bytes of Stage Z, closed form (survivors x D x 4) and, when committed,
+    the uncached-read counter of the same workload;
+  * cpu_baseline: the reference's CPU IVF-Flat (omp_cpu_ivfflat_f32, restated in oracle/,
+    FP32, OpenMP) on the same probes over a bounded query sample, the box's thread share,
+    threads pinned (OMP_PROC_BIND=spread, OMP_PLACES=cores), warmup 1 + 3 rounds; on float
+    data its ids are audited against the exact ones (exact tie / FP32 rounding / true miss).
 """
-import argparse
-import json
 import os
-import platform
-import statistics
-import sys
-import time
+
+# OpenMP reads its placement once, when the runtime loads (torch or the oracle library).
+os.environ.setdefault("OMP_PROC_BIND", "spread")
+os.environ.setdefault("OMP_PLACES", "cores")
+
+import argparse  # noqa: E402
+import json  # noqa: E402
+import platform  # noqa: E402
+import statistics  # noqa: E402
+import sys  # noqa: E402
+import time  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -34,8 +47,7 @@ sys.path.insert(0, ROOT)
 METRIC = "QPS at 100% exact top-10, 1×MI355X; achieved HBM GB/s vs peak"  # BASELINE.json metric, verbatim
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix throughput
-PROFILE_TRAFFIC = {1: os.path.join(ROOT, "profiles", "pair_scan_cfg2_traffic.json"),
-                   2: os.path.join(ROOT, "profiles", "lb_scan_cfg2_traffic.json")}
+PROFILES = os.path.join(ROOT, "profiles")
 
 
 def log(*a):
@@ -53,165 +65,207 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-# In-HBM configurations of BASELINE.json (configs[0..3]); cfg 2 is the metric's workload.
+def cpu_threads() -> int:
+    """The OpenMP threads the CPU baseline uses: OMP_NUM_THREADS when the host sets it (the GPU
+    boxes set it to their CPU share for one GPU), else every CPU this process may run on."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+# BASELINE.json configs; `check` / `cpu` are the default oracle-check and CPU-baseline samples.
 CONFIGS = {
-    1: dict(N=100_000, D=128, nlist=256, nprobe=16, K=10, B=1_000, T=64, n_centers=256,
-            desc="configs[0]: 256-component isotropic Gaussian mixture"),
-    2: dict(N=1_000_000, D=128, nlist=1024, nprobe=64, K=10, B=10_000, T=64, n_centers=1024,
-            desc="configs[1]: histogram-like u8-valued descriptors"),
-    3: dict(N=1_000_000, D=960, nlist=1024, nprobe=64, K=10, B=1_000, T=256, n_centers=1024,
-            desc="configs[2]: anisotropic power-law Gaussian, D=960"),
-    4: dict(N=10_000_000, D=96, nlist=4096, nprobe=64, K=10, B=10_000, T=64, n_centers=4096,
-            desc="configs[3]: L2-normalised 4096-centre mixture, D=96"),
-    # configs[4] (out of core, 1e8 rows): run with --xb-host, usually with a smaller --N
-    5: dict(N=100_000_000, D=128, nlist=16384, nprobe=128, K=10, B=10_000, T=64, n_centers=1024,
-            desc="configs[4]: histogram-like descriptors, out of core"),
+    1: dict(N=100_000, D=128, nlist=256, nprobe=16, K=10, B=1_000, T=64, n_centers=256, host=False,
+            check=-1, cpu=-1, desc="configs[0]: 256-component isotropic Gaussian mixture"),
+    2: dict(N=1_000_000, D=128, nlist=1024, nprobe=64, K=10, B=10_000, T=64, n_centers=1024, host=False,
+            check=-1, cpu=-1, desc="configs[1]: histogram-like u8-valued descriptors"),
+    3: dict(N=1_000_000, D=960, nlist=1024, nprobe=64, K=10, B=1_000, T=256, n_centers=1024, host=False,
+            check=-1, cpu=-1, desc="configs[2]: anisotropic power-law Gaussian, D=960"),
+    4: dict(N=10_000_000, D=96, nlist=4096, nprobe=64, K=10, B=10_000, T=64, n_centers=4096, host=False,
+            check=-1, cpu=2000, desc="configs[3]: L2-normalised 4096-centre mixture, D=96"),
+    5: dict(N=100_000_000, D=128, nlist=16384, nprobe=128, K=10, B=10_000, T=64, n_centers=1024, host=True,
+            check=1000, cpu=1000, desc="configs[4]: histogram-like u8-valued descriptors, out of core"),
 }
+FLOAT_CONFIGS = (1, 3, 4)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cfg", type=int, default=2, choices=sorted(CONFIGS))
-    ap.add_argument("--nprobe", type=int, default=0, help="0 = the config's value")
-    ap.add_argument("--K", type=int, default=0, help="0 = the config's value")
-    ap.add_argument("--ub", type=int, default=1, help="TRIDENT_UB_SEED for the timed runs")
-    ap.add_argument("--mode", type=int, default=2, help="2 cascade, 10 CM exact")
-    ap.add_argument("--route", type=int, default=0, help="mode-2 route: 0 auto, 1 per-pair, 2 batched")
-    ap.add_argument("--N", type=int, default=0)
-    ap.add_argument("--B", type=int, default=0)
-    ap.add_argument("--check", type=int, default=-1, help="queries checked against the oracle (-1 = all)")
-    ap.add_argument("--cpu-queries", type=int, default=-1, help="CPU-baseline sample (-1 = all B)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--xb-host", action="store_true",
-                    help="out of core: the FP32 base in mapped pinned host memory (Stage Z over PCIe)")
-    ap.add_argument("--sweep", action="store_true", help="also time other nprobe / ub values and the CM route")
-    ap.add_argument("--calibrate-w0", action="store_true", help="router crossover sweep over batch sizes")
-    args = ap.parse_args()
-    cfg = dict(CONFIGS[args.cfg])
-    for k in ("N", "B", "K", "nprobe"):
-        if getattr(args, k):
-            cfg[k] = getattr(args, k)
+def load_profile(name, **match):
+    """A committed rocprofv3 summary (profiles/<name>.json) if it was measured on this
+    workload (every key of `match` equal), else None."""
+    path = os.path.join(PROFILES, name + ".json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        p = json.load(f)
+    return p if all(p.get(k) == v for k, v in match.items()) else None
 
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build's path runs on a "
-              "single MI355X; sharding across GPUs is a design, not part of this build.", file=sys.stderr)
-        sys.exit(2)
 
-    import numpy as np
+class Workload:
+    """Synthetic data + index of one configuration, built on the GPU."""
+
+    def __init__(self, cfg_id, cfg, xb_host, dev):
+        import torch
+        from trident_amd import clustering, datagen
+        from trident_amd.index import SharedClusterStorage, TridentV4Index
+        self.cfg_id, self.cfg, self.xb_host = cfg_id, cfg, xb_host
+        N, D, nlist, K, B = cfg["N"], cfg["D"], cfg["nlist"], cfg["K"], cfg["B"]
+        t0 = time.perf_counter()
+        xb, xq = datagen.generate(cfg_id, device=dev, seed=0, N=N, D=D, B=B, n_centers=cfg["n_centers"])
+        torch.cuda.synchronize()
+        log(f"generated cfg{cfg_id} N={N} D={D} B={B} in {time.perf_counter() - t0:.1f}s")
+        t1 = time.perf_counter()
+        cen, lid, r, mean64, R64, t_train = clustering.train_clustering(
+            xb, nlist, seed=0, niter=20, max_train=min(N, max(64 * nlist, 256 * 1024)), device=dev)
+        self.st = SharedClusterStorage(xb, lid, r, nlist, device=dev, xb_placement="host" if xb_host else "device")
+        self.ix = TridentV4Index(self.st, cen, mean64, R64, tile_size=cfg["T"], device=dev, max_batch=B,
+                                 max_nprobe=max(128, cfg["nprobe"]), k=K)
+        del xb
+        torch.cuda.synchronize()
+        self.build_s = time.perf_counter() - t1
+        log(f"k-means {t_train:.1f}s, index build {self.ix.build_time_s:.1f}s, total {self.build_s:.1f}s; "
+            f"SQ8 {self.ix.sq8_bytes() / 1e6:.1f} MB")
+        self.xq = xq.contiguous()
+        self.xq_np = xq.cpu().numpy()
+
+    def free(self):
+        import torch
+        torch.cuda.synchronize()
+        if self.st._host_buf is not None:
+            self.st._host_buf.free()
+        self.ix = self.st = None
+        torch.cuda.empty_cache()
+
+
+def time_steps(run, steps, warmup, rounds):
+    """W warmup steps, then `steps` timed steps in `rounds` rounds; returns (ms per step over the
+    whole timed region, per-round QPS factors, stage events of every timed step)."""
     import torch
-
-    from trident_amd import _lib, clustering, datagen
-    from trident_amd.index import SharedClusterStorage, TridentV4Index
-
-    dev = torch.device("cuda:0")
-    t0 = time.perf_counter()
-    N, D, nlist, K, B = cfg["N"], cfg["D"], cfg["nlist"], cfg["K"], cfg["B"]
-    xb, xq = datagen.generate(args.cfg, device=dev, seed=0, N=N, D=D, B=B, n_centers=cfg["n_centers"])
+    from trident_amd import _lib
+    for _ in range(warmup):
+        run(None)
+    rounds = max(1, min(rounds, steps))
+    per = [steps // rounds + (1 if r < steps % rounds else 0) for r in range(rounds)]
+    evs = [_lib.StageEvents() for _ in range(steps)]
     torch.cuda.synchronize()
-    log(f"generated cfg{args.cfg} N={N} D={D} B={B} in {time.perf_counter() - t0:.1f}s")
-    t1 = time.perf_counter()
-    cen, lid, r, mean64, R64, t_train = clustering.train_clustering(
-        xb, nlist, seed=0, niter=20, max_train=min(N, max(64 * nlist, 256 * 1024)), device=dev)
-    st = SharedClusterStorage(xb, lid, r, nlist, device=dev,
-                              xb_placement="host" if args.xb_host else "device")
-    ix = TridentV4Index(st, cen, mean64, R64, tile_size=cfg["T"], device=dev, max_batch=B,
-                        max_nprobe=max(128, cfg["nprobe"]), k=K)
-    del xb
-    torch.cuda.synchronize()
-    log(f"k-means {t_train:.1f}s, index build {ix.build_time_s:.1f}s, total {time.perf_counter() - t1:.1f}s; "
-        f"SQ8 {ix.sq8_bytes() / 1e6:.1f} MB")
-    xq_d = xq.contiguous()
+    t_all, round_ms, k = 0.0, [], 0
+    for n in per:
+        torch.cuda.synchronize()
+        ts = time.perf_counter()
+        for _ in range(n):
+            run(evs[k])
+            k += 1
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - ts
+        t_all += dt
+        round_ms.append(dt * 1000.0 / n)
+    return t_all * 1000.0 / steps, round_ms, evs
 
-    def run(nprobe, mode, ub, events=None):
-        return ix.search(xq_d, nprobe, mode=mode, ub_seed=ub, stage_events=events, route=args.route)
 
-    # ---- timed region ----
-    nprobe, mode, ub = cfg["nprobe"], args.mode, args.ub
-    for _ in range(args.warmup):
-        run(nprobe, mode, ub)
-    evs = [_lib.StageEvents() for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    ts = time.perf_counter()
-    for i in range(args.steps):
-        run(nprobe, mode, ub, evs[i])
-    torch.cuda.synchronize()
-    te = time.perf_counter()
-    ms_per_step = (te - ts) * 1000.0 / args.steps
-    qps = B / (ms_per_step / 1000.0)
-    log(f"nprobe={nprobe} mode={mode} ub={ub}: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS")
-
-    E = _lib
-    stage = {
-        "front_end_ms": statistics.mean(e.elapsed_ms(E.EV_START, E.EV_PROBED) for e in evs),
-        "group_pairs_ms": statistics.mean(e.elapsed_ms(E.EV_PROBED, E.EV_GROUPED) for e in evs),
-        "pass1_scan_ms": statistics.mean(e.elapsed_ms(E.EV_GROUPED, E.EV_P1_SCAN) for e in evs),
-        "pass1_merge_ms": statistics.mean(e.elapsed_ms(E.EV_P1_SCAN, E.EV_P1_MERGE) for e in evs),
-        "pass2_scan_ms": statistics.mean(e.elapsed_ms(E.EV_P1_MERGE, E.EV_P2_SCAN) for e in evs),
-        "pass2_merge_ms": statistics.mean(e.elapsed_ms(E.EV_P2_SCAN, E.EV_END) for e in evs),
-    }
-    stage["gpu_total_ms"] = statistics.mean(e.elapsed_ms(E.EV_START, E.EV_END) for e in evs)
+def stage_breakdown(evs):
+    from trident_amd import _lib as E
+    pairs = {"front_end_ms": (E.EV_START, E.EV_PROBED), "group_pairs_ms": (E.EV_PROBED, E.EV_GROUPED),
+             "pass1_scan_ms": (E.EV_GROUPED, E.EV_P1_SCAN), "pass1_merge_ms": (E.EV_P1_SCAN, E.EV_P1_MERGE),
+             "pass2_scan_ms": (E.EV_P1_MERGE, E.EV_P2_SCAN), "pass2_merge_ms": (E.EV_P2_SCAN, E.EV_END),
+             "gpu_total_ms": (E.EV_START, E.EV_END)}
+    out = {k: statistics.mean(e.elapsed_ms(a, b) for e in evs) for k, (a, b) in pairs.items()}
     for e in evs:
         e.destroy()
+    return out
+
+
+class _RowsById:
+    """xb_sorted indexed by original id (for the audit), without a reordered copy."""
+
+    def __init__(self, xb_sorted, orig_ids):
+        import numpy as np
+        self.xb = xb_sorted
+        self.pos = np.empty(len(orig_ids), np.int64)
+        self.pos[orig_ids] = np.arange(len(orig_ids))
+
+    def __getitem__(self, i):
+        return self.xb[self.pos[i]]
+
+
+def measure(cfg_id, cfg, args, dev, primary=True):
+    """Builds the workload, times it and checks it; returns the JSON fields of one config."""
+    import numpy as np
+    import torch
+    from trident_amd import _lib, metrics
+
+    w = Workload(cfg_id, cfg, cfg["host"], dev)
+    ix, st = w.ix, w.st
+    N, D, K, B, nprobe = cfg["N"], cfg["D"], cfg["K"], cfg["B"], cfg["nprobe"]
+    mode, ub = args.mode, args.ub
+
+    def run(events):
+        return ix.search(w.xq, nprobe, mode=mode, ub_seed=ub, stage_events=events, route=args.route)
+
+    steps = args.steps if primary else args.extra_steps
+    ms_per_step, round_ms, evs = time_steps(run, steps, args.warmup, args.rounds)
+    qps = B / (ms_per_step / 1000.0)
+    round_qps = [B / (m / 1000.0) for m in round_ms]
+    stage = stage_breakdown(evs)
+    log(f"cfg{cfg_id} nprobe={nprobe} mode={mode} ub={ub}: {ms_per_step:.3f} ms/step, {qps:,.0f} QPS "
+        f"(rounds {statistics.mean(round_qps):,.0f} +- {statistics.pstdev(round_qps):,.0f})")
     log("stages (ms): " + ", ".join(f"{k}={v:.3f}" for k, v in stage.items()))
 
-    # ---- algorithmic bytes and pruning statistics (untimed) ----
+    # ---- algorithmic work and pruning statistics (untimed) ----
     stats = torch.zeros(4, dtype=torch.int64, device=dev)
-    d_out, i_out, _ = ix.search(xq_d, nprobe, mode=mode, ub_seed=ub, stats_buf=stats, route=args.route)
+    d_out, i_out, _ = ix.search(w.xq, nprobe, mode=mode, ub_seed=ub, stats_buf=stats, route=args.route)
     torch.cuda.synchronize()
     gpu_d, gpu_i = d_out.cpu().numpy().copy(), i_out.cpu().numpy().copy()
     probes = ix.probe_cids_buf[:B, :nprobe].cpu().numpy()
-    vec_off = st.cluster_vec_off.cpu().numpy().astype(np.int64)
-    sizes = np.diff(vec_off)
+    sizes = np.diff(st.cluster_vec_off.cpu().numpy().astype(np.int64))
     p_init = _lib.lib().trident_p_init_rule(mode, B, K, nprobe) if mode == 2 else 0
-    bytes_p2 = int(sizes[probes[:, p_init:]].sum()) * ix.D_pad
     bytes_all = int(sizes[probes].sum()) * ix.D_pad
+    bytes_p2 = int(sizes[probes[:, p_init:]].sum()) * ix.D_pad
     if mode == 10:
-        bytes_p2 = int(sizes[probes].sum()) * D * 4
-        bytes_all = bytes_p2
+        bytes_p2 = bytes_all = int(sizes[probes].sum()) * D * 4
     tot, dims, surv, ins = [int(v) for v in stats.tolist()]
     route = ix.route_for(B, nprobe, K, args.route) if mode == 2 else _lib.ROUTE_PAIR
     t_scan = stage["pass2_scan_ms"] * 1e-3
     if route == _lib.ROUTE_BATCHED:
-        # pass B scans every probed (query, vector) pair: D_pad int8 MACs per weight plane
         ops_alg = 4 * bytes_all
         achieved = ops_alg / t_scan / 1e12
-        roof = {"bound": "mfma", "kernel": "lb_scan_kernel<KS> (pass B, int8 matrix cores)",
+        roof = {"bound": "mfma", "kernel": "lb_scan_kernel<KS> (lower-bound pass, int8 matrix cores)",
                 "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": round(achieved / INT8_PEAK_TOPS, 4), "ops_alg_per_launch": ops_alg}
-        log(f"pass-B scan: {ops_alg / 1e12:.2f} T int8 ops in {stage['pass2_scan_ms']:.3f} ms -> {achieved:,.1f} TOP/s "
-            f"({achieved / INT8_PEAK_TOPS:.3f} of peak); survivors {surv}/{tot}")
+        prof_name = f"lb_scan_cfg{cfg_id}_traffic"
     else:
         achieved = bytes_p2 / t_scan / 1e9
         roof = {"bound": "hbm", "kernel": "pair_scan_kernel (pass 2)" if mode == 2 else "pair_scan_kernel (CM)",
                 "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "bytes_alg_per_launch": bytes_p2}
-        log(f"pass-2 scan: {bytes_p2 / 1e9:.2f} GB algorithmic in {stage['pass2_scan_ms']:.3f} ms -> {achieved:,.0f} GB/s "
-            f"({achieved / HBM_PEAK_GBPS:.2f} of peak); survivors {surv}/{tot}")
+        prof_name = f"pair_scan_cfg{cfg_id}_traffic"
     roof["launch_ms"] = round(stage["pass2_scan_ms"], 4)
+    prof = load_profile(prof_name, N=N, nprobe=nprobe, K=K, B=B) if mode == 2 else None
+    roof["traffic"] = prof["hbm_bytes_per_launch"] if prof else None
+    log(f"dominant kernel: {roof['kernel']} {roof['achieved']} {roof['unit']} = {roof['frac']:.3f} of peak "
+        f"in {roof['launch_ms']} ms; survivors {surv}/{tot}")
 
     # ---- exactness against the float64 oracle ----
     from oracle import oracle as O
     h = ix.host_arrays()
-    nchk = B if args.check < 0 else min(args.check, B)
-    xq_np = xq.cpu().numpy()
+    nchk = cfg["check"] if args.check == -1 else args.check
+    nchk = B if nchk < 0 else min(nchk, B)
     tc = time.perf_counter()
-    ref_cids, _ = O.coarse_probe(xq_np[:nchk], h["centroids"], nprobe)
-    ref_d, ref_i = O.ivf_exact(xq_np[:nchk], ref_cids, h["vec_off"], h["xb_sorted"], h["orig_ids_sorted"], K)
-    probe_same = int((ref_cids == probes[:nchk]).all(axis=1).sum())
-    ids_same = int((ref_i == gpu_i[:nchk]).all(axis=1).sum())
-    dist_same = int((ref_d.astype(np.float32) == gpu_d[:nchk]).all(axis=1).sum())
-    log(f"oracle check {nchk} queries in {time.perf_counter() - tc:.1f}s: probes identical {probe_same}, "
-        f"ids identical {ids_same}, distances identical {dist_same}")
+    ref_cids, _ = O.coarse_probe(w.xq_np[:nchk], h["centroids"], nprobe)
+    ref_d, ref_i = O.ivf_exact(w.xq_np[:nchk], ref_cids, h["vec_off"], h["xb_sorted"], h["orig_ids_sorted"], K)
+    exact = {"queries_checked": nchk,
+             "probes_identical": int((ref_cids == probes[:nchk]).all(axis=1).sum()),
+             "ids_identical": int((ref_i == gpu_i[:nchk]).all(axis=1).sum()),
+             "distances_identical": int((ref_d.astype(np.float32) == gpu_d[:nchk]).all(axis=1).sum())}
+    log(f"oracle check {nchk} queries in {time.perf_counter() - tc:.1f}s: " +
+        ", ".join(f"{k} {v}" for k, v in exact.items() if k != "queries_checked"))
 
-    # ---- CPU baseline: reference CPU IVF-Flat restated (FP32, OpenMP), same probes ----
+    # ---- CPU baseline: the reference CPU IVF-Flat restated (FP32, OpenMP), same probes ----
     cpu = None
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        nc = B if args.cpu_queries < 0 else min(args.cpu_queries, B)
-        fn = lambda: O.ivfflat_f32(xq_np[:nc], probes[:nc], h["vec_off"], h["xb_sorted"], h["orig_ids_sorted"],
+        threads = cpu_threads()
+        nc = cfg["cpu"] if args.cpu_queries == -1 else args.cpu_queries
+        nc = B if nc < 0 else min(nc, B)
+        fn = lambda: O.ivfflat_f32(w.xq_np[:nc], probes[:nc], h["vec_off"], h["xb_sorted"], h["orig_ids_sorted"],
                                    K, threads=threads)
         fn()
         rounds = []
@@ -219,92 +273,157 @@ def main():
             tb = time.perf_counter()
             fd, fi = fn()
             rounds.append(nc / (time.perf_counter() - tb))
-        f32_match = int((fi == gpu_i[:nc]).all(axis=1).sum())
+        f32_same = int((fi == gpu_i[:nc]).all(axis=1).sum())
         cpu = {"value": round(statistics.mean(rounds), 1), "unit": "queries/s", "cores": threads,
                "kind": "port",
-               "sample": f"first {nc} of {B} queries, nprobe={nprobe}, same probes as the GPU; warmup 1 + "
-                         f"3 rounds (std {statistics.pstdev(rounds):.1f}); CPU: {cpu_model()}; FP32 ids "
-                         f"identical to the GPU's exact ids on {f32_match}/{nc} queries"}
-        log(f"cpu baseline: {cpu['value']:,.1f} QPS on {threads} threads")
+               "sample": f"first {nc} of {B} queries, nprobe={nprobe}, same probes as the GPU; warmup 1 + 3 "
+                         f"rounds (std {statistics.pstdev(rounds):.1f} QPS); {threads} OpenMP threads "
+                         f"(OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}, OMP_PLACES={os.environ.get('OMP_PLACES')}) "
+                         f"of {os.cpu_count()} online CPUs, {len(os.sched_getaffinity(0))} in this process's "
+                         f"affinity; CPU: {cpu_model()}; FP32 ids identical to the GPU's exact ids on "
+                         f"{f32_same}/{nc} queries",
+               "online_cpus": os.cpu_count(), "cpu_model": cpu_model()}
+        if cfg_id in FLOAT_CONFIGS:
+            a = O.audit(fi, gpu_i[:nc], _RowsById(h["xb_sorted"], h["orig_ids_sorted"]), w.xq_np[:nc])
+            rec, strict, full = metrics.eval_accuracy_v4(fi, fd, gpu_i[:nc], gpu_d[:nc], gpu_i[:nc], k=K)
+            cpu["fp32_audit_vs_exact"] = {
+                "diff_slots": a["diff_slots"], "exact_tie": a["exact_tie"], "f32_rounding_le_1e-5": a["f32_rounding"],
+                "true_miss": a["true_miss"], "max_rel": a["max_rel"],
+                "strict_overlap_pct": round(strict, 4), "queries_all_slots_pct": round(full, 2)}
+        log(f"cpu baseline: {cpu['value']:,.1f} QPS on {threads} threads over {nc} queries")
 
-    sweep = {}
-    if args.sweep:
+    out = {"qps": qps, "ms_per_step": ms_per_step, "round_qps": round_qps, "stage": stage, "roof": roof,
+           "exact": exact, "cpu": cpu, "route": route, "p_init": p_init, "bytes_all": bytes_all,
+           "pruning": {"candidates": tot, "dims_scanned_frac": round(dims / max(tot * ix.D_pad, 1), 4),
+                       "survivors_frac": round(surv / max(tot, 1), 6), "refined_kept": ins},
+           "surv": surv, "nprobe": nprobe, "K": K, "B": B, "N": N, "D": D, "nlist": cfg["nlist"]}
+    if w.xb_host:
+        pcie = surv * D * 4
+        oc = {"stage_z_rows": surv, "row_bytes": D * 4, "pcie_bytes_closed_form": pcie,
+              "pcie_bytes_per_query": round(pcie / B, 1), "stage_z_ms": round(stage["pass2_merge_ms"], 4),
+              "pcie_GBps": round(pcie / max(stage["pass2_merge_ms"], 1e-9) / 1e6, 1)}
+        pp = load_profile(f"refine_cfg{cfg_id}_pcie", N=N, nprobe=nprobe, K=K, B=B)
+        if pp:
+            oc["pcie_bytes_measured"] = pp["pcie_bytes_per_launch"]
+            oc["pcie_bytes_measured_per_query"] = round(pp["pcie_bytes_per_launch"] / B, 1)
+            oc["pcie_counter"] = pp["counter"]
+        out["out_of_core"] = oc
+
+    if primary and args.sweep:
+        sweep = {}
         for npb, md, u in ((nprobe // 2, 2, ub), (nprobe * 2, 2, ub), (nprobe, 10, 0), (nprobe, 2, 0),
                            (nprobe, 2, 2)):
+            if npb > ix.max_nprobe or npb < 1:
+                continue
             for _ in range(2):
-                run(npb, md, u)
+                ix.search(w.xq, npb, mode=md, ub_seed=u, route=args.route)
             torch.cuda.synchronize()
             tb = time.perf_counter()
             for _ in range(5):
-                run(npb, md, u)
+                ix.search(w.xq, npb, mode=md, ub_seed=u, route=args.route)
             torch.cuda.synchronize()
             ms = (time.perf_counter() - tb) * 200.0
             sweep[f"nprobe{npb}_mode{md}_ub{u}"] = {"ms_per_step": round(ms, 3), "qps": round(B / ms * 1000.0, 1)}
             log(f"sweep nprobe={npb} mode={md} ub={u}: {ms:.3f} ms, {B / ms * 1000.0:,.0f} QPS")
-
-    w0 = None
-    if args.calibrate_w0:
+        out["sweep"] = sweep
+    if primary and args.calibrate_w0:
         from trident_amd import router
-        W0, rows = router.calibrate_w0(ix, xq_d, nprobe, batches=(1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024),
+        W0, rows = router.calibrate_w0(ix, w.xq, nprobe, batches=(1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024),
                                        warmup=3, iters=10, ub_seed=ub)
         for r_ in rows:
             log(f"W0 sweep B={r_['batch']:5d} W={r_['work']:.3e} cm={r_['ms_cm']:.3f}ms "
                 f"cascade={r_['ms_cascade']:.3f}ms -> {'cascade' if r_['cascade_faster'] else 'cm'}")
-        w0 = {"W0": W0, "rows": rows}
+        out["w0_calibration"] = {"W0": W0, "rows": rows}
         log(f"calibrated W0 = {W0:.3e}")
+    w.free()
+    return out
 
-    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 PMC summary of
-    # the same workload (cfg 2, nprobe 64 only)
-    roof["traffic"] = None
-    prof = PROFILE_TRAFFIC.get(route)
-    if args.cfg == 2 and nprobe == 64 and mode == 2 and prof and os.path.exists(prof):
-        with open(prof) as f:
-            roof["traffic"] = json.load(f).get("hbm_bytes_per_launch")
 
-    line = {
-        "metric": METRIC, "value": round(qps, 1), "unit": "queries/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "u8 codes x int8 weights (i32 MFMA) / f32 bounds / f64 exact distances", "data": "synthetic",
-        "config": {"workload": f"BASELINE {cfg['desc']}, N={N}, D={D}, nlist={nlist}, nprobe={nprobe}, "
-                               f"K={K}, B={B}",
-                   "route": ("batched" if route == _lib.ROUTE_BATCHED else "pair") if mode == 2 else "cm_exact",
-                   "ub_seed": ub, "p_init": p_init, "tile_size": cfg["T"], "parallelism": "single GPU",
-                   "xb_placement": "host (mapped, out of core)" if args.xb_host else "device"},
-        "roofline": roof,
-        "cpu_baseline": cpu,
-        "exact": {"queries_checked": nchk, "probes_identical": probe_same, "ids_identical": ids_same,
-                  "distances_identical": dist_same},
-        "stages_ms": {k: round(v, 4) for k, v in stage.items()},
-        "pruning": {"candidates": tot, "dims_scanned_frac": round(dims / max(tot * ix.D_pad, 1), 4),
-                    "survivors_frac": round(surv / max(tot, 1), 5), "refined_inserted": ins},
-        "bytes_alg_total": bytes_all,
-    }
-    # the metric's HBM view of the same launch: algorithmic code bytes (every probed vector at
-    # full depth, no pruning credit; above 1.0 only through on-chip reuse) and the
-    # physical traffic the committed rocprofv3 summary measured for this workload
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=12)
+    ap.add_argument("--rounds", type=int, default=5, help="timed steps are split into this many rounds")
+    ap.add_argument("--cfg", type=int, default=5, choices=sorted(CONFIGS))
+    ap.add_argument("--nprobe", type=int, default=0, help="0 = the config's value")
+    ap.add_argument("--K", type=int, default=0, help="0 = the config's value")
+    ap.add_argument("--ub", type=int, default=1, help="TRIDENT_UB_SEED for the timed runs")
+    ap.add_argument("--mode", type=int, default=2, help="2 cascade, 10 CM exact")
+    ap.add_argument("--route", type=int, default=0, help="mode-2 route: 0 auto, 1 per-pair, 2 batched")
+    ap.add_argument("--N", type=int, default=0)
+    ap.add_argument("--B", type=int, default=0)
+    ap.add_argument("--check", type=int, default=-1, help="queries checked against the oracle (-1 = config default)")
+    ap.add_argument("--cpu-queries", type=int, default=-1, help="CPU-baseline sample (-1 = config default)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--xb-host", action="store_true", help="FP32 base in mapped pinned host memory (out of core)")
+    ap.add_argument("--xb-device", action="store_true", help="FP32 base in HBM (cfg 5 defaults to host)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the cfg 2 line after cfg 5")
+    ap.add_argument("--extra-steps", type=int, default=20)
+    ap.add_argument("--sweep", action="store_true", help="also time other nprobe / ub values and the CM route")
+    ap.add_argument("--calibrate-w0", action="store_true", help="router crossover sweep over batch sizes")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): this build's path runs on a "
+              "single MI355X; sharding across GPUs is a design, not part of this build.", file=sys.stderr)
+        sys.exit(2)
+    cfg = dict(CONFIGS[args.cfg])
+    for k in ("N", "B", "K", "nprobe"):
+        if getattr(args, k):
+            cfg[k] = getattr(args, k)
+    if args.xb_host:
+        cfg["host"] = True
+    if args.xb_device:
+        cfg["host"] = False
+
+    import torch
+    dev = torch.device("cuda:0")
+    r = measure(args.cfg, cfg, args, dev, primary=True)
+    from trident_amd import _lib
+    roof = r["roof"]
     t_l = roof["launch_ms"] * 1e-3
-    alg = bytes_all if mode == 2 else bytes_p2
+    alg = r["bytes_all"]
     hv = {"bytes_alg_per_launch": alg, "alg_GBps": round(alg / t_l / 1e9, 1),
           "alg_frac_of_peak": round(alg / t_l / 1e9 / HBM_PEAK_GBPS, 3)}
     if roof.get("traffic"):
         hv.update({"physical_bytes_per_launch": roof["traffic"],
                    "physical_GBps": round(roof["traffic"] / t_l / 1e9, 1),
                    "physical_frac_of_peak": round(roof["traffic"] / t_l / 1e9 / HBM_PEAK_GBPS, 3)})
-    line["hbm_view"] = hv
-    if args.xb_host:
-        # Stage Z reads every survivor's FP32 row from mapped host memory once (128-byte
-        # segments); a query whose candidate list overflowed would add an exhaustive rescan of
-        # its probed rows, which this count leaves out
-        pcie = surv * D * 4
-        line["out_of_core"] = {"stage_z_rows": surv, "row_bytes": D * 4, "pcie_bytes": pcie,
-                               "pcie_bytes_per_query": round(pcie / B, 1),
-                               "stage_z_ms": round(stage["pass2_merge_ms"], 4),
-                               "pcie_GBps": round(pcie / max(stage["pass2_merge_ms"], 1e-9) / 1e6, 1)}
-    if sweep:
-        line["sweep"] = sweep
-    if w0 is not None:
-        line["w0_calibration"] = w0
+    line = {
+        "metric": METRIC, "value": round(r["qps"], 1), "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u8 codes x int8 weights (i32 MFMA) / f32 bounds / f64 exact distances", "data": "synthetic",
+        "config": {"workload": f"BASELINE {cfg['desc']}, N={r['N']}, D={r['D']}, nlist={r['nlist']}, "
+                               f"nprobe={r['nprobe']}, K={r['K']}, B={r['B']}",
+                   "route": ("batched" if r["route"] == _lib.ROUTE_BATCHED else "pair") if args.mode == 2 else "cm_exact",
+                   "ub_seed": args.ub, "p_init": r["p_init"], "tile_size": cfg["T"], "parallelism": "single GPU",
+                   "xb_placement": "host (mapped, out of core)" if cfg["host"] else "device"},
+        "roofline": roof,
+        "cpu_baseline": r["cpu"],
+        "rounds": {"n": len(r["round_qps"]), "qps_mean": round(statistics.mean(r["round_qps"]), 1),
+                   "qps_std": round(statistics.pstdev(r["round_qps"]), 1)},
+        "exact": r["exact"],
+        "stages_ms": {k: round(v, 4) for k, v in r["stage"].items()},
+        "pruning": r["pruning"],
+        "bytes_alg_total": r["bytes_all"],
+        "hbm_view": hv,
+    }
+    for k in ("out_of_core", "sweep", "w0_calibration"):
+        if k in r:
+            line[k] = r[k]
+    if args.cfg == 5 and not args.no_extra:
+        c2 = dict(CONFIGS[2])
+        e = measure(2, c2, args, dev, primary=False)
+        line["extra"] = {"cfg2": {
+            "workload": f"BASELINE {c2['desc']}, N={c2['N']}, D=128, nlist={c2['nlist']}, nprobe={c2['nprobe']}, "
+                        f"K={c2['K']}, B={c2['B']}",
+            "qps": round(e["qps"], 1), "ms_per_step": round(e["ms_per_step"], 4), "steps": args.extra_steps,
+            "rounds_qps_mean": round(statistics.mean(e["round_qps"]), 1),
+            "rounds_qps_std": round(statistics.pstdev(e["round_qps"]), 1),
+            "exact": e["exact"], "roofline": e["roof"], "cpu_baseline": e["cpu"],
+            "stages_ms": {k: round(v, 4) for k, v in e["stage"].items()}}}
     print(json.dumps(line), flush=True)
 
 

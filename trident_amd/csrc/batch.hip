@@ -64,19 +64,18 @@ __device__ __forceinline__ int splits_of(int n) {
     return min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec);
 }
 
-__device__ __forceinline__ int units_of_entry(const int32_t* seg_off, const int32_t* vec_off,
-                                              int nlist, int e) {
+// Entry e < nlist: the seeding units of cluster e (its pass-1 queries, <= 16 per unit); entry
+// nlist + c: the lower-bound units of cluster c (all its queries, <= uqB per unit).
+__device__ __forceinline__ int units_of_entry(const int32_t* seg, const int32_t* vec_off,
+                                              int nlist, int uqB, int e) {
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
-    const int32_t* so = seg_off + p * (nlist + 1);
-    const int q = so[c + 1] - so[c];
-    const int uq = p ? kUnitQ : kUnitQ0;
+    const int q = (p ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
+    const int uq = p ? uqB : kUnitQ0;
     return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c]) : 0;
 }
 
-__device__ __forceinline__ int groups_of_entry(const int32_t* seg_off, int nlist, int e) {
-    const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
-    const int32_t* so = seg_off + p * (nlist + 1);
-    return (so[c + 1] - so[c] + kGroupQ - 1) / kGroupQ;
+__device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
+    return (seg[c + 1] - seg[c] + kGroupQ - 1) / kGroupQ;
 }
 
 // Block-wide exclusive scan of one count per thread (grid 1); returns the total.
@@ -101,77 +100,75 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t local, uint32_t& ru
     return total;
 }
 
-// grid 1: exclusive scans of the unit counts and of the weight-group counts of the 2 * nlist
-// (pass, cluster) segments.
-__global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg_off,
-                                                        const int32_t* vec_off, int nlist,
-                                                        int32_t* unit_off, int32_t* grp_off) {
+// grid 1: exclusive scans of the unit counts of the 2 * nlist (pass, cluster) entries and of
+// the weight-group counts of the nlist cluster segments.
+__global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg, const int32_t* vec_off,
+                                                        int nlist, int uqB, int32_t* unit_off,
+                                                        int32_t* grp_off) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
     const int tid = threadIdx.x;
     const int E = 2 * nlist;
     const int per = (E + kBlock - 1) / kBlock;
     const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
+    const int perc = (nlist + kBlock - 1) / kBlock;
+    const int c0 = min(nlist, tid * perc), c1 = min(nlist, c0 + perc);
     uint32_t lu = 0, lg = 0;
-    for (int e = e0; e < e1; ++e) {
-        lu += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
-        lg += (uint32_t)groups_of_entry(seg_off, nlist, e);
-    }
+    for (int e = e0; e < e1; ++e) lu += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, e);
+    for (int c = c0; c < c1; ++c) lg += (uint32_t)groups_of_cluster(seg, c);
     uint32_t ru = 0, rg = 0;
     const uint32_t tu = block_excl_scan(lu, ru, s_wtot);
     const uint32_t tg = block_excl_scan(lg, rg, s_wtot);
     for (int e = e0; e < e1; ++e) {
         unit_off[e] = (int32_t)ru;
-        grp_off[e] = (int32_t)rg;
-        ru += (uint32_t)units_of_entry(seg_off, vec_off, nlist, e);
-        rg += (uint32_t)groups_of_entry(seg_off, nlist, e);
+        ru += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, e);
+    }
+    for (int c = c0; c < c1; ++c) {
+        grp_off[c] = (int32_t)rg;
+        rg += (uint32_t)groups_of_cluster(seg, c);
     }
     if (tid == 0) {
         unit_off[E] = (int32_t)tu;
-        grp_off[E] = (int32_t)tg;
+        grp_off[nlist] = (int32_t)tg;
     }
 }
 
-// One thread per unit: locate its segment by binary search over unit_off, then its vector slice
-// and query block.  Slices start on 64-vector blocks and are never empty (n > 64 S (S - 1)
-// whenever S = ceil(n / kSplitVec) > 1).
-// Then one thread per weight group: {first pair, pair count}.
-__global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
-                                                        const int32_t* vec_off, int nlist,
-                                                        const int32_t* unit_off, int M1,
+// Largest e in [0, n) with off[e] <= x (off non-decreasing, off[0] <= x).
+__device__ __forceinline__ int seg_search(const int32_t* off, int n, int x) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= x) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// One thread per weight group ({first pair, pair count}: kGroupQ consecutive pairs of a cluster's
+// segment), then one thread per unit: its segment by binary search over unit_off, then its
+// vector slice and query block.  Slices start on 64-vector blocks and are never empty (n > 64 S
+// (S - 1) whenever S = ceil(n / kSplitVec) > 1).
+__global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off,
+                                                        int nlist, int uqB, const int32_t* unit_off,
                                                         int4* units, int max_units,
                                                         const int32_t* grp_off, int2* groups,
                                                         int max_groups) {
-    const int E = 2 * nlist;
-    const int ngrp = min(grp_off[E], max_groups);
+    const int ngrp = min(grp_off[nlist], max_groups);
     for (int gi = blockIdx.x * blockDim.x + threadIdx.x; gi < ngrp;
          gi += gridDim.x * blockDim.x) {
-        int lo = 0, hi = E - 1;  // largest e with grp_off[e] <= gi
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (grp_off[mid] <= gi) lo = mid;
-            else hi = mid - 1;
-        }
-        const int p = lo >= nlist ? 1 : 0, c = lo - p * nlist;
-        const int32_t* so = seg_off + p * (nlist + 1);
-        const int k = gi - grp_off[lo];
-        groups[gi] = make_int2((p ? M1 : 0) + so[c] + k * kGroupQ,
-                               min(kGroupQ, so[c + 1] - so[c] - k * kGroupQ));
+        const int c = seg_search(grp_off, nlist, gi);
+        const int k = gi - grp_off[c];
+        groups[gi] = make_int2(seg[c] + k * kGroupQ, min(kGroupQ, seg[c + 1] - seg[c] - k * kGroupQ));
     }
+    const int E = 2 * nlist;
     const int total = min(unit_off[E], max_units);
     for (int u = blockIdx.x * blockDim.x + threadIdx.x; u < total; u += gridDim.x * blockDim.x) {
-        int lo = 0, hi = E - 1;  // largest e with unit_off[e] <= u
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (unit_off[mid] <= u) lo = mid;
-            else hi = mid - 1;
-        }
-        const int p = lo >= nlist ? 1 : 0, c = lo - p * nlist;
-        const int32_t* so = seg_off + p * (nlist + 1);
+        const int e = seg_search(unit_off, E, u);
+        const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
         const int n = vec_off[c + 1] - vec_off[c];
         const int S = splits_of(n);
-        const int local = u - unit_off[lo];
-        const int q = so[c + 1] - so[c];
-        const int uq = p ? kUnitQ : kUnitQ0;
+        const int local = u - unit_off[e];
+        const int q = (p ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
+        const int uq = p ? uqB : kUnitQ0;
         // slice-major: a slice's query blocks are consecutive units, so the workgroups that
         // take them together read the slice's codes while they are in the XCD's L2
         const int QB = (q + uq - 1) / uq;
@@ -179,7 +176,7 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg_off,
         const int cnt = min(uq, q - qb * uq);
         const int len = ((n + S - 1) / S + kBlkV - 1) & ~(kBlkV - 1);
         const int vb = sp * len, ve = min(n, vb + len);
-        units[u] = make_int4(c | (cnt << 20), (p ? M1 : 0) + so[c] + qb * uq, vb, ve);
+        units[u] = make_int4(c | (cnt << 20), seg[c] + qb * uq, vb, ve);
     }
 }
 
@@ -370,13 +367,13 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
     }
 }
 
-// One weight group per wave (its <= 16 pairs share a cluster), 4 lanes per pair: lane l =
-// lane % 4 of pair slot lane / 4 owns dims 64 k + 16 l + [0, 16) (16-byte loads, one 16-byte
-// store per plane and 64-dim step), so the group's scale is a wave reduction (no LDS, no
-// barrier) and the per-pair sums take two shuffle levels.  The queries' int8 weight planes
-// against the cluster's SQ8 grid and each pair's threshold-independent scalars, all in float32
-// on the float32 rotated query q32 (the bounds take q32 as the query point: e_q grows by
-// |q32 - q64| <= 2^-24 |q32| per dimension):
+// One weight group per wave (its <= 32 pairs share a cluster), 2 lanes per pair: lane l =
+// lane % 2 of pair slot lane / 2 owns dims 64 k + 32 l + [0, 32) of every 64-dim step k
+// (16-byte loads, two 16-byte stores per plane and step), so the group's scale is a wave
+// reduction (no LDS, no barrier) and the per-pair sums take one shuffle.  The queries' int8
+// weight planes against the cluster's SQ8 grid and each pair's threshold-independent scalars,
+// all in float32 on the float32 rotated query q32 (the bounds take q32 as the query point: e_q
+// grows by |q32 - q64| <= 2^-24 |q32| per dimension):
 //   w_d = delta_d * (q32_d - vmin_d) (two roundings, <= 2^-22 |w_d|, charged to err_q);  one
 //   scale for the group: s = 2^(ilogb(m) - 14), doubled if m / s > 32639, for m = the largest
 //   |w_d| of the group's pairs, so |w_int| <= 32639;  w_int = rint(w / s) = 256 hi + lo
@@ -386,14 +383,14 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
 //   acc_max = 128 (sum |w| / s + D_pad / 2) >= |sum (c - 128) w_int|
 // (per-dimension sums of the exact residuals would tighten err_q by ~2x, a 2^-16-relative
 // change of the bounds, for four more instructions per dimension).
-// (A common scale lets the lower-bound scan compare a wave's 16 queries against one integer
+// (A common scale lets the lower-bound scan compare a wave's 32 queries against one integer
 // threshold per vector.)  Plane bytes past D_pad (up to DP) are zero, so the scan may read
 // whole 64-dim steps.
 template <int KS>
 __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
-    const int lane = threadIdx.x & 63, l = lane & 3, slot = lane >> 2;
+    const int lane = threadIdx.x & 63, l = lane & 1, slot = lane >> 1;
     const int gi = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
-    if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;
+    if (gi >= min(a.grp_off[a.nlist], a.max_groups)) return;
     const int2 grp = a.groups[gi];
     const bool valid = slot < grp.y;
     const int pp = grp.x + (valid ? slot : 0);  // idle slots redo the first pair, store nothing
@@ -401,34 +398,37 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     const int D_pad = a.D_pad, DP = a.DP;
     const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
     const float* xr = a.xrot32 + (size_t)q * D_pad;
-    // Up to 256 dims the weights stay in registers between the group scale and the
+    // Up to 128 dims the weights stay in registers between the group scale and the
     // quantisation; wider, the second loop recomputes them (the same operations, so the same
     // values).
-    constexpr bool KEEP = KS <= 4;
-    float w[KEEP ? KS : 1][16];
+    constexpr bool KEEP = KS <= 2;
+    float w[KEEP ? KS : 1][32];
     float mx = 0.0f, Qp = 0.0f, qq = 0.0f, wl1 = 0.0f;
-    auto weights = [&](int k, float (&wk)[16], auto sums_c) {
+    auto weights = [&](int k, float (&wk)[32], auto sums_c) {
         constexpr bool SUMS = decltype(sums_c)::value;
-        const int d0 = 64 * k + 16 * l;  // D_pad is a multiple of 32: all 16 dims or none
 #pragma unroll
-        for (int e = 0; e < 16; ++e) wk[e] = 0.0f;
-        if (d0 < D_pad) {
+        for (int h2 = 0; h2 < 2; ++h2) {
+            const int d0 = 64 * k + 32 * l + 16 * h2;  // D_pad is a multiple of 32: all 16 or none
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const float4 x4 = *reinterpret_cast<const float4*>(xr + d0 + 4 * h);
-                const float4 v4 = *reinterpret_cast<const float4*>(a.vmin + off + d0 + 4 * h);
-                const float4 g4 = *reinterpret_cast<const float4*>(a.delta + off + d0 + 4 * h);
-                const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w},
-                            gv[4] = {g4.x, g4.y, g4.z, g4.w};
+            for (int e = 0; e < 16; ++e) wk[16 * h2 + e] = 0.0f;
+            if (d0 < D_pad) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float qp = xv[e] - vv[e];
-                    wk[4 * h + e] = gv[e] * qp;
-                    if constexpr (SUMS) {
-                        mx = fmaxf(mx, fabsf(wk[4 * h + e]));
-                        wl1 += fabsf(wk[4 * h + e]);
-                        Qp = fmaf(qp, qp, Qp);
-                        qq = fmaf(xv[e], xv[e], qq);
+                for (int h = 0; h < 4; ++h) {
+                    const float4 x4 = *reinterpret_cast<const float4*>(xr + d0 + 4 * h);
+                    const float4 v4 = *reinterpret_cast<const float4*>(a.vmin + off + d0 + 4 * h);
+                    const float4 g4 = *reinterpret_cast<const float4*>(a.delta + off + d0 + 4 * h);
+                    const float xv[4] = {x4.x, x4.y, x4.z, x4.w}, vv[4] = {v4.x, v4.y, v4.z, v4.w},
+                                gv[4] = {g4.x, g4.y, g4.z, g4.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float qp = xv[e] - vv[e];
+                        wk[16 * h2 + 4 * h + e] = gv[e] * qp;
+                        if constexpr (SUMS) {
+                            mx = fmaxf(mx, fabsf(wk[16 * h2 + 4 * h + e]));
+                            wl1 += fabsf(wk[16 * h2 + 4 * h + e]);
+                            Qp = fmaf(qp, qp, Qp);
+                            qq = fmaf(xv[e], xv[e], qq);
+                        }
                     }
                 }
             }
@@ -442,21 +442,19 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         // second loop instead of recomputing them
 #pragma unroll 1
         for (int k = 0; k < KS; ++k) {
-            float wk[16];
+            float wk[32];
             weights(k, wk, std::true_type{});
         }
     }
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, kWave));  // the group
-#pragma unroll
-    for (int o = 1; o < 4; o <<= 1) {  // the pair
-        Qp += __shfl_xor(Qp, o, kWave);
-        qq += __shfl_xor(qq, o, kWave);
-        wl1 += __shfl_xor(wl1, o, kWave);
-    }
+    // the pair's two lanes
+    Qp += __shfl_xor(Qp, 1, kWave);
+    qq += __shfl_xor(qq, 1, kWave);
+    wl1 += __shfl_xor(wl1, 1, kWave);
     float l1g = wl1;  // the group's largest sum |w|
 #pragma unroll
-    for (int o = 4; o < kWave; o <<= 1) l1g = fmaxf(l1g, __shfl_xor(l1g, o, kWave));
+    for (int o = 2; o < kWave; o <<= 1) l1g = fmaxf(l1g, __shfl_xor(l1g, o, kWave));
     // s and 1/s are powers of two in [2^-114, 2^114], so w * (1/s) is exactly w / s and
     // s * wi is exact.  Two limits: |w_int| <= 32639 (the hi / lo split), and, for every pair,
     // sum |w_int| <= sum |w| / s + D_pad / 2 <= 2^23 - 1, so that |acc| <= 128 sum |w_int| <
@@ -475,35 +473,37 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
 #pragma unroll KEEP ? KS : 1
     for (int k = 0; k < KS; ++k) {
-        float wre[16];
+        float wre[32];
         if constexpr (!KEEP) weights(k, wre, std::false_type{});
-        const float(&wk)[16] = KEEP ? w[KEEP ? k : 0] : wre;
-        uint32_t hw[4], lw[4];
+        const float(&wk)[32] = KEEP ? w[KEEP ? k : 0] : wre;
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-            int wi[4];
+        for (int h2 = 0; h2 < 2; ++h2) {
+            uint32_t hw[4], lw[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                wi[e] = (int)rintf(wk[4 * h + e] * inv_s);  // 0 for dims >= D_pad
-                wsum += wi[e];
+            for (int h = 0; h < 4; ++h) {
+                int wi[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    wi[e] = (int)rintf(wk[16 * h2 + 4 * h + e] * inv_s);  // 0 for dims >= D_pad
+                    wsum += wi[e];
+                }
+                // lo = the low byte of wi as int8, hi = (wi - lo) / 256 = the second byte of
+                // wi + 128
+                lw[h] = ((uint32_t)wi[0] & 0xffu) | (((uint32_t)wi[1] & 0xffu) << 8) |
+                        (((uint32_t)wi[2] & 0xffu) << 16) | ((uint32_t)wi[3] << 24);
+                hw[h] = (((uint32_t)(wi[0] + 128) >> 8) & 0xffu) |
+                        ((uint32_t)(wi[1] + 128) & 0xff00u) |
+                        ((((uint32_t)(wi[2] + 128) >> 8) & 0xffu) << 16) |
+                        ((uint32_t)(wi[3] + 128) >> 8 << 24);
             }
-            // lo = the low byte of wi as int8, hi = (wi - lo) / 256 = the second byte of
-            // wi + 128
-            lw[h] = ((uint32_t)wi[0] & 0xffu) | (((uint32_t)wi[1] & 0xffu) << 8) |
-                    (((uint32_t)wi[2] & 0xffu) << 16) | ((uint32_t)wi[3] << 24);
-            hw[h] = (((uint32_t)(wi[0] + 128) >> 8) & 0xffu) |
-                    ((uint32_t)(wi[1] + 128) & 0xff00u) |
-                    ((((uint32_t)(wi[2] + 128) >> 8) & 0xffu) << 16) |
-                    ((uint32_t)(wi[3] + 128) >> 8 << 24);
-        }
-        if (valid) {
-            *reinterpret_cast<uint4*>(hi_p + 64 * k + 16 * l) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-            *reinterpret_cast<uint4*>(hi_p + DP + 64 * k + 16 * l) =
-                make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            if (valid) {
+                const int b = 64 * k + 32 * l + 16 * h2;
+                *reinterpret_cast<uint4*>(hi_p + b) = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+                *reinterpret_cast<uint4*>(hi_p + DP + b) = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+            }
         }
     }
-#pragma unroll
-    for (int o = 1; o < 4; o <<= 1) wsum += __shfl_xor(wsum, o, kWave);
+    wsum += __shfl_xor(wsum, 1, kWave);
     if (valid && l == 0) {
         PairRec r;
         r.Qp = (double)Qp;
@@ -575,14 +575,17 @@ __device__ __forceinline__ void merge16_groups(float (&m)[16]) {
 // Integer lower-bound threshold of one vector for a wave: an int32 <= (A - r (r + 2 tq)) / c1
 // for the stored A (rounded down), r and tq (rounded up), computed in f32 with a margin m of
 // 2^-21 (A + y) / c1 + 1 over its three roundings (each <= 2^-24 of a term <= A + y); c1 is a
-// power of two, so the scaling is exact.  Out-of-range values saturate (a NaN from an
-// overflowed margin gives INT_MIN: every row passes); rows past the slice (r = +inf) get
-// INT_MAX, which acc + kq < 2^31 - 1 never reaches.
+// power of two, so the scaling is exact.  Out-of-range values saturate to [-2^31 + 128,
+// 2^31 - 128] (a NaN from an overflowed margin gives the lower end: every row passes); rows past
+// the slice (r = +inf) get INT_MAX.  The tested sum S = acc + kq of a real query lies in
+// [-2^31 + 128, 2^31 - 128] (|acc| <= 128 (2^23 - 1), |kq| <= 2^30), so the lower clamp never
+// rejects a row the exact threshold passes, rows past the slice never pass, and an empty query
+// row (zero weights, kq = INT_MIN) never passes either.
 __device__ __forceinline__ int lb_thr(float A, float r, float tq, float inv_c1) {
     const float y = r * fmaf(2.0f, tq, r);
     const float X = (A - y) * inv_c1;
     const float m = fmaf(0x1p-21f * (A + y), inv_c1, 1.0f);
-    const float v = fminf(fmaxf(floorf(X - m), -2147483648.0f), 2147483520.0f);
+    const float v = fminf(fmaxf(floorf(X - m), -2147483520.0f), 2147483520.0f);
     return r <= 3.0e38f ? (int)v : INT_MAX;
 }
 
@@ -605,19 +608,23 @@ __device__ __forceinline__ const void* sgpr_ptr(const void* p) {
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
     return (const void*)(size_t)(((uint64_t)hi << 32) | lo);
 }
+// Both are wave-uniform at every call; readfirstlane states it, so that the compiler keeps them in
+// SGPRs even where it cannot prove the uniformity itself.
 __device__ __forceinline__ void load_lds16(const void* base, uint32_t off, const void* lds) {
     uint32_t keep;
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr(lds));
     asm volatile(
         "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
         "global_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-        : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
+        : "=&s"(keep) : "v"(off), "s"(sgpr_ptr(base)), "s"(m) : "memory");
 }
 __device__ __forceinline__ void load_lds4(const void* base, uint32_t off, const void* lds) {
     uint32_t keep;
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)lds_addr(lds));
     asm volatile(
         "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\t"
         "global_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
-        : "=&s"(keep) : "v"(off), "s"(base), "s"(lds_addr(lds)) : "memory");
+        : "=&s"(keep) : "v"(off), "s"(sgpr_ptr(base)), "s"(m) : "memory");
 }
 
 // Vectors per LDS block of the scan kernels: 64 while D_pad <= 256 (16 KiB of codes a block),
@@ -715,10 +722,10 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int total = min(a.unit_off[a.unit_end], a.max_units);
-    const int nx = (total + 7) >> 3;
+    const int u0 = a.unit_off[a.unit_beg], u1 = min(a.unit_off[a.unit_end], a.max_units);
+    const int nx = (max(u1 - u0, 0) + 7) >> 3;
     const int xcd = (int)(blockIdx.x & 7);
-    const int rb = xcd * nx, re = min(total, rb + nx);
+    const int rb = u0 + xcd * nx, re = min(u1, rb + nx);
     int32_t* ctr = a.ctr + xcd * kCtrStride;
     const int T = a.T, G16 = a.D_pad >> 4;
 
@@ -1103,7 +1110,7 @@ template __global__ void ub_kth_kernel<128>(BatchArgs);
 // ---------------------------------------------------------------------------------------------
 // Lower-bound pass.
 //
-// lb_prep_kernel: one 16-lane group per weight group, one lane per pair, after the seeding pass.
+// lb_prep_kernel: one 32-lane group per weight group, one lane per pair, after the seeding pass.
 // For pair (q, c) with t_q = sqrt(tau_q * rot_sq_max) (1 + 1e-12) + e_q the lower-bound
 // condition is (norm form against sqrt(tau) scaled to the rotated space)
 //     A - r^2 - 2 t_q r  <=  c1 (acc + cW) + G,   G = 2 err - Q + t_q^2,  c1 = 2 s,
@@ -1121,12 +1128,13 @@ template __global__ void ub_kth_kernel<128>(BatchArgs);
 //            |kq| <= 2^30 (pair_prep_kernel keeps |acc| < 2^30, so the int32 sum cannot
 //            overflow).
 __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, slot = tid & 15;
-    const int gi = blockIdx.x * (kBlock / kGroupQ) + (tid >> 4);
+    static_assert(kGroupQ == 32, "one 32-lane half wave per weight group");
+    const int tid = threadIdx.x, lane = tid & 63, slot = tid & 31;
+    const int gi = blockIdx.x * (kBlock / kGroupQ) + (tid >> 5);
     if (a.tau_sq_out)  // the seeded thresholds, rounded up to float32, for the caller
         for (int q = blockIdx.x * kBlock + tid; q < a.B; q += gridDim.x * kBlock)
             a.tau_sq_out[q] = __double2float_ru(a.tau[q]);
-    if (gi >= min(a.grp_off[2 * a.nlist], a.max_groups)) return;  // whole 16-lane groups
+    if (gi >= min(a.grp_off[a.nlist], a.max_groups)) return;  // whole 32-lane groups
     const int2 grp = a.groups[gi];
     const bool valid = slot < grp.y;
     const int p = grp.x + (valid ? slot : 0);
@@ -1155,8 +1163,8 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
         mg = 0x1p-50 * (fabs(Kd) + (2.0 * err_q + Qp + tq * tq) / c1);
         tqf = __double2float_ru(tq);
     }
-    // group reductions over the 16 lanes of this weight group
-    const double c1_0 = shfl_f64(c1, lane & ~15);
+    // group reductions over the 32 lanes of this weight group
+    const double c1_0 = shfl_f64(c1, lane & ~31);
     int bad = valid && (!thr || c1 != c1_0);
     float tqw = valid ? tqf : 0.0f;
 #pragma unroll
@@ -1183,19 +1191,297 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
 }
 
 
-// Pass B, every probe: units and wave mapping as in batch_scan_kernel.  Block b + 1's code
-// cells and row scalars (A_lo, r) move global -> LDS directly (no staging registers) while the
-// waves scan block b; each wave on the integer test turns the row scalars into its own int32
-// thresholds.  Survivors are queued per wave in LDS and appended with one atomic per query and
-// flush.
+// Pass B, narrow layout (D_pad <= 256, 64-vector LDS blocks), every probe of a unit's cluster
+// slice.  Queries are the rows of the matrix-core product (A operand, 16 per MFMA, weights held
+// in registers) and vectors its columns (B operand, read from LDS), so a lane's four results
+// (rows 4 g + r, column j = lane & 15) share one vector and the integer test needs one int32
+// threshold per lane: max over the lane's rows of S = acc + kq against thr_x.  Each wave owns
+// 32 queries (two 16-row halves: eight MFMAs per 64-dim code fragment pair read from LDS), a
+// unit up to 128, so a slice's codes are staged once per 128 queries of the cluster.  Block
+// b + 1's code cells and row scalars (A_lo, r) move global -> LDS directly (no staging
+// registers) while the waves scan block b; each wave turns the row scalars into its own int32
+// thresholds once per block.  Survivors are queued per wave in LDS and appended with one atomic
+// per query and flush.
 template <int KS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 7 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 4 : 1)))
 void lb_scan_kernel(BatchArgs a) {
+    static_assert(KS <= 4, "narrow layout: D_pad <= 256");
+    constexpr int BV = 64;
+    constexpr int QW = 32;  // queries per wave
+    __shared__ uint4 s_codes[2][KS * 4 * BV];
+    __shared__ __align__(16) float s_A[2][BV];
+    __shared__ __align__(16) float s_r[2][BV];
+    __shared__ int s_thr[2][kWavesPerBlock][BV];
+    __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
+    __shared__ int s_scnt[kWavesPerBlock][QW], s_sbase[kWavesPerBlock][QW],
+        s_sqid[kWavesPerBlock][QW];
+    __shared__ float4 s_qf[kWavesPerBlock][QW];  // per query slot: (c1f, c2f, H32, -)
+    __shared__ int s_unit[2];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int j = lane & 15, g = lane >> 4;
+    const int u0 = a.unit_off[a.unit_beg], u1 = min(a.unit_off[a.unit_end], a.max_units);
+    const int nx = (max(u1 - u0, 0) + 7) >> 3;
+    const int xcd = (int)(blockIdx.x & 7);
+    const int rb = u0 + xcd * nx, re = min(u1, rb + nx);
+    int32_t* ctr = a.ctr + xcd * kCtrStride;
+    const int T = a.T, G16 = a.D_pad >> 4;
+    unsigned long long st_cand = 0, st_surv = 0;
+    if (lane < QW) s_scnt[wid][lane] = 0;
+
+    // Next unit's counter value: taken two blocks before the current unit ends, published in
+    // s_unit at its end (slot (it + 1) & 1, read at the start of unit it + 1; its previous read,
+    // at the start of unit it - 1, is separated from the write by the barrier at the top of
+    // unit it).  The explicit LDS wait keeps that write ahead of the barrier.
+    if (tid == 0) s_unit[0] = atomicAdd(ctr, 1);
+    for (int it = 0;; ++it) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int ui = __builtin_amdgcn_readfirstlane(s_unit[it & 1]) + rb;
+        if (ui < rb || ui >= re) break;
+        int nxt = 0;
+        const int4 un = a.units[ui];
+        const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
+        const int G = (cnt + QW - 1) / QW;  // 32-query blocks (1..4)
+        const int R = kWavesPerBlock / G;   // waves sharing a block split its tiles
+        const int gq = wid / R, rr = wid - gq * R;
+        const bool active = gq < G;
+        const int nq = active ? min(QW, cnt - gq * QW) : 0;
+        const bool two = nq > 16;           // the second half holds queries (wave-uniform)
+        const int v0 = a.vec_off[cid];
+        const int t0 = a.tile_off[cid];
+        const int pb = start + gq * QW;     // the wave's first pair: a weight group's first
+
+        // ---- this wave's queries: weight rows and the constants of lb_prep_kernel ----
+        v4i whi[2][KS], wlo[2][KS], kq4[2];
+        bool int_ok = false;
+        float tqw = 0.0f, inv_c1w = 0.0f;
+        if (active) {
+            const LbRec L0 = a.lbr[pb];
+            int_ok = __builtin_amdgcn_readfirstlane(L0.int_ok) != 0;
+            tqw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.tqw)));
+            inv_c1w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.inv_c1w)));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int qi = 16 * h + j;  // the A row this lane supplies
+                const bool hv = qi < nq;
+                const int8_t* hp = a.pw + (size_t)(pb + (hv ? qi : 0)) * 2 * a.DP + g * 16;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    const v4i vh = *reinterpret_cast<const v4i*>(hp + ks * 64);
+                    const v4i vl = *reinterpret_cast<const v4i*>(hp + a.DP + ks * 64);
+                    whi[h][ks] = hv ? vh : v4i{0, 0, 0, 0};
+                    wlo[h][ks] = hv ? vl : v4i{0, 0, 0, 0};
+                }
+                // C rows this lane receives: queries 16 h + 4 g + r (empty rows: INT_MIN)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int qr = 16 * h + 4 * g + r;
+                    kq4[h][r] = qr < nq ? (int_ok ? a.lbr[pb + qr].kq : 0) : (int_ok ? INT_MIN : 0);
+                }
+            }
+            if (lane < QW) {
+                const bool hv = lane < nq;
+                const LbRec L = a.lbr[pb + (hv ? lane : 0)];
+                s_sqid[wid][lane] = a.pair_qid[pb + (hv ? lane : 0)];
+                s_qf[wid][lane] = hv ? make_float4(L.c1f, L.c2f, L.H32, 0.0f)
+                                     : make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // never passes
+            }
+        }
+
+        // ---- survivor queue (entries li << 5 | query slot) ----
+        int nsq = 0;
+        auto flush = [&]() __attribute__((always_inline)) {
+            for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 31u], 1);
+            __builtin_amdgcn_wave_barrier();
+            if (lane < QW) {
+                const int c = s_scnt[wid][lane];
+                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[s_sqid[wid][lane]], c) : 0;
+                s_scnt[wid][lane] = 0;
+            }
+            __builtin_amdgcn_wave_barrier();
+            for (int e = lane; e < nsq; e += kWave) {
+                const uint32_t ent = s_sq[wid][e];
+                const int jj = (int)(ent & 31u);
+                const int slot = s_sbase[wid][jj] + atomicAdd(&s_scnt[wid][jj], 1);
+                if (slot < a.cap)
+                    a.cand_id[(size_t)s_sqid[wid][jj] * a.cap + slot] = v0 + (int)(ent >> 5);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane < QW) s_scnt[wid][lane] = 0;
+            if (a.stats) st_surv += (unsigned long long)nsq;
+            nsq = 0;
+        };
+
+        // ---- rare: queue the passing (query row, vector) entries of a tile; `pass(h, r)` is
+        // this lane's test of row 4 g + r of half h against its vector li ----
+        auto queue = [&](auto pass, bool has2, int li) __attribute__((always_inline)) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (h == 1 && !has2) break;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const bool ps = pass(h, r);
+                    const uint64_t pm = __ballot(ps);
+                    if (pm == 0ull) continue;
+                    if (nsq + __popcll(pm) > kLbQ) flush();
+                    if (ps) {
+                        const int idx = __builtin_amdgcn_mbcnt_hi(
+                            (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
+                        s_sq[wid][nsq + idx] = ((uint32_t)li << 5) | (uint32_t)(16 * h + 4 * g + r);
+                    }
+                    nsq += __popcll(pm);
+                }
+            }
+        };
+
+        // ---- one 16-vector tile: INT = the integer test, TWO = both halves hold queries ----
+        auto tile = [&](auto int_c, auto two_c, int buf, int t, int li0) __attribute__((always_inline)) {
+            constexpr bool INT = decltype(int_c)::value, TWO = decltype(two_c)::value;
+            const uint4* blk = s_codes[buf];
+            v4i B[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const uint4 v = blk[(ks * 4 + g) * BV + t * 16 + j];
+                B[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+            }
+            int th = 0;
+            if constexpr (INT) th = s_thr[buf][wid][t * 16 + j];
+            v4i h0 = {0, 0, 0, 0}, l0 = kq4[0], h1 = {0, 0, 0, 0}, l1 = kq4[1];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[0][ks], B[ks], h0, 0, 0, 0);
+                l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], l0, 0, 0, 0);
+                if constexpr (TWO) {
+                    h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[1][ks], B[ks], h1, 0, 0, 0);
+                    l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[1][ks], B[ks], l1, 0, 0, 0);
+                }
+            }
+            // The matrix core does not interlock VALU reads of its results: 16 wait states (plus
+            // the compiler's own padding) between the last MFMA and the first accumulator read,
+            // fenced so that the scheduler cannot move either side across.
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_nop 7\n\ts_nop 7");
+            __builtin_amdgcn_sched_barrier(0);
+            // rows 4 g + r (queries), column j (vector li0 + j): S = acc + kq, exact in int32
+            int S[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                S[0][r] = (h0[r] << 8) + l0[r];
+                S[1][r] = TWO ? (h1[r] << 8) + l1[r] : INT_MIN;
+            }
+            const int li = li0 + j;
+            if constexpr (INT) {
+                int m = max(max(S[0][0], S[0][1]), max(S[0][2], S[0][3]));
+                if constexpr (TWO) m = max(m, max(max(S[1][0], S[1][1]), max(S[1][2], S[1][3])));
+                if (__ballot(m >= th) == 0ull) return;
+                queue([&](int h, int r) __attribute__((always_inline)) { return S[h][r] >= th; }, TWO, li);
+            } else {
+                const float Av = s_A[buf][t * 16 + j], rv = s_r[buf][t * 16 + j];
+                const float P = fmaf(-rv, rv, Av);
+                const bool in = li < ve;
+                auto pass = [&](int h, int r) __attribute__((always_inline)) {
+                    const float4 c = s_qf[wid][16 * h + 4 * g + r];
+                    return in && fmaf(c.y, rv, P) <= fmaf(c.x, (float)S[h][r], c.z);
+                };
+                bool any = false;
+#pragma unroll
+                for (int h = 0; h < (TWO ? 2 : 1); ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) any |= pass(h, r);
+                if (__ballot(any) == 0ull) return;
+                queue(pass, TWO, li);
+            }
+        };
+        auto tiles = [&](auto int_c, auto two_c, int buf, int blk0) __attribute__((always_inline)) {
+            if (R == 1 && blk0 + BV <= ve) {  // the common case: straight-line tiles
+#pragma unroll
+                for (int t = 0; t < BV / 16; ++t) tile(int_c, two_c, buf, t, blk0 + t * 16);
+            } else {
+                for (int t = rr; t < BV / 16; t += R) {
+                    if (blk0 + t * 16 >= ve) break;
+                    tile(int_c, two_c, buf, t, blk0 + t * 16);
+                }
+            }
+        };
+
+        // ---- stream the slice through LDS in 64-vector blocks ----
+        const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
+        int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
+        auto gload = [&](int buf, int blk0) __attribute__((always_inline)) {
+            // block-major cells: the block's groups are consecutive runs of 64 cells
+            const uint4* base = cells_c + (size_t)ct * G16 * T + (size_t)cw * G16 + wid * BV;
+#pragma unroll
+            for (int jj = 0; jj < KS; ++jj)
+                if (wid + 4 * jj < G16)
+                    load_lds16(base + (size_t)(4 * jj) * BV, 16u * lane,
+                               &s_codes[buf][(wid + 4 * jj) * BV]);
+            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
+                const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
+                load_lds4(a.vec_Ar + v0, off, s_A[buf]);
+                load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
+            }
+            cw += BV;
+            if (cw == T) {
+                cw = 0;
+                ++ct;
+            }
+        };
+        const int nblk = (ve - vb + BV - 1) / BV;
+        if (nblk > 0) gload(0, vb);
+        for (int b = 0; b < nblk; ++b) {
+            const int buf = b & 1;
+            // this wave's direct loads of block b have landed; the barrier covers everyone's
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+            const int blk0 = vb + b * BV;
+            if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
+            if (!active) continue;
+            if (int_ok) {
+                const float A = s_A[buf][lane], r = s_r[buf][lane];
+                s_thr[buf][wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                __builtin_amdgcn_wave_barrier();
+                if (two) tiles(std::true_type{}, std::true_type{}, buf, blk0);
+                else tiles(std::true_type{}, std::false_type{}, buf, blk0);
+            } else {
+                if (two) tiles(std::false_type{}, std::true_type{}, buf, blk0);
+                else tiles(std::false_type{}, std::false_type{}, buf, blk0);
+            }
+        }
+        if (a.stats && active && rr == 0)
+            st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
+        if (nsq > 0) flush();
+        if (tid == 0) s_unit[(it + 1) & 1] = nblk > 0 ? nxt : atomicAdd(ctr, 1);
+    }
+
+    if (a.stats && lane == 0) {
+        const int slot = (int)(blockIdx.x % kStatSlots) * 4;
+        atomicAdd(&a.stats[slot + 0], st_cand);
+        atomicAdd(&a.stats[slot + 1], st_cand * (unsigned long long)(a.D_pad));
+        atomicAdd(&a.stats[slot + 2], st_surv);
+    }
+}
+
+template __global__ void lb_scan_kernel<1>(BatchArgs);
+template __global__ void lb_scan_kernel<2>(BatchArgs);
+template __global__ void lb_scan_kernel<3>(BatchArgs);
+template __global__ void lb_scan_kernel<4>(BatchArgs);
+
+// Pass B, wide layout (256 < D_pad <= 1024, one 16-vector tile per LDS block in a ring):
+// units of <= 64 queries, each wave owns 16 (the MFMA's B columns; vectors are its A rows)
+// or, when a unit holds fewer, several waves share 16 queries and split each block's 64-dim
+// steps (replicas, partial sums exchanged through LDS).  Block loads, thresholds and the
+// survivor queue as in lb_scan_kernel.
+template <int KS>
+__global__ __launch_bounds__(256) void lb_scan_wide_kernel(BatchArgs a) {
     constexpr int BV = block_vectors(KS);
+    static_assert(BV == 16, "wide layout");
     // code buffers, row scalars and replica partial sums as in ub_scan_kernel
-    constexpr int NBC = BV == 64 ? 2 : kWideAhead + 1;
+    constexpr int NBC = kWideAhead + 1;
     __shared__ uint4 s_codes[NBC][KS * 4 * BV];
-    constexpr int NAB = BV == 64 ? 2 : 8, NP = BV == 64 ? 1 : 2;
+    constexpr int NAB = 8, NP = 2;
     __shared__ __align__(16) float s_A[NAB][BV];
     __shared__ __align__(16) float s_r[NAB][BV];
     __shared__ int4 s_part[NP][NP > 1 ? kWavesPerBlock : 1][NP > 1 ? kWave : 1];
@@ -1209,10 +1495,10 @@ void lb_scan_kernel(BatchArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 15, g = lane >> 4;
-    const int total = min(a.unit_off[a.unit_end], a.max_units);
-    const int nx = (total + 7) >> 3;
+    const int u0 = a.unit_off[a.unit_beg], u1 = min(a.unit_off[a.unit_end], a.max_units);
+    const int nx = (max(u1 - u0, 0) + 7) >> 3;
     const int xcd = (int)(blockIdx.x & 7);
-    const int rb = xcd * nx, re = min(total, rb + nx);
+    const int rb = u0 + xcd * nx, re = min(u1, rb + nx);
     int32_t* ctr = a.ctr + xcd * kCtrStride;
     const int T = a.T, G16 = a.D_pad >> 4;
     unsigned long long st_cand = 0, st_surv = 0;
@@ -1250,7 +1536,7 @@ void lb_scan_kernel(BatchArgs a) {
             const int pj = start + gq * kWaveQ + (hasq ? j : 0);
             q = a.pair_qid[pj];
             const int8_t* hp = a.pw + (size_t)pj * 2 * a.DP + g * 16;
-            if (BV == 64 || R == 1) {
+            if (R == 1) {
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     bhi[ks] = *reinterpret_cast<const v4i*>(hp + ks * 64);
@@ -1307,7 +1593,7 @@ void lb_scan_kernel(BatchArgs a) {
             if (a.stats) st_surv += (unsigned long long)nsq;
             nsq = 0;
             // wide ring: the block waits count only the ring's loads, so the stores drain here
-            if constexpr (BV != 64) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         };
 
         // ---- rare: queue a tile's passes (rows row0 + r of this lane, r < 4).  The integer
@@ -1330,59 +1616,9 @@ void lb_scan_kernel(BatchArgs a) {
             }
         };
 
-        // ---- one 16-vector tile: INT = the integer test (wave-uniform mode) ----
-        auto tile = [&](auto int_c, int buf, int t, int li0) {
-            constexpr bool INT = decltype(int_c)::value;
-            const uint4* blk = s_codes[buf];
-            v4i A[KS];
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                const uint4 v = blk[(ks * 4 + g) * BV + t * 16 + j];
-                A[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-            }
-            int4 th = make_int4(0, 0, 0, 0);
-            if constexpr (INT) th = *reinterpret_cast<const int4*>(&s_thr[buf][wid][t * 16 + 4 * g]);
-            v4i acc_hi = {0, 0, 0, 0}, acc_lo = {kq, kq, kq, kq};
-#pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
-                acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
-            }
-            // The matrix core does not interlock VALU reads of its results: 16 wait states (plus
-            // the compiler's own padding) between the last MFMA and the first accumulator read,
-            // fenced so that the scheduler cannot move either side across.
-            __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_nop 7\n\ts_nop 7");
-            __builtin_amdgcn_sched_barrier(0);
-            // rows 4g + r (vectors), column j (query): S = acc + kq, exact in int32
-            int S[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
-            const int row0 = t * 16 + 4 * g;
-            uint64_t sm[4];
-            if constexpr (INT) {
-                sm[0] = __ballot(S[0] >= th.x);
-                sm[1] = __ballot(S[1] >= th.y);
-                sm[2] = __ballot(S[2] >= th.z);
-                sm[3] = __ballot(S[3] >= th.w);
-            } else {
-                const float4 A4 = *reinterpret_cast<const float4*>(&s_A[buf][row0]);
-                const float4 r4 = *reinterpret_cast<const float4*>(&s_r[buf][row0]);
-                const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
-                const float4 c = s_qf[wid][j];
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    sm[r] = __ballot(li0 + 4 * g + r < ve &&
-                                     fmaf(c.y, rv[r], fmaf(-rv[r], rv[r], Av[r])) <=
-                                         fmaf(c.x, (float)S[r], c.z));
-            }
-            if (((sm[0] | sm[1] | sm[2] | sm[3]) & qmask) == 0ull) return;
-            queue(sm, li0 + 4 * g);
-        };
-
-        // ---- wide layout (D_pad > 256), as in ub_scan_kernel: this wave's share of the
-        // 64-dim steps of the block's one tile; the replica with rr = 0 carries kq, so the
-        // partial sums add up to acc + kq ----
+        // ---- this wave's share of the 64-dim steps of the block's one tile (as in
+        // ub_scan_kernel); the replica with rr = 0 carries kq, so the partial sums add up to
+        // acc + kq ----
         auto wide_partial = [&](int buf, int (&S)[4], auto r_c) {
             constexpr int RC = decltype(r_c)::value, NS = (KS + RC - 1) / RC;
             const uint4* blk = s_codes[buf];
@@ -1443,28 +1679,13 @@ void lb_scan_kernel(BatchArgs a) {
             wide_judge(S, b & 1, abuf, vb + b * BV);
         };
 
-        // ---- stream the slice through LDS in 64-vector blocks (as batch_scan_kernel) ----
+        // ---- stream the slice through LDS in 16-vector blocks ----
         const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
         int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
         auto gload = [&](int buf, int abuf, int blk0) {
-            if constexpr (BV == 64) {
-                // block-major cells: the block's groups are consecutive runs of 64 cells
-                const uint4* base = cells_c + (size_t)ct * G16 * T + (size_t)cw * G16 + wid * BV;
-#pragma unroll
-                for (int jj = 0; jj < KS; ++jj)
-                    if (wid + 4 * jj < G16)
-                        load_lds16(base + (size_t)(4 * jj) * BV, 16u * lane,
-                                   &s_codes[buf][(wid + 4 * jj) * BV]);
-                if (wid == 0) {  // rows past the slice read the slice's last row (never used)
-                    const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
-                    load_lds4(a.vec_Ar + v0, off, s_A[abuf]);
-                    load_lds4(a.vec_Ar + v0, off + 4u, s_r[abuf]);
-                }
-            } else {
-                load_code_block16<KS>(cells_c + (size_t)ct * G16 * T + (size_t)cw * G16, G16,
-                                      wid, lane, s_codes[buf], a.vec_Ar + v0, blk0, ve - 1,
-                                      s_A[abuf], s_r[abuf]);
-            }
+            load_code_block16<KS>(cells_c + (size_t)ct * G16 * T + (size_t)cw * G16, G16, wid,
+                                  lane, s_codes[buf], a.vec_Ar + v0, blk0, ve - 1, s_A[abuf],
+                                  s_r[abuf]);
             cw += BV;
             if (cw == T) {
                 cw = 0;
@@ -1472,39 +1693,7 @@ void lb_scan_kernel(BatchArgs a) {
             }
         };
         const int nblk = (ve - vb + BV - 1) / BV;
-        if constexpr (BV == 64) {
-            if (nblk > 0) gload(0, 0, vb);
-            for (int b = 0; b < nblk; ++b) {
-                const int buf = b & 1;
-                // this wave's direct loads of block b have landed; the barrier covers everyone's
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
-                const int blk0 = vb + b * BV;
-                if (b + 1 < nblk) gload(buf ^ 1, buf ^ 1, blk0 + BV);
-                if (active) {
-                    if (int_ok) {
-                        const float A = s_A[buf][lane], r = s_r[buf][lane];
-                        s_thr[buf][wid][lane] =
-                            blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
-                        if (R == 1 && blk0 + BV <= ve) {  // the common case: straight-line tiles
-#pragma unroll
-                            for (int t = 0; t < BV / 16; ++t) tile(std::true_type{}, buf, t, blk0 + t * 16);
-                        } else {
-                            for (int t = rr; t < BV / 16; t += R) {
-                                if (blk0 + t * 16 >= ve) break;
-                                tile(std::true_type{}, buf, t, blk0 + t * 16);
-                            }
-                        }
-                    } else {
-                        for (int t = rr; t < BV / 16; t += R) {
-                            if (blk0 + t * 16 >= ve) break;
-                            tile(std::false_type{}, buf, t, blk0 + t * 16);
-                        }
-                    }
-                }
-            }
-        } else {
+        {
             // ring and replica finish as in ub_scan_kernel
             const int nload = (KS - wid + 3) / 4 + (wid == 0 ? 2 : 0);
             for (int p = 0; p < kWideAhead && p < nblk; ++p) gload(p, p, vb + p * BV);
@@ -1555,22 +1744,18 @@ void lb_scan_kernel(BatchArgs a) {
     }
 }
 
-template __global__ void lb_scan_kernel<1>(BatchArgs);
-template __global__ void lb_scan_kernel<2>(BatchArgs);
-template __global__ void lb_scan_kernel<3>(BatchArgs);
-template __global__ void lb_scan_kernel<4>(BatchArgs);
-template __global__ void lb_scan_kernel<5>(BatchArgs);
-template __global__ void lb_scan_kernel<6>(BatchArgs);
-template __global__ void lb_scan_kernel<7>(BatchArgs);
-template __global__ void lb_scan_kernel<8>(BatchArgs);
-template __global__ void lb_scan_kernel<9>(BatchArgs);
-template __global__ void lb_scan_kernel<10>(BatchArgs);
-template __global__ void lb_scan_kernel<11>(BatchArgs);
-template __global__ void lb_scan_kernel<12>(BatchArgs);
-template __global__ void lb_scan_kernel<13>(BatchArgs);
-template __global__ void lb_scan_kernel<14>(BatchArgs);
-template __global__ void lb_scan_kernel<15>(BatchArgs);
-template __global__ void lb_scan_kernel<16>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<5>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<6>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<7>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<8>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<9>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<10>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<11>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<12>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<13>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<14>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<15>(BatchArgs);
+template __global__ void lb_scan_wide_kernel<16>(BatchArgs);
 
 // tau_sq output of the batched route: the seeded float64 threshold, rounded up to float32.
 __global__ void tau_to_f32_kernel(const double* tau, float* out, int B) {

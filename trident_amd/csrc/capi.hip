@@ -120,7 +120,7 @@ struct Workspace {
     int32_t* unit_ctr;               // [2, 8 * kCtrStride] per-launch, per-XCD counters
     int64_t max_units;
     int2* groups;                    // [max_groups] batched-route weight groups
-    int32_t* grp_off;                // [2 * nlist + 1]
+    int32_t* grp_off;                // [nlist + 1]
     int64_t max_groups;
     int8_t* pw;                      // [B * nprobe, 2, DP] batched-route weight planes
     PairRec* prec;                   // [B * nprobe]
@@ -184,7 +184,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.unit_ctr = c.take<int32_t>(2 * 8 * kCtrStride);
     w.max_groups = max_groups_of(B * nprobe, ix->nlist);
     w.groups = c.take<int2>(w.max_groups);
-    w.grp_off = c.take<int32_t>(2 * (int64_t)ix->nlist + 1);
+    w.grp_off = c.take<int32_t>((int64_t)ix->nlist + 1);
     w.pw = c.take<int8_t>(B * nprobe * 2 * plane_bytes(ix->D_pad));
     w.prec = c.take<PairRec>(B * nprobe);
     w.lbr = c.take<LbRec>(B * nprobe);
@@ -333,12 +333,17 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
 }
 
 // Seeding pass: ub_scan_kernel<KS, M> (M = per-lane list length, 4 when K <= 16);
-// lower-bound pass: lb_scan_kernel<KS>.
+// lower-bound pass: lb_scan_kernel<KS> (D_pad <= 256) or lb_scan_wide_kernel<KS>.
 template <bool UB, int KS, int M>
 const void* batch_kernel_ptr() {
     if constexpr (UB) return reinterpret_cast<const void*>(&ub_scan_kernel<KS, M>);
-    else return reinterpret_cast<const void*>(&lb_scan_kernel<KS>);
+    else if constexpr (KS <= 4) return reinterpret_cast<const void*>(&lb_scan_kernel<KS>);
+    else return reinterpret_cast<const void*>(&lb_scan_wide_kernel<KS>);
 }
+
+// Queries per lower-bound unit: 128 on the narrow layout (four waves of 32), 64 on the wide
+// layout (four waves of 16).
+inline int lb_unit_q(int D_pad) { return D_pad <= 256 ? kUnitQ : kUnitQWide; }
 
 // Persistent grid of a batched-scan variant: as many workgroups as are resident at once (CUs x
 // the occupancy its registers and LDS allow), rounded to a multiple of 8 so every XCD gets the
@@ -370,9 +375,12 @@ int launch_batch_ks(const BatchArgs& b, hipStream_t st) {
         else
             ub_scan_kernel<KS, 16><<<persistent_grid<true, KS, 16>(), kBlock, 0, st>>>(b);
         return check_launch("ub_scan_kernel");
-    } else {
+    } else if constexpr (KS <= 4) {
         lb_scan_kernel<KS><<<persistent_grid<false, KS, 0>(), kBlock, 0, st>>>(b);
         return check_launch("lb_scan_kernel");
+    } else {
+        lb_scan_wide_kernel<KS><<<persistent_grid<false, KS, 0>(), kBlock, 0, st>>>(b);
+        return check_launch("lb_scan_wide_kernel");
     }
 }
 
@@ -393,7 +401,7 @@ bool with_ks(int ks, F&& f) {
 
 int launch_pair_prep(const BatchArgs& b, hipStream_t st) {
     if (b.M <= 0) return TRIDENT_OK;
-    static_assert(kGroupQ * 4 == kWave, "one weight group per wave, 4 lanes a pair");
+    static_assert(kGroupQ * 2 == kWave, "one weight group per wave, 2 lanes a pair");
     // one group per wave; waves past the group count return
     const unsigned grid = (unsigned)((b.max_groups + kWavesPerBlock - 1) / kWavesPerBlock);
     const bool ok = with_ks(b.DP / 64, [&](auto ks_c) {
@@ -553,15 +561,24 @@ int launch_scatter_pairs(const int32_t* probe_cids, const float* probe_dqcs, int
     return check_launch("scatter_pairs_kernel");
 }
 
+// joint = false: each pass's pairs grouped by cluster in its own array (p1*, p2*), seg_off =
+// [2, nlist + 1] per-pass segment offsets (the per-pair route).  joint = true: one cluster-major
+// array (p1* and p2* the same array), each cluster's pass-1 pairs before its pass-2 pairs,
+// seg_off rows = cluster starts and pass-2 starts (the batched route).
 int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int B, int nprobe,
                 int p_init, int nlist, int32_t* counts, int32_t* seg_off, int32_t* cursor,
                 int32_t* p1c, int32_t* p1q, float* p1d, int32_t* p2c, int32_t* p2q, float* p2d,
-                hipStream_t st) {
+                bool joint, hipStream_t st) {
     int rc = fill(counts, 0, 2 * ((int64_t)nlist + 1), st);
     if (rc) return rc;
     if ((rc = launch_count_pairs(probe_cids, ld, B, nprobe, p_init, nlist, counts, st))) return rc;
-    scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
-    if ((rc = check_launch("scan_pairs_kernel"))) return rc;
+    if (joint) {
+        scan_pairs_joint_kernel<<<1, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
+        if ((rc = check_launch("scan_pairs_joint_kernel"))) return rc;
+    } else {
+        scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
+        if ((rc = check_launch("scan_pairs_kernel"))) return rc;
+    }
     return launch_scatter_pairs(probe_cids, probe_dqcs, ld, B, nprobe, p_init, nlist, cursor, p1c,
                                 p1q, p1d, p2c, p2q, p2d, st);
 }
@@ -698,13 +715,18 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         return rc;
     if ((rc = mark(TRIDENT_EV_PROBED))) return rc;
 
+    int route = TRIDENT_ROUTE_PAIR;
+    if (cascade && (rc = choose_route(ix, sp, B, K, nprobe, &route))) return rc;
+    const bool batched = route == TRIDENT_ROUTE_BATCHED;
     const int64_t M1 = (int64_t)B * p_init, M2 = (int64_t)B * (nprobe - p_init);
+    // per-pair route: the two passes' pairs in consecutive arrays; batched: one cluster-major
+    // array (group_pairs)
     int32_t *p1c = w.pair_cids, *p1q = w.pair_qids;
     float* p1d = w.pair_dqcs;
-    int32_t *p2c = w.pair_cids + M1, *p2q = w.pair_qids + M1;
-    float* p2d = w.pair_dqcs + M1;
+    int32_t *p2c = batched ? p1c : w.pair_cids + M1, *p2q = batched ? p1q : w.pair_qids + M1;
+    float* p2d = batched ? p1d : w.pair_dqcs + M1;
     if ((rc = group_pairs(pc, pd, ld, B, nprobe, p_init, ix->nlist, w.counts, w.seg_off, w.cursor,
-                          p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, st)))
+                          p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, batched, st)))
         return rc;
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
@@ -727,9 +749,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     m.list_id = w.list_id;
     m.tau64 = w.tau64;
 
-    int route = TRIDENT_ROUTE_PAIR;
-    if (cascade && (rc = choose_route(ix, sp, B, K, nprobe, &route))) return rc;
-    if (route == TRIDENT_ROUTE_BATCHED) {
+    if (batched) {
         BatchArgs b{};
         b.cells = reinterpret_cast<const uint4*>(ix->sq8_cells);
         b.tile_oids = ix->tile_orig_ids;
@@ -772,7 +792,9 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.max_units = (int)w.max_units;
         b.pair_qid = w.pair_qids;
         b.pair_cid = w.pair_cids;
+        b.seg = w.seg_off;
         b.M = (int)(M1 + M2);
+        b.unit_q = lb_unit_q(ix->D_pad);
         b.DP = (int)plane_bytes(ix->D_pad);
         b.pw = w.pw;
         b.prec = w.prec;
@@ -790,15 +812,16 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                             kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep, w.unit_ctr);
         if ((rc = check_launch("aux_bounds_kernel"))) return rc;
         unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
-                                               w.unit_off, w.grp_off);
+                                               b.unit_q, w.unit_off, w.grp_off);
         if ((rc = check_launch("unit_scan_kernel"))) return rc;
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
-                           st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, w.unit_off, (int)M1,
+                           st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, w.unit_off,
                                  w.units, (int)w.max_units, w.grp_off, w.groups,
                                  (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if ((rc = launch_pair_prep(b, st))) return rc;
         if (M1 > 0) {  // pass A: per-query upper-bound threshold from the first p_init probes
+            b.unit_beg = 0;
             b.unit_end = ix->nlist;
             b.ctr = w.unit_ctr;
             if ((rc = launch_batch<true>(b, st))) return rc;
@@ -819,6 +842,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         if ((rc = check_launch("lb_prep_kernel"))) return rc;
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
         // pass B over every probe: lower bound, exact refine, append <= tau
+        b.unit_beg = ix->nlist;
         b.unit_end = 2 * ix->nlist;
         b.ctr = w.unit_ctr + 8 * kCtrStride;
         if ((rc = launch_batch<false>(b, st))) return rc;

@@ -398,6 +398,33 @@ __global__ __launch_bounds__(256) void scan_pairs_kernel(const int32_t* counts, 
     }
 }
 
+// grid 1, block 256: the cluster-major layout (each cluster's pass-1 pairs, then its pass-2
+// pairs) from counts [2, nlist + 1]: seg_off row 0 = cluster starts, row 1 = pass-2 starts; the
+// cursor rows are the same offsets, so the scatter kernels place pass p's pair of cluster c at
+// cursor[p][c]++ in one array.
+__global__ __launch_bounds__(256) void scan_pairs_joint_kernel(const int32_t* counts, int nlist,
+                                                               int32_t* seg_off, int32_t* cursor) {
+    __shared__ uint32_t s_wtot[kWavesPerBlock];
+    const int tid = threadIdx.x;
+    const int32_t *c1 = counts, *c2 = counts + (nlist + 1);
+    const int chunk = (nlist + kBlock - 1) / kBlock;
+    const int a0 = min(nlist, tid * chunk), a1 = min(nlist, a0 + chunk);
+    uint32_t local = 0;
+    for (int c = a0; c < a1; ++c) local += (uint32_t)(c1[c] + c2[c]);
+    uint32_t total = 0;
+    uint32_t run = block_exclusive_scan(local, s_wtot, &total);
+    for (int c = a0; c < a1; ++c) {
+        const uint32_t n1 = (uint32_t)c1[c];
+        seg_off[c] = cursor[c] = (int32_t)run;
+        seg_off[nlist + 1 + c] = cursor[nlist + 1 + c] = (int32_t)(run + n1);
+        run += n1 + (uint32_t)c2[c];
+    }
+    if (tid == 0) {
+        seg_off[nlist] = cursor[nlist] = (int32_t)total;
+        seg_off[2 * nlist + 1] = cursor[2 * nlist + 1] = (int32_t)total;
+    }
+}
+
 __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      const float* __restrict__ probe_dqcs, int ld, int B,
                                      int nprobe, int p_init, int nlist, int32_t* cursor,

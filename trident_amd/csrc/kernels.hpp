@@ -108,16 +108,21 @@ struct BatchArgs {
     const float* xrot32;        // [B, D_pad] xrot64 rounded to float32
     const double* qerr;         // [B, D_pad]
     const int4* units;          // work units {cid | cnt << 20, pair start, v_begin, v_end}
-    const int32_t* unit_off;    // [2 * nlist + 1] unit offsets of the (pass, cluster) segments
-    int unit_end;               // this launch covers units [0, unit_off[unit_end])
+    const int32_t* unit_off;    // [2 * nlist + 1] unit offsets: seeding units of cluster c at
+                                // [unit_off[c], unit_off[c + 1]), lower-bound units of cluster c
+                                // at [unit_off[nlist + c], unit_off[nlist + c + 1])
+    int unit_beg, unit_end;     // this launch covers units [unit_off[unit_beg], unit_off[unit_end])
     int max_units;
     int32_t* ctr;               // [8 * kCtrStride] per-XCD work counters, zero at launch
-    const int32_t* pair_qid;    // pass-1 pairs then pass-2 pairs
-    const int32_t* pair_cid;
+    const int32_t* pair_qid;    // the pairs grouped by cluster, each cluster's seeding (pass-1)
+    const int32_t* pair_cid;    // pairs first: cluster c at [seg[c], seg[c + 1]), its seeding
+                                // pairs at [seg[c], seg[nlist + 1 + c])
+    const int32_t* seg;         // [2, nlist + 1] cluster starts, seeding ends
     int M;                      // pairs (both passes)
     int nlist;
+    int unit_q;                 // queries per lower-bound unit (kUnitQ or kUnitQWide)
     const int2* groups;        // weight groups {first pair, pair count}
-    const int32_t* grp_off;     // [2 * nlist + 1]; grp_off[2 * nlist] = number of groups
+    const int32_t* grp_off;     // [nlist + 1]; grp_off[nlist] = number of groups
     int max_groups;
     int DP;                     // 64 * ceil(D_pad / 64): bytes per weight plane
     int8_t* pw;                 // [M, 2, DP] int8 weight planes (hi, lo), natural dim order
@@ -175,6 +180,12 @@ __global__ void count_pairs_kernel(const int32_t* __restrict__ probe_cids, int l
 
 __global__ void scan_pairs_kernel(const int32_t* counts, int nlist, int32_t* seg_off,
                                   int32_t* cursor);
+
+// grid 1: the cluster-major layout of the batched route, each cluster's pass-1 pairs followed
+// by its pass-2 pairs: seg_off[c] = the cluster's first pair, seg_off[nlist + 1 + c] = its first
+// pass-2 pair (both rows end with M); cursor receives the two rows for the scatter.
+__global__ void scan_pairs_joint_kernel(const int32_t* counts, int nlist, int32_t* seg_off,
+                                        int32_t* cursor);
 
 __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      const float* __restrict__ probe_dqcs, int ld, int B,
@@ -236,20 +247,24 @@ __global__ void pair_scan_kernel(ScanArgs a);
 template <int KP>
 __global__ void merge_kernel(MergeArgs a);
 
-// Batched-route work units: <= 64 queries of one cluster x one slice of ~kSplitVec vectors
-// (at most kMaxSplit slices per cluster); units of the seeding pass hold <= 16 queries.  Pass p
-// with M_p pairs has at most kMaxSplit * sum_c ceil(q_c / uq_p) <= kMaxSplit * (M_p / uq_p +
-// nlist) units, so both passes together stay within kMaxSplit * (ceil(M / 16) + 2 nlist) for
-// M = M_1 + M_2 pairs, whatever the split (max_units_of).
-constexpr int kUnitQ = 64;
+// Batched-route work units: queries of one cluster x one slice of ~kSplitVec vectors (at most
+// kMaxSplit slices per cluster).  Seeding units hold <= 16 of the cluster's pass-1 queries;
+// lower-bound units hold <= kUnitQ (D_pad <= 256) or kUnitQWide of all its queries, both passes
+// together, so a slice is read once per 128 (64) queries.  With q_c queries in cluster c,
+// sum_c ceil(q_c / uq) <= M / uq + nlist, so a launch pair has at most kMaxSplit * (ceil(M_1 /
+// 16) + ceil(M / 64) + 2 nlist) <= max_units_of(M) units for M = M_1 + M_2 pairs, whatever
+// the split.
+constexpr int kUnitQ = 128;
+constexpr int kUnitQWide = 64;
 constexpr int kUnitQ0 = 16;
 constexpr int kSplitVec = 1024;
 constexpr int kMaxSplit = 8;
 constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
 
-// Weight groups: the 16 consecutive pairs of a segment that one wave scans together share one
-// weight scale (pairs 16 k .. 16 k + 15 of the segment; units start on such boundaries).
-constexpr int kGroupQ = 16;
+// Weight groups: the 32 consecutive pairs of a cluster's segment that one lower-bound wave
+// scans together share one weight scale (pairs 32 k .. 32 k + 31 of the segment; units start
+// on such boundaries, seeding waves of 16 queries use half a group).
+constexpr int kGroupQ = 32;
 // Relative error bound of the batched route's per-pair float32 sums over D_pad terms (Q = sum
 // (q - vmin)^2, sum |w|, |q|^2): n - 1 additions in any order, each rounding by <= 2^-24 of a
 // partial sum of non-negative terms, give (n - 1) 2^-24 (1 + n 2^-24); the rounded difference
@@ -264,18 +279,19 @@ constexpr int kSurvQ = 512;
 // smaller units (16 queries) for every pair, since the split between the passes (p_init) is a
 // search parameter that the workspace size does not know.
 inline int64_t max_units_of(int64_t pairs, int64_t nlist) {
-    return (int64_t)kMaxSplit * ((pairs + kUnitQ0 - 1) / kUnitQ0 + 2 * nlist);
+    return (int64_t)kMaxSplit *
+           ((pairs + kUnitQ0 - 1) / kUnitQ0 + (pairs + kUnitQWide - 1) / kUnitQWide + 2 * nlist);
 }
 
 inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
-    return (pairs + kGroupQ - 1) / kGroupQ + 2 * nlist;
+    return (pairs + kGroupQ - 1) / kGroupQ + nlist;
 }
 
-__global__ void unit_scan_kernel(const int32_t* seg_off, const int32_t* vec_off, int nlist,
+__global__ void unit_scan_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
                                  int32_t* unit_off, int32_t* grp_off);
 
-__global__ void unit_fill_kernel(const int32_t* seg_off, const int32_t* vec_off, int nlist,
-                                 const int32_t* unit_off, int M1, int4* units, int max_units,
+__global__ void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
+                                 const int32_t* unit_off, int4* units, int max_units,
                                  const int32_t* grp_off, int2* groups, int max_groups);
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
@@ -301,7 +317,10 @@ __host__ __device__ constexpr int ub_per_unit(int K) { return K < 64 ? K : 64; }
 inline int64_t ub_cap_of(int64_t K) { return 3 * kMaxSplit * (int64_t)ub_per_unit((int)K); }
 
 template <int KS>
-__global__ void lb_scan_kernel(BatchArgs a);
+__global__ void lb_scan_kernel(BatchArgs a);       // KS <= 4 (D_pad <= 256)
+
+template <int KS>
+__global__ void lb_scan_wide_kernel(BatchArgs a);  // 4 < KS <= 16
 
 template <bool HOST, int DQ>
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
