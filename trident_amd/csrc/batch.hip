@@ -64,12 +64,13 @@ __device__ __forceinline__ int splits_of(int n) {
     return min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec);
 }
 
-// Entry e < nlist: the seeding units of cluster e (its pass-1 queries, <= 16 per unit); entry
-// nlist + c: the lower-bound units of cluster c (all its queries, <= uqB per unit).
+// Entry e < nlist: the seeding units of cluster e (its pass-1 queries, or all of them when
+// seed_all, <= 16 per unit); entry nlist + c: the lower-bound units of cluster c (all its
+// queries, <= uqB per unit).
 __device__ __forceinline__ int units_of_entry(const int32_t* seg, const int32_t* vec_off,
-                                              int nlist, int uqB, int e) {
+                                              int nlist, int uqB, int seed_all, int e) {
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
-    const int q = (p ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
+    const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
     const int uq = p ? uqB : kUnitQ0;
     return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c]) : 0;
 }
@@ -103,8 +104,8 @@ __device__ __forceinline__ uint32_t block_excl_scan(uint32_t local, uint32_t& ru
 // grid 1: exclusive scans of the unit counts of the 2 * nlist (pass, cluster) entries and of
 // the weight-group counts of the nlist cluster segments.
 __global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg, const int32_t* vec_off,
-                                                        int nlist, int uqB, int32_t* unit_off,
-                                                        int32_t* grp_off) {
+                                                        int nlist, int uqB, int seed_all,
+                                                        int32_t* unit_off, int32_t* grp_off) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
     const int tid = threadIdx.x;
     const int E = 2 * nlist;
@@ -113,14 +114,15 @@ __global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg, cons
     const int perc = (nlist + kBlock - 1) / kBlock;
     const int c0 = min(nlist, tid * perc), c1 = min(nlist, c0 + perc);
     uint32_t lu = 0, lg = 0;
-    for (int e = e0; e < e1; ++e) lu += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, e);
+    for (int e = e0; e < e1; ++e)
+        lu += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, e);
     for (int c = c0; c < c1; ++c) lg += (uint32_t)groups_of_cluster(seg, c);
     uint32_t ru = 0, rg = 0;
     const uint32_t tu = block_excl_scan(lu, ru, s_wtot);
     const uint32_t tg = block_excl_scan(lg, rg, s_wtot);
     for (int e = e0; e < e1; ++e) {
         unit_off[e] = (int32_t)ru;
-        ru += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, e);
+        ru += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, e);
     }
     for (int c = c0; c < c1; ++c) {
         grp_off[c] = (int32_t)rg;
@@ -148,7 +150,8 @@ __device__ __forceinline__ int seg_search(const int32_t* off, int n, int x) {
 // vector slice and query block.  Slices start on 64-vector blocks and are never empty (n > 64 S
 // (S - 1) whenever S = ceil(n / kSplitVec) > 1).
 __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off,
-                                                        int nlist, int uqB, const int32_t* unit_off,
+                                                        int nlist, int uqB, int seed_all,
+                                                        const int32_t* unit_off,
                                                         int4* units, int max_units,
                                                         const int32_t* grp_off, int2* groups,
                                                         int max_groups) {
@@ -167,7 +170,7 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, cons
         const int n = vec_off[c + 1] - vec_off[c];
         const int S = splits_of(n);
         const int local = u - unit_off[e];
-        const int q = (p ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
+        const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
         const int uq = p ? uqB : kUnitQ0;
         // slice-major: a slice's query blocks are consecutive units, so the workgroups that
         // take them together read the slice's codes while they are in the XCD's L2
@@ -193,21 +196,23 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
-// Exact test of the listed survivors, in place: slot s of query q holds a sorted position on
-// entry and (key, original id) on exit, or (kKeyInvalid, kIdInvalid) when the canonical
-// float64 distance exceeds tau[q].  One wave per (query, 64-slot chunk of its list), one
-// survivor per lane (a query with many survivors spreads over many waves); each lane walks its
-// own row in dimension order with 16-byte loads, against the query row staged in LDS (DQ >= D
-// floats per wave: 256, or 1024 for the wide batched route).  An overflowed list
-// (count > cap) is left alone: the merge rescans that query's probes exhaustively.
+// Exact test of the listed survivors, in place: slot s >= seed_cnt[q] of query q holds a sorted
+// position on entry and (key, original id) on exit, or (kKeyInvalid, kIdInvalid) when the
+// canonical float64 distance exceeds tau[q] or the row is one of the query's seeds (slots
+// [0, seed_cnt), refined by ub_kth_kernel: their rows are not read again).  One wave per
+// (query, 64-slot chunk of its list), one survivor per lane (a query with many survivors
+// spreads over many waves); each lane walks its own row in dimension order with 16-byte loads,
+// against the query row staged in LDS (DQ >= D floats per wave: 256, or 1024 for the wide
+// batched route).  An overflowed list (count > cap) is left alone: the merge rescans that
+// query's probes exhaustively.
 template <bool HOST, int DQ>
 __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int B) {
     __shared__ __align__(16) float s_q[kWavesPerBlock][HOST ? 1 : DQ];  // host: float64 copy below
     const int lane = threadIdx.x & 63, wid = (int)(threadIdx.x >> 6);
     const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + wid);
     if (q >= B) return;
-    const int cnt = a.cand_cnt[q];
-    if (cnt > a.cap || (int)blockIdx.y * kWave >= cnt) return;
+    const int cnt = a.cand_cnt[q], ns = a.seed_cnt[q];
+    if (cnt > a.cap || ns + (int)blockIdx.y * kWave >= cnt) return;
     const double tau = a.tau[q];
     const int D = a.D;  // <= DQ (the launch picks DQ from D)
     if constexpr (!HOST) {
@@ -217,35 +222,57 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
     const float* qr = s_q[wid];
     uint64_t* ck = a.cand_key + (size_t)q * a.cap;
     int32_t* ci = a.cand_id + (size_t)q * a.cap;
+    // the seeds' original ids: lane k holds seed k (and seed 64 + k)
+    const int so0 = lane < ns ? ci[lane] : -1, so1 = lane + kWave < ns ? ci[kWave + lane] : -1;
+    auto is_seed = [&](int oid) {
+        bool hit = false;
+        for (int k = 0; k < min(ns, kWave); ++k) hit |= oid == __builtin_amdgcn_readlane(so0, k);
+        for (int k = kWave; k < ns; ++k) hit |= oid == __builtin_amdgcn_readlane(so1, k - kWave);
+        return hit;
+    };
     const bool vec4 = (D & 3) == 0 && (reinterpret_cast<uintptr_t>(a.xb) & 15) == 0;
     unsigned long long ins = 0;
     if constexpr (HOST) {
         // base in mapped host memory: rows cross PCIe, so they are read as 128-byte row
-        // segments (all of a 32-dim chunk's loads in flight) and staged through LDS
+        // segments (all of a 32-dim chunk's loads in flight) and staged through LDS; seed rows
+        // are left out of the chunk
         __shared__ int32_t s_pos[kWavesPerBlock][kWave];
         __shared__ double s_q64[kWavesPerBlock][DQ];
         __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
         for (int d = lane; d < D; d += kWave) s_q64[wid][d] = (double)a.xq[(size_t)q * D + d];
-        for (int s0 = (int)blockIdx.y * kWave; s0 < cnt; s0 += kWave * (int)gridDim.y) {
-            const int s = s0 + lane, n = min(kWave, cnt - s0);
-            const int pos = s < cnt ? ci[s] : 0;
-            s_pos[wid][lane] = pos;
+        for (int s0 = ns + (int)blockIdx.y * kWave; s0 < cnt; s0 += kWave * (int)gridDim.y) {
+            const int s = s0 + lane;
+            const bool in = s < cnt;
+            const int pos = in ? ci[s] : 0;
+            const int oid = in ? a.orig_ids[pos] : -1;
+            const bool need = in && !(ns > 0 && is_seed(oid));
+            const uint64_t m = __ballot(need);
+            const int nq = __popcll(m), rk = need ? mask_rank(m) : 0;
+            if (need) s_pos[wid][rk] = pos;
             wave_sync();
-            const double acc = refine_rows_mlp(a.xb, D, s_pos[wid], n, s_stage[wid], s_q64[wid]);
+            double acc = 0.0;
+            if (nq > 0) acc = refine_rows_mlp(a.xb, D, s_pos[wid], nq, s_stage[wid], s_q64[wid]);
             wave_sync();
-            if (s < cnt) {
-                const bool ok = acc <= tau;
-                ck[s] = ok ? key_of(acc) : kKeyInvalid;
-                ci[s] = ok ? a.orig_ids[pos] : kIdInvalid;
-                if (a.stats) ins += __popcll(__ballot(ok));
+            const double d = shfl_f64(acc, rk);
+            const bool ok = need && d <= tau;
+            if (in) {
+                ck[s] = ok ? key_of(d) : kKeyInvalid;
+                ci[s] = ok ? oid : kIdInvalid;
             }
+            if (a.stats) ins += __popcll(__ballot(ok));
         }
         if (a.stats && lane == 0 && ins)
             atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
         return;
     }
-    for (int s = (int)blockIdx.y * kWave + lane; s < cnt; s += kWave * (int)gridDim.y) {
+    for (int s = ns + (int)blockIdx.y * kWave + lane; s < cnt; s += kWave * (int)gridDim.y) {
         const int pos = ci[s];
+        const int oid = a.orig_ids[pos];
+        if (ns > 0 && is_seed(oid)) {
+            ck[s] = kKeyInvalid;
+            ci[s] = kIdInvalid;
+            continue;
+        }
         const float* xr = a.xb + (size_t)pos * D;
         double acc = 0.0;
         if (vec4) {
@@ -280,11 +307,14 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
         }
         const bool ok = acc <= tau;
         ck[s] = ok ? key_of(acc) : kKeyInvalid;
-        ci[s] = ok ? a.orig_ids[pos] : kIdInvalid;
-        if (a.stats) ins += __popcll(__ballot(ok));  // lane 0 is active in every round
+        ci[s] = ok ? oid : kIdInvalid;
+        if (a.stats) ins += (unsigned long long)ok;
     }
-    if (a.stats && lane == 0 && ins)
-        atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
+    if (a.stats) {
+#pragma unroll
+        for (int o = 1; o < kWave; o <<= 1) ins += __shfl_xor(ins, o, kWave);
+        if (lane == 0 && ins) atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], ins);
+    }
 }
 
 template __global__ void refine_survivors_kernel<false, 256>(BatchArgs, int);
@@ -363,6 +393,8 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
             a.tau[q] = INFINITY;
             a.cand_cnt[q] = 0;
             a.ub_cnt[q] = 0;
+            a.ub_best[q] = 0x7f800000u;  // +inf
+            a.seed_cnt[q] = 0;
         }
     }
 }
@@ -680,6 +712,21 @@ __device__ __forceinline__ void load_code_block16(const uint4* block_cells, int 
     }
 }
 
+// A seeding bound with its row (index in the unit's slice) in the low 16 bits: rounded up to a
+// multiple of 2^16 in the bit pattern first, so it stays an upper bound (at most 2^-7 larger);
+// rows past 2^16 - 2 of a slice carry kNoRow.  Non-finite and huge bounds become +inf.
+__device__ __forceinline__ float enc_row(float u, int idx) {
+    const uint32_t b = __float_as_uint(u);
+    if (!(b < 0x7f7f0000u)) return INFINITY;
+    const uint32_t r = idx < (int)kNoRow ? (uint32_t)idx : kNoRow;
+    return __uint_as_float(((b + 0x10000u) & 0xffff0000u) | r);
+}
+// The list entry of an encoded bound: (bits, sorted position or -1).
+__device__ __forceinline__ uint2 row_entry(float u, int row0) {
+    const uint32_t b = __float_as_uint(u), r = b & 0xffffu;
+    return make_uint2(b, (u < INFINITY && r != kNoRow) ? (uint32_t)(row0 + (int)r) : 0xffffffffu);
+}
+
 // Pass A (seeding), the first p_init probes: for every query of a unit the K-th smallest upper
 // bound over the cluster -> atomicMin into tau[q] (float64 bit pattern).  Units (<= 16
 // queries, whole clusters) and wave mapping as in lb_scan_kernel; block b + 1's code cells and
@@ -819,7 +866,7 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 const float E = fmaf(nc1, (float)S, Cq) + Av[r] * (1.0f + 0x1p-21f);
                 float u = fmaf(__builtin_amdgcn_sqrtf(fmaxf(E, 0x1p-126f)), 1.0f + 0x1p-20f,
                                rv[r] + e_q) * (1.0f + 0x1p-21f);
-                if (li0 + 4 * g + r >= ve) u = INFINITY;  // rows past the slice
+                u = li0 + 4 * g + r < ve ? enc_row(u, li0 + 4 * g + r - vb) : INFINITY;
                 // sorted insertion (selects, not fminf: no NaN here, and no canonicalisation)
                 if constexpr (M <= 4) {
 #pragma unroll
@@ -873,7 +920,7 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 const float E = fmaf(nc1, (float)S[r], Cq) + Av[r] * (1.0f + 0x1p-21f);
                 float u = fmaf(__builtin_amdgcn_sqrtf(fmaxf(E, 0x1p-126f)), 1.0f + 0x1p-20f,
                                rv[r] + e_q) * (1.0f + 0x1p-21f);
-                if (li0 + 4 * g + r >= ve) u = INFINITY;
+                u = li0 + 4 * g + r < ve ? enc_row(u, li0 + 4 * g + r - vb) : INFINITY;
                 if (u < ubl[M - 1]) {
 #pragma unroll
                     for (int i = M - 1; i > 0; --i)
@@ -1004,12 +1051,19 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 }
             }
             if (active && rr == 0 && g == 0 && hasq) {
-                // the unit's K smallest kept bounds (K distinct rows) join the query's list
+                // the unit's K smallest kept bounds (K distinct rows) join the query's list; a
+                // unit that no longer fits offers its K-th bound instead
                 const int base = atomicAdd(&a.ub_cnt[q], a.K);
-                float* dst = a.ub_list + (size_t)q * a.ub_cap;
+                uint2* dst = a.ub_list + (size_t)q * a.ub_cap;
+                const int row0 = a.vec_off[cid] + vb;
+                float uk = INFINITY;
 #pragma unroll
-                for (int i = 0; i < kUbList; ++i)
-                    if (i < a.K && base + i < a.ub_cap) dst[base + i] = ubl[i];
+                for (int i = 0; i < kUbList; ++i) {
+                    if (i < a.K && base + i < a.ub_cap) dst[base + i] = row_entry(ubl[i], row0);
+                    if (i == a.K - 1) uk = ubl[i];
+                }
+                if (base + a.K > a.ub_cap && uk < INFINITY)
+                    atomicMin(&a.ub_best[q], __float_as_uint(uk));
             }
         } else {
             if (active) {
@@ -1031,9 +1085,13 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                     int base = 0;
                     if (lane == 0) base = atomicAdd(&a.ub_cnt[qq], nl);
                     base = __shfl(base, 0, kWave);
+                    const float uv = L.k0 == kKeyInvalid ? INFINITY : (float)dist_of(L.k0);
                     if (lane < nl && base + lane < a.ub_cap)
                         a.ub_list[(size_t)qq * a.ub_cap + base + lane] =
-                            L.k0 == kKeyInvalid ? INFINITY : (float)dist_of(L.k0);
+                            row_entry(uv, a.vec_off[cid] + vb);
+                    // K <= 64: the unit's own K-th bound, when its entries did not fit
+                    if (a.K <= 64 && lane == a.K - 1 && base + nl > a.ub_cap && uv < INFINITY)
+                        atomicMin(&a.ub_best[qq], __float_as_uint(uv));
                 }
             }
         }
@@ -1075,37 +1133,100 @@ template __global__ void ub_scan_kernel<14, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<15, 16>(BatchArgs);
 template __global__ void ub_scan_kernel<16, 16>(BatchArgs);
 
-// Seeding threshold, one wave per query: tau[q] = the K-th smallest bound u of its list (each
-// seeding unit's min(K, 64) smallest, all of distinct rows, so K rows have distance <= that u;
-// KP >= K entries are kept while selecting),
-// squared and mapped back through the rotation (u^2 / sigma_min^2, margin 1e-6 as the
-// reference's Stage X).  Fewer than K listed bounds leave tau = +inf.  A list longer than
-// ub_cap keeps its first ub_cap entries: the K-th smallest of a subset is still a bound.
-template <int KP>
+// Seeding threshold, one wave per query.  Its list holds each seeding unit's min(K, 64) smallest
+// bounds u with their rows (all distinct rows); the K smallest (u, position) entries are the
+// query's seeds:
+//   tau_ub = the K-th smallest u (K rows have distance <= it), also over ub_best (a unit's own
+//            K-th bound when the list was full), squared and mapped back through the rotation
+//            (u^2 / sigma_min^2, margin 1e-6 as the reference's Stage X);
+//   tau_x  = the largest canonical float64 distance of the K seeds, each refined here (K distinct
+//            rows have distance <= it; never above tau_ub of the same K rows);
+//   tau    = min(tau_ub, tau_x).
+// The seeds with distance <= tau become the query's first candidates, already refined
+// (seed_cnt); the refine of the lower-bound pass skips them.  A query with fewer than K listed
+// bounds, or a seed without a recorded row, keeps tau_ub (+inf without bounds) and no seeds.
+// A list longer than ub_cap keeps its first ub_cap entries: the K-th smallest of a subset is
+// still a bound.
+template <int KP, int DQ>
 __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6));
+    __shared__ double s_q64[kWavesPerBlock][DQ];
+    __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
+    __shared__ int32_t s_pos[kWavesPerBlock][KP];
+    const int lane = threadIdx.x & 63, wid = (int)(threadIdx.x >> 6);
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + wid);
     if (q >= a.B) return;
-    const int n = min(a.ub_cnt[q], a.ub_cap);
-    if (n < a.K) return;
-    const float* lst = a.ub_list + (size_t)q * a.ub_cap;
-    WaveList<KP> L;
-    L.init();
-    for (int i0 = 0; i0 < n; i0 += kWave) {
-        const int i = i0 + lane;
-        L.insert(i < n ? key_of((double)lst[i]) : kKeyInvalid, i < n ? i : kIdInvalid);
+    const int K = a.K, n = min(a.ub_cnt[q], a.ub_cap);
+    const float ubest = __uint_as_float(a.ub_best[q]);
+    double tau = ubest < INFINITY ? (double)ubest * ubest / a.rot_sq_min * (1.0 + 1e-6) : INFINITY;
+    if (n >= K) {
+        const uint2* lst = a.ub_list + (size_t)q * a.ub_cap;
+        WaveList<KP> L;
+        L.init();
+        for (int i0 = 0; i0 < n; i0 += kWave) {
+            const int i = i0 + lane;
+            const uint2 e = i < n ? lst[i] : make_uint2(0u, 0u);
+            L.insert(i < n ? key_of((double)__uint_as_float(e.x)) : kKeyInvalid,
+                     i < n ? (int32_t)e.y : kIdInvalid);
+        }
+        uint64_t kk;
+        int32_t ki;
+        L.at(K - 1, kk, ki);
+        const double u = kk != kKeyInvalid ? dist_of(kk) : INFINITY;
+        if (u < (double)INFINITY) tau = fmin(tau, u * u / a.rot_sq_min * (1.0 + 1e-6));
+        // exact seeding: every one of the K smallest entries is finite and has its row
+        bool ok = lane >= K || (L.k0 != kKeyInvalid && L.i0 >= 0);
+        if constexpr (KP > 64) ok = ok && (lane + kWave >= K || (L.k1 != kKeyInvalid && L.i1 >= 0));
+        if (u < (double)INFINITY && __ballot(!ok) == 0ull) {
+            if (lane < K) s_pos[wid][lane] = L.i0;
+            if constexpr (KP > 64)
+                if (lane + kWave < K) s_pos[wid][kWave + lane] = L.i1;
+            for (int d = lane; d < a.D; d += kWave) s_q64[wid][d] = (double)a.xq[(size_t)q * a.D + d];
+            wave_sync();
+            double dv[KP / kWave];
+            double mx = 0.0;
+#pragma unroll
+            for (int h = 0; h < KP / kWave; ++h) {
+                const int nr = min(kWave, K - h * kWave);
+                dv[h] = 0.0;
+                if (nr > 0) {
+                    dv[h] = refine_rows_mlp(a.xb, a.D, s_pos[wid] + h * kWave, nr, s_stage[wid],
+                                            s_q64[wid]);
+                    if (lane < nr) mx = fmax(mx, dv[h]);
+                }
+            }
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
+            tau = fmin(tau, mx);
+            // the seeds as the first candidates (refined): those within tau
+            int cnt = 0;
+            uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+            int32_t* ci = a.cand_id + (size_t)q * a.cap;
+#pragma unroll
+            for (int h = 0; h < KP / kWave; ++h) {
+                const int r = h * kWave + lane;
+                const bool keep = r < K && dv[h] <= tau;
+                const uint64_t m = __ballot(keep);
+                if (keep) {
+                    const int slot = cnt + mask_rank(m);
+                    ck[slot] = key_of(dv[h]);
+                    ci[slot] = a.orig_ids[s_pos[wid][r]];
+                }
+                cnt += __popcll(m);
+            }
+            if (lane == 0) {
+                a.cand_cnt[q] = cnt;
+                a.seed_cnt[q] = cnt;
+                if (a.stats && cnt) atomicAdd(&a.stats[(q % kStatSlots) * 4 + 3], (unsigned long long)cnt);
+            }
+        }
     }
-    uint64_t kk;
-    int32_t ki;
-    L.at(a.K - 1, kk, ki);
-    if (lane == 0 && kk != kKeyInvalid) {
-        const double u = dist_of(kk);
-        if (u < (double)INFINITY) a.tau[q] = u * u / a.rot_sq_min * (1.0 + 1e-6);
-    }
+    if (lane == 0) a.tau[q] = tau;
 }
 
-template __global__ void ub_kth_kernel<64>(BatchArgs);
-template __global__ void ub_kth_kernel<128>(BatchArgs);
+template __global__ void ub_kth_kernel<64, 256>(BatchArgs);
+template __global__ void ub_kth_kernel<64, 1024>(BatchArgs);
+template __global__ void ub_kth_kernel<128, 256>(BatchArgs);
+template __global__ void ub_kth_kernel<128, 1024>(BatchArgs);
 
 // ---------------------------------------------------------------------------------------------
 // Lower-bound pass.

@@ -127,8 +127,10 @@ struct Workspace {
     LbRec* lbr;                      // [B * nprobe]
     double* cbound;                  // [nlist, kCbStride]
     double* qep;                     // [B]
-    float* ub_list;                  // [B, ub_cap] seeding bounds (batched route)
+    uint2* ub_list;                  // [B, ub_cap] seeding bounds and rows (batched route)
     int32_t* ub_cnt;                 // [B]
+    uint32_t* ub_best;               // [B]
+    int32_t* seed_cnt;               // [B]
     int64_t ub_cap;
     float* qt32;                     // band front end: queries, matrix-core tile layout
     float* qn32;                     // [B] their squared norms
@@ -191,8 +193,10 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.cbound = c.take<double>(kCbStride * (int64_t)ix->nlist);
     w.qep = c.take<double>(B);
     w.ub_cap = ub_cap_of(std::min<int64_t>(K, 64));
-    w.ub_list = c.take<float>(B * w.ub_cap);
+    w.ub_list = c.take<uint2>(B * w.ub_cap);
     w.ub_cnt = c.take<int32_t>(B);
+    w.ub_best = c.take<uint32_t>(B);
+    w.seed_cnt = c.take<int32_t>(B);
     const int64_t Dq = band_dq(ix->D);
     w.qt32 = c.take<float>((B + 15) / 16 * 16 * Dq);
     w.qn32 = c.take<float>(B);
@@ -803,6 +807,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.qep = w.qep;
         b.ub_list = w.ub_list;
         b.ub_cnt = w.ub_cnt;
+        b.ub_best = w.ub_best;
+        b.seed_cnt = w.seed_cnt;
         b.ub_cap = (int)w.ub_cap;
         b.nlist = ix->nlist;
         b.groups = w.groups;
@@ -811,25 +817,32 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         aux_bounds_kernel<<<(unsigned)((ix->nlist + B + kWavesPerBlock - 1) / kWavesPerBlock),
                             kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep, w.unit_ctr);
         if ((rc = check_launch("aux_bounds_kernel"))) return rc;
+        // TRIDENT_UB_SEED 2 seeds from every probe, 0 and 1 from the first p_init
+        const int seed_all = sp->ub_seed == 2 ? 1 : 0;
         unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
-                                               b.unit_q, w.unit_off, w.grp_off);
+                                               b.unit_q, seed_all, w.unit_off, w.grp_off);
         if ((rc = check_launch("unit_scan_kernel"))) return rc;
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
-                           st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, w.unit_off,
-                                 w.units, (int)w.max_units, w.grp_off, w.groups,
+                           st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, seed_all,
+                                 w.unit_off, w.units, (int)w.max_units, w.grp_off, w.groups,
                                  (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if ((rc = launch_pair_prep(b, st))) return rc;
-        if (M1 > 0) {  // pass A: per-query upper-bound threshold from the first p_init probes
+        if (M1 > 0 || seed_all) {
+            // pass A: per-query upper bounds from the seeding probes, then the exact distances of
+            // each query's K best-bound rows (the seeds) set the threshold
             b.unit_beg = 0;
             b.unit_end = ix->nlist;
             b.ctr = w.unit_ctr;
             if ((rc = launch_batch<true>(b, st))) return rc;
             const unsigned kg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
-            if (K <= 64)
-                ub_kth_kernel<64><<<kg, kBlock, 0, st>>>(b);
-            else
-                ub_kth_kernel<128><<<kg, kBlock, 0, st>>>(b);
+            if (K <= 64) {
+                if (ix->D <= 256) ub_kth_kernel<64, 256><<<kg, kBlock, 0, st>>>(b);
+                else ub_kth_kernel<64, 1024><<<kg, kBlock, 0, st>>>(b);
+            } else {
+                if (ix->D <= 256) ub_kth_kernel<128, 256><<<kg, kBlock, 0, st>>>(b);
+                else ub_kth_kernel<128, 1024><<<kg, kBlock, 0, st>>>(b);
+            }
             if ((rc = check_launch("ub_kth_kernel"))) return rc;
         }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;

@@ -131,8 +131,11 @@ struct BatchArgs {
     const double* cbound;       // [nlist, kCbStride] (A_max, r_max, r_lo) per cluster
     const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (set from the seeding lists)
-    float* ub_list;             // [B, ub_cap] seeding bounds: each seeding unit's K smallest
+    uint2* ub_list;             // [B, ub_cap] seeding bounds: each seeding unit's K smallest, as
+                                // (bound bits with the row in the low 16, sorted position or -1)
     int32_t* ub_cnt;            // [B] entries appended to ub_list (may exceed ub_cap)
+    uint32_t* ub_best;          // [B] smallest K-th bound of a unit whose entries did not fit
+    int32_t* seed_cnt;          // [B] leading candidate slots already refined exactly (seeds)
     int ub_cap;
     float* tau_sq_out;          // [B] caller's float32 copy of the seeded tau, or null
     int xb_host;                // xb is mapped host memory (Stage Z reads cross PCIe)
@@ -287,11 +290,13 @@ inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
     return (pairs + kGroupQ - 1) / kGroupQ + nlist;
 }
 
+// seed_all: the seeding units cover every pair of a cluster (TRIDENT_UB_SEED 2), not only its
+// pass-1 pairs.
 __global__ void unit_scan_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
-                                 int32_t* unit_off, int32_t* grp_off);
+                                 int seed_all, int32_t* unit_off, int32_t* grp_off);
 
 __global__ void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
-                                 const int32_t* unit_off, int4* units, int max_units,
+                                 int seed_all, const int32_t* unit_off, int4* units, int max_units,
                                  const int32_t* grp_off, int2* groups, int max_groups);
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
@@ -306,15 +311,21 @@ constexpr int kLbQ = 64;
 
 __global__ void lb_prep_kernel(BatchArgs a);
 
-template <int KP>
+template <int KP, int DQ>
 __global__ void ub_kth_kernel(BatchArgs a);
 
 // Bounds a seeding unit lists per query: its K smallest, at most 64.
 __host__ __device__ constexpr int ub_per_unit(int K) { return K < 64 ? K : 64; }
 
 // Seeding-list slots per query: at most 3 seeding probes (trident_p_init_rule) x kMaxSplit
-// slices, ub_per_unit(K) bounds each.
+// slices, ub_per_unit(K) bounds each; a unit whose entries no longer fit offers its K-th bound
+// to ub_best instead.
 inline int64_t ub_cap_of(int64_t K) { return 3 * kMaxSplit * (int64_t)ub_per_unit((int)K); }
+
+// Seeding bounds carry their row: the bound is rounded up to a multiple of 2^16 in its bit
+// pattern (at most 2^-7 of its value) and the low 16 bits hold the row's index in the unit's
+// slice, or kNoRow when the slice is longer or the bound is not finite.
+constexpr uint32_t kNoRow = 0xffffu;
 
 template <int KS>
 __global__ void lb_scan_kernel(BatchArgs a);       // KS <= 4 (D_pad <= 256)
