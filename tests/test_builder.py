@@ -256,3 +256,54 @@ def test_centroid_band_layouts_positions():
         n64 = (cen.double() ** 2).sum(1)  # summation order may differ in the last bit
         assert torch.allclose(norms.double(), n64, rtol=1e-6, atol=0)
         assert abs(nmax - float(n64.max())) <= 1e-12 * float(n64.max())
+
+
+@pytest.mark.parametrize("which", ["hist", "gmm"])
+def test_derived_vec_ar_matches_the_builder(which, hist_ix, gmm_ix):
+    """index.derive_vec_Ar (the drop-in path for an index passed in the reference layout alone)
+    recomputes the builder's per-vector scalars from sq8_packed, the stored rotation and the
+    base: identical bits, and r bounds |x R + b - x_hat| measured independently in numpy."""
+    from trident_amd.index import cells_from_packed, derive_vec_Ar
+    ix = (hist_ix if which == "hist" else gmm_ix)[0]
+    st = ix.storage
+    got = derive_vec_Ar(ix.sq8_packed, st.cluster_vec_off, ix.cluster_tile_off, st.xb_sorted, ix.W_combined,
+                        ix.b_combined, ix.vmin_pad, ix.delta_pad, ix.per_cluster_sq8, ix.nlist, ix.tile_size)
+    assert torch.equal(got, ix.vec_Ar)
+    assert torch.equal(cells_from_packed(ix.sq8_packed, ix.D_pad, ix.tile_size), ix.sq8_cells)
+    # independent check of r on every vector: decode the codes from the cells, rotate in numpy
+    D, Dp, nl = ix.D, ix.D_pad, ix.nlist
+    R = ix.W_combined[:, nl:nl + D].double().numpy()
+    b = ix.b_combined.reshape(-1)[nl:nl + D].double().numpy()
+    xb = st.xb_sorted.double().numpy()
+    vo = st.cluster_vec_off.numpy()
+    lid = np.repeat(np.arange(nl), np.diff(vo))
+    packed = ix.sq8_packed.numpy().reshape(-1, Dp // 4, ix.tile_size)
+    to = ix.cluster_tile_off.numpy()
+    loc = np.arange(len(xb)) - vo[lid]
+    codes = packed[to[lid] + loc // ix.tile_size, :, loc % ix.tile_size].view(np.uint8).astype(np.float64)
+    xhat = ix.vmin_pad.double().numpy()[lid] + codes * ix.delta_pad.double().numpy()[lid]
+    xr = np.zeros_like(xhat)
+    xr[:, :D] = xb @ R + b
+    r_np = np.sqrt(((xr - xhat) ** 2).sum(1))
+    assert (got[:, 1].double().numpy() >= r_np).all()
+    a_np = ((codes * ix.delta_pad.double().numpy()[lid]) ** 2).sum(1)
+    assert (got[:, 0].double().numpy() <= a_np).all()
+
+
+def test_tile_band_brackets_residual_norms(hist_ix):
+    """tile_r_minmax holds, per tile, float32 bounds around every |x - c(x)| of its vectors."""
+    ix, xb, _, cen, lid = hist_ix
+    st = ix.storage
+    T, nl = ix.tile_size, ix.nlist
+    vo = st.cluster_vec_off.numpy()
+    to = ix.cluster_tile_off.numpy()
+    xs = st.xb_sorted.double().numpy()
+    lids = np.repeat(np.arange(nl), np.diff(vo))
+    r = np.sqrt(((xs - ix.centroids.double().numpy()[lids]) ** 2).sum(1))
+    tile = to[lids] + (np.arange(len(xs)) - vo[lids]) // T
+    band = ix.tile_r_minmax.double().numpy()
+    assert (band[tile, 0] <= r).all() and (band[tile, 1] >= r).all()
+    # tight: the band of each tile is within float32 rounding of its extreme norms
+    for t in np.unique(tile)[:50]:
+        rr = r[tile == t]
+        assert band[t, 0] >= rr.min() * (1 - 1e-6) and band[t, 1] <= rr.max() * (1 + 1e-6)

@@ -604,6 +604,17 @@ __device__ __forceinline__ void merge16_groups(float (&m)[16]) {
     }
 }
 
+// Residual-norm band (reference src/trident_v4_kernels.cu:686-695): |q - x| >= | |q - c| -
+// |x - c| |, so no vector of a tile whose |x - c| lies in [rmin, rmax] is within sqrt(tau) of q
+// when rmax < dqc - sqrt(tau) or rmin > dqc + sqrt(tau).  tol covers the float32 storage of
+// both norms (as the per-pair route).  A query without a threshold never skips.
+__device__ __forceinline__ bool l1_skips(float dqc, double tau, float rmin, float rmax) {
+    if (!(tau < (double)INFINITY)) return false;
+    const double t = sqrt(tau) * (1.0 + 1e-6), dq = (double)dqc, rmx = (double)rmax;
+    const double tol = 1e-6 * (dq + rmx) + 1e-30;
+    return rmx + tol < dq - t || (double)rmin - tol > dq + t;
+}
+
 // Integer lower-bound threshold of one vector for a wave: an int32 <= (A - r (r + 2 tq)) / c1
 // for the stored A (rounded down), r and tq (rounded up), computed in f32 with a margin m of
 // 2^-21 (A + y) / c1 + 1 over its three roundings (each <= 2^-24 of a term <= A + y); c1 is a
@@ -1410,6 +1421,13 @@ void lb_scan_kernel(BatchArgs a) {
                                      : make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // never passes
             }
         }
+        // residual-norm band: lane l < nq holds query slot l's |q - c| and threshold
+        float l1_dqc = 0.0f;
+        double l1_tau = -1.0;  // lanes without a query skip every tile
+        if (a.use_l1 && active && lane < nq) {
+            l1_dqc = a.pair_dqc[pb + lane];
+            l1_tau = a.tau[a.pair_qid[pb + lane]];
+        }
 
         // ---- survivor queue (entries li << 5 | query slot) ----
         int nsq = 0;
@@ -1560,6 +1578,11 @@ void lb_scan_kernel(BatchArgs a) {
             const int blk0 = vb + b * BV;
             if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
             if (!active) continue;
+            if (a.use_l1) {  // the wave leaves the block when none of its queries reaches its tile
+                const float* rm = a.tile_rmm + 2 * (size_t)(t0 + blk0 / T);
+                const bool need = l1_tau >= 0.0 && !l1_skips(l1_dqc, l1_tau, rm[0], rm[1]);
+                if (__ballot(need) == 0ull) continue;
+            }
             if (int_ok) {
                 const float A = s_A[buf][lane], r = s_r[buf][lane];
                 s_thr[buf][wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
@@ -1685,6 +1708,14 @@ __global__ __launch_bounds__(256) void lb_scan_wide_kernel(BatchArgs a) {
             }
         }
         const uint64_t qmask = __ballot(hasq);
+        // residual-norm band: lane j < nq holds its query's |q - c| and threshold
+        float l1_dqc = 0.0f;
+        double l1_tau = -1.0;  // lanes without a query skip every tile
+        if (a.use_l1 && active && hasq && g == 0) {
+            const int pj = start + gq * kWaveQ + j;
+            l1_dqc = a.pair_dqc[pj];
+            l1_tau = a.tau[a.pair_qid[pj]];
+        }
         // the float test's constants and the query ids wait in LDS for the rare path and flush
         if (active && lane < kWaveQ) {
             s_sqid[wid][lane] = q;
@@ -1818,7 +1849,8 @@ __global__ __launch_bounds__(256) void lb_scan_wide_kernel(BatchArgs a) {
             // ring and replica finish as in ub_scan_kernel
             const int nload = (KS - wid + 3) / 4 + (wid == 0 ? 2 : 0);
             for (int p = 0; p < kWideAhead && p < nblk; ++p) gload(p, p, vb + p * BV);
-            int cs = 0;  // b % NBC
+            int cs = 0;             // b % NBC
+            bool band_prev = false;  // block b - 1 was scanned (its deferred finish is due)
             for (int b = 0; b < nblk; ++b) {
                 wait_vmcnt(min(kWideAhead - 1, nblk - 1 - b) * nload);
                 __syncthreads();
@@ -1827,28 +1859,39 @@ __global__ __launch_bounds__(256) void lb_scan_wide_kernel(BatchArgs a) {
                 if (b + kWideAhead < nblk)
                     gload(cs == 0 ? NBC - 1 : cs - 1, (b + kWideAhead) & 7,
                           blk0 + kWideAhead * BV);
+                bool band = active;  // the wave's queries reach the block's tile
+                if (a.use_l1 && active) {
+                    const float* rm = a.tile_rmm + 2 * (size_t)(t0 + blk0 / T);
+                    band = __ballot(l1_tau >= 0.0 && !l1_skips(l1_dqc, l1_tau, rm[0], rm[1])) != 0ull;
+                }
                 if (active) {
-                    if (int_ok && lane < BV) {
+                    // band is the same for the replica waves of a query group (same queries)
+                    if (band && int_ok && lane < BV) {
                         const float A = s_A[b & 7][lane], r = s_r[b & 7][lane];
                         s_thr[b & 1][wid][lane] =
                             blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
                     }
                     int S[4];
                     if (R == 1) {
-                        wide_partial(cs, S, std::integral_constant<int, 1>{});
-                        wide_judge(S, b & 1, b & 7, blk0);
+                        if (band) {
+                            wide_partial(cs, S, std::integral_constant<int, 1>{});
+                            wide_judge(S, b & 1, b & 7, blk0);
+                        }
                     } else {
-                        if (R == 2) wide_partial(cs, S, std::integral_constant<int, 2>{});
-                        else wide_partial(cs, S, std::integral_constant<int, 4>{});
-                        s_part[b & 1][wid][lane] = make_int4(S[0], S[1], S[2], S[3]);
-                        if (b > 0) wide_finish(b - 1, (b - 1) & 7);
+                        if (band) {
+                            if (R == 2) wide_partial(cs, S, std::integral_constant<int, 2>{});
+                            else wide_partial(cs, S, std::integral_constant<int, 4>{});
+                            s_part[b & 1][wid][lane] = make_int4(S[0], S[1], S[2], S[3]);
+                        }
+                        if (b > 0 && band_prev) wide_finish(b - 1, (b - 1) & 7);
                     }
                 }
+                band_prev = band;
                 cs = cs + 1 == NBC ? 0 : cs + 1;
             }
             if (R > 1 && nblk > 0) {
                 __syncthreads();
-                if (active) wide_finish(nblk - 1, (nblk - 1) & 7);
+                if (active && band_prev) wide_finish(nblk - 1, (nblk - 1) & 7);
             }
         }
         if (a.stats && active && rr == 0)

@@ -788,6 +788,9 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.cap = (int)cap;
         b.K = K;
         b.stats = out->stats ? w.stat_slots : nullptr;
+        b.use_l1 = sp->use_l1 ? 1 : 0;
+        b.tile_rmm = ix->tile_r_minmax;
+        b.pair_dqc = w.pair_dqcs;
         b.rot_sq_min = ix->rot_sq_min;
         b.rot_sq_max = ix->rot_sq_max;
         b.sum_rel = sum_rel_of(ix->D_pad);

@@ -139,6 +139,9 @@ struct BatchArgs {
     int ub_cap;
     float* tau_sq_out;          // [B] caller's float32 copy of the seeded tau, or null
     int xb_host;                // xb is mapped host memory (Stage Z reads cross PCIe)
+    int use_l1;                 // residual-norm tile band: skip tiles no query can reach
+    const float* tile_rmm;      // [tiles, 2] (min, max) of |x - c| per tile (use_l1)
+    const float* pair_dqc;      // [M] |q - c| per pair (use_l1)
     int B;
     uint64_t* cand_key;
     int32_t* cand_id;

@@ -33,6 +33,8 @@ from ._lib import TridentIndexView, TridentSearchOutputs, TridentSearchParams, c
 _ws_lock = threading.Lock()
 _ws_cache = {}
 _rot_cache = {}
+_derived_lock = threading.Lock()
+_derived_cache = {}  # index identity -> (vec_Ar, sq8_cells, cent_band), at most two indexes
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -189,6 +191,35 @@ def centroid_band_layouts(W_combined: torch.Tensor, nlist: int):
     return rows, tiles, n64.to(torch.float32), float(n64.max()) if nlist else 0.0
 
 
+def _identity(*ts):
+    return tuple((int(t.data_ptr()), tuple(t.shape), int(t._version)) for t in ts)
+
+
+def derived_layouts(W_combined, b_combined, sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted,
+                    vmin, delta, per_cluster_sq8: int, nlist: int, tile_size: int):
+    """(vec_Ar, sq8_cells, cent_band) for an index passed in the reference layout alone, derived
+    once per index (tensor identities and versions) and cached: the per-vector scalars measured
+    on the data (index.derive_vec_Ar), the code cells regrouped from sq8_packed
+    (index.cells_from_packed) and the centroid layouts of the matrix-core coarse pass."""
+    from . import index as _index
+    key = _identity(W_combined, b_combined, sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted,
+                    vmin, delta) + (int(per_cluster_sq8), int(nlist), int(tile_size))
+    with _derived_lock:
+        hit = _derived_cache.get(key)
+        if hit is not None:
+            return hit
+        D_pad = int(W_combined.shape[1]) - int(nlist)
+        vec_Ar = _index.derive_vec_Ar(sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted,
+                                      W_combined, b_combined, vmin, delta, per_cluster_sq8, nlist,
+                                      tile_size)
+        cells = _index.cells_from_packed(sq8_packed, D_pad, int(tile_size))
+        band = centroid_band_layouts(W_combined, nlist)
+        if len(_derived_cache) >= 2:
+            _derived_cache.pop(next(iter(_derived_cache)))
+        _derived_cache[key] = (vec_Ar, cells, band)
+        return vec_Ar, cells, band
+
+
 def env_ub_seed() -> int:
     return int(os.environ.get("TRIDENT_UB_SEED", "0") or 0)
 
@@ -338,6 +369,15 @@ def launch_trident_v4_search(
 
     if rot_sq_bounds is None:
         rot_sq_bounds = rotation_sq_bounds(W_combined, nlist, D)
+    if mode == 2 and (vec_Ar is None or sq8_cells is None) and int(route) != 1 and \
+            (int(route) == 2 or B * nprobe >= 8 * nlist) and D_pad <= 1024 and K <= 128:
+        # a reference caller passes neither: derive them (once per index) so that the batched
+        # route can run, as it would for an index built by TridentV4Index
+        vec_Ar, sq8_cells, band = derived_layouts(W_combined, b_combined, sq8_packed, cluster_vec_off,
+                                                  cluster_tile_off, xb_sorted, vmin, delta,
+                                                  per_cluster_sq8, nlist, tile_size)
+        if cent_band is None:
+            cent_band = band
     view = make_index_view(
         N=N, D=D, D_pad=D_pad, nlist=nlist, tile_size=tile_size, per_cluster_sq8=per_cluster_sq8,
         W_combined=W_combined, b_combined=b_combined, rot_sq_min=rot_sq_bounds[0],

@@ -62,6 +62,68 @@ def round_up_f32(x64: torch.Tensor) -> torch.Tensor:
     return x32
 
 
+def cells_from_packed(sq8_packed: torch.Tensor, D_pad: int, T: int) -> torch.Tensor:
+    """The batched route's code cells from the reference tile packing: cell (t, b, g, v) = dims
+    16 g .. 16 g + 15 of slot b V + v of tile t (words 4 g .. 4 g + 3 of sq8_packed[t, :, slot]),
+    every byte c stored as c ^ 0x80, V = cell_block(D_pad) slots per contiguous block."""
+    dev = sq8_packed.device
+    tiles = int(sq8_packed.numel()) // ((D_pad // 4) * T)
+    packed = sq8_packed.view(tiles, D_pad // 4, T)
+    G16, V = D_pad // 16, cell_block(D_pad)
+    cells = torch.empty((tiles, T // V, G16, V, 4), device=dev, dtype=torch.int32)
+    flip = torch.tensor(-0x7f7f7f80, dtype=torch.int32, device=dev)  # 0x80808080
+    tstep = max(1, (1 << 24) // max(T * (D_pad // 4), 1))
+    for ts in range(0, tiles, tstep):
+        te = min(tiles, ts + tstep)
+        cells[ts:te] = packed[ts:te].view(te - ts, G16, 4, T // V, V).permute(0, 3, 1, 4, 2) ^ flip
+    return cells
+
+
+def derive_vec_Ar(sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted, W_combined, b_combined,
+                  vmin, delta, per_cluster_sq8: int, nlist: int, T: int, chunk_rows: int = 1 << 20):
+    """The batched route's per-vector scalars [N, 2] of any index in the reference layout, from
+    its own tensors: A = sum_d (code_d delta_d)^2 (rounded down after a 1e-13 margin) and
+    r >= |x R + b - x_hat| with R, b the float32 rotation stored in W_combined / b_combined (the
+    map the query path applies), x_hat = vmin + code delta from sq8_packed, plus the float64
+    rotation error bound (rounded up).  r is measured on the data, so it holds whatever rotation
+    or eps produced the codes (the reference quantises a float64 rotation with eps = 0.5001
+    delta)."""
+    dev = sq8_packed.device
+    N, D = int(xb_sorted.shape[0]), int(xb_sorted.shape[1])
+    D_pad = int(W_combined.shape[1]) - nlist
+    R = W_combined[:, nlist:nlist + D].to(dev, torch.float64)
+    b = b_combined.reshape(-1)[nlist:nlist + D].to(dev, torch.float64)
+    colabs = R.abs().sum(0)
+    rot_err_coef = (D + 2) * 2.0 * _U53
+    vec_off = cluster_vec_off.to(dev, torch.int64)
+    tile_off = cluster_tile_off.to(dev, torch.int64)
+    counts = vec_off[1:] - vec_off[:-1]
+    lid = torch.repeat_interleave(torch.arange(nlist, device=dev), counts)
+    local = torch.arange(N, device=dev) - vec_off[lid]
+    tile = tile_off[lid] + torch.div(local, T, rounding_mode="floor")
+    slot = local % T
+    packed = sq8_packed.view(-1, D_pad // 4, T)
+    rows = nlist if per_cluster_sq8 else 1
+    vm_all = vmin.reshape(rows, D_pad).to(dev, torch.float64)
+    dl_all = delta.reshape(rows, D_pad).to(dev, torch.float64)
+    out = torch.empty((N, 2), device=dev, dtype=torch.float32)
+    for s in range(0, N, chunk_rows):
+        e = min(N, s + chunk_rows)
+        codes = packed[tile[s:e], :, slot[s:e]].contiguous().view(torch.uint8)   # [n, D_pad]
+        ci = lid[s:e] if per_cluster_sq8 else torch.zeros(e - s, dtype=torch.int64, device=dev)
+        cdl = codes.double() * dl_all[ci]
+        xhat = vm_all[ci] + cdl
+        x = xb_sorted[s:e].to(dev, torch.float64)
+        xr = torch.zeros((e - s, D_pad), device=dev, dtype=torch.float64)
+        xr[:, :D] = x @ R + b
+        rerr = rot_err_coef * (x.abs().amax(1, keepdim=True) * colabs + b.abs())
+        a64 = (cdl * cdl).sum(1) * (1.0 - 1e-13)
+        r = torch.sqrt(((xr - xhat) ** 2).sum(1)) + torch.sqrt((rerr ** 2).sum(1))
+        out[s:e, 0] = -round_up_f32(-a64)
+        out[s:e, 1] = round_up_f32(r * (1.0 + 1e-12) + 1e-300)
+    return out
+
+
 class PinnedHostBuffer:
     """Device-mapped pinned host memory from ``hipHostMalloc`` (C ABI), viewed as a CPU tensor.
 
@@ -245,8 +307,11 @@ class TridentV4Index:
         #   vec_Ar[v, 1] >= r_v >= |x_rot(exact) - x_hat|_2   (quantisation + rotation error)
         # The kernel uses vec_Ar[v, 0] * (1 + 2^-22) >= A_v as the upper value of A_v.
         self.vec_Ar = torch.empty((N, 2), device=dev, dtype=torch.float32)
+        # residual norms |x - c(x)| in float64, for the tile band of use_l1 (tile_r_minmax)
+        res_norm = torch.empty(N, device=dev, dtype=torch.float64)
         for s in range(0, N, chunk_rows):
             e = min(N, s + chunk_rows)
+            res_norm[s:e] = torch.sqrt(((rows_dev(s, e).double() - cen[lid_sorted[s:e]].double()) ** 2).sum(1))
             xr64, rerr = rotate(s, e)
             xr32 = xr64.to(torch.float32)
             ci = lid_sorted[s:e] if self.per_cluster_sq8 else torch.zeros(e - s, dtype=torch.int64, device=dev)
@@ -289,22 +354,21 @@ class TridentV4Index:
             g = codes32[safe[ts:te]]                         # [nt, T, D4]
             g = torch.where(valid[ts:te].unsqueeze(-1), g, torch.zeros_like(g))
             self.sq8_packed[ts:te] = g.permute(0, 2, 1)
-        # Batched-route copy: 16-byte cells, cell (t, b, g, v) = dims 16 g .. 16 g + 15 of slot
-        # s = b V + v (words 4 g .. 4 g + 3 of sq8_packed[t, :, s]), every byte c stored as
-        # c ^ 0x80; the V slots of a scan block are one contiguous run.
-        G16, V = D_pad // 16, cell_block(D_pad)
-        self.sq8_cells = torch.empty((tiles, T // V, G16, V, 4), device=dev, dtype=torch.int32)
-        flip = torch.tensor(-0x7f7f7f80, dtype=torch.int32, device=dev)  # 0x80808080
+        # Batched-route copy: 16-byte cells, every scan block of V slots one contiguous run
+        self.sq8_cells = cells_from_packed(self.sq8_packed, D_pad, T)
+        # The tile band (reference :198-230 takes it from the clustering's float32 r_vec): the
+        # smallest and largest |x - c| of each tile, measured here in float64 and rounded
+        # outward to float32 (an empty tile gets [+inf, -inf]: never reached).
+        self.tile_r_minmax = torch.empty((tiles, 2), device=dev, dtype=torch.float32)
         for ts in range(0, tiles, tstep):
             te = min(tiles, ts + tstep)
-            self.sq8_cells[ts:te] = (self.sq8_packed[ts:te].view(te - ts, G16, 4, T // V, V)
-                                     .permute(0, 3, 1, 4, 2) ^ flip)
-        self.tile_r_minmax =torch.zeros((tiles, 2), device=dev, dtype=torch.float32)
-        if storage.r_vec_sorted is not None:
-            r = storage.r_vec_sorted.to(dev)[safe]
-            self.tile_r_minmax[:, 0] = torch.where(valid, r, torch.full_like(r, math.inf)).amin(1)
-            self.tile_r_minmax[:, 1] = torch.where(valid, r, torch.full_like(r, -math.inf)).amax(1)
-        del codes, codes32
+            r = res_norm[safe[ts:te]]
+            v = valid[ts:te]
+            rmin = torch.where(v, r, torch.full_like(r, math.inf)).amin(1) * (1.0 - 1e-12)
+            rmax = torch.where(v, r, torch.full_like(r, -math.inf)).amax(1) * (1.0 + 1e-12)
+            self.tile_r_minmax[ts:te, 0] = -round_up_f32(-rmin)
+            self.tile_r_minmax[ts:te, 1] = round_up_f32(rmax)
+        del codes, codes32, res_norm
 
         # ---- dimension blocks (reference :231-255) ----
         if var_block:
