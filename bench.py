@@ -217,7 +217,7 @@ def measure(cfg_id, cfg, args, dev, primary=True):
     gpu_d, gpu_i = d_out.cpu().numpy().copy(), i_out.cpu().numpy().copy()
     probes = ix.probe_cids_buf[:B, :nprobe].cpu().numpy()
     sizes = np.diff(st.cluster_vec_off.cpu().numpy().astype(np.int64))
-    p_init = _lib.lib().trident_p_init_rule(mode, B, K, nprobe) if mode == 2 else 0
+    p_init = _lib.lib().trident_p_init_rule(mode, B, K, nprobe, 0) if mode == 2 else 0
     bytes_all = int(sizes[probes].sum()) * ix.D_pad
     bytes_p2 = int(sizes[probes[:, p_init:]].sum()) * ix.D_pad
     if mode == 10:

@@ -8,7 +8,7 @@
  *
  * Reference interfaces replaced (paths relative to the reference checkout):
  *   trident_search          launch_trident_v4_search, src/trident_v4_kernels.cu:1172-1604
- *                           (modes 2 and 10), bound in Python at :1606-1627
+ *                           (modes 0, 1, 2, 10, 11), bound in Python at :1606-1627
  *   trident_coarse_probe    at::addmm_out coarse GEMM + trident_topk_centroids_kernel,
  *                           src/trident_v4_kernels.cu:1233-1259 and :68-162
  *   trident_group_pairs     trident_counting_sort_pairs_kernel, :168-263 (+ split :1264-1276)
@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TRIDENT_ABI_VERSION 1
+#define TRIDENT_ABI_VERSION 2
 
 enum TridentStatus {
     TRIDENT_OK = 0,
@@ -40,8 +40,15 @@ enum TridentStatus {
 };
 
 enum TridentMode {
-    TRIDENT_MODE_CASCADE = 2,   /* Stage X (optional) + Stage Y SQ8 LB cascade + Stage Z exact refine */
-    TRIDENT_MODE_CM_EXACT = 10  /* cluster-major exhaustive exact scan (reference CM-FP32 route) */
+    TRIDENT_MODE_SQ8_RERANK = 0, /* reference K0 / CM-SQ8+RR: top rerank_m by the SQ8 reconstruction
+                                    distance, exact rerank to top-K (top-K by it when rerank_m = 0);
+                                    approximate */
+    TRIDENT_MODE_SQ8 = 1,        /* reference K1: top-K by the SQ8 reconstruction distance
+                                    (acc_hat, returned as the distance); approximate */
+    TRIDENT_MODE_CASCADE = 2,    /* Stage X (optional) + Stage Y SQ8 LB cascade + Stage Z exact refine */
+    TRIDENT_MODE_CM_EXACT = 10,  /* cluster-major exhaustive exact scan (reference CM-FP32 route) */
+    TRIDENT_MODE_TRIBASE = 11    /* exact scan skipping x with | |q-c| - |x-c| | > tau (reference
+                                    Tribase-GPU); needs r_vec_sorted */
 };
 
 /* Device-resident index layout produced by trident_amd.TridentV4Index
@@ -86,6 +93,9 @@ typedef struct TridentIndexView {
                                         of centroid 16 t + l % 16 */
     const float* cent_norms;         /* [nlist] float32(sum_d c_d^2) */
     double cent_norm_max;            /* max_c sum_d c_d^2 (float64) */
+    const float* r_vec_sorted;       /* [N] |x - c(x)| in sorted order, float32 of the float64 norm
+                                        (reference r_vec_sorted, src/trident_v4_kernels.cu:1216);
+                                        mode 11 only, else may be NULL */
 } TridentIndexView;
 
 /* How mode 2 is executed.  Both are exact; they differ in speed only. */
@@ -104,6 +114,8 @@ typedef struct TridentSearchParams {
     int32_t use_l1;  /* residual-norm tile band (needs tile_r_minmax) */
     int32_t p_init;  /* pass-1 probes per query; -1 = reference rule */
     int32_t route;   /* TridentRoute (mode 2 only) */
+    int32_t rerank_m; /* mode 0: candidates reranked exactly, M = min(max(rerank_m, K), 200);
+                         0 = no rerank.  Ignored by the other modes */
 } TridentSearchParams;
 
 /* Stage boundaries at which trident_search records the caller's events (if given). */
@@ -135,7 +147,8 @@ int trident_event_create(void** event);
 int trident_event_destroy(void* event);
 int trident_event_elapsed_ms(void* start, void* stop, float* ms);
 
-/* Bytes of scratch trident_search needs for batches up to max_B x max_nprobe x max_K. */
+/* Bytes of scratch trident_search needs for batches up to max_B x max_nprobe x max_K.  For mode 0
+ * with rerank_m > 0, max_K must cover M = min(max(rerank_m, K), 200) as well. */
 size_t trident_workspace_bytes(const TridentIndexView* ix, int32_t max_B, int32_t max_nprobe,
                                int32_t max_K);
 
@@ -174,8 +187,9 @@ int trident_group_pairs(const int32_t* probe_cids, int32_t probe_ld, int32_t B, 
                         int32_t* p2_cids, int32_t* p2_qids, int32_t* seg_off,
                         int32_t* counts_ws, void* stream);
 
-/* The reference two-pass split rule for mode 2 / 10 (src/trident_v4_kernels.cu:1264-1276). */
-int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe);
+/* The reference two-pass split rule (src/trident_v4_kernels.cu:1264-1276): mode 0 by rerank_m,
+ * modes 1 / 2 / 11 by B, K and nprobe, mode 10 single-pass. */
+int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe, int32_t rerank_m);
 
 /* The route (TRIDENT_ROUTE_PAIR or TRIDENT_ROUTE_BATCHED) a mode-2 trident_search with these
  * sizes and requested route takes, or a negative error code when the request cannot run.

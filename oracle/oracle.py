@@ -39,6 +39,11 @@ def lib():
         L.oracle_ivf_exact.argtypes = [P, i64, i32, P, i32, P, P, P, i32, P, P, i32]
         L.oracle_ivfflat_f32.argtypes = [P, i64, i32, P, i32, P, P, P, i32, P, P, i32]
         L.oracle_pair_dists.argtypes = [P, i32, P, P, P, i64, P]
+        L.oracle_rotate_query.argtypes = [P, i32, i32, P, i32, P, P]
+        L.oracle_rotate_query.restype = None
+        L.oracle_ivf_sq8.argtypes = [P, i64, i32, i32, P, P, i32, P, i32, i32, P, P, i32, P, P, P, P,
+                                     i32, P, i32, i32, i32, i32, P, P, i32]
+        L.oracle_ivf_sq8.restype = i32
         L.oracle_dist_f64.argtypes = [P, P, i32]
         L.oracle_dist_f64.restype = dbl
         L.oracle_max_threads.restype = i32
@@ -115,6 +120,69 @@ def pair_dists(xq, xb_sorted, qids, spos):
     out = np.empty(len(qi), np.float64)
     lib().oracle_pair_dists(pq, xq.shape[1], pxb, pqi, psp, len(qi), out.ctypes.data)
     return out
+
+
+def sq8_mode_plan(mode, B, K, nprobe, rerank_m):
+    """(p_init, k_p1, k_p2, M) of modes 0 / 1: the reference's two-pass split
+    (src/trident_v4_kernels.cu:1264-1276), per-pair list lengths (:1439-1443, K_LOC cap :576)
+    and rerank length (:1071-1073).  Mode 1 keeps K per pair: the reference's K_LOC = 10 gives
+    the same top-K for every K <= 10, the only K its merge returns (:984)."""
+    if mode == 0:
+        if nprobe <= 1 or (B == 1 and rerank_m == 0):
+            p_init = 0
+        elif (rerank_m > 20 or K > 10) and nprobe >= 4:
+            p_init = 2
+        else:
+            p_init = 1
+    elif nprobe <= 1:
+        p_init = 0
+    elif B == 1 and K <= 10:
+        p_init = 1
+    else:
+        p_init = 2 if nprobe <= 16 else 3
+    eff = max(rerank_m, K) if (mode == 0 and rerank_m > 0) else 0
+    if eff:
+        k1 = min(eff, 128)
+        k2 = min(eff, max(K, max(16, (eff + nprobe - 1) // nprobe + 8)), 200)
+        return p_init, k1, k2, min(eff, 200)
+    return p_init, K, K, 0
+
+
+def rotate_query(q, W_combined, b_combined, nlist, D_pad):
+    """q R + b as the SQ8 modes compute it (float64 fma chain per column)."""
+    q, pq = _c(q, np.float32)
+    W, pw = _c(W_combined, np.float32)
+    b, pb = _c(b_combined.reshape(-1), np.float32)
+    out = np.empty(D_pad, np.float64)
+    lib().oracle_rotate_query(pq, q.shape[0], D_pad, pw, nlist, pb, out.ctypes.data)
+    return out
+
+
+def ivf_sq8(xq, probe_cids, p_init, ix, K, k_p1, k_p2, M, threads=0):
+    """Modes 0 / 1 (see trident_oracle.c): (d float32 [B, K], ids int64 [B, K]).  ``ix`` holds
+    numpy copies of the index tensors: W_combined, b_combined, nlist, D_pad, vec_off, tile_off,
+    T, sq8_packed, tile_oids, vmin, delta, per_cluster, xb_sorted."""
+    xq, pq = _c(xq, np.float32)
+    pcid, ppc = _c(probe_cids, np.int32)
+    W, pw = _c(ix["W_combined"], np.float32)
+    b, pb = _c(np.asarray(ix["b_combined"]).reshape(-1), np.float32)
+    voff, pvo = _c(ix["vec_off"], np.int32)
+    toff, pto = _c(ix["tile_off"], np.int32)
+    codes, pcd = _c(np.asarray(ix["sq8_packed"]).view(np.uint32), np.uint32)
+    toid, pti = _c(ix["tile_oids"], np.int32)
+    vmin, pvm = _c(ix["vmin"], np.float32)
+    dlt, pdl = _c(ix["delta"], np.float32)
+    xb, pxb = _c(ix["xb_sorted"], np.float32)
+    B, D = xq.shape
+    d = np.empty((B, K), np.float32)
+    ids = np.empty((B, K), np.int64)
+    rc = lib().oracle_ivf_sq8(pq, B, D, int(ix["D_pad"]), pw, pb, int(ix["nlist"]), ppc, pcid.shape[1],
+                              int(p_init), pvo, pto, int(ix["T"]), pcd, pti, pvm, pdl,
+                              int(ix["per_cluster"]), pxb, K, int(k_p1), int(k_p2), int(M),
+                              d.ctypes.data, ids.ctypes.data, threads or default_threads())
+    if rc:
+        raise ValueError("oracle_ivf_sq8: bad arguments")
+    return d, ids
 
 
 # ----------------------------------------------------------------------------------------

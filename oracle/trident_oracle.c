@@ -24,6 +24,19 @@
  *   oracle_ivfflat_f32     the reference CPU baseline omp_cpu_ivfflat_f32
  *                          (benchmarks/phase8_ooc_100m_4080.py:141-204): FP32 direct
  *                          sum with an OpenMP SIMD reduction and (d, id) insertion.
+ *   oracle_rotate_query    the query rotation q -> q R + b of the SQ8 modes as one float64
+ *                          fma chain per column over d in order, plus b_j (the reference
+ *                          computes it with its float32 GEMM, src/trident_v4_kernels.cu:
+ *                          1241-1243; this path fixes the float64 chain instead).
+ *   oracle_ivf_sq8         modes 1 (K1) and 0 (K0 / CM-SQ8+RR),
+ *                          src/trident_v4_kernels.cu:529-962 and :1044-1170: every probed
+ *                          vector's SQ8 reconstruction distance acc_hat = sum_d fmaf(a_d, a_d,
+ *                          acc), a_d = fmaf(code_d, delta_d, fl32(vmin_d - q_rot,d)), dims in
+ *                          order; each (query, cluster) pair keeps its k_pass best by
+ *                          (acc_hat, original id) (K_LOC, :576), the pool's best M (mode 0,
+ *                          :1071-1073) are reranked by the canonical float64 distance and
+ *                          the top-K by (d, id) returned; without a rerank the top-K by
+ *                          (acc_hat, id), acc_hat as the distance.
  *
  * Parity pins: see the checks in tests/test_oracle.py (brute force in numpy on tiny
  * inputs, committed golden fixtures, integer-valued data where every summation order is
@@ -173,6 +186,125 @@ int oracle_ivfflat_f32(const float* xq, int64_t B, int D, const int32_t* probe_c
                 }
             }
         }
+    }
+    return 0;
+}
+
+/* q R + b for one query: xr[j] = fma chain over d of (double)q_d * (double)W[d][nlist + j], then
+ * + (double)b[nlist + j]; j < D_pad. */
+void oracle_rotate_query(const float* q, int D, int D_pad, const float* W, int nlist,
+                         const float* bvec, double* xr) {
+    const int ldw = nlist + D_pad;
+    for (int j = 0; j < D_pad; ++j) {
+        double acc = 0.0;
+        for (int d = 0; d < D; ++d) acc = fma((double)q[d], (double)W[(int64_t)d * ldw + nlist + j], acc);
+        xr[j] = acc + (double)bvec[nlist + j];
+    }
+}
+
+/* (key, id) strictly-less for 64-bit keys (acc_hat bits << 32 | original id). */
+static inline void insert_key(uint64_t* lk, int64_t* li, int K, uint64_t k, int64_t id) {
+    if (!(k < lk[K - 1] || (k == lk[K - 1] && id < li[K - 1]))) return;
+    int j = K - 1;
+    while (j > 0 && (k < lk[j - 1] || (k == lk[j - 1] && id < li[j - 1]))) {
+        lk[j] = lk[j - 1];
+        li[j] = li[j - 1];
+        --j;
+    }
+    lk[j] = k;
+    li[j] = id;
+}
+
+static inline uint32_t f32_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+
+static inline float bits_f32(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Modes 0 / 1.  Probe p of a query belongs to pass 1 when p < p_init and keeps k_p1 entries per
+ * pair, else k_p2.  M > 0: rerank the pool's M best exactly (out_d = float32 of the float64
+ * distance); M == 0: top-K by acc_hat (out_d = acc_hat).  Ids are original ids. */
+int oracle_ivf_sq8(const float* xq, int64_t B, int D, int D_pad, const float* W, const float* bvec,
+                   int nlist, const int32_t* probe_cids, int nprobe, int p_init,
+                   const int32_t* vec_off, const int32_t* tile_off, int T,
+                   const uint32_t* sq8_packed, const int32_t* tile_oids, const float* vmin,
+                   const float* delta, int per_cluster, const float* xb_sorted, int K, int k_p1,
+                   int k_p2, int M, float* out_d, int64_t* out_i, int nthreads) {
+    if (K < 1 || D < 1 || D_pad < D || D_pad % 4 || k_p1 < 1 || k_p2 < 1 || M < 0) return -1;
+    const int D4 = D_pad / 4;
+    const int KL = M > 0 ? (M > K ? M : K) : K; /* pooled list length */
+    int kmax = k_p1 > k_p2 ? k_p1 : k_p2;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        double* xr = (double*)malloc(sizeof(double) * (size_t)D_pad);
+        float* base = (float*)malloc(sizeof(float) * (size_t)D_pad);
+        uint64_t* pk = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)kmax);
+        int64_t* pi = (int64_t*)malloc(sizeof(int64_t) * (size_t)kmax);
+        uint64_t* gk = (uint64_t*)malloc(sizeof(uint64_t) * (size_t)KL);
+        int64_t* gi = (int64_t*)malloc(sizeof(int64_t) * (size_t)KL); /* sorted position */
+        double* ld = (double*)malloc(sizeof(double) * (size_t)K);
+        int64_t* li = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int64_t q = 0; q < B; ++q) {
+            const float* qv = xq + q * (int64_t)D;
+            oracle_rotate_query(qv, D, D_pad, W, nlist, bvec, xr);
+            for (int j = 0; j < KL; ++j) { gk[j] = UINT64_MAX; gi[j] = INT64_MAX; }
+            for (int p = 0; p < nprobe; ++p) {
+                const int32_t c = probe_cids[q * nprobe + p];
+                if (c < 0) continue;
+                const int kp = p < p_init ? k_p1 : k_p2;
+                const int64_t off = per_cluster ? (int64_t)c * D_pad : 0;
+                for (int d = 0; d < D_pad; ++d) base[d] = (float)((double)vmin[off + d] - xr[d]);
+                for (int j = 0; j < kp; ++j) { pk[j] = UINT64_MAX; pi[j] = INT64_MAX; }
+                const int64_t v0 = vec_off[c], n = vec_off[c + 1] - v0, t0 = tile_off[c];
+                for (int64_t l = 0; l < n; ++l) {
+                    const int64_t tile = t0 + l / T, slot = l % T;
+                    float acc = 0.0f;
+                    for (int d4 = 0; d4 < D4; ++d4) {
+                        const uint32_t w = sq8_packed[(tile * D4 + d4) * T + slot];
+                        for (int b = 0; b < 4; ++b) {
+                            const int d = 4 * d4 + b;
+                            const float a = fmaf((float)((w >> (8 * b)) & 0xffu), delta[off + d], base[d]);
+                            acc = fmaf(a, a, acc);
+                        }
+                    }
+                    const int32_t oid = tile_oids[tile * T + slot];
+                    insert_key(pk, pi, kp, ((uint64_t)f32_bits(acc) << 32) | (uint32_t)oid, v0 + l);
+                }
+                for (int j = 0; j < kp && pk[j] != UINT64_MAX; ++j) insert_key(gk, gi, KL, pk[j], pi[j]);
+            }
+            if (M > 0) {
+                for (int j = 0; j < K; ++j) { ld[j] = INFINITY; li[j] = INT64_MAX; }
+                const int m = M < KL ? M : KL;
+                for (int j = 0; j < m && gk[j] != UINT64_MAX; ++j) {
+                    const double d = oracle_dist_f64(xb_sorted + gi[j] * D, qv, D);
+                    insert_sorted(ld, li, K, d, (int64_t)(uint32_t)gk[j]);
+                }
+                for (int j = 0; j < K; ++j) {
+                    const int valid = li[j] != INT64_MAX;
+                    out_d[q * K + j] = valid ? (float)ld[j] : INFINITY;
+                    out_i[q * K + j] = valid ? li[j] : -1;
+                }
+            } else {
+                for (int j = 0; j < K; ++j) {
+                    const int valid = gk[j] != UINT64_MAX;
+                    out_d[q * K + j] = valid ? bits_f32((uint32_t)(gk[j] >> 32)) : INFINITY;
+                    out_i[q * K + j] = valid ? (int64_t)(uint32_t)gk[j] : -1;
+                }
+            }
+        }
+        free(xr); free(base); free(pk); free(pi); free(gk); free(gi); free(ld); free(li);
     }
     return 0;
 }

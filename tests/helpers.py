@@ -66,3 +66,23 @@ def run_search(b, xq_dev, nprobe, K, mode=2, ub=0, use_l1=0, stats=None, route=1
                           route=route)
     torch.cuda.synchronize()
     return d.cpu().numpy().copy(), i.cpu().numpy().copy()
+
+
+def sq8_arrays(b):
+    """numpy copies of the index tensors the SQ8 modes read (oracle.ivf_sq8's ``ix``)."""
+    ix = b.ix
+    return dict(W_combined=ix.W_combined.cpu().numpy(), b_combined=ix.b_combined.cpu().numpy(),
+                nlist=ix.nlist, D_pad=ix.D_pad, vec_off=b.vec_off,
+                tile_off=ix.cluster_tile_off.cpu().numpy(), T=ix.tile_size,
+                sq8_packed=ix.sq8_packed.cpu().numpy(), tile_oids=ix.tile_orig_ids.cpu().numpy(),
+                vmin=ix.vmin_pad.cpu().numpy(), delta=ix.delta_pad.cpu().numpy(),
+                per_cluster=ix.per_cluster_sq8, xb_sorted=b.xb_sorted)
+
+
+def oracle_sq8(b, xq, nprobe, K, mode, rerank_m=0, arrays=None):
+    """Modes 0 / 1 on the CPU oracle with the reference's split and list lengths."""
+    xq = np.ascontiguousarray(xq, np.float32)
+    cids, _ = O.coarse_probe(xq, b.centroids_idx, nprobe)
+    p_init, k1, k2, M = O.sq8_mode_plan(mode, len(xq), K, nprobe, rerank_m)
+    d, i = O.ivf_sq8(xq, cids, p_init, arrays or sq8_arrays(b), K, k1, k2, M)
+    return d, i

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
     exported = set(re.findall(r"\bT (trident_[a-z0-9_]+)", out))
     assert exported == set(names), f"undeclared exports: {exported - set(names)}"
-    assert L.trident_abi_version() == 1
+    assert L.trident_abi_version() == _lib.ABI_VERSION == 2
 
 
 def test_struct_layout_matches_header(tmp_path):
@@ -61,19 +61,57 @@ def test_struct_layout_matches_header(tmp_path):
 
 def test_p_init_rule():
     f = _lib.lib().trident_p_init_rule
-    # reference src/trident_v4_kernels.cu:1270-1275 (mode 2) and mode 10 -> 0
-    assert f(2, 1000, 10, 1) == 0
-    assert f(2, 1, 10, 64) == 1
-    assert f(2, 1, 11, 64) == 3
-    assert f(2, 1000, 10, 16) == 2
-    assert f(2, 1000, 10, 2) == 2
-    assert f(2, 1000, 10, 17) == 3
-    assert f(10, 1000, 10, 64) == 0
+    # reference src/trident_v4_kernels.cu:1264-1276: modes 1 / 2 / 11 share one rule, mode 0 has
+    # its own (by rerank_m), mode 10 is single-pass
+    for mode in (1, 2, 11):
+        assert f(mode, 1000, 10, 1, 0) == 0
+        assert f(mode, 1, 10, 64, 0) == 1
+        assert f(mode, 1, 11, 64, 0) == 3
+        assert f(mode, 1000, 10, 16, 0) == 2
+        assert f(mode, 1000, 10, 2, 0) == 2
+        assert f(mode, 1000, 10, 17, 0) == 3
+    assert f(10, 1000, 10, 64, 0) == 0
+    assert f(0, 1000, 10, 1, 100) == 0
+    assert f(0, 1, 10, 32, 0) == 0
+    assert f(0, 1, 10, 32, 50) == 2
+    assert f(0, 1000, 10, 32, 20) == 1
+    assert f(0, 1000, 11, 4, 0) == 2
+    assert f(0, 1000, 11, 3, 0) == 1
+
+
+def _fake_view():
+    """A view whose pointers are never dereferenced (argument checks only)."""
+    v = TridentIndexView()
+    v.N, v.D, v.D_pad, v.nlist, v.tile_size, v.num_blocks = 1000, 128, 128, 16, 64, 4
+    v.rot_sq_min = v.rot_sq_max = 1.0
+    for f in ("W_combined", "b_combined", "cluster_vec_off", "cluster_tile_off", "xb_sorted",
+              "tile_orig_ids", "sq8_packed", "vmin", "delta", "eps_dim", "blk_bounds4"):
+        setattr(v, f, 256)
+    return v
+
+
+def test_mode_arguments_are_checked_before_any_launch():
+    L = _lib.lib()
+    out = TridentSearchOutputs()
+    out.topk_d = out.topk_i = 256
+    v = _fake_view()
+    sp = TridentSearchParams(7, 4, 10, 8, 0, 0, -1, 0, 0)
+    assert L.trident_search(ctypes.byref(v), ctypes.byref(sp), None, None, 0, ctypes.byref(out), None) == 2
+    assert b"mode 7" in L.trident_last_error()
+    sp = TridentSearchParams(11, 4, 10, 8, 0, 0, -1, 0, 0)
+    assert L.trident_search(ctypes.byref(v), ctypes.byref(sp), None, None, 0, ctypes.byref(out), None) == 1
+    assert b"r_vec_sorted" in L.trident_last_error()
+    sp = TridentSearchParams(0, 4, 10, 8, 0, 0, -1, 0, -5)
+    assert L.trident_search(ctypes.byref(v), ctypes.byref(sp), None, None, 0, ctypes.byref(out), None) == 1
+    assert b"rerank_m" in L.trident_last_error()
+    # mode 0's merged lists need room for M = min(max(rerank_m, K), 200) entries
+    assert L.trident_workspace_bytes(ctypes.byref(v), 64, 8, 200) > L.trident_workspace_bytes(
+        ctypes.byref(v), 64, 8, 10)
 
 
 def test_host_validation_errors_without_gpu():
     L = _lib.lib()
-    sp = TridentSearchParams(2, 4, 10, 8, 0, 0, -1, 0)
+    sp = TridentSearchParams(2, 4, 10, 8, 0, 0, -1, 0, 0)
     out = TridentSearchOutputs()
     rc = L.trident_search(None, ctypes.byref(sp), None, None, 0, ctypes.byref(out), None)
     assert rc == 1 and b"NULL" in L.trident_last_error()
@@ -95,7 +133,7 @@ def test_noalloc_refuses_oversized_batches_without_touching_the_device():
               "tile_orig_ids"):
         setattr(v, f, 256)
     out = TridentSearchOutputs()
-    sp = TridentSearchParams(2, 10_000, 10, 64, 1, 0, -1, 0)
+    sp = TridentSearchParams(2, 10_000, 10, 64, 1, 0, -1, 0, 0)
     need = L.trident_workspace_bytes(ctypes.byref(v), 10_000, 64, 10)
     assert need > _lib.NOALLOC_SCRATCH_BYTES
     rc = L.trident_search_noalloc(ctypes.byref(v), ctypes.byref(sp), None, ctypes.byref(out), None)
@@ -115,12 +153,12 @@ def test_workspace_size_scales_with_batch():
 
 def test_python_boundary_rejects_bad_inputs():
     cpu = torch.zeros(4, 8)
-    with pytest.raises(NotImplementedError):
-        ext.launch_trident_v4_search(0, 64, 0, 1, 0, 4, *([None] * 35))
+    with pytest.raises(_lib.TridentError, match="unknown mode 3"):
+        ext.launch_trident_v4_search(3, 64, 0, 1, 0, 4, *([None] * 35))
     with pytest.raises(_lib.TridentError, match="device tensor"):
         ext.launch_trident_v4_search(2, 64, 0, 1, 0, 4, cpu, *([None] * 34))
     with pytest.raises(_lib.TridentError, match="rerank_m"):
-        ext.launch_trident_v4_search(2, 64, 0, 1, 20, 4, cpu, *([None] * 34))
+        ext.launch_trident_v4_search(0, 64, 0, 1, -1, 4, cpu, *([None] * 34))
 
 
 def test_ub_seed_env(monkeypatch):

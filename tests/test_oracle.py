@@ -194,3 +194,171 @@ def test_planted_probe_order_mistake_is_caught():
     wrong = np.stack([sorted(range(cd.shape[1]), key=lambda c: (cd[r, c], -c))[: int(z["nprobe"])]
                       for r in range(len(q))])
     assert not np.array_equal(wrong, z["probes"])
+
+
+# ---------------------------------------------------------------------------------------------
+# Modes 0 / 1 (oracle_ivf_sq8): pinned by an exact-rational restatement on a tiny index
+# ---------------------------------------------------------------------------------------------
+def _round_f32(fr: Fraction) -> float:
+    """Round a rational to the nearest float32 (ties to even), once."""
+    if fr == 0:
+        return 0.0
+    sign = -1 if fr < 0 else 1
+    x = abs(fr)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    qe = max(e - 23, -149)
+    m = x / Fraction(2) ** qe
+    n = m.numerator // m.denominator
+    rem = m - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * float(Fraction(n) * Fraction(2) ** qe)
+
+
+def _fmaf(a, b, c):
+    return _round_f32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def _fma64(a, b, c):
+    return float(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def _tiny_sq8_index(seed=0):
+    rng = np.random.default_rng(seed)
+    nlist, D, D_pad, T = 3, 20, 32, 64
+    sizes = [70, 5, 130]
+    vec_off = np.zeros(nlist + 1, np.int32)
+    vec_off[1:] = np.cumsum(sizes)
+    ntile = [(n + T - 1) // T for n in sizes]
+    tile_off = np.zeros(nlist + 1, np.int32)
+    tile_off[1:] = np.cumsum(ntile)
+    tiles = int(tile_off[-1])
+    N = int(vec_off[-1])
+    oids = rng.permutation(N).astype(np.int32)
+    tile_oids = np.full((tiles, T), -1, np.int32)
+    for c in range(nlist):
+        for l in range(sizes[c]):
+            tile_oids[tile_off[c] + l // T, l % T] = oids[vec_off[c] + l]
+    W = np.zeros((D, nlist + D_pad), np.float32)
+    W[:, :nlist] = rng.standard_normal((D, nlist)).astype(np.float32)
+    W[:, nlist:nlist + D] = rng.standard_normal((D, D)).astype(np.float32) / np.sqrt(D)
+    bvec = np.zeros(nlist + D_pad, np.float32)
+    bvec[nlist:nlist + D] = rng.standard_normal(D).astype(np.float32) * 0.1
+    vmin = (rng.standard_normal((nlist, D_pad)) - 3.0).astype(np.float32)
+    delta = (rng.random((nlist, D_pad)) * 0.05 + 0.01).astype(np.float32)
+    codes = rng.integers(0, 2**32, size=(tiles, D_pad // 4, T), dtype=np.uint64).astype(np.uint32)
+    xb = rng.standard_normal((N, D)).astype(np.float32)
+    xq = rng.standard_normal((4, D)).astype(np.float32)
+    ix = dict(W_combined=W, b_combined=bvec, nlist=nlist, D_pad=D_pad, vec_off=vec_off, tile_off=tile_off,
+              T=T, sq8_packed=codes, tile_oids=tile_oids, vmin=vmin, delta=delta, per_cluster=1, xb_sorted=xb)
+    return ix, xq
+
+
+def _exact_hats(ix, q, c):
+    """Every acc_hat of cluster c for query q, exact rational fmaf / fma (one rounding each)."""
+    nlist, D_pad, T = ix["nlist"], ix["D_pad"], ix["T"]
+    W, bvec = ix["W_combined"], ix["b_combined"]
+    xr = []
+    for j in range(D_pad):
+        acc = 0.0
+        for d in range(q.shape[0]):
+            acc = _fma64(q[d], W[d, nlist + j], acc)
+        xr.append(acc + float(bvec[nlist + j]))
+    base = [float(np.float32(float(ix["vmin"][c, d]) - xr[d])) for d in range(D_pad)]
+    out = []
+    v0, n, t0 = ix["vec_off"][c], ix["vec_off"][c + 1] - ix["vec_off"][c], ix["tile_off"][c]
+    for l in range(n):
+        tile, slot = t0 + l // T, l % T
+        acc = 0.0
+        for d in range(D_pad):
+            code = (int(ix["sq8_packed"][tile, d // 4, slot]) >> (8 * (d % 4))) & 0xFF
+            a = _fmaf(code, ix["delta"][c, d], base[d])
+            acc = _fmaf(a, a, acc)
+        out.append((acc, int(ix["tile_oids"][tile, slot]), v0 + l))
+    return out
+
+
+def _exact_dist(x, q):
+    acc = 0.0
+    for d in range(len(q)):
+        t = float(x[d]) - float(q[d])
+        acc = _fma64(t, t, acc)
+    return acc
+
+
+def test_sq8_hats_match_exact_rational_fmaf():
+    """Mode 1 with K = every vector returns every acc_hat, sorted by (acc_hat, id): bit-identical
+    to the exact-rational restatement (one rounding per fmaf, dims in order)."""
+    ix, xq = _tiny_sq8_index()
+    q = xq[:2]
+    N = int(ix["vec_off"][-1])
+    probes = np.array([[2, 0, 1], [1, 2, 0]], np.int32)
+    d, i = O.ivf_sq8(q, probes, 0, ix, N, N, N, 0)
+    for b in range(len(q)):
+        ref = sorted((h, oid) for c in range(3) for (h, oid, _) in _exact_hats(ix, q[b], c))
+        assert [oid for _, oid in ref] == i[b].tolist()
+        assert np.array_equal(np.array([h for h, _ in ref], np.float32), d[b])
+    # power of the check: an unfused a * a + acc, or the dims summed in reverse, change the
+    # bits of some of these hats (so an oracle written either way fails the comparison above)
+    c, nlist, D_pad, T = 2, ix["nlist"], ix["D_pad"], ix["T"]
+    xr = O.rotate_query(q[0], ix["W_combined"], ix["b_combined"], nlist, D_pad)
+    base = (ix["vmin"][c].astype(np.float64) - xr).astype(np.float32)
+    n_unfused = n_rev = 0
+    for h, _, spos in _exact_hats(ix, q[0], c)[:40]:
+        l = spos - ix["vec_off"][c]
+        tile, slot = ix["tile_off"][c] + l // T, l % T
+        codes = [(int(ix["sq8_packed"][tile, d // 4, slot]) >> (8 * (d % 4))) & 0xFF for d in range(D_pad)]
+        a = [_fmaf(codes[d], ix["delta"][c, d], base[d]) for d in range(D_pad)]
+        unfused = np.float32(0)
+        for d in range(D_pad):
+            unfused = np.float32(unfused + np.float32(np.float32(a[d]) * np.float32(a[d])))
+        rev = 0.0
+        for d in reversed(range(D_pad)):
+            rev = _fmaf(a[d], a[d], rev)
+        n_unfused += float(unfused) != h
+        n_rev += rev != h
+    assert n_unfused > 0 and n_rev > 0
+
+
+def _pool_ref(ix, q, probes, p_init, K, k1, k2, M):
+    pool = []
+    for p, c in enumerate(probes):
+        kp = k1 if p < p_init else k2
+        pool += sorted((h, oid, spos) for (h, oid, spos) in _exact_hats(ix, q, c))[:kp]
+    pool.sort()
+    if M == 0:
+        top = pool[:K]
+        return [h for h, _, _ in top], [oid for _, oid, _ in top]
+    ranked = sorted((_exact_dist(ix["xb_sorted"][spos], q), oid) for (_, oid, spos) in pool[:M])[:K]
+    return [float(np.float32(dd)) for dd, _ in ranked], [oid for _, oid in ranked]
+
+
+@pytest.mark.parametrize("K,k1,k2,M,p_init", [(5, 5, 5, 0, 1), (3, 12, 4, 9, 1), (4, 40, 6, 30, 2),
+                                               (10, 2, 3, 0, 0)])
+def test_sq8_pool_and_rerank_match_restatement(K, k1, k2, M, p_init):
+    """Per-pair truncation (k_p1 for the first p_init probes, k_p2 after), the pooled top-M and
+    the exact rerank, against the exact-rational restatement."""
+    ix, xq = _tiny_sq8_index(seed=1)
+    probes = np.array([[2, 0, 1], [0, 1, 2], [1, 2, 0], [2, 1, 0]], np.int32)
+    d, i = O.ivf_sq8(xq, probes, p_init, ix, K, k1, k2, M)
+    for b in range(len(xq)):
+        rd, ri = _pool_ref(ix, xq[b], probes[b], p_init, K, k1, k2, M)
+        n = len(ri)
+        assert i[b, :n].tolist() == ri and (i[b, n:] == -1).all()
+        assert np.array_equal(d[b, :n], np.array(rd, np.float32))
+
+
+def test_sq8_mode_plan_known_values():
+    """The reference's split and list lengths at hand-evaluated points
+    (src/trident_v4_kernels.cu:1264-1276, :1439-1443, :1071-1073)."""
+    assert O.sq8_mode_plan(0, 1000, 10, 32, 100) == (2, 100, 16, 100)
+    assert O.sq8_mode_plan(0, 1000, 10, 3, 100) == (1, 100, 42, 100)
+    assert O.sq8_mode_plan(0, 1000, 10, 8, 20) == (1, 20, 16, 20)
+    assert O.sq8_mode_plan(0, 1, 10, 8, 0) == (0, 10, 10, 0)
+    assert O.sq8_mode_plan(0, 64, 10, 1, 200) == (0, 128, 200, 200)
+    assert O.sq8_mode_plan(0, 64, 50, 16, 300) == (2, 128, 50, 200)
+    assert O.sq8_mode_plan(0, 64, 10, 16, 300) == (2, 128, 27, 200)
+    assert O.sq8_mode_plan(1, 1, 10, 8, 0) == (1, 10, 10, 0)
+    assert O.sq8_mode_plan(1, 500, 10, 64, 0) == (3, 10, 10, 0)

@@ -10,8 +10,12 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libtrident_hip.so")
 
 TRIDENT_OK = 0
+ABI_VERSION = 2  # TRIDENT_ABI_VERSION
+MODE_SQ8_RERANK = 0
+MODE_SQ8 = 1
 MODE_CASCADE = 2
 MODE_CM_EXACT = 10
+MODE_TRIBASE = 11
 
 _P = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -32,12 +36,14 @@ class TridentIndexView(ctypes.Structure):
         ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P), ("vec_Ar", _P),
         ("sq8_cells", _P),
         ("cent_rows", _P), ("cent_tiles", _P), ("cent_norms", _P), ("cent_norm_max", _f64),
+        ("r_vec_sorted", _P),
     ]
 
 
 class TridentSearchParams(ctypes.Structure):
     _fields_ = [("mode", _i32), ("B", _i32), ("K", _i32), ("nprobe", _i32),
-                ("ub_seed", _i32), ("use_l1", _i32), ("p_init", _i32), ("route", _i32)]
+                ("ub_seed", _i32), ("use_l1", _i32), ("p_init", _i32), ("route", _i32),
+                ("rerank_m", _i32)]
 
 
 ROUTE_AUTO, ROUTE_PAIR, ROUTE_BATCHED = 0, 1, 2
@@ -62,7 +68,7 @@ EXPORTS = {
     "trident_coarse_probe": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _i32, _P,
                                             ctypes.c_size_t, _P, _P, _i32, _P]),
     "trident_group_pairs": (ctypes.c_int, [_P, _i32, _i32, _i32, _i32, _i32, _P, _P, _P, _P, _P, _P, _P]),
-    "trident_p_init_rule": (_i32, [_i32, _i32, _i32, _i32]),
+    "trident_p_init_rule": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "trident_route_for": (_i32, [ctypes.POINTER(TridentIndexView), _i32, _i32, _i32, _i32]),
     "trident_sq8_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _P, _P, _P, _i32,
                                           _P, ctypes.c_size_t, _P, _P, _P]),
@@ -92,6 +98,9 @@ def lib():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
+        if L.trident_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {L.trident_abi_version()}, these bindings "
+                               f"expect {ABI_VERSION}: rebuild it")
         _LIB = L
     return _LIB
 

@@ -8,6 +8,8 @@
 //   fill / count / scan / scatter pairs                    (:1279-1289)
 //   pass 1: fill cand_cnt, pair_scan, merge  -> tau        (:1451-1512)
 //   pass 2: fill cand_cnt, pair_scan(tau), merge -> top-K  (:1514-1575)
+//   mode 0 with rerank_m > 0: merges keep the top M by acc_hat, rerank -> top-K
+//                                                          (:1487-1500, :1550-1566, :1044-1170)
 // Every launch goes on the caller's stream; no allocation, no host synchronisation.
 // Counters are cleared with a fill kernel (no memset nodes), so the sequence can be
 // captured in a graph.
@@ -158,7 +160,7 @@ inline int64_t cand_cap(int64_t nprobe, int64_t K, int64_t D_pad) {
 Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
     Carver c{static_cast<char*>(base)};
     Workspace w;
-    const int64_t KP = K <= 64 ? 64 : 128;
+    const int64_t KP = K <= 64 ? 64 : K <= 128 ? 128 : 256;
     const int64_t cap = cand_cap(nprobe, K, ix->D_pad);
     w.xq64 = c.take<double>(B * ix->D);
     w.xrot64 = c.take<double>(B * ix->D_pad);
@@ -278,28 +280,69 @@ ScanArgs make_scan_args(const TridentIndexView* ix, const Workspace& w, int K, i
     return a;
 }
 
-template <int KP, bool CASCADE, bool UB>
+template <int KP, int KIND>
 int launch_scan(const ScanArgs& a, hipStream_t st) {
     if (a.M <= 0) return TRIDENT_OK;
     const size_t dyn = scan_dyn_lds_bytes(a.D, a.D_pad);
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)pair_scan_kernel<KP, CASCADE, UB>,
+        hipError_t e = hipFuncSetAttribute((const void*)pair_scan_kernel<KP, KIND>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
         if (e != hipSuccess)
             return fail(TRIDENT_ERR_HIP, "hipFuncSetAttribute(pair_scan): %s", hipGetErrorString(e));
         attr_set = true;
     }
     const unsigned nx = (unsigned)((a.M + 7) / 8);
-    pair_scan_kernel<KP, CASCADE, UB><<<dim3(nx * 8), dim3(kBlock), dyn, st>>>(a);
+    pair_scan_kernel<KP, KIND><<<dim3(nx * 8), dim3(kBlock), dyn, st>>>(a);
     return check_launch("pair_scan_kernel");
 }
 
-template <int KP>
-int dispatch_scan(const ScanArgs& a, bool cascade, bool ub, hipStream_t st) {
-    if (!cascade) return launch_scan<KP, false, false>(a, st);
-    if (ub) return launch_scan<KP, true, true>(a, st);
-    return launch_scan<KP, true, false>(a, st);
+template <int KO>
+int launch_rerank(const RerankArgs& r, hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)rerank_kernel<KO>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 96 * 1024);
+        if (e != hipSuccess)
+            return fail(TRIDENT_ERR_HIP, "hipFuncSetAttribute(rerank): %s", hipGetErrorString(e));
+        attr_set = true;
+    }
+    rerank_kernel<KO><<<(unsigned)r.B, kBlock, (size_t)r.D * sizeof(double), st>>>(r);
+    return check_launch("rerank_kernel");
+}
+
+// Mode 0 reranks the top M = min(max(rerank_m, K), 200) entries by acc_hat (reference
+// :1439-1444, :1071-1073); its merged lists hold max(K, M) entries, every other mode's K.
+inline int64_t rerank_len(int mode, int64_t K, int64_t rerank_m) {
+    return mode == TRIDENT_MODE_SQ8_RERANK && rerank_m > 0
+               ? std::min<int64_t>(std::max<int64_t>(rerank_m, K), 200) : 0;
+}
+inline int64_t merged_list_len(int mode, int64_t K, int64_t rerank_m) {
+    return std::max<int64_t>(K, rerank_len(mode, K, rerank_m));
+}
+
+inline int list_kp(int64_t k) { return k <= 64 ? 64 : k <= 128 ? 128 : 256; }
+
+// One per-pair pass with a.K entries per pair (a.K <= 128, or <= 256 for kScanHat).
+int dispatch_scan(const ScanArgs& a, int kind, hipStream_t st) {
+    const int kp = list_kp(a.K);
+    switch (kind) {
+        case kScanCascade:
+            return kp == 64 ? launch_scan<64, kScanCascade>(a, st) : launch_scan<128, kScanCascade>(a, st);
+        case kScanCascadeUb:
+            return kp == 64 ? launch_scan<64, kScanCascadeUb>(a, st)
+                            : launch_scan<128, kScanCascadeUb>(a, st);
+        case kScanExact:
+            return kp == 64 ? launch_scan<64, kScanExact>(a, st) : launch_scan<128, kScanExact>(a, st);
+        case kScanTribase:
+            return kp == 64 ? launch_scan<64, kScanTribase>(a, st) : launch_scan<128, kScanTribase>(a, st);
+        case kScanHat:
+            return kp == 64    ? launch_scan<64, kScanHat>(a, st)
+                   : kp == 128 ? launch_scan<128, kScanHat>(a, st)
+                               : launch_scan<256, kScanHat>(a, st);
+        default:
+            return fail(TRIDENT_ERR_UNSUPPORTED, "scan kind %d", kind);
+    }
 }
 
 // Route of a mode-2 search.  The batched route needs the per-vector scalars, K <= 128 (a
@@ -428,8 +471,10 @@ int launch_merge(const MergeArgs& m, int KP, hipStream_t st) {
     const unsigned grid = (unsigned)((m.B + kWavesPerBlock - 1) / kWavesPerBlock);
     if (KP == 64)
         merge_kernel<64><<<grid, kBlock, 0, st>>>(m);
-    else
+    else if (KP == 128)
         merge_kernel<128><<<grid, kBlock, 0, st>>>(m);
+    else
+        merge_kernel<256><<<grid, kBlock, 0, st>>>(m);
     return check_launch("merge_kernel");
 }
 
@@ -595,8 +640,15 @@ int trident_abi_version(void) { return TRIDENT_ABI_VERSION; }
 
 const char* trident_last_error(void) { return g_last_error.c_str(); }
 
-int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe) {
-    if (mode != TRIDENT_MODE_CASCADE) return 0;
+int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe,
+                            int32_t rerank_m) {
+    if (mode == TRIDENT_MODE_SQ8_RERANK) {
+        if (nprobe <= 1 || (B == 1 && rerank_m == 0)) return 0;
+        if ((rerank_m > 20 || K > 10) && nprobe >= 4) return 2;
+        return 1;
+    }
+    if (mode != TRIDENT_MODE_CASCADE && mode != TRIDENT_MODE_SQ8 && mode != TRIDENT_MODE_TRIBASE)
+        return 0;
     if (nprobe <= 1) return 0;
     if (B == 1 && K <= 10) return 1;
     if (nprobe <= 16) return 2;
@@ -668,9 +720,12 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if (rc) return rc;
     if (!sp || !out) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "params/outputs are NULL");
     const int mode = sp->mode, B = sp->B, K = sp->K, nprobe = sp->nprobe;
-    if (mode != TRIDENT_MODE_CASCADE && mode != TRIDENT_MODE_CM_EXACT)
+    if (mode != TRIDENT_MODE_CASCADE && mode != TRIDENT_MODE_CM_EXACT &&
+        mode != TRIDENT_MODE_TRIBASE && mode != TRIDENT_MODE_SQ8 && mode != TRIDENT_MODE_SQ8_RERANK)
         return fail(TRIDENT_ERR_UNSUPPORTED,
-                    "mode %d is not supported (2 = cascade, 10 = cluster-major exact)", mode);
+                    "mode %d is not supported (0 = SQ8 + rerank, 1 = SQ8, 2 = cascade, 10 = "
+                    "cluster-major exact, 11 = Tribase)", mode);
+    if (sp->rerank_m < 0) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "rerank_m=%d", sp->rerank_m);
     if (B < 0) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "B=%d", B);
     if (K < 1 || K > 128) return fail(TRIDENT_ERR_UNSUPPORTED, "K=%d outside [1, 128]", K);
     if (nprobe < 1 || nprobe > ix->nlist || nprobe > 512)
@@ -686,20 +741,37 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if ((out->probe_cids || out->probe_dqcs) && out->probe_ld < nprobe)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "probe_ld=%d < nprobe=%d", out->probe_ld, nprobe);
     const bool cascade = mode == TRIDENT_MODE_CASCADE;
-    if (cascade && (rc = validate_cascade_index(ix))) return rc;
+    // modes 0 / 1: SQ8 reconstruction distance in the rotated space
+    const bool hat = mode == TRIDENT_MODE_SQ8 || mode == TRIDENT_MODE_SQ8_RERANK;
+    if ((cascade || hat) && (rc = validate_cascade_index(ix))) return rc;
     if (sp->use_l1 && cascade && !ix->tile_r_minmax)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "use_l1 needs tile_r_minmax");
+    if (mode == TRIDENT_MODE_TRIBASE && !ix->r_vec_sorted)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "mode 11 needs r_vec_sorted");
+    // Mode 0 with a rerank: pass p keeps k_p entries per pair (reference :1439-1443, K_LOC :576)
+    const int64_t eff_rr = mode == TRIDENT_MODE_SQ8_RERANK && sp->rerank_m > 0
+                               ? std::max<int64_t>(sp->rerank_m, K) : 0;
+    const int64_t M_rr = rerank_len(mode, K, sp->rerank_m);
+    int64_t k_p1 = K, k_p2 = K;
+    if (eff_rr > 0) {
+        k_p1 = std::min<int64_t>(eff_rr, 128);
+        k_p2 = std::min<int64_t>(
+            eff_rr, std::max<int64_t>(K, std::max<int64_t>(16, (eff_rr + nprobe - 1) / nprobe + 8)));
+        k_p2 = std::min<int64_t>(k_p2, 200);
+    }
+    const int64_t K_list = merged_list_len(mode, K, sp->rerank_m);
     if (B == 0) return TRIDENT_OK;
     if (!xq) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "xq is NULL");
 
-    Workspace w = carve(ix, workspace, B, nprobe, K);
+    Workspace w = carve(ix, workspace, B, nprobe, K_list);
     if (!workspace || workspace_bytes < w.bytes)
         return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu < %zu bytes", workspace_bytes,
                     w.bytes);
     hipStream_t st = static_cast<hipStream_t>(stream);
 
-    int p_init = sp->p_init >= 0 ? sp->p_init : trident_p_init_rule(mode, B, K, nprobe);
-    if (!cascade) p_init = 0;
+    int p_init =
+        sp->p_init >= 0 ? sp->p_init : trident_p_init_rule(mode, B, K, nprobe, sp->rerank_m);
+    if (mode == TRIDENT_MODE_CM_EXACT) p_init = 0;
     if (p_init > nprobe) p_init = nprobe;
 
     // Probes always land in the workspace (row stride nprobe); the caller's buffers, when
@@ -714,8 +786,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                                : fail(TRIDENT_ERR_HIP, "hipEventRecord: %s", hipGetErrorString(e));
     };
     if ((rc = mark(TRIDENT_EV_START))) return rc;
-    if ((rc = run_front_end(ix, xq, B, nprobe, cascade, w, out->probe_cids, out->probe_dqcs,
-                            out->probe_ld, st)))
+    if ((rc = run_front_end(ix, xq, B, nprobe, cascade || hat, w, out->probe_cids,
+                            out->probe_dqcs, out->probe_ld, st)))
         return rc;
     if ((rc = mark(TRIDENT_EV_PROBED))) return rc;
 
@@ -734,17 +806,19 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         return rc;
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
-    const int KP = K <= 64 ? 64 : 128;
-    const int64_t cap = cand_cap(nprobe, K, ix->D_pad);
+    const int KP = list_kp(K_list);
+    const int64_t cap = cand_cap(nprobe, K_list, ix->D_pad);
     if (out->stats) {
         if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
         if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
     }
     ScanArgs a = make_scan_args(ix, w, K, cap, cascade ? sp->use_l1 : 0,
                                 out->stats ? w.stat_slots : nullptr);
+    a.r_vec = ix->r_vec_sorted;
     MergeArgs m{};
     m.B = B;
-    m.K = K;
+    m.K = (int)K_list;
+    m.hat = hat ? 1 : 0;
     m.cap = (int)cap;
     m.cand_key = w.cand_key;
     m.cand_id = w.cand_id;
@@ -901,20 +975,29 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         return TRIDENT_OK;
     }
 
+    // the scan kind of each pass
+    const int kind1 = cascade ? (sp->ub_seed != 0 ? kScanCascadeUb : kScanCascade)
+                      : hat   ? kScanHat
+                      : mode == TRIDENT_MODE_TRIBASE ? kScanTribase
+                                                     : kScanExact;
+    const int kind2 = cascade ? (sp->ub_seed == 2 || (sp->ub_seed == 1 && M1 == 0) ? kScanCascadeUb
+                                                                                   : kScanCascade)
+                              : kind1;
+    // mode 0 with a rerank: the merges only build the top-M list; rerank_kernel writes the outputs
+    const bool rerank = eff_rr > 0;
     if (M1 > 0) {
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;
         a.pair_cid = p1c;
         a.pair_qid = p1q;
         a.pair_dqc = pd ? p1d : nullptr;
         a.M = (int)M1;
+        a.K = (int)k_p1;
         a.tau_in = nullptr;
-        const bool ub1 = cascade && sp->ub_seed != 0;
-        rc = KP == 64 ? dispatch_scan<64>(a, cascade, ub1, st) : dispatch_scan<128>(a, cascade, ub1, st);
-        if (rc) return rc;
+        if ((rc = dispatch_scan(a, kind1, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
         m.use_prev = 0;
         m.tau_sq_out = out->tau_sq;
-        const bool last = M2 == 0;
+        const bool last = M2 == 0 && !rerank;
         m.out_d = last ? out->topk_d : nullptr;
         m.out_i = last ? out->topk_i : nullptr;
         if ((rc = launch_merge(m, KP, st))) return rc;
@@ -928,18 +1011,33 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         a.pair_qid = p2q;
         a.pair_dqc = pd ? p2d : nullptr;
         a.M = (int)M2;
-        a.tau_in = M1 > 0 ? w.tau64 : nullptr;
-        const bool ub2 = cascade && (sp->ub_seed == 2 || (sp->ub_seed == 1 && M1 == 0));
-        rc = KP == 64 ? dispatch_scan<64>(a, cascade, ub2, st) : dispatch_scan<128>(a, cascade, ub2, st);
-        if (rc) return rc;
+        a.K = (int)k_p2;
+        // acc_hat lists take no threshold: tau64 bounds exact distances only
+        a.tau_in = M1 > 0 && !hat ? w.tau64 : nullptr;
+        if ((rc = dispatch_scan(a, kind2, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
         m.use_prev = M1 > 0 ? 1 : 0;
         m.tau_sq_out = M1 > 0 ? nullptr : out->tau_sq;
-        m.out_d = out->topk_d;
-        m.out_i = out->topk_i;
+        m.out_d = rerank ? nullptr : out->topk_d;
+        m.out_i = rerank ? nullptr : out->topk_i;
         if ((rc = launch_merge(m, KP, st))) return rc;
     } else if ((rc = mark(TRIDENT_EV_P2_SCAN))) {
         return rc;
+    }
+    if (rerank) {
+        RerankArgs r{};
+        r.B = B;
+        r.K = K;
+        r.M = (int)M_rr;
+        r.list_key = w.list_key;
+        r.list_id = w.list_id;
+        r.KP = KP;
+        r.xb = ix->xb_sorted;
+        r.xq64 = w.xq64;
+        r.D = ix->D;
+        r.out_d = out->topk_d;
+        r.out_i = out->topk_i;
+        if ((rc = K <= 64 ? launch_rerank<64>(r, st) : launch_rerank<128>(r, st))) return rc;
     }
     if ((rc = mark(TRIDENT_EV_END))) return rc;
     if (out->stats) {
@@ -959,7 +1057,8 @@ int trident_search_noalloc(const TridentIndexView* ix, const TridentSearchParams
                     sp->nprobe);
     // the size check comes before any HIP call, so an oversized request fails without touching
     // the device
-    const size_t need = carve(ix, nullptr, sp->B, sp->nprobe, sp->K).bytes;
+    const size_t need =
+        carve(ix, nullptr, sp->B, sp->nprobe, merged_list_len(sp->mode, sp->K, sp->rerank_m)).bytes;
     if (need > (size_t)TRIDENT_NOALLOC_SCRATCH_BYTES)
         return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL,
                     "trident_search_noalloc: B=%d nprobe=%d K=%d needs %zu bytes of scratch, more "

@@ -7,13 +7,15 @@
 // and sort after every real candidate (NaN distances sort after +inf).
 //
 // Top-K lists live in registers of one wave64: a 64-entry list is one entry per lane, a
-// 128-entry list two entries per lane, both sorted ascending across lanes.  Inserting a
+// 128- (256-) entry list two (four) entries per lane, sorted ascending across lanes.  Inserting a
 // batch of up to 64 candidates is a register bitonic sort of the batch followed by a
 // bitonic merge with the list -- no LDS, no block barrier, no single-lane insertion loop.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 namespace trident {
 
@@ -162,6 +164,90 @@ struct WaveList<128> {
         i1 = hi_i;
     }
 };
+
+// Two sorted 64-entry sequences (a, b) -> the 64 smallest (a) and 64 largest (b) of their union,
+// each sorted: min / max of a[i] and b[63 - i] are bitonic.
+__device__ __forceinline__ void merge_halves(uint64_t& ak, int32_t& ai, uint64_t& bk, int32_t& bi) {
+    const uint64_t rk = shfl_xor_u64(bk, kWave - 1);
+    const int32_t ri = __shfl_xor(bi, kWave - 1, kWave);
+    const bool r_lo = ent_less(rk, ri, ak, ai);
+    uint64_t lo_k = r_lo ? rk : ak, hi_k = r_lo ? ak : rk;
+    int32_t lo_i = r_lo ? ri : ai, hi_i = r_lo ? ai : ri;
+    wave_merge64(lo_k, lo_i);
+    wave_merge64(hi_k, hi_i);
+    ak = lo_k;
+    ai = lo_i;
+    bk = hi_k;
+    bi = hi_i;
+}
+
+// Best 256 candidates seen: chunk c (k_c / i_c) holds ranks 64 c .. 64 c + 63.
+template <>
+struct WaveList<256> {
+    uint64_t k0, k1, k2, k3;
+    int32_t i0, i1, i2, i3;
+    __device__ __forceinline__ void init() {
+        k0 = k1 = k2 = k3 = kKeyInvalid;
+        i0 = i1 = i2 = i3 = kIdInvalid;
+    }
+    // (reads lane l of every chunk and selects among the values: a select among the members
+    // themselves becomes a dynamically indexed stack array)
+    __device__ __forceinline__ void at(int idx, uint64_t& k, int32_t& i) const {
+        const int c = idx >> 6, l = idx & (kWave - 1);
+        const uint64_t r0 = readlane_u64(k0, l), r1 = readlane_u64(k1, l);
+        const uint64_t r2 = readlane_u64(k2, l), r3 = readlane_u64(k3, l);
+        const int32_t j0 = __builtin_amdgcn_readlane(i0, l), j1 = __builtin_amdgcn_readlane(i1, l);
+        const int32_t j2 = __builtin_amdgcn_readlane(i2, l), j3 = __builtin_amdgcn_readlane(i3, l);
+        k = c == 0 ? r0 : c == 1 ? r1 : c == 2 ? r2 : r3;
+        i = c == 0 ? j0 : c == 1 ? j1 : c == 2 ? j2 : j3;
+    }
+    __device__ __forceinline__ void insert(uint64_t bk, int32_t bi) {
+        wave_sort64(bk, bi);
+        uint64_t rk = shfl_xor_u64(bk, kWave - 1);
+        int32_t ri = __shfl_xor(bi, kWave - 1, kWave);
+        // Ranks 0..191 survive a 64-entry batch; ranks 192..255 become the smallest 64 of
+        // (chunk 3, batch).  That chunk then bubbles down: each chunk holds entries no smaller
+        // than all 64 of the chunk below it, so the largest 64 of (chunk c, carried chunk) are
+        // ranks 64 c + 64 .. of the whole list.
+        if (ent_less(rk, ri, k3, i3)) {
+            k3 = rk;
+            i3 = ri;
+        }
+        wave_merge64(k3, i3);
+        merge_halves(k2, i2, k3, i3);
+        merge_halves(k1, i1, k2, i2);
+        merge_halves(k0, i0, k1, i1);
+    }
+};
+
+// Chunk C (ranks 64 C .. 64 C + 63, one per lane) of a list.
+template <int C, int KP>
+__device__ __forceinline__ void list_chunk(const WaveList<KP>& L, uint64_t& k, int32_t& i) {
+    if constexpr (C == 0) {
+        k = L.k0;
+        i = L.i0;
+    } else if constexpr (C == 1) {
+        k = L.k1;
+        i = L.i1;
+    } else if constexpr (C == 2) {
+        k = L.k2;
+        i = L.i2;
+    } else {
+        k = L.k3;
+        i = L.i3;
+    }
+}
+
+// f(std::integral_constant<int, C>) for every chunk C of a KP-entry list, in order.
+template <int KP, typename F>
+__device__ __forceinline__ void for_chunks(F&& f) {
+    f(std::integral_constant<int, 0>{});
+    if constexpr (KP >= 128) f(std::integral_constant<int, 1>{});
+    if constexpr (KP == 256) {
+        f(std::integral_constant<int, 2>{});
+        f(std::integral_constant<int, 3>{});
+    }
+}
 
 // Offers one candidate per lane; only entries that beat the current K-th entry are merged.
 // Returns true (wave-uniform) when the list changed.

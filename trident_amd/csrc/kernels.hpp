@@ -27,7 +27,8 @@ struct ScanArgs {
     // pairs of this pass, grouped by cluster
     const int32_t* pair_cid;
     const int32_t* pair_qid;
-    const float* pair_dqc;      // |q - c| per pair (use_l1) or null
+    const float* pair_dqc;      // |q - c| per pair (use_l1, Tribase) or null
+    const float* r_vec;         // [N] |x - c| in sorted order (Tribase) or null
     int M;
     // per-query threshold from the previous pass (float64), or null
     const double* tau_in;
@@ -35,7 +36,7 @@ struct ScanArgs {
     uint64_t* cand_key;
     int32_t* cand_id;
     int32_t* cand_cnt;
-    int cap, K;
+    int cap, K;                 // K: entries kept (and emitted) per pair
     unsigned long long* stats;  // [4] or null
     double lb_scale;            // tau -> float32 Stage Y threshold factor
     double ub_scale;            // Stage X sum -> float64 distance bound factor
@@ -49,6 +50,9 @@ struct MergeArgs {
     uint64_t* list_key;   // [B, KP] per-query running top list
     int32_t* list_id;
     int use_prev;
+    // 1: keys are (acc_hat bits, original id) (kScanHat): out_d / tau_sq_out receive acc_hat,
+    // out_i the original id, tau64 is set to +inf
+    int hat;
     double* tau64;        // [B] K-th distance after this merge (+inf if fewer than K)
     float* out_d;         // [B, K] or null (final pass only)
     int64_t* out_i;
@@ -247,11 +251,38 @@ __global__ void scatter_pairs_lds_kernel(const int32_t* __restrict__ probe_cids,
                                          int32_t* __restrict__ p2_qids,
                                          float* __restrict__ p2_dqcs);
 
-template <int KP, bool CASCADE, bool UB>
+// Routes of pair_scan_kernel (one per reference mode family).
+enum ScanKind {
+    kScanCascade = 0,    // mode 2, Stage Y / Z
+    kScanCascadeUb = 1,  // mode 2, Stage X seeding + Stage Y / Z
+    kScanExact = 2,      // mode 10, every vector refined exactly
+    kScanTribase = 3,    // mode 11, exact with the per-vector triangle-inequality skip
+    kScanHat = 4         // modes 0 / 1, SQ8 reconstruction distance, no refinement
+};
+
+template <int KP, int KIND>
 __global__ void pair_scan_kernel(ScanArgs a);
 
 template <int KP>
 __global__ void merge_kernel(MergeArgs a);
+
+// Mode 0's rerank: one workgroup per query takes the M <= 256 entries of its merged list
+// (kScanHat keys, sorted positions as ids), computes their canonical float64 distances and
+// writes the K best by (distance, original id).
+struct RerankArgs {
+    int B, K, M;
+    const uint64_t* list_key;  // [B, KP]
+    const int32_t* list_id;
+    int KP;
+    const float* xb;
+    const double* xq64;        // [B, D]
+    int D;
+    float* out_d;              // [B, K]
+    int64_t* out_i;
+};
+
+template <int KO>
+__global__ void rerank_kernel(RerankArgs a);
 
 // Batched-route work units: queries of one cluster x one slice of ~kSplitVec vectors (at most
 // kMaxSplit slices per cluster).  Seeding units hold <= 16 of the cluster's pass-1 queries;

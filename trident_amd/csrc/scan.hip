@@ -20,8 +20,19 @@
 //                    merged at the end and the pair emits at most K entries
 //                    (reference :943-961 emission, :19-60 ordering).
 //
-// CM route (CASCADE == false, reference mode 10, :268-374): no Stage X/Y, every vector is
-// refined exactly.
+// The kernel's KIND (enum ScanKind) selects the route:
+//   kScanCascade / kScanCascadeUb   mode 2 (Stage Y / Z, with Stage X seeding for the latter);
+//   kScanExact                      mode 10, CM-FP32 (reference :268-374): no Stage X/Y, every
+//                                   vector refined exactly;
+//   kScanTribase                    mode 11, Tribase (reference :379-521): as kScanExact, but a
+//                                   vector with | |q - c| - |x - c| | > sqrt(tau) is not refined
+//                                   (triangle inequality, margins for the float32 norms);
+//   kScanHat                        modes 0 / 1 (reference :529-962, MODE 0 / 1): no refinement;
+//                                   vectors are ranked by their SQ8 reconstruction distance in
+//                                   the rotated space, acc_hat = sum_d fmaf(code_d, delta_d,
+//                                   base_d)^2 in dimension order (base_d = fl32(vmin_d - q_rot,d)),
+//                                   keyed (acc_hat bits, original id) with the sorted position as
+//                                   the entry's id.
 //
 // Rigour.  Stage Y prunes x when  lb_f32(x) > round_up(tau * lb_scale)  with
 // lb_scale = rot_sq_max * (1 + rho) * (1 + 1e-12), rho = (D_pad + 4) * 2^-24.  Per dimension
@@ -95,22 +106,79 @@ __device__ __forceinline__ void list_store(const WaveList<KP>& L, uint64_t* k, i
     const int lane = lane_id();
     k[lane] = L.k0;
     i[lane] = L.i0;
-    if constexpr (KP == 128) {
+    if constexpr (KP >= 128) {
         k[kWave + lane] = L.k1;
         i[kWave + lane] = L.i1;
     }
+    if constexpr (KP == 256) {
+        k[2 * kWave + lane] = L.k2;
+        i[2 * kWave + lane] = L.i2;
+        k[3 * kWave + lane] = L.k3;
+        i[3 * kWave + lane] = L.i3;
+    }
 }
+
+template <int KP>
+__device__ __forceinline__ void list_load(WaveList<KP>& L, const uint64_t* k, const int32_t* i) {
+    const int lane = lane_id();
+    L.k0 = k[lane];
+    L.i0 = i[lane];
+    if constexpr (KP >= 128) {
+        L.k1 = k[kWave + lane];
+        L.i1 = i[kWave + lane];
+    }
+    if constexpr (KP == 256) {
+        L.k2 = k[2 * kWave + lane];
+        L.i2 = i[2 * kWave + lane];
+        L.k3 = k[3 * kWave + lane];
+        L.i3 = i[3 * kWave + lane];
+    }
+}
+
 
 template <int KP>
 __device__ __forceinline__ void list_absorb(WaveList<KP>& L, int K, const uint64_t* k,
                                             const int32_t* i) {
     const int lane = lane_id();
-    list_offer(L, K, k[lane], i[lane]);
-    if constexpr (KP == 128) list_offer(L, K, k[kWave + lane], i[kWave + lane]);
+    for_chunks<KP>([&](auto cc) __attribute__((always_inline)) {
+        constexpr int c = decltype(cc)::value;
+        if (c * kWave < K) list_offer(L, K, k[c * kWave + lane], i[c * kWave + lane]);
+    });
 }
 
-template <int KP, bool CASCADE, bool UB>
+__device__ __forceinline__ float hat_step(uint32_t code, float dl, float bs, float acc) {
+    const float a = fmaf((float)code, dl, bs);
+    return fmaf(a, a, acc);
+}
+
+__device__ __forceinline__ float sq8_hat(const uint32_t* cp, int T, int D4, const float* s_base,
+                                         const float* s_dlt) {
+    float acc = 0.0f;
+#pragma unroll 4
+    for (int d4 = 0; d4 < D4; ++d4) {
+        const uint32_t w = cp[(size_t)d4 * T];
+        const float4 bs = *reinterpret_cast<const float4*>(s_base + 4 * d4);
+        const float4 dl = *reinterpret_cast<const float4*>(s_dlt + 4 * d4);
+        acc = hat_step(w & 0xffu, dl.x, bs.x, acc);
+        acc = hat_step((w >> 8) & 0xffu, dl.y, bs.y, acc);
+        acc = hat_step((w >> 16) & 0xffu, dl.z, bs.z, acc);
+        acc = hat_step(w >> 24, dl.w, bs.w, acc);
+    }
+    return acc;
+}
+
+// Key of a kScanHat entry: ordered by (acc_hat, original id); acc_hat >= 0.
+__device__ __forceinline__ uint64_t hat_key(float acc_hat, int32_t oid) {
+    return ((uint64_t)__float_as_uint(acc_hat) << 32) | (uint32_t)oid;
+}
+
+template <int KP, int KIND>
 __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
+    constexpr bool CASCADE = KIND == kScanCascade || KIND == kScanCascadeUb;
+    constexpr bool UB = KIND == kScanCascadeUb;
+    constexpr bool TRI = KIND == kScanTribase;
+    constexpr bool HAT = KIND == kScanHat;
+    constexpr bool SQ8 = CASCADE || HAT;  // reads the codes
     extern __shared__ __align__(16) unsigned char dyn_smem[];
     __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
     __shared__ int32_t s_qspos[kWavesPerBlock][kQueueCap];
@@ -144,7 +212,7 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
 
     const double tau_init = a.tau_in ? a.tau_in[q] : (double)INFINITY;
     for (int d = tid; d < D; d += kBlock) s_q64[d] = a.xq64[(size_t)q * D + d];
-    if constexpr (CASCADE) {
+    if constexpr (SQ8) {
         const size_t off = a.per_cluster ? (size_t)cid * D_pad : 0;
         const double* xr = a.xrot64 + (size_t)q * D_pad;
         const double* qe = a.qerr + (size_t)q * D_pad;
@@ -231,6 +299,37 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
         const int li = s * kWave + lane;
         const bool valid = li < n;
         bool alive = valid;
+        if constexpr (HAT) {
+            // no refinement: the lane's vector enters the wave list by its reconstruction distance
+            const int tile = s / (T / kWave), sub = s % (T / kWave);
+            const uint32_t* cp = sq8c + (size_t)tile * D4 * T + sub * kWave + lane;
+            const float hat = valid ? sq8_hat(cp, T, D4, s_base, s_dlt) : 0.0f;
+            const int32_t oid = valid ? a.tile_oids[(size_t)t0 * T + li] : 0;
+            if (a.stats) {
+                const int nv = __popcll(__ballot(valid));
+                st_cand += nv;
+                st_dims += (unsigned long long)nv * (unsigned)D_pad;
+            }
+            list_offer(L, K, valid ? hat_key(hat, oid) : kKeyInvalid, valid ? v0 + li : kIdInvalid);
+            continue;
+        }
+        if constexpr (TRI) {
+            // Tribase: |q - x| >= | |q - c| - |x - c| |.  Both norms are float32 values within
+            // 1e-5 (relative) of the exact ones (|q - c| is the rounded float64 norm, |x - c| the
+            // index's r_vec_sorted); thr is this wave's running K-th distance, so a skipped
+            // vector has d64 > thr and cannot enter the top K.
+            if (a.stats) st_cand += __popcll(__ballot(valid));
+            if (valid && thr < (double)INFINITY) {
+                const double dqc = (double)a.pair_dqc[p], rx = (double)a.r_vec[v0 + li];
+                const double tol = 1e-5 * (dqc + rx) + 1e-30;
+                if (fabs(dqc - rx) - tol > sqrt(thr) * (1.0 + 1e-6)) alive = false;
+            }
+            if (a.stats) {
+                const int na = __popcll(__ballot(alive));
+                st_dims += (unsigned long long)na * (unsigned)D;
+                st_surv += na;
+            }
+        }
         if constexpr (CASCADE) {
             const int tile = s / (T / kWave), sub = s % (T / kWave);
             const float tau_s = __uint_as_float(__atomic_load_n(&s_tau_bits, __ATOMIC_RELAXED));
@@ -315,31 +414,32 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
     __syncthreads();
     if (wid != 0) return;
     for (int w = 1; w < kWavesPerBlock; ++w) list_absorb(L, K, s_ck + w * KP, s_ci + w * KP);
-    const bool e0 = lane < K && L.k0 != kKeyInvalid;
-    const uint64_t m0 = __ballot(e0);
-    int cnt = __popcll(m0);
-    bool e1 = false;
-    if constexpr (KP == 128) {
-        e1 = kWave + lane < K && L.k1 != kKeyInvalid;
-        cnt += __popcll(__ballot(e1));
-    }
+    // valid entries are a prefix of the sorted list
+    int cnt = 0;
+    for_chunks<KP>([&](auto cc) __attribute__((always_inline)) {
+        constexpr int c = decltype(cc)::value;
+        uint64_t k;
+        int32_t i;
+        list_chunk<c>(L, k, i);
+        cnt += __popcll(__ballot(c * kWave + lane < K && k != kKeyInvalid));
+    });
     if (cnt == 0) return;
     int base = 0;
     if (lane == 0) base = atomicAdd(&a.cand_cnt[q], cnt);
     base = __builtin_amdgcn_readfirstlane(base);
-    if (base + cnt > a.cap) return;  // unreachable: cap = nprobe * K
+    if (base + cnt > a.cap) return;  // unreachable: cap >= nprobe * K
     uint64_t* ck = a.cand_key + (size_t)q * a.cap + base;
     int32_t* ci = a.cand_id + (size_t)q * a.cap + base;
-    if (e0) {
-        ck[lane] = L.k0;
-        ci[lane] = L.i0;
-    }
-    if constexpr (KP == 128) {
-        if (e1) {
-            ck[kWave + lane] = L.k1;
-            ci[kWave + lane] = L.i1;
+    for_chunks<KP>([&](auto cc) __attribute__((always_inline)) {
+        constexpr int c = decltype(cc)::value;
+        uint64_t k;
+        int32_t i;
+        list_chunk<c>(L, k, i);
+        if (c * kWave + lane < cnt) {
+            ck[c * kWave + lane] = k;
+            ci[c * kWave + lane] = i;
         }
-    }
+    });
 }
 
 // Sums the kStatSlots telemetry slots into the caller's int64[4] (added to its contents).
@@ -362,14 +462,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     L.init();
     uint64_t* lk = a.list_key + (size_t)q * KP;
     int32_t* li = a.list_id + (size_t)q * KP;
-    if (a.use_prev) {
-        L.k0 = lk[lane];
-        L.i0 = li[lane];
-        if constexpr (KP == 128) {
-            L.k1 = lk[kWave + lane];
-            L.i1 = li[kWave + lane];
-        }
-    }
+    if (a.use_prev) list_load(L, lk, li);
     const int raw = a.cand_cnt[q];
     if (raw > a.cap && a.probe_cids) {
         // Overflowed list: rescan every probed vector exactly (canonical float64 distance).
@@ -410,25 +503,86 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     L.at(a.K - 1, kk, ki);
     const bool full = kk != kKeyInvalid;
     if (lane == 0) {
-        a.tau64[q] = full ? dist_of(kk) : (double)INFINITY;
-        if (a.tau_sq_out) a.tau_sq_out[q] = full ? __double2float_ru(dist_of(kk)) : INFINITY;
+        if (a.hat) {
+            // acc_hat orders the list but bounds no exact distance
+            a.tau64[q] = (double)INFINITY;
+            if (a.tau_sq_out) a.tau_sq_out[q] = full ? __uint_as_float((uint32_t)(kk >> 32)) : INFINITY;
+        } else {
+            a.tau64[q] = full ? dist_of(kk) : (double)INFINITY;
+            if (a.tau_sq_out) a.tau_sq_out[q] = full ? __double2float_ru(dist_of(kk)) : INFINITY;
+        }
     }
     if (a.out_d) {
         float* od = a.out_d + (size_t)q * a.K;
         int64_t* oi = a.out_i + (size_t)q * a.K;
-        if (lane < a.K) {
-            const bool v = L.k0 != kKeyInvalid;
-            od[lane] = v ? (float)dist_of(L.k0) : INFINITY;
-            oi[lane] = v ? (int64_t)L.i0 : -1;
-        }
-        if constexpr (KP == 128) {
-            if (kWave + lane < a.K) {
-                const bool v = L.k1 != kKeyInvalid;
-                od[kWave + lane] = v ? (float)dist_of(L.k1) : INFINITY;
-                oi[kWave + lane] = v ? (int64_t)L.i1 : -1;
+        for_chunks<KP>([&](auto cc) __attribute__((always_inline)) {
+            constexpr int c = decltype(cc)::value;
+            uint64_t k;
+            int32_t i;
+            list_chunk<c>(L, k, i);
+            const int r = c * kWave + lane;
+            if (r < a.K) {
+                const bool v = k != kKeyInvalid;
+                if (a.hat) {
+                    od[r] = v ? __uint_as_float((uint32_t)(k >> 32)) : INFINITY;
+                    oi[r] = v ? (int64_t)(int32_t)(uint32_t)k : -1;
+                } else {
+                    od[r] = v ? (float)dist_of(k) : INFINITY;
+                    oi[r] = v ? (int64_t)i : -1;
+                }
             }
-        }
+        });
     }
+}
+
+// Mode 0's exact rerank of the merged top-M list (RerankArgs).  Wave w refines list entries
+// 64 w .. 64 w + 63 with the per-pair scan's staged float64 rows (refine_rows), keys them
+// (distance, original id) and the workgroup keeps the K <= KO best.
+template <int KO>
+__global__ __launch_bounds__(256) void rerank_kernel(RerankArgs a) {
+    extern __shared__ __align__(16) unsigned char dyn_smem[];
+    __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
+    __shared__ int32_t s_spos[kWavesPerBlock][kWave];
+    __shared__ uint64_t s_ok[kWavesPerBlock][KO];
+    __shared__ int32_t s_oi[kWavesPerBlock][KO];
+    const int q = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+    double* s_q64 = reinterpret_cast<double*>(dyn_smem);
+    for (int d = tid; d < a.D; d += kBlock) s_q64[d] = a.xq64[(size_t)q * a.D + d];
+    __syncthreads();
+    const int r = wid * kWave + lane;
+    const bool in = r < a.M && r < a.KP;
+    const uint64_t hk = in ? a.list_key[(size_t)q * a.KP + r] : kKeyInvalid;
+    const bool v = hk != kKeyInvalid;
+    const int32_t spos = v ? a.list_id[(size_t)q * a.KP + r] : 0;
+    // valid entries are a prefix of the sorted list, so each wave's are a prefix of its 64
+    const int nv = __popcll(__ballot(v));
+    s_spos[wid][lane] = spos;
+    wave_sync();
+    double d64 = 0.0;
+    if (nv > 0) d64 = refine_rows(a.xb, a.D, s_spos[wid], nv, s_stage[wid], s_q64);
+    WaveList<KO> L;
+    L.init();
+    list_offer(L, a.K, v ? key_of(d64) : kKeyInvalid, v ? (int32_t)(uint32_t)hk : kIdInvalid);
+    list_store(L, s_ok[wid], s_oi[wid]);
+    __syncthreads();
+    if (wid != 0) return;
+    for (int w = 1; w < kWavesPerBlock; ++w) list_absorb(L, a.K, s_ok[w], s_oi[w]);
+    float* od = a.out_d + (size_t)q * a.K;
+    int64_t* oi = a.out_i + (size_t)q * a.K;
+    for_chunks<KO>([&](auto cc) __attribute__((always_inline)) {
+        constexpr int c = decltype(cc)::value;
+        uint64_t k;
+        int32_t i;
+        list_chunk<c>(L, k, i);
+        const int rr = c * kWave + lane;
+        if (rr < a.K) {
+            const bool ok = k != kKeyInvalid;
+            od[rr] = ok ? (float)dist_of(k) : INFINITY;
+            oi[rr] = ok ? (int64_t)i : -1;
+        }
+    });
 }
 
 // One thread per (query, sorted position) pair: the Stage Y lower bound and the Stage X
@@ -464,13 +618,21 @@ __global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,
     ub[i] = (double)acc_u * a.ub_scale;
 }
 
-template __global__ void pair_scan_kernel<64, true, false>(ScanArgs);
-template __global__ void pair_scan_kernel<64, true, true>(ScanArgs);
-template __global__ void pair_scan_kernel<64, false, false>(ScanArgs);
-template __global__ void pair_scan_kernel<128, true, false>(ScanArgs);
-template __global__ void pair_scan_kernel<128, true, true>(ScanArgs);
-template __global__ void pair_scan_kernel<128, false, false>(ScanArgs);
+template __global__ void pair_scan_kernel<64, kScanCascade>(ScanArgs);
+template __global__ void pair_scan_kernel<64, kScanCascadeUb>(ScanArgs);
+template __global__ void pair_scan_kernel<64, kScanExact>(ScanArgs);
+template __global__ void pair_scan_kernel<64, kScanTribase>(ScanArgs);
+template __global__ void pair_scan_kernel<64, kScanHat>(ScanArgs);
+template __global__ void pair_scan_kernel<128, kScanCascade>(ScanArgs);
+template __global__ void pair_scan_kernel<128, kScanCascadeUb>(ScanArgs);
+template __global__ void pair_scan_kernel<128, kScanExact>(ScanArgs);
+template __global__ void pair_scan_kernel<128, kScanTribase>(ScanArgs);
+template __global__ void pair_scan_kernel<128, kScanHat>(ScanArgs);
+template __global__ void pair_scan_kernel<256, kScanHat>(ScanArgs);
 template __global__ void merge_kernel<64>(MergeArgs);
 template __global__ void merge_kernel<128>(MergeArgs);
+template __global__ void merge_kernel<256>(MergeArgs);
+template __global__ void rerank_kernel<64>(RerankArgs);
+template __global__ void rerank_kernel<128>(RerankArgs);
 
 }  // namespace trident

@@ -16,9 +16,15 @@ Differences from the reference, all stricter supersets:
   The reference workspace tensors (proj_buf, cdists_buf, p1_*/p2_*, topm_*, cand_*) are
   accepted for signature compatibility; probe_cids_buf / probe_dqcs_buf receive the probes
   and tau_sq the pass-1 threshold, as in the reference;
-* modes 0 (CM-SQ8+RR), 1 (K1) and 11 (Tribase) are comparison routes outside the lossless
-  path and raise NotImplementedError; ``warp_refine`` only selected a refinement schedule
-  and does not change results, so it is accepted and ignored.
+* modes 0 (CM-SQ8+RR), 1 (K1) and 11 (Tribase), the reference's comparison routes, run
+  the reference algorithms: modes 0 / 1 rank by the SQ8 reconstruction distance acc_hat in
+  the rotated space (float64 rotation rounded once, see ``trident_search``), mode 0 then
+  reranks the top M = min(max(rerank_m, K), 200) exactly; mode 11 is exact.  use_l1 is
+  applied by mode 2 only (for modes 0 / 1 the reference's tile skip compares acc_hat with
+  original-space norms and bounds nothing).  When ``r_vec_sorted`` is not given, mode 11
+  derives it (float64 |x - c| rounded to float32) once per index;
+* ``warp_refine`` only selected a refinement schedule and does not change results, so it
+  is accepted and ignored.
 """
 import ctypes
 import os
@@ -139,7 +145,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
                     rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
                     eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
-                    cent_band=None) -> TridentIndexView:
+                    cent_band=None, r_vec_sorted=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -160,6 +166,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.blk_bounds4 = _ptr(blk_bounds4)
     v.vec_Ar = _ptr(vec_Ar)
     v.sq8_cells = _ptr(sq8_cells)
+    v.r_vec_sorted = _ptr(r_vec_sorted)
     if cent_band is not None:
         rows, tiles, norms, nmax = cent_band
         v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
@@ -220,23 +227,52 @@ def derived_layouts(W_combined, b_combined, sq8_packed, cluster_vec_off, cluster
         return vec_Ar, cells, band
 
 
+def derived_r_vec(W_combined, cluster_vec_off, xb_sorted, nlist: int, chunk_rows: int = 1 << 20):
+    """Mode 11's per-vector |x - c| [N] float32 (float64 norm, rounded to nearest) for an index
+    passed in the reference layout without r_vec_sorted; centroids c_d = -W_combined[d, c] / 2.
+    Cached like derived_layouts."""
+    key = ("r_vec",) + _identity(W_combined, cluster_vec_off, xb_sorted) + (int(nlist),)
+    with _derived_lock:
+        hit = _derived_cache.get(key)
+        if hit is not None:
+            return hit
+        dev = W_combined.device
+        cen = (-0.5 * W_combined[:, :nlist]).t().to(torch.float64)
+        vec_off = cluster_vec_off.to(dev, torch.int64)
+        lid = torch.repeat_interleave(torch.arange(nlist, device=dev), vec_off[1:] - vec_off[:-1])
+        N = int(xb_sorted.shape[0])
+        out = torch.empty(N, device=dev, dtype=torch.float32)
+        for s in range(0, N, chunk_rows):
+            e = min(N, s + chunk_rows)
+            x = xb_sorted[s:e].to(dev, torch.float64)
+            out[s:e] = torch.sqrt(((x - cen[lid[s:e]]) ** 2).sum(1)).to(torch.float32)
+        if len(_derived_cache) >= 2:
+            _derived_cache.pop(next(iter(_derived_cache)))
+        _derived_cache[key] = out
+        return out
+
+
 def env_ub_seed() -> int:
     return int(os.environ.get("TRIDENT_UB_SEED", "0") or 0)
 
 
 def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: torch.Tensor,
                 topk_i: torch.Tensor, *, mode: int = 2, ub_seed: int = 0, use_l1: int = 0,
-                p_init: int = -1, route: int = 0, probe_cids: Optional[torch.Tensor] = None,
+                p_init: int = -1, route: int = 0, rerank_m: int = 0,
+                probe_cids: Optional[torch.Tensor] = None,
                 probe_dqcs: Optional[torch.Tensor] = None, tau_sq: Optional[torch.Tensor] = None,
                 stats: Optional[torch.Tensor] = None, record_events: bool = False,
                 stream: Optional[torch.cuda.Stream] = None, stage_events=None) -> float:
     """Runs trident_search on an index view; all tensors already validated by the caller."""
     B, K = int(xq.shape[0]), int(topk_d.shape[1])
     L = _lib.lib()
-    nbytes = L.trident_workspace_bytes(ctypes.byref(view), max(B, 1), int(nprobe), K)
+    # mode 0's merged lists hold M = min(max(rerank_m, K), 200) entries
+    k_ws = max(K, min(int(rerank_m), 200)) if int(mode) == _lib.MODE_SQ8_RERANK else K
+    nbytes = L.trident_workspace_bytes(ctypes.byref(view), max(B, 1), int(nprobe), k_ws)
     st = stream if stream is not None else torch.cuda.current_stream(xq.device)
     slot = _workspace_slot(xq.device, st)
-    sp = TridentSearchParams(int(mode), B, K, int(nprobe), int(ub_seed), int(use_l1), int(p_init), int(route))
+    sp = TridentSearchParams(int(mode), B, K, int(nprobe), int(ub_seed), int(use_l1), int(p_init), int(route),
+                             int(rerank_m))
     out = TridentSearchOutputs()
     out.topk_d, out.topk_i = topk_d.data_ptr(), topk_i.data_ptr()
     out.probe_cids = _ptr(probe_cids)
@@ -286,12 +322,9 @@ def launch_trident_v4_search(
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
-    if mode in (0, 1, 11):
-        raise NotImplementedError(
-            f"mode {mode} is a comparison route of the reference (CM-SQ8+RR / K1 / Tribase), "
-            "not part of the lossless path; use mode 2 (cascade) or 10 (cluster-major exact)")
-    _need(mode in (2, 10), f"unknown mode {mode}")
-    _need(int(rerank_m) == 0, "rerank_m applies to mode 0 only; must be 0 for modes 2 and 10")
+    _need(mode in (0, 1, 2, 10, 11), f"unknown mode {mode} (0, 1, 2, 10 or 11)")
+    _need(int(rerank_m) >= 0, "rerank_m must be >= 0")
+    sq8 = mode in (0, 1, 2)  # modes reading the SQ8 codes
     dev = xq_orig.device
     _need(dev.type == "cuda", "xq_orig must be a device tensor")
     _check_tensor("xq_orig", xq_orig, torch.float32, dev, 2)
@@ -328,7 +361,7 @@ def launch_trident_v4_search(
     else:
         tile_r_minmax = None
     _need(not (int(use_l1) and mode == 2 and tile_r_minmax is None), "use_l1 needs tile_r_minmax")
-    if mode == 2:
+    if sq8:
         _check_tensor("sq8_packed", sq8_packed, torch.int32, dev)
         _need(sq8_packed.numel() == tiles * (D_pad // 4) * int(tile_size),
               "sq8_packed must hold [tiles, D_pad/4, tile_size] words")
@@ -367,6 +400,14 @@ def launch_trident_v4_search(
         _check_tensor("tau_sq", tau_sq, torch.float32, dev)
         _need(tau_sq.numel() >= B, "tau_sq needs B entries")
 
+    if mode == 11:
+        if r_vec_sorted is not None:
+            _check_tensor("r_vec_sorted", r_vec_sorted, torch.float32, dev)
+            _need(r_vec_sorted.numel() == N, f"r_vec_sorted must hold N={N} floats")
+        else:
+            r_vec_sorted = derived_r_vec(W_combined, cluster_vec_off, xb_sorted, nlist)
+    else:
+        r_vec_sorted = None
     if rot_sq_bounds is None:
         rot_sq_bounds = rotation_sq_bounds(W_combined, nlist, D)
     if mode == 2 and (vec_Ar is None or sq8_cells is None) and int(route) != 1 and \
@@ -381,15 +422,16 @@ def launch_trident_v4_search(
     view = make_index_view(
         N=N, D=D, D_pad=D_pad, nlist=nlist, tile_size=tile_size, per_cluster_sq8=per_cluster_sq8,
         W_combined=W_combined, b_combined=b_combined, rot_sq_min=rot_sq_bounds[0],
-        rot_sq_max=rot_sq_bounds[1], sq8_packed=sq8_packed if mode == 2 else None,
+        rot_sq_max=rot_sq_bounds[1], sq8_packed=sq8_packed if sq8 else None,
         tile_orig_ids=tile_orig_ids, tile_r_minmax=tile_r_minmax,
         cluster_tile_off=cluster_tile_off, cluster_vec_off=cluster_vec_off, xb_sorted=xb_sorted,
-        orig_ids_sorted=orig_ids_sorted, vmin=vmin if mode == 2 else None,
-        delta=delta if mode == 2 else None, eps_dim=eps_dim if mode == 2 else None,
+        orig_ids_sorted=orig_ids_sorted, vmin=vmin if sq8 else None,
+        delta=delta if sq8 else None, eps_dim=eps_dim if sq8 else None,
         blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
-        sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band)
+        sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
-                       use_l1=int(use_l1), p_init=p_init, route=route, probe_cids=probe_cids_buf,
+                       use_l1=int(use_l1), p_init=p_init, route=route,
+                       rerank_m=int(rerank_m) if mode == 0 else 0, probe_cids=probe_cids_buf,
                        probe_dqcs=probe_dqcs_buf, tau_sq=tau_sq, stats=stats_buf,
                        record_events=bool(record_events), stage_events=stage_events)

@@ -368,6 +368,8 @@ class TridentV4Index:
             rmax = torch.where(v, r, torch.full_like(r, -math.inf)).amax(1) * (1.0 + 1e-12)
             self.tile_r_minmax[ts:te, 0] = -round_up_f32(-rmin)
             self.tile_r_minmax[ts:te, 1] = round_up_f32(rmax)
+        # mode 11's per-vector |x - c| (reference r_vec_sorted): the float64 norm rounded to nearest
+        self.r_vec_sorted = res_norm.to(torch.float32)
         del codes, codes32, res_norm
 
         # ---- dimension blocks (reference :231-255) ----
@@ -455,7 +457,8 @@ class TridentV4Index:
             self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
             bool(record_kernel_ms), int(warp_refine), stats_buf,
             ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events,
-            vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band)
+            vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band,
+            r_vec_sorted=self.r_vec_sorted)
         return topk_d, topk_i, kern_ms
 
     def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
