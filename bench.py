@@ -104,9 +104,9 @@ def load_profile(name, **match):
 class Workload:
     """Synthetic data + index of one configuration, built on the GPU."""
 
-    def __init__(self, cfg_id, cfg, xb_host, dev):
+    def __init__(self, cfg_id, cfg, xb_host, dev, index_cache=""):
         import torch
-        from trident_amd import clustering, datagen
+        from trident_amd import clustering, datagen, persist
         from trident_amd.index import SharedClusterStorage, TridentV4Index
         self.cfg_id, self.cfg, self.xb_host = cfg_id, cfg, xb_host
         N, D, nlist, K, B = cfg["N"], cfg["D"], cfg["nlist"], cfg["K"], cfg["B"]
@@ -115,16 +115,34 @@ class Workload:
         torch.cuda.synchronize()
         log(f"generated cfg{cfg_id} N={N} D={D} B={B} in {time.perf_counter() - t0:.1f}s")
         t1 = time.perf_counter()
-        cen, lid, r, mean64, R64, t_train = clustering.train_clustering(
-            xb, nlist, seed=0, niter=20, max_train=min(N, max(64 * nlist, 256 * 1024)), device=dev)
-        self.st = SharedClusterStorage(xb, lid, r, nlist, device=dev, xb_placement="host" if xb_host else "device")
-        self.ix = TridentV4Index(self.st, cen, mean64, R64, tile_size=cfg["T"], device=dev, max_batch=B,
-                                 max_nprobe=max(128, cfg["nprobe"]), k=K)
+        placement = "host" if xb_host else "device"
+        cached = index_cache and os.path.exists(os.path.join(index_cache, "meta.npz"))
+        if cached:
+            # the saved index holds no base: the regenerated one is sorted by its sort_perm
+            self.ix = persist.load_index(index_cache, device=dev, xb_placement=placement, xb_raw=xb,
+                                         max_batch=B, max_nprobe=max(128, cfg["nprobe"]), k=K)
+            self.st = self.ix.storage
+            same = (self.ix.N, self.ix.D, self.ix.nlist, self.ix.tile_size) == (N, D, nlist, cfg["T"])
+            if not same:
+                raise SystemExit(f"{index_cache} holds another configuration")
+        else:
+            cen, lid, r, mean64, R64, t_train = clustering.train_clustering(
+                xb, nlist, seed=0, niter=20, max_train=min(N, max(64 * nlist, 256 * 1024)), device=dev)
+            self.st = SharedClusterStorage(xb, lid, r, nlist, device=dev, xb_placement=placement)
+            self.ix = TridentV4Index(self.st, cen, mean64, R64, tile_size=cfg["T"], device=dev, max_batch=B,
+                                     max_nprobe=max(128, cfg["nprobe"]), k=K)
         del xb
         torch.cuda.synchronize()
         self.build_s = time.perf_counter() - t1
-        log(f"k-means {t_train:.1f}s, index build {self.ix.build_time_s:.1f}s, total {self.build_s:.1f}s; "
-            f"SQ8 {self.ix.sq8_bytes() / 1e6:.1f} MB")
+        if cached:
+            log(f"index loaded from {index_cache} in {self.build_s:.1f}s; SQ8 {self.ix.sq8_bytes() / 1e6:.1f} MB")
+        else:
+            log(f"k-means {t_train:.1f}s, index build {self.ix.build_time_s:.1f}s, total {self.build_s:.1f}s; "
+                f"SQ8 {self.ix.sq8_bytes() / 1e6:.1f} MB")
+            if index_cache:
+                t2 = time.perf_counter()
+                persist.save_index(self.ix, index_cache, include_base=False, mean64=mean64, R64=R64)
+                log(f"index saved to {index_cache} in {time.perf_counter() - t2:.1f}s")
         self.xq = xq.contiguous()
         self.xq_np = xq.cpu().numpy()
 
@@ -193,7 +211,7 @@ def measure(cfg_id, cfg, args, dev, primary=True):
     import torch
     from trident_amd import _lib, metrics
 
-    w = Workload(cfg_id, cfg, cfg["host"], dev)
+    w = Workload(cfg_id, cfg, cfg["host"], dev, index_cache=args.index_cache if primary else "")
     ix, st = w.ix, w.st
     N, D, K, B, nprobe = cfg["N"], cfg["D"], cfg["K"], cfg["B"], cfg["nprobe"]
     mode, ub = args.mode, args.ub
@@ -359,6 +377,8 @@ def main():
     ap.add_argument("--xb-host", action="store_true", help="FP32 base in mapped pinned host memory (out of core)")
     ap.add_argument("--xb-device", action="store_true", help="FP32 base in HBM (cfg 5 defaults to host)")
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg 2 line after cfg 5")
+    ap.add_argument("--index-cache", default="", help="directory of a saved index (trident_amd.persist): "
+                    "loaded when present, else written after the build (without the base)")
     ap.add_argument("--extra-steps", type=int, default=20)
     ap.add_argument("--sweep", action="store_true", help="also time other nprobe / ub values and the CM route")
     ap.add_argument("--calibrate-w0", action="store_true", help="router crossover sweep over batch sizes")

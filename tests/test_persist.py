@@ -1,0 +1,98 @@
+"""Row f1: the on-disk index (trident_amd.persist).
+
+CPU: a saved and reloaded index holds every tensor of the built one bit for bit (with the base
+from xb_sorted.bin, and from the original-order base when saved without it); interrupted or
+damaged directories are refused.  GPU: a reloaded index (base in HBM and in mapped host memory)
+searches exactly like the float64 oracle and like the index it was saved from."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import assert_exact, build_index, oracle_search
+from trident_amd import clustering, datagen, persist
+from trident_amd.index import SharedClusterStorage, TridentV4Index
+
+_TENSORS = ("centroids", "W_combined", "b_combined", "W_coarse_only", "b_coarse_only", "vmin_pad",
+            "delta_pad", "eps_pad", "blk_bounds4", "tile_r_minmax", "cluster_tile_off", "sq8_packed",
+            "sq8_cells", "tile_orig_ids", "vec_Ar", "r_vec_sorted")
+_STORAGE = ("xb_sorted", "orig_ids_sorted", "cluster_vec_off", "list_ids_sorted")
+
+
+@pytest.fixture(scope="module")
+def cpu_index():
+    xb, _ = datagen.cfg1(N=5000, D=72, B=8, n_centers=16, seed=7)
+    cen, lid, r, mean64, R64, _ = clustering.train_clustering(xb, 20, seed=0, niter=4)
+    st = SharedClusterStorage(xb.numpy(), lid, r, 20, device="cpu")
+    ix = TridentV4Index(st, cen, mean64, R64, tile_size=64, device="cpu", max_batch=8, max_nprobe=8)
+    return ix, xb.numpy(), mean64, R64
+
+
+def _same_index(a, b):
+    for n in ("N", "D", "D_pad", "nlist", "tile_size", "per_cluster_sq8", "total_tiles", "rot_sq_min",
+              "rot_sq_max"):
+        assert getattr(a, n) == getattr(b, n), n
+    for n in _TENSORS:
+        ta, tb = getattr(a, n), getattr(b, n)
+        assert ta.dtype == tb.dtype and torch.equal(ta.cpu(), tb.cpu()), n
+    for n in _STORAGE:
+        assert torch.equal(getattr(a.storage, n).cpu(), getattr(b.storage, n).cpu()), n
+    for x, y in zip(a.cent_band, b.cent_band):
+        assert (torch.equal(x, y) if isinstance(x, torch.Tensor) else x == y)
+
+
+def test_round_trip_with_base(cpu_index, tmp_path):
+    ix, _, mean64, R64 = cpu_index
+    persist.save_index(ix, str(tmp_path), mean64=mean64, R64=R64)
+    assert sorted(os.listdir(tmp_path)) == sorted(
+        ["meta.npz", "sort_perm.bin", "sq8_packed.bin", "tile_orig_ids.bin", "vec_Ar.bin", "r_vec_sorted.bin",
+         "xb_sorted.bin"])
+    got = persist.load_index(str(tmp_path), device="cpu", max_batch=8, max_nprobe=8)
+    _same_index(ix, got)
+    with np.load(tmp_path / "meta.npz", allow_pickle=False) as z:
+        assert np.array_equal(z["mean64"], mean64) and np.array_equal(z["R64"], R64)
+
+
+def test_round_trip_without_base(cpu_index, tmp_path):
+    ix, xb, _, _ = cpu_index
+    persist.save_index(ix, str(tmp_path), include_base=False)
+    assert not (tmp_path / "xb_sorted.bin").exists()
+    with pytest.raises(ValueError, match="xb_raw"):
+        persist.load_index(str(tmp_path), device="cpu")
+    got = persist.load_index(str(tmp_path), device="cpu", xb_raw=xb, max_batch=8, max_nprobe=8)
+    _same_index(ix, got)
+
+
+def test_damaged_directories_are_refused(cpu_index, tmp_path):
+    ix, _, _, _ = cpu_index
+    with pytest.raises(ValueError, match="meta.npz"):
+        persist.load_index(str(tmp_path), device="cpu")
+    persist.save_index(ix, str(tmp_path))
+    f = tmp_path / "vec_Ar.bin"
+    with open(f, "r+b") as h:
+        h.truncate(os.path.getsize(f) - 8)
+    with pytest.raises(ValueError, match="vec_Ar.bin"):
+        persist.load_index(str(tmp_path), device="cpu")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("placement", ["device", "host"])
+def test_reloaded_index_searches_exactly(dev, tmp_path, placement):
+    xb, xq = datagen.cfg2(N=30_000, D=128, B=256, n_centers=64, seed=71)
+    b = build_index(xb, 64, dev, max_batch=256)
+    persist.save_index(b.ix, str(tmp_path))
+    ix2 = persist.load_index(str(tmp_path), device=dev, xb_placement=placement, max_batch=256, max_nprobe=128)
+    _same_index(b.ix, ix2)
+    q = torch.as_tensor(xq.numpy()).to(dev).contiguous()
+    for mode, route in ((2, 1), (2, 2), (10, 0), (11, 0)):
+        _, rd, ri = oracle_search(b, xq.numpy(), 16, 10)
+        d1, i1, _ = b.ix.search(q, 16, mode=mode, k=10, route=route, ub_seed=1)
+        d1, i1 = d1.cpu().numpy().copy(), i1.cpu().numpy().copy()
+        d2, i2, _ = ix2.search(q, 16, mode=mode, k=10, route=route, ub_seed=1)
+        torch.cuda.synchronize()
+        assert_exact(d2.cpu().numpy(), i2.cpu().numpy(), rd, ri, f"reloaded mode {mode} route {route}")
+        assert np.array_equal(d1, d2.cpu().numpy()) and np.array_equal(i1, i2.cpu().numpy())
+    if ix2.storage._host_buf is not None:
+        torch.cuda.synchronize()
+        ix2.storage._host_buf.free()

@@ -194,6 +194,44 @@ class SharedClusterStorage:
         self.list_ids_sorted = lid[sort_perm].to(torch.int32).contiguous()
         self.r_vec_sorted = None if r_vec is None else _as_tensor(r_vec, self.dev, torch.float32)[sort_perm].contiguous()
 
+    @classmethod
+    def from_sorted(cls, xb_sorted, sort_perm, vec_off, device="cuda:0", xb_placement: str = "device",
+                    xb_raw=None, chunk_rows: int = 1 << 22):
+        """Storage of an already sorted layout (a saved index): rows come from ``xb_sorted``
+        ([N, D], e.g. a memmap) or, when it is None, from ``xb_raw[sort_perm]``; nothing is
+        re-sorted.  ``sort_perm`` [N] holds the original id of each sorted row."""
+        self = cls.__new__(cls)
+        self.dev = torch.device(device)
+        perm = np.ascontiguousarray(sort_perm, np.int64)
+        voff = np.ascontiguousarray(vec_off, np.int64)
+        self.N, self.nlist = int(perm.shape[0]), int(voff.shape[0]) - 1
+        src = xb_sorted if xb_sorted is not None else xb_raw
+        self.D = int(src.shape[1])
+        self.placement = xb_placement
+        self._host_buf = None
+        if xb_placement == "host":
+            self._host_buf = PinnedHostBuffer((self.N, self.D), torch.float32, owner=self)
+            self.xb_sorted = self._host_buf.tensor
+        else:
+            self.xb_sorted = torch.empty((self.N, self.D), device=self.dev, dtype=torch.float32)
+        for s in range(0, self.N, chunk_rows):
+            e = min(self.N, s + chunk_rows)
+            if xb_sorted is not None:
+                rows = torch.from_numpy(np.array(xb_sorted[s:e], dtype=np.float32))
+            else:
+                xr = xb_raw if isinstance(xb_raw, torch.Tensor) else torch.as_tensor(np.asarray(xb_raw))
+                rows = xr[torch.as_tensor(perm[s:e]).to(xr.device)].to(torch.float32)
+            self.xb_sorted[s:e] = rows.to(self.xb_sorted.device)
+        self.orig_ids_sorted = torch.as_tensor(perm.astype(np.int32)).to(self.dev)
+        self.cluster_vec_off = torch.as_tensor(voff.astype(np.int32)).to(self.dev)
+        counts = (voff[1:] - voff[:-1]).astype(np.int32)
+        self.counts = counts
+        self.sort_perm = perm.astype(np.int32)
+        self.list_ids_sorted = torch.repeat_interleave(
+            torch.arange(self.nlist, dtype=torch.int32), torch.as_tensor(counts.astype(np.int64))).to(self.dev)
+        self.r_vec_sorted = None
+        return self
+
     def xb_sorted_host(self) -> np.ndarray:
         return self.xb_sorted.cpu().numpy() if self.xb_sorted.device.type != "cpu" else self.xb_sorted.numpy()
 

@@ -1,0 +1,184 @@
+"""On-disk index: one directory of ``meta.npz`` plus raw ``.bin`` arrays, loaded by memory map.
+
+The reference's 100M engine keeps its built index as ``meta.npz`` (centroids, mean64, R64,
+sort_perm, vec_off, tile_off, vmin, delta) next to ``sq8_packed.bin``, ``tile_orig_ids.bin``
+and the base as raw memmaps (benchmarks/phase8_ooc_100m_4080.py:228-248), written by its GPU
+build (scripts/phase7_step2_gpu_build_verify.py:68-272).  This format keeps that split -- the
+small arrays and scalars in ``meta.npz``, every array proportional to N in a ``.bin`` file read
+with ``numpy.memmap`` and streamed to the device in chunks -- and stores everything a
+``TridentV4Index`` holds, so loading rebuilds nothing:
+
+  meta.npz            format, version, sizes and options, rot_sq_min / rot_sq_max, centroids,
+                      mean64, R64 (the clustering's float64 rotation, kept for reference),
+                      W_combined, b_combined, vec_off, tile_off, vmin, delta, eps, blk_bounds4,
+                      tile_r_minmax, and the .bin manifest (name, dtype, shape)
+  sort_perm.bin       int32 [N]            original id of each sorted row (orig_ids_sorted)
+  sq8_packed.bin      int32 [tiles, D_pad/4, T]   the reference's code packing
+  tile_orig_ids.bin   int32 [tiles, T]
+  vec_Ar.bin          float32 [N, 2]       per-vector scalars of the batched route
+  r_vec_sorted.bin    float32 [N]          |x - c| (mode 11)
+  xb_sorted.bin       float32 [N, D]       the cluster-sorted base (optional)
+
+The code cells of the batched route and the centroid layouts of the coarse pass are
+regrouped from sq8_packed / W_combined on load (cheap, on the device).  Every file is written
+under a temporary name and renamed into place (``os.replace``); ``meta.npz`` goes last, so a
+directory with a ``meta.npz`` is complete.  The loader checks the format, the version and every
+file's size against the manifest.
+"""
+import os
+import time
+from typing import Optional
+
+import numpy as np
+import torch
+
+from . import ext as _ext
+from .index import SharedClusterStorage, TridentV4Index, cells_from_packed
+
+FORMAT = "trident-amd-ivf-sq8"
+VERSION = 1
+
+_CHUNK_ROWS = 1 << 20
+_SCALARS = ("N", "D", "D_pad", "nlist", "tile_size", "per_cluster_sq8", "use_pca", "var_block",
+            "total_tiles")
+
+
+def _write_bin(path: str, t: torch.Tensor, chunk_rows: int = _CHUNK_ROWS):
+    """Streams a tensor (device, host or pinned) to ``path`` row chunk by row chunk."""
+    tmp = f"{path}.tmp-{os.getpid()}"
+    with open(tmp, "wb") as f:
+        n = int(t.shape[0]) if t.dim() else 1
+        for s in range(0, max(n, 1), chunk_rows):
+            part = t[s:s + chunk_rows] if t.dim() else t
+            f.write(part.detach().to("cpu").contiguous().numpy().tobytes())
+    os.replace(tmp, path)
+
+
+def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=None, R64=None) -> dict:
+    """Writes ``ix`` (and, with ``include_base``, its sorted base) under directory ``path``.
+    Returns the manifest."""
+    os.makedirs(path, exist_ok=True)
+    st = ix.storage
+    bins = {
+        "sort_perm": st.orig_ids_sorted,
+        "sq8_packed": ix.sq8_packed,
+        "tile_orig_ids": ix.tile_orig_ids,
+        "vec_Ar": ix.vec_Ar,
+        "r_vec_sorted": ix.r_vec_sorted,
+    }
+    if include_base:
+        _need(st.xb_sorted is not None, "the storage's base has been freed")
+        bins["xb_sorted"] = st.xb_sorted
+    manifest = {}
+    for name, t in bins.items():
+        _write_bin(os.path.join(path, name + ".bin"), t)
+        manifest[name] = (str(t.dtype).replace("torch.", ""), tuple(int(s) for s in t.shape))
+    meta = {k: np.int64(getattr(ix, k)) for k in _SCALARS}
+    meta.update(
+        format=np.array(FORMAT), version=np.int64(VERSION),
+        rot_sq_min=np.float64(ix.rot_sq_min), rot_sq_max=np.float64(ix.rot_sq_max),
+        centroids=ix.centroids.cpu().numpy(),
+        W_combined=ix.W_combined.cpu().numpy(), b_combined=ix.b_combined.cpu().numpy(),
+        vec_off=st.cluster_vec_off.cpu().numpy(), tile_off=ix.cluster_tile_off.cpu().numpy(),
+        vmin=ix.vmin_pad.cpu().numpy(), delta=ix.delta_pad.cpu().numpy(), eps=ix.eps_pad.cpu().numpy(),
+        blk_bounds4=ix.blk_bounds4.cpu().numpy(), tile_r_minmax=ix.tile_r_minmax.cpu().numpy(),
+        bin_names=np.array(list(manifest)),
+        bin_dtypes=np.array([manifest[n][0] for n in manifest]),
+        bin_shapes=np.array([",".join(map(str, manifest[n][1])) for n in manifest]),
+    )
+    if mean64 is not None:
+        meta["mean64"] = np.asarray(mean64, np.float64)
+    if R64 is not None:
+        meta["R64"] = np.asarray(R64, np.float64)
+    tmp = os.path.join(path, f"meta.tmp-{os.getpid()}.npz")
+    np.savez(tmp, **meta)
+    os.replace(tmp, os.path.join(path, "meta.npz"))
+    return manifest
+
+
+def _need(cond: bool, msg: str):
+    if not cond:
+        raise ValueError(msg)
+
+
+_NP = {"int32": np.int32, "float32": np.float32}
+_TORCH = {"int32": torch.int32, "float32": torch.float32}
+
+
+def _open_bins(path: str, meta) -> dict:
+    out = {}
+    for name, dt, shp in zip(meta["bin_names"], meta["bin_dtypes"], meta["bin_shapes"]):
+        name, dt = str(name), str(dt)
+        shape = tuple(int(s) for s in str(shp).split(",") if s)
+        f = os.path.join(path, name + ".bin")
+        _need(os.path.exists(f), f"{f} is missing")
+        want = int(np.prod(shape)) * np.dtype(_NP[dt]).itemsize
+        _need(os.path.getsize(f) == want, f"{f}: {os.path.getsize(f)} bytes, the manifest says {want}")
+        out[name] = np.memmap(f, dtype=_NP[dt], mode="r", shape=shape) if want else np.zeros(shape, _NP[dt])
+    return out
+
+
+def _to_device(a: np.ndarray, dev, chunk_rows: int = _CHUNK_ROWS) -> torch.Tensor:
+    t = torch.empty(a.shape, dtype=_TORCH[str(a.dtype)], device=dev)
+    n = a.shape[0] if a.ndim else 1
+    for s in range(0, n, chunk_rows):
+        t[s:s + chunk_rows] = torch.from_numpy(np.array(a[s:s + chunk_rows]))
+    return t
+
+
+def load_index(path: str, device="cuda:0", xb_placement: str = "device", xb_raw=None,
+               max_batch: int = 1024, max_nprobe: int = 512, k: int = 10) -> TridentV4Index:
+    """Loads an index written by ``save_index``.  The base comes from ``xb_sorted.bin`` when the
+    directory has one, else from ``xb_raw`` (the original-order base, sorted here by sort_perm).
+    ``xb_placement`` = "device" (HBM) or "host" (device-mapped pinned host memory)."""
+    t0 = time.perf_counter()
+    meta_f = os.path.join(path, "meta.npz")
+    _need(os.path.exists(meta_f), f"{meta_f} is missing (not a saved index, or an interrupted save)")
+    with np.load(meta_f, allow_pickle=False) as z:
+        meta = {k2: z[k2] for k2 in z.files}
+    _need(str(meta["format"]) == FORMAT, f"{path}: format {meta['format']!s}, expected {FORMAT}")
+    _need(int(meta["version"]) == VERSION, f"{path}: version {int(meta['version'])}, expected {VERSION}")
+    sc = {k2: int(meta[k2]) for k2 in _SCALARS}
+    bins = _open_bins(path, meta)
+    N, D, nlist = sc["N"], sc["D"], sc["nlist"]
+    dev = torch.device(device)
+    sort_perm = np.asarray(bins["sort_perm"])
+    if "xb_sorted" in bins:
+        xb_sorted = bins["xb_sorted"]
+    else:
+        _need(xb_raw is not None, f"{path} holds no base: pass xb_raw (the base in original order)")
+        _need(tuple(xb_raw.shape) == (N, D), f"xb_raw must be [{N}, {D}]")
+        xb_sorted = None
+    st = SharedClusterStorage.from_sorted(xb_sorted, sort_perm, meta["vec_off"], device=dev,
+                                          xb_placement=xb_placement, xb_raw=xb_raw)
+    ix = TridentV4Index.__new__(TridentV4Index)
+    ix.storage, ix.dev = st, dev
+    for k2, v in sc.items():
+        setattr(ix, k2, v)
+    ix.W_tile = ix.tile_size // 32
+    ix.D4 = ix.D_pad // 4
+    ix.k = int(k)
+    ix.rot_sq_min, ix.rot_sq_max = float(meta["rot_sq_min"]), float(meta["rot_sq_max"])
+    f32 = lambda a: torch.as_tensor(np.ascontiguousarray(a), dtype=torch.float32).to(dev)
+    i32 = lambda a: torch.as_tensor(np.ascontiguousarray(a), dtype=torch.int32).to(dev)
+    ix.centroids = f32(meta["centroids"])
+    ix.W_combined, ix.b_combined = f32(meta["W_combined"]), f32(meta["b_combined"])
+    ix.W_coarse_only = ix.W_combined[:, :nlist].contiguous()
+    ix.b_coarse_only = ix.b_combined[:, :nlist].contiguous()
+    ix.cent_band = _ext.centroid_band_layouts(ix.W_combined, nlist)
+    ix.vmin_pad, ix.delta_pad, ix.eps_pad = f32(meta["vmin"]), f32(meta["delta"]), f32(meta["eps"])
+    ix.blk_bounds4 = i32(meta["blk_bounds4"])
+    ix.tile_r_minmax = f32(meta["tile_r_minmax"])
+    ix.cluster_tile_off = i32(meta["tile_off"])
+    ix.sq8_packed = _to_device(bins["sq8_packed"], dev)
+    ix.sq8_cells = cells_from_packed(ix.sq8_packed, ix.D_pad, ix.tile_size)
+    ix.tile_orig_ids = _to_device(bins["tile_orig_ids"], dev)
+    ix.vec_Ar = _to_device(bins["vec_Ar"], dev)
+    ix.r_vec_sorted = _to_device(bins["r_vec_sorted"], dev)
+    ix.max_batch, ix.max_nprobe = int(max_batch), int(max_nprobe)
+    ix._alloc_buffers()
+    if dev.type == "cuda":
+        torch.cuda.synchronize(dev)
+    ix.build_time_s = 0.0
+    ix.load_time_s = time.perf_counter() - t0
+    return ix
