@@ -327,6 +327,27 @@ def measure(cfg_id, cfg, args, dev, primary=True):
             oc["pcie_counter"] = pp["counter"]
         out["out_of_core"] = oc
 
+    if primary and args.pipeline_batches > 0:
+        # End to end from host memory (PCIe-inclusive): queries uploaded, searched and read back
+        # in batches of B, `depth` batches in flight on separate streams (trident_amd.pipeline).
+        from trident_amd.pipeline import SearchPipeline
+        nb = args.pipeline_batches
+        xq_all = np.concatenate([w.xq_np] * nb)
+        pipe_out = {}
+        for depth in (1, 2, 3):
+            pipe = SearchPipeline(ix, nprobe, K, batch=B, depth=depth, mode=mode, ub_seed=ub, route=args.route)
+            pipe.run(xq_all[:B * depth])  # warm-up: every slot's workspace and buffers
+            tb = time.perf_counter()
+            pd_, pi_ = pipe.run(xq_all)
+            sec = time.perf_counter() - tb
+            same = bool(np.array_equal(pi_[:B], gpu_i) and np.array_equal(pd_[-B:], gpu_d))
+            pipe_out[f"depth{depth}"] = {"qps": round(len(xq_all) / sec, 1), "ms_per_batch": round(sec * 1e3 / nb, 3),
+                                         "results_identical": same}
+            log(f"pipelined from host, depth {depth}: {len(xq_all) / sec:,.0f} QPS "
+                f"({sec * 1e3 / nb:.3f} ms per batch of {B}), results identical {same}")
+            del pipe
+        out["pipelined_from_host"] = dict(batches=nb, batch=B, **pipe_out)
+
     if primary and args.sweep:
         sweep = {}
         for npb, md, u in ((nprobe // 2, 2, ub), (nprobe * 2, 2, ub), (nprobe, 10, 0), (nprobe, 2, 0),
@@ -377,6 +398,8 @@ def main():
     ap.add_argument("--xb-host", action="store_true", help="FP32 base in mapped pinned host memory (out of core)")
     ap.add_argument("--xb-device", action="store_true", help="FP32 base in HBM (cfg 5 defaults to host)")
     ap.add_argument("--no-extra", action="store_true", help="skip the cfg 2 line after cfg 5")
+    ap.add_argument("--pipeline-batches", type=int, default=12,
+                    help="batches of B host queries for the pipelined end-to-end line (0 = skip)")
     ap.add_argument("--index-cache", default="", help="directory of a saved index (trident_amd.persist): "
                     "loaded when present, else written after the build (without the base)")
     ap.add_argument("--extra-steps", type=int, default=20)
@@ -430,7 +453,7 @@ def main():
         "bytes_alg_total": r["bytes_all"],
         "hbm_view": hv,
     }
-    for k in ("out_of_core", "sweep", "w0_calibration"):
+    for k in ("out_of_core", "sweep", "w0_calibration", "pipelined_from_host"):
         if k in r:
             line[k] = r[k]
     if args.cfg == 5 and not args.no_extra:

@@ -499,10 +499,11 @@ class TridentV4Index:
             r_vec_sorted=self.r_vec_sorted)
         return topk_d, topk_i, kern_ms
 
-    def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
-        """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a mode-2 search of B queries takes."""
+    def view(self):
+        """The C-ABI view (TridentIndexView) of this index; it holds raw pointers, so the index
+        must outlive it."""
         st = self.storage
-        view = _ext.make_index_view(
+        return _ext.make_index_view(
             N=st.N, D=self.D, D_pad=self.D_pad, nlist=self.nlist, tile_size=self.tile_size,
             per_cluster_sq8=self.per_cluster_sq8, W_combined=self.W_combined, b_combined=self.b_combined,
             rot_sq_min=self.rot_sq_min, rot_sq_max=self.rot_sq_max, sq8_packed=self.sq8_packed,
@@ -510,7 +511,11 @@ class TridentV4Index:
             cluster_tile_off=self.cluster_tile_off, cluster_vec_off=st.cluster_vec_off,
             xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
             delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
-            sq8_cells=self.sq8_cells, cent_band=self.cent_band)
+            sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted)
+
+    def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
+        """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a mode-2 search of B queries takes."""
+        view = self.view()
         r = _lib.lib().trident_route_for(ctypes.byref(view), int(B), int(k or self.k), int(nprobe), int(route))
         if r < 0:
             _lib.check(-r, "trident_route_for")
