@@ -7,8 +7,8 @@
 //
 //     |x_hat - q_rot|^2 = A_x - 2 sum_d c_d w_d + Q_q,   A_x = sum_d (c_d delta_d)^2,  Q_q = |q'|^2
 //
-// w is quantised to w = s * w_int + err (s a power of two shared by the 16 queries a wave
-// scans together, |w_int| <= 32639, split w_int = 256 * hi + lo into two int8 planes); with
+// w is quantised to w = s * w_int + err (s a power of two shared by the <= 32 pairs of a weight
+// group, |w_int| <= 32639, split w_int = 256 * hi + lo into two int8 planes); with
 // c' = c - 128 the dot product
 //     sum_d c_d w_int,d = 256 * MFMA(c', hi) + MFMA(c', lo) + 128 * sum_d w_int,d
 // is computed EXACTLY by v_mfma_i32_16x16x64_i8 (two per 64 dims), and
@@ -19,30 +19,37 @@
 // Scaled by the rotation's squared singular-value bounds these bound the canonical float64
 // distance.
 //
-// Pass A (UB):  for the first p_init probes of each query, the K-th smallest upper bound over
-//               the cluster -> atomicMin into tau[q] (the reference's Stage X seeding,
-//               src/trident_v4_kernels.cu:626-676, computed for 64 queries at once; the K-th
-//               smallest upper bound of any K vectors bounds the K-th distance).
-// Pass B (LB):  for every probe, vectors whose lower bound passes tau[q] are queued in LDS and
-//               appended (sorted position) to the query's candidate list.  The bulk test is
-//               one int32 compare per (vector, query), acc + kq >= thr_x, with per-query and
-//               per-vector constants rounded outward; rows that pass are re-tested in float32
-//               with an additive slack that bounds every rounding of it (0.07% of (vector,
-//               query) pairs survive on cfg-2 data).
-// Refine:       one wave per query computes the canonical float64 distance of each listed
-//               survivor and keeps it iff <= tau[q] (the reference's Stage Z, :796-941).
+// Pass A (seeding, Stage X; reference src/trident_v4_kernels.cu:626-676): for the seeding
+//               probes of each query (the first p_init, or every probe with TRIDENT_UB_SEED 2)
+//               every row's upper bound; each unit (<= 16 queries) appends its K smallest
+//               (bound, row) entries to the query's list.  ub_kth_kernel then takes the query's
+//               K smallest entries (the seeds), refines them exactly and sets
+//               tau[q] = min(K-th bound, K-th seed distance); the seeds become the query's
+//               first candidates.
+// Pass B (LB, Stage Y):  for every probe, rows whose lower bound passes tau[q] are queued in LDS
+//               and appended (sorted position) to the query's candidate list.  The test is one
+//               int32 compare per (row, query) lane group, max(acc + kq) >= thr_x, with
+//               per-query and per-vector constants rounded outward (0.04% of (row, query)
+//               pairs survive on cfg-2 data); weight groups without the integer form use a
+//               float32 test with an additive slack that bounds every rounding of it.
+// Refine (Stage Z, :796-941): one wave per (query, 64-slot chunk of its list) computes the
+//               canonical float64 distance of each listed non-seed survivor and keeps it iff
+//               <= tau[q].
 //
-// Scheduling: a work unit is (cluster, <= 64 queries, slice of the cluster's vectors); each of
-// the workgroup's 4 waves owns 16 of the queries (the MFMA N dimension).  Units of one launch
-// are split into 8 contiguous ranges, one per XCD (blockIdx & 7), so a cluster's codes are read
-// from HBM once per XCD and then served by that XCD's L2; within a range each workgroup takes
-// the next unit from its XCD's counter (persistent grid, one atomic per unit).  The unit's
-// vectors stream through LDS in 64-vector blocks, double-buffered: all 256 threads load block
-// b+1 (16-byte code cells, 1 KiB contiguous per wave and load) while the waves run block b
-// from LDS, one barrier per block.  Lane l = (i = l & 15, g = l >> 4) holds, for every 64-dim step,
-// bytes of dims step*64 + g*16 + [0, 16): vector i's codes in the A operand and query i's
-// weights in the B operand (any dim-to-byte assignment shared by A and B computes the same
-// contraction); the result row 4g + r, column i sits in lane l, register r.
+// Scheduling: a work unit is (cluster, a block of its queries, slice of <= ~1024 of its
+// vectors).  Pass B (narrow layout, D_pad <= 256): queries are the MFMA's A rows (16 per MFMA,
+// two halves = 32 per wave, 128 per unit), vectors its B columns, so a slice's codes are staged
+// in LDS once per 128 queries.  Pass A and the wide layout (D_pad > 256): vectors are the A rows
+// and 16 queries per wave the B columns.  Units of one launch are split into 8 contiguous
+// ranges, one per XCD (blockIdx & 7), so a cluster's codes are read from HBM once per XCD and
+// then served by that XCD's L2; within a range each workgroup takes the next unit from its
+// XCD's counter (persistent grid, one atomic per unit).  The slice streams through LDS in
+// 64-vector blocks (16 in the wide layout), double-buffered: block b + 1 moves global -> LDS
+// with direct loads (16-byte code cells, 1 KiB contiguous per wave and load) while the waves
+// compute block b, one barrier per block.  Lane l = (i = l & 15, g = l >> 4) holds, for every
+// 64-dim step, bytes of dims step*64 + g*16 + [0, 16) of its A row i and of its B column i (any
+// dim-to-byte assignment shared by A and B computes the same contraction); the result row
+// 4g + r, column i sits in lane l, register r.
 #include <type_traits>
 
 #include "common.hpp"
