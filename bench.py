@@ -230,7 +230,9 @@ def measure(cfg_id, cfg, args, dev, primary=True):
 
     # ---- algorithmic work and pruning statistics (untimed) ----
     stats = torch.zeros(4, dtype=torch.int64, device=dev)
-    d_out, i_out, _ = ix.search(w.xq, nprobe, mode=mode, ub_seed=ub, stats_buf=stats, route=args.route)
+    hrows = torch.zeros(1, dtype=torch.int64, device=dev)
+    d_out, i_out, _ = ix.search(w.xq, nprobe, mode=mode, ub_seed=ub, stats_buf=stats, route=args.route,
+                                host_rows_buf=hrows)
     torch.cuda.synchronize()
     gpu_d, gpu_i = d_out.cpu().numpy().copy(), i_out.cpu().numpy().copy()
     probes = ix.probe_cids_buf[:B, :nprobe].cpu().numpy()
@@ -319,11 +321,14 @@ def measure(cfg_id, cfg, args, dev, primary=True):
                        "survivors_frac": round(surv / max(tot, 1), 6), "refined_kept": ins},
            "surv": surv, "nprobe": nprobe, "K": K, "B": B, "N": N, "D": D, "nlist": cfg["nlist"]}
     if w.xb_host:
-        # every row read from host memory is read once: the K seed rows of each query (exact
-        # seeding) and the Stage Z survivors that are not seeds; `surv` counts both
-        pcie = surv * D * 4
-        oc = {"host_rows_read": surv, "row_bytes": D * 4, "pcie_bytes_closed_form": pcie,
-              "pcie_bytes_per_query": round(pcie / B, 1), "stage_z_ms": round(stage["pass2_merge_ms"], 4)}
+        # rows read from host memory, counted by the library (each once: exact seeds, Stage Z
+        # rows that residual bounds could not clear, overflow rescans); 4 D bytes each
+        hr = int(hrows.item())
+        pcie = hr * D * 4
+        oc = {"host_rows_read": hr, "row_bytes": D * 4, "pcie_bytes_closed_form": pcie,
+              "pcie_bytes_per_query": round(pcie / B, 1), "pass_b_survivors": surv,
+              "fine_level": ix.fine_codes is not None,
+              "stage_z_ms": round(stage["pass2_merge_ms"], 4)}
         pp = load_profile(f"refine_cfg{cfg_id}_pcie", N=N, nprobe=nprobe, K=K, B=B)
         if pp:
             oc["pcie_bytes_measured"] = pp["pcie_bytes_per_search"]

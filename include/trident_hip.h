@@ -96,6 +96,14 @@ typedef struct TridentIndexView {
     const float* r_vec_sorted;       /* [N] |x - c(x)| in sorted order, float32 of the float64 norm
                                         (reference r_vec_sorted, src/trident_v4_kernels.cu:1216);
                                         mode 11 only, else may be NULL */
+    /* Fine level (optional, both or none; no counterpart in the reference): 16-bit codes of
+     * every rotated row on its own grid.  Used by the batched route when xb_sorted is mapped
+     * host memory: the seeds' and the survivors' bounds then come from HBM within ~1e-3
+     * relative, and only rows that can still enter the top-K cross PCIe. */
+    const uint16_t* fine_codes;      /* [N, D_pad] sorted order: rint((x_rot - offset) / step) */
+    const float* fine_qp;            /* [N, 4]: offset, step (x_fine = offset + code * step, one
+                                        rounding in float64), rho >= |x_rot(exact) - x_fine|
+                                        (rounded up), 0 */
 } TridentIndexView;
 
 /* How mode 2 is executed.  Both are exact; they differ in speed only. */
@@ -140,6 +148,8 @@ typedef struct TridentSearchOutputs {
     float* tau_sq;        /* [B] pass-1 threshold (squared, rounded up), or NULL */
     int64_t* stats;       /* [4] candidates, scanned dims, survivors, refined-inserted; or NULL */
     void* const* events;  /* hipEvent_t handles recorded at TridentStageEvent points, or NULL */
+    int64_t* host_rows;   /* [1] base rows read from a host-mapped xb_sorted (4*D bytes each, over
+                             PCIe: exact seeds, Stage Z, overflow rescans), or NULL */
 } TridentSearchOutputs;
 
 /* Timing events for TridentSearchOutputs.events (hipEventCreate / Destroy / ElapsedTime). */
@@ -205,6 +215,13 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
                        const int32_t* qids, const int32_t* cids, const int64_t* spos, int32_t n,
                        void* workspace, size_t workspace_bytes, double* lb, double* ub,
                        void* stream);
+
+/* The fine-level bounds the out-of-core search uses, for (query, sorted-position) pairs:
+ * lb[i] <= d64(q, x) <= ub[i].  No reference counterpart (exposed for bound-rigour tests).
+ * workspace: >= trident_workspace_bytes(ix, B, 1, 1) bytes. */
+int trident_fine_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
+                       const int32_t* qids, const int64_t* spos, int32_t n, void* workspace,
+                       size_t workspace_bytes, double* lb, double* ub, void* stream);
 
 /* Pinned, device-mapped host memory for the out-of-core base. */
 int trident_host_alloc_mapped(size_t bytes, void** host_ptr);

@@ -1,0 +1,106 @@
+"""Out-of-core search with the second SQ level (residual codes): the bounds it takes from HBM
+bracket the canonical float64 distance and are tight, and searches that use them stay exact
+while refining fewer rows over PCIe than without them."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import assert_exact, build_index, oracle_search
+from trident_amd import _lib, datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _q(xq, dev):
+    return torch.as_tensor(np.ascontiguousarray(xq, np.float32)).to(dev).contiguous()
+
+
+@pytest.fixture(scope="module")
+def host_sets(dev):
+    out = {}
+    xb, xq = datagen.cfg2(N=40_000, D=128, B=600, n_centers=64, seed=91)
+    out["hist"] = build_index(xb, 64, dev, xb_placement="host", max_batch=1024), xq.numpy()
+    xb, xq = datagen.cfg3(N=8_000, D=300, B=200, n_centers=32, seed=92)
+    out["wide300"] = build_index(xb, 24, dev, xb_placement="host", max_batch=256), xq.numpy()
+    xb, xq = datagen.cfg1(N=20_000, D=72, B=400, n_centers=32, seed=93)
+    out["gmm72"] = build_index(xb, 40, dev, xb_placement="host", max_batch=512, per_cluster_sq8=0), xq.numpy()
+    yield out
+    torch.cuda.synchronize()
+    for b, _ in out.values():
+        b.ix.storage._host_buf.free()
+
+
+@pytest.mark.parametrize("name", ["hist", "wide300", "gmm72"])
+def test_fine_bounds_bracket_exact_distance(host_sets, dev, name):
+    b, xq = host_sets[name]
+    ix = b.ix
+    assert ix.fine_codes is not None and ix.fine_qp is not None
+    xq = xq[:6]
+    cids, _ = O.coarse_probe(xq, b.centroids_idx, 4)
+    qids, spos = [], []
+    for q in range(len(xq)):
+        for c in cids[q]:
+            for s in range(b.vec_off[c], b.vec_off[c + 1]):
+                qids.append(q), spos.append(s)
+    qids = np.array(qids, np.int32)
+    spos = np.array(spos, np.int64)
+    d64 = O.pair_dists(xq, b.xb_sorted, qids, spos)
+    view = ix.view()
+    L = _lib.lib()
+    nbytes = L.trident_workspace_bytes(ctypes.byref(view), len(xq), 1, 1)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    tq, ts = (torch.as_tensor(a).to(dev) for a in (qids, spos))
+    lb = torch.empty(len(qids), dtype=torch.float64, device=dev)
+    ub = torch.empty_like(lb)
+    xqd = _q(xq, dev)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = L.trident_fine_bounds(ctypes.byref(view), P(xqd), len(xq), P(tq), P(ts), len(qids), P(ws),
+                              ctypes.c_size_t(nbytes), P(lb), P(ub),
+                              ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(rc, "trident_fine_bounds")
+    torch.cuda.synchronize()
+    lb, ub = lb.cpu().numpy(), ub.cpu().numpy()
+    assert (lb <= d64).all(), f"lb > d64 by {(lb - d64).max()}"
+    assert (ub >= d64).all(), f"ub < d64 by {(d64 - ub).max()}"
+    # a second SQ level: the bracket is a small fraction of the distance
+    assert np.median((ub - lb) / d64) < 2e-2, np.median((ub - lb) / d64)
+
+
+@pytest.mark.parametrize("name", ["hist", "wide300", "gmm72"])
+def test_fine_mode_is_exact_and_refines_fewer_rows(host_sets, dev, name):
+    b, xq = host_sets[name]
+    ix = b.ix
+    xqd = _q(xq, dev)
+    for K, nprobe, ub in ((10, 16, 1), (1, 8, 1), (100, 6, 2), (10, 24, 0)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        kept, rows = {}, {}
+        for res in (True, False):
+            codes, rho = ix.fine_codes, ix.fine_qp
+            if not res:
+                ix.fine_codes = ix.fine_qp = None
+            try:
+                st = torch.zeros(4, dtype=torch.int64, device=dev)
+                hr = torch.full((1,), -1, dtype=torch.int64, device=dev)
+                d, i, _ = ix.search(xqd, nprobe, mode=2, k=K, ub_seed=ub, route=2, stats_buf=st,
+                                    host_rows_buf=hr)
+                torch.cuda.synchronize()
+                assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri,
+                             f"{name} res={res} K={K} nprobe={nprobe} ub={ub}")
+                kept[res], rows[res] = int(st[3]), int(hr[0])
+            finally:
+                ix.fine_codes, ix.fine_qp = codes, rho
+        # rows refined exactly and kept (d64 <= tau) were read; the residual filter reads fewer
+        assert rows[True] >= kept[True] and rows[False] >= kept[False], (rows, kept)
+        assert kept[True] <= kept[False] and rows[True] < rows[False], (rows, kept)
+
+
+def test_host_rows_is_zero_for_a_device_base(dev):
+    xb, xq = datagen.cfg2(N=20_000, D=64, B=200, n_centers=32, seed=94)
+    b = build_index(xb, 32, dev, max_batch=256)
+    hr = torch.full((1,), -1, dtype=torch.int64, device=dev)
+    b.ix.search(_q(xq.numpy(), dev), 8, mode=2, k=10, route=2, host_rows_buf=hr)
+    torch.cuda.synchronize()
+    assert int(hr[0]) == 0

@@ -40,6 +40,11 @@ def _same_index(a, b):
         assert torch.equal(getattr(a.storage, n).cpu(), getattr(b.storage, n).cpu()), n
     for x, y in zip(a.cent_band, b.cent_band):
         assert (torch.equal(x, y) if isinstance(x, torch.Tensor) else x == y)
+    for n in ("fine_codes", "fine_qp"):
+        ta, tb = getattr(a, n, None), getattr(b, n, None)
+        assert (ta is None) == (tb is None), n
+        if ta is not None:
+            assert ta.dtype == tb.dtype and torch.equal(ta.cpu(), tb.cpu()), n
 
 
 def test_round_trip_with_base(cpu_index, tmp_path):
@@ -62,6 +67,17 @@ def test_round_trip_without_base(cpu_index, tmp_path):
         persist.load_index(str(tmp_path), device="cpu")
     got = persist.load_index(str(tmp_path), device="cpu", xb_raw=xb, max_batch=8, max_nprobe=8)
     _same_index(ix, got)
+
+
+def test_round_trip_with_fine_level(tmp_path):
+    xb, _ = datagen.cfg2(N=4000, D=64, B=8, n_centers=16, seed=8)
+    cen, lid, r, mean64, R64, _ = clustering.train_clustering(xb, 16, seed=0, niter=4)
+    st = SharedClusterStorage(xb.numpy(), lid, r, 16, device="cpu")
+    ix = TridentV4Index(st, cen, mean64, R64, tile_size=64, device="cpu", max_batch=8, max_nprobe=8,
+                        fine_level=True)
+    persist.save_index(ix, str(tmp_path))
+    assert (tmp_path / "fine_codes.bin").exists() and (tmp_path / "fine_qp.bin").exists()
+    _same_index(ix, persist.load_index(str(tmp_path), device="cpu", max_batch=8, max_nprobe=8))
 
 
 def test_damaged_directories_are_refused(cpu_index, tmp_path):

@@ -36,7 +36,7 @@ class TridentIndexView(ctypes.Structure):
         ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P), ("vec_Ar", _P),
         ("sq8_cells", _P),
         ("cent_rows", _P), ("cent_tiles", _P), ("cent_norms", _P), ("cent_norm_max", _f64),
-        ("r_vec_sorted", _P),
+        ("r_vec_sorted", _P), ("fine_codes", _P), ("fine_qp", _P),
     ]
 
 
@@ -52,7 +52,7 @@ ROUTE_AUTO, ROUTE_PAIR, ROUTE_BATCHED = 0, 1, 2
 class TridentSearchOutputs(ctypes.Structure):
     _fields_ = [("topk_d", _P), ("topk_i", _P), ("probe_cids", _P), ("probe_dqcs", _P),
                 ("probe_ld", _i32), ("n_events", _i32), ("tau_sq", _P), ("stats", _P),
-                ("events", ctypes.POINTER(_P))]
+                ("events", ctypes.POINTER(_P)), ("host_rows", _P)]
 
 
 # Stage boundaries recorded into TridentSearchOutputs.events (enum TridentStageEvent).
@@ -71,6 +71,8 @@ EXPORTS = {
     "trident_p_init_rule": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "trident_route_for": (_i32, [ctypes.POINTER(TridentIndexView), _i32, _i32, _i32, _i32]),
     "trident_sq8_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _P, _P, _P, _i32,
+                                          _P, ctypes.c_size_t, _P, _P, _P]),
+    "trident_fine_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _P, _P, _i32,
                                           _P, ctypes.c_size_t, _P, _P, _P]),
     "trident_host_alloc_mapped": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_P)]),
     "trident_host_free": (ctypes.c_int, [_P]),

@@ -203,6 +203,116 @@ __device__ __forceinline__ double shfl_f64(double v, int src) {
     return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
 }
 
+// Fine-level bounds of sorted row pos for a query whose float64 rotated row is q64 (D_pad
+// values) and whose rotation error has norm <= qe: lb <= d64(x, q) <= ub.  The row's fine codes
+// (16 bits per dimension on its own grid) give x_fine_d = offset + code_d * step, one rounding
+// per dimension (the product is exact in float64), as the builder computes it, and
+// rho_x >= |x_rot(exact) - x_fine|.  With h = |x_fine - q64| in float64 (relative error
+// <= (D_pad + 2) 2^-53 < 1e-12), |x_rot - q_rot| lies in [h (1 - 1e-12) - rho_x - qe,
+// h (1 + 1e-12) + rho_x + qe], mapped to the original space by the rotation's squared
+// singular-value bounds, with 1e-12 for the canonical float64 distance's own rounding.
+__device__ inline void fine_row_bounds(const BatchArgs& a, const double* q64, double qe, int pos,
+                                       double& lb, double& ub) {
+    const int D_pad = a.D_pad;
+    const uint4* rc = reinterpret_cast<const uint4*>(a.fine_codes + (size_t)pos * D_pad);
+    const float4 qp = reinterpret_cast<const float4*>(a.fine_qp)[pos];  // offset, step, rho
+    const double o = (double)qp.x, st = (double)qp.y;
+    double s = 0.0;
+    for (int g0 = 0; g0 < D_pad / 8; g0 += 4) {  // 32 dims, four 16-byte loads in flight
+        uint4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = g0 + u < D_pad / 8 ? rc[g0 + u] : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (g0 + u >= D_pad / 8) break;
+            const uint32_t w4[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const double c = (double)((w4[k >> 1] >> (16 * (k & 1))) & 0xffffu);
+                const double t = fma(c, st, o) - q64[8 * (g0 + u) + k];
+                s = fma(t, t, s);
+            }
+        }
+    }
+    const double h = sqrt(s);
+    const double e = (double)qp.z + qe;
+    const double lo = fmax(h * (1.0 - 1e-12) - e, 0.0), hi = h * (1.0 + 1e-12) + e;
+    lb = lo * lo / a.rot_sq_max * (1.0 - 1e-12);
+    ub = hi * hi / a.rot_sq_min * (1.0 + 1e-12);
+}
+
+// Fine filter (fine_mode), after the lower-bound pass, in two launches:
+//   fine_filter_kernel: the fine-level bounds of every listed survivor, one wave per (query,
+//     64-slot chunk) as the refine (a query with many survivors spreads over many waves); the
+//     slot's key holds them until the refine: lb rounded down to float32 in the high word, ub
+//     rounded up in the low word;
+//   fine_tau_kernel: one wave per query, tau drops to the K-th smallest ub (K distinct rows have
+//     d64 <= it).
+// Every row with d64 <= the old tau is listed, so every row of the exact top-K keeps
+// lb <= the new tau, and the refine reads only rows with lb <= tau.  An overflowed list
+// (count > cap) is left alone: the merge rescans that query's probes.
+__device__ __forceinline__ float fine_lb_of(uint64_t k) { return __uint_as_float((uint32_t)(k >> 32)); }
+__device__ __forceinline__ float fine_ub_of(uint64_t k) { return __uint_as_float((uint32_t)k); }
+
+template <int DQ>
+__global__ __launch_bounds__(256) void fine_filter_kernel(BatchArgs a, int B) {
+    __shared__ double s_q64[kWavesPerBlock][DQ];
+    const int lane = threadIdx.x & 63, wid = (int)(threadIdx.x >> 6);
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + wid);
+    if (q >= B) return;
+    const int cnt = a.cand_cnt[q];
+    if (cnt > a.cap || (int)blockIdx.y * kWave >= cnt) return;
+    for (int d = lane; d < a.D_pad; d += kWave) s_q64[wid][d] = a.xrot64[(size_t)q * a.D_pad + d];
+    wave_sync();
+    const double qe = sqrt(a.qep[q]) * (1.0 + 1e-12);
+    uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+    const int32_t* ci = a.cand_id + (size_t)q * a.cap;
+    for (int sl = (int)blockIdx.y * kWave + lane; sl < cnt; sl += kWave * (int)gridDim.y) {
+        double lb, ub;
+        fine_row_bounds(a, s_q64[wid], qe, ci[sl], lb, ub);
+        ck[sl] = ((uint64_t)__float_as_uint(__double2float_rd(lb)) << 32) |
+                 __float_as_uint(__double2float_ru(ub));
+    }
+}
+
+template <int KP>
+__global__ __launch_bounds__(256) void fine_tau_kernel(BatchArgs a, int B) {
+    const int lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6));
+    if (q >= B) return;
+    const int cnt = a.cand_cnt[q];
+    if (cnt <= 0 || cnt > a.cap) return;
+    const uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+    WaveList<KP> L;
+    L.init();
+    for (int s0 = 0; s0 < cnt; s0 += kWave) {
+        const int sl = s0 + lane;
+        const bool in = sl < cnt;
+        list_offer(L, a.K, in ? key_of((double)fine_ub_of(ck[sl])) : kKeyInvalid, in ? sl : kIdInvalid);
+    }
+    uint64_t kk;
+    int32_t ki;
+    L.at(a.K - 1, kk, ki);
+    if (lane == 0 && kk != kKeyInvalid) a.tau[q] = fmin(a.tau[q], dist_of(kk));
+}
+
+template __global__ void fine_filter_kernel<256>(BatchArgs, int);
+template __global__ void fine_filter_kernel<1024>(BatchArgs, int);
+template __global__ void fine_tau_kernel<64>(BatchArgs, int);
+template __global__ void fine_tau_kernel<128>(BatchArgs, int);
+
+// One thread per (query, sorted position) pair: the fine-level bounds, for bound-rigour tests.
+__global__ void fine_bounds_kernel(BatchArgs a, const int32_t* __restrict__ qids,
+                                  const int64_t* __restrict__ spos, int n, double* lb,
+                                  double* ub) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int q = qids[i], pos = (int)spos[i];
+    double ep = 0.0;
+    for (int d = 0; d < a.D_pad; ++d) ep = fma(a.qerr[(size_t)q * a.D_pad + d], a.qerr[(size_t)q * a.D_pad + d], ep);
+    fine_row_bounds(a, a.xrot64 + (size_t)q * a.D_pad, sqrt(ep) * (1.0 + 1e-12), pos, lb[i], ub[i]);
+}
+
 // Exact test of the listed survivors, in place: slot s >= seed_cnt[q] of query q holds a sorted
 // position on entry and (key, original id) on exit, or (kKeyInvalid, kIdInvalid) when the
 // canonical float64 distance exceeds tau[q] or the row is one of the query's seeds (slots
@@ -252,13 +362,16 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
             const bool in = s < cnt;
             const int pos = in ? ci[s] : 0;
             const int oid = in ? a.orig_ids[pos] : -1;
-            const bool need = in && !(ns > 0 && is_seed(oid));
+            // fine_mode: rows whose fine lower bound (the slot's key) exceeds tau stay off PCIe
+            const bool need = in && !(ns > 0 && is_seed(oid)) &&
+                              !(a.fine_mode && (double)fine_lb_of(ck[s]) > tau);
             const uint64_t m = __ballot(need);
             const int nq = __popcll(m), rk = need ? mask_rank(m) : 0;
             if (need) s_pos[wid][rk] = pos;
             wave_sync();
             double acc = 0.0;
             if (nq > 0) acc = refine_rows_mlp(a.xb, D, s_pos[wid], nq, s_stage[wid], s_q64[wid]);
+            if (a.host_rows && lane == 0 && nq > 0) atomicAdd(a.host_rows, (unsigned long long)nq);
             wave_sync();
             const double d = shfl_f64(acc, rk);
             const bool ok = need && d <= tau;
@@ -275,7 +388,7 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
     for (int s = ns + (int)blockIdx.y * kWave + lane; s < cnt; s += kWave * (int)gridDim.y) {
         const int pos = ci[s];
         const int oid = a.orig_ids[pos];
-        if (ns > 0 && is_seed(oid)) {
+        if ((ns > 0 && is_seed(oid)) || (a.fine_mode && (double)fine_lb_of(ck[s]) > tau)) {
             ck[s] = kKeyInvalid;
             ci[s] = kIdInvalid;
             continue;
@@ -1194,7 +1307,28 @@ __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
         // exact seeding: every one of the K smallest entries is finite and has its row
         bool ok = lane >= K || (L.k0 != kKeyInvalid && L.i0 >= 0);
         if constexpr (KP > 64) ok = ok && (lane + kWave >= K || (L.k1 != kKeyInvalid && L.i1 >= 0));
-        if (u < (double)INFINITY && __ballot(!ok) == 0ull) {
+        if (u < (double)INFINITY && __ballot(!ok) == 0ull && a.fine_mode) {
+            // fine codes: the K seeds' upper bounds from HBM; no row crosses PCIe here and
+            // no seed is listed (the lower-bound pass lists every row with d64 <= tau)
+            for (int d = lane; d < a.D_pad; d += kWave) s_q64[wid][d] = a.xrot64[(size_t)q * a.D_pad + d];
+            wave_sync();
+            const double qe = sqrt(a.qep[q]) * (1.0 + 1e-12);
+            double mx = 0.0;
+            for_chunks<KP>([&](auto cc) __attribute__((always_inline)) {
+                constexpr int h = decltype(cc)::value;
+                uint64_t hk;
+                int32_t pos;
+                list_chunk<h>(L, hk, pos);
+                if (h * kWave + lane < K) {
+                    double lb, ub;
+                    fine_row_bounds(a, s_q64[wid], qe, pos, lb, ub);
+                    mx = fmax(mx, ub);
+                }
+            });
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
+            tau = fmin(tau, mx);
+        } else if (u < (double)INFINITY && __ballot(!ok) == 0ull) {
             if (lane < K) s_pos[wid][lane] = L.i0;
             if constexpr (KP > 64)
                 if (lane + kWave < K) s_pos[wid][kWave + lane] = L.i1;
@@ -1215,6 +1349,7 @@ __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
 #pragma unroll
             for (int o = 1; o < kWave; o <<= 1) mx = fmax(mx, shfl_f64(mx, lane ^ o));
             tau = fmin(tau, mx);
+            if (a.host_rows && a.xb_host && lane == 0) atomicAdd(a.host_rows, (unsigned long long)K);
             // the seeds as the first candidates (refined): those within tau
             int cnt = 0;
             uint64_t* ck = a.cand_key + (size_t)q * a.cap;

@@ -812,10 +812,24 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
         if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
     }
+    // where the base lives: mapped host memory (out of core) changes the refine and, with
+    // residual codes, the seeding; the PCIe telemetry counts rows read from there
+    bool xb_host = false;
+    {
+        hipPointerAttribute_t pa;
+        xb_host = hipPointerGetAttributes(&pa, ix->xb_sorted) == hipSuccess &&
+                  pa.type == hipMemoryTypeHost;
+        (void)hipGetLastError();  // an unregistered pointer is not an error here
+    }
+    unsigned long long* host_rows =
+        out->host_rows && xb_host ? reinterpret_cast<unsigned long long*>(out->host_rows) : nullptr;
+    if (out->host_rows && (rc = fill(reinterpret_cast<int32_t*>(out->host_rows), 0, 2, st))) return rc;
     ScanArgs a = make_scan_args(ix, w, K, cap, cascade ? sp->use_l1 : 0,
                                 out->stats ? w.stat_slots : nullptr);
     a.r_vec = ix->r_vec_sorted;
+    a.host_rows = host_rows;
     MergeArgs m{};
+    m.host_rows = host_rows;
     m.B = B;
     m.K = (int)K_list;
     m.hat = hat ? 1 : 0;
@@ -850,12 +864,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.tau = w.tau64;
         b.tau_sq_out = nullptr;
         b.B = B;
-        {
-            hipPointerAttribute_t pa;
-            b.xb_host = hipPointerGetAttributes(&pa, ix->xb_sorted) == hipSuccess &&
-                        pa.type == hipMemoryTypeHost;
-            (void)hipGetLastError();  // an unregistered pointer is not an error here
-        }
+        b.xb_host = xb_host ? 1 : 0;
+        b.host_rows = host_rows;
         b.cand_key = w.cand_key;
         b.cand_id = w.cand_id;
         b.cand_cnt = w.cand_cnt;
@@ -868,6 +878,11 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.rot_sq_min = ix->rot_sq_min;
         b.rot_sq_max = ix->rot_sq_max;
         b.sum_rel = sum_rel_of(ix->D_pad);
+        // fine level: used when the rows live across PCIe (the seeds' and survivors' bounds
+        // then come from HBM, and only rows that can still enter the top-K are read)
+        b.fine_codes = ix->fine_codes;
+        b.fine_qp = ix->fine_qp;
+        b.fine_mode = ix->fine_codes && ix->fine_qp && b.xb_host ? 1 : 0;
         b.units = w.units;
         b.unit_off = w.unit_off;
         b.max_units = (int)w.max_units;
@@ -937,6 +952,16 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.ctr = w.unit_ctr + 8 * kCtrStride;
         if ((rc = launch_batch<false>(b, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
+        if (b.fine_mode) {
+            const unsigned qg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
+            const dim3 fgrid(qg, (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
+            if (ix->D <= 256) fine_filter_kernel<256><<<fgrid, kBlock, 0, st>>>(b, B);
+            else fine_filter_kernel<1024><<<fgrid, kBlock, 0, st>>>(b, B);
+            if ((rc = check_launch("fine_filter_kernel"))) return rc;
+            if (K <= 64) fine_tau_kernel<64><<<qg, kBlock, 0, st>>>(b, B);
+            else fine_tau_kernel<128><<<qg, kBlock, 0, st>>>(b, B);
+            if ((rc = check_launch("fine_tau_kernel"))) return rc;
+        }
         // one wave per (query, 64-slot chunk of its list): a query with many survivors spreads
         // over many waves
         // the chunk dimension stops at 16: waves loop over further chunks
@@ -1037,6 +1062,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         r.D = ix->D;
         r.out_d = out->topk_d;
         r.out_i = out->topk_i;
+        r.host_rows = host_rows;
         if ((rc = K <= 64 ? launch_rerank<64>(r, st) : launch_rerank<128>(r, st))) return rc;
     }
     if ((rc = mark(TRIDENT_EV_END))) return rc;
@@ -1105,6 +1131,41 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
     ScanArgs a = make_scan_args(ix, w, 1, 1, 0, nullptr);
     sq8_bounds_kernel<<<(n + 255) / 256, 256, 0, st>>>(a, qids, cids, spos, n, lb, ub);
     return check_launch("sq8_bounds_kernel");
+}
+
+int trident_fine_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
+                       const int32_t* qids, const int64_t* spos, int32_t n, void* workspace,
+                       size_t workspace_bytes, double* lb, double* ub, void* stream) {
+    int rc = validate_index(ix);
+    if (rc) return rc;
+    if (!ix->fine_codes || !ix->fine_qp)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "fine_bounds needs fine_codes and fine_qp");
+    if (B < 1 || n < 0 || !xq || !qids || !spos || !lb || !ub)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "bad fine_bounds arguments");
+    Workspace w = carve(ix, workspace, B, 1, 1);
+    if (!workspace || workspace_bytes < w.bytes)
+        return fail(TRIDENT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu < %zu bytes", workspace_bytes,
+                    w.bytes);
+    if (n == 0) return TRIDENT_OK;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int ldw = ix->nlist + ix->D_pad;
+    const int cols = std::max(ix->D, ix->D_pad);
+    prep_queries_kernel<<<dim3((cols + 127) / 128, (B + 4 * kPrepQB - 1) / (4 * kPrepQB)),
+                          dim3(64, 4), 0, st>>>(
+        xq, B, ix->D, ix->D_pad, ix->W_combined, ldw, ix->nlist, ix->b_combined, w.xq64,
+        w.xrot64, w.xrot32, w.qerr, 1);
+    if ((rc = check_launch("prep_queries_kernel"))) return rc;
+    BatchArgs b{};
+    b.D = ix->D;
+    b.D_pad = ix->D_pad;
+    b.xrot64 = w.xrot64;
+    b.qerr = w.qerr;
+    b.rot_sq_min = ix->rot_sq_min;
+    b.rot_sq_max = ix->rot_sq_max;
+    b.fine_codes = ix->fine_codes;
+    b.fine_qp = ix->fine_qp;
+    fine_bounds_kernel<<<(n + 255) / 256, 256, 0, st>>>(b, qids, spos, n, lb, ub);
+    return check_launch("fine_bounds_kernel");
 }
 
 int trident_event_create(void** event) {

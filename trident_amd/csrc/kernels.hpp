@@ -38,6 +38,7 @@ struct ScanArgs {
     int32_t* cand_cnt;
     int cap, K;                 // K: entries kept (and emitted) per pair
     unsigned long long* stats;  // [4] or null
+    unsigned long long* host_rows;  // [1] rows read from a host-mapped base, or null
     double lb_scale;            // tau -> float32 Stage Y threshold factor
     double ub_scale;            // Stage X sum -> float64 distance bound factor
 };
@@ -67,6 +68,7 @@ struct MergeArgs {
     const int32_t* tile_oids;
     const int32_t* tile_off;
     int T, D;
+    unsigned long long* host_rows;  // [1] rows read by the rescan (host-mapped base), or null
 };
 
 // Per-(query, cluster) pair scalars of the batched bound (threshold-independent part).
@@ -154,6 +156,13 @@ struct BatchArgs {
     unsigned long long* stats;  // [kStatSlots, 4] or null
     double rot_sq_min, rot_sq_max;
     double sum_rel;             // relative error bound of the per-pair float32 sums (sum_rel_of)
+    // Fine level (used when the base is in host memory): per sorted row, 16-bit codes of x_rot
+    // on the row's own grid and (offset, step, rho >= |x_rot - x_fine|), so that bounds within
+    // ~1e-3 relative come from HBM instead of the exact row over PCIe.
+    const uint16_t* fine_codes; // [N, D_pad] or null
+    const float* fine_qp;       // [N, 4] (offset, step, rho, 0)
+    int fine_mode;              // 1: seeds bounded and survivors filtered with the fine level
+    unsigned long long* host_rows;  // [1] rows read from the host-mapped base, or null
 };
 
 constexpr int kStatSlots = 64;  // telemetry counters are spread over this many [4] slots
@@ -279,6 +288,7 @@ struct RerankArgs {
     int D;
     float* out_d;              // [B, K]
     int64_t* out_i;
+    unsigned long long* host_rows;  // [1] rows read from a host-mapped base, or null
 };
 
 template <int KO>
@@ -347,6 +357,15 @@ __global__ void lb_prep_kernel(BatchArgs a);
 
 template <int KP, int DQ>
 __global__ void ub_kth_kernel(BatchArgs a);
+
+template <int DQ>
+__global__ void fine_filter_kernel(BatchArgs a, int B);
+
+template <int KP>
+__global__ void fine_tau_kernel(BatchArgs a, int B);
+
+__global__ void fine_bounds_kernel(BatchArgs a, const int32_t* __restrict__ qids,
+                                  const int64_t* __restrict__ spos, int n, double* lb, double* ub);
 
 // Bounds a seeding unit lists per query: its K smallest, at most 64.
 __host__ __device__ constexpr int ub_per_unit(int K) { return K < 64 ? K : 64; }

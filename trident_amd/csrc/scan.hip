@@ -279,6 +279,7 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
 
     auto flush = [&](int cnt) {
         const double d64 = refine_rows(a.xb, D, my_qspos, cnt, my_stage, s_q64);
+        if (a.host_rows && lane == 0) atomicAdd(a.host_rows, (unsigned long long)cnt);
         const bool ok = lane < cnt && d64 <= thr;
         if (a.stats) st_ins += __popcll(__ballot(ok));
         if (list_offer(L, K, ok ? key_of(d64) : kKeyInvalid, ok ? my_qoid[lane] : kIdInvalid)) {
@@ -471,6 +472,7 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
         for (int p = 0; p < a.nprobe; ++p) {
             const int c = a.probe_cids[(size_t)q * a.nprobe + p];
             const int v0 = a.vec_off[c], n = a.vec_off[c + 1] - v0, t0 = a.tile_off[c];
+            if (a.host_rows && lane == 0) atomicAdd(a.host_rows, (unsigned long long)max(n, 0));
             for (int b0 = 0; b0 < n; b0 += kWave) {
                 const int li = b0 + lane;
                 uint64_t k = kKeyInvalid;
@@ -562,6 +564,7 @@ __global__ __launch_bounds__(256) void rerank_kernel(RerankArgs a) {
     wave_sync();
     double d64 = 0.0;
     if (nv > 0) d64 = refine_rows(a.xb, a.D, s_spos[wid], nv, s_stage[wid], s_q64);
+    if (a.host_rows && lane == 0 && nv > 0) atomicAdd(a.host_rows, (unsigned long long)nv);
     WaveList<KO> L;
     L.init();
     list_offer(L, a.K, v ? key_of(d64) : kKeyInvalid, v ? (int32_t)(uint32_t)hk : kIdInvalid);

@@ -145,7 +145,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
                     rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
                     eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
-                    cent_band=None, r_vec_sorted=None) -> TridentIndexView:
+                    cent_band=None, r_vec_sorted=None, fine_codes=None, fine_qp=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -167,6 +167,8 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.vec_Ar = _ptr(vec_Ar)
     v.sq8_cells = _ptr(sq8_cells)
     v.r_vec_sorted = _ptr(r_vec_sorted)
+    v.fine_codes = _ptr(fine_codes)
+    v.fine_qp = _ptr(fine_qp)
     if cent_band is not None:
         rows, tiles, norms, nmax = cent_band
         v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
@@ -262,7 +264,8 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
                 probe_cids: Optional[torch.Tensor] = None,
                 probe_dqcs: Optional[torch.Tensor] = None, tau_sq: Optional[torch.Tensor] = None,
                 stats: Optional[torch.Tensor] = None, record_events: bool = False,
-                stream: Optional[torch.cuda.Stream] = None, stage_events=None) -> float:
+                stream: Optional[torch.cuda.Stream] = None, stage_events=None,
+                host_rows: Optional[torch.Tensor] = None) -> float:
     """Runs trident_search on an index view; all tensors already validated by the caller."""
     B, K = int(xq.shape[0]), int(topk_d.shape[1])
     L = _lib.lib()
@@ -285,6 +288,7 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
     out.probe_ld = ld
     out.tau_sq = _ptr(tau_sq)
     out.stats = _ptr(stats)
+    out.host_rows = _ptr(host_rows)
     if stage_events is not None:
         out.events = stage_events.handles
         out.n_events = _lib.EV_COUNT
@@ -319,6 +323,8 @@ def launch_trident_v4_search(
     vec_Ar: Optional[torch.Tensor] = None, route: int = 0,
     sq8_cells: Optional[torch.Tensor] = None,
     cent_band=None,
+    fine_codes: Optional[torch.Tensor] = None, fine_qp: Optional[torch.Tensor] = None,
+    host_rows: Optional[torch.Tensor] = None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -370,6 +376,12 @@ def launch_trident_v4_search(
             _check_tensor(name, t, torch.float32, dev)
             _need(t.numel() == rows * D_pad, f"{name} must be [{rows}, D_pad]")
         _check_tensor("blk_bounds4", blk_bounds4, torch.int32, dev, 1)
+    if fine_codes is not None or fine_qp is not None:
+        _need(fine_codes is not None and fine_qp is not None, "fine_codes and fine_qp go together")
+        _check_tensor("fine_codes", fine_codes, torch.int16, dev, 2)
+        _need(tuple(fine_codes.shape) == (N, D_pad), "fine_codes must be [N, D_pad] int16 (uint16 bits)")
+        _check_tensor("fine_qp", fine_qp, torch.float32, dev, 2)
+        _need(tuple(fine_qp.shape) == (N, 4), "fine_qp must be [N, 4] float32")
     if vec_Ar is not None:
         _check_tensor("vec_Ar", vec_Ar, torch.float32, dev, 2)
         _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float32")
@@ -388,6 +400,9 @@ def launch_trident_v4_search(
     if stats_buf is not None:
         _check_tensor("stats_buf", stats_buf, torch.int64, dev)
         _need(stats_buf.numel() >= 4, "stats_buf needs 4 entries")
+    if host_rows is not None:
+        _check_tensor("host_rows", host_rows, torch.int64, dev)
+        _need(host_rows.numel() >= 1, "host_rows needs 1 entry")
     if probe_cids_buf is not None:
         _check_tensor("probe_cids_buf", probe_cids_buf, torch.int32, dev, 2)
         _need(probe_cids_buf.shape[0] >= B and probe_cids_buf.shape[1] >= nprobe, "probe_cids_buf too small")
@@ -428,10 +443,11 @@ def launch_trident_v4_search(
         orig_ids_sorted=orig_ids_sorted, vmin=vmin if sq8 else None,
         delta=delta if sq8 else None, eps_dim=eps_dim if sq8 else None,
         blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
-        sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted)
+        sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted,
+        fine_codes=fine_codes if mode == 2 else None, fine_qp=fine_qp if mode == 2 else None)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route,
                        rerank_m=int(rerank_m) if mode == 0 else 0, probe_cids=probe_cids_buf,
-                       probe_dqcs=probe_dqcs_buf, tau_sq=tau_sq, stats=stats_buf,
+                       probe_dqcs=probe_dqcs_buf, tau_sq=tau_sq, stats=stats_buf, host_rows=host_rows,
                        record_events=bool(record_events), stage_events=stage_events)

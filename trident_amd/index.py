@@ -257,8 +257,14 @@ class TridentV4Index:
 
     def __init__(self, storage: SharedClusterStorage, centroids, mean64, R64, tile_size: int = 256,
                  per_cluster_sq8: int = 1, use_pca: int = 1, var_block: int = 0, max_batch: int = 1024,
-                 max_nprobe: int = 512, device="cuda:0", k: int = 10, chunk_rows: int = 1 << 20):
+                 max_nprobe: int = 512, device="cuda:0", k: int = 10, chunk_rows: int = 1 << 20,
+                 fine_level: Optional[bool] = None):
+        """``fine_level`` (default: when the base is in host memory) also builds the fine level
+        (``fine_codes``, ``fine_qp``: 16-bit codes of every rotated row on its own grid) that the
+        out-of-core search bounds its rows with."""
         t_start = time.perf_counter()
+        if fine_level is None:
+            fine_level = getattr(storage, "placement", "device") == "host"
         self.storage = storage
         self.dev = torch.device(device)
         self.N, self.D, self.nlist = storage.N, storage.D, storage.nlist
@@ -347,6 +353,13 @@ class TridentV4Index:
         self.vec_Ar = torch.empty((N, 2), device=dev, dtype=torch.float32)
         # residual norms |x - c(x)| in float64, for the tile band of use_l1 (tile_r_minmax)
         res_norm = torch.empty(N, device=dev, dtype=torch.float64)
+        # Fine level: per row, offset = the smallest rotated coordinate (rounded down to float32),
+        # step = its range / 65535 (rounded up), code = rint((x_rot - offset) / step) in 16 bits
+        # (stored as int16 bit patterns), x_fine = offset + code * step (the product is exact in
+        # float64, the sum rounded once, as the kernels compute it) and rho >= |x_rot(exact) -
+        # x_fine| (the float64 rotation's error included), rounded up.
+        self.fine_codes = torch.empty((N, D_pad), device=dev, dtype=torch.int16) if fine_level else None
+        self.fine_qp = torch.zeros((N, 4), device=dev, dtype=torch.float32) if fine_level else None
         for s in range(0, N, chunk_rows):
             e = min(N, s + chunk_rows)
             res_norm[s:e] = torch.sqrt(((rows_dev(s, e).double() - cen[lid_sorted[s:e]].double()) ** 2).sum(1))
@@ -365,6 +378,17 @@ class TridentV4Index:
             self.vec_Ar[s:e, 0] = -round_up_f32(-a64)
             r_q = torch.sqrt(((xr64 - xhat) ** 2).sum(1)) + torch.sqrt((rerr ** 2).sum(1))
             self.vec_Ar[s:e, 1] = round_up_f32(r_q * (1.0 + 1e-12) + 1e-300)
+            if fine_level:
+                lo = -round_up_f32(-xr64.amin(1))                            # offset <= min
+                span = (xr64.amax(1) - lo.double()) / 65535.0
+                st = round_up_f32(torch.clamp(span * (1.0 + 2.0 ** -40), min=2.0 ** -100))
+                c = torch.clamp(torch.round((xr64 - lo.double().unsqueeze(1)) / st.double().unsqueeze(1)), 0.0, 65535.0)
+                self.fine_codes[s:e] = (c - 65536.0 * (c >= 32768.0)).to(torch.int16)
+                xf = lo.double().unsqueeze(1) + c * st.double().unsqueeze(1)
+                rho = torch.sqrt(((xr64 - xf) ** 2).sum(1)) + torch.sqrt((rerr ** 2).sum(1))
+                self.fine_qp[s:e, 0] = lo
+                self.fine_qp[s:e, 1] = st
+                self.fine_qp[s:e, 2] = round_up_f32(rho * (1.0 + 1e-12) + 1e-300)
         self.vmin_pad = vmin.contiguous()
         self.delta_pad = delta.contiguous()
         self.eps_pad = round_up_f32(err_max * (1.0 + 2.0 ** -20) + 1e-300).contiguous()
@@ -468,9 +492,12 @@ class TridentV4Index:
     def search(self, xq_gpu: torch.Tensor, nprobe: int, mode: int = 2, use_l1: int = 0, rerank_m: int = 0,
                tile_override: int = 0, warp_refine: int = 1, stats_buf: Optional[torch.Tensor] = None,
                record_kernel_ms: bool = False, k: Optional[int] = None, ub_seed: Optional[int] = None,
-               stage_events=None, route: int = 0):
-        """Reference TridentV4Index.search (phase4a_suite.py:280-342) plus ``k=``, ``ub_seed=`` and
-        ``route=`` (0 auto, 1 per-pair cascade, 2 cluster-batched matrix-core cascade)."""
+               stage_events=None, route: int = 0, p_init: int = -1,
+               host_rows_buf: Optional[torch.Tensor] = None):
+        """Reference TridentV4Index.search (phase4a_suite.py:280-342) plus ``k=``, ``ub_seed=``,
+        ``route=`` (0 auto, 1 per-pair cascade, 2 cluster-batched matrix-core cascade) and
+        ``p_init=`` (probes of the first pass per query; -1 = the reference's rule) and
+        ``host_rows_buf=`` (int64 [1]: receives the base rows read from host memory)."""
         if k is not None:
             self.set_k(k)
         B = int(xq_gpu.shape[0])
@@ -495,8 +522,10 @@ class TridentV4Index:
             self.cand_buf_d, self.cand_buf_i, self.cand_cnt,
             bool(record_kernel_ms), int(warp_refine), stats_buf,
             ub_seed=ub_seed, rot_sq_bounds=(self.rot_sq_min, self.rot_sq_max), stage_events=stage_events,
+            p_init=p_init,
             vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band,
-            r_vec_sorted=self.r_vec_sorted)
+            r_vec_sorted=self.r_vec_sorted, fine_codes=self.fine_codes, fine_qp=self.fine_qp,
+            host_rows=host_rows_buf)
         return topk_d, topk_i, kern_ms
 
     def view(self):
@@ -511,7 +540,8 @@ class TridentV4Index:
             cluster_tile_off=self.cluster_tile_off, cluster_vec_off=st.cluster_vec_off,
             xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
             delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
-            sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted)
+            sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted,
+            fine_codes=self.fine_codes, fine_qp=self.fine_qp)
 
     def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
         """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a mode-2 search of B queries takes."""

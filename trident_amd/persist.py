@@ -17,6 +17,8 @@ with ``numpy.memmap`` and streamed to the device in chunks -- and stores everyth
   tile_orig_ids.bin   int32 [tiles, T]
   vec_Ar.bin          float32 [N, 2]       per-vector scalars of the batched route
   r_vec_sorted.bin    float32 [N]          |x - c| (mode 11)
+  fine_codes.bin      int16 [N, D_pad]     fine level: 16-bit row codes (when the index has it)
+  fine_qp.bin         float32 [N, 4]       their offset, step and error bound
   xb_sorted.bin       float32 [N, D]       the cluster-sorted base (optional)
 
 The code cells of the batched route and the centroid layouts of the coarse pass are
@@ -66,6 +68,9 @@ def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=
         "vec_Ar": ix.vec_Ar,
         "r_vec_sorted": ix.r_vec_sorted,
     }
+    if getattr(ix, "fine_codes", None) is not None:
+        bins["fine_codes"] = ix.fine_codes
+        bins["fine_qp"] = ix.fine_qp
     if include_base:
         _need(st.xb_sorted is not None, "the storage's base has been freed")
         bins["xb_sorted"] = st.xb_sorted
@@ -101,8 +106,8 @@ def _need(cond: bool, msg: str):
         raise ValueError(msg)
 
 
-_NP = {"int32": np.int32, "float32": np.float32}
-_TORCH = {"int32": torch.int32, "float32": torch.float32}
+_NP = {"int32": np.int32, "float32": np.float32, "int16": np.int16}
+_TORCH = {"int32": torch.int32, "float32": torch.float32, "int16": torch.int16}
 
 
 def _open_bins(path: str, meta) -> dict:
@@ -175,6 +180,8 @@ def load_index(path: str, device="cuda:0", xb_placement: str = "device", xb_raw=
     ix.tile_orig_ids = _to_device(bins["tile_orig_ids"], dev)
     ix.vec_Ar = _to_device(bins["vec_Ar"], dev)
     ix.r_vec_sorted = _to_device(bins["r_vec_sorted"], dev)
+    ix.fine_codes = _to_device(bins["fine_codes"], dev) if "fine_codes" in bins else None
+    ix.fine_qp = _to_device(bins["fine_qp"], dev) if "fine_qp" in bins else None
     ix.max_batch, ix.max_nprobe = int(max_batch), int(max_nprobe)
     ix._alloc_buffers()
     if dev.type == "cuda":
