@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TRIDENT_ABI_VERSION 2
+#define TRIDENT_ABI_VERSION 3
 
 enum TridentStatus {
     TRIDENT_OK = 0,
@@ -104,6 +104,10 @@ typedef struct TridentIndexView {
     const float* fine_qp;            /* [N, 4]: offset, step (x_fine = offset + code * step, one
                                         rounding in float64), rho >= |x_rot(exact) - x_fine|
                                         (rounded up), 0 */
+    /* Per-cluster constants of the batched route's bounds (optional; no counterpart in the
+     * reference): [nlist, 4] float64 filled once per index by trident_cluster_bounds.  When
+     * NULL every batched search recomputes them, one pass over vec_Ar (8 N bytes). */
+    const double* cluster_bounds;
 } TridentIndexView;
 
 /* How mode 2 is executed.  Both are exact; they differ in speed only. */
@@ -219,6 +223,12 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
 /* The fine-level bounds the out-of-core search uses, for (query, sorted-position) pairs:
  * lb[i] <= d64(q, x) <= ub[i].  No reference counterpart (exposed for bound-rigour tests).
  * workspace: >= trident_workspace_bytes(ix, B, 1, 1) bytes. */
+/* Fills cluster_bounds ([nlist, 4] float64, device) from delta, eps_dim and vec_Ar: per cluster
+ * A_max >= every |code * delta|^2, r_max >= every stored residual bound, r_lo = the smallest
+ * stored residual bound.  No reference counterpart (index-constant part of the batched route's
+ * bounds, hoisted out of the search). */
+int trident_cluster_bounds(const TridentIndexView* ix, double* cluster_bounds, void* stream);
+
 int trident_fine_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
                        const int32_t* qids, const int64_t* spos, int32_t n, void* workspace,
                        size_t workspace_bytes, double* lb, double* ub, void* stream);

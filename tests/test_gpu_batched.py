@@ -242,3 +242,34 @@ def test_batched_short_and_empty_lists(dev, D):
         d, i = run_search(b, _q(xq, dev), nprobe, K, mode=2, ub=1, route=2)
         assert_exact(d, i, rd, ri, f"short/empty D={D} K={K} nprobe={nprobe}")
         assert (ri == -1).any()  # some query really has fewer than K candidates
+
+
+@pytest.mark.parametrize("name", ["hist", "gmm"])
+def test_cluster_bounds_table(sets, dev, name):
+    """trident_cluster_bounds against a float64 restatement (A_max = 255^2 sum delta^2, r_max =
+    max(2 sqrt(sum eps^2), max r_x), r_lo = min r_x, each with its 1e-12 margin), and a search
+    that recomputes the table per call returns the same results as one given the table."""
+    from trident_amd import ext
+    b, xq = sets[name]
+    ix = b.ix
+    cb = ext.compute_cluster_bounds(ix.view(), dev).cpu().numpy()
+    delta = ix.delta_pad.double().cpu().numpy().reshape(-1, ix.D_pad)
+    eps = ix.eps_pad.double().cpu().numpy().reshape(-1, ix.D_pad)
+    r = ix.vec_Ar[:, 1].double().cpu().numpy()
+    vo = b.vec_off
+    for c in range(ix.nlist):
+        row = c if delta.shape[0] > 1 else 0
+        a_max = 65025.0 * float((delta[row] ** 2).sum()) * (1 + 1e-12)
+        rc = r[vo[c]:vo[c + 1]]
+        r_max = max(2.0 * np.sqrt(float((eps[row] ** 2).sum())), float(rc.max()) if rc.size else 0.0)
+        assert cb[c, 0] == pytest.approx(a_max, rel=1e-13), c
+        assert cb[c, 1] == pytest.approx(r_max * (1 + 1e-12), rel=1e-13), c
+        assert cb[c, 2] == (float(rc.min()) if rc.size else 0.0), c
+    xqd = _q(xq, dev)
+    d1, i1 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=2)
+    saved, ix.cluster_bounds = ix.cluster_bounds, None
+    try:
+        d2, i2 = run_search(b, xqd, 16, 10, mode=2, ub=1, route=2)
+    finally:
+        ix.cluster_bounds = saved
+    assert np.array_equal(i1, i2) and np.array_equal(d1, d2)

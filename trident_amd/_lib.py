@@ -10,7 +10,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libtrident_hip.so")
 
 TRIDENT_OK = 0
-ABI_VERSION = 2  # TRIDENT_ABI_VERSION
+ABI_VERSION = 3  # TRIDENT_ABI_VERSION
 MODE_SQ8_RERANK = 0
 MODE_SQ8 = 1
 MODE_CASCADE = 2
@@ -36,7 +36,7 @@ class TridentIndexView(ctypes.Structure):
         ("vmin", _P), ("delta", _P), ("eps_dim", _P), ("blk_bounds4", _P), ("vec_Ar", _P),
         ("sq8_cells", _P),
         ("cent_rows", _P), ("cent_tiles", _P), ("cent_norms", _P), ("cent_norm_max", _f64),
-        ("r_vec_sorted", _P), ("fine_codes", _P), ("fine_qp", _P),
+        ("r_vec_sorted", _P), ("fine_codes", _P), ("fine_qp", _P), ("cluster_bounds", _P),
     ]
 
 
@@ -72,6 +72,7 @@ EXPORTS = {
     "trident_route_for": (_i32, [ctypes.POINTER(TridentIndexView), _i32, _i32, _i32, _i32]),
     "trident_sq8_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _P, _P, _P, _i32,
                                           _P, ctypes.c_size_t, _P, _P, _P]),
+    "trident_cluster_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _P]),
     "trident_fine_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _P, _P, _i32,
                                           _P, ctypes.c_size_t, _P, _P, _P]),
     "trident_host_alloc_mapped": (ctypes.c_int, [ctypes.c_size_t, ctypes.POINTER(_P)]),

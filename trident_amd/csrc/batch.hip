@@ -86,57 +86,50 @@ __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
     return (seg[c + 1] - seg[c] + kGroupQ - 1) / kGroupQ;
 }
 
-// Block-wide exclusive scan of one count per thread (grid 1); returns the total.
-__device__ __forceinline__ uint32_t block_excl_scan(uint32_t local, uint32_t& run,
-                                                    uint32_t* s_wtot) {
-    const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    uint32_t inc = local;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        const uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
-        if (lane >= o) inc += t;
+// Exclusive scans of the unit counts of the 2 * nlist (pass, cluster) entries and of the
+// weight-group counts of the nlist cluster segments, in two launches of ceil(2 nlist / kBlock)
+// <= kBlock blocks, one entry (and one cluster) per thread: in-block offsets plus block totals
+// (blk_tot[b] units, blk_tot[kBlock + b] groups), then the carries of the blocks before.
+__global__ __launch_bounds__(256) void unit_scan_local_kernel(const int32_t* seg,
+                                                              const int32_t* vec_off, int nlist,
+                                                              int uqB, int seed_all,
+                                                              int32_t* unit_off, int32_t* grp_off,
+                                                              int32_t* blk_tot) {
+    __shared__ uint32_t s_wtot[kWavesPerBlock];
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    const uint32_t nu =
+        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, i) : 0u;
+    const uint32_t ng = i < nlist ? (uint32_t)groups_of_cluster(seg, i) : 0u;
+    uint32_t tu = 0, tg = 0;
+    const uint32_t ru = block_exclusive_scan(nu, s_wtot, &tu);
+    const uint32_t rg = block_exclusive_scan(ng, s_wtot, &tg);
+    if (i < 2 * nlist) unit_off[i] = (int32_t)ru;
+    if (i < nlist) grp_off[i] = (int32_t)rg;
+    if (threadIdx.x == 0) {
+        blk_tot[blockIdx.x] = (int32_t)tu;
+        blk_tot[kBlock + blockIdx.x] = (int32_t)tg;
     }
-    if (lane == kWave - 1) s_wtot[wid] = inc;
-    __syncthreads();
-    uint32_t total = 0;
-    run = inc - local;
-    for (int w = 0; w < kWavesPerBlock; ++w) {
-        if (w < wid) run += s_wtot[w];
-        total += s_wtot[w];
-    }
-    __syncthreads();  // s_wtot is reused by the next scan
-    return total;
 }
 
-// grid 1: exclusive scans of the unit counts of the 2 * nlist (pass, cluster) entries and of
-// the weight-group counts of the nlist cluster segments.
-__global__ __launch_bounds__(256) void unit_scan_kernel(const int32_t* seg, const int32_t* vec_off,
-                                                        int nlist, int uqB, int seed_all,
-                                                        int32_t* unit_off, int32_t* grp_off) {
+__global__ __launch_bounds__(256) void unit_scan_carry_kernel(int nlist, const int32_t* blk_tot,
+                                                              int nblk, int32_t* unit_off,
+                                                              int32_t* grp_off) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
-    const int tid = threadIdx.x;
-    const int E = 2 * nlist;
-    const int per = (E + kBlock - 1) / kBlock;
-    const int e0 = min(E, tid * per), e1 = min(E, e0 + per);
-    const int perc = (nlist + kBlock - 1) / kBlock;
-    const int c0 = min(nlist, tid * perc), c1 = min(nlist, c0 + perc);
-    uint32_t lu = 0, lg = 0;
-    for (int e = e0; e < e1; ++e)
-        lu += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, e);
-    for (int c = c0; c < c1; ++c) lg += (uint32_t)groups_of_cluster(seg, c);
-    uint32_t ru = 0, rg = 0;
-    const uint32_t tu = block_excl_scan(lu, ru, s_wtot);
-    const uint32_t tg = block_excl_scan(lg, rg, s_wtot);
-    for (int e = e0; e < e1; ++e) {
-        unit_off[e] = (int32_t)ru;
-        ru += (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, e);
+    __shared__ uint32_t s_carry[2];
+    const int tid = threadIdx.x, i = blockIdx.x * kBlock + tid;
+    uint32_t tu = 0, tg = 0;
+    const uint32_t cu = block_exclusive_scan(tid < nblk ? (uint32_t)blk_tot[tid] : 0u, s_wtot, &tu);
+    const uint32_t cg =
+        block_exclusive_scan(tid < nblk ? (uint32_t)blk_tot[kBlock + tid] : 0u, s_wtot, &tg);
+    if (tid == (int)blockIdx.x) {
+        s_carry[0] = cu;
+        s_carry[1] = cg;
     }
-    for (int c = c0; c < c1; ++c) {
-        grp_off[c] = (int32_t)rg;
-        rg += (uint32_t)groups_of_cluster(seg, c);
-    }
-    if (tid == 0) {
-        unit_off[E] = (int32_t)tu;
+    __syncthreads();
+    if (i < 2 * nlist) unit_off[i] += (int32_t)s_carry[0];
+    if (i < nlist) grp_off[i] += (int32_t)s_carry[1];
+    if (blockIdx.x == 0 && tid == 0) {
+        unit_off[2 * nlist] = (int32_t)tu;
         grp_off[nlist] = (int32_t)tg;
     }
 }
@@ -454,13 +447,14 @@ __device__ __forceinline__ double sum16_f64(double v) {
     return v;
 }
 
-// Waves [0, nlist): per-cluster bounds of the f32 slack, A_max = 255^2 sum delta^2 (>= A_x,
+// Waves [0, ncl): per-cluster bounds of the f32 slack (ncl = nlist, or 0 when the index
+// carries them), A_max = 255^2 sum delta^2 (>= A_x,
 // codes <= 255) and r_max = max(2 sqrt(sum eps^2), the largest stored r_x) (the first term
 // bounds r_x = |a| + |b| <= 2 |a + b| for the non-negative per-dim error terms when eps bounds
 // them; the second holds for any eps, e.g. an index built with the reference's 0.5001 delta),
 // and r_lo = the smallest stored r_x of the cluster.  Waves [nlist, nlist + B): per-query sum of qerr^2 (the rotation error of q_rot,
 // squared).
-__global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist, int B,
+__global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int ncl, int B,
                                                          double* cbound, double* qep,
                                                          int32_t* unit_ctr) {
     const int lane = threadIdx.x & 63;
@@ -468,9 +462,9 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
     const int D_pad = a.D_pad;
     // the per-launch state of both passes starts here (one launch instead of three fills):
     // work counters, tau = +inf (pass A takes atomicMin), empty survivor lists (pass B)
-    if (blockIdx.x == 0)
+    if (blockIdx.x == 0 && unit_ctr)
         for (int i = threadIdx.x; i < 2 * 8 * kCtrStride; i += blockDim.x) unit_ctr[i] = 0;
-    if (wv < nlist) {
+    if (wv < ncl) {
         const size_t off = a.per_cluster ? (size_t)wv * D_pad : 0;
         double dd = 0.0, ee = 0.0;
         for (int d = lane; d < D_pad; d += kWave) {
@@ -502,8 +496,8 @@ __global__ __launch_bounds__(256) void aux_bounds_kernel(BatchArgs a, int nlist,
             cbound[kCbStride * wv + 1] = fmax(2.0 * sqrt(ee), (double)rhi) * (1.0 + 1e-12);
             cbound[kCbStride * wv + 2] = rlo < INFINITY ? (double)rlo : 0.0;
         }
-    } else if (wv < nlist + B) {
-        const int q = wv - nlist;
+    } else if (wv < ncl + B) {
+        const int q = wv - ncl;
         const double* qe = a.qerr + (size_t)q * D_pad;
         double ep = 0.0;
         for (int d = lane; d < D_pad; d += kWave) ep = fma(qe[d], qe[d], ep);

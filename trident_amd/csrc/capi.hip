@@ -107,6 +107,7 @@ struct Workspace {
     int32_t* counts;
     int32_t* seg_off;
     int32_t* cursor;
+    int32_t* blk_tot;  // [2 * kBlock] block totals of the multi-block scans
     int32_t* pair_cids;
     int32_t* pair_qids;
     float* pair_dqcs;
@@ -172,6 +173,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.counts = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
     w.seg_off = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
     w.cursor = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
+    w.blk_tot = c.take<int32_t>(2 * kBlock);
     w.pair_cids = c.take<int32_t>(B * nprobe);
     w.pair_qids = c.take<int32_t>(B * nprobe);
     w.pair_dqcs = c.take<float>(B * nprobe);
@@ -617,13 +619,18 @@ int launch_scatter_pairs(const int32_t* probe_cids, const float* probe_dqcs, int
 int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int B, int nprobe,
                 int p_init, int nlist, int32_t* counts, int32_t* seg_off, int32_t* cursor,
                 int32_t* p1c, int32_t* p1q, float* p1d, int32_t* p2c, int32_t* p2q, float* p2d,
-                bool joint, hipStream_t st) {
+                bool joint, int32_t* blk_tot, hipStream_t st) {
     int rc = fill(counts, 0, 2 * ((int64_t)nlist + 1), st);
     if (rc) return rc;
     if ((rc = launch_count_pairs(probe_cids, ld, B, nprobe, p_init, nlist, counts, st))) return rc;
     if (joint) {
-        scan_pairs_joint_kernel<<<1, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
-        if ((rc = check_launch("scan_pairs_joint_kernel"))) return rc;
+        // nlist <= 19200 (validate_index), so the block totals fit one block's scan
+        const int nblk = (nlist + kBlock - 1) / kBlock;
+        scan_pairs_joint_local_kernel<<<nblk, kBlock, 0, st>>>(counts, nlist, seg_off, blk_tot);
+        if ((rc = check_launch("scan_pairs_joint_local_kernel"))) return rc;
+        scan_pairs_joint_carry_kernel<<<nblk, kBlock, 0, st>>>(counts, nlist, blk_tot, nblk,
+                                                               seg_off, cursor);
+        if ((rc = check_launch("scan_pairs_joint_carry_kernel"))) return rc;
     } else {
         scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
         if ((rc = check_launch("scan_pairs_kernel"))) return rc;
@@ -802,7 +809,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     int32_t *p2c = batched ? p1c : w.pair_cids + M1, *p2q = batched ? p1q : w.pair_qids + M1;
     float* p2d = batched ? p1d : w.pair_dqcs + M1;
     if ((rc = group_pairs(pc, pd, ld, B, nprobe, p_init, ix->nlist, w.counts, w.seg_off, w.cursor,
-                          p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, batched, st)))
+                          p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, batched, w.blk_tot,
+                          st)))
         return rc;
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
@@ -895,7 +903,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.pw = w.pw;
         b.prec = w.prec;
         b.lbr = w.lbr;
-        b.cbound = w.cbound;
+        // index-constant per-cluster bounds: the view's table when it has one
+        b.cbound = ix->cluster_bounds ? ix->cluster_bounds : w.cbound;
         b.qep = w.qep;
         b.ub_list = w.ub_list;
         b.ub_cnt = w.ub_cnt;
@@ -906,14 +915,22 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.groups = w.groups;
         b.grp_off = w.grp_off;
         b.max_groups = (int)w.max_groups;
-        aux_bounds_kernel<<<(unsigned)((ix->nlist + B + kWavesPerBlock - 1) / kWavesPerBlock),
-                            kBlock, 0, st>>>(b, ix->nlist, B, w.cbound, w.qep, w.unit_ctr);
+        const int ncl = ix->cluster_bounds ? 0 : ix->nlist;
+        aux_bounds_kernel<<<(unsigned)((ncl + B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock,
+                            0, st>>>(b, ncl, B, w.cbound, w.qep, w.unit_ctr);
         if ((rc = check_launch("aux_bounds_kernel"))) return rc;
         // TRIDENT_UB_SEED 2 seeds from every probe, 0 and 1 from the first p_init
         const int seed_all = sp->ub_seed == 2 ? 1 : 0;
-        unit_scan_kernel<<<1, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist,
-                                               b.unit_q, seed_all, w.unit_off, w.grp_off);
-        if ((rc = check_launch("unit_scan_kernel"))) return rc;
+        {
+            const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= 150 (nlist <= 19200)
+            unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
+                                                            ix->nlist, b.unit_q, seed_all,
+                                                            w.unit_off, w.grp_off, w.blk_tot);
+            if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
+            unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
+                                                            w.unit_off, w.grp_off);
+            if ((rc = check_launch("unit_scan_carry_kernel"))) return rc;
+        }
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, seed_all,
                                  w.unit_off, w.units, (int)w.max_units, w.grp_off, w.groups,
@@ -1131,6 +1148,24 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
     ScanArgs a = make_scan_args(ix, w, 1, 1, 0, nullptr);
     sq8_bounds_kernel<<<(n + 255) / 256, 256, 0, st>>>(a, qids, cids, spos, n, lb, ub);
     return check_launch("sq8_bounds_kernel");
+}
+
+int trident_cluster_bounds(const TridentIndexView* ix, double* cluster_bounds, void* stream) {
+    int rc = validate_index(ix);
+    if (rc) return rc;
+    if (!ix->vec_Ar || !ix->delta || !ix->eps_dim || !cluster_bounds)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "cluster_bounds needs vec_Ar, delta, eps_dim");
+    BatchArgs b{};
+    b.D_pad = ix->D_pad;
+    b.per_cluster = ix->per_cluster_sq8;
+    b.delta = ix->delta;
+    b.eps = ix->eps_dim;
+    b.vec_off = ix->cluster_vec_off;
+    b.vec_Ar = reinterpret_cast<const float2*>(ix->vec_Ar);
+    aux_bounds_kernel<<<(unsigned)((ix->nlist + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
+                        static_cast<hipStream_t>(stream)>>>(b, ix->nlist, 0, cluster_bounds,
+                                                            nullptr, nullptr);
+    return check_launch("aux_bounds_kernel");
 }
 
 int trident_fine_bounds(const TridentIndexView* ix, const float* xq, int32_t B,

@@ -55,6 +55,31 @@ __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// Block-wide exclusive scan of one uint32 per thread (blocks of kBlock threads); *total (when
+// given) receives the block's sum.  Two barriers: s_wave_tot may be reused right after.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot,
+                                                         uint32_t* total) {
+    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    uint32_t inc = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
+        if (lane >= o) inc += t;
+    }
+    if (lane == kWave - 1) s_wave_tot[wid] = inc;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+        const uint32_t t = s_wave_tot[w];
+        if (w < wid) before += t;
+        all += t;
+    }
+    __syncthreads();
+    if (total) *total = all;
+    return before + inc - v;
+}
+
 // Orders this wave's LDS accesses around the call (producer/consumer inside one wave).
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -172,30 +172,6 @@ __global__ __launch_bounds__(256) void coarse_dist_kernel(const double* __restri
     }
 }
 
-// Block-wide exclusive scan of one uint32 per thread (256 threads).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* s_wave_tot,
-                                                         uint32_t* total) {
-    const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-    uint32_t inc = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        uint32_t t = (uint32_t)__shfl_up((int)inc, o, kWave);
-        if (lane >= o) inc += t;
-    }
-    if (lane == kWave - 1) s_wave_tot[wid] = inc;
-    __syncthreads();
-    uint32_t before = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < kWavesPerBlock; ++w) {
-        const uint32_t t = s_wave_tot[w];
-        if (w < wid) before += t;
-        all += t;
-    }
-    __syncthreads();
-    if (total) *total = all;
-    return before + inc - v;
-}
-
 // One block of 256 threads per query.  Radix-selects the exact nprobe-th smallest float64
 // key, takes every smaller key plus the smallest cids among the equal ones, then sorts the
 // selection by (d, cid).  Keys live in LDS (nlist * 8 bytes of dynamic LDS).  Results go to
@@ -398,28 +374,45 @@ __global__ __launch_bounds__(256) void scan_pairs_kernel(const int32_t* counts, 
     }
 }
 
-// grid 1, block 256: the cluster-major layout (each cluster's pass-1 pairs, then its pass-2
-// pairs) from counts [2, nlist + 1]: seg_off row 0 = cluster starts, row 1 = pass-2 starts; the
-// cursor rows are the same offsets, so the scatter kernels place pass p's pair of cluster c at
-// cursor[p][c]++ in one array.
-__global__ __launch_bounds__(256) void scan_pairs_joint_kernel(const int32_t* counts, int nlist,
-                                                               int32_t* seg_off, int32_t* cursor) {
+// The cluster-major layout (each cluster's pass-1 pairs, then its pass-2 pairs) from counts
+// [2, nlist + 1]: seg_off row 0 = cluster starts, row 1 = pass-2 starts; the cursor rows are the
+// same offsets, so the scatter kernels place pass p's pair of cluster c at cursor[p][c]++ in one
+// array.  Two launches over ceil(nlist / kBlock) blocks of one cluster per thread (coalesced):
+// the first scans each block's clusters and writes the in-block offsets and the block's total,
+// the second adds the totals of the blocks before it (at most kBlock blocks).
+__global__ __launch_bounds__(256) void scan_pairs_joint_local_kernel(const int32_t* counts,
+                                                                     int nlist, int32_t* seg_off,
+                                                                     int32_t* blk_tot) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
-    const int tid = threadIdx.x;
-    const int32_t *c1 = counts, *c2 = counts + (nlist + 1);
-    const int chunk = (nlist + kBlock - 1) / kBlock;
-    const int a0 = min(nlist, tid * chunk), a1 = min(nlist, a0 + chunk);
-    uint32_t local = 0;
-    for (int c = a0; c < a1; ++c) local += (uint32_t)(c1[c] + c2[c]);
+    const int c = blockIdx.x * kBlock + threadIdx.x;
+    const uint32_t n = c < nlist ? (uint32_t)(counts[c] + counts[nlist + 1 + c]) : 0u;
     uint32_t total = 0;
-    uint32_t run = block_exclusive_scan(local, s_wtot, &total);
-    for (int c = a0; c < a1; ++c) {
-        const uint32_t n1 = (uint32_t)c1[c];
-        seg_off[c] = cursor[c] = (int32_t)run;
-        seg_off[nlist + 1 + c] = cursor[nlist + 1 + c] = (int32_t)(run + n1);
-        run += n1 + (uint32_t)c2[c];
+    const uint32_t run = block_exclusive_scan(n, s_wtot, &total);
+    if (c < nlist) seg_off[c] = (int32_t)run;
+    if (threadIdx.x == 0) blk_tot[blockIdx.x] = (int32_t)total;
+}
+
+__global__ __launch_bounds__(256) void scan_pairs_joint_carry_kernel(const int32_t* counts,
+                                                                     int nlist,
+                                                                     const int32_t* blk_tot,
+                                                                     int nblk, int32_t* seg_off,
+                                                                     int32_t* cursor) {
+    __shared__ uint32_t s_wtot[kWavesPerBlock];
+    const int tid = threadIdx.x, c = blockIdx.x * kBlock + tid;
+    uint32_t total = 0;
+    const uint32_t t = tid < nblk ? (uint32_t)blk_tot[tid] : 0u;
+    // the exclusive prefix at thread blockIdx.x is this block's carry; broadcast it through LDS
+    __shared__ uint32_t s_carry;
+    const uint32_t before = block_exclusive_scan(t, s_wtot, &total);
+    if (tid == (int)blockIdx.x) s_carry = before;
+    __syncthreads();
+    if (c < nlist) {
+        const uint32_t base = (uint32_t)seg_off[c] + s_carry;
+        const uint32_t n1 = (uint32_t)counts[c];
+        seg_off[c] = cursor[c] = (int32_t)base;
+        seg_off[nlist + 1 + c] = cursor[nlist + 1 + c] = (int32_t)(base + n1);
     }
-    if (tid == 0) {
+    if (blockIdx.x == 0 && tid == 0) {
         seg_off[nlist] = cursor[nlist] = (int32_t)total;
         seg_off[2 * nlist + 1] = cursor[2 * nlist + 1] = (int32_t)total;
     }

@@ -200,11 +200,15 @@ __global__ void count_pairs_kernel(const int32_t* __restrict__ probe_cids, int l
 __global__ void scan_pairs_kernel(const int32_t* counts, int nlist, int32_t* seg_off,
                                   int32_t* cursor);
 
-// grid 1: the cluster-major layout of the batched route, each cluster's pass-1 pairs followed
-// by its pass-2 pairs: seg_off[c] = the cluster's first pair, seg_off[nlist + 1 + c] = its first
-// pass-2 pair (both rows end with M); cursor receives the two rows for the scatter.
-__global__ void scan_pairs_joint_kernel(const int32_t* counts, int nlist, int32_t* seg_off,
-                                        int32_t* cursor);
+// The cluster-major layout of the batched route, each cluster's pass-1 pairs followed by its
+// pass-2 pairs: seg_off[c] = the cluster's first pair, seg_off[nlist + 1 + c] = its first pass-2
+// pair (both rows end with M); cursor receives the two rows for the scatter.  Two launches of
+// nblk = ceil(nlist / kBlock) <= kBlock blocks: in-block offsets and block totals, then carries.
+__global__ void scan_pairs_joint_local_kernel(const int32_t* counts, int nlist, int32_t* seg_off,
+                                              int32_t* blk_tot);
+__global__ void scan_pairs_joint_carry_kernel(const int32_t* counts, int nlist,
+                                              const int32_t* blk_tot, int nblk, int32_t* seg_off,
+                                              int32_t* cursor);
 
 __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
                                      const float* __restrict__ probe_dqcs, int ld, int B,
@@ -336,8 +340,12 @@ inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
 
 // seed_all: the seeding units cover every pair of a cluster (TRIDENT_UB_SEED 2), not only its
 // pass-1 pairs.
-__global__ void unit_scan_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
-                                 int seed_all, int32_t* unit_off, int32_t* grp_off);
+// Two launches of ceil(2 nlist / kBlock) blocks; blk_tot holds 2 * kBlock block totals.
+__global__ void unit_scan_local_kernel(const int32_t* seg, const int32_t* vec_off, int nlist,
+                                       int uqB, int seed_all, int32_t* unit_off, int32_t* grp_off,
+                                       int32_t* blk_tot);
+__global__ void unit_scan_carry_kernel(int nlist, const int32_t* blk_tot, int nblk,
+                                       int32_t* unit_off, int32_t* grp_off);
 
 __global__ void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
                                  int seed_all, const int32_t* unit_off, int4* units, int max_units,
@@ -392,7 +400,9 @@ __global__ void refine_survivors_kernel(BatchArgs a, int B);
 template <int KS>
 __global__ void pair_prep_kernel(BatchArgs a);
 
-__global__ void aux_bounds_kernel(BatchArgs a, int nlist, int B, double* cbound, double* qep,
+// Waves [0, ncl) fill the per-cluster bounds, waves [ncl, ncl + B) the per-query state; block
+// 0 clears unit_ctr when given.
+__global__ void aux_bounds_kernel(BatchArgs a, int ncl, int B, double* cbound, double* qep,
                                   int32_t* unit_ctr);
 
 __global__ void sq8_bounds_kernel(ScanArgs a, const int32_t* __restrict__ qids,

@@ -145,7 +145,8 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
                     rot_sq_min, rot_sq_max, sq8_packed, tile_orig_ids, tile_r_minmax,
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
                     eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
-                    cent_band=None, r_vec_sorted=None, fine_codes=None, fine_qp=None) -> TridentIndexView:
+                    cent_band=None, r_vec_sorted=None, fine_codes=None, fine_qp=None,
+                    cluster_bounds=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -169,11 +170,22 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.r_vec_sorted = _ptr(r_vec_sorted)
     v.fine_codes = _ptr(fine_codes)
     v.fine_qp = _ptr(fine_qp)
+    v.cluster_bounds = _ptr(cluster_bounds)
     if cent_band is not None:
         rows, tiles, norms, nmax = cent_band
         v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
         v.cent_norm_max = float(nmax)
     return v
+
+
+def compute_cluster_bounds(view: TridentIndexView, device) -> torch.Tensor:
+    """The index-constant per-cluster table of the batched route ([nlist, 4] float64), filled by
+    trident_cluster_bounds on the current stream; pass it back as ``cluster_bounds``."""
+    out = torch.empty((int(view.nlist), 4), dtype=torch.float64, device=device)
+    st = torch.cuda.current_stream(device).cuda_stream
+    _lib.check(_lib.lib().trident_cluster_bounds(ctypes.byref(view), out.data_ptr(), st),
+               "trident_cluster_bounds")
+    return out
 
 
 def band_dq(D: int) -> int:
@@ -325,6 +337,7 @@ def launch_trident_v4_search(
     cent_band=None,
     fine_codes: Optional[torch.Tensor] = None, fine_qp: Optional[torch.Tensor] = None,
     host_rows: Optional[torch.Tensor] = None,
+    cluster_bounds: Optional[torch.Tensor] = None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -382,6 +395,10 @@ def launch_trident_v4_search(
         _need(tuple(fine_codes.shape) == (N, D_pad), "fine_codes must be [N, D_pad] int16 (uint16 bits)")
         _check_tensor("fine_qp", fine_qp, torch.float32, dev, 2)
         _need(tuple(fine_qp.shape) == (N, 4), "fine_qp must be [N, 4] float32")
+    if cluster_bounds is not None:
+        _need(vec_Ar is not None, "cluster_bounds is derived from vec_Ar: pass both")
+        _check_tensor("cluster_bounds", cluster_bounds, torch.float64, dev, 2)
+        _need(tuple(cluster_bounds.shape) == (nlist, 4), "cluster_bounds must be [nlist, 4] float64")
     if vec_Ar is not None:
         _check_tensor("vec_Ar", vec_Ar, torch.float32, dev, 2)
         _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float32")
@@ -444,7 +461,8 @@ def launch_trident_v4_search(
         delta=delta if sq8 else None, eps_dim=eps_dim if sq8 else None,
         blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
         sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted,
-        fine_codes=fine_codes if mode == 2 else None, fine_qp=fine_qp if mode == 2 else None)
+        fine_codes=fine_codes if mode == 2 else None, fine_qp=fine_qp if mode == 2 else None,
+        cluster_bounds=cluster_bounds if mode == 2 else None)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route,

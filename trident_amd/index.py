@@ -457,6 +457,7 @@ class TridentV4Index:
 
         # ---- search buffers (reference :257-278, K explicit) ----
         self.max_batch, self.max_nprobe = int(max_batch), int(max_nprobe)
+        self._fill_cluster_bounds()
         self._alloc_buffers()
         self.build_time_s = time.perf_counter() - t_start
 
@@ -525,7 +526,7 @@ class TridentV4Index:
             p_init=p_init,
             vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band,
             r_vec_sorted=self.r_vec_sorted, fine_codes=self.fine_codes, fine_qp=self.fine_qp,
-            host_rows=host_rows_buf)
+            host_rows=host_rows_buf, cluster_bounds=self.cluster_bounds)
         return topk_d, topk_i, kern_ms
 
     def view(self):
@@ -541,7 +542,14 @@ class TridentV4Index:
             xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
             delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
             sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted,
-            fine_codes=self.fine_codes, fine_qp=self.fine_qp)
+            fine_codes=self.fine_codes, fine_qp=self.fine_qp,
+            cluster_bounds=getattr(self, "cluster_bounds", None))
+
+    def _fill_cluster_bounds(self):
+        """The batched route's per-cluster constants (A_max, r_max, r_lo), once per index."""
+        self.cluster_bounds = None
+        if self.dev.type == "cuda":
+            self.cluster_bounds = _ext.compute_cluster_bounds(self.view(), self.dev)
 
     def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
         """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a mode-2 search of B queries takes."""

@@ -183,6 +183,7 @@ def load_index(path: str, device="cuda:0", xb_placement: str = "device", xb_raw=
     ix.fine_codes = _to_device(bins["fine_codes"], dev) if "fine_codes" in bins else None
     ix.fine_qp = _to_device(bins["fine_qp"], dev) if "fine_qp" in bins else None
     ix.max_batch, ix.max_nprobe = int(max_batch), int(max_nprobe)
+    ix._fill_cluster_bounds()
     ix._alloc_buffers()
     if dev.type == "cuda":
         torch.cuda.synchronize(dev)
