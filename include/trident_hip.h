@@ -110,11 +110,15 @@ typedef struct TridentIndexView {
     const double* cluster_bounds;
 } TridentIndexView;
 
-/* How mode 2 is executed.  Both are exact; they differ in speed only. */
+/* How modes 2 and 10 are executed.  Both routes are exact; they differ in speed only.  Mode 10
+ * batched is the float32 matrix-core cluster-major scan: it needs the base in device memory,
+ * K <= 16 and D_pad <= 256 (AUTO takes it from 4 queries per probed cluster on average). */
 enum TridentRoute {
     TRIDENT_ROUTE_AUTO = 0,     /* batched when clusters are shared by enough queries */
-    TRIDENT_ROUTE_PAIR = 1,     /* one workgroup per (cluster, query): Stage X / Y / Z per pair */
-    TRIDENT_ROUTE_BATCHED = 2   /* one workgroup per (cluster, query block): int8 matrix-core bound */
+    TRIDENT_ROUTE_PAIR = 1,     /* one workgroup per (cluster, query): Stage X / Y / Z per pair
+                                   (mode 10: the float64 scan of every row) */
+    TRIDENT_ROUTE_BATCHED = 2   /* one workgroup per (cluster, query block): int8 matrix-core bound
+                                   (mode 10: float32 matrix-core distances with an error band) */
 };
 
 typedef struct TridentSearchParams {
@@ -125,7 +129,7 @@ typedef struct TridentSearchParams {
     int32_t ub_seed; /* TRIDENT_UB_SEED semantics: 0 off, 1 pass 1, 2 both passes */
     int32_t use_l1;  /* residual-norm tile band (needs tile_r_minmax) */
     int32_t p_init;  /* pass-1 probes per query; -1 = reference rule */
-    int32_t route;   /* TridentRoute (mode 2 only) */
+    int32_t route;   /* TridentRoute (modes 2 and 10) */
     int32_t rerank_m; /* mode 0: candidates reranked exactly, M = min(max(rerank_m, K), 200);
                          0 = no rerank.  Ignored by the other modes */
 } TridentSearchParams;

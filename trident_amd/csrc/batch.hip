@@ -189,12 +189,6 @@ __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int
         p[i] = v;
 }
 
-__device__ __forceinline__ double shfl_f64(double v, int src) {
-    const uint64_t k = (uint64_t)__double_as_longlong(v);
-    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)k, src, kWave);
-    const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(k >> 32), src, kWave);
-    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
-}
 
 // Fine-level bounds of sorted row pos for a query whose float64 rotated row is q64 (D_pad
 // values) and whose rotation error has norm <= qe: lb <= d64(x, q) <= ub.  The row's fine codes

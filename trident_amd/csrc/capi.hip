@@ -381,6 +381,72 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
     }
 }
 
+// Mode 10: the matrix-core cluster-major scan (cm_scan_kernel) or the per-pair float64 scan.
+// The matrix-core route reads every probed row from the base, so it needs the base in HBM; it
+// keeps per-query thresholds from 16-vector tiles, so K <= 16; its query rows live in registers,
+// so D_pad <= 256.  AUTO takes it when clusters are shared by at least 4 queries on average
+// (16-row tiles with fewer rows leave most of each matrix instruction idle).
+int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
+                    int nprobe, bool xb_host, bool* cm) {
+    const bool ok = ix->orig_ids_sorted && !xb_host && K <= 16 && ix->D_pad <= 256 &&
+                    ix->N < (1 << 27) &&
+                    max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
+    switch (sp->route) {
+        case TRIDENT_ROUTE_PAIR:
+            *cm = false;
+            return TRIDENT_OK;
+        case TRIDENT_ROUTE_BATCHED:
+            if (!ok)
+                return fail(TRIDENT_ERR_UNSUPPORTED,
+                            "mode 10 batched route needs orig_ids_sorted, the base in device "
+                            "memory, K <= 16, D_pad <= 256 and N < 2^27 (K=%d, D_pad=%d, N=%d)",
+                            K, ix->D_pad, ix->N);
+            *cm = true;
+            return TRIDENT_OK;
+        case TRIDENT_ROUTE_AUTO:
+            *cm = ok && (double)B * nprobe >= 4.0 * ix->nlist;
+            return TRIDENT_OK;
+        default:
+            return fail(TRIDENT_ERR_INVALID_ARGUMENT, "route=%d outside {0,1,2}", sp->route);
+    }
+}
+
+template <int D4>
+const void* cm_kernel_ptr() {
+    return reinterpret_cast<const void*>(&cm_scan_kernel<D4>);
+}
+
+// Resident grid of cm_scan_kernel<D4> (CUs x occupancy), cached per device and variant.
+template <int D4>
+unsigned cm_grid() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!cached[dev]) {
+        int cu = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cu < 1)
+            cu = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, cm_kernel_ptr<D4>(), kBlock, 0) !=
+                hipSuccess ||
+            per_cu < 1)
+            per_cu = 2;
+        cached[dev] = std::max(8, cu * per_cu);
+    }
+    return (unsigned)cached[dev];
+}
+
+template <int D4 = 8>
+int launch_cm(const BatchArgs& b, hipStream_t st) {
+    if constexpr (D4 > 64) {
+        return fail(TRIDENT_ERR_UNSUPPORTED, "mode 10 batched route needs D_pad <= 256");
+    } else {
+        if (b.D_pad != 4 * D4) return launch_cm<D4 + 8>(b, st);
+        cm_scan_kernel<D4><<<cm_grid<D4>(), kBlock, 0, st>>>(b);
+        return check_launch("cm_scan_kernel");
+    }
+}
+
 // Seeding pass: ub_scan_kernel<KS, M> (M = per-lane list length, 4 when K <= 16);
 // lower-bound pass: lb_scan_kernel<KS> (D_pad <= 256) or lb_scan_wide_kernel<KS>.
 template <bool UB, int KS, int M>
@@ -798,9 +864,23 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         return rc;
     if ((rc = mark(TRIDENT_EV_PROBED))) return rc;
 
+    // where the base lives: mapped host memory (out of core) changes the refine and, with
+    // residual codes, the seeding; the PCIe telemetry counts rows read from there
+    bool xb_host = false;
+    {
+        hipPointerAttribute_t pa;
+        xb_host = hipPointerGetAttributes(&pa, ix->xb_sorted) == hipSuccess &&
+                  pa.type == hipMemoryTypeHost;
+        (void)hipGetLastError();  // an unregistered pointer is not an error here
+    }
     int route = TRIDENT_ROUTE_PAIR;
     if (cascade && (rc = choose_route(ix, sp, B, K, nprobe, &route))) return rc;
-    const bool batched = route == TRIDENT_ROUTE_BATCHED;
+    bool cm = false;
+    if (mode == TRIDENT_MODE_CM_EXACT &&
+        (rc = choose_cm_route(ix, sp, B, K, nprobe, xb_host, &cm)))
+        return rc;
+    // both batched routes group the pairs cluster-major in one array
+    const bool batched = route == TRIDENT_ROUTE_BATCHED || cm;
     const int64_t M1 = (int64_t)B * p_init, M2 = (int64_t)B * (nprobe - p_init);
     // per-pair route: the two passes' pairs in consecutive arrays; batched: one cluster-major
     // array (group_pairs)
@@ -819,15 +899,6 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if (out->stats) {
         if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
         if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
-    }
-    // where the base lives: mapped host memory (out of core) changes the refine and, with
-    // residual codes, the seeding; the PCIe telemetry counts rows read from there
-    bool xb_host = false;
-    {
-        hipPointerAttribute_t pa;
-        xb_host = hipPointerGetAttributes(&pa, ix->xb_sorted) == hipSuccess &&
-                  pa.type == hipMemoryTypeHost;
-        (void)hipGetLastError();  // an unregistered pointer is not an error here
     }
     unsigned long long* host_rows =
         out->host_rows && xb_host ? reinterpret_cast<unsigned long long*>(out->host_rows) : nullptr;
@@ -848,6 +919,94 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     m.list_key = w.list_key;
     m.list_id = w.list_id;
     m.tau64 = w.tau64;
+
+    if (cm) {
+        // mode 10 on the matrix cores: one pass over every probe; the listed rows carry (lb, ub)
+        // keys, tau = the K-th smallest listed ub, and the refine reads rows with lb <= tau only
+        BatchArgs b{};
+        b.vec_off = ix->cluster_vec_off;
+        b.xb = ix->xb_sorted;
+        b.orig_ids = ix->orig_ids_sorted;
+        b.D = ix->D;
+        b.D_pad = ix->D_pad;
+        b.xq = xq;
+        b.qerr = w.qerr;
+        b.tau = w.tau64;
+        b.B = B;
+        b.host_rows = host_rows;
+        b.cand_key = w.cand_key;
+        b.cand_id = w.cand_id;
+        b.cand_cnt = w.cand_cnt;
+        b.cap = (int)cap;
+        b.K = K;
+        b.stats = out->stats ? w.stat_slots : nullptr;
+        b.units = w.units;
+        b.unit_off = w.unit_off;
+        b.max_units = (int)w.max_units;
+        b.pair_qid = w.pair_qids;
+        b.pair_cid = w.pair_cids;
+        b.seg = w.seg_off;
+        b.M = (int)(M1 + M2);
+        b.nlist = ix->nlist;
+        b.unit_q = kUnitQWide;
+        b.ub_cnt = w.ub_cnt;
+        b.ub_best = w.ub_best;
+        b.seed_cnt = w.seed_cnt;
+        b.qep = w.qep;
+        b.fine_mode = 1;  // the candidate keys hold (lb, ub): the refine skips lb > tau
+        // per-query state (tau, counts, thresholds) and the work counters
+        aux_bounds_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
+                            st>>>(b, 0, B, w.cbound, w.qep, w.unit_ctr);
+        if ((rc = check_launch("aux_bounds_kernel"))) return rc;
+        {
+            const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;
+            unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
+                                                            ix->nlist, b.unit_q, 0, w.unit_off,
+                                                            w.grp_off, w.blk_tot);
+            if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
+            unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
+                                                            w.unit_off, w.grp_off);
+            if ((rc = check_launch("unit_scan_carry_kernel"))) return rc;
+        }
+        unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
+                           st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, 0,
+                                 w.unit_off, w.units, (int)w.max_units, w.grp_off, w.groups,
+                                 (int)w.max_groups);
+        if ((rc = check_launch("unit_fill_kernel"))) return rc;
+        if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
+        if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
+        b.unit_beg = ix->nlist;
+        b.unit_end = 2 * ix->nlist;
+        b.ctr = w.unit_ctr;
+        if ((rc = launch_cm(b, st))) return rc;
+        if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
+        const unsigned qg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
+        fine_tau_kernel<64><<<qg, kBlock, 0, st>>>(b, B);
+        if ((rc = check_launch("fine_tau_kernel"))) return rc;
+        const dim3 rgrid(qg, (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
+        refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+        if ((rc = check_launch("refine_survivors_kernel"))) return rc;
+        m.use_prev = 0;
+        m.tau_sq_out = out->tau_sq;
+        m.out_d = out->topk_d;
+        m.out_i = out->topk_i;
+        m.probe_cids = w.probe_cids;
+        m.nprobe = nprobe;
+        m.vec_off = ix->cluster_vec_off;
+        m.xb = ix->xb_sorted;
+        m.xq64 = w.xq64;
+        m.tile_oids = ix->tile_orig_ids;
+        m.tile_off = ix->cluster_tile_off;
+        m.T = ix->tile_size;
+        m.D = ix->D;
+        if ((rc = launch_merge(m, KP, st))) return rc;
+        if ((rc = mark(TRIDENT_EV_END))) return rc;
+        if (out->stats) {
+            stats_fold_kernel<<<1, 64, 0, st>>>(w.stat_slots, out->stats);
+            if ((rc = check_launch("stats_fold_kernel"))) return rc;
+        }
+        return TRIDENT_OK;
+    }
 
     if (batched) {
         BatchArgs b{};

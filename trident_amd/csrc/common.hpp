@@ -49,6 +49,14 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
     return ((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
+// Lane src's value of v (ds_bpermute twice).
+__device__ __forceinline__ double shfl_f64(double v, int src) {
+    const uint64_t k = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)k, src, kWave);
+    const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(k >> 32), src, kWave);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
     uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
     uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), l);

@@ -397,6 +397,13 @@ __global__ void lb_scan_wide_kernel(BatchArgs a);  // 4 < KS <= 16
 template <bool HOST, int DQ>
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
 
+// Mode 10 on the float32 matrix cores (D_pad = 4 D4 <= 256, K <= 16): the lower-bound units of
+// one launch (unit_beg / unit_end), each listing (lb, ub) keys of the rows that can still enter
+// the top-K; a.ctr[0] is the work counter (zero at launch), a.ub_best the per-query thresholds
+// (+inf at launch).
+template <int D4>
+__global__ void cm_scan_kernel(BatchArgs a);
+
 template <int KS>
 __global__ void pair_prep_kernel(BatchArgs a);
 
