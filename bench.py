@@ -377,13 +377,18 @@ def measure(cfg_id, cfg, args, dev, primary=True):
         out["sweep"] = sweep
     if primary and args.calibrate_w0:
         from trident_amd import router
-        W0, rows = router.calibrate_w0(ix, w.xq, nprobe, batches=(1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024),
+        W0, rows = router.calibrate_w0(ix, w.xq, nprobe,
+                                       batches=(1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048,
+                                                4096, 8192, B),
                                        warmup=3, iters=10, ub_seed=ub)
         for r_ in rows:
+            mx = r_["ms_cm_matrix"]
             log(f"W0 sweep B={r_['batch']:5d} W={r_['work']:.3e} cm={r_['ms_cm']:.3f}ms "
+                f"(pair {r_['ms_cm_pair']:.3f}, matrix {'-' if mx is None else f'{mx:.3f}'}) "
                 f"cascade={r_['ms_cascade']:.3f}ms -> {'cascade' if r_['cascade_faster'] else 'cm'}")
-        out["w0_calibration"] = {"W0": W0, "rows": rows}
-        log(f"calibrated W0 = {W0:.3e}")
+        W0s = router.stable_crossover(rows)
+        out["w0_calibration"] = {"W0": W0, "W0_stable": W0s, "rows": rows}
+        log(f"calibrated W0 = {W0:.3e} (reference rule), stable crossover = {W0s:.3e}")
     w.free()
     return out
 

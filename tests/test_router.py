@@ -55,3 +55,11 @@ def test_eval_accuracy_v4_semantics():
     assert measure_latency_qps(lambda: calls.append(1), warmup=2, iters=3) >= 0 and len(calls) == 5
     q, s = measure_runs(lambda: None, warmup=1, iters=3, b_size=10)
     assert q > 0 and s >= 0
+
+
+def test_stable_crossover_ignores_an_isolated_win():
+    rows = [{"work": w, "cascade_faster": f} for w, f in
+            ((1e6, True), (2e6, False), (4e6, False), (8e6, True), (1.6e7, True))]
+    assert router.stable_crossover(rows) == 8e6     # the reference rule would give 1e6
+    assert router.stable_crossover(rows[:3]) == float("inf")
+    assert router.stable_crossover([{"work": 5.0, "cascade_faster": True}]) == 5.0

@@ -881,6 +881,10 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         return rc;
     // both batched routes group the pairs cluster-major in one array
     const bool batched = route == TRIDENT_ROUTE_BATCHED || cm;
+    // the matrix-core mode 10 first scans each query's nearest probe (p_init of them when the
+    // caller sets it) for thresholds only, so that its other probes, scanned together, start
+    // from a threshold instead of +inf
+    if (cm) p_init = sp->p_init >= 0 ? std::min(sp->p_init, nprobe) : (nprobe > 1 ? 1 : 0);
     const int64_t M1 = (int64_t)B * p_init, M2 = (int64_t)B * (nprobe - p_init);
     // per-pair route: the two passes' pairs in consecutive arrays; batched: one cluster-major
     // array (group_pairs)
@@ -973,11 +977,20 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                                  w.unit_off, w.units, (int)w.max_units, w.grp_off, w.groups,
                                  (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
+        if (M1 > 0) {  // warm-up: thresholds from the first probes, nothing listed
+            b.cm_emit = 0;
+            b.unit_beg = 0;
+            b.unit_end = ix->nlist;
+            b.ctr = w.unit_ctr;
+            if ((rc = launch_cm(b, st))) return rc;
+        }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
+        // every probe (the first ones again: the warm-up listed nothing)
+        b.cm_emit = 1;
         b.unit_beg = ix->nlist;
         b.unit_end = 2 * ix->nlist;
-        b.ctr = w.unit_ctr;
+        b.ctr = w.unit_ctr + 8 * kCtrStride;
         if ((rc = launch_cm(b, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
         const unsigned qg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);

@@ -25,10 +25,12 @@
 // (S + E)), so lb = max(base - E, 0) <= d64 <= base + E = ub.
 //
 // Threshold.  Per query, ub_best holds a float32 value t such that at least K distinct probed
-// rows have ub <= t (so the K-th smallest d64 is <= t).  Each wave, per block, takes for each of
-// its query rows the smallest ub of every column lane (distinct vectors) and, when at least K of
-// those 16 are below the query's current t, lowers t to their K-th smallest (atomicMin on the
-// float bits, which order like the values for non-negative floats).  A row is listed iff its lb
+// rows have ub <= t (so the K-th smallest d64 is <= t).  Each lane keeps, for each of its query
+// rows, the smallest ub of its column over the unit so far (column j of every tile: distinct
+// vectors); when at least K of a row's 16 column minima are below the query's current t, t drops
+// to their K-th smallest (atomicMin on the float bits, which order like the values for
+// non-negative floats).  After such a drop only K - 1 minima are below t, so the selection runs
+// again only when another column's minimum falls below t.  A row is listed iff its lb
 // is <= the query's t at that moment; every row of the exact top-K (ties included) qualifies,
 // because lb <= d64 <= the K-th smallest d64 <= t.  The listed (lb, ub) keys then give tau = the
 // K-th smallest listed ub (fine_tau_kernel), and the refine computes the canonical distance of
@@ -108,9 +110,13 @@ __global__ __launch_bounds__(256) void cm_scan_kernel(BatchArgs a) {
         const int nq = active ? min(kCmQW, cnt - gq * kCmQW) : 0;
 
         // ---- this wave's queries: A operands (row j, dims g D4 .. g D4 + D4 - 1) and norms ----
+        // (initialised on every path: nothing is carried from the previous unit)
         float qa[D4];
-        int rq[4];
-        float t_row[4], nq_r[4], qn_r[4];
+#pragma unroll
+        for (int k = 0; k < D4; ++k) qa[k] = 0.0f;
+        int rq[4] = {-1, -1, -1, -1};
+        float t_row[4] = {-1.0f, -1.0f, -1.0f, -1.0f}, nq_r[4] = {}, qn_r[4] = {};
+        float cmin[4] = {INFINITY, INFINITY, INFINITY, INFINITY};  // column minima of ub
         if (active) {
             const bool qv = j < nq;
             const int qid = qv ? a.pair_qid[start + gq * kCmQW + j] : 0;
@@ -151,15 +157,27 @@ __global__ __launch_bounds__(256) void cm_scan_kernel(BatchArgs a) {
             const int nvb = min(kCmBV, ve - blk0);
             // ---- stage the block's rows (columns [0, D)), zero rows past the slice ----
             {
+                // chunk i = tid + kBlock k < 64 ceil(D / 4) <= 64 D4, in two halves whose loads
+                // are all issued before their LDS stores (two memory round trips per block)
                 const int n4 = (D + 3) >> 2;
-                for (int i = tid; i < kCmBV * n4; i += kBlock) {
-                    const int r = i / n4, c = i - r * n4;
-                    const int left = r < nvb ? D - 4 * c : 0;
-                    const float4 v =
-                        load_upto4(a.xb + (size_t)(v0 + blk0 + min(r, nvb - 1)) * D + 4 * c,
-                                   min(left, 4), xvec);
-                    // 4 c + 4 <= D_pad (a multiple of 4): the chunk's columns past D get zeros
-                    *reinterpret_cast<float4*>(s_x + r * RS + 4 * c) = v;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    float4 v[D4 / 8];
+#pragma unroll
+                    for (int k = 0; k < D4 / 8; ++k) {
+                        const int i = tid + kBlock * (h * (D4 / 8) + k);
+                        const int r = i / n4, c = i - r * n4;
+                        const int left = i < kCmBV * n4 && r < nvb ? D - 4 * c : 0;
+                        v[k] = load_upto4(a.xb + (size_t)(v0 + blk0 + min(r, nvb - 1)) * D + 4 * c,
+                                          min(left, 4), xvec);
+                    }
+#pragma unroll
+                    for (int k = 0; k < D4 / 8; ++k) {
+                        const int i = tid + kBlock * (h * (D4 / 8) + k);
+                        const int r = i / n4, c = i - r * n4;
+                        // 4 c + 4 <= D_pad (a multiple of 4): columns past D get zeros
+                        if (i < kCmBV * n4) *reinterpret_cast<float4*>(s_x + r * RS + 4 * c) = v[k];
+                    }
                 }
             }
             __syncthreads();
@@ -179,9 +197,14 @@ __global__ __launch_bounds__(256) void cm_scan_kernel(BatchArgs a) {
             }
             __syncthreads();
             if (active) {
+                // other units may have lowered the thresholds (four loads in flight, rows
+                // without a query read query 0 and keep t = -1)
+                uint32_t tb[4];
 #pragma unroll
-                for (int r = 0; r < 4; ++r)  // other units may have lowered the thresholds
-                    if (rq[r] >= 0) t_row[r] = fminf(t_row[r], __uint_as_float(a.ub_best[rq[r]]));
+                for (int r = 0; r < 4; ++r) tb[r] = a.ub_best[max(rq[r], 0)];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (rq[r] >= 0) t_row[r] = fminf(t_row[r], __uint_as_float(tb[r]));
                 // ---- the wave's tiles: rr, rr + R, ... (16 vectors each), one at a time ----
 #pragma unroll 1
                 for (int tl = rr; tl < kCmBV / 16 && 16 * tl < nvb; tl += R) {
@@ -225,15 +248,16 @@ __global__ __launch_bounds__(256) void cm_scan_kernel(BatchArgs a) {
                         }
                         lbf[r] = vv ? lb : INFINITY;
                         ubf[r] = vv ? ub : INFINITY;
+                        cmin[r] = fminf(cmin[r], ubf[r]);
                     }
-                    // ---- thresholds: the K-th smallest ub of the tile's 16 vectors, per query
-                    // row, when at least K of them are below the query's t ----
+                    // ---- thresholds: the K-th smallest column minimum per query row, when at
+                    // least K of the row's 16 are below the query's t ----
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const uint64_t bm = __ballot(ubf[r] < t_row[r]);
+                        const uint64_t bm = __ballot(cmin[r] < t_row[r]);
                         const int cg = __popcll((bm >> (16 * g)) & 0xffffull);
                         if (__ballot(cg >= K) == 0ull) continue;
-                        const float my = ubf[r];
+                        const float my = cmin[r];
                         int rank = 0;
 #pragma unroll 1
                         for (int o = 1; o < 16; ++o) {  // rare: kept rolled (no hoisted lane maps)
@@ -248,9 +272,11 @@ __global__ __launch_bounds__(256) void cm_scan_kernel(BatchArgs a) {
                             if (j == 0) atomicMin(&a.ub_best[rq[r]], __float_as_uint(kth));
                         }
                     }
-                    // ---- list the rows with lb <= t: one atomic per (row, lane group) ----
+                    // ---- list the rows with lb <= t: one atomic per (row, lane group); the
+                    // warm-up pass (cm_emit = 0) only sets thresholds ----
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (!a.cm_emit) break;
                         // vv explicitly: a query without a threshold yet has t = +inf, and
                         // the +inf keys of columns past the slice would compare <= it
                         const bool ps = vv && lbf[r] <= t_row[r];

@@ -297,38 +297,11 @@ __device__ __forceinline__ bool list_offer(WaveList<KP>& L, int K, uint64_t ck, 
 
 constexpr int kStageCh = 32;  // dims per Stage Z staging chunk
 
-// Canonical float64 distance of the first `nq` queued survivors (lane i <- survivor i).
-// Rows are staged through LDS 32 dims at a time with 128-byte coalesced row loads.
+// Canonical float64 distance of the first `nq` (>= 1) queued survivors (lane i <- survivor i),
+// in dimension order: rows are staged through LDS 32 dims at a time with 128-byte coalesced row
+// loads, every load of a chunk (64 rows, two per load) issued before the chunk is staged, so a
+// chunk costs one memory round trip (HBM, or PCIe for a base in mapped host memory).
 __device__ __forceinline__ double refine_rows(const float* __restrict__ xb, int D,
-                                              const int32_t* q_spos, int nq,
-                                              float (*stage)[kWave + 1], const double* s_q64) {
-    const int lane = lane_id();
-    double acc = 0.0;
-    const int half = lane >> 5, kk = lane & 31;
-    for (int d0 = 0; d0 < D; d0 += kStageCh) {
-        const int ch = min(kStageCh, D - d0);
-        for (int r0 = 0; r0 < nq; r0 += 2) {
-            const int r = r0 + half;
-            float v = 0.0f;
-            if (r < nq && kk < ch) v = xb[(size_t)q_spos[r] * D + d0 + kk];
-            if (r < nq) stage[kk][r] = v;
-        }
-        wave_sync();
-        if (lane < nq) {
-            for (int k = 0; k < ch; ++k) {
-                const double t = (double)stage[k][lane] - s_q64[d0 + k];
-                acc = fma(t, t, acc);
-            }
-        }
-        wave_sync();
-    }
-    return acc;
-}
-
-// As refine_rows, with every load of a 32-dim chunk (64 rows, two per 128-byte load) issued
-// before the chunk is staged: one memory round trip per chunk.  For bases in mapped host memory,
-// where each round trip crosses PCIe.  nq >= 1.
-__device__ __forceinline__ double refine_rows_mlp(const float* __restrict__ xb, int D,
                                                   const int32_t* q_spos, int nq,
                                                   float (*stage)[kWave + 1],
                                                   const double* s_q64) {

@@ -162,6 +162,7 @@ struct BatchArgs {
     const uint16_t* fine_codes; // [N, D_pad] or null
     const float* fine_qp;       // [N, 4] (offset, step, rho, 0)
     int fine_mode;              // 1: seeds bounded and survivors filtered with the fine level
+    int cm_emit;                // cm_scan_kernel: 1 lists rows, 0 only lowers the thresholds
     unsigned long long* host_rows;  // [1] rows read from the host-mapped base, or null
 };
 

@@ -4,13 +4,16 @@ Reference: benchmarks/phase4a_suite.py:1063-1079 (per-batch choice) and :999-103
 (calibration).  The work measure is W = B * nprobe * (N / nlist) * D; the route is mode 10
 when W < W0, else mode 2.  The calibration sweeps batch sizes, times both routes with the
 reference's methodology (warmup, back-to-back calls, one synchronise) and sets W0 to the
-smallest work at which the cascade is at least as fast.
+smallest work at which the cascade is at least as fast (the reference's rule);
+``stable_crossover`` gives the smallest work from which the cascade wins at every larger
+measured work, which ignores an isolated win at a tiny batch.
 
 W0 is hardware-specific.  The reference's A100 value is 946,811,200 (README rounds it to
-9.0e8).  On MI355X the cascade is faster than the exact scan at every batch size measured,
-B = 1 included (cfg 1: 0.128 vs 0.405 ms at B = 1, nprobe 16; cfg 4: 0.280 vs 1.486 ms at
-B = 1, nprobe 64), so the calibrated crossover is the smallest work timed:
-W(B=1, cfg 1) = 8.0e5.  Any batch at or above it takes the cascade.
+9.0e8).  On MI355X (calibrate_w0, bench.py --calibrate-w0) mode 10 is the faster route up to
+B = 64 and the cascade from B = 128, where the cascade's int8 matrix-core batched route takes
+over: configs[0] (N 1e5, nprobe 16) crosses at W = 1.02e8, configs[1] (N 1e6, nprobe 64) at
+W = 1.02e9.  W0_MI355X is the smaller of the two, as the reference takes the smaller of its
+datasets' crossovers.
 """
 import time
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -18,8 +21,8 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import torch
 
 W0_REFERENCE_A100 = 946_811_200.0
-# Smallest measured work at which mode 2 beat mode 10 on MI355X (calibrate_w0 on cfg 1 and cfg 4).
-W0_MI355X = 8.0e5
+# Smallest stable crossover over the calibrated configs on MI355X (configs[0]: B = 128).
+W0_MI355X = 1.024e8
 
 MODE_CM_EXACT = 10
 MODE_CASCADE = 2
@@ -58,14 +61,35 @@ def calibrate_w0(index, xq_pool: torch.Tensor, nprobe: int,
             break
         q = xq_pool[:b].contiguous()
         w = work_measure(b, nprobe, N, nlist, D)
-        ms_cm = _time_ms(lambda: index.search(q, nprobe, mode=MODE_CM_EXACT), warmup, iters)
+        # mode 10 on each of its routes (1: float64 per pair, 2: float32 matrix cores), the
+        # faster of them standing for mode 10
+        ms_routes = {}
+        for rt in (1, 2):
+            try:
+                ms_routes[rt] = _time_ms(lambda: index.search(q, nprobe, mode=MODE_CM_EXACT, route=rt),
+                                         warmup, iters)
+            except RuntimeError:  # the matrix-core route does not apply (K, D or placement)
+                pass
+        ms_cm = min(ms_routes.values())
         ms_k2 = _time_ms(lambda: index.search(q, nprobe, mode=MODE_CASCADE, ub_seed=ub_seed), warmup, iters)
         rows.append({"batch": b, "nprobe": nprobe, "work": w, "ms_cm": ms_cm, "ms_cascade": ms_k2,
+                     "ms_cm_pair": ms_routes.get(1), "ms_cm_matrix": ms_routes.get(2),
                      "qps_cm": b * 1000.0 / ms_cm, "qps_cascade": b * 1000.0 / ms_k2,
                      "cascade_faster": ms_k2 <= ms_cm})
         if ms_k2 <= ms_cm:
             crossings.append(w)
     return (min(crossings) if crossings else float("inf")), rows
+
+
+def stable_crossover(rows: List[Dict]) -> float:
+    """Smallest work from which the cascade is at least as fast at every larger measured work
+    (+inf when mode 10 wins the largest)."""
+    w0 = float("inf")
+    for r in sorted(rows, key=lambda r: r["work"], reverse=True):
+        if not r["cascade_faster"]:
+            break
+        w0 = r["work"]
+    return w0
 
 
 class CostRouter:
