@@ -47,6 +47,7 @@ sys.path.insert(0, ROOT)
 METRIC = "QPS at 100% exact top-10, 1×MI355X; achieved HBM GB/s vs peak"  # BASELINE.json metric, verbatim
 HBM_PEAK_GBPS = 8000.0
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix throughput
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense float32 matrix throughput
 PROFILES = os.path.join(ROOT, "profiles")
 
 
@@ -245,9 +246,17 @@ def measure(cfg_id, cfg, args, dev, primary=True):
     if mode == 10:
         bytes_p2 = bytes_all = int(sizes[probes].sum()) * D * 4
     tot, dims, surv, ins = [int(v) for v in stats.tolist()]
-    route = ix.route_for(B, nprobe, K, args.route) if mode == 2 else _lib.ROUTE_PAIR
+    route = ix.route_for(B, nprobe, K, args.route, mode=mode)
     t_scan = stage["pass2_scan_ms"] * 1e-3
-    if route == _lib.ROUTE_BATCHED:
+    if route == _lib.ROUTE_BATCHED and mode == 10:
+        # float32 matrix cores: 2 D_pad flops per (query, probed row) of the listing pass
+        flops = 2.0 * int(sizes[probes].sum()) * ix.D_pad
+        achieved = flops / t_scan / 1e12
+        roof = {"bound": "mfma", "kernel": "cm_scan_kernel<D4> (mode 10, float32 matrix cores)",
+                "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "flops_alg_per_launch": flops}
+        prof_name = f"cm_scan_cfg{cfg_id}_traffic"
+    elif route == _lib.ROUTE_BATCHED:
         ops_alg = 4 * bytes_all
         achieved = ops_alg / t_scan / 1e12
         roof = {"bound": "mfma", "kernel": "lb_scan_kernel<KS> (lower-bound pass, int8 matrix cores)",

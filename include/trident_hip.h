@@ -216,6 +216,12 @@ int32_t trident_p_init_rule(int32_t mode, int32_t B, int32_t K, int32_t nprobe, 
 int32_t trident_route_for(const TridentIndexView* ix, int32_t B, int32_t K, int32_t nprobe,
                           int32_t requested_route);
 
+/* As trident_route_for for mode 2 or mode 10 (for mode 10 TRIDENT_ROUTE_BATCHED is the float32
+ * matrix-core scan, which also depends on where xb_sorted lives); other modes take the per-pair
+ * route.  No reference counterpart. */
+int32_t trident_route_for_mode(const TridentIndexView* ix, int32_t mode, int32_t B, int32_t K,
+                               int32_t nprobe, int32_t requested_route);
+
 /* Per-candidate SQ8 bounds exactly as Stage Y (lb) and Stage X (ub) evaluate them, scaled to
  * bound the canonical float64 distance: lb[i] <= d64(q, x) <= ub[i] for the n (query,
  * sorted-position) pairs.  cids/qids/spos are device arrays of length n. */

@@ -70,6 +70,7 @@ EXPORTS = {
     "trident_group_pairs": (ctypes.c_int, [_P, _i32, _i32, _i32, _i32, _i32, _P, _P, _P, _P, _P, _P, _P]),
     "trident_p_init_rule": (_i32, [_i32, _i32, _i32, _i32, _i32]),
     "trident_route_for": (_i32, [ctypes.POINTER(TridentIndexView), _i32, _i32, _i32, _i32]),
+    "trident_route_for_mode": (_i32, [ctypes.POINTER(TridentIndexView), _i32, _i32, _i32, _i32, _i32]),
     "trident_sq8_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _i32, _P, _P, _P, _i32,
                                           _P, ctypes.c_size_t, _P, _P, _P]),
     "trident_cluster_bounds": (ctypes.c_int, [ctypes.POINTER(TridentIndexView), _P, _P]),

@@ -738,6 +738,25 @@ int32_t trident_route_for(const TridentIndexView* ix, int32_t B, int32_t K, int3
     return rc ? -rc : route;
 }
 
+int32_t trident_route_for_mode(const TridentIndexView* ix, int32_t mode, int32_t B, int32_t K,
+                               int32_t nprobe, int32_t requested_route) {
+    if (!ix) return fail(TRIDENT_ERR_INVALID_ARGUMENT, "index view is NULL");
+    if (mode == TRIDENT_MODE_CASCADE) return trident_route_for(ix, B, K, nprobe, requested_route);
+    if (mode != TRIDENT_MODE_CM_EXACT) return TRIDENT_ROUTE_PAIR;
+    TridentSearchParams sp{};
+    sp.route = requested_route;
+    bool xb_host = false;
+    {
+        hipPointerAttribute_t pa;
+        xb_host = hipPointerGetAttributes(&pa, ix->xb_sorted) == hipSuccess &&
+                  pa.type == hipMemoryTypeHost;
+        (void)hipGetLastError();
+    }
+    bool cm = false;
+    const int rc = choose_cm_route(ix, &sp, B, K, nprobe, xb_host, &cm);
+    return rc ? -rc : (cm ? TRIDENT_ROUTE_BATCHED : TRIDENT_ROUTE_PAIR);
+}
+
 size_t trident_workspace_bytes(const TridentIndexView* ix, int32_t max_B, int32_t max_nprobe,
                                int32_t max_K) {
     if (!ix || max_B < 0 || max_nprobe < 1 || max_K < 1) return 0;

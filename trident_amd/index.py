@@ -551,10 +551,12 @@ class TridentV4Index:
         if self.dev.type == "cuda":
             self.cluster_bounds = _ext.compute_cluster_bounds(self.view(), self.dev)
 
-    def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0) -> int:
-        """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a mode-2 search of B queries takes."""
+    def route_for(self, B: int, nprobe: int, k: Optional[int] = None, route: int = 0, mode: int = 2) -> int:
+        """The route (_lib.ROUTE_PAIR / ROUTE_BATCHED) a search of B queries takes (mode 2, or
+        mode 10 whose batched route is the float32 matrix-core scan)."""
         view = self.view()
-        r = _lib.lib().trident_route_for(ctypes.byref(view), int(B), int(k or self.k), int(nprobe), int(route))
+        r = _lib.lib().trident_route_for_mode(ctypes.byref(view), int(mode), int(B), int(k or self.k),
+                                              int(nprobe), int(route))
         if r < 0:
             _lib.check(-r, "trident_route_for")
         return int(r)
