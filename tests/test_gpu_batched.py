@@ -94,8 +94,8 @@ def test_batched_host_mapped_base(dev):
 
 @pytest.mark.parametrize("K", [1, 10, 64])
 def test_batched_large_clusters_split_into_slices(dev, K):
-    """~5000 vectors per cluster: in the lower-bound pass every cluster is scanned as 5 vector
-    slices (units of <= 64 queries x ~1024 vectors), so survivors come from many slices."""
+    """~5000 vectors per cluster: in both passes every cluster is scanned as 3 vector slices
+    (units of <= 128 queries x ~2048 vectors), so survivors come from many slices."""
     xb, xq = datagen.cfg1(N=40_000, D=64, B=300, n_centers=8, seed=26)
     b = build_index(xb, 8, dev, max_batch=512)
     sizes = np.diff(b.vec_off)

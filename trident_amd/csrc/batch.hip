@@ -66,20 +66,21 @@ constexpr int kWaveQ = 16;   // queries per wave
 // Vector slices of a cluster (both passes), so that no unit runs far longer than the others.
 // The seeding pass loses nothing by slicing: every unit hands its K smallest bounds to the
 // query's list, and the threshold is the K-th smallest over all of them.
-__device__ __forceinline__ int splits_of(int n) {
+__device__ __forceinline__ int splits_of(int n, int sv) {
     if (n <= 0) return 0;
-    return min(kMaxSplit, (n + kSplitVec - 1) / kSplitVec);
+    return min(kMaxSplit, (n + sv - 1) / sv);
 }
 
 // Entry e < nlist: the seeding units of cluster e (its pass-1 queries, or all of them when
 // seed_all, <= 16 per unit); entry nlist + c: the lower-bound units of cluster c (all its
 // queries, <= uqB per unit).
 __device__ __forceinline__ int units_of_entry(const int32_t* seg, const int32_t* vec_off,
-                                              int nlist, int uqB, int seed_all, int e) {
+                                              int nlist, int uqB, int seed_all, int sv,
+                                              int e) {
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
     const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
     const int uq = p ? uqB : kUnitQ0;
-    return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c]) : 0;
+    return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c], sv) : 0;
 }
 
 __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
@@ -92,13 +93,13 @@ __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
 // (blk_tot[b] units, blk_tot[kBlock + b] groups), then the carries of the blocks before.
 __global__ __launch_bounds__(256) void unit_scan_local_kernel(const int32_t* seg,
                                                               const int32_t* vec_off, int nlist,
-                                                              int uqB, int seed_all,
+                                                              int uqB, int seed_all, int sv,
                                                               int32_t* unit_off, int32_t* grp_off,
                                                               int32_t* blk_tot) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const uint32_t nu =
-        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, i) : 0u;
+        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, sv, i) : 0u;
     const uint32_t ng = i < nlist ? (uint32_t)groups_of_cluster(seg, i) : 0u;
     uint32_t tu = 0, tg = 0;
     const uint32_t ru = block_exclusive_scan(nu, s_wtot, &tu);
@@ -148,9 +149,9 @@ __device__ __forceinline__ int seg_search(const int32_t* off, int n, int x) {
 // One thread per weight group ({first pair, pair count}: kGroupQ consecutive pairs of a cluster's
 // segment), then one thread per unit: its segment by binary search over unit_off, then its
 // vector slice and query block.  Slices start on 64-vector blocks and are never empty (n > 64 S
-// (S - 1) whenever S = ceil(n / kSplitVec) > 1).
+// (S - 1) whenever S = ceil(n / sv) > 1, for sv >= 512).
 __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off,
-                                                        int nlist, int uqB, int seed_all,
+                                                        int nlist, int uqB, int seed_all, int sv,
                                                         const int32_t* unit_off,
                                                         int4* units, int max_units,
                                                         const int32_t* grp_off, int2* groups,
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, cons
         const int e = seg_search(unit_off, E, u);
         const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
         const int n = vec_off[c + 1] - vec_off[c];
-        const int S = splits_of(n);
+        const int S = splits_of(n, sv);
         const int local = u - unit_off[e];
         const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
         const int uq = p ? uqB : kUnitQ0;
@@ -609,7 +610,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         for (int i = 0; i < 8 && ldexpf(l1u, -es) > lim; ++i) ++es;
     }
     const float s = ldexpf(1.0f, es), inv_s = ldexpf(1.0f, -es);
-    int wsum = 0;
+    int wsum = 0, lsum = 0;  // sum w_int, sum |lo|
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
 #pragma unroll KEEP ? KS : 1
     for (int k = 0; k < KS; ++k) {
@@ -626,6 +627,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     wi[e] = (int)rintf(wk[16 * h2 + 4 * h + e] * inv_s);  // 0 for dims >= D_pad
                     wsum += wi[e];
+                    lsum += abs((int)(int8_t)(wi[e] & 0xff));
                 }
                 // lo = the low byte of wi as int8, hi = (wi - lo) / 256 = the second byte of
                 // wi + 128
@@ -644,6 +646,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         }
     }
     wsum += __shfl_xor(wsum, 1, kWave);
+    lsum += __shfl_xor(lsum, 1, kWave);
     if (valid && l == 0) {
         PairRec r;
         r.Qp = (double)Qp;
@@ -659,6 +662,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         r.a_max = a.cbound[kCbStride * c];
         r.r_max = a.cbound[kCbStride * c + 1];
         r.acc_max = 128.0 * (l1 * (double)inv_s + 0.5 * (double)D_pad);
+        r.lo_max = 128.0 * (double)lsum;  // <= 128 * 128 * D_pad <= 2^24
         a.prec[pp] = r;
     }
 }
@@ -1448,8 +1452,12 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     L.int_ok = !nok;
     L.tqw = tqw;
     L.inv_c1w = L.int_ok ? (float)(1.0 / c1_0) : 0.0f;  // a power of two in [2^-100, 2^100]
-    L.pad = 0;
-    if (valid) a.lbr[p] = L;
+    // |kq| <= 2^30 and lo_max <= 2^24: no int32 overflow
+    L.kq_pre = L.int_ok ? L.kq + (int)pr.lo_max : 0;
+    if (valid) {
+        a.lbr[p] = L;
+        a.lbk[p] = make_int2(L.kq, L.kq_pre);
+    }
 }
 
 
@@ -1470,15 +1478,19 @@ void lb_scan_kernel(BatchArgs a) {
     static_assert(KS <= 4, "narrow layout: D_pad <= 256");
     constexpr int BV = 64;
     constexpr int QW = 32;  // queries per wave
-    __shared__ uint4 s_codes[2][KS * 4 * BV];
-    __shared__ __align__(16) float s_A[2][BV];
-    __shared__ __align__(16) float s_r[2][BV];
-    __shared__ int s_thr[2][kWavesPerBlock][BV];
+    // LDS ring of blocks: NBUF - 1 blocks in flight while one is scanned (the loads' latency,
+    // not the matrix cores, bounds a block when the codes stream from HBM)
+    constexpr int NBUF = KS <= 2 ? 4 : 2;
+    __shared__ uint4 s_codes[NBUF][KS * 4 * BV];
+    __shared__ __align__(16) float s_A[NBUF][BV];
+    __shared__ __align__(16) float s_r[NBUF][BV];
+    __shared__ int s_thr[kWavesPerBlock][BV];  // the wave's thresholds of the block it scans
     __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
     __shared__ int s_scnt[kWavesPerBlock][QW], s_sbase[kWavesPerBlock][QW],
         s_sqid[kWavesPerBlock][QW];
     __shared__ float4 s_qf[kWavesPerBlock][QW];  // per query slot: (c1f, c2f, H32, -)
     __shared__ int s_unit[2];
+    __shared__ int4 s_urec[2];  // the units' records, fetched during the previous unit
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1492,19 +1504,28 @@ void lb_scan_kernel(BatchArgs a) {
     unsigned long long st_cand = 0, st_surv = 0;
     if (lane < QW) s_scnt[wid][lane] = 0;
 
-    // Next unit's counter value: taken two blocks before the current unit ends, published in
-    // s_unit at its end (slot (it + 1) & 1, read at the start of unit it + 1; its previous read,
-    // at the start of unit it - 1, is separated from the write by the barrier at the top of
-    // unit it).  The explicit LDS wait keeps that write ahead of the barrier.
-    if (tid == 0) s_unit[0] = atomicAdd(ctr, 1);
+    // Next unit: its counter value is taken three blocks before the current unit ends and its
+    // record moves global -> LDS two blocks before (thread 0, a direct load into s_urec), both
+    // published at the end of the unit (slot (it + 1) & 1, read at the start of unit it + 1;
+    // its previous read, at the start of unit it - 1, is separated from the writes by the
+    // barrier at the top of unit it).  The explicit waits keep the LDS write and the direct
+    // load ahead of the barrier.
+    if (tid == 0) {
+        const int u = atomicAdd(ctr, 1);
+        s_unit[0] = u;
+        if (rb + u < re) s_urec[0] = a.units[rb + u];
+    }
     for (int it = 0;; ++it) {
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __syncthreads();
         const int ui = __builtin_amdgcn_readfirstlane(s_unit[it & 1]) + rb;
         if (ui < rb || ui >= re) break;
         int nxt = 0;
-        const int4 un = a.units[ui];
-        const int cid = un.x & 0xfffff, cnt = un.x >> 20, start = un.y, vb = un.z, ve = un.w;
+        const int4 un = s_urec[it & 1];
+        const int cid = __builtin_amdgcn_readfirstlane(un.x & 0xfffff),
+                  cnt = __builtin_amdgcn_readfirstlane(un.x >> 20),
+                  start = __builtin_amdgcn_readfirstlane(un.y),
+                  vb = __builtin_amdgcn_readfirstlane(un.z), ve = __builtin_amdgcn_readfirstlane(un.w);
         const int G = (cnt + QW - 1) / QW;  // 32-query blocks (1..4)
         const int R = kWavesPerBlock / G;   // waves sharing a block split its tiles
         const int gq = wid / R, rr = wid - gq * R;
@@ -1516,14 +1537,19 @@ void lb_scan_kernel(BatchArgs a) {
         const int pb = start + gq * QW;     // the wave's first pair: a weight group's first
 
         // ---- this wave's queries: weight rows and the constants of lb_prep_kernel ----
-        v4i whi[2][KS], wlo[2][KS], kq4[2];
+        v4i whi[2][KS], wlo[2][KS], kq4[2], hq4[2];
         bool int_ok = false;
         float tqw = 0.0f, inv_c1w = 0.0f;
         if (active) {
+            // every prologue load is issued before the first use (one memory round trip): the
+            // group's constants, the (kq, kq_pre) of the lane's rows (lbk is padded by 32
+            // entries, so rows past the unit stay inside it), the weight rows
             const LbRec L0 = a.lbr[pb];
-            int_ok = __builtin_amdgcn_readfirstlane(L0.int_ok) != 0;
-            tqw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.tqw)));
-            inv_c1w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.inv_c1w)));
+            int2 kk[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) kk[h][r] = a.lbk[pb + 16 * h + 4 * g + r];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int qi = 16 * h + j;  // the A row this lane supplies
@@ -1536,11 +1562,20 @@ void lb_scan_kernel(BatchArgs a) {
                     whi[h][ks] = hv ? vh : v4i{0, 0, 0, 0};
                     wlo[h][ks] = hv ? vl : v4i{0, 0, 0, 0};
                 }
+            }
+            int_ok = __builtin_amdgcn_readfirstlane(L0.int_ok) != 0;
+            tqw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.tqw)));
+            inv_c1w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.inv_c1w)));
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
                 // C rows this lane receives: queries 16 h + 4 g + r (empty rows: INT_MIN)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int qr = 16 * h + 4 * g + r;
-                    kq4[h][r] = qr < nq ? (int_ok ? a.lbr[pb + qr].kq : 0) : (int_ok ? INT_MIN : 0);
+                    kq4[h][r] = qr < nq ? (int_ok ? kk[h][r].x : 0) : (int_ok ? INT_MIN : 0);
+                    // hi-plane start: ceil(kq_pre / 256) (|kq_pre| < 2^31 - 255); empty rows
+                    // start far below any threshold
+                    hq4[h][r] = qr < nq && int_ok ? (kk[h][r].y + 255) >> 8 : -(1 << 25);
                 }
             }
             if (lane < QW) {
@@ -1616,15 +1651,48 @@ void lb_scan_kernel(BatchArgs a) {
                 B[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
             int th = 0;
-            if constexpr (INT) th = s_thr[buf][wid][t * 16 + j];
+            if constexpr (INT) th = s_thr[wid][t * 16 + j];
             v4i h0 = {0, 0, 0, 0}, l0 = kq4[0], h1 = {0, 0, 0, 0}, l1 = kq4[1];
+            if constexpr (INT) {
+                // Hi plane first, started at ceil(kq_pre / 256) per row: S = 256 acc_hi + acc_lo
+                // + kq <= 256 h with |acc_lo| <= lo_max, so a tile whose rows all have
+                // h < floor((th - 1) / 256) + 1 (i.e. 256 h < th) fails the exact test too and
+                // costs no lo-plane work.
+                h0 = hq4[0];
+                h1 = hq4[1];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[0][ks], B[ks], h0, 0, 0, 0);
-                l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], l0, 0, 0, 0);
-                if constexpr (TWO) {
-                    h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[1][ks], B[ks], h1, 0, 0, 0);
-                    l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[1][ks], B[ks], l1, 0, 0, 0);
+                for (int ks = 0; ks < KS; ++ks) {
+                    h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[0][ks], B[ks], h0, 0, 0, 0);
+                    if constexpr (TWO)
+                        h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[1][ks], B[ks], h1, 0, 0, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_nop 7\n\ts_nop 7");
+                __builtin_amdgcn_sched_barrier(0);
+                const int thh = ((th - 1) >> 8) + 1;
+                int mh = max(max(h0[0], h0[1]), max(h0[2], h0[3]));
+                if constexpr (TWO) mh = max(mh, max(max(h1[0], h1[1]), max(h1[2], h1[3])));
+                if (__ballot(mh >= thh) == 0ull) return;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {  // back to the plain hi sums
+                    h0[r] -= hq4[0][r];
+                    if constexpr (TWO) h1[r] -= hq4[1][r];
+                }
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], l0, 0, 0, 0);
+                    if constexpr (TWO)
+                        l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[1][ks], B[ks], l1, 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) {
+                    h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[0][ks], B[ks], h0, 0, 0, 0);
+                    l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], l0, 0, 0, 0);
+                    if constexpr (TWO) {
+                        h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[1][ks], B[ks], h1, 0, 0, 0);
+                        l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[1][ks], B[ks], l1, 0, 0, 0);
+                    }
                 }
             }
             // The matrix core does not interlock VALU reads of its results: 16 wait states (plus
@@ -1676,11 +1744,14 @@ void lb_scan_kernel(BatchArgs a) {
         };
 
         // ---- stream the slice through LDS in 64-vector blocks ----
-        const uint4* cells_c = a.cells + (size_t)t0 * G16 * T;  // cluster's first tile
-        int ct = vb / T, cw = vb - ct * T;  // tile and slot of the next block to load
+        // Block-major cells ([tiles, T / 64, G16, 64]): a cluster's 64-vector blocks are
+        // consecutive runs of G16 * 64 cells, so block v0 .. v0 + 63 of the cluster starts at
+        // cell G16 * v0 and the next block to load is one pointer step away (no per-block
+        // tile / slot arithmetic in the scalar unit).
+        const uint4* next_blk = a.cells + (size_t)t0 * G16 * T + (size_t)G16 * vb;
         auto gload = [&](int buf, int blk0) __attribute__((always_inline)) {
-            // block-major cells: the block's groups are consecutive runs of 64 cells
-            const uint4* base = cells_c + (size_t)ct * G16 * T + (size_t)cw * G16 + wid * BV;
+            // the block's groups are consecutive runs of 64 cells
+            const uint4* base = next_blk + wid * BV;
 #pragma unroll
             for (int jj = 0; jj < KS; ++jj)
                 if (wid + 4 * jj < G16)
@@ -1691,22 +1762,30 @@ void lb_scan_kernel(BatchArgs a) {
                 load_lds4(a.vec_Ar + v0, off, s_A[buf]);
                 load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
             }
-            cw += BV;
-            if (cw == T) {
-                cw = 0;
-                ++ct;
-            }
+            next_blk += (size_t)G16 * BV;
         };
         const int nblk = (ve - vb + BV - 1) / BV;
-        if (nblk > 0) gload(0, vb);
+        // direct loads this wave issues per block (its code groups, plus the row scalars)
+        int nl = wid == 0 ? 2 : 0;
+#pragma unroll
+        for (int jj = 0; jj < KS; ++jj) nl += wid + 4 * jj < G16 ? 1 : 0;
+#pragma unroll
+        for (int pb0 = 0; pb0 < NBUF - 1; ++pb0)
+            if (pb0 < nblk) gload(pb0, vb + pb0 * BV);
         for (int b = 0; b < nblk; ++b) {
-            const int buf = b & 1;
-            // this wave's direct loads of block b have landed; the barrier covers everyone's
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            const int buf = b % NBUF;
+            // this wave's direct loads of block b have landed: vector memory operations complete
+            // in issue order, and only the loads of blocks b + 1 .. b + NBUF - 2 (plus any
+            // stores or atomics, which only make the wait longer) were issued after them; the
+            // barrier covers everyone's.  It also retires block b - 1, whose buffer is refilled
+            // next.
+            wait_vmcnt(nl * min(NBUF - 2, nblk - 1 - b));
             __syncthreads();
-            if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
+            if (tid == 0 && b == max(nblk - 3, 0)) nxt = atomicAdd(ctr, 1);
+            if (tid == 0 && b == max(nblk - 2, 0) && rb + nxt < re)  // one direct 16-byte load
+                load_lds16(a.units + rb, 16u * (uint32_t)nxt, &s_urec[(it + 1) & 1]);
             const int blk0 = vb + b * BV;
-            if (b + 1 < nblk) gload(buf ^ 1, blk0 + BV);
+            if (b + NBUF - 1 < nblk) gload((b + NBUF - 1) % NBUF, blk0 + (NBUF - 1) * BV);
             if (!active) continue;
             if (a.use_l1) {  // the wave leaves the block when none of its queries reaches its tile
                 const float* rm = a.tile_rmm + 2 * (size_t)(t0 + blk0 / T);
@@ -1715,7 +1794,7 @@ void lb_scan_kernel(BatchArgs a) {
             }
             if (int_ok) {
                 const float A = s_A[buf][lane], r = s_r[buf][lane];
-                s_thr[buf][wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                s_thr[wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
                 __builtin_amdgcn_wave_barrier();
                 if (two) tiles(std::true_type{}, std::true_type{}, buf, blk0);
                 else tiles(std::true_type{}, std::false_type{}, buf, blk0);
@@ -1727,7 +1806,13 @@ void lb_scan_kernel(BatchArgs a) {
         if (a.stats && active && rr == 0)
             st_cand += (unsigned long long)nq * (unsigned long long)(ve - vb);
         if (nsq > 0) flush();
-        if (tid == 0) s_unit[(it + 1) & 1] = nblk > 0 ? nxt : atomicAdd(ctr, 1);
+        if (tid == 0) {
+            if (nblk == 0) {  // (slices are never empty; kept for safety)
+                nxt = atomicAdd(ctr, 1);
+                if (rb + nxt < re) s_urec[(it + 1) & 1] = a.units[rb + nxt];
+            }
+            s_unit[(it + 1) & 1] = nxt;
+        }
     }
 
     if (a.stats && lane == 0) {

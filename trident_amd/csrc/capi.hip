@@ -128,6 +128,7 @@ struct Workspace {
     int8_t* pw;                      // [B * nprobe, 2, DP] batched-route weight planes
     PairRec* prec;                   // [B * nprobe]
     LbRec* lbr;                      // [B * nprobe]
+    int2* lbk;                       // [B * nprobe] (kq, kq_pre)
     double* cbound;                  // [nlist, kCbStride]
     double* qep;                     // [B]
     uint2* ub_list;                  // [B, ub_cap] seeding bounds and rows (batched route)
@@ -194,6 +195,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.pw = c.take<int8_t>(B * nprobe * 2 * plane_bytes(ix->D_pad));
     w.prec = c.take<PairRec>(B * nprobe);
     w.lbr = c.take<LbRec>(B * nprobe);
+    w.lbk = c.take<int2>(B * nprobe + 32);  // + 32: the scan reads whole 32-row groups
     w.cbound = c.take<double>(kCbStride * (int64_t)ix->nlist);
     w.qep = c.take<double>(B);
     w.ub_cap = ub_cap_of(std::min<int64_t>(K, 64));
@@ -984,8 +986,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         {
             const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
-                                                            ix->nlist, b.unit_q, 0, w.unit_off,
-                                                            w.grp_off, w.blk_tot);
+                                                            ix->nlist, b.unit_q, 0, kSplitVec,
+                                                            w.unit_off, w.grp_off, w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
             unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
                                                             w.unit_off, w.grp_off);
@@ -993,8 +995,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, 0,
-                                 w.unit_off, w.units, (int)w.max_units, w.grp_off, w.groups,
-                                 (int)w.max_groups);
+                                 kSplitVec, w.unit_off, w.units, (int)w.max_units, w.grp_off,
+                                 w.groups, (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if (M1 > 0) {  // warm-up: thresholds from the first probes, nothing listed
             b.cm_emit = 0;
@@ -1094,6 +1096,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.pw = w.pw;
         b.prec = w.prec;
         b.lbr = w.lbr;
+        b.lbk = w.lbk;
         // index-constant per-cluster bounds: the view's table when it has one
         b.cbound = ix->cluster_bounds ? ix->cluster_bounds : w.cbound;
         b.qep = w.qep;
@@ -1112,11 +1115,13 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         if ((rc = check_launch("aux_bounds_kernel"))) return rc;
         // TRIDENT_UB_SEED 2 seeds from every probe, 0 and 1 from the first p_init
         const int seed_all = sp->ub_seed == 2 ? 1 : 0;
+        const int split_vec = ix->D_pad <= 256 ? kSplitVecNarrow : kSplitVec;
         {
             const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= 150 (nlist <= 19200)
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
                                                             ix->nlist, b.unit_q, seed_all,
-                                                            w.unit_off, w.grp_off, w.blk_tot);
+                                                            split_vec, w.unit_off, w.grp_off,
+                                                            w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
             unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
                                                             w.unit_off, w.grp_off);
@@ -1124,8 +1129,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, seed_all,
-                                 w.unit_off, w.units, (int)w.max_units, w.grp_off, w.groups,
-                                 (int)w.max_groups);
+                                 split_vec, w.unit_off, w.units, (int)w.max_units, w.grp_off,
+                                 w.groups, (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if ((rc = launch_pair_prep(b, st))) return rc;
         if (M1 > 0 || seed_all) {

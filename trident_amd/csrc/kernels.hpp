@@ -81,6 +81,7 @@ struct PairRec {
     double a_max;    // >= A_x for every vector of the cluster
     double r_max;    // >= r_x for every vector of the cluster
     double acc_max;  // >= |sum c'_d w_int,d|
+    double lo_max;   // 128 * sum |lo_d| >= |sum c'_d lo_d| (the lo plane's share of the sum)
 };
 
 // Per-pair constants of the batched lower-bound scan (they depend on tau, so they are computed
@@ -92,7 +93,7 @@ struct LbRec {
     float tqw;         // the group's largest tq, rounded up
     float inv_c1w;     // 1 / c1 of the group (a power of two)
     int32_t int_ok;    // the group takes the integer test
-    int32_t pad;
+    int32_t kq_pre;    // kq + lo_max: with the hi plane alone, acc_hi * 256 + kq_pre >= the sum
 };
 
 // Everything one cluster-batched scan launch reads (csrc/batch.hip).
@@ -134,6 +135,7 @@ struct BatchArgs {
     int8_t* pw;                 // [M, 2, DP] int8 weight planes (hi, lo), natural dim order
     PairRec* prec;              // [M]
     LbRec* lbr;                 // [M]
+    int2* lbk;                  // [M] (kq, kq_pre) of lbr, packed for the scan's row loads
     const double* cbound;       // [nlist, kCbStride] (A_max, r_max, r_lo) per cluster
     const double* qep;          // [B] sum of qerr^2 per query
     double* tau;                // [B] float64 thresholds (set from the seeding lists)
@@ -309,6 +311,10 @@ __global__ void rerank_kernel(RerankArgs a);
 constexpr int kUnitQ = 128;
 constexpr int kUnitQWide = 64;
 constexpr int kUnitQ0 = 16;
+// Slice length sv (vectors) of the units: the narrow layout's longer slices halve the units'
+// fixed costs; the wide layout and mode 10's matrix-core scan keep shorter ones (their units do
+// more work per vector, so shorter slices balance the workgroups better).
+constexpr int kSplitVecNarrow = 2048;
 constexpr int kSplitVec = 1024;
 constexpr int kMaxSplit = 8;
 constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
@@ -343,13 +349,14 @@ inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
 // pass-1 pairs.
 // Two launches of ceil(2 nlist / kBlock) blocks; blk_tot holds 2 * kBlock block totals.
 __global__ void unit_scan_local_kernel(const int32_t* seg, const int32_t* vec_off, int nlist,
-                                       int uqB, int seed_all, int32_t* unit_off, int32_t* grp_off,
+                                       int uqB, int seed_all, int sv, int32_t* unit_off,
+                                       int32_t* grp_off,
                                        int32_t* blk_tot);
 __global__ void unit_scan_carry_kernel(int nlist, const int32_t* blk_tot, int nblk,
                                        int32_t* unit_off, int32_t* grp_off);
 
 __global__ void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
-                                 int seed_all, const int32_t* unit_off, int4* units, int max_units,
+                                 int seed_all, int sv, const int32_t* unit_off, int4* units, int max_units,
                                  const int32_t* grp_off, int2* groups, int max_groups);
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
