@@ -71,16 +71,24 @@ __device__ __forceinline__ int splits_of(int n, int sv) {
     return min(kMaxSplit, (n + sv - 1) / sv);
 }
 
+// Slices a seeding unit set scans: at most the first two of a cluster's slices (up to 2 sv
+// rows).  Seeding needs K good rows per query, not every row of its first probes; the
+// threshold stays exact (the K-th exact distance of rows that exist), only looser.  At N = 1e8
+// (clusters of ~6,100 rows) this halves the seeding pass for a slightly longer lower-bound pass
+// (measured: one slice per seeding cluster instead let some queries' candidate lists overflow).
+__device__ __forceinline__ int seed_slices(int S) { return min(S, 2); }
+
 // Entry e < nlist: the seeding units of cluster e (its pass-1 queries, or all of them when
-// seed_all, <= 16 per unit); entry nlist + c: the lower-bound units of cluster c (all its
-// queries, <= uqB per unit).
+// seed_all, <= 16 per unit; the first seed_slices(S) slices); entry nlist + c: the lower-bound
+// units of cluster c (all its queries, <= uqB per unit, every slice).
 __device__ __forceinline__ int units_of_entry(const int32_t* seg, const int32_t* vec_off,
                                               int nlist, int uqB, int seed_all, int sv,
                                               int e) {
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
     const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
     const int uq = p ? uqB : kUnitQ0;
-    return q > 0 ? ((q + uq - 1) / uq) * splits_of(vec_off[c + 1] - vec_off[c], sv) : 0;
+    const int S = splits_of(vec_off[c + 1] - vec_off[c], sv);
+    return q > 0 ? ((q + uq - 1) / uq) * (p ? S : seed_slices(S)) : 0;
 }
 
 __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {

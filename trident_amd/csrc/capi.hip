@@ -154,16 +154,17 @@ inline int64_t plane_bytes(int D_pad) { return 64 * (int64_t)((D_pad + 63) / 64)
 // which with the base in host memory crosses PCIe for every probed row.  Past 64 neighbours in
 // more than 256 dims the K-th distance sits in the bulk of the distance distribution (cfg 3,
 // K = 100: ~1 % of candidates pass, ~2,300 per query with a long tail), so those lists are 8x
-// deeper.
-inline int64_t cand_cap(int64_t nprobe, int64_t K, int64_t D_pad) {
-    return nprobe * std::max<int64_t>(K, 64) * (K > 64 && D_pad > 256 ? 8 : 1);
+// deeper.  An index with a fine level keeps its base in host memory, where an overflow costs
+// most, so its lists are twice as deep again.
+inline int64_t cand_cap(int64_t nprobe, int64_t K, int64_t D_pad, bool fine) {
+    return nprobe * std::max<int64_t>(K, 64) * (K > 64 && D_pad > 256 ? 8 : 1) * (fine ? 2 : 1);
 }
 
 Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprobe, int64_t K) {
     Carver c{static_cast<char*>(base)};
     Workspace w;
     const int64_t KP = K <= 64 ? 64 : K <= 128 ? 128 : 256;
-    const int64_t cap = cand_cap(nprobe, K, ix->D_pad);
+    const int64_t cap = cand_cap(nprobe, K, ix->D_pad, ix->fine_codes && ix->fine_qp);
     w.xq64 = c.take<double>(B * ix->D);
     w.xrot64 = c.take<double>(B * ix->D_pad);
     w.xrot32 = c.take<float>(B * ix->D_pad);
@@ -920,7 +921,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 
     const int KP = list_kp(K_list);
-    const int64_t cap = cand_cap(nprobe, K_list, ix->D_pad);
+    const int64_t cap = cand_cap(nprobe, K_list, ix->D_pad, ix->fine_codes && ix->fine_qp);
     if (out->stats) {
         if ((rc = fill(reinterpret_cast<int32_t*>(out->stats), 0, 8, st))) return rc;
         if ((rc = fill(reinterpret_cast<int32_t*>(w.stat_slots), 0, 2 * 4 * kStatSlots, st))) return rc;
