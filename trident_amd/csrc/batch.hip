@@ -1469,8 +1469,8 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
 }
 
 
-// Pass B, narrow layout (D_pad <= 256, 64-vector LDS blocks), every probe of a unit's cluster
-// slice.  Queries are the rows of the matrix-core product (A operand, 16 per MFMA, weights held
+// Pass B, narrow layout (D_pad <= 256; LDS blocks of 128 rows up to D_pad 128, else 64), every
+// probe of a unit's cluster slice.  Queries are the rows of the matrix-core product (A operand, 16 per MFMA, weights held
 // in registers) and vectors its columns (B operand, read from LDS), so a lane's four results
 // (rows 4 g + r, column j = lane & 15) share one vector and the integer test needs one int32
 // threshold per lane: max over the lane's rows of S = acc + kq against thr_x.  Each wave owns
@@ -1484,19 +1484,24 @@ template <int KS>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(KS <= 2 ? 4 : 1)))
 void lb_scan_kernel(BatchArgs a) {
     static_assert(KS <= 4, "narrow layout: D_pad <= 256");
-    constexpr int BV = 64;
-    constexpr int QW = 32;  // queries per wave
-    // LDS ring of blocks: NBUF - 1 blocks in flight while one is scanned (the loads' latency,
-    // not the matrix cores, bounds a block when the codes stream from HBM)
-    constexpr int NBUF = KS <= 2 ? 4 : 2;
-    __shared__ uint4 s_codes[NBUF][KS * 4 * BV];
-    __shared__ __align__(16) float s_A[NBUF][BV];
-    __shared__ __align__(16) float s_r[NBUF][BV];
-    __shared__ int s_thr[kWavesPerBlock][BV];  // the wave's thresholds of the block it scans
+    constexpr int BV = 64;               // rows of one cell run (G16 * 64 cells)
+    constexpr int SB = KS <= 2 ? 2 : 1;  // cell runs per LDS block
+    constexpr int BR = SB * BV;          // rows per LDS block
+    constexpr int QW = 32;               // queries per wave
+    // Two LDS blocks: one is scanned while the next one's loads are in flight.  A block is as
+    // large as 32 KB of codes allows, so that its fixed costs (the barrier, the wave's
+    // thresholds, the load issue) are spread over as many tiles as possible.
+    constexpr int NBUF = 2;
+    __shared__ uint4 s_codes[NBUF][SB][KS * 4 * BV];
+    __shared__ __align__(16) float s_A[NBUF][BR];
+    __shared__ __align__(16) float s_r[NBUF][BR];
     __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
     __shared__ int s_scnt[kWavesPerBlock][QW], s_sbase[kWavesPerBlock][QW],
         s_sqid[kWavesPerBlock][QW];
     __shared__ float4 s_qf[kWavesPerBlock][QW];  // per query slot: (c1f, c2f, H32, -)
+    // per query slot: kq, the lo-plane accumulators' start (empty slots INT_MIN); read only by
+    // tiles that pass the hi-plane prefilter, so it is not held in registers
+    __shared__ __align__(16) int s_kq[kWavesPerBlock][QW];
     __shared__ int s_unit[2];
     __shared__ int4 s_urec[2];  // the units' records, fetched during the previous unit
 
@@ -1545,7 +1550,7 @@ void lb_scan_kernel(BatchArgs a) {
         const int pb = start + gq * QW;     // the wave's first pair: a weight group's first
 
         // ---- this wave's queries: weight rows and the constants of lb_prep_kernel ----
-        v4i whi[2][KS], wlo[2][KS], kq4[2], hq4[2];
+        v4i whi[2][KS], wlo[2][KS], hq4[2];
         bool int_ok = false;
         float tqw = 0.0f, inv_c1w = 0.0f;
         if (active) {
@@ -1580,7 +1585,6 @@ void lb_scan_kernel(BatchArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int qr = 16 * h + 4 * g + r;
-                    kq4[h][r] = qr < nq ? (int_ok ? kk[h][r].x : 0) : (int_ok ? INT_MIN : 0);
                     // hi-plane start: ceil(kq_pre / 256) (|kq_pre| < 2^31 - 255); empty rows
                     // start far below any threshold
                     hq4[h][r] = qr < nq && int_ok ? (kk[h][r].y + 255) >> 8 : -(1 << 25);
@@ -1589,6 +1593,7 @@ void lb_scan_kernel(BatchArgs a) {
             if (lane < QW) {
                 const bool hv = lane < nq;
                 const LbRec L = a.lbr[pb + (hv ? lane : 0)];
+                s_kq[wid][lane] = hv ? L.kq : INT_MIN;
                 s_sqid[wid][lane] = a.pair_qid[pb + (hv ? lane : 0)];
                 s_qf[wid][lane] = hv ? make_float4(L.c1f, L.c2f, L.H32, 0.0f)
                                      : make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // never passes
@@ -1604,6 +1609,7 @@ void lb_scan_kernel(BatchArgs a) {
 
         // ---- survivor queue (entries li << 5 | query slot) ----
         int nsq = 0;
+        int thr_r[SB];  // the integer thresholds of the block's rows sb * 64 + lane
         auto flush = [&]() __attribute__((always_inline)) {
             for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 31u], 1);
             __builtin_amdgcn_wave_barrier();
@@ -1651,16 +1657,20 @@ void lb_scan_kernel(BatchArgs a) {
         // ---- one 16-vector tile: INT = the integer test, TWO = both halves hold queries ----
         auto tile = [&](auto int_c, auto two_c, int buf, int t, int li0) __attribute__((always_inline)) {
             constexpr bool INT = decltype(int_c)::value, TWO = decltype(two_c)::value;
-            const uint4* blk = s_codes[buf];
+            const uint4* blk = s_codes[buf][t >> 2];
             v4i B[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
-                const uint4 v = blk[(ks * 4 + g) * BV + t * 16 + j];
+                const uint4 v = blk[(ks * 4 + g) * BV + (t & 3) * 16 + j];
                 B[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
             int th = 0;
-            if constexpr (INT) th = s_thr[wid][t * 16 + j];
-            v4i h0 = {0, 0, 0, 0}, l0 = kq4[0], h1 = {0, 0, 0, 0}, l1 = kq4[1];
+            // the threshold of column j (row t * 16 + j of the block), held by lane
+            // (t & 3) * 16 + j in its run's register
+            if constexpr (INT)
+                th = __builtin_amdgcn_ds_bpermute((((t & 3) << 4) | j) << 2,
+                                                  SB == 1 || (t >> 2) == 0 ? thr_r[0] : thr_r[SB - 1]);
+            v4i h0 = {0, 0, 0, 0}, l0 = {0, 0, 0, 0}, h1 = {0, 0, 0, 0}, l1 = {0, 0, 0, 0};
             if constexpr (INT) {
                 // Hi plane first, started at ceil(kq_pre / 256) per row: S = 256 acc_hi + acc_lo
                 // + kq <= 256 h with |acc_lo| <= lo_max, so a tile whose rows all have
@@ -1686,6 +1696,8 @@ void lb_scan_kernel(BatchArgs a) {
                     h0[r] -= hq4[0][r];
                     if constexpr (TWO) h1[r] -= hq4[1][r];
                 }
+                l0 = *reinterpret_cast<const v4i*>(&s_kq[wid][4 * g]);
+                if constexpr (TWO) l1 = *reinterpret_cast<const v4i*>(&s_kq[wid][16 + 4 * g]);
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
                     l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], l0, 0, 0, 0);
@@ -1740,46 +1752,56 @@ void lb_scan_kernel(BatchArgs a) {
             }
         };
         auto tiles = [&](auto int_c, auto two_c, int buf, int blk0) __attribute__((always_inline)) {
-            if (R == 1 && blk0 + BV <= ve) {  // the common case: straight-line tiles
+            if (R == 1 && blk0 + BR <= ve) {  // the common case: straight-line tiles
 #pragma unroll
-                for (int t = 0; t < BV / 16; ++t) tile(int_c, two_c, buf, t, blk0 + t * 16);
+                for (int t = 0; t < BR / 16; ++t) tile(int_c, two_c, buf, t, blk0 + t * 16);
             } else {
-                for (int t = rr; t < BV / 16; t += R) {
+                for (int t = rr; t < BR / 16; t += R) {
                     if (blk0 + t * 16 >= ve) break;
                     tile(int_c, two_c, buf, t, blk0 + t * 16);
                 }
             }
         };
 
-        // ---- stream the slice through LDS in 64-vector blocks ----
-        // Block-major cells ([tiles, T / 64, G16, 64]): a cluster's 64-vector blocks are
-        // consecutive runs of G16 * 64 cells, so block v0 .. v0 + 63 of the cluster starts at
+        // ---- stream the slice through LDS in blocks of SB cell runs ----
+        // Block-major cells ([tiles, T / 64, G16, 64]): a cluster's 64-vector runs are
+        // consecutive runs of G16 * 64 cells, so rows v0 .. v0 + 63 of the cluster start at
         // cell G16 * v0 and the next block to load is one pointer step away (no per-block
         // tile / slot arithmetic in the scalar unit).
         const uint4* next_blk = a.cells + (size_t)t0 * G16 * T + (size_t)G16 * vb;
         auto gload = [&](int buf, int blk0) __attribute__((always_inline)) {
-            // the block's groups are consecutive runs of 64 cells
-            const uint4* base = next_blk + wid * BV;
 #pragma unroll
-            for (int jj = 0; jj < KS; ++jj)
-                if (wid + 4 * jj < G16)
-                    load_lds16(base + (size_t)(4 * jj) * BV, 16u * lane,
-                               &s_codes[buf][(wid + 4 * jj) * BV]);
-            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
-                const uint32_t off = 8u * (uint32_t)min(blk0 + lane, ve - 1);
-                load_lds4(a.vec_Ar + v0, off, s_A[buf]);
-                load_lds4(a.vec_Ar + v0, off + 4u, s_r[buf]);
+            for (int sb = 0; sb < SB; ++sb) {
+                // a run past the slice end loads the block's first run again (its rows are never
+                // scanned): the cells after a cluster's last run belong to the next cluster or lie
+                // past the array, and every block issues the same loads (the waits count them)
+                const uint4* base =
+                    (sb == 0 || blk0 + sb * BV < ve ? next_blk + (size_t)sb * G16 * BV : next_blk) +
+                    wid * BV;
+#pragma unroll
+                for (int jj = 0; jj < KS; ++jj)
+                    if (wid + 4 * jj < G16)
+                        load_lds16(base + (size_t)(4 * jj) * BV, 16u * lane,
+                                   &s_codes[buf][sb][(wid + 4 * jj) * BV]);
             }
-            next_blk += (size_t)G16 * BV;
-        };
-        const int nblk = (ve - vb + BV - 1) / BV;
-        // direct loads this wave issues per block (its code groups, plus the row scalars)
-        int nl = wid == 0 ? 2 : 0;
+            if (wid == 0) {  // rows past the slice read the slice's last row (never used)
 #pragma unroll
-        for (int jj = 0; jj < KS; ++jj) nl += wid + 4 * jj < G16 ? 1 : 0;
+                for (int sb = 0; sb < SB; ++sb) {
+                    const uint32_t off = 8u * (uint32_t)min(blk0 + sb * BV + lane, ve - 1);
+                    load_lds4(a.vec_Ar + v0, off, &s_A[buf][sb * BV]);
+                    load_lds4(a.vec_Ar + v0, off + 4u, &s_r[buf][sb * BV]);
+                }
+            }
+            next_blk += (size_t)G16 * BR;
+        };
+        const int nblk = (ve - vb + BR - 1) / BR;
+        // direct loads this wave issues per block (its code groups, plus the row scalars)
+        int nl = wid == 0 ? 2 * SB : 0;
+#pragma unroll
+        for (int jj = 0; jj < KS; ++jj) nl += wid + 4 * jj < G16 ? SB : 0;
 #pragma unroll
         for (int pb0 = 0; pb0 < NBUF - 1; ++pb0)
-            if (pb0 < nblk) gload(pb0, vb + pb0 * BV);
+            if (pb0 < nblk) gload(pb0, vb + pb0 * BR);
         for (int b = 0; b < nblk; ++b) {
             const int buf = b % NBUF;
             // this wave's direct loads of block b have landed: vector memory operations complete
@@ -1792,18 +1814,23 @@ void lb_scan_kernel(BatchArgs a) {
             if (tid == 0 && b == max(nblk - 3, 0)) nxt = atomicAdd(ctr, 1);
             if (tid == 0 && b == max(nblk - 2, 0) && rb + nxt < re)  // one direct 16-byte load
                 load_lds16(a.units + rb, 16u * (uint32_t)nxt, &s_urec[(it + 1) & 1]);
-            const int blk0 = vb + b * BV;
-            if (b + NBUF - 1 < nblk) gload((b + NBUF - 1) % NBUF, blk0 + (NBUF - 1) * BV);
+            const int blk0 = vb + b * BR;
+            if (b + NBUF - 1 < nblk) gload((b + NBUF - 1) % NBUF, blk0 + (NBUF - 1) * BR);
             if (!active) continue;
-            if (a.use_l1) {  // the wave leaves the block when none of its queries reaches its tile
-                const float* rm = a.tile_rmm + 2 * (size_t)(t0 + blk0 / T);
-                const bool need = l1_tau >= 0.0 && !l1_skips(l1_dqc, l1_tau, rm[0], rm[1]);
+            if (a.use_l1) {  // the wave leaves the block when none of its queries reaches its tiles
+                const int ta = blk0 / T, tb = (min(blk0 + BR, ve) - 1) / T;
+                const float* rm = a.tile_rmm + 2 * (size_t)(t0 + ta);
+                bool need = l1_tau >= 0.0 && !l1_skips(l1_dqc, l1_tau, rm[0], rm[1]);
+                if (tb != ta) need = need || (l1_tau >= 0.0 && !l1_skips(l1_dqc, l1_tau, rm[2], rm[3]));
                 if (__ballot(need) == 0ull) continue;
             }
             if (int_ok) {
-                const float A = s_A[buf][lane], r = s_r[buf][lane];
-                s_thr[wid][lane] = blk0 + lane < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
-                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int sb = 0; sb < SB; ++sb) {
+                    const int i = sb * BV + lane;
+                    const float A = s_A[buf][i], r = s_r[buf][i];
+                    thr_r[sb] = blk0 + i < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                }
                 if (two) tiles(std::true_type{}, std::true_type{}, buf, blk0);
                 else tiles(std::true_type{}, std::false_type{}, buf, blk0);
             } else {
