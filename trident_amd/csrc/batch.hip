@@ -759,9 +759,10 @@ __device__ __forceinline__ int lb_thr(float A, float r, float tq, float inv_c1) 
 // block's first tile on the next block's loads.  It does not see these, so the callers wait
 // themselves (vmcnt(0) before the barrier that publishes a block); the compiler's waits for
 // its own global loads only grow more conservative (the counter retires in order).
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
-}
+// A generic pointer into LDS is the shared aperture's base in the high half and the LDS
+// address in the low half, so the low half is taken as is (an address-space cast would add a
+// null test per load).
+__device__ __forceinline__ uint32_t lds_addr(const void* p) { return (uint32_t)(size_t)p; }
 // M0 (the LDS address of the load, latched at issue) is saved and restored around it.
 // A wave-uniform base pointer kept in SGPRs: inside lane-divergent branches the compiler may
 // otherwise materialise it in VGPRs, which the direct loads' saddr operand cannot take.
@@ -1609,7 +1610,9 @@ void lb_scan_kernel(BatchArgs a) {
 
         // ---- survivor queue (entries li << 5 | query slot) ----
         int nsq = 0;
-        int thr_r[SB];  // the integer thresholds of the block's rows sb * 64 + lane
+        // the integer thresholds th of the block's rows sb * 64 + lane, and their hi-plane form
+        // thh = floor((th - 1) / 256) + 1 (256 h < th iff h < thh)
+        int thr_r[SB], thh_r[SB];
         auto flush = [&]() __attribute__((always_inline)) {
             for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 31u], 1);
             __builtin_amdgcn_wave_barrier();
@@ -1664,12 +1667,12 @@ void lb_scan_kernel(BatchArgs a) {
                 const uint4 v = blk[(ks * 4 + g) * BV + (t & 3) * 16 + j];
                 B[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
-            int th = 0;
-            // the threshold of column j (row t * 16 + j of the block), held by lane
-            // (t & 3) * 16 + j in its run's register
+            // the thresholds of column j (row t * 16 + j of the block) are held by lane
+            // (t & 3) * 16 + j in its run's registers
+            const int src = (((t & 3) << 4) | j) << 2;
+            int thh = 0;
             if constexpr (INT)
-                th = __builtin_amdgcn_ds_bpermute((((t & 3) << 4) | j) << 2,
-                                                  SB == 1 || (t >> 2) == 0 ? thr_r[0] : thr_r[SB - 1]);
+                thh = __builtin_amdgcn_ds_bpermute(src, SB == 1 || (t >> 2) == 0 ? thh_r[0] : thh_r[SB - 1]);
             v4i h0 = {0, 0, 0, 0}, l0 = {0, 0, 0, 0}, h1 = {0, 0, 0, 0}, l1 = {0, 0, 0, 0};
             if constexpr (INT) {
                 // Hi plane first, started at ceil(kq_pre / 256) per row: S = 256 acc_hi + acc_lo
@@ -1687,7 +1690,6 @@ void lb_scan_kernel(BatchArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
                 asm volatile("s_nop 7\n\ts_nop 7");
                 __builtin_amdgcn_sched_barrier(0);
-                const int thh = ((th - 1) >> 8) + 1;
                 int mh = max(max(h0[0], h0[1]), max(h0[2], h0[3]));
                 if constexpr (TWO) mh = max(mh, max(max(h1[0], h1[1]), max(h1[2], h1[3])));
                 if (__ballot(mh >= thh) == 0ull) return;
@@ -1730,6 +1732,8 @@ void lb_scan_kernel(BatchArgs a) {
             }
             const int li = li0 + j;
             if constexpr (INT) {
+                const int th =
+                    __builtin_amdgcn_ds_bpermute(src, SB == 1 || (t >> 2) == 0 ? thr_r[0] : thr_r[SB - 1]);
                 int m = max(max(S[0][0], S[0][1]), max(S[0][2], S[0][3]));
                 if constexpr (TWO) m = max(m, max(max(S[1][0], S[1][1]), max(S[1][2], S[1][3])));
                 if (__ballot(m >= th) == 0ull) return;
@@ -1829,7 +1833,9 @@ void lb_scan_kernel(BatchArgs a) {
                 for (int sb = 0; sb < SB; ++sb) {
                     const int i = sb * BV + lane;
                     const float A = s_A[buf][i], r = s_r[buf][i];
-                    thr_r[sb] = blk0 + i < ve ? lb_thr(A, r, tqw, inv_c1w) : INT_MAX;
+                    const int th = lb_thr(A, r, tqw, inv_c1w);  // rows past the slice: INT_MAX
+                    thr_r[sb] = blk0 + i < ve ? th : INT_MAX;
+                    thh_r[sb] = ((thr_r[sb] - 1) >> 8) + 1;
                 }
                 if (two) tiles(std::true_type{}, std::true_type{}, buf, blk0);
                 else tiles(std::true_type{}, std::false_type{}, buf, blk0);
