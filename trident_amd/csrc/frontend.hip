@@ -896,7 +896,9 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     int Dq, int nprobe,
     int32_t* __restrict__ out_cids, float* __restrict__ out_dqcs, int ld,
     int32_t* __restrict__ out2_cids, float* __restrict__ out2_dqcs, int ld2) {
-    __shared__ int32_t s_band[kWavesPerBlock][2 * kWave];
+    // the band's centroids (up to 8 per lane)
+    constexpr int kBandMax = 8 * kWave;
+    __shared__ int32_t s_band[kWavesPerBlock][kBandMax];
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = blockIdx.x * kWavesPerBlock + wid;
@@ -909,7 +911,11 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         const int c = i * kWave + lane;
         v[i] = !STREAM && c < nlist ? arow[c] : INFINITY;
     }
-    if constexpr (STREAM) {  // the lane's V smallest, ascending (selects: no NaN here)
+    // STREAM: the lane's V smallest, ascending, with their centroids (vi)
+    int vi[STREAM ? V : 1];
+#pragma unroll
+    for (int i = 0; i < (STREAM ? V : 1); ++i) vi[i] = -1;
+    if constexpr (STREAM) {  // (selects: no NaN here)
         // eight of the lane's values per round, all loaded before the first insertion
         for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
             float xs[8];
@@ -921,11 +927,17 @@ __global__ __launch_bounds__(256) void select_band_kernel(
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const float x = xs[u];
+                const int cx = c0 + u * kWave + lane;
                 if (x < v[V - 1]) {
 #pragma unroll
-                    for (int i = V - 1; i > 0; --i)
-                        v[i] = x < v[i - 1] ? v[i - 1] : (x < v[i] ? x : v[i]);
-                    v[0] = x < v[0] ? x : v[0];
+                    for (int i = V - 1; i > 0; --i) {
+                        const bool up = x < v[i - 1], here = x < v[i];
+                        v[i] = up ? v[i - 1] : (here ? x : v[i]);
+                        vi[i] = up ? vi[i - 1] : (here ? cx : vi[i]);
+                    }
+                    const bool here = x < v[0];
+                    v[0] = here ? x : v[0];
+                    vi[0] = here ? cx : vi[0];
                 }
             }
         }
@@ -1036,11 +1048,28 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         }
         return acc;
     };
-    // STREAM: the band is compacted from the row in one pass (eight values per lane loaded
-    // per round), counting past the 128 slots without writing; the registers hold part of it
+    // The band is compacted from the registers (from_regs) when they hold all of it and it
+    // fits kBandMax: STREAM when every lane's V-th smallest lies above thr (the lanes' lists
+    // then hold every value <= thr), else whenever its count does.  Otherwise, STREAM, it is
+    // compacted from the row in one more pass (eight values per lane loaded per round),
+    // counting past the 128 slots without writing.
     int mband = nlist + 1, nb_stream = 0;
+    bool from_regs = false;
     if (thr < INFINITY) {
-        if constexpr (STREAM) {
+        // (not past V = 32 without STREAM: the unrolled compaction would cost a wave per SIMD)
+        const bool regs_hold =
+            STREAM ? __ballot(v[V - 1] <= thr) == 0ull : V <= 32 && count_le(thr) <= kBandMax;
+        if (regs_hold && (!STREAM || kWave * V <= kBandMax)) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const bool take = v[i] <= thr;
+                const uint64_t mk = __ballot(take);
+                if (take) band[nb_stream + mask_rank(mk)] = STREAM ? vi[STREAM ? i : 0] : i * kWave + lane;
+                nb_stream += __popcll(mk);
+            }
+            mband = nb_stream;
+            from_regs = true;
+        } else if constexpr (STREAM) {
             for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
                 float xs[8];
 #pragma unroll
@@ -1066,7 +1095,7 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         // the common case: the band fits two entries per lane.  Compact it, compute the exact
         // distances, and rank every entry by counting the entries before it in (d, cid) order.
         int nb = 0;
-        if constexpr (STREAM) {
+        if (STREAM || from_regs) {
             nb = nb_stream;  // compacted above
         } else {
 #pragma unroll
@@ -1106,40 +1135,56 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         if (h1 && r1 < nprobe) emit(r1, k1, c1);
         return;
     }
-    // a wide band (data far from the origin): 64 band centroids at a time into a register list
+    // a wide band: 64 band centroids at a time into a register list
     WaveList<KP> L;
     L.init();
     int nb = 0;
-    auto refine = [&](int n) {
+    auto refine = [&](int b0, int n) {
         const bool has = lane < n;
-        const int c = band[has ? lane : 0];
+        const int c = band[b0 + (has ? lane : 0)];
         const double dd = exact(c);
         list_offer(L, nprobe, has ? key_of(dd) : kKeyInvalid, has ? c : kIdInvalid);
     };
-    // the band, from the approximations again (L2; a rolled loop keeps one copy of refine)
-    const int nch = (nlist + kWave - 1) / kWave;
-#pragma unroll 1
-    for (int i = 0; i < nch; ++i) {
-        const int c = i * kWave + lane;
-        const bool take = c < nlist && arow[c] <= thr;
-        const uint64_t mk = __ballot(take);
-        if (take) band[nb + mask_rank(mk)] = i * kWave + lane;
-        nb += __popcll(mk);
-        if (nb >= kWave) {
-            wave_sync();
-            refine(kWave);
-            wave_sync();
-            const int rest = nb - kWave;  // <= 63 entries move down
-            const int moved = lane < rest ? band[kWave + lane] : 0;
-            wave_sync();
-            if (lane < rest) band[lane] = moved;
-            wave_sync();
-            nb = rest;
-        }
-    }
-    if (nb > 0) {
+    if (from_regs) {  // the band is in LDS already
         wave_sync();
-        refine(nb);
+#pragma unroll 1
+        for (int b0 = 0; b0 < mband; b0 += kWave) refine(b0, min(kWave, mband - b0));
+    } else {
+        // the band, from the approximations again (L2), R values per lane loaded per round
+        constexpr int R = STREAM ? 8 : 1;
+        const int nch = (nlist + kWave - 1) / kWave;
+#pragma unroll 1
+        for (int i0 = 0; i0 < nch; i0 += R) {
+            float xs[R];
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                const int c = (i0 + u) * kWave + lane;
+                xs[u] = c < nlist ? arow[c] : INFINITY;
+            }
+#pragma unroll 1
+            for (int u = 0; u < R; ++u) {
+                const int c = (i0 + u) * kWave + lane;
+                const bool take = c < nlist && xs[u] <= thr;
+                const uint64_t mk = __ballot(take);
+                if (take) band[nb + mask_rank(mk)] = c;
+                nb += __popcll(mk);
+                if (nb >= kWave) {
+                    wave_sync();
+                    refine(0, kWave);
+                    wave_sync();
+                    const int rest = nb - kWave;  // <= 63 entries move down
+                    const int moved = lane < rest ? band[kWave + lane] : 0;
+                    wave_sync();
+                    if (lane < rest) band[lane] = moved;
+                    wave_sync();
+                    nb = rest;
+                }
+            }
+        }
+        if (nb > 0) {
+            wave_sync();
+            refine(0, nb);
+        }
     }
     if (lane < nprobe) emit(lane, L.k0, L.i0);
     if constexpr (KP == 128) {
