@@ -588,9 +588,8 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                              st>>>(xq, B, ix->D, Dq, w.qt32, w.qn32);
         if ((rc = check_launch("pad_queries_kernel"))) return rc;
         float* a32 = reinterpret_cast<float*>(w.cd64);  // [B, nlist] approximations
-        coarse_gemm_kernel<<<dim3((unsigned)((B + 63) / 64),
-                                  (unsigned)((ix->nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles))),
-                             kBlock, 0, st>>>(w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq,
+        const int64_t ncg = (ix->nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles);
+        coarse_gemm_kernel<<<(unsigned)(8 * ((B + 63) / 64) * ((ncg + 7) / 8)), kBlock, 0, st>>>(w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq,
                                               a32);
         if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
         const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);

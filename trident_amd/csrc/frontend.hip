@@ -738,8 +738,12 @@ __global__ __launch_bounds__(256) void pad_centroids_kernel(const float* __restr
     }
 }
 
-// grid (ceil(B / 64), ceil(nlist / (16 kGemmTiles))), block 256: each wave 16 queries (one query
-// tile), all four waves the same kGemmTiles centroid tiles in the same order.  v_mfma_f32_16x16x4f32 with query
+// One-dimensional grid of 8 * ceil(B / 64) * ceil(ncg / 8) blocks (ncg = ceil(nlist / (16
+// kGemmTiles)) centroid groups), block 256.  Blocks are dealt to the XCDs round-robin, so block
+// b runs on XCD b % 8: XCD x takes centroid groups [x cpx, (x + 1) cpx) (cpx = ceil(ncg / 8)) for
+// every query block, and its share of the centroid tiles (1 MiB at nlist 16,384) stays in its
+// L2.  Each wave 16 queries (one query tile), all four waves the same kGemmTiles centroid tiles
+// in the same order.  v_mfma_f32_16x16x4f32 with query
 // rows as A (16 x 4) and centroids as B (4 x 16), operands straight from the tile layouts: a
 // chunk of 32 k-steps is 8 + 8 coalesced float4 loads, issued whole before its 32 MFMAs; steps
 // past S are zero (clamped loads, no branch among the MFMAs).
@@ -754,14 +758,18 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, g = lane >> 4;
-    const int qb0 = blockIdx.x * 64 + wid * 16;
+    const int ncg = (nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles), cpx = (ncg + 7) >> 3;
+    const int xcd = (int)(blockIdx.x & 7), local = (int)(blockIdx.x >> 3);
+    const int bx = local / cpx, by = xcd * cpx + (local - (local / cpx) * cpx);
+    if (by >= ncg || bx * 64 >= B) return;  // the whole block
+    const int qb0 = bx * 64 + wid * 16;
     const bool wave_live = qb0 < B;  // waves past the last query still help with the LDS copy
     const int qtile = wave_live ? qb0 / 16 : 0;
     const int qb = wave_live ? qb0 : 0;
     const int F = Dq >> 4;  // float4 per lane and row tile (= S / 4)
     const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
     const bool qv = wave_live && qb + m < B;
-    const int ntile = min(kGemmTiles, (nlist - blockIdx.y * 16 * kGemmTiles + 15) / 16);
+    const int ntile = min(kGemmTiles, (nlist - by * 16 * kGemmTiles + 15) / 16);
     auto store = [&](int n0, const f4 (&acc4)[4]) {
         // matrix-core results: wait states before the first VALU read, fenced
         __builtin_amdgcn_sched_barrier(0);
@@ -806,7 +814,7 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
         // operands stay in registers for all tiles
         __shared__ float4 s_b[kGemmTiles * 8 * kWave];
         const float4* cb = reinterpret_cast<const float4*>(cmt32) +
-                           (size_t)(blockIdx.y * kGemmTiles) * F * kWave;
+                           (size_t)(by * kGemmTiles) * F * kWave;
         for (int i = threadIdx.x; i < ntile * F * kWave; i += blockDim.x) s_b[i] = cb[i];
         const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         float4 av[8];
@@ -840,14 +848,14 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
                 acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, av[j].z, acc4[2], 0, 0, 0);
                 acc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].w, av[j].w, acc4[3], 0, 0, 0);
             }
-            store_t(blockIdx.y * 16 * kGemmTiles + t * 16, acc4);
+            store_t(by * 16 * kGemmTiles + t * 16, acc4);
         }
         return;
     }
     if (!wave_live) return;
 #pragma unroll 1
     for (int t = 0; t < kGemmTiles; ++t) {
-        const int n0 = blockIdx.y * 16 * kGemmTiles + t * 16;
+        const int n0 = by * 16 * kGemmTiles + t * 16;
         if (n0 >= nlist) break;
         const bool cv = n0 + m < nlist;
         const float4* ct = reinterpret_cast<const float4*>(cmt32) + (size_t)(n0 >> 4) * F * kWave +
