@@ -30,6 +30,9 @@ Afterwards (untimed):
 """
 import os
 
+# The CPUs this process may use, read before an OpenMP runtime binds its initial thread to one
+# place (after that, sched_getaffinity of the main thread names that place only).
+AFFINITY_CPUS = len(os.sched_getaffinity(0))
 # OpenMP reads its placement once, when the runtime loads (torch or the oracle library).
 os.environ.setdefault("OMP_PROC_BIND", "spread")
 os.environ.setdefault("OMP_PLACES", "cores")
@@ -72,7 +75,7 @@ def cpu_threads() -> int:
     env = os.environ.get("OMP_NUM_THREADS", "")
     if env.isdigit() and int(env) > 0:
         return int(env)
-    return len(os.sched_getaffinity(0))
+    return AFFINITY_CPUS
 
 
 # BASELINE.json configs; `check` / `cpu` are the default oracle-check and CPU-baseline samples.
@@ -310,8 +313,8 @@ def measure(cfg_id, cfg, args, dev, primary=True):
                "sample": f"first {nc} of {B} queries, nprobe={nprobe}, same probes as the GPU; warmup 1 + 3 "
                          f"rounds (std {statistics.pstdev(rounds):.1f} QPS); {threads} OpenMP threads "
                          f"(OMP_PROC_BIND={os.environ.get('OMP_PROC_BIND')}, OMP_PLACES={os.environ.get('OMP_PLACES')}) "
-                         f"of {os.cpu_count()} online CPUs, {len(os.sched_getaffinity(0))} in this process's "
-                         f"affinity; CPU: {cpu_model()}; FP32 ids identical to the GPU's exact ids on "
+                         f"of {os.cpu_count()} online CPUs, {AFFINITY_CPUS} in this process's "
+                         f"affinity at start; CPU: {cpu_model()}; FP32 ids identical to the GPU's exact ids on "
                          f"{f32_same}/{nc} queries",
                "online_cpus": os.cpu_count(), "cpu_model": cpu_model()}
         if cfg_id in FLOAT_CONFIGS:
