@@ -104,3 +104,28 @@ def test_host_rows_is_zero_for_a_device_base(dev):
     b.ix.search(_q(xq.numpy(), dev), 8, mode=2, k=10, route=2, host_rows_buf=hr)
     torch.cuda.synchronize()
     assert int(hr[0]) == 0
+
+
+def test_fine_tau_long_candidate_lists(dev):
+    """Rows nearly equidistant from every query: the lower bounds let almost every probed row
+    through, so the candidate lists run past 256 slots (the fine threshold's per-lane top-16
+    path for K <= 16, its sorted list for K = 20) while staying within their capacity."""
+    rng = np.random.default_rng(97)
+    D, N, nlist = 32, 1800, 16
+    u = rng.standard_normal((N, D))
+    u /= np.linalg.norm(u, axis=1, keepdims=True)
+    xb = (100.0 * u * (1.0 + 1e-3 * rng.standard_normal((N, 1)))).astype(np.float32)
+    xq = (0.01 * rng.standard_normal((8, D))).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), nlist, dev, xb_placement="host", max_batch=64)
+    try:
+        assert b.ix.fine_codes is not None
+        for K in (1, 10, 16, 20):
+            _, rd, ri = oracle_search(b, xq, nlist, K)
+            st = torch.zeros(4, dtype=torch.int64, device=dev)
+            d, i, _ = b.ix.search(_q(xq, dev), nlist, mode=2, k=K, ub_seed=1, stats_buf=st, route=2)
+            torch.cuda.synchronize()
+            assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"long lists K={K}")
+            assert int(st[2]) > 256 * len(xq), int(st[2])  # survivors: lists past 256 slots
+    finally:
+        torch.cuda.synchronize()
+        b.ix.storage._host_buf.free()

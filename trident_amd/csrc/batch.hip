@@ -279,6 +279,64 @@ __global__ __launch_bounds__(256) void fine_tau_kernel(BatchArgs a, int B) {
     const int cnt = a.cand_cnt[q];
     if (cnt <= 0 || cnt > a.cap) return;
     const uint64_t* ck = a.cand_key + (size_t)q * a.cap;
+    if (cnt <= 4 * kWave) {
+        // Up to 256 slots: the K-th smallest ub by bisection on its float32 bits (the ub are
+        // non-negative, so their bit patterns order as their values; 0xffffffff marks an empty
+        // register): the smallest x with count(ub <= x) >= K, 32 halvings of [0, 2^32 - 1].
+        uint32_t v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int sl = i * kWave + lane;
+            v[i] = sl < cnt ? __float_as_uint(fine_ub_of(ck[sl])) : 0xffffffffu;
+        }
+        if (cnt < a.K) return;  // fewer than K rows: tau stays
+        uint32_t lo = 0u, hi = 0xfffffffeu;
+        while (lo < hi) {
+            const uint32_t mid = lo + ((hi - lo) >> 1);
+            int n = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) n += __popcll(__ballot(v[i] <= mid));
+            if (n >= a.K) hi = mid;
+            else lo = mid + 1u;
+        }
+        if (lane == 0) a.tau[q] = fmin(a.tau[q], (double)__uint_as_float(lo));
+        return;
+    }
+    if (a.K <= 16) {
+        // A long list (a query whose seeding threshold was loose): each lane keeps the 16
+        // smallest ub of its slots (sorted, in registers; the overall K-th smallest is among
+        // the lanes' K smallest), then the same bisection over those 64 x 16 values.
+        uint32_t v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = 0xffffffffu;
+        for (int s0 = 0; s0 < cnt; s0 += 4 * kWave) {
+            uint32_t x4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int sl = s0 + u * kWave + lane;
+                x4[u] = sl < cnt ? __float_as_uint(fine_ub_of(ck[sl])) : 0xffffffffu;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t x = x4[u];
+                if (__ballot(x < v[15]) == 0ull) continue;
+#pragma unroll
+                for (int i = 15; i > 0; --i) v[i] = x < v[i - 1] ? v[i - 1] : (x < v[i] ? x : v[i]);
+                v[0] = x < v[0] ? x : v[0];
+            }
+        }
+        uint32_t lo = 0u, hi = 0xfffffffeu;
+        while (lo < hi) {
+            const uint32_t mid = lo + ((hi - lo) >> 1);
+            int n = 0;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) n += __popcll(__ballot(v[i] <= mid));
+            if (n >= a.K) hi = mid;
+            else lo = mid + 1u;
+        }
+        if (lane == 0) a.tau[q] = fmin(a.tau[q], (double)__uint_as_float(lo));
+        return;
+    }
     WaveList<KP> L;
     L.init();
     for (int s0 = 0; s0 < cnt; s0 += kWave) {
