@@ -588,10 +588,20 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                              st>>>(xq, B, ix->D, Dq, w.qt32, w.qn32);
         if ((rc = check_launch("pad_queries_kernel"))) return rc;
         float* a32 = reinterpret_cast<float*>(w.cd64);  // [B, nlist] approximations
-        const int64_t ncg = (ix->nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles);
-        coarse_gemm_kernel<<<(unsigned)(8 * ((B + 63) / 64) * ((ncg + 7) / 8)), kBlock, 0, st>>>(w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq,
-                                              a32);
-        if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
+        if (Dq <= 128) {
+            const int64_t nst = ((ix->nlist + 15) / 16 + kStageTiles - 1) / kStageTiles;
+            const int64_t spx = (nst + 7) / 8, nqb = (B + 63) / 64;
+            const int64_t want = std::min<int64_t>(spx, std::max<int64_t>(1, kStreamBlocks / (8 * nqb)));
+            const int64_t run_stages = (spx + want - 1) / want, nrun = (spx + run_stages - 1) / run_stages;
+            coarse_gemm_stream_kernel<<<(unsigned)(8 * nqb * nrun), kBlock, 0, st>>>(
+                w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq, (int)run_stages, a32);
+            if ((rc = check_launch("coarse_gemm_stream_kernel"))) return rc;
+        } else {
+            const int64_t ncg = (ix->nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles);
+            coarse_gemm_kernel<<<(unsigned)(8 * ((B + 63) / 64) * ((ncg + 7) / 8)), kBlock, 0, st>>>(
+                w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq, a32);
+            if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
+        }
         const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
         const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= 2048 ? 32 : ix->nlist <= kBandMaxNlist ? 64 : 0;
 #define TRIDENT_BAND_LAUNCH(KPV, VV, SS)                                                         \

@@ -741,9 +741,9 @@ __global__ __launch_bounds__(256) void pad_centroids_kernel(const float* __restr
 // One-dimensional grid of 8 * ceil(B / 64) * ceil(ncg / 8) blocks (ncg = ceil(nlist / (16
 // kGemmTiles)) centroid groups), block 256.  Blocks are dealt to the XCDs round-robin, so block
 // b runs on XCD b % 8: XCD x takes centroid groups [x cpx, (x + 1) cpx) (cpx = ceil(ncg / 8)) for
-// every query block, and its share of the centroid tiles (1 MiB at nlist 16,384) stays in its
-// L2.  Each wave 16 queries (one query tile), all four waves the same kGemmTiles centroid tiles
-// in the same order.  v_mfma_f32_16x16x4f32 with query
+// every query block, and its share of the centroid tiles stays in its L2.  Used for Dq > 128
+// (coarse_gemm_stream_kernel takes Dq <= 128).  Each wave 16 queries (one query tile), all four
+// waves the same kGemmTiles centroid tiles in the same order.  v_mfma_f32_16x16x4f32 with query
 // rows as A (16 x 4) and centroids as B (4 x 16), operands straight from the tile layouts: a
 // chunk of 32 k-steps is 8 + 8 coalesced float4 loads, issued whole before its 32 MFMAs; steps
 // past S are zero (clamped loads, no branch among the MFMAs).
@@ -763,13 +763,12 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
     const int bx = local / cpx, by = xcd * cpx + (local - (local / cpx) * cpx);
     if (by >= ncg || bx * 64 >= B) return;  // the whole block
     const int qb0 = bx * 64 + wid * 16;
-    const bool wave_live = qb0 < B;  // waves past the last query still help with the LDS copy
+    const bool wave_live = qb0 < B;
     const int qtile = wave_live ? qb0 / 16 : 0;
     const int qb = wave_live ? qb0 : 0;
     const int F = Dq >> 4;  // float4 per lane and row tile (= S / 4)
     const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
     const bool qv = wave_live && qb + m < B;
-    const int ntile = min(kGemmTiles, (nlist - by * 16 * kGemmTiles + 15) / 16);
     auto store = [&](int n0, const f4 (&acc4)[4]) {
         // matrix-core results: wait states before the first VALU read, fenced
         __builtin_amdgcn_sched_barrier(0);
@@ -786,72 +785,6 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
             }
         }
     };
-    // centroids as A and queries as B: lane (m, g) then holds centroids n0 + 4 g .. + 3 of
-    // query qb + m, one 16-byte store (16-byte aligned when nlist % 4 == 0)
-    auto store_t = [&](int n0, const f4 (&acc4)[4]) {
-        __builtin_amdgcn_sched_barrier(0);
-        asm volatile("s_nop 7\n\ts_nop 7");
-        __builtin_amdgcn_sched_barrier(0);
-        const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-        const int q = qb + m, c0 = n0 + 4 * g;
-        if (q >= B) return;
-        const float nq = qn32[q];
-        float* dst = a32 + (size_t)q * nlist + c0;
-        if ((nlist & 3) == 0 && c0 + 4 <= nlist) {
-            const float4 nc = *reinterpret_cast<const float4*>(cn32 + c0);
-            *reinterpret_cast<float4*>(dst) =
-                make_float4(fmaf(-2.0f, acc[0], nq + nc.x), fmaf(-2.0f, acc[1], nq + nc.y),
-                            fmaf(-2.0f, acc[2], nq + nc.z), fmaf(-2.0f, acc[3], nq + nc.w));
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (c0 + i < nlist) dst[i] = fmaf(-2.0f, acc[i], nq + cn32[c0 + i]);
-        }
-    };
-    if (F <= 8) {
-        // Dq <= 128: the block's kGemmTiles centroid tiles are copied to LDS once (one
-        // contiguous run of the tile layout) and shared by the four waves; each wave's query
-        // operands stay in registers for all tiles
-        __shared__ float4 s_b[kGemmTiles * 8 * kWave];
-        const float4* cb = reinterpret_cast<const float4*>(cmt32) +
-                           (size_t)(by * kGemmTiles) * F * kWave;
-        for (int i = threadIdx.x; i < ntile * F * kWave; i += blockDim.x) s_b[i] = cb[i];
-        const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float4 av[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) av[j] = qt[(size_t)(j < F ? j : 0) * kWave];
-        if (F < 8) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (j >= F) av[j] = z4;
-        }
-        if (qb + 16 > B && !qv) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) av[j] = z4;
-        }
-        __syncthreads();
-        if (!wave_live) return;  // after the barrier
-#pragma unroll 1
-        for (int t = 0; t < ntile; ++t) {
-            float4 bv[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) bv[j] = s_b[(t * F + (j < F ? j : 0)) * kWave + lane];
-            f4 acc4[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-            // consecutive MFMAs go to different accumulators (k-step 4 j + u -> chain u);
-            // centroids are the A operand, queries the B operand
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {  // av[j] is zero for j >= F
-                acc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].x, av[j].x, acc4[0], 0, 0, 0);
-                acc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].y, av[j].y, acc4[1], 0, 0, 0);
-                acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, av[j].z, acc4[2], 0, 0, 0);
-                acc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].w, av[j].w, acc4[3], 0, 0, 0);
-            }
-            store_t(by * 16 * kGemmTiles + t * 16, acc4);
-        }
-        return;
-    }
     if (!wave_live) return;
 #pragma unroll 1
     for (int t = 0; t < kGemmTiles; ++t) {
@@ -887,6 +820,132 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
         }
         store(n0, acc4);
     }
+}
+
+// Dq <= 128: the coarse pass with a block's query tiles kept for a run of centroid stages.
+// One-dimensional grid of 8 * ceil(B / 64) * nrun blocks: block b runs on XCD x = b % 8 and
+// takes query block bx and run r of XCD x's share of the stages (kStageTiles 16-centroid tiles
+// each; XCD x owns stages [x spx, (x + 1) spx), split into nrun runs of run_stages), so its
+// centroid tiles stay in its L2.  The four waves' query operands stay in registers for the
+// whole run; each stage's tiles are fetched into registers while the waves compute the
+// previous stage from LDS, then written to the other LDS buffer.
+__global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
+                                                                 const float* __restrict__ qn32,
+                                                                 int B,
+                                                                 const float* __restrict__ cmt32,
+                                                                 const float* __restrict__ cn32,
+                                                                 int nlist, int Dq,
+                                                                 int run_stages,
+                                                                 float* __restrict__ a32) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int PER_MAX = kStageTiles * 8 * kWave;  // float4 of a stage at Dq = 128
+    constexpr int PT = PER_MAX / kBlock;              // float4 each thread moves per stage
+    __shared__ float4 s_b[2][PER_MAX];
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int m = lane & 15, g = lane >> 4;
+    const int F = Dq >> 4;  // float4 per lane and row tile
+    const int ntl_all = (nlist + 15) / 16;
+    const int nst = (ntl_all + kStageTiles - 1) / kStageTiles, spx = (nst + 7) >> 3;
+    const int nrun = (spx + run_stages - 1) / run_stages;
+    const int xcd = (int)(blockIdx.x & 7), local = (int)(blockIdx.x >> 3);
+    const int bx = local / nrun, run = local - bx * nrun;
+    const int s_beg = xcd * spx + run * run_stages;
+    const int s_end = min(min(s_beg + run_stages, (xcd + 1) * spx), nst);
+    if (s_beg >= s_end || bx * 64 >= B) return;  // the whole block
+    const int qb0 = bx * 64 + wid * 16;
+    const bool wave_live = qb0 < B;  // waves past the last query still load and wait
+    const int qtile = wave_live ? qb0 / 16 : 0;
+    const int qb = wave_live ? qb0 : 0;
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float4 av[8];
+    {
+        const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            // steps past Dq are zero (F is wave-uniform); rows past B are never stored
+            if (j < F) av[j] = qt[(size_t)j * kWave];
+            else av[j] = z4;
+        }
+    }
+    const float4* cb = reinterpret_cast<const float4*>(cmt32);
+    // thread i moves float4s i, i + 256, ... of a stage's contiguous run (zero past nlist)
+    float4 r0, r1, r2, r3;
+    static_assert(PT == 4, "four float4 per thread and stage");
+#define TRIDENT_FETCH(st_)                                                                       \
+    {                                                                                           \
+        const int t0_ = (st_) * kStageTiles, n_ = min(kStageTiles, ntl_all - t0_) * F * kWave;  \
+        const float4* p_ = cb + (size_t)t0_ * F * kWave; /* element 0 exists */                  \
+        const int i_ = (int)threadIdx.x;                                                         \
+        /* slots past the stage's tiles are never read: they load element 0 again */            \
+        r0 = p_[i_ < n_ ? i_ : 0];                                                               \
+        r1 = p_[i_ + kBlock < n_ ? i_ + kBlock : 0];                                             \
+        r2 = p_[i_ + 2 * kBlock < n_ ? i_ + 2 * kBlock : 0];                                     \
+        r3 = p_[i_ + 3 * kBlock < n_ ? i_ + 3 * kBlock : 0];                                     \
+    }
+#define TRIDENT_PUT(b_)                                                                          \
+    {                                                                                           \
+        s_b[b_][threadIdx.x] = r0;                                                               \
+        s_b[b_][threadIdx.x + kBlock] = r1;                                                      \
+        s_b[b_][threadIdx.x + 2 * kBlock] = r2;                                                  \
+        s_b[b_][threadIdx.x + 3 * kBlock] = r3;                                                  \
+    }
+    TRIDENT_FETCH(s_beg)
+    TRIDENT_PUT(0)
+    __syncthreads();
+    for (int st = s_beg; st < s_end; ++st) {
+        const int buf = (st - s_beg) & 1;
+        if (st + 1 < s_end) TRIDENT_FETCH(st + 1)
+        if (wave_live) {
+            const int t0 = st * kStageTiles, ntl = min(kStageTiles, ntl_all - t0);
+#pragma unroll 1
+            for (int t = 0; t < ntl; ++t) {
+                float4 bv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    if (j < F) bv[j] = s_b[buf][(t * F + j) * kWave + lane];
+                    else bv[j] = z4;
+                }
+                f4 acc4[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+                // centroids are the A operand, queries the B operand; consecutive MFMAs go to
+                // different accumulators (k-step 4 j + u -> chain u)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    acc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].x, av[j].x, acc4[0], 0, 0, 0);
+                    acc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].y, av[j].y, acc4[1], 0, 0, 0);
+                    acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, av[j].z, acc4[2], 0, 0, 0);
+                    acc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].w, av[j].w, acc4[3], 0, 0, 0);
+                }
+                // matrix-core results: wait states before the first VALU read, fenced
+                __builtin_amdgcn_sched_barrier(0);
+                asm volatile("s_nop 7\n\ts_nop 7");
+                __builtin_amdgcn_sched_barrier(0);
+                const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+                // lane (m, g) holds centroids n0 + 4 g .. + 3 of query qb + m
+                const int q = qb + m, c0 = 16 * (t0 + t) + 4 * g;
+                if (q < B) {
+                    const float nq = qn32[q];
+                    float* dst = a32 + (size_t)q * nlist + c0;
+                    if ((nlist & 3) == 0 && c0 + 4 <= nlist) {
+                        const float4 nc = *reinterpret_cast<const float4*>(cn32 + c0);
+                        *reinterpret_cast<float4*>(dst) =
+                            make_float4(fmaf(-2.0f, acc[0], nq + nc.x), fmaf(-2.0f, acc[1], nq + nc.y),
+                                        fmaf(-2.0f, acc[2], nq + nc.z), fmaf(-2.0f, acc[3], nq + nc.w));
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (c0 + i < nlist) dst[i] = fmaf(-2.0f, acc[i], nq + cn32[c0 + i]);
+                    }
+                }
+            }
+        }
+        if (st + 1 < s_end) TRIDENT_PUT(buf ^ 1)
+        __syncthreads();
+    }
+#undef TRIDENT_FETCH
+#undef TRIDENT_PUT
 }
 
 // One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM, each lane's V

@@ -242,6 +242,15 @@ __global__ void select_band_kernel(const float* __restrict__ a32, const double* 
                                    int32_t* __restrict__ out2_cids,
                                    float* __restrict__ out2_dqcs, int ld2);
 constexpr int kGemmTiles = 4;  // coarse_gemm_kernel: 16-centroid tiles per wave
+// coarse_gemm_stream_kernel (Dq <= 128): 16-centroid tiles per stage; the run of stages per
+// block is the longest that still gives a grid of about kStreamBlocks blocks
+constexpr int kStageTiles = 2;
+constexpr int kStreamBlocks = 5120;
+__global__ void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
+                                          const float* __restrict__ qn32, int B,
+                                          const float* __restrict__ cmt32,
+                                          const float* __restrict__ cn32, int nlist, int Dq,
+                                          int run_stages, float* __restrict__ a32);
 // band front end: up to 64 x 64 approximations per lane in registers; past that each lane
 // streams its share of the row and keeps its 8 smallest
 constexpr int kBandMaxNlist = 4096;
