@@ -295,37 +295,78 @@ __device__ __forceinline__ bool list_offer(WaveList<KP>& L, int K, uint64_t ck, 
     return true;
 }
 
-constexpr int kStageCh = 32;  // dims per Stage Z staging chunk
+// Stage Z staging area per wave: kStageCh x (kWave + 1) floats, used by refine_rows as
+// kStageRows rows of kStageDims + 1 floats
+constexpr int kStageCh = 32;
+constexpr int kStageRows = 16, kStageDims = 128;
+static_assert(kStageRows * (kStageDims + 1) <= kStageCh * (kWave + 1), "staging area");
 
-// Canonical float64 distance of the first `nq` (>= 1) queued survivors (lane i <- survivor i),
-// in dimension order: rows are staged through LDS 32 dims at a time with 128-byte coalesced row
-// loads, every load of a chunk (64 rows, two per load) issued before the chunk is staged, so a
-// chunk costs one memory round trip (HBM, or PCIe for a base in mapped host memory).
+// Canonical float64 distance of the first `nq` (1 .. 64) queued survivors (lane i <- survivor
+// i), in dimension order.  Rows move in groups of 16, 128 dims (512 contiguous bytes) of each
+// row at a time, every load of a group issued before the first is used, and are staged in LDS
+// (row stride 129 floats: the lanes' reads of their rows fall in distinct banks).  Whole
+// 512-byte runs in flight matter for a base in mapped host memory: random rows cross PCIe at
+// ~51 GB/s read this way against ~40 GB/s as 128-byte pieces one 32-dim chunk at a time.
 __device__ __forceinline__ double refine_rows(const float* __restrict__ xb, int D,
-                                                  const int32_t* q_spos, int nq,
-                                                  float (*stage)[kWave + 1],
-                                                  const double* s_q64) {
+                                              const int32_t* q_spos, int nq,
+                                              float (*stage)[kWave + 1],
+                                              const double* s_q64) {
     const int lane = lane_id();
-    double acc = 0.0;
     const int half = lane >> 5, kk = lane & 31;
-    for (int d0 = 0; d0 < D; d0 += kStageCh) {
-        const int ch = min(kStageCh, D - d0);
-        float v[kWave / 2];
+    float* st = &stage[0][0];
+    constexpr int RS = kStageDims + 1;
+    const bool vec4 = (D & 3) == 0 && (reinterpret_cast<uintptr_t>(xb) & 15) == 0;
+    double acc = 0.0;
+    for (int g0 = 0; g0 < nq; g0 += kStageRows) {
+        const int ng = min(kStageRows, nq - g0);
+        const bool mine = lane >= g0 && lane < g0 + ng;
+        for (int d0 = 0; d0 < D; d0 += kStageDims) {
+            const int ch = min(kStageDims, D - d0);
+            if (vec4) {
+                // lane (half, kk): float4 kk of rows g0 + 2 k + half; rows past the group and
+                // float4s past the chunk reload the last ones (never staged)
+                const int c4 = min(kk, (ch >> 2) - 1);
+                float4 v[kStageRows / 2];
 #pragma unroll
-        for (int k = 0; k < kWave / 2; ++k) {
-            const int r = min(2 * k + half, nq - 1);  // rows past nq reload the last one
-            v[k] = xb[(size_t)q_spos[r] * D + d0 + min(kk, ch - 1)];
-        }
+                for (int k = 0; k < kStageRows / 2; ++k) {
+                    const int r = g0 + min(2 * k + half, ng - 1);
+                    v[k] = *reinterpret_cast<const float4*>(xb + (size_t)q_spos[r] * D + d0 + 4 * c4);
+                }
+                if (4 * kk < ch) {
 #pragma unroll
-        for (int k = 0; k < kWave / 2; ++k) stage[kk][2 * k + half] = v[k];
-        wave_sync();
-        if (lane < nq) {
-            for (int k = 0; k < ch; ++k) {
-                const double t = (double)stage[k][lane] - s_q64[d0 + k];
-                acc = fma(t, t, acc);
+                    for (int k = 0; k < kStageRows / 2; ++k) {
+                        float* dst = st + (2 * k + half) * RS + 4 * kk;
+                        dst[0] = v[k].x;
+                        dst[1] = v[k].y;
+                        dst[2] = v[k].z;
+                        dst[3] = v[k].w;
+                    }
+                }
+            } else {
+                // any D: lane (half, kk) holds dims kk, kk + 32, kk + 64, kk + 96 of its rows
+                float v[kStageRows / 2][4];
+#pragma unroll
+                for (int k = 0; k < kStageRows / 2; ++k) {
+                    const float* xr = xb + (size_t)q_spos[g0 + min(2 * k + half, ng - 1)] * D + d0;
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) v[k][m] = xr[min(kk + 32 * m, ch - 1)];
+                }
+#pragma unroll
+                for (int k = 0; k < kStageRows / 2; ++k)
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+                        if (kk + 32 * m < ch) st[(2 * k + half) * RS + kk + 32 * m] = v[k][m];
             }
+            wave_sync();
+            if (mine) {
+                const float* sr = st + (lane - g0) * RS;
+                for (int k = 0; k < ch; ++k) {
+                    const double t = (double)sr[k] - s_q64[d0 + k];
+                    acc = fma(t, t, acc);
+                }
+            }
+            wave_sync();
         }
-        wave_sync();
     }
     return acc;
 }
