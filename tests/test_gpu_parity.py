@@ -99,6 +99,22 @@ def test_band_front_end_far_from_origin(dev):
         _check_probes(b, xq, dev, nprobe)
 
 
+@pytest.mark.parametrize("offset", [3.0e3, 3.0e4])
+def test_band_front_end_stream_wide_band(dev, offset):
+    """Past 4096 centroids each wave filters its row through an LDS list tightened by
+    bisection.  Offsets from the origin widen the error band: to a few hundred centroids (the
+    band refined from the list 64 at a time) and to nearly all of them (the list cannot shrink,
+    the band is taken from the row again); the probes must still be the oracle's."""
+    nlist = 4500
+    xb, xq = datagen.cfg1(N=3 * nlist, D=64, B=48, n_centers=nlist, seed=45)
+    b = build_index(xb + offset, nlist, dev, max_batch=64, max_nprobe=128)
+    xq = (xq + offset).numpy()
+    dup = np.repeat(xq[:4], 2, axis=0)
+    xq = np.concatenate([xq, dup]).astype(np.float32)
+    for nprobe in (5, 64, 128):
+        _check_probes(b, xq, dev, nprobe)
+
+
 def test_coarse_probe_selectors_all_widths(dev):
     """nprobe <= 64 and <= 128 use the one-wave register selector, larger ones the block radix
     select; all must give the oracle's (d, cid) order, including at the 64 / 128 edges."""

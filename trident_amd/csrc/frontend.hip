@@ -948,14 +948,22 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
 #undef TRIDENT_PUT
 }
 
-// One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM, each lane's V
-// smallest of its nlist / 64 (any nlist >= 64 V).  T comes from a bisection on the register
-// values (count(a <= hi) >= nprobe is kept invariant: counted over a subset of the row, it
-// never exceeds the row's count), and every centroid of the band a <= T + 2E gets its
-// canonical float64 distance (t = q_d - c_d, acc = fma(t, t, acc) in dimension order -- the
-// oracle's chain).  A band of <= 128 (the usual case: a few more than nprobe) is ranked by
-// counting, each entry against all others in (d, cid) order; a wider one streams through the
-// (d, cid) register list 64 centroids at a time.  Outputs as select_probes_wave_kernel.
+// One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM (any nlist), the
+// row streamed through a running filter.  T is any value with count(a <= T) >= nprobe over the
+// row: then every centroid among the nprobe nearest (by the exact distance) lies in the band
+// a <= T + 2E, and every centroid of the band gets its canonical float64 distance (t = q_d -
+// c_d, acc = fma(t, t, acc) in dimension order -- the oracle's chain).  Without STREAM, T comes
+// from a bisection on the register values.  STREAM: the wave appends each approximation a <=
+// cut = T + 2E of the row to an LDS list (ballot + mbcnt); T starts at +inf and, whenever the
+// list fills, becomes the result of a bisection over the list (count(a <= T) >= nprobe over
+// the list, so over the row), and entries above the new cut are dropped.  Values dropped or
+// never listed lie above every later cut, so the list holds every approximation <= the final
+// cut and counts over it equal the row's below that cut: the final bisection runs on the list.
+// A list that cannot shrink below half its capacity (a band of more than ~512 centroids) ends
+// the filter: the band is then taken from the row again with cut = T + 2E for the T reached.
+// A band of <= 128 (the usual case: a few more than nprobe) is ranked by counting, each entry
+// against all others in (d, cid) order; a wider one streams through the (d, cid) register list
+// 64 centroids at a time.  Outputs as select_probes_wave_kernel.
 template <int KP, int V, bool STREAM>
 __global__ __launch_bounds__(256) void select_band_kernel(
     const float* __restrict__ a32, const double* __restrict__ xq64, const float* __restrict__ cm32,
@@ -963,52 +971,19 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     int Dq, int nprobe,
     int32_t* __restrict__ out_cids, float* __restrict__ out_dqcs, int ld,
     int32_t* __restrict__ out2_cids, float* __restrict__ out2_dqcs, int ld2) {
-    // the band's centroids (up to 8 per lane)
+    // the band's centroids (up to 8 per lane); STREAM: the filter's list (up to 16 per lane),
+    // its centroids in s_band and its approximations in s_lval
     constexpr int kBandMax = 8 * kWave;
-    __shared__ int32_t s_band[kWavesPerBlock][kBandMax];
+    constexpr int kListPer = 16, kListCap = kListPer * kWave;
+    __shared__ int32_t s_band[kWavesPerBlock][STREAM ? kListCap : kBandMax];
+    __shared__ float s_lval[kWavesPerBlock][STREAM ? kListCap : 1];
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int q = blockIdx.x * kWavesPerBlock + wid;
     if (q >= B) return;
     const double* qrow = xq64 + (size_t)q * D;
     const float* arow = a32 + (size_t)q * nlist;
-    float v[V];
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-        const int c = i * kWave + lane;
-        v[i] = !STREAM && c < nlist ? arow[c] : INFINITY;
-    }
-    // STREAM: the lane's V smallest, ascending, with their centroids (vi)
-    int vi[STREAM ? V : 1];
-#pragma unroll
-    for (int i = 0; i < (STREAM ? V : 1); ++i) vi[i] = -1;
-    if constexpr (STREAM) {  // (selects: no NaN here)
-        // eight of the lane's values per round, all loaded before the first insertion
-        for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
-            float xs[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = c0 + u * kWave + lane;
-                xs[u] = c < nlist ? arow[c] : INFINITY;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const float x = xs[u];
-                const int cx = c0 + u * kWave + lane;
-                if (x < v[V - 1]) {
-#pragma unroll
-                    for (int i = V - 1; i > 0; --i) {
-                        const bool up = x < v[i - 1], here = x < v[i];
-                        v[i] = up ? v[i - 1] : (here ? x : v[i]);
-                        vi[i] = up ? vi[i - 1] : (here ? cx : vi[i]);
-                    }
-                    const bool here = x < v[0];
-                    v[0] = here ? x : v[0];
-                    vi[0] = here ? cx : vi[0];
-                }
-            }
-        }
-    }
+    int32_t* band = s_band[wid];
     // the error bound E (float64, then rounded up to float32)
     double nq = 0.0;
     for (int d = lane; d < D; d += kWave) nq = fma(qrow[d], qrow[d], nq);
@@ -1019,51 +994,151 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     const double E = (kappa + 0x1p-21) * (nq + cmax2) *
                          (1.0 + 0x1p-10) + 1e-30;
     const float Ef = __double2float_ru(E);
-    // bisection: count(a <= hi) >= nprobe throughout.  hi starts at the largest lane minimum
-    // when every lane holds a value and nprobe <= 64 (then >= 64 values lie at or below it),
-    // else at the largest value; counts come from ballots (no cross-lane shuffles).
-    float lmin = INFINITY, lmax = -INFINITY;
+    // E carries a 2^-10 relative margin, which covers the float64 rounding of this sum
+    auto cut_of = [&](float t) { return __double2float_ru((double)t + 2.0 * E); };
+    // bisection over values held N per lane: count(a <= hi) >= nprobe throughout (hi starts at
+    // hi0, or at the largest value when hi0 is +inf); stops once the count is at most nprobe
+    // + slack or the interval is no wider than Ef.  Counts come from ballots.
+    auto bisect = [&](const float* w, auto n_c, float hi0, int slack) __attribute__((always_inline)) {
+        constexpr int N = decltype(n_c)::value;
+        float lmin = INFINITY, lmax = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-        lmin = fminf(lmin, v[i]);
-        if (v[i] < INFINITY) lmax = fmaxf(lmax, v[i]);
-    }
-    float lo = lmin, hi = lmax, t0 = lmin;
+        for (int i = 0; i < N; ++i) {
+            lmin = fminf(lmin, w[i]);
+            if (w[i] < INFINITY) lmax = fmaxf(lmax, w[i]);
+        }
+        float lo = lmin, hi = lmax;
 #pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-        lo = fminf(lo, __shfl_xor(lo, o, kWave));
-        hi = fmaxf(hi, __shfl_xor(hi, o, kWave));
-        t0 = fmaxf(t0, __shfl_xor(t0, o, kWave));
-    }
-    if (nprobe <= kWave && t0 < INFINITY) hi = t0;
-    // STREAM: every lane holds V values (nlist >= 64 V), so >= 64 V >= nprobe lie at or below
-    // the largest lane's V-th smallest
-    if (STREAM && lmax < INFINITY) {
-        float tv = v[V - 1];
+        for (int o = 1; o < kWave; o <<= 1) {
+            lo = fminf(lo, __shfl_xor(lo, o, kWave));
+            hi = fmaxf(hi, __shfl_xor(hi, o, kWave));
+        }
+        hi = fminf(hi, hi0);
+        for (int it = 0; it < 40 && hi - lo > Ef; ++it) {
+            const float mid = lo + 0.5f * (hi - lo);
+            if (!(mid > lo && mid < hi)) break;
+            int n = 0;
 #pragma unroll
-        for (int o = 1; o < kWave; o <<= 1) tv = fmaxf(tv, __shfl_xor(tv, o, kWave));
-        if (kWave * V >= nprobe) hi = fminf(hi, tv);
-    }
+            for (int i = 0; i < N; ++i) n += __popcll(__ballot(w[i] <= mid));
+            if (n >= nprobe) {
+                hi = mid;
+                if (n <= nprobe + slack) break;
+            } else {
+                lo = mid;
+            }
+        }
+        return hi;
+    };
+    float v[STREAM ? 1 : V];
     auto count_le = [&](float x) {
         int n = 0;
 #pragma unroll
-        for (int i = 0; i < V; ++i) n += __popcll(__ballot(v[i] <= x));
+        for (int i = 0; i < (STREAM ? 1 : V); ++i) n += __popcll(__ballot(v[i] <= x));
         return n;
     };
-    for (int it = 0; it < 40 && hi - lo > Ef; ++it) {
-        const float mid = lo + 0.5f * (hi - lo);
-        if (!(mid > lo && mid < hi)) break;
-        const int n = count_le(mid);
-        if (n >= nprobe) {
-            hi = mid;
-            if (n <= nprobe + 2) break;
-        } else {
-            lo = mid;
+    float thr;
+    int mband = nlist + 1, nb_stream = 0;
+    bool from_regs = false;
+    if constexpr (STREAM) {
+        float* lval = s_lval[wid];
+        float T = INFINITY, cut = INFINITY;
+        int n = 0;
+        bool open = true;
+        // the list's entries lane + 64 i into registers (+inf past n)
+        auto load_list = [&](float (&w)[kListPer]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < kListPer; ++i) {
+                const int e = i * kWave + lane;
+                w[i] = e < n ? lval[e] : INFINITY;
+            }
+        };
+        // keeps the entries <= c, in list order
+        auto compact = [&](const float (&w)[kListPer], float c) __attribute__((always_inline)) {
+            int32_t id[kListPer];
+#pragma unroll
+            for (int i = 0; i < kListPer; ++i) id[i] = band[min(i * kWave + lane, kListCap - 1)];
+            wave_sync();
+            int m = 0;
+#pragma unroll
+            for (int i = 0; i < kListPer; ++i) {
+                // slots past n are never kept (c may be +inf when E overflows)
+                const bool keep = i * kWave + lane < n && w[i] <= c;
+                const uint64_t mk = __ballot(keep);
+                if (keep) {
+                    lval[m + mask_rank(mk)] = w[i];
+                    band[m + mask_rank(mk)] = id[i];
+                }
+                m += __popcll(mk);
+            }
+            wave_sync();
+            n = m;
+        };
+        // eight of the lane's values per round, all loaded before the first is filtered
+        for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
+            if (n > kListCap - 8 * kWave) {  // the round could overflow the list: tighten T
+                float w[kListPer];
+                wave_sync();
+                load_list(w);
+                T = bisect(w, std::integral_constant<int, kListPer>{}, T, 32);
+                cut = cut_of(T);
+                compact(w, cut);
+                if (n > kListCap - 8 * kWave) {
+                    open = false;
+                    break;
+                }
+            }
+            float xs[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * kWave + lane;
+                xs[u] = c < nlist ? arow[c] : INFINITY;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool take = c0 + u * kWave + lane < nlist && xs[u] <= cut;
+                const uint64_t mk = __ballot(take);
+                if (mk == 0ull) continue;
+                if (take) {
+                    const int at = n + mask_rank(mk);
+                    lval[at] = xs[u];
+                    band[at] = c0 + u * kWave + lane;
+                }
+                n += __popcll(mk);
+            }
         }
+        if (open) {
+            float w[kListPer];
+            wave_sync();
+            load_list(w);
+            const float hi = bisect(w, std::integral_constant<int, kListPer>{}, T, 2);
+            thr = cut_of(hi);
+            compact(w, thr);  // the band, in LDS
+            mband = nb_stream = n;
+            from_regs = true;
+        } else {
+            thr = cut;  // T is valid for the row: the band is taken from the row again
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const int c = i * kWave + lane;
+            v[i] = c < nlist ? arow[c] : INFINITY;
+        }
+        // hi starts at the largest lane minimum when every lane holds a value and nprobe <= 64
+        // (then >= 64 values lie at or below it), else at the largest value
+        float t0 = INFINITY;
+        {
+            float lmin = INFINITY;
+#pragma unroll
+            for (int i = 0; i < V; ++i) lmin = fminf(lmin, v[i]);
+            t0 = lmin;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) t0 = fmaxf(t0, __shfl_xor(t0, o, kWave));
+        }
+        const float hi = bisect(v, std::integral_constant<int, V>{},
+                                nprobe <= kWave && t0 < INFINITY ? t0 : INFINITY, 2);
+        thr = cut_of(hi);
     }
-    // E carries a 2^-10 relative margin, which covers the float64 rounding of this sum
-    const float thr = __double2float_ru((double)hi + 2.0 * E);
-    int32_t* band = s_band[wid];
     auto emit = [&](int rank, uint64_t key, int32_t cid) {
         const float dq = (float)sqrt(dist_of(key));
         out_cids[(size_t)q * ld + rank] = cid;
@@ -1115,28 +1190,12 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         }
         return acc;
     };
-    // The band is compacted from the registers (from_regs) when they hold all of it and it
-    // fits kBandMax: STREAM when every lane's V-th smallest lies above thr (the lanes' lists
-    // then hold every value <= thr), else whenever its count does.  Otherwise, STREAM, it is
-    // compacted from the row in one more pass (eight values per lane loaded per round),
-    // counting past the 128 slots without writing.
-    int mband = nlist + 1, nb_stream = 0;
-    bool from_regs = false;
-    if (thr < INFINITY) {
-        // (not past V = 32 without STREAM: the unrolled compaction would cost a wave per SIMD)
-        const bool regs_hold =
-            STREAM ? __ballot(v[V - 1] <= thr) == 0ull : V <= 32 && count_le(thr) <= kBandMax;
-        if (regs_hold && (!STREAM || kWave * V <= kBandMax)) {
-#pragma unroll
-            for (int i = 0; i < V; ++i) {
-                const bool take = v[i] <= thr;
-                const uint64_t mk = __ballot(take);
-                if (take) band[nb_stream + mask_rank(mk)] = STREAM ? vi[STREAM ? i : 0] : i * kWave + lane;
-                nb_stream += __popcll(mk);
-            }
-            mband = nb_stream;
-            from_regs = true;
-        } else if constexpr (STREAM) {
+    // The band is in LDS (from_regs) when the registers held all of it and it fit kBandMax,
+    // or, STREAM, when the filter's list held it.  Otherwise, STREAM, it is compacted from the
+    // row in one more pass (eight values per lane loaded per round), counting past the 128
+    // slots without writing.
+    if constexpr (STREAM) {
+        if (!from_regs) {
             for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
                 float xs[8];
 #pragma unroll
@@ -1154,6 +1213,19 @@ __global__ __launch_bounds__(256) void select_band_kernel(
                 }
             }
             mband = nb_stream;
+        }
+    } else if (thr < INFINITY) {
+        // (not past V = 32: the unrolled compaction would cost a wave per SIMD)
+        if (V <= 32 && count_le(thr) <= kBandMax) {
+#pragma unroll
+            for (int i = 0; i < V; ++i) {
+                const bool take = v[i] <= thr;
+                const uint64_t mk = __ballot(take);
+                if (take) band[nb_stream + mask_rank(mk)] = i * kWave + lane;
+                nb_stream += __popcll(mk);
+            }
+            mband = nb_stream;
+            from_regs = true;
         } else {
             mband = count_le(thr);
         }
@@ -1162,8 +1234,10 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         // the common case: the band fits two entries per lane.  Compact it, compute the exact
         // distances, and rank every entry by counting the entries before it in (d, cid) order.
         int nb = 0;
-        if (STREAM || from_regs) {
+        if constexpr (STREAM) {
             nb = nb_stream;  // compacted above
+        } else if (from_regs) {
+            nb = nb_stream;
         } else {
 #pragma unroll
             for (int i = 0; i < V; ++i) {
