@@ -111,6 +111,7 @@ struct Workspace {
     int32_t* pair_cids;
     int32_t* pair_qids;
     float* pair_dqcs;
+    int32_t* pair_rank;              // group_pairs past the LDS histogram: arrival ranks
     uint64_t* cand_key;
     int32_t* cand_id;
     int32_t* cand_cnt;
@@ -179,6 +180,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.pair_cids = c.take<int32_t>(B * nprobe);
     w.pair_qids = c.take<int32_t>(B * nprobe);
     w.pair_dqcs = c.take<float>(B * nprobe);
+    w.pair_rank = c.take<int32_t>(B * nprobe);
     w.cand_key = c.take<uint64_t>(B * cap);
     w.cand_id = c.take<int32_t>(B * cap);
     w.cand_cnt = c.take<int32_t>(B);
@@ -691,16 +693,27 @@ int launch_scatter_pairs(const int32_t* probe_cids, const float* probe_dqcs, int
 }
 
 // joint = false: each pass's pairs grouped by cluster in its own array (p1*, p2*), seg_off =
-// [2, nlist + 1] per-pass segment offsets (the per-pair route).  joint = true: one cluster-major
+// [2, nlist + 1] per-pass segment offsets (the per-pair route).  With a rank buffer (B * nprobe)
+// and counters past the LDS histogram, the count keeps each pair's rank in its bin and the
+// scatter needs no atomics.  joint = true: one cluster-major
 // array (p1* and p2* the same array), each cluster's pass-1 pairs before its pass-2 pairs,
 // seg_off rows = cluster starts and pass-2 starts (the batched route).
 int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int B, int nprobe,
                 int p_init, int nlist, int32_t* counts, int32_t* seg_off, int32_t* cursor,
                 int32_t* p1c, int32_t* p1q, float* p1d, int32_t* p2c, int32_t* p2q, float* p2d,
-                bool joint, int32_t* blk_tot, hipStream_t st) {
+                bool joint, int32_t* blk_tot, int32_t* rank, hipStream_t st) {
     int rc = fill(counts, 0, 2 * ((int64_t)nlist + 1), st);
     if (rc) return rc;
-    if ((rc = launch_count_pairs(probe_cids, ld, B, nprobe, p_init, nlist, counts, st))) return rc;
+    const bool ranked = rank && group_lds_bytes(nlist) > 64 * 1024;
+    const int64_t total = (int64_t)B * nprobe;
+    const unsigned gblocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
+    if (ranked) {
+        count_pairs_rank_kernel<<<gblocks, 256, 0, st>>>(probe_cids, ld, B, nprobe, p_init, nlist,
+                                                         counts, rank);
+        if ((rc = check_launch("count_pairs_rank_kernel"))) return rc;
+    } else if ((rc = launch_count_pairs(probe_cids, ld, B, nprobe, p_init, nlist, counts, st))) {
+        return rc;
+    }
     if (joint) {
         // nlist <= 19200 (validate_index), so the block totals fit one block's scan
         const int nblk = (nlist + kBlock - 1) / kBlock;
@@ -712,6 +725,12 @@ int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int 
     } else {
         scan_pairs_kernel<<<2, kBlock, 0, st>>>(counts, nlist, seg_off, cursor);
         if ((rc = check_launch("scan_pairs_kernel"))) return rc;
+    }
+    if (ranked) {
+        scatter_pairs_rank_kernel<<<gblocks, 256, 0, st>>>(probe_cids, probe_dqcs, ld, B, nprobe,
+                                                           p_init, nlist, seg_off, rank, p1c, p1q,
+                                                           p1d, p2c, p2q, p2d);
+        return check_launch("scatter_pairs_rank_kernel");
     }
     return launch_scatter_pairs(probe_cids, probe_dqcs, ld, B, nprobe, p_init, nlist, cursor, p1c,
                                 p1q, p1d, p2c, p2q, p2d, st);
@@ -925,7 +944,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     float* p2d = batched ? p1d : w.pair_dqcs + M1;
     if ((rc = group_pairs(pc, pd, ld, B, nprobe, p_init, ix->nlist, w.counts, w.seg_off, w.cursor,
                           p1c, p1q, pd ? p1d : nullptr, p2c, p2q, pd ? p2d : nullptr, batched, w.blk_tot,
-                          st)))
+                          w.pair_rank, st)))
         return rc;
     if ((rc = mark(TRIDENT_EV_GROUPED))) return rc;
 

@@ -441,6 +441,47 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
     }
 }
 
+// Large nlist with a rank buffer (B * nprobe entries): the count keeps each pair's arrival
+// rank in its bin (the returned counter value), so the scatter places the pair at seg_off[bin]
+// + rank with plain loads -- one global atomic per pair instead of two.
+__global__ void count_pairs_rank_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
+                                        int nprobe, int p_init, int nlist, int32_t* counts,
+                                        int32_t* __restrict__ rank) {
+    const int64_t total = (int64_t)B * nprobe;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int q = (int)(idx / nprobe), p = (int)(idx - (int64_t)q * nprobe);
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
+        rank[idx] = atomicAdd(&counts[(p < p_init ? 0 : (nlist + 1)) + cid], 1);
+    }
+}
+
+__global__ void scatter_pairs_rank_kernel(const int32_t* __restrict__ probe_cids,
+                                          const float* __restrict__ probe_dqcs, int ld, int B,
+                                          int nprobe, int p_init, int nlist,
+                                          const int32_t* __restrict__ seg_off,
+                                          const int32_t* __restrict__ rank,
+                                          int32_t* __restrict__ p1_cids, int32_t* __restrict__ p1_qids,
+                                          float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
+                                          int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs) {
+    const int64_t total = (int64_t)B * nprobe;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int q = (int)(idx / nprobe), p = (int)(idx - (int64_t)q * nprobe);
+        const int cid = probe_cids[(size_t)q * ld + p];
+        if ((unsigned)cid >= (unsigned)nlist) continue;  // invalid caller input: never index
+        const bool first = p < p_init;
+        const int slot = seg_off[(first ? 0 : (nlist + 1)) + cid] + rank[idx];
+        int32_t* oc = first ? p1_cids : p2_cids;
+        int32_t* oq = first ? p1_qids : p2_qids;
+        float* od = first ? p1_dqcs : p2_dqcs;
+        oc[slot] = cid;
+        oq[slot] = q;
+        if (od) od[slot] = probe_dqcs ? probe_dqcs[(size_t)q * ld + p] : 0.0f;
+    }
+}
+
 // One wave per query (nprobe <= KP): the query's float64 centroid distances go through a
 // register list of the KP best (d, cid) entries, sorted across lanes.  Each chunk of 1024 keys
 // (16 per lane) is first cut at T0 = the largest over lanes of each lane's r-th smallest entry,

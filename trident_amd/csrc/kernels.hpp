@@ -263,6 +263,18 @@ constexpr int kPrepQB = 4;         // queries per wave of prep_queries_kernel
 // Dynamic LDS bytes of the LDS grouping kernels; they are used while this is <= 64 KiB.
 inline size_t group_lds_bytes(int nlist) { return (size_t)2 * (nlist + 1) * sizeof(int32_t); }
 
+__global__ void count_pairs_rank_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
+                                        int nprobe, int p_init, int nlist, int32_t* counts,
+                                        int32_t* __restrict__ rank);
+__global__ void scatter_pairs_rank_kernel(const int32_t* __restrict__ probe_cids,
+                                          const float* __restrict__ probe_dqcs, int ld, int B,
+                                          int nprobe, int p_init, int nlist,
+                                          const int32_t* __restrict__ seg_off,
+                                          const int32_t* __restrict__ rank,
+                                          int32_t* __restrict__ p1_cids, int32_t* __restrict__ p1_qids,
+                                          float* __restrict__ p1_dqcs, int32_t* __restrict__ p2_cids,
+                                          int32_t* __restrict__ p2_qids, float* __restrict__ p2_dqcs);
+
 __global__ void count_pairs_lds_kernel(const int32_t* __restrict__ probe_cids, int ld, int B,
                                        int nprobe, int p_init, int nlist, int32_t* counts);
 
