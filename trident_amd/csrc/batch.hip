@@ -214,12 +214,12 @@ __device__ inline void fine_row_bounds(const BatchArgs& a, const double* q64, do
     const float4 qp = reinterpret_cast<const float4*>(a.fine_qp)[pos];  // offset, step, rho
     const double o = (double)qp.x, st = (double)qp.y;
     double s = 0.0;
-    for (int g0 = 0; g0 < D_pad / 8; g0 += 4) {  // 32 dims, four 16-byte loads in flight
-        uint4 w[4];
+    for (int g0 = 0; g0 < D_pad / 8; g0 += 16) {  // 128 dims, sixteen 16-byte loads in flight
+        uint4 w[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = g0 + u < D_pad / 8 ? rc[g0 + u] : make_uint4(0, 0, 0, 0);
+        for (int u = 0; u < 16; ++u) w[u] = g0 + u < D_pad / 8 ? rc[g0 + u] : make_uint4(0, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 16; ++u) {
             if (g0 + u >= D_pad / 8) break;
             const uint32_t w4[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
 #pragma unroll
