@@ -942,17 +942,15 @@ template <int KS, int M>
 __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
     // The code buffers double as the end-of-unit list exchange (after a barrier).
     constexpr int BV = block_vectors(KS);
-    // code buffers: a ring of four 64-vector blocks (three in flight while one is scanned: the
-    // units are small, so a block's scan is short and one block in flight left each waiting on
-    // its load) up to D_pad 128, two past it
-    constexpr int NBC = BV == 64 ? (KS <= 2 ? 4 : 2) : kWideAhead + 1;
+    constexpr int NBC = BV == 64 ? 2 : kWideAhead + 1;  // code buffers
     constexpr int kCodeU4 = NBC * KS * 4 * BV, kUblU4 = kWavesPerBlock * kWaveQ * kWave / 4;
     __shared__ uint4 s_big[kCodeU4 > kUblU4 ? kCodeU4 : kUblU4];
     uint4(*s_codes)[KS * 4 * BV] = reinterpret_cast<uint4(*)[KS * 4 * BV]>(s_big);
     float(*s_ubl)[kWaveQ * kWave] = reinterpret_cast<float(*)[kWaveQ * kWave]>(s_big);
-    // Row scalars: in the codes' ring, or (wide layout) a ring of 8 that also holds the block
-    // its replica waves finish one block late.  s_part: the replicas' partial sums.
-    constexpr int NAB = BV == 64 ? NBC : 8, NP = BV == 64 ? 1 : 2;
+    // Row scalars: double-buffered with the codes, or (wide layout) a ring of 8 that also
+    // holds the block its replica waves finish one block late.  s_part: the replicas' partial
+    // sums.
+    constexpr int NAB = BV == 64 ? 2 : 8, NP = BV == 64 ? 1 : 2;
     __shared__ __align__(16) float s_A[NAB][BV];
     __shared__ __align__(16) float s_r[NAB][BV];
     __shared__ int4 s_part[NP][NP > 1 ? kWavesPerBlock : 1][NP > 1 ? kWave : 1];
@@ -1165,22 +1163,14 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
         };
         const int nblk = (ve - vb + BV - 1) / BV;
         if constexpr (BV == 64) {
-            // Ring: block b in buffer b % NBC with blocks b + 1 .. b + NBC - 2 in flight; a wave
-            // waits only for its own loads of block b (vector memory operations retire in issue
-            // order; the next unit's counter atomic is issued two blocks before the end, where
-            // the waits that follow cover it too).
-            constexpr int AH = NBC - 1;
-            int nload = wid == 0 ? 2 : 0;
-#pragma unroll
-            for (int jj = 0; jj < KS; ++jj) nload += wid + 4 * jj < G16 ? 1 : 0;
-            for (int p = 0; p < AH && p < nblk; ++p) gload(p, p, vb + p * BV);
+            if (nblk > 0) gload(0, 0, vb);
             for (int b = 0; b < nblk; ++b) {
-                const int buf = b % NBC;
-                wait_vmcnt(min(AH - 1, nblk - 1 - b) * nload);
+                const int buf = b & 1;
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
                 if (tid == 0 && b == max(nblk - 2, 0)) nxt = atomicAdd(ctr, 1);
                 const int blk0 = vb + b * BV;
-                if (b + AH < nblk) gload((b + AH) % NBC, (b + AH) % NBC, blk0 + AH * BV);
+                if (b + 1 < nblk) gload(buf ^ 1, buf ^ 1, blk0 + BV);
                 if (active) {
                     for (int t = rr; t < BV / 16; t += R) {
                         if (blk0 + t * 16 >= ve) break;
