@@ -78,8 +78,8 @@ def test_band_front_end_derived_centroids(gmm, dev):
 
 @pytest.mark.parametrize("nlist", [2048, 4096, 5000])
 def test_band_front_end_wide_nlist(dev, nlist):
-    """The matrix-core band front end with 32 and 64 approximations per lane, and past 4096
-    centroids with each lane streaming its share of the row (8 smallest in registers)."""
+    """The matrix-core band front end with 32 approximations per lane in registers (nlist 2048)
+    and past 2048 centroids with each wave filtering its streamed row through an LDS list."""
     xb, xq = datagen.cfg4(N=3 * nlist, D=96, B=96, n_centers=nlist, seed=43)
     b = build_index(xb, nlist, dev, max_batch=128, max_nprobe=128)
     for nprobe in (1, 64, 100, 128):
@@ -101,7 +101,7 @@ def test_band_front_end_far_from_origin(dev):
 
 @pytest.mark.parametrize("offset", [3.0e3, 3.0e4])
 def test_band_front_end_stream_wide_band(dev, offset):
-    """Past 4096 centroids each wave filters its row through an LDS list tightened by
+    """Past 2048 centroids each wave filters its row through an LDS list tightened by
     bisection.  Offsets from the origin widen the error band: to a few hundred centroids (the
     band refined from the list 64 at a time) and to nearly all of them (the list cannot shrink,
     the band is taken from the row again); the probes must still be the oracle's."""

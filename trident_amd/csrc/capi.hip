@@ -605,7 +605,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
             if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
         }
         const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
-        const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= 2048 ? 32 : ix->nlist <= kBandMaxNlist ? 64 : 0;
+        const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= kBandMaxNlist ? 32 : 0;
 #define TRIDENT_BAND_LAUNCH(KPV, VV, SS)                                                         \
     select_band_kernel<KPV, VV, SS><<<grid, kBlock, 0, st>>>(                                   \
         a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, nprobe,          \
@@ -614,12 +614,10 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
         if (nprobe <= 64) {
             if (V == 16) TRIDENT_BAND_LAUNCH(64, 16, false);
             else if (V == 32) TRIDENT_BAND_LAUNCH(64, 32, false);
-            else if (V == 64) TRIDENT_BAND_LAUNCH(64, 64, false);
             else TRIDENT_BAND_LAUNCH(64, 8, true);
         } else {
             if (V == 16) TRIDENT_BAND_LAUNCH(128, 16, false);
             else if (V == 32) TRIDENT_BAND_LAUNCH(128, 32, false);
-            else if (V == 64) TRIDENT_BAND_LAUNCH(128, 64, false);
             else TRIDENT_BAND_LAUNCH(128, 8, true);
         }
 #undef TRIDENT_BAND_LAUNCH

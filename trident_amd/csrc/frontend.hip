@@ -677,7 +677,7 @@ __global__ __launch_bounds__(256) void scatter_pairs_lds_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// Band front end (nlist <= 4096, nprobe <= 128): approximate coarse distances on the matrix
+// Band front end (nprobe <= 128): approximate coarse distances on the matrix
 // cores with a rigorous error bound, then the canonical float64 distance for the band of
 // centroids that can still be among the nprobe nearest, and the exact (d, cid) selection.
 //
@@ -1380,10 +1380,8 @@ __global__ __launch_bounds__(256) void select_band_kernel(
         int, int, int, int32_t*, float*, int, int32_t*, float*, int);
 TRIDENT_SELECT_BAND(64, 16, false)
 TRIDENT_SELECT_BAND(64, 32, false)
-TRIDENT_SELECT_BAND(64, 64, false)
 TRIDENT_SELECT_BAND(128, 16, false)
 TRIDENT_SELECT_BAND(128, 32, false)
-TRIDENT_SELECT_BAND(128, 64, false)
 TRIDENT_SELECT_BAND(64, 8, true)
 TRIDENT_SELECT_BAND(128, 8, true)
 #undef TRIDENT_SELECT_BAND

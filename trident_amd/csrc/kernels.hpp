@@ -251,9 +251,10 @@ __global__ void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
                                           const float* __restrict__ cmt32,
                                           const float* __restrict__ cn32, int nlist, int Dq,
                                           int run_stages, float* __restrict__ a32);
-// band front end: up to 64 x 64 approximations per lane in registers; past that each lane
-// streams its share of the row and keeps its 8 smallest
-constexpr int kBandMaxNlist = 4096;
+// band front end: up to 32 x 64 approximations in registers (16 or 32 per lane); past that
+// each wave filters its streamed row through an LDS list (faster from nlist 4096 on than 64
+// values per lane in registers)
+constexpr int kBandMaxNlist = 2048;
 inline int band_dq(int D) { return (D + 15) & ~15; }
 
 constexpr int kCoarseQW = 4;       // queries per wave of coarse_dist_kernel
