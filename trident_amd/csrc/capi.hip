@@ -595,8 +595,19 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
             const int64_t spx = (nst + 7) / 8, nqb = (B + 63) / 64;
             const int64_t want = std::min<int64_t>(spx, std::max<int64_t>(1, kStreamBlocks / (8 * nqb)));
             const int64_t run_stages = (spx + want - 1) / want, nrun = (spx + run_stages - 1) / run_stages;
-            coarse_gemm_stream_kernel<<<(unsigned)(8 * nqb * nrun), kBlock, 0, st>>>(
-                w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq, (int)run_stages, a32);
+            const dim3 sgrid((unsigned)(8 * nqb * nrun));
+            switch (Dq >> 4) {
+#define TRIDENT_GEMM_CASE(NF)                                                                   \
+    case NF:                                                                                    \
+        coarse_gemm_stream_kernel<NF><<<sgrid, kBlock, 0, st>>>(w.qt32, w.qn32, B, cmt, cn,        \
+                                                                ix->nlist, Dq, (int)run_stages, a32); \
+        break;
+                TRIDENT_GEMM_CASE(1) TRIDENT_GEMM_CASE(2) TRIDENT_GEMM_CASE(3) TRIDENT_GEMM_CASE(4)
+                TRIDENT_GEMM_CASE(5) TRIDENT_GEMM_CASE(6) TRIDENT_GEMM_CASE(7) TRIDENT_GEMM_CASE(8)
+#undef TRIDENT_GEMM_CASE
+                default:
+                    return fail(TRIDENT_ERR_INVALID_ARGUMENT, "coarse GEMM: Dq=%d", (int)Dq);
+            }
             if ((rc = check_launch("coarse_gemm_stream_kernel"))) return rc;
         } else {
             const int64_t ncg = (ix->nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles);

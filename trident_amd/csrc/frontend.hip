@@ -870,6 +870,7 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
 // centroid tiles stay in its L2.  The four waves' query operands stay in registers for the
 // whole run; each stage's tiles are fetched into registers while the waves compute the
 // previous stage from LDS, then written to the other LDS buffer.
+template <int F>  // Dq / 16: float4 per lane and row tile; only the F k-groups that hold data run
 __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
                                                                  const float* __restrict__ qn32,
                                                                  int B,
@@ -879,13 +880,12 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
                                                                  int run_stages,
                                                                  float* __restrict__ a32) {
     typedef float f4 __attribute__((ext_vector_type(4)));
-    constexpr int PER_MAX = kStageTiles * 8 * kWave;  // float4 of a stage at Dq = 128
-    constexpr int PT = PER_MAX / kBlock;              // float4 each thread moves per stage
-    __shared__ float4 s_b[2][PER_MAX];
+    constexpr int PT = (kStageTiles * F * kWave + kBlock - 1) / kBlock;  // float4 per thread, stage
+    __shared__ float4 s_b[2][PT * kBlock];
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, g = lane >> 4;
-    const int F = Dq >> 4;  // float4 per lane and row tile
+    static_assert(F >= 1 && F <= 8, "Dq <= 128");
     const int ntl_all = (nlist + 15) / 16;
     const int nst = (ntl_all + kStageTiles - 1) / kStageTiles, spx = (nst + 7) >> 3;
     const int nrun = (spx + run_stages - 1) / run_stages;
@@ -898,21 +898,17 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
     const bool wave_live = qb0 < B;  // waves past the last query still load and wait
     const int qtile = wave_live ? qb0 / 16 : 0;
     const int qb = wave_live ? qb0 : 0;
-    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    float4 av[8];
+    float4 av[F];  // rows past B are never stored
     {
         const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            // steps past Dq are zero (F is wave-uniform); rows past B are never stored
-            if (j < F) av[j] = qt[(size_t)j * kWave];
-            else av[j] = z4;
-        }
+        for (int j = 0; j < F; ++j) av[j] = qt[(size_t)j * kWave];
     }
     const float4* cb = reinterpret_cast<const float4*>(cmt32);
-    // thread i moves float4s i, i + 256, ... of a stage's contiguous run (zero past nlist)
+    // thread i moves float4s i, i + 256, ... of a stage's contiguous run (named registers: an
+    // array indexed in a loop went to scratch)
+    static_assert(PT >= 1 && PT <= 4, "at most four float4 per thread and stage");
     float4 r0, r1, r2, r3;
-    static_assert(PT == 4, "four float4 per thread and stage");
 #define TRIDENT_FETCH(st_)                                                                       \
     {                                                                                           \
         const int t0_ = (st_) * kStageTiles, n_ = min(kStageTiles, ntl_all - t0_) * F * kWave;  \
@@ -920,16 +916,16 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
         const int i_ = (int)threadIdx.x;                                                         \
         /* slots past the stage's tiles are never read: they load element 0 again */            \
         r0 = p_[i_ < n_ ? i_ : 0];                                                               \
-        r1 = p_[i_ + kBlock < n_ ? i_ + kBlock : 0];                                             \
-        r2 = p_[i_ + 2 * kBlock < n_ ? i_ + 2 * kBlock : 0];                                     \
-        r3 = p_[i_ + 3 * kBlock < n_ ? i_ + 3 * kBlock : 0];                                     \
+        if constexpr (PT > 1) r1 = p_[i_ + kBlock < n_ ? i_ + kBlock : 0];                       \
+        if constexpr (PT > 2) r2 = p_[i_ + 2 * kBlock < n_ ? i_ + 2 * kBlock : 0];               \
+        if constexpr (PT > 3) r3 = p_[i_ + 3 * kBlock < n_ ? i_ + 3 * kBlock : 0];               \
     }
 #define TRIDENT_PUT(b_)                                                                          \
     {                                                                                           \
         s_b[b_][threadIdx.x] = r0;                                                               \
-        s_b[b_][threadIdx.x + kBlock] = r1;                                                      \
-        s_b[b_][threadIdx.x + 2 * kBlock] = r2;                                                  \
-        s_b[b_][threadIdx.x + 3 * kBlock] = r3;                                                  \
+        if constexpr (PT > 1) s_b[b_][threadIdx.x + kBlock] = r1;                                \
+        if constexpr (PT > 2) s_b[b_][threadIdx.x + 2 * kBlock] = r2;                            \
+        if constexpr (PT > 3) s_b[b_][threadIdx.x + 3 * kBlock] = r3;                            \
     }
     TRIDENT_FETCH(s_beg)
     TRIDENT_PUT(0)
@@ -941,19 +937,16 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
             const int t0 = st * kStageTiles, ntl = min(kStageTiles, ntl_all - t0);
 #pragma unroll 1
             for (int t = 0; t < ntl; ++t) {
-                float4 bv[8];
+                float4 bv[F];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    if (j < F) bv[j] = s_b[buf][(t * F + j) * kWave + lane];
-                    else bv[j] = z4;
-                }
+                for (int j = 0; j < F; ++j) bv[j] = s_b[buf][(t * F + j) * kWave + lane];
                 f4 acc4[4];
 #pragma unroll
                 for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
                 // centroids are the A operand, queries the B operand; consecutive MFMAs go to
                 // different accumulators (k-step 4 j + u -> chain u)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < F; ++j) {
                     acc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].x, av[j].x, acc4[0], 0, 0, 0);
                     acc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].y, av[j].y, acc4[1], 0, 0, 0);
                     acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, av[j].z, acc4[2], 0, 0, 0);
@@ -988,6 +981,20 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
 #undef TRIDENT_FETCH
 #undef TRIDENT_PUT
 }
+
+#define TRIDENT_GEMM_STREAM(NF)                                                                 \
+    template __global__ void coarse_gemm_stream_kernel<NF>(const float*, const float*, int,      \
+                                                           const float*, const float*, int, int, \
+                                                           int, float*);
+TRIDENT_GEMM_STREAM(1)
+TRIDENT_GEMM_STREAM(2)
+TRIDENT_GEMM_STREAM(3)
+TRIDENT_GEMM_STREAM(4)
+TRIDENT_GEMM_STREAM(5)
+TRIDENT_GEMM_STREAM(6)
+TRIDENT_GEMM_STREAM(7)
+TRIDENT_GEMM_STREAM(8)
+#undef TRIDENT_GEMM_STREAM
 
 // One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM (any nlist), the
 // row streamed through a running filter.  T is any value with count(a <= T) >= nprobe over the

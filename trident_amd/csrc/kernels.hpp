@@ -246,6 +246,7 @@ constexpr int kGemmTiles = 4;  // coarse_gemm_kernel: 16-centroid tiles per wave
 // block is the longest that still gives a grid of about kStreamBlocks blocks
 constexpr int kStageTiles = 2;
 constexpr int kStreamBlocks = 5120;
+template <int F>
 __global__ void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
                                           const float* __restrict__ qn32, int B,
                                           const float* __restrict__ cmt32,
