@@ -115,6 +115,16 @@ def test_band_front_end_stream_wide_band(dev, offset):
         _check_probes(b, xq, dev, nprobe)
 
 
+@pytest.mark.parametrize("D", [12, 72, 100, 112])
+def test_band_front_end_query_widths(dev, D):
+    """The streamed coarse GEMM runs one instantiation per 16-dim group count (Dq = 16, 80,
+    112): widths the other tests do not reach, zero-padded past D."""
+    xb, xq = datagen.cfg1(N=6_000, D=D, B=80, n_centers=64, seed=46 + D)
+    b = build_index(xb, 96, dev, max_batch=128, max_nprobe=128)
+    for nprobe in (1, 16, 96):
+        _check_probes(b, xq.numpy(), dev, nprobe)
+
+
 def test_coarse_probe_selectors_all_widths(dev):
     """nprobe <= 64 and <= 128 use the one-wave register selector, larger ones the block radix
     select; all must give the oracle's (d, cid) order, including at the 64 / 128 edges."""
