@@ -404,9 +404,9 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
     const bool vec4 = (D & 3) == 0 && (reinterpret_cast<uintptr_t>(a.xb) & 15) == 0;
     unsigned long long ins = 0;
     if constexpr (HOST) {
-        // base in mapped host memory: rows cross PCIe, so they are read as 128-byte row
-        // segments (all of a 32-dim chunk's loads in flight) and staged through LDS; seed rows
-        // are left out of the chunk
+        // base in mapped host memory: rows cross PCIe, so the wave's rows are read whole (512
+        // contiguous bytes at a time, a group's loads all in flight: refine_rows) and staged
+        // through LDS; seed rows are left out of the group
         __shared__ int32_t s_pos[kWavesPerBlock][kWave];
         __shared__ double s_q64[kWavesPerBlock][DQ];
         __shared__ float s_stage[kWavesPerBlock][kStageCh][kWave + 1];
