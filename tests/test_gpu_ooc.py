@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import assert_exact, build_index, oracle_search
+from tests.helpers import assert_exact, build_index, oracle_search, run_search
 from trident_amd import _lib, datagen
 
 pytestmark = pytest.mark.gpu
@@ -129,3 +129,22 @@ def test_fine_tau_long_candidate_lists(dev):
     finally:
         torch.cuda.synchronize()
         b.ix.storage._host_buf.free()
+
+
+@pytest.mark.parametrize("placement", ["device", "host"])
+def test_stage_z_rows_not_multiple_of_four(dev, placement):
+    """D = 50: rows are not 16-byte aligned, so Stage Z stages them with 4-byte loads (each lane
+    dims kk + 32 m of its rows) instead of float4 runs; both routes, base in device and mapped
+    host memory, against the oracle."""
+    xb, xq = datagen.cfg1(N=8_000, D=50, B=96, n_centers=32, seed=71)
+    b = build_index(xb, 32, dev, xb_placement=placement, max_batch=128)
+    try:
+        for route in (1, 2):
+            for nprobe, K in ((4, 10), (12, 1)):
+                _, rd, ri = oracle_search(b, xq.numpy(), nprobe, K)
+                d, i = run_search(b, _q(xq.numpy(), dev), nprobe, K, mode=2, route=route)
+                assert_exact(d, i, rd, ri, f"D=50 {placement} route={route} nprobe={nprobe} K={K}")
+    finally:
+        if placement == "host":
+            torch.cuda.synchronize()
+            b.ix.storage._host_buf.free()
