@@ -92,6 +92,89 @@ def test_damaged_directories_are_refused(cpu_index, tmp_path):
         persist.load_index(str(tmp_path), device="cpu")
 
 
+def test_interrupted_resave_is_refused(cpu_index, tmp_path, monkeypatch):
+    """A re-save over an existing index removes its meta.npz first: interrupted before the new
+    meta lands (here: the meta write fails), the directory holds no loadable index, although
+    every .bin has the right size."""
+    ix, _, _, _ = cpu_index
+    persist.save_index(ix, str(tmp_path))
+
+    def boom(*a, **k):
+        raise OSError("interrupted")
+
+    monkeypatch.setattr(persist.np, "savez", boom)
+    with pytest.raises(OSError, match="interrupted"):
+        persist.save_index(ix, str(tmp_path))
+    monkeypatch.undo()
+    with pytest.raises(ValueError, match="meta.npz"):
+        persist.load_index(str(tmp_path), device="cpu")
+
+
+def test_bin_from_another_save_is_refused(cpu_index, tmp_path):
+    """Each .bin carries its save's token: a file of the right size from another save of the
+    same shapes is refused."""
+    ix, _, _, _ = cpu_index
+    a, b = tmp_path / "a", tmp_path / "b"
+    persist.save_index(ix, str(a))
+    persist.save_index(ix, str(b))
+    os.replace(a / "sq8_packed.bin", b / "sq8_packed.bin")
+    with pytest.raises(ValueError, match="another save"):
+        persist.load_index(str(b), device="cpu")
+
+
+def test_inconsistent_meta_is_refused(cpu_index, tmp_path):
+    """Manifest shapes and list offsets are checked against the index sizes before any copy."""
+    ix, _, _, _ = cpu_index
+    persist.save_index(ix, str(tmp_path))
+    meta_f = tmp_path / "meta.npz"
+    with np.load(meta_f, allow_pickle=False) as z:
+        meta = {k: z[k] for k in z.files}
+
+    def rewrite(**changes):
+        m = dict(meta, **changes)
+        np.savez(str(tmp_path / "meta.npz"), **m)
+
+    off = meta["vec_off"].copy()
+    off[-1] += 1
+    rewrite(vec_off=off)
+    with pytest.raises(ValueError, match="vec_off"):
+        persist.load_index(str(tmp_path), device="cpu")
+    shapes = meta["bin_shapes"].copy()
+    i = list(map(str, meta["bin_names"])).index("vec_Ar")
+    shapes[i] = f"{int(meta['N']) - 1},2"
+    rewrite(bin_shapes=shapes)
+    with pytest.raises(ValueError, match="vec_Ar"):
+        persist.load_index(str(tmp_path), device="cpu")
+    rewrite(total_tiles=np.int64(int(meta["total_tiles"]) + 1))
+    with pytest.raises(ValueError, match="tile_off"):
+        persist.load_index(str(tmp_path), device="cpu")
+    rewrite()
+    persist.load_index(str(tmp_path), device="cpu", max_batch=8, max_nprobe=8)
+
+
+def test_save_after_releasing_the_packing(tmp_path):
+    """An index that keeps only the batched route's cells on its device saves the reference
+    packing rebuilt from them: the reload holds the same sq8_packed as the index before the
+    release."""
+    xb, _ = datagen.cfg2(N=3000, D=64, B=8, n_centers=16, seed=9)
+    cen, lid, r, mean64, R64, _ = clustering.train_clustering(xb, 12, seed=0, niter=3)
+    st = SharedClusterStorage(xb.numpy(), lid, r, 12, device="cpu")
+    ix = TridentV4Index(st, cen, mean64, R64, tile_size=64, device="cpu", max_batch=8, max_nprobe=8)
+    before = ix.sq8_packed.clone()
+    ix.release_packed_codes()
+    assert not ix.has_packed_codes and "sq8_packed" not in ix.hbm_footprint()
+    persist.save_index(ix, str(tmp_path))
+    got = persist.load_index(str(tmp_path), device="cpu", max_batch=8, max_nprobe=8)
+    assert torch.equal(got.sq8_packed, before) and torch.equal(got.sq8_cells, ix.sq8_cells)
+
+
+def test_user_meta_round_trip(cpu_index, tmp_path):
+    ix, _, _, _ = cpu_index
+    persist.save_index(ix, str(tmp_path), include_base=False, user={"cfg": 4, "seed": 11, "tag": "x"})
+    assert persist.read_user_meta(str(tmp_path)) == {"cfg": 4, "seed": 11, "tag": "x"}
+    assert persist.read_user_meta(str(tmp_path / "nothing")) == {}
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("placement", ["device", "host"])
 def test_reloaded_index_searches_exactly(dev, tmp_path, placement):

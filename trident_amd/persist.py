@@ -22,10 +22,19 @@ with ``numpy.memmap`` and streamed to the device in chunks -- and stores everyth
   xb_sorted.bin       float32 [N, D]       the cluster-sorted base (optional)
 
 The code cells of the batched route and the centroid layouts of the coarse pass are
-regrouped from sq8_packed / W_combined on load (cheap, on the device).  Every file is written
-under a temporary name and renamed into place (``os.replace``); ``meta.npz`` goes last, so a
-directory with a ``meta.npz`` is complete.  The loader checks the format, the version and every
-file's size against the manifest.
+regrouped from sq8_packed / W_combined on load (cheap, on the device).
+
+Consistency.  A save first removes any ``meta.npz`` already in the directory, writes every
+``.bin`` under a temporary name and renames it into place (``os.replace``), and writes
+``meta.npz`` last, so an interrupted save leaves a directory without a ``meta.npz``, which the
+loader refuses.  Every ``.bin`` ends with the save's 16-byte random token (after the array's
+bytes), and ``meta.npz`` records it: a ``.bin`` left over from another save (a re-save over an
+index of the same shapes, interrupted after some files were replaced) carries another token and
+is refused.  The loader also checks the format, the version, every file's size and shape
+against the manifest and the index sizes (N, D, D_pad, nlist, tiles, T), and the list offsets
+(0 = vec_off[0] <= ... <= vec_off[nlist] = N, the same for the tile offsets), before anything is
+copied to the device.  Callers may store their own scalars (``user`` = {name: int/float/str})
+and read them back with ``read_user_meta``.
 """
 import os
 import time
@@ -38,32 +47,41 @@ from . import ext as _ext
 from .index import SharedClusterStorage, TridentV4Index, cells_from_packed
 
 FORMAT = "trident-amd-ivf-sq8"
-VERSION = 1
+VERSION = 2
+_TOKEN_BYTES = 16
 
 _CHUNK_ROWS = 1 << 20
 _SCALARS = ("N", "D", "D_pad", "nlist", "tile_size", "per_cluster_sq8", "use_pca", "var_block",
             "total_tiles")
 
 
-def _write_bin(path: str, t: torch.Tensor, chunk_rows: int = _CHUNK_ROWS):
-    """Streams a tensor (device, host or pinned) to ``path`` row chunk by row chunk."""
+def _write_bin(path: str, t: torch.Tensor, token: bytes, chunk_rows: int = _CHUNK_ROWS):
+    """Streams a tensor (device, host or pinned) to ``path`` row chunk by row chunk, then the
+    save's token."""
     tmp = f"{path}.tmp-{os.getpid()}"
     with open(tmp, "wb") as f:
         n = int(t.shape[0]) if t.dim() else 1
         for s in range(0, max(n, 1), chunk_rows):
             part = t[s:s + chunk_rows] if t.dim() else t
             f.write(part.detach().to("cpu").contiguous().numpy().tobytes())
+        f.write(token)
     os.replace(tmp, path)
 
 
-def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=None, R64=None) -> dict:
+def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=None, R64=None,
+               user: Optional[dict] = None) -> dict:
     """Writes ``ix`` (and, with ``include_base``, its sorted base) under directory ``path``.
-    Returns the manifest."""
+    ``user``: the caller's own scalars, stored in meta.npz (``read_user_meta``).  Returns the
+    manifest."""
     os.makedirs(path, exist_ok=True)
+    meta_f = os.path.join(path, "meta.npz")
+    if os.path.exists(meta_f):  # until the new meta lands, the directory is no index
+        os.remove(meta_f)
+    token = os.urandom(_TOKEN_BYTES)
     st = ix.storage
     bins = {
         "sort_perm": st.orig_ids_sorted,
-        "sq8_packed": ix.sq8_packed,
+        "sq8_packed": ix.packed_codes(),  # rebuilt from the cells if the index released it
         "tile_orig_ids": ix.tile_orig_ids,
         "vec_Ar": ix.vec_Ar,
         "r_vec_sorted": ix.r_vec_sorted,
@@ -76,11 +94,12 @@ def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=
         bins["xb_sorted"] = st.xb_sorted
     manifest = {}
     for name, t in bins.items():
-        _write_bin(os.path.join(path, name + ".bin"), t)
+        _write_bin(os.path.join(path, name + ".bin"), t, token)
         manifest[name] = (str(t.dtype).replace("torch.", ""), tuple(int(s) for s in t.shape))
     meta = {k: np.int64(getattr(ix, k)) for k in _SCALARS}
     meta.update(
         format=np.array(FORMAT), version=np.int64(VERSION),
+        token=np.frombuffer(token, np.uint8).copy(),
         rot_sq_min=np.float64(ix.rot_sq_min), rot_sq_max=np.float64(ix.rot_sq_max),
         centroids=ix.centroids.cpu().numpy(),
         W_combined=ix.W_combined.cpu().numpy(), b_combined=ix.b_combined.cpu().numpy(),
@@ -95,10 +114,22 @@ def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=
         meta["mean64"] = np.asarray(mean64, np.float64)
     if R64 is not None:
         meta["R64"] = np.asarray(R64, np.float64)
+    for k2, v in (user or {}).items():
+        _need(isinstance(v, (int, float, str, np.integer, np.floating)), f"user[{k2!r}] must be a scalar")
+        meta["user_" + str(k2)] = np.array(v)
     tmp = os.path.join(path, f"meta.tmp-{os.getpid()}.npz")
     np.savez(tmp, **meta)
-    os.replace(tmp, os.path.join(path, "meta.npz"))
+    os.replace(tmp, meta_f)
     return manifest
+
+
+def read_user_meta(path: str) -> dict:
+    """The ``user`` scalars a save stored (empty when the directory holds no index)."""
+    meta_f = os.path.join(path, "meta.npz")
+    if not os.path.exists(meta_f):
+        return {}
+    with np.load(meta_f, allow_pickle=False) as z:
+        return {k2[5:]: z[k2].item() for k2 in z.files if k2.startswith("user_")}
 
 
 def _need(cond: bool, msg: str):
@@ -110,17 +141,62 @@ _NP = {"int32": np.int32, "float32": np.float32, "int16": np.int16}
 _TORCH = {"int32": torch.int32, "float32": torch.float32, "int16": torch.int16}
 
 
-def _open_bins(path: str, meta) -> dict:
+def _expected_shapes(sc: dict) -> dict:
+    N, D, DP, T, tiles = sc["N"], sc["D"], sc["D_pad"], sc["tile_size"], sc["total_tiles"]
+    return {"sort_perm": ((N,), "int32"), "sq8_packed": ((tiles, DP // 4, T), "int32"),
+            "tile_orig_ids": ((tiles, T), "int32"), "vec_Ar": ((N, 2), "float32"),
+            "r_vec_sorted": ((N,), "float32"), "fine_codes": ((N, DP), "int16"),
+            "fine_qp": ((N, 4), "float32"), "xb_sorted": ((N, D), "float32")}
+
+
+def _open_bins(path: str, meta, sc: dict) -> dict:
     out = {}
+    token = bytes(np.asarray(meta["token"], np.uint8))
+    want_shapes = _expected_shapes(sc)
     for name, dt, shp in zip(meta["bin_names"], meta["bin_dtypes"], meta["bin_shapes"]):
         name, dt = str(name), str(dt)
         shape = tuple(int(s) for s in str(shp).split(",") if s)
+        _need(name in want_shapes, f"{path}: unknown array {name!r} in the manifest")
+        _need((shape, dt) == want_shapes[name],
+              f"{path}: {name} is {dt} {shape} in the manifest, the index sizes say "
+              f"{want_shapes[name][1]} {want_shapes[name][0]}")
         f = os.path.join(path, name + ".bin")
         _need(os.path.exists(f), f"{f} is missing")
         want = int(np.prod(shape)) * np.dtype(_NP[dt]).itemsize
-        _need(os.path.getsize(f) == want, f"{f}: {os.path.getsize(f)} bytes, the manifest says {want}")
+        got = os.path.getsize(f)
+        _need(got == want + _TOKEN_BYTES, f"{f}: {got} bytes, the manifest says {want + _TOKEN_BYTES}")
+        with open(f, "rb") as fh:
+            fh.seek(want)
+            _need(fh.read(_TOKEN_BYTES) == token, f"{f} belongs to another save (token mismatch)")
         out[name] = np.memmap(f, dtype=_NP[dt], mode="r", shape=shape) if want else np.zeros(shape, _NP[dt])
+    for name in ("sort_perm", "sq8_packed", "tile_orig_ids", "vec_Ar", "r_vec_sorted"):
+        _need(name in out, f"{path}: {name}.bin is not in the manifest")
+    _need(("fine_codes" in out) == ("fine_qp" in out), f"{path}: the fine level is incomplete")
     return out
+
+
+def _check_offsets(path: str, off: np.ndarray, n_lists: int, total: int, what: str):
+    off = np.asarray(off)
+    _need(off.ndim == 1 and off.shape[0] == n_lists + 1, f"{path}: {what} must have nlist + 1 entries")
+    _need(int(off[0]) == 0 and int(off[-1]) == total, f"{path}: {what} must run from 0 to {total}")
+    _need(bool(np.all(np.diff(off.astype(np.int64)) >= 0)), f"{path}: {what} is not monotone")
+
+
+def _check_meta(path: str, meta, sc: dict):
+    N, D, DP, nlist, T, tiles = (sc["N"], sc["D"], sc["D_pad"], sc["nlist"], sc["tile_size"],
+                                 sc["total_tiles"])
+    _need(N >= 0 and D >= 1 and nlist >= 1 and T >= 64 and T % 64 == 0 and DP >= D and DP % 32 == 0,
+          f"{path}: inconsistent sizes {sc}")
+    _check_offsets(path, meta["vec_off"], nlist, N, "vec_off")
+    _check_offsets(path, meta["tile_off"], nlist, tiles, "tile_off")
+    _need(tuple(meta["centroids"].shape) == (nlist, D), f"{path}: centroids must be [{nlist}, {D}]")
+    _need(tuple(meta["W_combined"].shape) == (D, nlist + DP), f"{path}: W_combined must be [{D}, {nlist + DP}]")
+    _need(meta["b_combined"].size == nlist + DP, f"{path}: b_combined must hold {nlist + DP} values")
+    rows = nlist if sc["per_cluster_sq8"] else 1
+    for name in ("vmin", "delta", "eps"):
+        _need(meta[name].shape[-1] == DP and meta[name].size in (DP, rows * DP),
+              f"{path}: {name} must be [{rows}, {DP}]")
+    _need(meta["tile_r_minmax"].size == 2 * tiles, f"{path}: tile_r_minmax must be [{tiles}, 2]")
 
 
 def _to_device(a: np.ndarray, dev, chunk_rows: int = _CHUNK_ROWS) -> torch.Tensor:
@@ -144,7 +220,8 @@ def load_index(path: str, device="cuda:0", xb_placement: str = "device", xb_raw=
     _need(str(meta["format"]) == FORMAT, f"{path}: format {meta['format']!s}, expected {FORMAT}")
     _need(int(meta["version"]) == VERSION, f"{path}: version {int(meta['version'])}, expected {VERSION}")
     sc = {k2: int(meta[k2]) for k2 in _SCALARS}
-    bins = _open_bins(path, meta)
+    _check_meta(path, meta, sc)
+    bins = _open_bins(path, meta, sc)
     N, D, nlist = sc["N"], sc["D"], sc["nlist"]
     dev = torch.device(device)
     sort_perm = np.asarray(bins["sort_perm"])

@@ -9,6 +9,11 @@ the batches overlap, so one batch's copies and its PCIe-bound stages (the exact 
 an out-of-core base) run beside another batch's HBM-bound scans.  All streams have the default
 priority.  Results are identical to searching each batch alone: every batch's kernels read
 only its own buffers and the shared read-only index.
+
+Ordering with the caller's work: every slot stream waits for the caller's current stream when
+``run`` starts, so an index whose build kernels (cluster bounds, derived layouts) are still
+queued there is complete before any batch reads it.  ``close`` (or leaving a ``with`` block)
+drains the slots and frees their workspaces.
 """
 import numpy as np
 import torch
@@ -23,9 +28,11 @@ class _Slot:
         self.host_q = torch.empty((batch, D), dtype=torch.float32, pin_memory=True)
         self.host_d = torch.empty((batch, k), dtype=torch.float32, pin_memory=True)
         self.host_i = torch.empty((batch, k), dtype=torch.int64, pin_memory=True)
-        self.dev_q = torch.empty((batch, D), dtype=torch.float32, device=dev)
-        self.dev_d = torch.empty((batch, k), dtype=torch.float32, device=dev)
-        self.dev_i = torch.empty((batch, k), dtype=torch.int64, device=dev)
+        # allocated on the slot's own stream, the only stream that writes them
+        with torch.cuda.stream(self.stream):
+            self.dev_q = torch.empty((batch, D), dtype=torch.float32, device=dev)
+            self.dev_d = torch.empty((batch, k), dtype=torch.float32, device=dev)
+            self.dev_i = torch.empty((batch, k), dtype=torch.int64, device=dev)
         self.done = torch.cuda.Event()
         self.pending = None  # (start, end) of the batch whose results are in flight
 
@@ -49,6 +56,21 @@ class SearchPipeline:
         self._view = ix.view()
         self._slots = [_Slot(ix.dev, self.batch, ix.D, self.k) for _ in range(self.depth)]
 
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False
+
+    def close(self) -> None:
+        """Wait for the slots' streams and free their library workspaces (each slot stream
+        holds one, sized for a full batch)."""
+        for slot in self._slots:
+            slot.stream.synchronize()
+            _ext.release_workspace(self.ix.dev, slot.stream)
+            slot.pending = None
+
     def _drain(self, slot, out_d, out_i):
         if slot.pending is None:
             return
@@ -65,6 +87,9 @@ class SearchPipeline:
         Q = xq.shape[0]
         out_d = np.empty((Q, self.k), np.float32)
         out_i = np.empty((Q, self.k), np.int64)
+        caller = torch.cuda.current_stream(self.ix.dev)
+        for slot in self._slots:  # the index and anything the caller queued come first
+            slot.stream.wait_stream(caller)
         for b, s in enumerate(range(0, Q, self.batch)):
             e = min(Q, s + self.batch)
             n = e - s
