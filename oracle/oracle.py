@@ -38,6 +38,8 @@ def lib():
         L.oracle_coarse_probe.argtypes = [P, i64, i32, P, i32, i32, P, P, i32]
         L.oracle_ivf_exact.argtypes = [P, i64, i32, P, i32, P, P, P, i32, P, P, i32]
         L.oracle_ivfflat_f32.argtypes = [P, i64, i32, P, i32, P, P, P, i32, P, P, i32]
+        L.oracle_ivf_exact_cm.argtypes = [P, i64, i32, P, i32, P, P, P, i32, i32, P, P, i32]
+        L.oracle_ivf_exact_cm.restype = i32
         L.oracle_pair_dists.argtypes = [P, i32, P, P, P, i64, P]
         L.oracle_rotate_query.argtypes = [P, i32, i32, P, i32, P, P]
         L.oracle_rotate_query.restype = None
@@ -91,6 +93,26 @@ def ivf_exact(xq, probe_cids, vec_off, xb_sorted, orig_ids, K, threads=0):
                                 ids.ctypes.data, threads or default_threads())
     if rc:
         raise ValueError("oracle_ivf_exact: bad arguments")
+    return d, ids
+
+
+def ivf_exact_cm(xq, probe_cids, vec_off, xb_sorted, orig_ids, K, threads=0):
+    """``ivf_exact``'s result computed cluster-major (each probed list read once for every query
+    that probes it): the fast form for large batches whose queries share clusters."""
+    xq, pq = _c(xq, np.float32)
+    pcid, ppc = _c(probe_cids, np.int32)
+    voff, pvo = _c(vec_off, np.int32)
+    xb, pxb = _c(xb_sorted, np.float32)
+    oid, poi = _c(orig_ids, np.int32)
+    B, D = xq.shape
+    d = np.empty((B, K), np.float64)
+    ids = np.empty((B, K), np.int64)
+    rc = lib().oracle_ivf_exact_cm(pq, B, D, ppc, pcid.shape[1], pvo, pxb, poi, len(voff) - 1, K,
+                                   d.ctypes.data, ids.ctypes.data, threads or default_threads())
+    if rc == -2:
+        raise MemoryError("oracle_ivf_exact_cm: pair lists do not fit in host memory")
+    if rc:
+        raise ValueError("oracle_ivf_exact_cm: bad arguments")
     return d, ids
 
 

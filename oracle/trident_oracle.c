@@ -21,6 +21,8 @@
  *                          (d, id) lexicographic: benchmarks/phase4b_suite.py:197-219,
  *                          tie-break of benchmarks/phase3a_lossless_audit.py:62 and
  *                          insert_topk (src/trident_v4_kernels.cu:19-60).
+ *   oracle_ivf_exact_cm    the same result computed cluster-major (each probed list read
+ *                          once for all the queries that probe it), for large batches.
  *   oracle_ivfflat_f32     the reference CPU baseline omp_cpu_ivfflat_f32
  *                          (benchmarks/phase8_ooc_100m_4080.py:141-204): FP32 direct
  *                          sum with an OpenMP SIMD reduction and (d, id) insertion.
@@ -57,6 +59,21 @@ double oracle_dist_f64(const float* x, const float* q, int D) {
         acc = fma(t, t, acc);
     }
     return acc;
+}
+
+/* oracle_dist_f64 of 8 consecutive rows (row stride D): the same per-row fma chain in dimension
+ * order, eight independent chains interleaved so that the FMA units are not left waiting on one
+ * chain's latency.  Bit-identical to eight oracle_dist_f64 calls. */
+static inline void oracle_dist8_f64(const float* x, const float* q, int D, double* out) {
+    double a[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+    for (int d = 0; d < D; ++d) {
+        const double qd = (double)q[d];
+        for (int r = 0; r < 8; ++r) {
+            const double t = (double)x[(int64_t)r * D + d] - qd;
+            a[r] = fma(t, t, a[r]);
+        }
+    }
+    for (int r = 0; r < 8; ++r) out[r] = a[r];
 }
 
 /* (d, id) strictly-less, the ordering contract of insert_topk. */
@@ -129,7 +146,14 @@ int oracle_ivf_exact(const float* xq, int64_t B, int D, const int32_t* probe_cid
             for (int p = 0; p < nprobe; ++p) {
                 int32_t c = probe_cids[q * nprobe + p];
                 if (c < 0) continue;
-                for (int64_t v = vec_off[c]; v < vec_off[c + 1]; ++v) {
+                int64_t v = vec_off[c];
+                const int64_t ve = vec_off[c + 1];
+                for (; v + 8 <= ve; v += 8) {
+                    double d8[8];
+                    oracle_dist8_f64(xb_sorted + v * D, qv, D, d8);
+                    for (int r = 0; r < 8; ++r) insert_sorted(ld, li, K, d8[r], (int64_t)orig_ids[v + r]);
+                }
+                for (; v < ve; ++v) {
                     double d = oracle_dist_f64(xb_sorted + v * D, qv, D);
                     insert_sorted(ld, li, K, d, (int64_t)orig_ids[v]);
                 }
@@ -306,6 +330,132 @@ int oracle_ivf_sq8(const float* xq, int64_t B, int D, int D_pad, const float* W,
         }
         free(xr); free(base); free(pk); free(pi); free(gk); free(gi); free(ld); free(li);
     }
+    return 0;
+}
+
+/* oracle_ivf_exact computed cluster-major, for large batches: the (query, probe) pairs are
+ * grouped by cluster; each cluster's rows are read once, in chunks of 256 rows (kept in the
+ * core's cache), for every query that probes it, into one top-K list per pair (by (d, id));
+ * then each query merges its nprobe lists.  A row belongs to one list, so the merged list is
+ * the top-K by (d, id) over the probed lists: the same result as oracle_ivf_exact (the same
+ * canonical distances, the same order), with far fewer memory reads when many queries share
+ * clusters.  Returns -2 when the pair lists or a thread's buffers cannot be allocated. */
+int oracle_ivf_exact_cm(const float* xq, int64_t B, int D, const int32_t* probe_cids, int nprobe,
+                        const int32_t* vec_off, const float* xb_sorted, const int32_t* orig_ids,
+                        int nlist, int K, double* out_d, int64_t* out_i, int nthreads) {
+    if (K < 1 || D < 1 || nlist < 1) return -1;
+    const int64_t M = B * (int64_t)nprobe;
+    int64_t* start = (int64_t*)calloc((size_t)nlist + 1, sizeof(int64_t));
+    int64_t* pairs = (int64_t*)malloc(sizeof(int64_t) * (size_t)(M > 0 ? M : 1));
+    double* pd = (double*)malloc(sizeof(double) * (size_t)(M > 0 ? M : 1) * (size_t)K);
+    int64_t* pid = (int64_t*)malloc(sizeof(int64_t) * (size_t)(M > 0 ? M : 1) * (size_t)K);
+    if (!start || !pairs || !pd || !pid) {
+        free(start); free(pairs); free(pd); free(pid);
+        return -2;
+    }
+    for (int64_t e = 0; e < M; ++e) {
+        const int32_t c = probe_cids[e];
+        if (c >= 0 && c < nlist) ++start[c + 1];
+    }
+    for (int c = 0; c < nlist; ++c) start[c + 1] += start[c];
+    {
+        int64_t* fill = (int64_t*)malloc(sizeof(int64_t) * (size_t)nlist);
+        if (!fill) { free(start); free(pairs); free(pd); free(pid); return -2; }
+        memcpy(fill, start, sizeof(int64_t) * (size_t)nlist);
+        for (int64_t e = 0; e < M; ++e) {
+            const int32_t c = probe_cids[e];
+            if (c >= 0 && c < nlist) pairs[fill[c]++] = e; /* e = q * nprobe + p */
+        }
+        free(fill);
+    }
+    for (int64_t e = 0; e < M * K; ++e) { pd[e] = INFINITY; pid[e] = INT64_MAX; }
+    /* Each chunk of CH rows is copied once per cluster, as float64 and dimension-major
+     * (xt[d * CH + r] = (double)x_r,d), so that 32 rows' fma chains run side by side in
+     * contiguous vectors; every row still gets t = (double)x_d - (double)q_d and
+     * acc = fma(t, t, acc) for d in order, so the distances are oracle_dist_f64's. */
+    const int CH = D <= 256 ? 256 : 64;
+    int bad_alloc = 0;
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#pragma omp parallel
+#endif
+    {
+        double* xt = (double*)malloc(sizeof(double) * (size_t)CH * (size_t)D);
+        double* q64 = (double*)malloc(sizeof(double) * (size_t)D);
+        double* dd = (double*)malloc(sizeof(double) * (size_t)CH);
+        if (!xt || !q64 || !dd) {
+#ifdef _OPENMP
+#pragma omp atomic write
+#endif
+            bad_alloc = 1;
+        }
+#ifdef _OPENMP
+#pragma omp for schedule(dynamic, 1)
+#endif
+        for (int c = 0; c < nlist; ++c) {
+            if (!xt || !q64 || !dd) continue;
+            const int64_t v0 = vec_off[c], v1 = vec_off[c + 1];
+            for (int64_t cb = v0; cb < v1 && start[c + 1] > start[c]; cb += CH) {
+                const int n = (int)((cb + CH < v1 ? cb + CH : v1) - cb);
+                const int n32 = (n + 31) & ~31;
+                for (int r = 0; r < n32; ++r)
+                    for (int d = 0; d < D; ++d)
+                        xt[(int64_t)d * CH + r] = r < n ? (double)xb_sorted[(cb + r) * D + d] : 0.0;
+                for (int64_t k = start[c]; k < start[c + 1]; ++k) {
+                    const int64_t e = pairs[k];
+                    const float* qv = xq + (e / nprobe) * (int64_t)D;
+                    for (int d = 0; d < D; ++d) q64[d] = (double)qv[d];
+                    for (int g = 0; g < n32; g += 32) {
+                        double a[32];
+                        for (int r = 0; r < 32; ++r) a[r] = 0.0;
+                        for (int d = 0; d < D; ++d) {
+                            const double qd = q64[d];
+                            const double* xr = xt + (int64_t)d * CH + g;
+                            for (int r = 0; r < 32; ++r) {
+                                const double t = xr[r] - qd;
+                                a[r] = fma(t, t, a[r]);
+                            }
+                        }
+                        for (int r = 0; r < 32; ++r) dd[g + r] = a[r];
+                    }
+                    double* ld = pd + e * K;
+                    int64_t* li = pid + e * K;
+                    for (int r = 0; r < n; ++r) insert_sorted(ld, li, K, dd[r], (int64_t)orig_ids[cb + r]);
+                }
+            }
+        }
+        free(xt);
+        free(q64);
+        free(dd);
+    }
+    if (bad_alloc) {
+        free(start); free(pairs); free(pd); free(pid);
+        return -2;
+    }
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+    {
+        double* ld = (double*)malloc(sizeof(double) * (size_t)K);
+        int64_t* li = (int64_t*)malloc(sizeof(int64_t) * (size_t)K);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t q = 0; q < B; ++q) {
+            for (int j = 0; j < K; ++j) { ld[j] = INFINITY; li[j] = INT64_MAX; }
+            for (int64_t e = q * nprobe; e < (q + 1) * nprobe; ++e)
+                for (int j = 0; j < K && pid[e * K + j] != INT64_MAX; ++j)
+                    insert_sorted(ld, li, K, pd[e * K + j], pid[e * K + j]);
+            for (int j = 0; j < K; ++j) {
+                const int valid = li[j] != INT64_MAX;
+                out_d[q * K + j] = valid ? ld[j] : INFINITY;
+                out_i[q * K + j] = valid ? li[j] : -1;
+            }
+        }
+        free(ld);
+        free(li);
+    }
+    free(start); free(pairs); free(pd); free(pid);
     return 0;
 }
 

@@ -158,6 +158,71 @@ def test_audit_known_answers():
     assert (b["exact_tie"], b["f32_rounding"], b["true_miss"]) == (1, 1, 1)
 
 
+@pytest.mark.parametrize("name", ["int_ties", "float_gmm", "short"])
+def test_cluster_major_golden_fixture(name):
+    """ivf_exact_cm (each list read once for all queries probing it) gives the fixture's result
+    bit for bit (same canonical distances, same (d, id) order)."""
+    z = np.load(os.path.join(GOLD, f"{name}.npz"), allow_pickle=False)
+    order, vec_off = sorted_lists(z["list_ids"], len(z["centroids"]))
+    d, i = O.ivf_exact_cm(z["xq"], z["probes"], vec_off, z["xb"][order], order, int(z["K"]))
+    d0, i0 = O.ivf_exact(z["xq"], z["probes"], vec_off, z["xb"][order], order, int(z["K"]))
+    assert np.array_equal(i, z["topk_i"]) and np.array_equal(i, i0)
+    assert np.array_equal(d, d0, equal_nan=True)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_cluster_major_matches_ivf_exact(seed):
+    """Random lists with heavy exact ties and duplicated rows, empty lists, K past the probed
+    rows, lists of fewer and more than the 256-row chunk and the 8-row groups, many queries per
+    cluster: the cluster-major scan equals the query-major one bit for bit, and numpy brute force
+    on the ids."""
+    rng = np.random.default_rng(100 + seed)
+    D = int(rng.integers(1, 70))
+    nlist = int(rng.integers(1, 12))
+    N = int(rng.integers(0, 3000))
+    xb = rng.integers(0, 3, size=(N, D)).astype(np.float32) if seed % 2 == 0 else \
+        rng.standard_normal((N, D)).astype(np.float32)
+    if N > 10:
+        xb[N // 2:N // 2 + 5] = xb[3]  # duplicated rows: ties broken by id
+    lid = rng.integers(0, max(nlist - 1, 1), size=N).astype(np.int32)  # the last list may be empty
+    cen = rng.standard_normal((nlist, D)).astype(np.float32)
+    xq = rng.integers(0, 3, size=(60, D)).astype(np.float32) if seed % 2 == 0 else \
+        rng.standard_normal((60, D)).astype(np.float32)
+    nprobe = int(rng.integers(1, nlist + 1))
+    K = int(rng.integers(1, 60))
+    order, vec_off = sorted_lists(lid, nlist)
+    cids, _ = O.coarse_probe(xq, cen, nprobe)
+    d0, i0 = O.ivf_exact(xq, cids, vec_off, xb[order], order, K)
+    d1, i1 = O.ivf_exact_cm(xq, cids, vec_off, xb[order], order, K, threads=3)
+    assert np.array_equal(i0, i1)
+    assert np.array_equal(d0, d1)
+    _, bi = O.np_ivf_exact(xq, xb, lid, cids, K)
+    assert np.array_equal(i1, bi)
+
+
+def test_pair_dists_against_numpy():
+    """pair_dists: the canonical distance of explicit (query, sorted row) pairs equals numpy's
+    float64 distance on integer data (every order exact) and is within 1e-13 on floats; a mutant
+    that swaps the query and row indices of the pairs fails."""
+    rng = np.random.default_rng(5)
+    for integer in (True, False):
+        xb = (rng.integers(0, 200, size=(40, 13)) if integer else rng.standard_normal((40, 13))).astype(np.float32)
+        xq = (rng.integers(0, 200, size=(7, 13)) if integer else rng.standard_normal((7, 13))).astype(np.float32)
+        qids = rng.integers(0, 7, size=50).astype(np.int32)
+        spos = rng.integers(0, 40, size=50).astype(np.int64)
+        got = O.pair_dists(xq, xb, qids, spos)
+        ref = ((xb[spos].astype(np.float64) - xq[qids].astype(np.float64)) ** 2).sum(1)
+        if integer:
+            assert np.array_equal(got, ref)
+        else:
+            np.testing.assert_allclose(got, ref, rtol=1e-13)
+        for i in range(0, 50, 7):  # each value is the canonical fma chain of its pair
+            assert got[i] == fma_exact_sum(xb[spos[i]], xq[qids[i]])
+        swapped = ((xb[np.minimum(qids, 39)].astype(np.float64) -
+                    xq[np.minimum(spos, 6)].astype(np.float64)) ** 2).sum(1)
+        assert not np.allclose(got, swapped, rtol=1e-6), "a swapped-index mutant was not detected"
+
+
 # ---- planted mistakes: each mutated oracle must fail the checks above ----
 
 def _mut_no_tiebreak(xq, xb, lid, probes, K):
