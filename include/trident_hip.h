@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TRIDENT_ABI_VERSION 3
+#define TRIDENT_ABI_VERSION 4
 
 enum TridentStatus {
     TRIDENT_OK = 0,
@@ -63,7 +63,10 @@ typedef struct TridentIndexView {
     const float* b_combined; /* [ldw]: [|c|^2 | b | 0], rotation x -> x R + b */
     double rot_sq_min;       /* lower bound on the squared singular values of R */
     double rot_sq_max;       /* upper bound on the squared singular values of R */
-    const uint32_t* sq8_packed;      /* [total_tiles, D_pad / 4, tile_size] */
+    const uint32_t* sq8_packed;      /* [total_tiles, D_pad / 4, tile_size]; may be NULL when
+                                        sq8_cells is set: mode 2 then takes the batched route
+                                        only (the per-pair route, modes 0 / 1 and
+                                        trident_sq8_bounds read it) */
     const int32_t* tile_orig_ids;    /* [total_tiles, tile_size], -1 padded */
     const float* tile_r_minmax;      /* [total_tiles, 2] residual-norm band, or NULL */
     const int32_t* cluster_tile_off; /* [nlist + 1] */
@@ -158,6 +161,10 @@ typedef struct TridentSearchOutputs {
     void* const* events;  /* hipEvent_t handles recorded at TridentStageEvent points, or NULL */
     int64_t* host_rows;   /* [1] base rows read from a host-mapped xb_sorted (4*D bytes each, over
                              PCIe: exact seeds, Stage Z, overflow rescans), or NULL */
+    int64_t* host_rows_seed; /* [1] the part of host_rows read by the first (seeding) pass:
+                                the exact seeds of the batched route, the first pass of the
+                                per-pair route; 0 for a device base; or NULL.  No reference
+                                counterpart (its per-pass PCIe split came from a profiler). */
 } TridentSearchOutputs;
 
 /* Timing events for TridentSearchOutputs.events (hipEventCreate / Destroy / ElapsedTime). */
@@ -230,15 +237,15 @@ int trident_sq8_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
                        void* workspace, size_t workspace_bytes, double* lb, double* ub,
                        void* stream);
 
-/* The fine-level bounds the out-of-core search uses, for (query, sorted-position) pairs:
- * lb[i] <= d64(q, x) <= ub[i].  No reference counterpart (exposed for bound-rigour tests).
- * workspace: >= trident_workspace_bytes(ix, B, 1, 1) bytes. */
 /* Fills cluster_bounds ([nlist, 4] float64, device) from delta, eps_dim and vec_Ar: per cluster
  * A_max >= every |code * delta|^2, r_max >= every stored residual bound, r_lo = the smallest
  * stored residual bound.  No reference counterpart (index-constant part of the batched route's
  * bounds, hoisted out of the search). */
 int trident_cluster_bounds(const TridentIndexView* ix, double* cluster_bounds, void* stream);
 
+/* The fine-level bounds the out-of-core search uses, for (query, sorted-position) pairs:
+ * lb[i] <= d64(q, x) <= ub[i].  No reference counterpart (exposed for bound-rigour tests).
+ * workspace: >= trident_workspace_bytes(ix, B, 1, 1) bytes. */
 int trident_fine_bounds(const TridentIndexView* ix, const float* xq, int32_t B,
                        const int32_t* qids, const int64_t* spos, int32_t n, void* workspace,
                        size_t workspace_bytes, double* lb, double* ub, void* stream);

@@ -156,6 +156,19 @@ def test_cells_hold_the_packed_codes(which, hist_ix, gmm_ix, wide_ix):
     assert cells.shape[1:] == (ix.tile_size // V, ix.D_pad // 16, V, 16)
 
 
+@pytest.mark.parametrize("which", ["hist", "gmm", "wide"])
+def test_packing_rebuilt_from_cells(which, hist_ix, gmm_ix, wide_ix):
+    """packed_from_cells inverts cells_from_packed bit for bit (narrow and wide cell blocks), so
+    an index that releases sq8_packed on the device still saves the reference packing; a
+    mutant that forgets the 0x80 flip is caught."""
+    from trident_amd.index import packed_from_cells
+    ix = {"hist": hist_ix, "gmm": gmm_ix, "wide": wide_ix}[which][0]
+    got = packed_from_cells(ix.sq8_cells, ix.D_pad, ix.tile_size)
+    assert got.dtype == torch.int32 and torch.equal(got, ix.sq8_packed.view_as(got))
+    flip = torch.tensor(-0x7f7f7f80, dtype=torch.int32)
+    assert not torch.equal(got ^ flip, ix.sq8_packed.view_as(got))
+
+
 @pytest.mark.parametrize("which", ["hist", "gmm"])
 def test_eps_bounds_quantisation_error(which, hist_ix, gmm_ix):
     ix = (hist_ix if which == "hist" else gmm_ix)[0]

@@ -148,3 +148,37 @@ def test_stage_z_rows_not_multiple_of_four(dev, placement):
         if placement == "host":
             torch.cuda.synchronize()
             b.ix.storage._host_buf.free()
+
+
+def test_sq8_cells_only_on_the_device(dev):
+    """The out-of-core configuration as the reference runs it: the base in mapped host memory,
+    the fine level dropped and the reference packing released, so the device holds the SQ8
+    codes once (the batched route's cells) plus ids and per-vector scalars.  Mode 2 takes the
+    batched route by itself (also where AUTO would choose the per-pair route), stays exact at
+    every ub_seed, reads survivors over PCIe, and refuses the per-pair route and modes 0 / 1."""
+    xb, xq = datagen.cfg2(N=30_000, D=128, B=300, n_centers=48, seed=95)
+    b = build_index(xb, 48, dev, xb_placement="host", max_batch=512)
+    ix = b.ix
+    try:
+        fp0 = ix.hbm_footprint()
+        ix.release_fine_level()
+        ix.release_packed_codes()
+        fp1 = ix.hbm_footprint()
+        assert "fine_codes" in fp0 and "sq8_packed" in fp0
+        assert "fine_codes" not in fp1 and "sq8_packed" not in fp1 and "xb_sorted" not in fp1
+        assert fp1["sq8_cells"] == ix.sq8_cells.numel() * 4 and fp1["total"] < fp0["total"]
+        xqd = _q(xq.numpy(), dev)
+        for K, nprobe, ub, B in ((10, 12, 0, 300), (10, 12, 1, 300), (10, 12, 2, 300), (5, 4, 1, 3)):
+            _, rd, ri = oracle_search(b, xq.numpy()[:B], nprobe, K)
+            assert ix.route_for(B, nprobe, K) == _lib.ROUTE_BATCHED
+            hr = torch.zeros(1, dtype=torch.int64, device=dev)
+            d, i, _ = ix.search(xqd[:B], nprobe, mode=2, k=K, ub_seed=ub, host_rows_buf=hr)
+            torch.cuda.synchronize()
+            assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"cells only K={K} ub={ub} B={B}")
+            assert int(hr[0]) >= K * B  # survivors cross PCIe: no fine level
+        for kw in (dict(mode=2, route=1), dict(mode=1), dict(mode=0, rerank_m=20)):
+            with pytest.raises((ValueError, RuntimeError)):
+                ix.search(xqd, 8, k=10, **kw)
+    finally:
+        torch.cuda.synchronize()
+        ix.storage._host_buf.free()

@@ -10,7 +10,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libtrident_hip.so")
 
 TRIDENT_OK = 0
-ABI_VERSION = 3  # TRIDENT_ABI_VERSION
+ABI_VERSION = 4  # TRIDENT_ABI_VERSION
 MODE_SQ8_RERANK = 0
 MODE_SQ8 = 1
 MODE_CASCADE = 2
@@ -52,7 +52,7 @@ ROUTE_AUTO, ROUTE_PAIR, ROUTE_BATCHED = 0, 1, 2
 class TridentSearchOutputs(ctypes.Structure):
     _fields_ = [("topk_d", _P), ("topk_i", _P), ("probe_cids", _P), ("probe_dqcs", _P),
                 ("probe_ld", _i32), ("n_events", _i32), ("tau_sq", _P), ("stats", _P),
-                ("events", ctypes.POINTER(_P)), ("host_rows", _P)]
+                ("events", ctypes.POINTER(_P)), ("host_rows", _P), ("host_rows_seed", _P)]
 
 
 # Stage boundaries recorded into TridentSearchOutputs.events (enum TridentStageEvent).

@@ -240,14 +240,23 @@ int validate_index(const TridentIndexView* ix) {
                           !(ix->cent_norm_max < INFINITY)))
         return fail(TRIDENT_ERR_INVALID_ARGUMENT,
                     "cent_rows needs cent_tiles, cent_norms and a finite cent_norm_max >= 0");
-    if ((int64_t)ix->nlist * 8 > 150 * 1024)
-        return fail(TRIDENT_ERR_UNSUPPORTED, "nlist=%d exceeds the LDS probe selector", ix->nlist);
     return TRIDENT_OK;
 }
 
-int validate_cascade_index(const TridentIndexView* ix) {
-    if (!ix->sq8_packed || !ix->vmin || !ix->delta || !ix->eps_dim || !ix->blk_bounds4)
+// The batched routes scan per-cluster counters in blocks of kBlock clusters and carry the block
+// totals in one block (unit_scan_carry_kernel: 2 nlist counters, at most kBlock blocks).
+constexpr int kMaxBatchedNlist = kBlock * kBlock / 2;
+
+// The SQ8 parameters every SQ8 route reads; the reference packing (sq8_packed) only where
+// `packed` (the per-pair scans, modes 0 / 1, the bound entry points).  A mode-2 index may carry
+// the batched route's cells (sq8_cells) alone: choose_route then takes the batched route.
+int validate_cascade_index(const TridentIndexView* ix, bool packed = true) {
+    if (!ix->vmin || !ix->delta || !ix->eps_dim || !ix->blk_bounds4)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "cascade route needs the SQ8 tensors");
+    if (packed && !ix->sq8_packed)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "this route reads sq8_packed, which the index view lacks");
+    if (!ix->sq8_packed && !ix->sq8_cells)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "the index view holds neither sq8_packed nor sq8_cells");
     return TRIDENT_OK;
 }
 
@@ -361,25 +370,35 @@ int dispatch_scan(const ScanArgs& a, int kind, hipStream_t st) {
 int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                  int nprobe, int* route) {
     const bool ok = ix->vec_Ar && ix->sq8_cells && ix->orig_ids_sorted && K <= 128 &&
-                    ix->D_pad <= 1024 &&
+                    ix->D_pad <= 1024 && ix->nlist <= kMaxBatchedNlist &&
                     ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
+    // an index without the reference packing (sq8_packed) has only the batched route
+    const bool pair_ok = ix->sq8_packed != nullptr;
     switch (sp->route) {
         case TRIDENT_ROUTE_PAIR:
+            if (!pair_ok)
+                return fail(TRIDENT_ERR_UNSUPPORTED,
+                            "the per-pair route reads sq8_packed, which the index view lacks");
             *route = TRIDENT_ROUTE_PAIR;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_BATCHED:
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
-                            "batched route needs vec_Ar, sq8_cells, K <= 128, D_pad <= 1024 and "
-                            "N < 2^27 "
-                            "(K=%d, D_pad=%d, N=%d)",
-                            K, ix->D_pad, ix->N);
+                            "batched route needs vec_Ar, sq8_cells, K <= 128, D_pad <= 1024, "
+                            "nlist <= %d and N < 2^27 (K=%d, D_pad=%d, nlist=%d, N=%d)",
+                            kMaxBatchedNlist, K, ix->D_pad, ix->nlist, ix->N);
             *route = TRIDENT_ROUTE_BATCHED;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_AUTO:
-            *route = (ok && (double)B * nprobe >= 8.0 * ix->nlist) ? TRIDENT_ROUTE_BATCHED
-                                                                 : TRIDENT_ROUTE_PAIR;
+            if (!pair_ok && !ok)
+                return fail(TRIDENT_ERR_UNSUPPORTED,
+                            "the index view lacks sq8_packed (per-pair route) and this search "
+                            "cannot take the batched route (K=%d, D_pad=%d, N=%d)",
+                            K, ix->D_pad, ix->N);
+            *route = (ok && (!pair_ok || (double)B * nprobe >= 8.0 * ix->nlist))
+                         ? TRIDENT_ROUTE_BATCHED
+                         : TRIDENT_ROUTE_PAIR;
             return TRIDENT_OK;
         default:
             return fail(TRIDENT_ERR_INVALID_ARGUMENT, "route=%d outside {0,1,2}", sp->route);
@@ -394,7 +413,7 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
 int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                     int nprobe, bool xb_host, bool* cm) {
     const bool ok = ix->orig_ids_sorted && !xb_host && K <= 16 && ix->D_pad <= 256 &&
-                    ix->N < (1 << 27) &&
+                    ix->nlist <= kMaxBatchedNlist && ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
         case TRIDENT_ROUTE_PAIR:
@@ -404,8 +423,9 @@ int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, i
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
                             "mode 10 batched route needs orig_ids_sorted, the base in device "
-                            "memory, K <= 16, D_pad <= 256 and N < 2^27 (K=%d, D_pad=%d, N=%d)",
-                            K, ix->D_pad, ix->N);
+                            "memory, K <= 16, D_pad <= 256, nlist <= %d and N < 2^27 (K=%d, "
+                            "D_pad=%d, nlist=%d, N=%d)",
+                            kMaxBatchedNlist, K, ix->D_pad, ix->nlist, ix->N);
             *cm = true;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_AUTO:
@@ -652,6 +672,11 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                 probe_dqcs, ld);
         return check_launch("select_probes_wave_kernel");
     }
+    // nprobe > 128: the radix selector keeps a query's nlist float64 keys in LDS
+    if ((int64_t)ix->nlist * 8 > 150 * 1024)
+        return fail(TRIDENT_ERR_UNSUPPORTED,
+                    "nprobe=%d > 128 needs nlist <= 19200 (the LDS probe selector); nlist=%d",
+                    nprobe, ix->nlist);
     const size_t dyn = (size_t)ix->nlist * sizeof(uint64_t);
     static bool attr_set = false;
     if (!attr_set) {
@@ -724,7 +749,7 @@ int group_pairs(const int32_t* probe_cids, const float* probe_dqcs, int ld, int 
         return rc;
     }
     if (joint) {
-        // nlist <= 19200 (validate_index), so the block totals fit one block's scan
+        // nlist <= kMaxBatchedNlist (choose_route), so the block totals fit one block's scan
         const int nblk = (nlist + kBlock - 1) / kBlock;
         scan_pairs_joint_local_kernel<<<nblk, kBlock, 0, st>>>(counts, nlist, seg_off, blk_tot);
         if ((rc = check_launch("scan_pairs_joint_local_kernel"))) return rc;
@@ -875,7 +900,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     const bool cascade = mode == TRIDENT_MODE_CASCADE;
     // modes 0 / 1: SQ8 reconstruction distance in the rotated space
     const bool hat = mode == TRIDENT_MODE_SQ8 || mode == TRIDENT_MODE_SQ8_RERANK;
-    if ((cascade || hat) && (rc = validate_cascade_index(ix))) return rc;
+    if ((cascade || hat) && (rc = validate_cascade_index(ix, hat))) return rc;
     if (sp->use_l1 && cascade && !ix->tile_r_minmax)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "use_l1 needs tile_r_minmax");
     if (mode == TRIDENT_MODE_TRIBASE && !ix->r_vec_sorted)
@@ -966,6 +991,16 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     unsigned long long* host_rows =
         out->host_rows && xb_host ? reinterpret_cast<unsigned long long*>(out->host_rows) : nullptr;
     if (out->host_rows && (rc = fill(reinterpret_cast<int32_t*>(out->host_rows), 0, 2, st))) return rc;
+    if (out->host_rows_seed &&
+        (rc = fill(reinterpret_cast<int32_t*>(out->host_rows_seed), 0, 2, st)))
+        return rc;
+    // at the end of the seeding pass: the rows it read from host memory so far
+    auto seed_rows = [&]() -> int {
+        if (!out->host_rows_seed || !host_rows) return TRIDENT_OK;
+        copy_u64_kernel<<<1, 64, 0, st>>>(host_rows,
+                                          reinterpret_cast<unsigned long long*>(out->host_rows_seed));
+        return check_launch("copy_u64_kernel");
+    };
     ScanArgs a = make_scan_args(ix, w, K, cap, cascade ? sp->use_l1 : 0,
                                 out->stats ? w.stat_slots : nullptr);
     a.r_vec = ix->r_vec_sorted;
@@ -1155,7 +1190,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         const int seed_all = sp->ub_seed == 2 ? 1 : 0;
         const int split_vec = ix->D_pad <= 256 ? kSplitVecNarrow : kSplitVec;
         {
-            const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= 150 (nlist <= 19200)
+            const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= kBlock (kMaxBatchedNlist)
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
                                                             ix->nlist, b.unit_q, seed_all,
                                                             split_vec, w.unit_off, w.grp_off,
@@ -1196,6 +1231,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                              (w.max_groups + kBlock / kGroupQ - 1) / (kBlock / kGroupQ), 1),
                          kBlock, 0, st>>>(b);
         if ((rc = check_launch("lb_prep_kernel"))) return rc;
+        if ((rc = seed_rows())) return rc;
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
         // pass B over every probe: lower bound, exact refine, append <= tau
         b.unit_beg = ix->nlist;
@@ -1280,6 +1316,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
     } else if ((rc = mark(TRIDENT_EV_P1_SCAN))) {
         return rc;
     }
+    if ((rc = seed_rows())) return rc;
     if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
     if (M2 > 0) {
         if ((rc = fill(w.cand_cnt, 0, B, st))) return rc;

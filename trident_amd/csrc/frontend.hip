@@ -13,6 +13,12 @@
 
 namespace trident {
 
+// One counter copied on the stream (a kernel, not a memcpy node, so that a captured graph
+// replays it like the kernels around it).
+__global__ void copy_u64_kernel(const unsigned long long* src, unsigned long long* dst) {
+    if (threadIdx.x == 0) *dst = *src;
+}
+
 __global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x)

@@ -171,6 +171,7 @@ struct BatchArgs {
 constexpr int kStatSlots = 64;  // telemetry counters are spread over this many [4] slots
 
 __global__ void fill_i32_kernel(int32_t* p, int32_t v, int64_t n);
+__global__ void copy_u64_kernel(const unsigned long long* src, unsigned long long* dst);
 
 __global__ void stats_fold_kernel(const unsigned long long* slots, int64_t* out);
 

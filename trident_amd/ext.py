@@ -107,8 +107,15 @@ class _Workspace:
         self.lock = threading.Lock()
 
 
+def _ws_key(device, stream):
+    d = torch.device(device)
+    if d.type == "cuda" and d.index is None:
+        d = torch.device("cuda", torch.cuda.current_device())
+    return (d, int(stream.cuda_stream))
+
+
 def _workspace_slot(device: torch.device, stream) -> _Workspace:
-    key = (device, int(stream.cuda_stream))
+    key = _ws_key(device, stream)
     with _ws_lock:
         slot = _ws_cache.get(key)
         if slot is None:
@@ -131,6 +138,16 @@ def _grow(slot: _Workspace, device, nbytes: int, st) -> torch.Tensor:
         with torch.cuda.stream(st):
             slot.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
     return slot.buf
+
+
+def release_workspace(device: torch.device, stream) -> None:
+    """Drop the workspace of one (device, stream); the next search on it allocates again."""
+    key = _ws_key(device, stream)
+    with _ws_lock:
+        slot = _ws_cache.pop(key, None)
+    if slot is not None:
+        with slot.lock:
+            slot.buf = None
 
 
 def release_workspaces() -> None:
@@ -301,6 +318,8 @@ def search_view(view: TridentIndexView, xq: torch.Tensor, nprobe: int, topk_d: t
     out.tau_sq = _ptr(tau_sq)
     out.stats = _ptr(stats)
     out.host_rows = _ptr(host_rows)
+    # a 2-entry host_rows buffer also receives the seeding pass's share in its second entry
+    out.host_rows_seed = host_rows.data_ptr() + 8 if host_rows is not None and host_rows.numel() >= 2 else None
     if stage_events is not None:
         out.events = stage_events.handles
         out.n_events = _lib.EV_COUNT
@@ -380,10 +399,17 @@ def launch_trident_v4_search(
     else:
         tile_r_minmax = None
     _need(not (int(use_l1) and mode == 2 and tile_r_minmax is None), "use_l1 needs tile_r_minmax")
-    if sq8:
+    # mode 2 on an index that keeps only the batched route's cells (TridentV4Index.
+    # release_packed_codes): an empty sq8_packed, and the batched route
+    packed = sq8 and not (mode == 2 and sq8_packed is not None and sq8_packed.numel() == 0 and
+                          sq8_cells is not None and vec_Ar is not None)
+    if sq8 and not packed:
+        _need(int(route) != 1, "the per-pair route reads sq8_packed, which this index released")
+    if packed:
         _check_tensor("sq8_packed", sq8_packed, torch.int32, dev)
         _need(sq8_packed.numel() == tiles * (D_pad // 4) * int(tile_size),
               "sq8_packed must hold [tiles, D_pad/4, tile_size] words")
+    if sq8:
         rows = nlist if int(per_cluster_sq8) else 1
         for name, t in (("vmin", vmin), ("delta", delta), ("eps_dim", eps_dim)):
             _check_tensor(name, t, torch.float32, dev)
@@ -454,7 +480,7 @@ def launch_trident_v4_search(
     view = make_index_view(
         N=N, D=D, D_pad=D_pad, nlist=nlist, tile_size=tile_size, per_cluster_sq8=per_cluster_sq8,
         W_combined=W_combined, b_combined=b_combined, rot_sq_min=rot_sq_bounds[0],
-        rot_sq_max=rot_sq_bounds[1], sq8_packed=sq8_packed if sq8 else None,
+        rot_sq_max=rot_sq_bounds[1], sq8_packed=sq8_packed if packed else None,
         tile_orig_ids=tile_orig_ids, tile_r_minmax=tile_r_minmax,
         cluster_tile_off=cluster_tile_off, cluster_vec_off=cluster_vec_off, xb_sorted=xb_sorted,
         orig_ids_sorted=orig_ids_sorted, vmin=vmin if sq8 else None,

@@ -79,6 +79,22 @@ def cells_from_packed(sq8_packed: torch.Tensor, D_pad: int, T: int) -> torch.Ten
     return cells
 
 
+def packed_from_cells(sq8_cells: torch.Tensor, D_pad: int, T: int) -> torch.Tensor:
+    """The reference tile packing [tiles, D_pad/4, T] from the batched route's cells (the
+    inverse of ``cells_from_packed``)."""
+    dev = sq8_cells.device
+    G16, V = D_pad // 16, cell_block(D_pad)
+    tiles = int(sq8_cells.numel()) // (G16 * T * 4)
+    cells = sq8_cells.view(tiles, T // V, G16, V, 4)
+    packed = torch.empty((tiles, D_pad // 4, T), device=dev, dtype=torch.int32)
+    flip = torch.tensor(-0x7f7f7f80, dtype=torch.int32, device=dev)  # 0x80808080
+    tstep = max(1, (1 << 24) // max(T * (D_pad // 4), 1))
+    for ts in range(0, tiles, tstep):
+        te = min(tiles, ts + tstep)
+        packed[ts:te] = (cells[ts:te].permute(0, 2, 4, 1, 3) ^ flip).reshape(te - ts, D_pad // 4, T)
+    return packed
+
+
 def derive_vec_Ar(sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted, W_combined, b_combined,
                   vmin, delta, per_cluster_sq8: int, nlist: int, T: int, chunk_rows: int = 1 << 20):
     """The batched route's per-vector scalars [N, 2] of any index in the reference layout, from
@@ -488,7 +504,67 @@ class TridentV4Index:
             self.topk_i_buf = torch.zeros((self.max_batch, self.k), device=self.dev, dtype=torch.int64)
 
     def sq8_bytes(self) -> int:
-        return int(self.sq8_packed.numel() * 4)
+        """Bytes of SQ8 codes held in HBM: the reference packing plus, when built, the batched
+        route's cells (the same codes regrouped)."""
+        n = int(self.sq8_packed.numel()) * 4
+        if getattr(self, "sq8_cells", None) is not None:
+            n += int(self.sq8_cells.numel()) * 4
+        return n
+
+    @property
+    def has_packed_codes(self) -> bool:
+        return int(self.sq8_packed.numel()) > 0
+
+    def release_packed_codes(self):
+        """Frees the reference-packed codes (``sq8_packed``) on the device, keeping the batched
+        route's cells (the same codes): mode 2 then runs the batched route only (the per-pair
+        route and modes 0 / 1 read the packing and are refused).  ``packed_codes()`` rebuilds
+        the packing from the cells when it is needed again (``save_index`` does)."""
+        if self.sq8_cells is None:
+            raise ValueError("the index has no sq8_cells: the packed codes are its only copy")
+        self.sq8_packed = torch.empty(0, dtype=torch.int32, device=self.dev)
+
+    def packed_codes(self) -> torch.Tensor:
+        """``sq8_packed`` [tiles, D_pad/4, T] (int32): the device tensor, or, once released, the
+        packing rebuilt from the cells (a new device tensor)."""
+        if self.has_packed_codes:
+            return self.sq8_packed
+        return packed_from_cells(self.sq8_cells, self.D_pad, self.tile_size)
+
+    def release_fine_level(self):
+        """Drops the fine level (``fine_codes``, ``fine_qp``): an out-of-core search then bounds
+        its seeds and survivors with the SQ8 codes alone and reads them from host memory."""
+        self.fine_codes = self.fine_qp = None
+
+    def hbm_footprint(self) -> dict:
+        """Bytes of every index tensor resident in device memory (the library's workspace and
+        the search buffers excluded), by name, plus their total under "total"."""
+        st = self.storage
+        named = {
+            "sq8_packed": self.sq8_packed, "sq8_cells": getattr(self, "sq8_cells", None),
+            "tile_orig_ids": self.tile_orig_ids, "tile_r_minmax": self.tile_r_minmax,
+            "vec_Ar": getattr(self, "vec_Ar", None), "r_vec_sorted": getattr(self, "r_vec_sorted", None),
+            "fine_codes": getattr(self, "fine_codes", None), "fine_qp": getattr(self, "fine_qp", None),
+            "cluster_bounds": getattr(self, "cluster_bounds", None),
+            "vmin_delta_eps": None, "centroids_and_projection": None,
+            "xb_sorted": st.xb_sorted, "orig_ids_sorted": st.orig_ids_sorted,
+            "list_ids_sorted": getattr(st, "list_ids_sorted", None),
+            "offsets": None,
+        }
+        out = {}
+        for k2, t in named.items():
+            if isinstance(t, torch.Tensor) and t.device.type == "cuda":
+                out[k2] = int(t.numel() * t.element_size())
+        small = lambda ts: sum(int(t.numel() * t.element_size()) for t in ts
+                               if isinstance(t, torch.Tensor) and t.device.type == "cuda")
+        out["vmin_delta_eps"] = small((self.vmin_pad, self.delta_pad, self.eps_pad))
+        out["centroids_and_projection"] = small(
+            (self.centroids, self.W_combined, self.b_combined, self.W_coarse_only, self.b_coarse_only)
+            + tuple(t for t in (self.cent_band or ()) if isinstance(t, torch.Tensor)))
+        out["offsets"] = small((self.cluster_tile_off, st.cluster_vec_off, self.blk_bounds4))
+        out = {k2: v for k2, v in out.items() if v}
+        out["total"] = sum(out.values())
+        return out
 
     def search(self, xq_gpu: torch.Tensor, nprobe: int, mode: int = 2, use_l1: int = 0, rerank_m: int = 0,
                tile_override: int = 0, warp_refine: int = 1, stats_buf: Optional[torch.Tensor] = None,
@@ -536,7 +612,8 @@ class TridentV4Index:
         return _ext.make_index_view(
             N=st.N, D=self.D, D_pad=self.D_pad, nlist=self.nlist, tile_size=self.tile_size,
             per_cluster_sq8=self.per_cluster_sq8, W_combined=self.W_combined, b_combined=self.b_combined,
-            rot_sq_min=self.rot_sq_min, rot_sq_max=self.rot_sq_max, sq8_packed=self.sq8_packed,
+            rot_sq_min=self.rot_sq_min, rot_sq_max=self.rot_sq_max,
+            sq8_packed=self.sq8_packed if self.has_packed_codes else None,
             tile_orig_ids=self.tile_orig_ids, tile_r_minmax=self.tile_r_minmax,
             cluster_tile_off=self.cluster_tile_off, cluster_vec_off=st.cluster_vec_off,
             xb_sorted=st.xb_sorted, orig_ids_sorted=st.orig_ids_sorted, vmin=self.vmin_pad,
