@@ -554,7 +554,8 @@ def main():
     t_l = roof["launch_ms"] * 1e-3
     # SURVEY's algorithmic bytes (every probed (query, list) pair's codes at full depth) and the
     # compulsory bytes (each probed list's codes once) of the dominant kernel's launch
-    byt_alg, byt_cmp = r["rows_all"] * (cfg["D"] + 31) // 32 * 32, r["rows_unique"] * (cfg["D"] + 31) // 32 * 32
+    D_pad = (cfg["D"] + 31) // 32 * 32
+    byt_alg, byt_cmp = r["rows_all"] * D_pad, r["rows_unique"] * D_pad
     hv = {"bytes_alg_per_launch": byt_alg, "alg_GBps": round(byt_alg / t_l / 1e9, 1),
           "alg_over_peak": round(byt_alg / t_l / 1e9 / HBM_PEAK_GBPS, 3),
           "bytes_compulsory_per_launch": byt_cmp, "compulsory_GBps": round(byt_cmp / t_l / 1e9, 1),

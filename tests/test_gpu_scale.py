@@ -185,3 +185,28 @@ def test_fp32_ivfflat_identity_by_audit(float_sets, dev, name, K):
     same = fi == i
     fin = same & np.isfinite(rd)
     np.testing.assert_allclose(fd[fin].astype(np.float64), rd[fin], rtol=1e-5)
+
+
+def test_configs0_at_its_stated_size(dev):
+    """BASELINE.json configs[0] exactly as stated: N = 100,000, D = 128, a 256-component
+    isotropic Gaussian mixture (centres U[0, 100], sigma 8), k-means nlist = 256, nprobe = 16,
+    K = 10, B = 1,000 queries from the same mixture, seed 0 -- generated and clustered on the
+    GPU as the bench does.  Every query is checked against the float64 oracle on both mode-2
+    routes, the auto route and mode 10."""
+    from trident_amd.index import SharedClusterStorage, TridentV4Index
+    N, D, nlist, nprobe, K, B = 100_000, 128, 256, 16, 10, 1_000
+    xb, xq = datagen.generate(1, device=dev, seed=0, N=N, D=D, B=B, n_centers=256)
+    cen, lid, r, mean64, R64, _ = clustering.train_clustering(xb, nlist, seed=0, niter=20, device=dev)
+    st = SharedClusterStorage(xb, lid, r, nlist, device=dev)
+    ix = TridentV4Index(st, cen, mean64, R64, tile_size=64, device=dev, max_batch=B, max_nprobe=128, k=K)
+    h = ix.host_arrays()
+    xq_np = xq.cpu().numpy()
+    cids, _ = O.coarse_probe(xq_np, h["centroids"], nprobe)
+    rd, ri = O.ivf_exact(xq_np, cids, h["vec_off"], h["xb_sorted"], h["orig_ids_sorted"], K)
+    assert ix.route_for(B, nprobe, K) == _lib.ROUTE_BATCHED
+    for mode, route, ub in ((2, 0, 1), (2, 1, 1), (2, 2, 0), (2, 2, 2), (10, 0, 0)):
+        d, i, _ = ix.search(xq.contiguous(), nprobe, mode=mode, k=K, ub_seed=ub, route=route)
+        torch.cuda.synchronize()
+        probes = ix.probe_cids_buf[:B, :nprobe].cpu().numpy()
+        assert np.array_equal(probes, cids), f"configs[0] probes mode={mode} route={route}"
+        assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"configs[0] mode={mode} route={route} ub={ub}")
