@@ -1044,11 +1044,6 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], bhi[ks], acc_hi, 0, 0, 0);
                 acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[ks], blo[ks], acc_lo, 0, 0, 0);
             }
-            // matrix-core results: 16 wait states (plus the compiler's padding) before the
-            // first read, fenced from the scheduler (see lb_scan_kernel)
-            __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_nop 7\n\ts_nop 7");
-            __builtin_amdgcn_sched_barrier(0);
             const float Av[4] = {A4.x, A4.y, A4.z, A4.w}, rv[4] = {r4.x, r4.y, r4.z, r4.w};
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -1094,9 +1089,6 @@ __global__ __launch_bounds__(256) void ub_scan_kernel(BatchArgs a) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], bhi[i], acc_hi, 0, 0, 0);
                 acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], blo[i], acc_lo, 0, 0, 0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_nop 7\n\ts_nop 7");
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
         };
@@ -1745,9 +1737,6 @@ void lb_scan_kernel(BatchArgs a) {
                     if constexpr (TWO)
                         h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(whi[1][ks], B[ks], h1, 0, 0, 0);
                 }
-                __builtin_amdgcn_sched_barrier(0);
-                asm volatile("s_nop 7\n\ts_nop 7");
-                __builtin_amdgcn_sched_barrier(0);
                 int mh = max(max(h0[0], h0[1]), max(h0[2], h0[3]));
                 if constexpr (TWO) mh = max(mh, max(max(h1[0], h1[1]), max(h1[2], h1[3])));
                 if (__ballot(mh >= thh) == 0ull) return;
@@ -1775,12 +1764,6 @@ void lb_scan_kernel(BatchArgs a) {
                     }
                 }
             }
-            // The matrix core does not interlock VALU reads of its results: 16 wait states (plus
-            // the compiler's own padding) between the last MFMA and the first accumulator read,
-            // fenced so that the scheduler cannot move either side across.
-            __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_nop 7\n\ts_nop 7");
-            __builtin_amdgcn_sched_barrier(0);
             // rows 4 g + r (queries), column j (vector li0 + j): S = acc + kq, exact in int32
             int S[2][4];
 #pragma unroll
@@ -2102,9 +2085,6 @@ __global__ __launch_bounds__(256) void lb_scan_wide_kernel(BatchArgs a) {
                 acc_hi = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], bhi[i], acc_hi, 0, 0, 0);
                 acc_lo = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[i], blo[i], acc_lo, 0, 0, 0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            asm volatile("s_nop 7\n\ts_nop 7");
-            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) S[r] = (acc_hi[r] << 8) + acc_lo[r];
         };
