@@ -182,3 +182,58 @@ def test_sq8_cells_only_on_the_device(dev):
     finally:
         torch.cuda.synchronize()
         ix.storage._host_buf.free()
+
+
+@pytest.mark.parametrize("placement", ["host", "device"])
+def test_overflowed_lists_are_rescanned_through_bounds(dev, placement):
+    """A candidate list that overflows its capacity is rescanned through the SQ8 bounds, not
+    exhaustively: the K-th smallest upper bound over the query's probed rows caps the threshold
+    and only rows whose lower bound passes it are read from host memory.  Explicit lists, nlist
+    8,192, base in mapped host memory: the three nearest clusters (the seeding probes) hold only
+    far rows, so the seeded threshold is loose and a dense shell of rows at distance 3 in the
+    other probed clusters overflows every list; the 10 true neighbours sit at distance 1.  The
+    result equals the oracle's, and each query reads fewer than 2 K nprobe rows (the exhaustive
+    rescan would read all 3,470 probed rows)."""
+    rng = np.random.default_rng(123)
+    D, nlist, nprobe, K, B = 16, 8192, 20, 10, 4
+
+    def sphere(n, radius, jitter=0.0):
+        u = rng.standard_normal((n, D))
+        u /= np.linalg.norm(u, axis=1, keepdims=True)
+        return radius * u * (1.0 + jitter * rng.standard_normal((n, 1)))
+
+    rows, lids = [], []
+    for c in range(3):                        # seeding probes: far rows only
+        rows.append(sphere(20, 10.0, 1e-2)); lids += [c] * 20
+    for c in range(3, nprobe):                # the shell: 17 x 200 rows at distance ~3
+        rows.append(sphere(200, 3.0, 1e-3)); lids += [c] * 200
+    rows.append(sphere(K, 1.0, 1e-2)); lids += [3] * K   # the true neighbours
+    far = nlist - nprobe                      # one distant row in every other cluster
+    rows.append(sphere(far, 1000.0, 1e-2)); lids += list(range(nprobe, nlist))
+    xb = torch.as_tensor(np.concatenate(rows).astype(np.float32))
+    cen = np.zeros((nlist, D), np.float32)
+    for c in range(nprobe):
+        cen[c, c % D] = 0.05 + 0.01 * c       # probe order: clusters 0, 1, 2, then the rest
+    cen[nprobe:] = sphere(far, 1000.0).astype(np.float32)
+    xq = np.zeros((B, D), np.float32)
+    xq[:, 0] = 0.001 * np.arange(B)
+    b = build_index(xb, nlist, dev, xb_placement=placement, list_ids=np.asarray(lids, np.int32),
+                    centroids=cen, max_batch=64, max_nprobe=128)
+    try:
+        cids, rd, ri = oracle_search(b, xq, nprobe, K)
+        assert (np.sort(cids[:, :3], 1) == [0, 1, 2]).all()
+        st = torch.zeros(4, dtype=torch.int64, device=dev)
+        hr = torch.zeros(2, dtype=torch.int64, device=dev)
+        d, i, _ = b.ix.search(_q(xq, dev), nprobe, mode=2, k=K, ub_seed=1, route=2, stats_buf=st,
+                              host_rows_buf=hr)
+        torch.cuda.synchronize()
+        assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"overflowed lists ({placement})")
+        cap = nprobe * max(K, 64) * (2 if placement == "host" else 1)  # a fine level doubles them
+        assert int(st[2]) > B * cap, (int(st[2]), B * cap)  # every list overflowed
+        if placement == "host":
+            stage_z = int(hr[0]) - int(hr[1])
+            assert stage_z < 2 * K * nprobe * B, (int(hr[0]), int(hr[1]))
+    finally:
+        torch.cuda.synchronize()
+        if b.ix.storage._host_buf is not None:
+            b.ix.storage._host_buf.free()

@@ -375,7 +375,7 @@ __global__ void fine_bounds_kernel(BatchArgs a, const int32_t* __restrict__ qids
 // spreads over many waves); each lane walks its own row in dimension order with 16-byte loads,
 // against the query row staged in LDS (DQ >= D floats per wave: 256, or 1024 for the wide
 // batched route).  An overflowed list (count > cap) is left alone: the merge rescans that
-// query's probes exhaustively.
+// query's probes through the SQ8 bounds (merge_kernel).
 template <bool HOST, int DQ>
 __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int B) {
     __shared__ __align__(16) float s_q[kWavesPerBlock][HOST ? 1 : DQ];  // host: float64 copy below

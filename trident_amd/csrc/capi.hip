@@ -562,12 +562,14 @@ int launch_batch(const BatchArgs& b, hipStream_t st) {
 
 int launch_merge(const MergeArgs& m, int KP, hipStream_t st) {
     const unsigned grid = (unsigned)((m.B + kWavesPerBlock - 1) / kWavesPerBlock);
+    // the bounded rescan stages 3 D_pad floats per wave (<= 48 KiB at D_pad 1024)
+    const size_t dyn = m.ovf_bounds ? (size_t)kWavesPerBlock * 3 * m.D_pad * sizeof(float) : 0;
     if (KP == 64)
-        merge_kernel<64><<<grid, kBlock, 0, st>>>(m);
+        merge_kernel<64><<<grid, kBlock, dyn, st>>>(m);
     else if (KP == 128)
-        merge_kernel<128><<<grid, kBlock, 0, st>>>(m);
+        merge_kernel<128><<<grid, kBlock, dyn, st>>>(m);
     else
-        merge_kernel<256><<<grid, kBlock, 0, st>>>(m);
+        merge_kernel<256><<<grid, kBlock, dyn, st>>>(m);
     return check_launch("merge_kernel");
 }
 
@@ -1278,6 +1280,18 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         m.tile_off = ix->cluster_tile_off;
         m.T = ix->tile_size;
         m.D = ix->D;
+        // an overflowed list is rescanned through the SQ8 bounds (rows near the top-K only)
+        m.ovf_bounds = 1;
+        m.cells = reinterpret_cast<const uint4*>(ix->sq8_cells);
+        m.vmin = ix->vmin;
+        m.delta = ix->delta;
+        m.eps = ix->eps_dim;
+        m.per_cluster = ix->per_cluster_sq8;
+        m.D_pad = ix->D_pad;
+        m.xrot64 = w.xrot64;
+        m.qerr = w.qerr;
+        m.lb_scale = a.lb_scale;
+        m.ub_scale = a.ub_scale;
         if ((rc = launch_merge(m, KP, st))) return rc;
         if ((rc = mark(TRIDENT_EV_END))) return rc;
         if (out->stats) {

@@ -58,8 +58,9 @@ struct MergeArgs {
     float* out_d;         // [B, K] or null (final pass only)
     int64_t* out_i;
     float* tau_sq_out;    // [B] or null
-    // Exhaustive fallback for a query whose candidate list overflowed `cap` (only the batched
-    // route appends without a per-pair cap): its probed lists are rescanned exactly.
+    // Rescan of a query whose candidate list overflowed `cap` (only the batched routes append
+    // without a per-pair cap): through the SQ8 bounds (ovf_bounds below), else every probed row
+    // refined exactly (mode 10's matrix route, whose index carries no SQ8 codes).
     const int32_t* probe_cids;  // [B, nprobe] or null (no fallback needed)
     int nprobe;
     const int32_t* vec_off;
@@ -69,6 +70,19 @@ struct MergeArgs {
     const int32_t* tile_off;
     int T, D;
     unsigned long long* host_rows;  // [1] rows read by the rescan (host-mapped base), or null
+    // Bounded rescan (ovf_bounds = 1, the batched cascade route): the overflowed query's probed
+    // rows get their Stage X / Y bounds from the SQ8 code cells and the per-dim parameters
+    // below; only rows whose lower bound passes the K-th smallest upper bound are read and
+    // refined.
+    int ovf_bounds;
+    const uint4* cells;         // [tiles, T / V, D_pad / 16, V] (bytes c ^ 0x80)
+    const float* vmin;
+    const float* delta;
+    const float* eps;
+    int per_cluster, D_pad;
+    const double* xrot64;       // [B, D_pad]
+    const double* qerr;         // [B, D_pad]
+    double lb_scale, ub_scale;  // as ScanArgs
 };
 
 // Per-(query, cluster) pair scalars of the batched bound (threshold-independent part).

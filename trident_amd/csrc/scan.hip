@@ -454,8 +454,85 @@ __global__ void stats_fold_kernel(const unsigned long long* slots, int64_t* out)
 
 // One wave per query: merges the pass's candidates (and the previous pass's list) into
 // the query's top list; writes the K-th distance and, on the final pass, the outputs.
+// Bounded rescan of an overflowed list (one wave, query q): pass UB = true offers every probed
+// row's Stage X upper bound (mapped to the float64 distance, as the per-pair scan) to L, so
+// that L's K-th entry bounds the K-th distance; pass UB = false reads and refines exactly only
+// the rows whose Stage Y lower bound does not exceed round_up(t * lb_scale) -- every row of the
+// exact top-K, since lb <= d64 <= t for them.  The per-dim constants of each (q, cluster) pair
+// are staged in the wave's LDS (3 D_pad floats); codes come from the batched route's cells
+// (c ^ 0x80, 16 dims a cell).
+template <int KP, bool UB>
+__device__ __forceinline__ void ovf_bounded_pass(const MergeArgs& a, int q, WaveList<KP>& L, double t,
+                                              float* s_par) {
+    const int lane = lane_id();
+    const int D_pad = a.D_pad, T = a.T, G16 = D_pad >> 4;
+    const int V = D_pad <= 256 ? 64 : 16;
+    float *s_bs = s_par, *s_dl = s_par + D_pad, *s_e = s_par + 2 * D_pad;
+    const double* qv = a.xq64 + (size_t)q * a.D;
+    const uint32_t tb = UB ? 0u : tau_bits_of(t, a.lb_scale);
+    for (int p = 0; p < a.nprobe; ++p) {
+        const int c = a.probe_cids[(size_t)q * a.nprobe + p];
+        const int v0 = a.vec_off[c], n = a.vec_off[c + 1] - v0, t0 = a.tile_off[c];
+        const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
+        wave_sync();  // the previous cluster's constants are no longer read
+        for (int d = lane; d < D_pad; d += kWave) {
+            float b32, e32;
+            dim_params((double)a.vmin[off + d], a.delta[off + d], a.eps[off + d],
+                       a.xrot64[(size_t)q * D_pad + d], a.qerr[(size_t)q * D_pad + d], b32, e32);
+            s_bs[d] = b32;
+            s_dl[d] = a.delta[off + d];
+            s_e[d] = e32;
+        }
+        wave_sync();
+        for (int b0 = 0; b0 < n; b0 += kWave) {
+            const int l = b0 + lane;
+            const bool in = l < n;
+            const int tile = t0 + (in ? l : 0) / T, slot = (in ? l : 0) % T;
+            float acc = 0.0f;
+            if (in) {
+                for (int g = 0; g < G16; ++g) {
+                    const uint4 cw = a.cells[((size_t)(tile * (T / V) + slot / V) * G16 + g) * V + slot % V];
+                    const uint32_t w[4] = {cw.x ^ 0x80808080u, cw.y ^ 0x80808080u,
+                                           cw.z ^ 0x80808080u, cw.w ^ 0x80808080u};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+#pragma unroll
+                        for (int by = 0; by < 4; ++by) {
+                            const int d = 16 * g + 4 * k + by;
+                            const uint32_t cd = (w[k] >> (8 * by)) & 0xffu;
+                            acc = UB ? ub_step(cd, s_dl[d], s_bs[d], s_e[d], acc)
+                                     : lb_step(cd, s_dl[d], s_bs[d], s_e[d], acc);
+                        }
+                }
+            }
+            if constexpr (UB) {
+                list_offer(L, a.K, in ? key_of((double)acc * a.ub_scale) : kKeyInvalid,
+                           in ? v0 + l : kIdInvalid);
+            } else {
+                const bool need = in && __float_as_uint(acc) <= tb;
+                if (a.host_rows && lane == 0)
+                    atomicAdd(a.host_rows, (unsigned long long)__popcll(__ballot(need)));
+                uint64_t k = kKeyInvalid;
+                int32_t id = kIdInvalid;
+                if (need) {
+                    const float* xr = a.xb + (size_t)(v0 + l) * a.D;
+                    double d64 = 0.0;
+                    for (int d = 0; d < a.D; ++d) {
+                        const double tt = (double)xr[d] - qv[d];
+                        d64 = fma(tt, tt, d64);
+                    }
+                    k = key_of(d64);
+                    id = a.tile_oids[(size_t)tile * T + slot];
+                }
+                list_offer(L, a.K, k, id);
+            }
+        }
+    }
+}
+
 template <int KP>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
+    extern __shared__ float s_ovf[];  // ovf_bounds: 3 D_pad floats per wave
     const int lane = threadIdx.x & 63;
     const int q = blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
     if (q >= a.B) return;
@@ -465,7 +542,20 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     int32_t* li = a.list_id + (size_t)q * KP;
     if (a.use_prev) list_load(L, lk, li);
     const int raw = a.cand_cnt[q];
-    if (raw > a.cap && a.probe_cids) {
+    if (raw > a.cap && a.probe_cids && a.ovf_bounds) {
+        // Overflowed list, SQ8 codes at hand: the K-th smallest upper bound over the probed rows
+        // (and the pass's threshold) bounds the K-th distance; only rows whose lower bound
+        // passes it are read and refined.
+        float* s_par = s_ovf + (threadIdx.x >> 6) * 3 * a.D_pad;
+        L.init();
+        ovf_bounded_pass<KP, true>(a, q, L, 0.0, s_par);
+        uint64_t kk;
+        int32_t ki;
+        L.at(a.K - 1, kk, ki);
+        const double t = fmin(a.tau64[q], kk != kKeyInvalid ? dist_of(kk) : (double)INFINITY);
+        L.init();
+        ovf_bounded_pass<KP, false>(a, q, L, t, s_par);
+    } else if (raw > a.cap && a.probe_cids) {
         // Overflowed list: rescan every probed vector exactly (canonical float64 distance).
         L.init();
         const double* qv = a.xq64 + (size_t)q * a.D;
