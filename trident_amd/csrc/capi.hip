@@ -151,8 +151,9 @@ inline int64_t plane_bytes(int D_pad) { return 64 * (int64_t)((D_pad + 63) / 64)
 
 // Candidate-list slots per query.  The batched route stores every lower-bound survivor there
 // (before its exact test), so lists are at least 64 * nprobe deep (12 bytes a slot; only used
-// slots are touched): a longer list makes the merge rescan that query's probes exhaustively,
-// which with the base in host memory crosses PCIe for every probed row.  Past 64 neighbours in
+// slots are touched): a longer list makes the merge rescan that query's probes (computing the
+// SQ8 bounds of every probed row, one wave per query, and refining the rows near the top-K),
+// so the lists are sized to make that rare.  Past 64 neighbours in
 // more than 256 dims the K-th distance sits in the bulk of the distance distribution (cfg 3,
 // K = 100: ~1 % of candidates pass, ~2,300 per query with a long tail), so those lists are 8x
 // deeper.  An index with a fine level keeps its base in host memory, where an overflow costs
