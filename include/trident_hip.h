@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TRIDENT_ABI_VERSION 4
+#define TRIDENT_ABI_VERSION 5
 
 enum TridentStatus {
     TRIDENT_OK = 0,
@@ -111,6 +111,12 @@ typedef struct TridentIndexView {
      * reference): [nlist, 4] float64 filled once per index by trident_cluster_bounds.  When
      * NULL every batched search recomputes them, one pass over vec_Ar (8 N bytes). */
     const double* cluster_bounds;
+    /* Per-row code norms of the batched route's lower-bound pass (optional; no counterpart in the
+     * reference): [N] float32 in sorted order, >= sqrt(sum_d (code_d - 128)^2) over the D_pad
+     * dims.  With them the pass bounds the lo weight plane's share of each row's sum by
+     * Cauchy-Schwarz (the row's norm times the query block's largest lo-plane norm) instead of
+     * 128 sum |lo|, so fewer tiles need the lo plane; NULL keeps the per-query bound. */
+    const float* vec_cn;
 } TridentIndexView;
 
 /* How modes 2 and 10 are executed.  Both routes are exact; they differ in speed only.  Mode 10

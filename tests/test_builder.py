@@ -349,3 +349,35 @@ def test_fine_codes_bound_the_rotated_rows():
     # 16 bits per dimension: far below the SQ8 residual norm
     r1 = ix.vec_Ar[:, 1].double().numpy()
     assert np.median(rho / r1) < 0.05
+
+
+
+@pytest.mark.parametrize("which", ["hist", "gmm", "wide"])
+def test_row_code_norms(which, hist_ix, gmm_ix, wide_ix):
+    """vec_cn: per sorted row, sqrt(sum (code - 128)^2) over D_pad dims rounded up to float32 --
+    checked against the codes unpacked from sq8_packed (the reference tile packing, not the
+    cells the norms are computed from) with an exact integer sum; and the Cauchy-Schwarz bound
+    it feeds (|sum (code - 128) lo| <= cn |lo|) against random int8 lo planes."""
+    ix = {"hist": hist_ix, "gmm": gmm_ix, "wide": wide_ix}[which][0]
+    st = ix.storage
+    T, D_pad = ix.tile_size, ix.D_pad
+    vec_off = st.cluster_vec_off.long().numpy()
+    tile_off = ix.cluster_tile_off.long().numpy()
+    packed = ix.sq8_packed.view(torch.uint8).reshape(-1, D_pad // 4, T, 4).numpy()
+    cn = ix.vec_cn.numpy()
+    assert cn.dtype == np.float32 and cn.shape == (st.N,)
+    rng = np.random.default_rng(3)
+    for c in range(ix.nlist):
+        loc = np.arange(vec_off[c + 1] - vec_off[c])
+        codes = packed[tile_off[c] + loc // T, :, loc % T, :].reshape(len(loc), -1).astype(np.int64)
+        ssq = ((codes - 128) ** 2).sum(1)
+        got = cn[vec_off[c]:vec_off[c + 1]].astype(np.float64)
+        assert np.all(got ** 2 >= ssq)                                        # upper bounds
+        # at most one float32 step above the least upper bound (the 2^-50 raise before rounding
+        # moves exact squares up by one step)
+        z = np.float32(0)
+        below2 = np.nextafter(np.nextafter(cn[vec_off[c]:vec_off[c + 1]], z), z).astype(np.float64)
+        assert np.all((below2 ** 2 < ssq) | (ssq == 0))
+        lo = rng.integers(-128, 128, size=(len(loc), D_pad))
+        dots = np.abs(((codes - 128) * lo).sum(1)).astype(np.float64)
+        assert np.all(dots <= got * np.sqrt((lo * lo).sum(1).astype(np.float64)))

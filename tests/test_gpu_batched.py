@@ -51,6 +51,35 @@ def test_batched_matches_pair_route_and_auto(sets, dev):
     assert np.array_equal(i0, i2) and np.array_equal(d0, d2)
 
 
+@pytest.mark.parametrize("name", ["hist", "norm96", "gmm"])
+def test_row_norm_allowance_changes_no_result(sets, dev, name):
+    """The lower-bound pass's hi-plane prefilter with the per-row code norms (vec_cn: a
+    Cauchy-Schwarz allowance for the lo plane) and without them (128 sum |lo| per query): the
+    prefilter only decides which tiles need the lo plane, so the results are identical, and
+    exact, and so is the candidate count.  (The survivor count is not compared: the order in
+    which a cluster's pairs land in its segment comes from atomics, and it decides which 32
+    queries share a weight group's scale, so it varies between identical runs.)"""
+    b, xq = sets[name]
+    ix = b.ix
+    xqd = _q(xq, dev)
+    for K, nprobe in ((1, 8), (10, 24), (100, 24)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        out = []
+        for keep in (True, False):
+            saved = ix.vec_cn
+            if not keep:
+                ix.vec_cn = None
+            try:
+                st = torch.zeros(4, dtype=torch.int64, device=dev)
+                d, i = run_search(b, xqd, nprobe, K, mode=2, ub=1, route=2, stats=st)
+            finally:
+                ix.vec_cn = saved
+            assert_exact(d, i, rd, ri, f"batched {name} K={K} nprobe={nprobe} row norms={keep}")
+            out.append((d, i, st.cpu().numpy()))
+        assert np.array_equal(out[0][1], out[1][1]) and np.array_equal(out[0][0], out[1][0])
+        assert out[0][2][0] == out[1][2][0] and out[0][2][1] == out[1][2][1], (out[0][2], out[1][2])
+
+
 @pytest.mark.parametrize("nprobe", [1, 2, 3])
 def test_batched_small_nprobe_and_single_query(sets, dev, nprobe):
     """nprobe 1 has no seeding pass (every candidate survives, candidate lists overflow and the

@@ -97,8 +97,9 @@ def test_reference_arguments_only_take_the_batched_route(opt_sets, dev):
         assert len(ext._derived_cache) == 1
         _, rd, ri = oracle_search(b, xq, nprobe, K)
         assert_exact(topk_d.cpu().numpy(), topk_i.cpu().numpy(), rd, ri, "reference arguments only")
-    vec_Ar, cells, band = next(iter(ext._derived_cache.values()))
+    vec_Ar, cells, band, vec_cn = next(iter(ext._derived_cache.values()))
     assert torch.equal(vec_Ar, ix.vec_Ar) and torch.equal(cells, ix.sq8_cells)
+    assert torch.equal(vec_cn, ix.vec_cn)
     # with the derived layouts the library picks the batched route for this batch
     view = ext.make_index_view(
         N=ix.N, D=ix.D, D_pad=ix.D_pad, nlist=ix.nlist, tile_size=ix.tile_size,

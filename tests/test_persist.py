@@ -16,7 +16,7 @@ from trident_amd.index import SharedClusterStorage, TridentV4Index
 
 _TENSORS = ("centroids", "W_combined", "b_combined", "W_coarse_only", "b_coarse_only", "vmin_pad",
             "delta_pad", "eps_pad", "blk_bounds4", "tile_r_minmax", "cluster_tile_off", "sq8_packed",
-            "sq8_cells", "tile_orig_ids", "vec_Ar", "r_vec_sorted")
+            "sq8_cells", "tile_orig_ids", "vec_Ar", "vec_cn", "r_vec_sorted")
 _STORAGE = ("xb_sorted", "orig_ids_sorted", "cluster_vec_off", "list_ids_sorted")
 
 

@@ -676,7 +676,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         for (int i = 0; i < 8 && ldexpf(l1u, -es) > lim; ++i) ++es;
     }
     const float s = ldexpf(1.0f, es), inv_s = ldexpf(1.0f, -es);
-    int wsum = 0, lsum = 0;  // sum w_int, sum |lo|
+    int wsum = 0, lsum = 0, lsq = 0;  // sum w_int, sum |lo|, sum lo^2 (<= 2^14 DP)
     int8_t* hi_p = a.pw + (size_t)pp * 2 * DP;
 #pragma unroll KEEP ? KS : 1
     for (int k = 0; k < KS; ++k) {
@@ -693,7 +693,9 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     wi[e] = (int)rintf(wk[16 * h2 + 4 * h + e] * inv_s);  // 0 for dims >= D_pad
                     wsum += wi[e];
-                    lsum += abs((int)(int8_t)(wi[e] & 0xff));
+                    const int lo = (int)(int8_t)(wi[e] & 0xff);
+                    lsum += abs(lo);
+                    lsq += lo * lo;
                 }
                 // lo = the low byte of wi as int8, hi = (wi - lo) / 256 = the second byte of
                 // wi + 128
@@ -713,6 +715,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
     }
     wsum += __shfl_xor(wsum, 1, kWave);
     lsum += __shfl_xor(lsum, 1, kWave);
+    lsq += __shfl_xor(lsq, 1, kWave);
     if (valid && l == 0) {
         PairRec r;
         r.Qp = (double)Qp;
@@ -729,6 +732,7 @@ __global__ __launch_bounds__(256) void pair_prep_kernel(BatchArgs a) {
         r.r_max = a.cbound[kCbStride * c + 1];
         r.acc_max = 128.0 * (l1 * (double)inv_s + 0.5 * (double)D_pad);
         r.lo_max = 128.0 * (double)lsum;  // <= 128 * 128 * D_pad <= 2^24
+        r.lo_l2 = sqrt((double)lsq) * (1.0 + 0x1p-50);  // lsq is exact; sqrt within half an ulp
         a.prec[pp] = r;
     }
 }
@@ -1492,10 +1496,13 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     const double c1_0 = shfl_f64(c1, lane & ~31);
     int bad = valid && (!thr || c1 != c1_0);
     float tqw = valid ? tqf : 0.0f;
+    // lo_l2 / 256 is exact in float64 (a power of two), rounded up to float32
+    float low = valid && a.vec_cn ? __double2float_ru(pr.lo_l2 * 0x1p-8) : 0.0f;
 #pragma unroll
     for (int o = 1; o < kGroupQ; o <<= 1) {
         bad |= __shfl_xor(bad, o, kWave);
         tqw = fmaxf(tqw, __shfl_xor(tqw, o, kWave));
+        low = fmaxf(low, __shfl_xor(low, o, kWave));
     }
     bool ok = !bad && c1_0 >= 0x1p-100 && c1_0 <= 0x1p100;
     if (ok && valid) {
@@ -1511,8 +1518,11 @@ __global__ __launch_bounds__(256) void lb_prep_kernel(BatchArgs a) {
     L.int_ok = !nok;
     L.tqw = tqw;
     L.inv_c1w = L.int_ok ? (float)(1.0 / c1_0) : 0.0f;  // a power of two in [2^-100, 2^100]
-    // |kq| <= 2^30 and lo_max <= 2^24: no int32 overflow
-    L.kq_pre = L.int_ok ? L.kq + (int)pr.lo_max : 0;
+    // The hi-plane prefilter's allowance for the lo plane: with row norms, lo_w * 256 * cn_x per
+    // row (Cauchy-Schwarz against the group's largest lo-plane norm), else lo_max per query
+    // (|kq| <= 2^30 and lo_max <= 2^24: no int32 overflow).
+    L.lo_w = low;
+    L.kq_pre = !L.int_ok ? 0 : a.vec_cn ? L.kq : L.kq + (int)pr.lo_max;
     if (valid) {
         a.lbr[p] = L;
         a.lbk[p] = make_int2(L.kq, L.kq_pre);
@@ -1546,9 +1556,9 @@ void lb_scan_kernel(BatchArgs a) {
     __shared__ uint4 s_codes[NBUF][SB][KS * 4 * BV];
     __shared__ __align__(16) float s_A[NBUF][BR];
     __shared__ __align__(16) float s_r[NBUF][BR];
+    __shared__ __align__(16) float s_cn[NBUF][BR];  // row code norms (vec_cn)
     __shared__ uint32_t s_sq[kWavesPerBlock][kLbQ];
-    __shared__ int s_scnt[kWavesPerBlock][QW], s_sbase[kWavesPerBlock][QW],
-        s_sqid[kWavesPerBlock][QW];
+    __shared__ int s_scnt[kWavesPerBlock][QW], s_sbase[kWavesPerBlock][QW];
     __shared__ float4 s_qf[kWavesPerBlock][QW];  // per query slot: (c1f, c2f, H32, -)
     // per query slot: kq, the lo-plane accumulators' start (empty slots INT_MIN); read only by
     // tiles that pass the hi-plane prefilter, so it is not held in registers
@@ -1603,7 +1613,7 @@ void lb_scan_kernel(BatchArgs a) {
         // ---- this wave's queries: weight rows and the constants of lb_prep_kernel ----
         v4i whi[2][KS], wlo[2][KS], hq4[2];
         bool int_ok = false;
-        float tqw = 0.0f, inv_c1w = 0.0f;
+        float tqw = 0.0f, inv_c1w = 0.0f, lo_w = 0.0f;
         if (active) {
             // every prologue load is issued before the first use (one memory round trip): the
             // group's constants, the (kq, kq_pre) of the lane's rows (lbk is padded by 32
@@ -1630,6 +1640,7 @@ void lb_scan_kernel(BatchArgs a) {
             int_ok = __builtin_amdgcn_readfirstlane(L0.int_ok) != 0;
             tqw = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.tqw)));
             inv_c1w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.inv_c1w)));
+            lo_w = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(L0.lo_w)));
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 // C rows this lane receives: queries 16 h + 4 g + r (empty rows: INT_MIN)
@@ -1645,7 +1656,6 @@ void lb_scan_kernel(BatchArgs a) {
                 const bool hv = lane < nq;
                 const LbRec L = a.lbr[pb + (hv ? lane : 0)];
                 s_kq[wid][lane] = hv ? L.kq : INT_MIN;
-                s_sqid[wid][lane] = a.pair_qid[pb + (hv ? lane : 0)];
                 s_qf[wid][lane] = hv ? make_float4(L.c1f, L.c2f, L.H32, 0.0f)
                                      : make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // never passes
             }
@@ -1661,14 +1671,14 @@ void lb_scan_kernel(BatchArgs a) {
         // ---- survivor queue (entries li << 5 | query slot) ----
         int nsq = 0;
         // the integer thresholds th of the block's rows sb * 64 + lane, and their hi-plane form
-        // thh = floor((th - 1) / 256) + 1 (256 h < th iff h < thh)
+        // thh = floor((th - 1) / 256) + 1 - cb (256 (h + cb) < th iff h < thh)
         int thr_r[SB], thh_r[SB];
         auto flush = [&]() __attribute__((always_inline)) {
             for (int e = lane; e < nsq; e += kWave) atomicAdd(&s_scnt[wid][s_sq[wid][e] & 31u], 1);
             __builtin_amdgcn_wave_barrier();
             if (lane < QW) {
                 const int c = s_scnt[wid][lane];
-                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[s_sqid[wid][lane]], c) : 0;
+                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[a.pair_qid[pb + lane]], c) : 0;
                 s_scnt[wid][lane] = 0;
             }
             __builtin_amdgcn_wave_barrier();
@@ -1677,7 +1687,7 @@ void lb_scan_kernel(BatchArgs a) {
                 const int jj = (int)(ent & 31u);
                 const int slot = s_sbase[wid][jj] + atomicAdd(&s_scnt[wid][jj], 1);
                 if (slot < a.cap)
-                    a.cand_id[(size_t)s_sqid[wid][jj] * a.cap + slot] = v0 + (int)(ent >> 5);
+                    a.cand_id[(size_t)a.pair_qid[pb + jj] * a.cap + slot] = v0 + (int)(ent >> 5);
             }
             __builtin_amdgcn_wave_barrier();
             if (lane < QW) s_scnt[wid][lane] = 0;
@@ -1725,10 +1735,11 @@ void lb_scan_kernel(BatchArgs a) {
                 thh = __builtin_amdgcn_ds_bpermute(src, SB == 1 || (t >> 2) == 0 ? thh_r[0] : thh_r[SB - 1]);
             v4i h0 = {0, 0, 0, 0}, l0 = {0, 0, 0, 0}, h1 = {0, 0, 0, 0}, l1 = {0, 0, 0, 0};
             if constexpr (INT) {
-                // Hi plane first, started at ceil(kq_pre / 256) per row: S = 256 acc_hi + acc_lo
-                // + kq <= 256 h with |acc_lo| <= lo_max, so a tile whose rows all have
-                // h < floor((th - 1) / 256) + 1 (i.e. 256 h < th) fails the exact test too and
-                // costs no lo-plane work.
+                // Hi plane first, started at ceil(kq_pre / 256) per row, so that
+                // S = 256 acc_hi + acc_lo + kq <= 256 h + 256 cb_x with cb_x the row's lo-plane
+                // allowance (0 when kq_pre carries lo_max, else ceil(cn_x lo_w) >= |acc_lo| / 256
+                // by Cauchy-Schwarz).  A tile whose rows all have h < thh (256 (h + cb_x) < th)
+                // fails the exact test too and costs no lo-plane work.
                 h0 = hq4[0];
                 h1 = hq4[1];
 #pragma unroll
@@ -1814,6 +1825,9 @@ void lb_scan_kernel(BatchArgs a) {
         // cell G16 * v0 and the next block to load is one pointer step away (no per-block
         // tile / slot arithmetic in the scalar unit).
         const uint4* next_blk = a.cells + (size_t)t0 * G16 * T + (size_t)G16 * vb;
+        // row norms: without vec_cn the A values stand in (finite; lo_w = 0 then)
+        const void* cn_base = a.vec_cn ? (const void*)(a.vec_cn + v0) : (const void*)(a.vec_Ar + v0);
+        const int cn_sh = a.vec_cn ? 2 : 3;
         auto gload = [&](int buf, int blk0) __attribute__((always_inline)) {
 #pragma unroll
             for (int sb = 0; sb < SB; ++sb) {
@@ -1832,16 +1846,17 @@ void lb_scan_kernel(BatchArgs a) {
             if (wid == 0) {  // rows past the slice read the slice's last row (never used)
 #pragma unroll
                 for (int sb = 0; sb < SB; ++sb) {
-                    const uint32_t off = 8u * (uint32_t)min(blk0 + sb * BV + lane, ve - 1);
-                    load_lds4(a.vec_Ar + v0, off, &s_A[buf][sb * BV]);
-                    load_lds4(a.vec_Ar + v0, off + 4u, &s_r[buf][sb * BV]);
+                    const uint32_t row = (uint32_t)min(blk0 + sb * BV + lane, ve - 1);
+                    load_lds4(a.vec_Ar + v0, 8u * row, &s_A[buf][sb * BV]);
+                    load_lds4(a.vec_Ar + v0, 8u * row + 4u, &s_r[buf][sb * BV]);
+                    load_lds4(cn_base, row << cn_sh, &s_cn[buf][sb * BV]);
                 }
             }
             next_blk += (size_t)G16 * BR;
         };
         const int nblk = (ve - vb + BR - 1) / BR;
         // direct loads this wave issues per block (its code groups, plus the row scalars)
-        int nl = wid == 0 ? 2 * SB : 0;
+        int nl = wid == 0 ? 3 * SB : 0;
 #pragma unroll
         for (int jj = 0; jj < KS; ++jj) nl += wid + 4 * jj < G16 ? SB : 0;
 #pragma unroll
@@ -1876,7 +1891,10 @@ void lb_scan_kernel(BatchArgs a) {
                     const float A = s_A[buf][i], r = s_r[buf][i];
                     const int th = lb_thr(A, r, tqw, inv_c1w);  // rows past the slice: INT_MAX
                     thr_r[sb] = blk0 + i < ve ? th : INT_MAX;
-                    thh_r[sb] = ((thr_r[sb] - 1) >> 8) + 1;
+                    // the lo plane's allowance in hi units: ceil(cn lo_w) >= |acc_lo| / 256
+                    // (the product's rounding is covered by the 2^-20 raise)
+                    const float p = s_cn[buf][i] * lo_w;
+                    thh_r[sb] = ((thr_r[sb] - 1) >> 8) + 1 - (int)ceilf(fmaf(p, 0x1p-20f, p));
                 }
                 if (two) tiles(std::true_type{}, std::true_type{}, buf, blk0);
                 else tiles(std::true_type{}, std::false_type{}, buf, blk0);

@@ -1130,6 +1130,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.eps = ix->eps_dim;
         b.orig_ids = ix->orig_ids_sorted;
         b.vec_Ar = reinterpret_cast<const float2*>(ix->vec_Ar);
+        b.vec_cn = ix->vec_cn;
         b.D = ix->D;
         b.D_pad = ix->D_pad;
         b.T = ix->tile_size;

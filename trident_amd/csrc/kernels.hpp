@@ -96,6 +96,7 @@ struct PairRec {
     double r_max;    // >= r_x for every vector of the cluster
     double acc_max;  // >= |sum c'_d w_int,d|
     double lo_max;   // 128 * sum |lo_d| >= |sum c'_d lo_d| (the lo plane's share of the sum)
+    double lo_l2;    // >= sqrt(sum lo_d^2): |sum c'_d lo_d| <= |c'|_2 lo_l2 (Cauchy-Schwarz)
 };
 
 // Per-pair constants of the batched lower-bound scan (they depend on tau, so they are computed
@@ -107,7 +108,9 @@ struct LbRec {
     float tqw;         // the group's largest tq, rounded up
     float inv_c1w;     // 1 / c1 of the group (a power of two)
     int32_t int_ok;    // the group takes the integer test
-    int32_t kq_pre;    // kq + lo_max: with the hi plane alone, acc_hi * 256 + kq_pre >= the sum
+    int32_t kq_pre;    // with the hi plane alone, acc_hi * 256 + kq_pre + lo_w * 256 * cn_x >= the
+                       // sum: kq + lo_max and lo_w = 0 without row norms, else kq
+    float lo_w;        // the group's largest lo_l2 / 256, rounded up (0 without row norms)
 };
 
 // Everything one cluster-batched scan launch reads (csrc/batch.hip).
@@ -123,6 +126,7 @@ struct BatchArgs {
     const float* eps;           // per-dim |x_rot - x_hat| bound (bounds r_x for the f32 slack)
     const int32_t* orig_ids;    // [N] sorted position -> original id
     const float2* vec_Ar;       // [N] (A rounded down, r rounded up)
+    const float* vec_cn;        // [N] >= |code - 128|_2 per row, or null
     int D, D_pad, T, per_cluster;
     const float* xq;            // [B, D] float32 queries
     const double* xrot64;       // [B, D_pad]

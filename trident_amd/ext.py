@@ -40,7 +40,7 @@ _ws_lock = threading.Lock()
 _ws_cache = {}
 _rot_cache = {}
 _derived_lock = threading.Lock()
-_derived_cache = {}  # index identity -> (vec_Ar, sq8_cells, cent_band), at most two indexes
+_derived_cache = {}  # index identity -> (vec_Ar, sq8_cells, cent_band, vec_cn), at most two indexes
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -163,7 +163,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
                     eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
                     cent_band=None, r_vec_sorted=None, fine_codes=None, fine_qp=None,
-                    cluster_bounds=None) -> TridentIndexView:
+                    cluster_bounds=None, vec_cn=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -188,6 +188,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.fine_codes = _ptr(fine_codes)
     v.fine_qp = _ptr(fine_qp)
     v.cluster_bounds = _ptr(cluster_bounds)
+    v.vec_cn = _ptr(vec_cn)
     if cent_band is not None:
         rows, tiles, norms, nmax = cent_band
         v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
@@ -235,10 +236,11 @@ def _identity(*ts):
 
 def derived_layouts(W_combined, b_combined, sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted,
                     vmin, delta, per_cluster_sq8: int, nlist: int, tile_size: int):
-    """(vec_Ar, sq8_cells, cent_band) for an index passed in the reference layout alone, derived
-    once per index (tensor identities and versions) and cached: the per-vector scalars measured
-    on the data (index.derive_vec_Ar), the code cells regrouped from sq8_packed
-    (index.cells_from_packed) and the centroid layouts of the matrix-core coarse pass."""
+    """(vec_Ar, sq8_cells, cent_band, vec_cn) for an index passed in the reference layout alone,
+    derived once per index (tensor identities and versions) and cached: the per-vector scalars
+    measured on the data (index.derive_vec_Ar), the code cells regrouped from sq8_packed
+    (index.cells_from_packed), the centroid layouts of the matrix-core coarse pass and the
+    per-row code norms (index.derive_vec_cn)."""
     from . import index as _index
     key = _identity(W_combined, b_combined, sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted,
                     vmin, delta) + (int(per_cluster_sq8), int(nlist), int(tile_size))
@@ -252,10 +254,11 @@ def derived_layouts(W_combined, b_combined, sq8_packed, cluster_vec_off, cluster
                                       tile_size)
         cells = _index.cells_from_packed(sq8_packed, D_pad, int(tile_size))
         band = centroid_band_layouts(W_combined, nlist)
+        vec_cn = _index.derive_vec_cn(cells, cluster_vec_off, cluster_tile_off, D_pad, int(tile_size))
         if len(_derived_cache) >= 2:
             _derived_cache.pop(next(iter(_derived_cache)))
-        _derived_cache[key] = (vec_Ar, cells, band)
-        return vec_Ar, cells, band
+        _derived_cache[key] = (vec_Ar, cells, band, vec_cn)
+        return vec_Ar, cells, band, vec_cn
 
 
 def derived_r_vec(W_combined, cluster_vec_off, xb_sorted, nlist: int, chunk_rows: int = 1 << 20):
@@ -357,6 +360,7 @@ def launch_trident_v4_search(
     fine_codes: Optional[torch.Tensor] = None, fine_qp: Optional[torch.Tensor] = None,
     host_rows: Optional[torch.Tensor] = None,
     cluster_bounds: Optional[torch.Tensor] = None,
+    vec_cn: Optional[torch.Tensor] = None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -428,6 +432,9 @@ def launch_trident_v4_search(
     if vec_Ar is not None:
         _check_tensor("vec_Ar", vec_Ar, torch.float32, dev, 2)
         _need(tuple(vec_Ar.shape) == (N, 2), "vec_Ar must be [N, 2] float32")
+    if vec_cn is not None:
+        _check_tensor("vec_cn", vec_cn, torch.float32, dev, 1)
+        _need(vec_cn.numel() == N, f"vec_cn must hold N={N} floats")
     if sq8_cells is not None:
         _check_tensor("sq8_cells", sq8_cells, torch.int32, dev)
         _need(sq8_cells.numel() == tiles * (D_pad // 16) * int(tile_size) * 4,
@@ -472,9 +479,9 @@ def launch_trident_v4_search(
             (int(route) == 2 or B * nprobe >= 8 * nlist) and D_pad <= 1024 and K <= 128:
         # a reference caller passes neither: derive them (once per index) so that the batched
         # route can run, as it would for an index built by TridentV4Index
-        vec_Ar, sq8_cells, band = derived_layouts(W_combined, b_combined, sq8_packed, cluster_vec_off,
-                                                  cluster_tile_off, xb_sorted, vmin, delta,
-                                                  per_cluster_sq8, nlist, tile_size)
+        vec_Ar, sq8_cells, band, vec_cn = derived_layouts(W_combined, b_combined, sq8_packed,
+                                                          cluster_vec_off, cluster_tile_off, xb_sorted,
+                                                          vmin, delta, per_cluster_sq8, nlist, tile_size)
         if cent_band is None:
             cent_band = band
     view = make_index_view(
@@ -488,7 +495,7 @@ def launch_trident_v4_search(
         blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
         sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted,
         fine_codes=fine_codes if mode == 2 else None, fine_qp=fine_qp if mode == 2 else None,
-        cluster_bounds=cluster_bounds if mode == 2 else None)
+        cluster_bounds=cluster_bounds if mode == 2 else None, vec_cn=vec_cn if mode == 2 else None)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route,

@@ -95,6 +95,33 @@ def packed_from_cells(sq8_cells: torch.Tensor, D_pad: int, T: int) -> torch.Tens
     return packed
 
 
+def derive_vec_cn(sq8_cells: torch.Tensor, cluster_vec_off, cluster_tile_off, D_pad: int, T: int,
+                  chunk_tiles: int = 1 << 14) -> torch.Tensor:
+    """Per-row code norms [N] float32 in sorted order: sqrt(sum_d (code_d - 128)^2) over the
+    D_pad dims, rounded up (the sum is an exact integer, the float64 root is raised by 2^-50
+    before the upward rounding), from the cells (whose bytes are code - 128 as int8).  The
+    lower-bound pass bounds the lo weight plane's share of a row's sum by this norm times the
+    plane's norm (Cauchy-Schwarz)."""
+    dev = sq8_cells.device
+    G16, V = D_pad // 16, cell_block(D_pad)
+    tiles = int(sq8_cells.numel()) // (G16 * T * 4)
+    cells = sq8_cells.view(tiles, T // V, G16, V, 4)
+    per_slot = torch.empty((tiles, T), device=dev, dtype=torch.float32)
+    for ts in range(0, tiles, chunk_tiles):
+        te = min(tiles, ts + chunk_tiles)
+        c8 = cells[ts:te].contiguous().view(torch.int8).view(te - ts, T // V, G16, V, 16).to(torch.int32)
+        ssq = (c8 * c8).sum(dim=(2, 4)).reshape(te - ts, T)   # exact: <= 2^14 D_pad
+        per_slot[ts:te] = round_up_f32(torch.sqrt(ssq.double()) * (1.0 + 2.0 ** -50))
+    vec_off = cluster_vec_off.to(dev, torch.int64)
+    tile_off = cluster_tile_off.to(dev, torch.int64)
+    N = int(vec_off[-1])
+    counts = vec_off[1:] - vec_off[:-1]
+    lid = torch.repeat_interleave(torch.arange(counts.numel(), device=dev), counts)
+    local = torch.arange(N, device=dev) - vec_off[lid]
+    tile = tile_off[lid] + torch.div(local, T, rounding_mode="floor")
+    return per_slot[tile, local % T].contiguous()
+
+
 def derive_vec_Ar(sq8_packed, cluster_vec_off, cluster_tile_off, xb_sorted, W_combined, b_combined,
                   vmin, delta, per_cluster_sq8: int, nlist: int, T: int, chunk_rows: int = 1 << 20):
     """The batched route's per-vector scalars [N, 2] of any index in the reference layout, from
@@ -263,6 +290,8 @@ class TridentV4Index:
                    256 dims): the same codes as 16-byte cells (16 dims of one slot), bytes XOR
                    0x80, every V-slot block contiguous -- the batched route's matrix-core operand
                    layout (one scan block is one contiguous run).
+      vec_cn       f32 [N] sorted order: |code - 128|_2 per row, rounded up (the lower-bound
+                   pass's Cauchy-Schwarz allowance for its lo weight plane)
       tile_orig_ids int32 [tiles, T] (-1 padded), tile_r_minmax f32 [tiles, 2]
       cluster_tile_off int32 [nlist + 1]; vmin / delta / eps_pad f32 [nlist or 1, D_pad]
       blk_bounds4  int32 [nb + 1] (32-dim blocks, or the variable scheme of :233-247)
@@ -434,6 +463,7 @@ class TridentV4Index:
             self.sq8_packed[ts:te] = g.permute(0, 2, 1)
         # Batched-route copy: 16-byte cells, every scan block of V slots one contiguous run
         self.sq8_cells = cells_from_packed(self.sq8_packed, D_pad, T)
+        self.vec_cn = derive_vec_cn(self.sq8_cells, storage.cluster_vec_off, self.cluster_tile_off, D_pad, T)
         # The tile band (reference :198-230 takes it from the clustering's float32 r_vec): the
         # smallest and largest |x - c| of each tile, measured here in float64 and rounded
         # outward to float32 (an empty tile gets [+inf, -inf]: never reached).
@@ -543,7 +573,8 @@ class TridentV4Index:
         named = {
             "sq8_packed": self.sq8_packed, "sq8_cells": getattr(self, "sq8_cells", None),
             "tile_orig_ids": self.tile_orig_ids, "tile_r_minmax": self.tile_r_minmax,
-            "vec_Ar": getattr(self, "vec_Ar", None), "r_vec_sorted": getattr(self, "r_vec_sorted", None),
+            "vec_Ar": getattr(self, "vec_Ar", None), "vec_cn": getattr(self, "vec_cn", None),
+            "r_vec_sorted": getattr(self, "r_vec_sorted", None),
             "fine_codes": getattr(self, "fine_codes", None), "fine_qp": getattr(self, "fine_qp", None),
             "cluster_bounds": getattr(self, "cluster_bounds", None),
             "vmin_delta_eps": None, "centroids_and_projection": None,
@@ -602,7 +633,7 @@ class TridentV4Index:
             p_init=p_init,
             vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band,
             r_vec_sorted=self.r_vec_sorted, fine_codes=self.fine_codes, fine_qp=self.fine_qp,
-            host_rows=host_rows_buf, cluster_bounds=self.cluster_bounds)
+            host_rows=host_rows_buf, cluster_bounds=self.cluster_bounds, vec_cn=getattr(self, "vec_cn", None))
         return topk_d, topk_i, kern_ms
 
     def view(self):
@@ -620,7 +651,7 @@ class TridentV4Index:
             delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
             sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted,
             fine_codes=self.fine_codes, fine_qp=self.fine_qp,
-            cluster_bounds=getattr(self, "cluster_bounds", None))
+            cluster_bounds=getattr(self, "cluster_bounds", None), vec_cn=getattr(self, "vec_cn", None))
 
     def _fill_cluster_bounds(self):
         """The batched route's per-cluster constants (A_max, r_max, r_lo), once per index."""

@@ -21,8 +21,9 @@ with ``numpy.memmap`` and streamed to the device in chunks -- and stores everyth
   fine_qp.bin         float32 [N, 4]       their offset, step and error bound
   xb_sorted.bin       float32 [N, D]       the cluster-sorted base (optional)
 
-The code cells of the batched route and the centroid layouts of the coarse pass are
-regrouped from sq8_packed / W_combined on load (cheap, on the device).
+The code cells of the batched route, their per-row norms and the centroid layouts of the
+coarse pass are regrouped / recomputed from sq8_packed / W_combined on load (cheap, on the
+device).
 
 Consistency.  A save first removes any ``meta.npz`` already in the directory, writes every
 ``.bin`` under a temporary name and renames it into place (``os.replace``), and writes
@@ -44,7 +45,7 @@ import numpy as np
 import torch
 
 from . import ext as _ext
-from .index import SharedClusterStorage, TridentV4Index, cells_from_packed
+from .index import SharedClusterStorage, TridentV4Index, cells_from_packed, derive_vec_cn
 
 FORMAT = "trident-amd-ivf-sq8"
 VERSION = 2
@@ -254,6 +255,7 @@ def load_index(path: str, device="cuda:0", xb_placement: str = "device", xb_raw=
     ix.cluster_tile_off = i32(meta["tile_off"])
     ix.sq8_packed = _to_device(bins["sq8_packed"], dev)
     ix.sq8_cells = cells_from_packed(ix.sq8_packed, ix.D_pad, ix.tile_size)
+    ix.vec_cn = derive_vec_cn(ix.sq8_cells, st.cluster_vec_off, ix.cluster_tile_off, ix.D_pad, ix.tile_size)
     ix.tile_orig_ids = _to_device(bins["tile_orig_ids"], dev)
     ix.vec_Ar = _to_device(bins["vec_Ar"], dev)
     ix.r_vec_sorted = _to_device(bins["r_vec_sorted"], dev)
