@@ -71,12 +71,14 @@ __device__ __forceinline__ int splits_of(int n, int sv) {
     return min(kMaxSplit, (n + sv - 1) / sv);
 }
 
-// Slices a seeding unit set scans: at most the first two of a cluster's slices (up to 2 sv
-// rows).  Seeding needs K good rows per query, not every row of its first probes; the
-// threshold stays exact (the K-th exact distance of rows that exist), only looser.  At N = 1e8
-// (clusters of ~6,100 rows) this halves the seeding pass for a slightly longer lower-bound pass
-// (measured: one slice per seeding cluster instead let some queries' candidate lists overflow).
-__device__ __forceinline__ int seed_slices(int S) { return min(S, 2); }
+// Slices a seeding unit set scans: the first of a cluster's slices (up to sv rows).  Seeding
+// needs K good rows per query, not every row of its first probes; the threshold stays exact
+// (the K-th exact distance of rows that exist), only looser.  At N = 1e8 (clusters of ~6,100
+// rows, three slices) one slice instead of two cut the seeding pass from 1.17 to 0.81 ms for
+// 0.2 ms more lower-bound pass and 0.1 ms more refinement; seeding from the first 1024 or 512
+// rows loosened the threshold so far that the lower-bound pass grew by 1.2 ms and candidate
+// lists overflowed.
+__device__ __forceinline__ int seed_slices(int S) { return min(S, 1); }
 
 // Entry e < nlist: the seeding units of cluster e (its pass-1 queries, or all of them when
 // seed_all, <= 16 per unit; the first seed_slices(S) slices); entry nlist + c: the lower-bound
