@@ -32,7 +32,7 @@ def cm_sets(dev):
 
 
 @pytest.mark.parametrize("name", ["hist", "norm96", "d200", "d50"])
-@pytest.mark.parametrize("K", [1, 10, 16])
+@pytest.mark.parametrize("K", [1, 10, 16, 17, 64, 100, 128])
 def test_cm_route_exact(cm_sets, dev, name, K):
     b, xq = cm_sets[name]
     for nprobe in (4, 24):
@@ -62,7 +62,7 @@ def test_cm_exact_ties(dev):
     lid = np.argmin(((xb[:, None, :] - cen[None]) ** 2).sum(-1), 1).astype(np.int32)
     xq = np.concatenate([base[:20], rng.integers(0, 3, size=(20, 16))]).astype(np.float32)
     b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=64)
-    for K, nprobe in ((1, 1), (5, 2), (10, 4), (16, 6)):
+    for K, nprobe in ((1, 1), (5, 2), (10, 4), (16, 6), (40, 3), (100, 6)):
         _, rd, ri = oracle_search(b, xq, nprobe, K)
         d, i = run_search(b, _q(xq, dev), nprobe, K, mode=10, route=2)
         assert_exact(d, i, rd, ri, f"cm ties K={K} nprobe={nprobe}")
@@ -82,7 +82,7 @@ def test_cm_short_and_empty_lists(dev, D):
     b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=64)
     assert (np.diff(b.vec_off) == 0).sum() > 0
     short = False
-    for K, nprobe in ((16, 2), (10, 3), (16, 12)):
+    for K, nprobe in ((16, 2), (10, 3), (16, 12), (50, 3), (128, 12)):
         _, rd, ri = oracle_search(b, xq, nprobe, K)
         d, i = run_search(b, _q(xq, dev), nprobe, K, mode=10, route=2)
         assert_exact(d, i, rd, ri, f"cm short/empty D={D} K={K} nprobe={nprobe}")
@@ -96,21 +96,30 @@ def test_cm_large_clusters_and_many_units(dev):
     xb, xq = datagen.cfg1(N=40_000, D=64, B=2000, n_centers=8, seed=67)
     b = build_index(xb, 8, dev, max_batch=2048)
     assert np.diff(b.vec_off).max() > 2048
-    for nprobe, K in ((1, 10), (3, 16), (8, 1)):
+    for nprobe, K in ((1, 10), (3, 16), (8, 1), (2, 100), (8, 128)):
         _, rd, ri = oracle_search(b, xq.numpy(), nprobe, K)
         d, i = run_search(b, _q(xq.numpy(), dev), nprobe, K, mode=10, route=2)
         assert_exact(d, i, rd, ri, f"cm large nprobe={nprobe} K={K}")
 
 
+def test_cm_route_k_above_16_matches_pair_route(cm_sets, dev):
+    """K > 16: thresholds from the warm-up's listed rows (cm_seed_kernel) instead of the scan's
+    16 column minima; the same results as the per-pair float64 route, on AUTO too."""
+    b, xq = cm_sets["norm96"]
+    xqd = _q(xq, dev)
+    for K in (17, 100):
+        d1, i1 = run_search(b, xqd, 24, K, mode=10, route=1)
+        d2, i2 = run_search(b, xqd, 24, K, mode=10, route=2)
+        d0, i0 = run_search(b, xqd, 24, K, mode=10, route=0)
+        assert np.array_equal(i1, i2) and np.array_equal(d1, d2)
+        assert np.array_equal(i0, i2) and np.array_equal(d0, d2)
+
+
 def test_cm_route_requirements(cm_sets, dev):
     b, xq = cm_sets["hist"]
     xqd = _q(xq[:8], dev)
-    with pytest.raises(TridentError, match="K <= 16"):
-        run_search(b, xqd, 4, 17, mode=10, route=2)
-    # AUTO falls back to the float64 per-pair route where the matrix-core route does not apply
-    _, rd, ri = oracle_search(b, xq[:8], 4, 17)
-    d, i = run_search(b, xqd, 4, 17, mode=10, route=0)
-    assert_exact(d, i, rd, ri, "cm auto K=17")
+    with pytest.raises(TridentError, match="K"):
+        run_search(b, xqd, 4, 129, mode=10, route=2)
 
 
 def test_cm_host_base_is_rejected_on_the_batched_route(dev):

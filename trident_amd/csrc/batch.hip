@@ -273,50 +273,46 @@ __global__ __launch_bounds__(256) void fine_filter_kernel(BatchArgs a, int B) {
     }
 }
 
+// The K-th smallest ub (the low half of a (lb, ub) key) over slots [0, n) of one query's
+// candidate list, one wave; +inf when n < K.  The ub are non-negative floats, so their bit
+// patterns order as their values.
 template <int KP>
-__global__ __launch_bounds__(256) void fine_tau_kernel(BatchArgs a, int B) {
+__device__ __forceinline__ float listed_kth_ub(const BatchArgs& a, const uint64_t* ck, int n) {
     const int lane = threadIdx.x & 63;
-    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6));
-    if (q >= B) return;
-    const int cnt = a.cand_cnt[q];
-    if (cnt <= 0 || cnt > a.cap) return;
-    const uint64_t* ck = a.cand_key + (size_t)q * a.cap;
-    if (cnt <= 4 * kWave) {
-        // Up to 256 slots: the K-th smallest ub by bisection on its float32 bits (the ub are
-        // non-negative, so their bit patterns order as their values; 0xffffffff marks an empty
-        // register): the smallest x with count(ub <= x) >= K, 32 halvings of [0, 2^32 - 1].
+    if (n < a.K) return INFINITY;
+    if (n <= 4 * kWave) {
+        // Up to 256 slots: bisection on the float32 bits (0xffffffff marks an empty register):
+        // the smallest x with count(ub <= x) >= K, 32 halvings of [0, 2^32 - 1].
         uint32_t v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int sl = i * kWave + lane;
-            v[i] = sl < cnt ? __float_as_uint(fine_ub_of(ck[sl])) : 0xffffffffu;
+            v[i] = sl < n ? __float_as_uint(fine_ub_of(ck[sl])) : 0xffffffffu;
         }
-        if (cnt < a.K) return;  // fewer than K rows: tau stays
         uint32_t lo = 0u, hi = 0xfffffffeu;
         while (lo < hi) {
             const uint32_t mid = lo + ((hi - lo) >> 1);
-            int n = 0;
+            int c = 0;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) n += __popcll(__ballot(v[i] <= mid));
-            if (n >= a.K) hi = mid;
+            for (int i = 0; i < 4; ++i) c += __popcll(__ballot(v[i] <= mid));
+            if (c >= a.K) hi = mid;
             else lo = mid + 1u;
         }
-        if (lane == 0) a.tau[q] = fmin(a.tau[q], (double)__uint_as_float(lo));
-        return;
+        return __uint_as_float(lo);
     }
     if (a.K <= 16) {
-        // A long list (a query whose seeding threshold was loose): each lane keeps the 16
-        // smallest ub of its slots (sorted, in registers; the overall K-th smallest is among
-        // the lanes' K smallest), then the same bisection over those 64 x 16 values.
+        // A long list: each lane keeps the 16 smallest ub of its slots (sorted, in registers;
+        // the overall K-th smallest is among the lanes' K smallest), then the same bisection
+        // over those 64 x 16 values.
         uint32_t v[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = 0xffffffffu;
-        for (int s0 = 0; s0 < cnt; s0 += 4 * kWave) {
+        for (int s0 = 0; s0 < n; s0 += 4 * kWave) {
             uint32_t x4[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const int sl = s0 + u * kWave + lane;
-                x4[u] = sl < cnt ? __float_as_uint(fine_ub_of(ck[sl])) : 0xffffffffu;
+                x4[u] = sl < n ? __float_as_uint(fine_ub_of(ck[sl])) : 0xffffffffu;
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -330,32 +326,65 @@ __global__ __launch_bounds__(256) void fine_tau_kernel(BatchArgs a, int B) {
         uint32_t lo = 0u, hi = 0xfffffffeu;
         while (lo < hi) {
             const uint32_t mid = lo + ((hi - lo) >> 1);
-            int n = 0;
+            int c = 0;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) n += __popcll(__ballot(v[i] <= mid));
-            if (n >= a.K) hi = mid;
+            for (int i = 0; i < 16; ++i) c += __popcll(__ballot(v[i] <= mid));
+            if (c >= a.K) hi = mid;
             else lo = mid + 1u;
         }
-        if (lane == 0) a.tau[q] = fmin(a.tau[q], (double)__uint_as_float(lo));
-        return;
+        return __uint_as_float(lo);
     }
     WaveList<KP> L;
     L.init();
-    for (int s0 = 0; s0 < cnt; s0 += kWave) {
+    for (int s0 = 0; s0 < n; s0 += kWave) {
         const int sl = s0 + lane;
-        const bool in = sl < cnt;
+        const bool in = sl < n;
         list_offer(L, a.K, in ? key_of((double)fine_ub_of(ck[sl])) : kKeyInvalid, in ? sl : kIdInvalid);
     }
     uint64_t kk;
     int32_t ki;
     L.at(a.K - 1, kk, ki);
-    if (lane == 0 && kk != kKeyInvalid) a.tau[q] = fmin(a.tau[q], dist_of(kk));
+    return kk != kKeyInvalid ? (float)dist_of(kk) : INFINITY;
+}
+
+template <int KP>
+__global__ __launch_bounds__(256) void fine_tau_kernel(BatchArgs a, int B) {
+    const int lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6));
+    if (q >= B) return;
+    const int cnt = a.cand_cnt[q];
+    if (cnt <= 0 || cnt > a.cap) return;
+    const float t = listed_kth_ub<KP>(a, a.cand_key + (size_t)q * a.cap, cnt);
+    if (lane == 0 && t < INFINITY) a.tau[q] = fmin(a.tau[q], (double)t);
+}
+
+// Mode 10's matrix-core route for K > 16, after its warm-up pass listed every row of the
+// queries' first probes: the K-th smallest listed ub (over the first cap entries when the list
+// overflowed: any K distinct probed rows with ub <= t make t an upper bound of the K-th
+// smallest distance) becomes the query's threshold (ub_best, read by the main pass, and tau),
+// and the list is emptied for the main pass, which lists every probe again.
+template <int KP>
+__global__ __launch_bounds__(256) void cm_seed_kernel(BatchArgs a, int B) {
+    const int lane = threadIdx.x & 63;
+    const int q = __builtin_amdgcn_readfirstlane(blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6));
+    if (q >= B) return;
+    const int n = min(a.cand_cnt[q], a.cap);
+    const float t = n > 0 ? listed_kth_ub<KP>(a, a.cand_key + (size_t)q * a.cap, n) : INFINITY;
+    if (lane == 0) {
+        if (t < INFINITY) {
+            a.ub_best[q] = min(a.ub_best[q], __float_as_uint(t));
+            a.tau[q] = fmin(a.tau[q], (double)t);
+        }
+        a.cand_cnt[q] = 0;
+    }
 }
 
 template __global__ void fine_filter_kernel<256>(BatchArgs, int);
 template __global__ void fine_filter_kernel<1024>(BatchArgs, int);
 template __global__ void fine_tau_kernel<64>(BatchArgs, int);
 template __global__ void fine_tau_kernel<128>(BatchArgs, int);
+template __global__ void cm_seed_kernel<64>(BatchArgs, int);
+template __global__ void cm_seed_kernel<128>(BatchArgs, int);
 
 // One thread per (query, sorted position) pair: the fine-level bounds, for bound-rigour tests.
 __global__ void fine_bounds_kernel(BatchArgs a, const int32_t* __restrict__ qids,

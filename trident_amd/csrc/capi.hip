@@ -407,13 +407,13 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
 }
 
 // Mode 10: the matrix-core cluster-major scan (cm_scan_kernel) or the per-pair float64 scan.
-// The matrix-core route reads every probed row from the base, so it needs the base in HBM; it
-// keeps per-query thresholds from 16-vector tiles, so K <= 16; its query rows live in registers,
-// so D_pad <= 256.  AUTO takes it when clusters are shared by at least 4 queries on average
-// (16-row tiles with fewer rows leave most of each matrix instruction idle).
+// The matrix-core route reads every probed row from the base, so it needs the base in HBM; its
+// query rows live in registers, so D_pad <= 256; K <= 128 (the merge's lists).  AUTO takes it
+// when clusters are shared by at least 4 queries on average (16-row tiles with fewer rows leave
+// most of each matrix instruction idle).
 int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                     int nprobe, bool xb_host, bool* cm) {
-    const bool ok = ix->orig_ids_sorted && !xb_host && K <= 16 && ix->D_pad <= 256 &&
+    const bool ok = ix->orig_ids_sorted && !xb_host && K <= 128 && ix->D_pad <= 256 &&
                     ix->nlist <= kMaxBatchedNlist && ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
@@ -424,7 +424,7 @@ int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, i
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
                             "mode 10 batched route needs orig_ids_sorted, the base in device "
-                            "memory, K <= 16, D_pad <= 256, nlist <= %d and N < 2^27 (K=%d, "
+                            "memory, K <= 128, D_pad <= 256, nlist <= %d and N < 2^27 (K=%d, "
                             "D_pad=%d, nlist=%d, N=%d)",
                             kMaxBatchedNlist, K, ix->D_pad, ix->nlist, ix->N);
             *cm = true;
@@ -1074,12 +1074,21 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
                                  kSplitVec, w.unit_off, w.units, (int)w.max_units, w.grp_off,
                                  w.groups, (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
-        if (M1 > 0) {  // warm-up: thresholds from the first probes, nothing listed
-            b.cm_emit = 0;
+        const unsigned qg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
+        if (M1 > 0) {
+            // warm-up over the first probes: for K <= 16 the scan's own thresholds (the K-th
+            // smallest of 16 column minima), nothing listed; past 16 every row is listed and
+            // cm_seed_kernel takes the K-th smallest listed ub, then empties the lists
+            b.cm_emit = K > 16 ? 1 : 0;
             b.unit_beg = 0;
             b.unit_end = ix->nlist;
             b.ctr = w.unit_ctr;
             if ((rc = launch_cm(b, st))) return rc;
+            if (K > 16) {
+                if (K <= 64) cm_seed_kernel<64><<<qg, kBlock, 0, st>>>(b, B);
+                else cm_seed_kernel<128><<<qg, kBlock, 0, st>>>(b, B);
+                if ((rc = check_launch("cm_seed_kernel"))) return rc;
+            }
         }
         if ((rc = mark(TRIDENT_EV_P1_SCAN))) return rc;
         if ((rc = mark(TRIDENT_EV_P1_MERGE))) return rc;
@@ -1090,8 +1099,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.ctr = w.unit_ctr + 8 * kCtrStride;
         if ((rc = launch_cm(b, st))) return rc;
         if ((rc = mark(TRIDENT_EV_P2_SCAN))) return rc;
-        const unsigned qg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
-        fine_tau_kernel<64><<<qg, kBlock, 0, st>>>(b, B);
+        if (K <= 64) fine_tau_kernel<64><<<qg, kBlock, 0, st>>>(b, B);
+        else fine_tau_kernel<128><<<qg, kBlock, 0, st>>>(b, B);
         if ((rc = check_launch("fine_tau_kernel"))) return rc;
         const dim3 rgrid(qg, (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
         refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);

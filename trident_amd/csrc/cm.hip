@@ -35,6 +35,11 @@
 // because lb <= d64 <= the K-th smallest d64 <= t.  The listed (lb, ub) keys then give tau = the
 // K-th smallest listed ub (fine_tau_kernel), and the refine computes the canonical distance of
 // the listed rows whose lb <= tau only.
+//
+// K > 16.  Sixteen column minima cannot certify K rows, so the in-scan selection never fires;
+// instead the warm-up launch over the first probes lists every row, and cm_seed_kernel sets
+// ub_best to the K-th smallest listed ub (K distinct probed rows have ub <= it) and empties the
+// lists before the main launch, which lists against that fixed threshold.
 #include <type_traits>
 
 #include "common.hpp"

@@ -422,6 +422,9 @@ __global__ void fine_filter_kernel(BatchArgs a, int B);
 template <int KP>
 __global__ void fine_tau_kernel(BatchArgs a, int B);
 
+template <int KP>
+__global__ void cm_seed_kernel(BatchArgs a, int B);
+
 __global__ void fine_bounds_kernel(BatchArgs a, const int32_t* __restrict__ qids,
                                   const int64_t* __restrict__ spos, int n, double* lb, double* ub);
 
@@ -447,7 +450,7 @@ __global__ void lb_scan_wide_kernel(BatchArgs a);  // 4 < KS <= 16
 template <bool HOST, int DQ>
 __global__ void refine_survivors_kernel(BatchArgs a, int B);
 
-// Mode 10 on the float32 matrix cores (D_pad = 4 D4 <= 256, K <= 16): the lower-bound units of
+// Mode 10 on the float32 matrix cores (D_pad = 4 D4 <= 256, K <= 128): the lower-bound units of
 // one launch (unit_beg / unit_end), each listing (lb, ub) keys of the rows that can still enter
 // the top-K; a.ctr[0] is the work counter (zero at launch), a.ub_best the per-query thresholds
 // (+inf at launch).
