@@ -288,13 +288,15 @@ def roofline(w, stage, probes, mode, route_used):
     if route_used == _lib.ROUTE_BATCHED and mode == 10:
         flops = 2.0 * rows_all * ix.D_pad  # float32 matrix cores: 2 D_pad flops per (query, row)
         achieved = flops / t_scan / 1e12
-        roof = {"bound": "mfma", "kernel": "cm_scan_kernel<D4> (mode 10, float32 matrix cores)",
+        kname = "cm_scan_kernel<D4>" if ix.D_pad <= 256 else "cm_scan_wide_kernel"
+        roof = {"bound": "mfma", "kernel": f"{kname} (mode 10, float32 matrix cores)",
                 "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "flops_alg_per_launch": flops}
     elif route_used == _lib.ROUTE_BATCHED:
         ops_alg = 4 * rows_all * ix.D_pad
         achieved = ops_alg / t_scan / 1e12
-        roof = {"bound": "mfma", "kernel": "lb_scan_kernel<KS> (lower-bound pass, int8 matrix cores)",
+        kname = "lb_scan_kernel<KS>" if ix.D_pad <= 256 else "lb_scan_wide_kernel<KS>"
+        roof = {"bound": "mfma", "kernel": f"{kname} (lower-bound pass, int8 matrix cores)",
                 "achieved": round(achieved, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                 "frac": round(achieved / INT8_PEAK_TOPS, 4), "ops_alg_per_launch": ops_alg}
     else:

@@ -115,6 +115,57 @@ def test_cm_route_k_above_16_matches_pair_route(cm_sets, dev):
         assert np.array_equal(i0, i2) and np.array_equal(d0, d2)
 
 
+@pytest.fixture(scope="module")
+def wide_sets(dev):
+    """Past 256 dims: the wide kernel (dims in 128-dim chunks), D % 4 == 0 and not."""
+    out = {}
+    xb, xq = datagen.cfg1(N=12_000, D=300, B=160, n_centers=16, seed=71)
+    out["d300"] = (build_index(xb, 24, dev, max_batch=256, tile_size=256), xq.numpy())
+    xb, xq = datagen.cfg3(N=8_000, D=960, B=96, n_centers=16, seed=72)
+    out["d960"] = (build_index(xb, 16, dev, max_batch=256, tile_size=256), xq.numpy())
+    xb, xq = datagen.cfg1(N=6_000, D=263, B=96, n_centers=16, seed=73)  # D % 4 == 3
+    out["d263"] = (build_index(xb, 12, dev, max_batch=256, tile_size=256), xq.numpy())
+    return out
+
+
+@pytest.mark.parametrize("name", ["d300", "d960", "d263"])
+@pytest.mark.parametrize("K", [1, 10, 16, 100])
+def test_cm_wide_route_exact(wide_sets, dev, name, K):
+    b, xq = wide_sets[name]
+    for nprobe in (2, 8):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=10, route=2)
+        assert_exact(d, i, rd, ri, f"cm wide {name} K={K} nprobe={nprobe}")
+
+
+def test_cm_wide_matches_pair_route_and_auto(wide_sets, dev):
+    b, xq = wide_sets["d960"]
+    xqd = _q(xq, dev)
+    for K in (10, 50):
+        d1, i1 = run_search(b, xqd, 8, K, mode=10, route=1)
+        d2, i2 = run_search(b, xqd, 8, K, mode=10, route=2)
+        d0, i0 = run_search(b, xqd, 8, K, mode=10, route=0)
+        assert np.array_equal(i1, i2) and np.array_equal(d1, d2)
+        assert np.array_equal(i0, i2) and np.array_equal(d0, d2)
+
+
+def test_cm_wide_exact_ties(dev):
+    """Duplicated rows at D = 320: every copy at the K-th distance listed, ids by (d, id)."""
+    rng = np.random.default_rng(74)
+    base = rng.integers(0, 3, size=(40, 320)).astype(np.float32)
+    xb = np.repeat(base, 20, axis=0)
+    nlist = 5
+    cen = rng.integers(0, 3, size=(nlist, 320)).astype(np.float32)
+    lid = np.argmin(((xb[:, None, :] - cen[None]) ** 2).sum(-1), 1).astype(np.int32)
+    xq = np.concatenate([base[:16], rng.integers(0, 3, size=(16, 320))]).astype(np.float32)
+    b = build_index(torch.as_tensor(xb), nlist, dev, list_ids=lid, centroids=cen, max_batch=64,
+                    tile_size=256)
+    for K, nprobe in ((1, 1), (10, 2), (30, 5)):
+        _, rd, ri = oracle_search(b, xq, nprobe, K)
+        d, i = run_search(b, _q(xq, dev), nprobe, K, mode=10, route=2)
+        assert_exact(d, i, rd, ri, f"cm wide ties K={K} nprobe={nprobe}")
+
+
 def test_cm_route_requirements(cm_sets, dev):
     b, xq = cm_sets["hist"]
     xqd = _q(xq[:8], dev)

@@ -63,3 +63,22 @@ def test_stable_crossover_ignores_an_isolated_win():
     assert router.stable_crossover(rows) == 8e6     # the reference rule would give 1e6
     assert router.stable_crossover(rows[:3]) == float("inf")
     assert router.stable_crossover([{"work": 5.0, "cascade_faster": True}]) == 5.0
+
+
+def test_pairs_rule_follows_the_batched_threshold():
+    """The MI355X rule: the cascade from B * nprobe = 8 nlist (its batched route) on, mode 10
+    below; CostRouter takes it unless given a W0 (then the reference's work rule)."""
+    assert router.choose_mode_pairs(127, 64, 1024) == 10
+    assert router.choose_mode_pairs(128, 64, 1024) == 2
+    assert router.choose_mode_pairs(512, 64, 4096) == 2 and router.choose_mode_pairs(511, 64, 4096) == 10
+
+    class Fake:
+        N, nlist, D, max_batch = 1_000_000, 1024, 960, 1024
+
+    r = router.CostRouter(Fake())
+    assert r.rule == "pairs" and r.mode_for(64, 64) == 10 and r.mode_for(128, 64) == 2
+    w = router.CostRouter(Fake(), W0=1e9)
+    assert w.rule == "work" and w.mode_for(64, 64) == 2        # W = 3.8e9 >= 1e9
+    assert router.CostRouter(Fake(), rule="work").W0 == router.W0_MI355X
+    with pytest.raises(ValueError):
+        router.CostRouter(Fake(), rule="fastest")

@@ -406,14 +406,14 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
     }
 }
 
-// Mode 10: the matrix-core cluster-major scan (cm_scan_kernel) or the per-pair float64 scan.
-// The matrix-core route reads every probed row from the base, so it needs the base in HBM; its
-// query rows live in registers, so D_pad <= 256; K <= 128 (the merge's lists).  AUTO takes it
-// when clusters are shared by at least 4 queries on average (16-row tiles with fewer rows leave
-// most of each matrix instruction idle).
+// Mode 10: the matrix-core cluster-major scan (cm_scan_kernel, cm_scan_wide_kernel past 256
+// dims) or the per-pair float64 scan.  The matrix-core route reads every probed row from the
+// base, so it needs the base in HBM; D_pad <= 1024 (the refine's query row in LDS) and K <= 128
+// (the merge's lists).  AUTO takes it when clusters are shared by at least 4 queries on average
+// (16-row tiles with fewer rows leave most of each matrix instruction idle).
 int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                     int nprobe, bool xb_host, bool* cm) {
-    const bool ok = ix->orig_ids_sorted && !xb_host && K <= 128 && ix->D_pad <= 256 &&
+    const bool ok = ix->orig_ids_sorted && !xb_host && K <= 128 && ix->D_pad <= 1024 &&
                     ix->nlist <= kMaxBatchedNlist && ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
@@ -424,7 +424,7 @@ int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, i
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
                             "mode 10 batched route needs orig_ids_sorted, the base in device "
-                            "memory, K <= 128, D_pad <= 256, nlist <= %d and N < 2^27 (K=%d, "
+                            "memory, K <= 128, D_pad <= 1024, nlist <= %d and N < 2^27 (K=%d, "
                             "D_pad=%d, nlist=%d, N=%d)",
                             kMaxBatchedNlist, K, ix->D_pad, ix->nlist, ix->N);
             *cm = true;
@@ -462,10 +462,32 @@ unsigned cm_grid() {
     return (unsigned)cached[dev];
 }
 
+// Resident grid of cm_scan_wide_kernel, cached per device.
+unsigned cm_wide_grid() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (!cached[dev]) {
+        int cu = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cu < 1)
+            cu = 256;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void*>(&cm_scan_wide_kernel), kBlock, 0) != hipSuccess ||
+            per_cu < 1)
+            per_cu = 2;
+        cached[dev] = std::max(8, cu * per_cu);
+    }
+    return (unsigned)cached[dev];
+}
+
 template <int D4 = 8>
 int launch_cm(const BatchArgs& b, hipStream_t st) {
     if constexpr (D4 > 64) {
-        return fail(TRIDENT_ERR_UNSUPPORTED, "mode 10 batched route needs D_pad <= 256");
+        if (b.D_pad > 1024)
+            return fail(TRIDENT_ERR_UNSUPPORTED, "mode 10 batched route needs D_pad <= 1024");
+        cm_scan_wide_kernel<<<cm_wide_grid(), kBlock, 0, st>>>(b);
+        return check_launch("cm_scan_wide_kernel");
     } else {
         if (b.D_pad != 4 * D4) return launch_cm<D4 + 8>(b, st);
         cm_scan_kernel<D4><<<cm_grid<D4>(), kBlock, 0, st>>>(b);
@@ -1103,7 +1125,8 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         else fine_tau_kernel<128><<<qg, kBlock, 0, st>>>(b, B);
         if ((rc = check_launch("fine_tau_kernel"))) return rc;
         const dim3 rgrid(qg, (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
-        refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+        if (ix->D <= 256) refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+        else refine_survivors_kernel<false, 1024><<<rgrid, kBlock, 0, st>>>(b, B);
         if ((rc = check_launch("refine_survivors_kernel"))) return rc;
         m.use_prev = 0;
         m.tau_sq_out = out->tau_sq;

@@ -457,6 +457,9 @@ __global__ void refine_survivors_kernel(BatchArgs a, int B);
 template <int D4>
 __global__ void cm_scan_kernel(BatchArgs a);
 
+// The same for 256 < D_pad <= 1024: dims in chunks of 128, query chunks reloaded per block.
+__global__ void cm_scan_wide_kernel(BatchArgs a);
+
 template <int KS>
 __global__ void pair_prep_kernel(BatchArgs a);
 

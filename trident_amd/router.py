@@ -9,11 +9,18 @@ smallest work at which the cascade is at least as fast (the reference's rule);
 measured work, which ignores an isolated win at a tiny batch.
 
 W0 is hardware-specific.  The reference's A100 value is 946,811,200 (README rounds it to
-9.0e8).  On MI355X (calibrate_w0, bench.py --calibrate-w0) mode 10 is the faster route up to
-B = 64 and the cascade from B = 128, where the cascade's int8 matrix-core batched route takes
-over: configs[0] (N 1e5, nprobe 16) crosses at W = 1.02e8, configs[1] (N 1e6, nprobe 64) at
-W = 1.02e9.  W0_MI355X is the smaller of the two, as the reference takes the smaller of its
-datasets' crossovers.
+9.0e8).  On MI355X (calibrate_w0, bench.py --calibrate-w0; mode 10 timed on its faster route,
+the float32 matrix cores at every calibrated batch) the stable crossovers are W = 2.56e7 at
+configs[0] (B = 32), 6.4e7 at configs[1] (B = 8), 7.68e9 at configs[2] (D = 960, B = 128) and
+7.68e9 at configs[3] (B = 512).  W0_MI355X is the smallest, as the reference takes the smaller
+of its datasets' crossovers.
+
+No single W0 fits all four: the crossing follows the pairs per probed cluster, not W.  From
+B * nprobe = 8 nlist on, the cascade runs its batched int8 matrix-core route and wins by 4-10x;
+below that it runs per (query, cluster) pair and mode 10's single float32 matrix-core pass is
+faster or within 10 % (except single queries).  ``choose_mode_pairs`` routes by that (the
+library's own AUTO threshold for the cascade's batched route), and ``CostRouter`` uses it unless
+it is given a W0.
 """
 import time
 from typing import Dict, List, Optional, Sequence, Tuple
@@ -21,8 +28,10 @@ from typing import Dict, List, Optional, Sequence, Tuple
 import torch
 
 W0_REFERENCE_A100 = 946_811_200.0
-# Smallest stable crossover over the calibrated configs on MI355X (configs[0]: B = 128).
-W0_MI355X = 1.024e8
+# Smallest stable crossover over the calibrated configs on MI355X (configs[0]: B = 32).
+W0_MI355X = 2.56e7
+# Pairs per cluster from which the cascade takes its batched route (capi.hip, choose_route).
+BATCHED_PAIRS_PER_CLUSTER = 8.0
 
 MODE_CM_EXACT = 10
 MODE_CASCADE = 2
@@ -36,6 +45,12 @@ def work_measure(B: int, nprobe: int, N: int, nlist: int, D: int) -> float:
 def choose_mode(work: float, W0: float) -> int:
     """mode 10 (exact cluster-major scan) below W0, else mode 2 (cascade) (reference :1079)."""
     return MODE_CM_EXACT if work < W0 else MODE_CASCADE
+
+
+def choose_mode_pairs(B: int, nprobe: int, nlist: int) -> int:
+    """MI355X rule: mode 2 (cascade) once B * nprobe >= 8 nlist (its batched route), else
+    mode 10."""
+    return MODE_CASCADE if float(B) * nprobe >= BATCHED_PAIRS_PER_CLUSTER * nlist else MODE_CM_EXACT
 
 
 def _time_ms(fn, warmup: int, iters: int) -> float:
@@ -93,14 +108,21 @@ def stable_crossover(rows: List[Dict]) -> float:
 
 
 class CostRouter:
-    """Routes each batch of an index to mode 10 or mode 2 by the work measure."""
+    """Routes each batch of an index to mode 10 or mode 2: ``rule="work"`` by the reference's
+    work measure against W0 (W0_MI355X unless given), ``rule="pairs"`` by choose_mode_pairs;
+    ``rule="auto"`` (the default) is "work" when a W0 is given, else "pairs"."""
 
-    def __init__(self, index, W0: Optional[float] = None):
+    def __init__(self, index, W0: Optional[float] = None, rule: str = "auto"):
+        if rule not in ("auto", "work", "pairs"):
+            raise ValueError(f"rule must be 'auto', 'work' or 'pairs', not {rule!r}")
         self.index = index
+        self.rule = ("work" if W0 is not None else "pairs") if rule == "auto" else rule
         self.W0 = W0_MI355X if W0 is None else float(W0)
 
     def mode_for(self, B: int, nprobe: int) -> int:
         ix = self.index
+        if self.rule == "pairs":
+            return choose_mode_pairs(B, nprobe, ix.nlist)
         return choose_mode(work_measure(B, nprobe, ix.N, ix.nlist, ix.D), self.W0)
 
     def search(self, xq: torch.Tensor, nprobe: int, **kw):
