@@ -29,6 +29,11 @@ Afterwards (untimed):
     FP32, OpenMP) on the same probes over a bounded query sample, the box's thread share,
     threads pinned (OMP_PROC_BIND=spread, OMP_PLACES=cores), warmup 1 + 3 rounds; on float
     data its ids are audited against the exact ones (exact tie / FP32 rounding / true miss).
+With ``--pipeline-batches`` > 0 (default 12): ``pipelined_from_host`` (queries uploaded from host
+memory, searched and read back with 1 / 2 / 3 batches in flight; PCIe-inclusive) and
+``two_streams_resident`` (queries resident in HBM, batches alternating between two streams so
+that one search's PCIe-bound refinement overlaps the next one's scans); both are reported beside
+``value``, which stays the one-stream step.
 With configs[4] (the default) the line also carries, under ``extra``:
   * ``cfg5_sq8_only``: the same index with the fine level dropped and the reference packing
     released, i.e. the configuration as BASELINE.json states it (SQ8 codes, ids and per-vector
@@ -380,6 +385,46 @@ def measure_variant(w, nprobe, K, mode, ub, route, steps, warmup, rounds, label=
     return out, (gd, gi, probes, stats, hrows, stage, ms, round_ms, roof, rows_all, rows_unique, route_used)
 
 
+def two_streams_resident(w, nprobe, K, mode, ub, route, nb, gpu_d, gpu_i):
+    """Queries resident in HBM, `nb` searches of the same batch alternating between two streams
+    (own outputs and library workspace each), so one search's PCIe-bound refinement runs beside
+    the next one's scans; the bench's `value` stays the one-stream step.  Not PCIe-inclusive."""
+    import numpy as np
+    import torch
+    from trident_amd import ext
+    ix, dev = w.ix, w.ix.dev
+    B = int(w.xq.shape[0])
+    view = ix.view()
+    streams = [torch.cuda.Stream(device=dev) for _ in range(2)]
+    outs = [(torch.empty((B, K), dtype=torch.float32, device=dev),
+             torch.empty((B, K), dtype=torch.int64, device=dev)) for _ in range(2)]
+
+    def run(n):
+        for k in range(n):
+            s = streams[k % 2]
+            with torch.cuda.stream(s):
+                ext.search_view(view, w.xq, nprobe, outs[k % 2][0], outs[k % 2][1], mode=mode, ub_seed=ub,
+                                route=route, stream=s)
+
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream(dev))
+    run(4)  # warm-up: both streams' workspaces
+    torch.cuda.synchronize(dev)
+    tb = time.perf_counter()
+    run(nb)
+    torch.cuda.synchronize(dev)
+    sec = time.perf_counter() - tb
+    same = all(bool(np.array_equal(o[1].cpu().numpy(), gpu_i) and np.array_equal(o[0].cpu().numpy(), gpu_d))
+               for o in outs)
+    for s in streams:
+        ext.release_workspace(dev, s)
+    res = {"batches": nb, "batch": B, "qps": round(nb * B / sec, 1), "ms_per_batch": round(sec * 1e3 / nb, 3),
+           "results_identical": same}
+    log(f"two streams, queries resident: {res['qps']:,.0f} QPS ({res['ms_per_batch']:.3f} ms per batch of "
+        f"{B}), results identical {same}")
+    return res
+
+
 def measure_primary(cfg_id, cfg, args, dev):
     """The headline line's fields: the config at its stated nprobe / K, timed, checked on every
     query, with roofline, footprint, PCIe split and the CPU baseline."""
@@ -444,6 +489,7 @@ def measure_primary(cfg_id, cfg, args, dev):
             log(f"pipelined from host, depth {depth}: {len(xq_all) / sec:,.0f} QPS "
                 f"({sec * 1e3 / nb:.3f} ms per batch of {B}), results identical {same}")
         out["pipelined_from_host"] = dict(batches=nb, batch=B, **pipe_out)
+        out["two_streams_resident"] = two_streams_resident(w, nprobe, K, mode, ub, args.route, nb, gpu_d, gpu_i)
 
     if args.sweep:
         sweep = {}
@@ -590,7 +636,7 @@ def main():
         "hbm_footprint_bytes": r["hbm_footprint"],
         "host_bytes": r["host_bytes"],
     }
-    for k in ("out_of_core", "sweep", "w0_calibration", "pipelined_from_host"):
+    for k in ("out_of_core", "sweep", "w0_calibration", "pipelined_from_host", "two_streams_resident"):
         if k in r:
             line[k] = r[k]
     extra = {}

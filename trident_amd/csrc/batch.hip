@@ -1748,16 +1748,18 @@ void lb_scan_kernel(BatchArgs a) {
             }
         };
 
-        // ---- one 16-vector tile: INT = the integer test, TWO = both halves hold queries ----
-        auto tile = [&](auto int_c, auto two_c, int buf, int t, int li0) __attribute__((always_inline)) {
-            constexpr bool INT = decltype(int_c)::value, TWO = decltype(two_c)::value;
+        // ---- one 16-vector tile: load_b reads its code fragments (the B operands) from LDS,
+        // tile_b runs it on them; INT = the integer test, TWO = both halves hold queries ----
+        auto load_b = [&](int buf, int t, v4i (&Bo)[KS]) __attribute__((always_inline)) {
             const uint4* blk = s_codes[buf][t >> 2];
-            v4i B[KS];
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const uint4 v = blk[(ks * 4 + g) * BV + (t & 3) * 16 + j];
-                B[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                Bo[ks] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
             }
+        };
+        auto tile_b = [&](auto int_c, auto two_c, int buf, int t, int li0, const v4i (&B)[KS]) __attribute__((always_inline)) {
+            constexpr bool INT = decltype(int_c)::value, TWO = decltype(two_c)::value;
             // the thresholds of column j (row t * 16 + j of the block) are held by lane
             // (t & 3) * 16 + j in its run's registers
             const int src = (((t & 3) << 4) | j) << 2;
@@ -1782,18 +1784,22 @@ void lb_scan_kernel(BatchArgs a) {
                 int mh = max(max(h0[0], h0[1]), max(h0[2], h0[3]));
                 if constexpr (TWO) mh = max(mh, max(max(h1[0], h1[1]), max(h1[2], h1[3])));
                 if (__ballot(mh >= thh) == 0ull) return;
+                // the lo plane continues from 256 (plain hi sum) + kq in the same registers
+                {
+                    const v4i k0 = *reinterpret_cast<const v4i*>(&s_kq[wid][4 * g]);
+                    v4i k1 = {0, 0, 0, 0};
+                    if constexpr (TWO) k1 = *reinterpret_cast<const v4i*>(&s_kq[wid][16 + 4 * g]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {  // back to the plain hi sums
-                    h0[r] -= hq4[0][r];
-                    if constexpr (TWO) h1[r] -= hq4[1][r];
+                    for (int r = 0; r < 4; ++r) {
+                        h0[r] = ((h0[r] - hq4[0][r]) << 8) + k0[r];
+                        if constexpr (TWO) h1[r] = ((h1[r] - hq4[1][r]) << 8) + k1[r];
+                    }
                 }
-                l0 = *reinterpret_cast<const v4i*>(&s_kq[wid][4 * g]);
-                if constexpr (TWO) l1 = *reinterpret_cast<const v4i*>(&s_kq[wid][16 + 4 * g]);
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) {
-                    l0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], l0, 0, 0, 0);
+                    h0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[0][ks], B[ks], h0, 0, 0, 0);
                     if constexpr (TWO)
-                        l1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[1][ks], B[ks], l1, 0, 0, 0);
+                        h1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(wlo[1][ks], B[ks], h1, 0, 0, 0);
                 }
             } else {
 #pragma unroll
@@ -1810,8 +1816,8 @@ void lb_scan_kernel(BatchArgs a) {
             int S[2][4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                S[0][r] = (h0[r] << 8) + l0[r];
-                S[1][r] = TWO ? (h1[r] << 8) + l1[r] : INT_MIN;
+                S[0][r] = INT ? h0[r] : (h0[r] << 8) + l0[r];
+                S[1][r] = TWO ? (INT ? h1[r] : (h1[r] << 8) + l1[r]) : INT_MIN;
             }
             const int li = li0 + j;
             if constexpr (INT) {
@@ -1839,13 +1845,23 @@ void lb_scan_kernel(BatchArgs a) {
             }
         };
         auto tiles = [&](auto int_c, auto two_c, int buf, int blk0) __attribute__((always_inline)) {
-            if (R == 1 && blk0 + BR <= ve) {  // the common case: straight-line tiles
+            if (R == 1 && blk0 + BR <= ve) {  // the common case: straight-line tiles, the next
+                                              // tile's codes read before this one's branches
+                v4i Bc[KS], Bn[KS];
+                load_b(buf, 0, Bn);
 #pragma unroll
-                for (int t = 0; t < BR / 16; ++t) tile(int_c, two_c, buf, t, blk0 + t * 16);
+                for (int t = 0; t < BR / 16; ++t) {
+#pragma unroll
+                    for (int ks = 0; ks < KS; ++ks) Bc[ks] = Bn[ks];
+                    if (t + 1 < BR / 16) load_b(buf, t + 1, Bn);
+                    tile_b(int_c, two_c, buf, t, blk0 + t * 16, Bc);
+                }
             } else {
                 for (int t = rr; t < BR / 16; t += R) {
                     if (blk0 + t * 16 >= ve) break;
-                    tile(int_c, two_c, buf, t, blk0 + t * 16);
+                    v4i Bc[KS];
+                    load_b(buf, t, Bc);
+                    tile_b(int_c, two_c, buf, t, blk0 + t * 16, Bc);
                 }
             }
         };
