@@ -369,7 +369,8 @@ def measure_variant(w, nprobe, K, mode, ub, route, steps, warmup, rounds, label=
     out = {"qps": round(B / (ms / 1000.0), 1), "ms_per_step": round(ms, 4), "steps": steps,
            "rounds_qps_mean": round(statistics.mean(round_qps), 1),
            "rounds_qps_std": round(statistics.pstdev(round_qps), 1),
-           "route": "batched" if route_used == _lib.ROUTE_BATCHED else "pair",
+           "route": (("cm_matrix" if mode == 10 else "batched") if route_used == _lib.ROUTE_BATCHED
+                     else "pair"),
            "exact": ex, "roofline": roof, "stages_ms": {k: round(v, 4) for k, v in stage.items()},
            "pruning": {"candidates": stats[0], "survivors": stats[2], "refined_kept": stats[3]}}
     if w.xb_host:
@@ -545,6 +546,13 @@ def measure_sweeps(args, dev, cfg_ids):
                 gd, gi, probes = raw[0], raw[1], raw[2]
                 v["cpu_baseline"] = cpu_baseline(w, npb, K, probes, gd, gi, cfg["cpu"])
             res[f"configs[{cid - 1}]_nprobe{npb}_K{K}"] = v
+        # mode 10 (exact cluster-major scan; the reference's router sends configs[0] there) at the
+        # config's stated nprobe and K, on the library's AUTO route (float32 matrix cores here)
+        npb, K = cfg["nprobe"], cfg["K"]
+        v, _ = measure_variant(w, npb, K, 10, 0, 0, args.extra_steps, 5, 2, label=f"cfg{cid} mode 10")
+        v["workload"] = (f"BASELINE {cfg['desc']}, N={cfg['N']}, D={cfg['D']}, nlist={cfg['nlist']}, "
+                         f"nprobe={npb}, K={K}, B={cfg['B']}, mode 10")
+        res[f"configs[{cid - 1}]_nprobe{npb}_K{K}_mode10"] = v
         w.free()
     return res
 

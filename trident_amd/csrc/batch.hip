@@ -71,26 +71,22 @@ __device__ __forceinline__ int splits_of(int n, int sv) {
     return min(kMaxSplit, (n + sv - 1) / sv);
 }
 
-// Slices a seeding unit set scans: the first of a cluster's slices (up to sv rows).  Seeding
-// needs K good rows per query, not every row of its first probes; the threshold stays exact
-// (the K-th exact distance of rows that exist), only looser.  At N = 1e8 (clusters of ~6,100
-// rows, three slices) one slice instead of two cut the seeding pass from 1.17 to 0.81 ms for
-// 0.2 ms more lower-bound pass and 0.1 ms more refinement; seeding from the first 1024 or 512
-// rows loosened the threshold so far that the lower-bound pass grew by 1.2 ms and candidate
-// lists overflowed.
-__device__ __forceinline__ int seed_slices(int S) { return min(S, 1); }
+// Slices a seeding unit set scans: the first seed_sl of a cluster's slices (sv rows each; the
+// caller's choice, 1 or 2).  Seeding needs K good rows per query, not every row of its first
+// probes; the threshold stays exact (the K-th exact distance of rows that exist), only looser.
+__device__ __forceinline__ int seed_slices(int S, int seed_sl) { return min(S, seed_sl); }
 
 // Entry e < nlist: the seeding units of cluster e (its pass-1 queries, or all of them when
-// seed_all, <= 16 per unit; the first seed_slices(S) slices); entry nlist + c: the lower-bound
-// units of cluster c (all its queries, <= uqB per unit, every slice).
+// seed_all, <= 16 per unit; the first seed_slices(S, seed_sl) slices); entry nlist + c: the
+// lower-bound units of cluster c (all its queries, <= uqB per unit, every slice).
 __device__ __forceinline__ int units_of_entry(const int32_t* seg, const int32_t* vec_off,
-                                              int nlist, int uqB, int seed_all, int sv,
+                                              int nlist, int uqB, int seed_all, int seed_sl, int sv,
                                               int e) {
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
     const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
     const int uq = p ? uqB : kUnitQ0;
     const int S = splits_of(vec_off[c + 1] - vec_off[c], sv);
-    return q > 0 ? ((q + uq - 1) / uq) * (p ? S : seed_slices(S)) : 0;
+    return q > 0 ? ((q + uq - 1) / uq) * (p ? S : seed_slices(S, seed_sl)) : 0;
 }
 
 __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
@@ -103,13 +99,14 @@ __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
 // (blk_tot[b] units, blk_tot[kBlock + b] groups), then the carries of the blocks before.
 __global__ __launch_bounds__(256) void unit_scan_local_kernel(const int32_t* seg,
                                                               const int32_t* vec_off, int nlist,
-                                                              int uqB, int seed_all, int sv,
-                                                              int32_t* unit_off, int32_t* grp_off,
-                                                              int32_t* blk_tot) {
+                                                              int uqB, int seed_all, int seed_sl,
+                                                              int sv, int32_t* unit_off,
+                                                              int32_t* grp_off, int32_t* blk_tot) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const uint32_t nu =
-        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, sv, i) : 0u;
+        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, seed_sl, sv, i)
+                      : 0u;
     const uint32_t ng = i < nlist ? (uint32_t)groups_of_cluster(seg, i) : 0u;
     uint32_t tu = 0, tg = 0;
     const uint32_t ru = block_exclusive_scan(nu, s_wtot, &tu);

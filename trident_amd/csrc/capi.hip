@@ -406,6 +406,16 @@ int choose_route(const TridentIndexView* ix, const TridentSearchParams* sp, int 
     }
 }
 
+// Slices of each seeding cluster the seeding pass (and mode 10's warm-up) scans: the first one
+// while K <= 64 and rows are cheap to refine (base in HBM, or a fine level in front of a host
+// base), else the first two.  A seeding threshold from fewer rows is looser: with K <= 50 and
+// such a base one slice is faster (configs[4] 7.25 -> 7.17 ms, configs[3] K = 10 1.66 -> 1.57
+// ms), but at K = 100 (configs[2] 5.5 -> 7.5 ms, configs[3] 3.0 ms -> overflowed candidate
+// lists) and for a host base without a fine level (every extra survivor crosses PCIe) it is not.
+inline int seed_slice_count(int K, bool xb_host, bool fine) {
+    return K <= 64 && (!xb_host || fine) ? 1 : 2;
+}
+
 // Mode 10: the matrix-core cluster-major scan (cm_scan_kernel, cm_scan_wide_kernel past 256
 // dims) or the per-pair float64 scan.  The matrix-core route reads every probed row from the
 // base, so it needs the base in HBM; D_pad <= 1024 (the refine's query row in LDS) and K <= 128
@@ -1084,8 +1094,10 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         {
             const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
-                                                            ix->nlist, b.unit_q, 0, kSplitVec,
-                                                            w.unit_off, w.grp_off, w.blk_tot);
+                                                            ix->nlist, b.unit_q, 0,
+                                                            seed_slice_count(K, false, false),
+                                                            kSplitVec, w.unit_off, w.grp_off,
+                                                            w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
             unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
                                                             w.unit_off, w.grp_off);
@@ -1225,10 +1237,11 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         // TRIDENT_UB_SEED 2 seeds from every probe, 0 and 1 from the first p_init
         const int seed_all = sp->ub_seed == 2 ? 1 : 0;
         const int split_vec = ix->D_pad <= 256 ? kSplitVecNarrow : kSplitVec;
+        const int seed_sl = seed_slice_count(K, xb_host, b.fine_mode != 0);
         {
             const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= kBlock (kMaxBatchedNlist)
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
-                                                            ix->nlist, b.unit_q, seed_all,
+                                                            ix->nlist, b.unit_q, seed_all, seed_sl,
                                                             split_vec, w.unit_off, w.grp_off,
                                                             w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;

@@ -388,12 +388,11 @@ inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
 }
 
 // seed_all: the seeding units cover every pair of a cluster (TRIDENT_UB_SEED 2), not only its
-// pass-1 pairs.
+// pass-1 pairs; seed_sl: the seeding units scan the first seed_sl slices of each cluster.
 // Two launches of ceil(2 nlist / kBlock) blocks; blk_tot holds 2 * kBlock block totals.
 __global__ void unit_scan_local_kernel(const int32_t* seg, const int32_t* vec_off, int nlist,
-                                       int uqB, int seed_all, int sv, int32_t* unit_off,
-                                       int32_t* grp_off,
-                                       int32_t* blk_tot);
+                                       int uqB, int seed_all, int seed_sl, int sv,
+                                       int32_t* unit_off, int32_t* grp_off, int32_t* blk_tot);
 __global__ void unit_scan_carry_kernel(int nlist, const int32_t* blk_tot, int nblk,
                                        int32_t* unit_off, int32_t* grp_off);
 
