@@ -143,17 +143,33 @@ struct Workspace {
     float* cmt32;                    // the centroids in the matrix-core tile layout
     float* cn32;                     // [nlist] their squared norms
     unsigned long long* cmax2;       // largest centroid squared norm (float64 bits)
+    // parallel rescan of overflowed candidate lists (batched route): slots for up to ovf_max
+    // queries, each with [nprobe, 128] per-probe lists
+    int64_t ovf_max;
+    int32_t* ovf_n;                  // [1]
+    int32_t* ovf_q;                  // [ovf_max]
+    int32_t* ovf_slot;               // [B]
+    double* ovf_t;                   // [ovf_max]
+    uint64_t* ovf_key;               // [ovf_max, nprobe, KP <= 128]
+    int32_t* ovf_id;
     size_t bytes;
 };
+
+// Overflowed queries rescanned in parallel per search (the rest take the merge's serial rescan):
+// 188 at B = 10,000, 18.5 MB of per-probe lists at K <= 64.  A configs[4] search whose seeding
+// threshold was made loose on purpose (p_init 1) overflows fewer than that: 243 -> 17 ms per
+// step against the serial rescan; larger budgets (B / 16, B / 4) changed nothing.
+inline int64_t ovf_slots_of(int64_t B) { return std::min<int64_t>(B, 32 + B / 64); }
 
 // Bytes of one batched-route weight plane: whole 64-dim steps.
 inline int64_t plane_bytes(int D_pad) { return 64 * (int64_t)((D_pad + 63) / 64); }
 
 // Candidate-list slots per query.  The batched route stores every lower-bound survivor there
 // (before its exact test), so lists are at least 64 * nprobe deep (12 bytes a slot; only used
-// slots are touched): a longer list makes the merge rescan that query's probes (computing the
-// SQ8 bounds of every probed row, one wave per query, and refining the rows near the top-K),
-// so the lists are sized to make that rare.  Past 64 neighbours in
+// slots are touched): a longer list makes that query's probes be rescanned (the SQ8 bounds of
+// every probed row, one wave per (query, probe) for up to ovf_slots_of(B) queries, one wave per
+// query past that, and the rows near the top-K refined), so the lists are sized to make that
+// rare.  Past 64 neighbours in
 // more than 256 dims the K-th distance sits in the bulk of the distance distribution (cfg 3,
 // K = 100: ~1 % of candidates pass, ~2,300 per query with a long tail), so those lists are 8x
 // deeper.  An index with a fine level keeps its base in host memory, where an overflow costs
@@ -214,6 +230,13 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.cmt32 = c.take<float>(((int64_t)ix->nlist + 15) / 16 * 16 * Dq);
     w.cn32 = c.take<float>(ix->nlist);
     w.cmax2 = c.take<unsigned long long>(1);
+    w.ovf_max = ovf_slots_of(B);
+    w.ovf_n = c.take<int32_t>(1);
+    w.ovf_q = c.take<int32_t>(w.ovf_max);
+    w.ovf_slot = c.take<int32_t>(B);
+    w.ovf_t = c.take<double>(w.ovf_max);
+    w.ovf_key = c.take<uint64_t>(w.ovf_max * nprobe * std::min<int64_t>(KP, 128));
+    w.ovf_id = c.take<int32_t>(w.ovf_max * nprobe * std::min<int64_t>(KP, 128));
     w.bytes = c.off;
     return w;
 }
@@ -1339,6 +1362,35 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         m.qerr = w.qerr;
         m.lb_scale = a.lb_scale;
         m.ub_scale = a.ub_scale;
+        // up to ovf_max overflowed lists are rescanned in parallel, one wave per (query, probe);
+        // without an overflow the launches find no slot and end at once
+        m.ovf_par = KP <= 128 ? 1 : 0;
+        if (m.ovf_par) {
+            m.ovf_max = (int)w.ovf_max;
+            m.ovf_n = w.ovf_n;
+            m.ovf_q = w.ovf_q;
+            m.ovf_slot = w.ovf_slot;
+            m.ovf_t = w.ovf_t;
+            m.ovf_key = w.ovf_key;
+            m.ovf_id = w.ovf_id;
+            if ((rc = fill(w.ovf_n, 0, 1, st))) return rc;
+            ovf_collect_kernel<<<(unsigned)((B + 255) / 256), 256, 0, st>>>(m);
+            if ((rc = check_launch("ovf_collect_kernel"))) return rc;
+            const size_t odyn = (size_t)kWavesPerBlock * 3 * ix->D_pad * sizeof(float);
+            const unsigned og = (unsigned)std::min<int64_t>(
+                (w.ovf_max * nprobe + kWavesPerBlock - 1) / kWavesPerBlock, 2048);
+            const unsigned kg = (unsigned)((w.ovf_max + kWavesPerBlock - 1) / kWavesPerBlock);
+            if (KP == 64) {
+                ovf_scan_kernel<64, true><<<og, kBlock, odyn, st>>>(m);
+                ovf_kth_kernel<64><<<kg, kBlock, 0, st>>>(m);
+                ovf_scan_kernel<64, false><<<og, kBlock, odyn, st>>>(m);
+            } else {
+                ovf_scan_kernel<128, true><<<og, kBlock, odyn, st>>>(m);
+                ovf_kth_kernel<128><<<kg, kBlock, 0, st>>>(m);
+                ovf_scan_kernel<128, false><<<og, kBlock, odyn, st>>>(m);
+            }
+            if ((rc = check_launch("ovf_scan_kernel"))) return rc;
+        }
         if ((rc = launch_merge(m, KP, st))) return rc;
         if ((rc = mark(TRIDENT_EV_END))) return rc;
         if (out->stats) {

@@ -83,6 +83,18 @@ struct MergeArgs {
     const double* xrot64;       // [B, D_pad]
     const double* qerr;         // [B, D_pad]
     double lb_scale, ub_scale;  // as ScanArgs
+    // Parallel bounded rescan (ovf_par = 1, with ovf_bounds): ovf_collect_kernel gives up to
+    // ovf_max overflowed queries a slot; ovf_scan_kernel rescans them one wave per (slot, probe),
+    // each keeping its cluster's K best in ovf_key / ovf_id [ovf_max, nprobe, KP] (upper bounds
+    // first, reduced by ovf_kth_kernel to the slot's threshold ovf_t, then refined distances);
+    // merge_kernel merges a slot's lists.  Overflowed queries past ovf_max take the serial rescan.
+    int ovf_par, ovf_max;
+    int32_t* ovf_n;       // [1] overflowed queries (may exceed ovf_max); zero before the collect
+    int32_t* ovf_q;       // [ovf_max] the query of each slot
+    int32_t* ovf_slot;    // [B] each query's slot, -1 for none
+    double* ovf_t;        // [ovf_max]
+    uint64_t* ovf_key;
+    int32_t* ovf_id;
 };
 
 // Per-(query, cluster) pair scalars of the batched bound (threshold-independent part).
@@ -420,6 +432,13 @@ __global__ void fine_filter_kernel(BatchArgs a, int B);
 
 template <int KP>
 __global__ void fine_tau_kernel(BatchArgs a, int B);
+
+// Parallel rescan of overflowed candidate lists (MergeArgs, ovf_par).
+__global__ void ovf_collect_kernel(MergeArgs a);
+template <int KP, bool UB>
+__global__ void ovf_scan_kernel(MergeArgs a);
+template <int KP>
+__global__ void ovf_kth_kernel(MergeArgs a);
 
 template <int KP>
 __global__ void cm_seed_kernel(BatchArgs a, int B);

@@ -461,16 +461,20 @@ __global__ void stats_fold_kernel(const unsigned long long* slots, int64_t* out)
 // exact top-K, since lb <= d64 <= t for them.  The per-dim constants of each (q, cluster) pair
 // are staged in the wave's LDS (3 D_pad floats); codes come from the batched route's cells
 // (c ^ 0x80, 16 dims a cell).
+// One probed cluster (probe p of query q) of an overflowed list's rescan: UB offers every row's
+// SQ8 upper bound (key, sorted position) to L; otherwise the rows whose lower bound is within t
+// are refined (canonical float64 distance) and offered as (distance, original id).  s_par holds
+// 3 D_pad floats of the wave's LDS.
 template <int KP, bool UB>
-__device__ __forceinline__ void ovf_bounded_pass(const MergeArgs& a, int q, WaveList<KP>& L, double t,
-                                              float* s_par) {
+__device__ __forceinline__ void ovf_cluster_pass(const MergeArgs& a, int q, int p, WaveList<KP>& L,
+                                                 double t, float* s_par) {
     const int lane = lane_id();
     const int D_pad = a.D_pad, T = a.T, G16 = D_pad >> 4;
     const int V = D_pad <= 256 ? 64 : 16;
     float *s_bs = s_par, *s_dl = s_par + D_pad, *s_e = s_par + 2 * D_pad;
     const double* qv = a.xq64 + (size_t)q * a.D;
     const uint32_t tb = UB ? 0u : tau_bits_of(t, a.lb_scale);
-    for (int p = 0; p < a.nprobe; ++p) {
+    {
         const int c = a.probe_cids[(size_t)q * a.nprobe + p];
         const int v0 = a.vec_off[c], n = a.vec_off[c + 1] - v0, t0 = a.tile_off[c];
         const size_t off = a.per_cluster ? (size_t)c * D_pad : 0;
@@ -530,6 +534,72 @@ __device__ __forceinline__ void ovf_bounded_pass(const MergeArgs& a, int q, Wave
     }
 }
 
+template <int KP, bool UB>
+__device__ __forceinline__ void ovf_bounded_pass(const MergeArgs& a, int q, WaveList<KP>& L, double t,
+                                              float* s_par) {
+    for (int p = 0; p < a.nprobe; ++p) ovf_cluster_pass<KP, UB>(a, q, p, L, t, s_par);
+}
+
+// Parallel form of the bounded rescan.  An overflowed query's slot holds, per probe, the K best
+// entries of that probe's cluster: every member of the query's top-K over all probed rows is
+// among its own cluster's K best, so merging the per-probe lists gives the same result as one
+// list over every probed row (the serial rescan).
+__global__ void ovf_collect_kernel(MergeArgs a) {
+    const int q = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (q >= a.B) return;
+    int slot = -1;
+    if (a.cand_cnt[q] > a.cap) {
+        const int s = atomicAdd(a.ovf_n, 1);
+        if (s < a.ovf_max) {
+            slot = s;
+            a.ovf_q[s] = q;
+        }
+    }
+    a.ovf_slot[q] = slot;
+}
+
+// One wave per (slot, probe) item, grid-strided (the grid is sized for the slots, items past the
+// taken slots end the loop at once): UB lists the cluster's K smallest upper bounds, else its K
+// best refined rows among those whose lower bound is within the slot's threshold.
+template <int KP, bool UB>
+__global__ __launch_bounds__(256) void ovf_scan_kernel(MergeArgs a) {
+    extern __shared__ float s_ovf[];  // 3 D_pad floats per wave
+    const int wid = (int)(threadIdx.x >> 6);
+    const int n = __builtin_amdgcn_readfirstlane(min(*a.ovf_n, a.ovf_max)) * a.nprobe;
+    float* s_par = s_ovf + wid * 3 * a.D_pad;
+    for (int it = (int)blockIdx.x * kWavesPerBlock + wid; it < n; it += (int)gridDim.x * kWavesPerBlock) {
+        const int slot = it / a.nprobe, p = it - slot * a.nprobe;
+        const int q = a.ovf_q[slot];
+        WaveList<KP> L;
+        L.init();
+        ovf_cluster_pass<KP, UB>(a, q, p, L, UB ? 0.0 : a.ovf_t[slot], s_par);
+        list_store(L, a.ovf_key + (size_t)it * KP, a.ovf_id + (size_t)it * KP);
+    }
+}
+
+// One wave per taken slot: the K-th smallest upper bound over the slot's per-probe lists (and
+// the pass's threshold) bounds the query's K-th distance.
+template <int KP>
+__global__ __launch_bounds__(256) void ovf_kth_kernel(MergeArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int slot = (int)blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
+    if (slot >= min(*a.ovf_n, a.ovf_max)) return;
+    const int q = a.ovf_q[slot];
+    const int total = a.nprobe * KP;
+    const uint64_t* k = a.ovf_key + (size_t)slot * total;
+    const int32_t* id = a.ovf_id + (size_t)slot * total;
+    WaveList<KP> L;
+    L.init();
+    for (int e0 = 0; e0 < total; e0 += kWave) {
+        const int e = e0 + lane;
+        list_offer(L, a.K, e < total ? k[e] : kKeyInvalid, e < total ? id[e] : kIdInvalid);
+    }
+    uint64_t kk;
+    int32_t ki;
+    L.at(a.K - 1, kk, ki);
+    if (lane == 0) a.ovf_t[slot] = fmin(a.tau64[q], kk != kKeyInvalid ? dist_of(kk) : (double)INFINITY);
+}
+
 template <int KP>
 __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     extern __shared__ float s_ovf[];  // ovf_bounds: 3 D_pad floats per wave
@@ -542,7 +612,18 @@ __global__ __launch_bounds__(256) void merge_kernel(MergeArgs a) {
     int32_t* li = a.list_id + (size_t)q * KP;
     if (a.use_prev) list_load(L, lk, li);
     const int raw = a.cand_cnt[q];
-    if (raw > a.cap && a.probe_cids && a.ovf_bounds) {
+    const int oslot = raw > a.cap && a.ovf_par ? a.ovf_slot[q] : -1;
+    if (oslot >= 0) {
+        // Overflowed list rescanned in parallel (ovf_scan_kernel): merge its per-probe lists.
+        L.init();
+        const int total = a.nprobe * KP;
+        const uint64_t* k = a.ovf_key + (size_t)oslot * total;
+        const int32_t* id = a.ovf_id + (size_t)oslot * total;
+        for (int e0 = 0; e0 < total; e0 += kWave) {
+            const int e = e0 + lane;
+            list_offer(L, a.K, e < total ? k[e] : kKeyInvalid, e < total ? id[e] : kIdInvalid);
+        }
+    } else if (raw > a.cap && a.probe_cids && a.ovf_bounds) {
         // Overflowed list, SQ8 codes at hand: the K-th smallest upper bound over the probed rows
         // (and the pass's threshold) bounds the K-th distance; only rows whose lower bound
         // passes it are read and refined.
@@ -722,6 +803,12 @@ template __global__ void pair_scan_kernel<128, kScanExact>(ScanArgs);
 template __global__ void pair_scan_kernel<128, kScanTribase>(ScanArgs);
 template __global__ void pair_scan_kernel<128, kScanHat>(ScanArgs);
 template __global__ void pair_scan_kernel<256, kScanHat>(ScanArgs);
+template __global__ void ovf_scan_kernel<64, true>(MergeArgs);
+template __global__ void ovf_scan_kernel<64, false>(MergeArgs);
+template __global__ void ovf_scan_kernel<128, true>(MergeArgs);
+template __global__ void ovf_scan_kernel<128, false>(MergeArgs);
+template __global__ void ovf_kth_kernel<64>(MergeArgs);
+template __global__ void ovf_kth_kernel<128>(MergeArgs);
 template __global__ void merge_kernel<64>(MergeArgs);
 template __global__ void merge_kernel<128>(MergeArgs);
 template __global__ void merge_kernel<256>(MergeArgs);
