@@ -87,14 +87,30 @@ def test_band_front_end_wide_nlist(dev, nlist):
 
 
 def test_band_front_end_far_from_origin(dev):
-    """Data offset far from the origin: the float32 matrix-core approximation loses most of its
-    digits to cancellation, the band widens to many (or all) centroids, and the selection must
+    """Data offset far from the origin: the matrix-core approximation loses most of its digits
+    to cancellation, the band widens to many (or all) centroids, and the selection must
     still be the float64 oracle's, ties included."""
     xb, xq = datagen.cfg1(N=20_000, D=128, B=100, n_centers=128, seed=44)
     b = build_index(xb + 3.0e4, 256, dev, max_batch=128, max_nprobe=128)
     xq = (xq + 3.0e4).numpy()
     dup = np.repeat(xq[:4], 2, axis=0)  # duplicated queries: identical rows
     xq = np.concatenate([xq, dup]).astype(np.float32)
+    for nprobe in (5, 64, 128):
+        _check_probes(b, xq, dev, nprobe)
+
+
+@pytest.mark.parametrize("low", [0x8000 + 0x40, 0xFF00])
+def test_band_front_end_split_adversarial(dev, low):
+    """Every stored and query value's low 16 bits set just above a bfloat16 tie (the split's
+    dropped terms all of one sign) or just below the next bfloat16 value: the coarse pass's
+    bfloat16 split is at its largest error, and the band must still hold every probe."""
+    def hostile(t):
+        u = t.contiguous().view(torch.int32)
+        return ((u & ~0xFFFF) | low).view(torch.float32)
+
+    xb, xq = datagen.cfg1(N=20_000, D=128, B=100, n_centers=128, seed=47)
+    b = build_index(hostile(xb), 256, dev, max_batch=128, max_nprobe=128)
+    xq = hostile(xq).numpy()
     for nprobe in (5, 64, 128):
         _check_probes(b, xq, dev, nprobe)
 
@@ -117,8 +133,8 @@ def test_band_front_end_stream_wide_band(dev, offset):
 
 @pytest.mark.parametrize("D", [12, 72, 100, 112])
 def test_band_front_end_query_widths(dev, D):
-    """The streamed coarse GEMM runs one instantiation per 16-dim group count (Dq = 16, 80,
-    112): widths the other tests do not reach, zero-padded past D."""
+    """The coarse pass runs one instantiation per 32-dim step count (Dq = 16, 80, 112: one,
+    three and four steps): widths the other tests do not reach, zero-padded past D."""
     xb, xq = datagen.cfg1(N=6_000, D=D, B=80, n_centers=64, seed=46 + D)
     b = build_index(xb, 96, dev, max_batch=128, max_nprobe=128)
     for nprobe in (1, 16, 96):

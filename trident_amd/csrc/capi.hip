@@ -137,7 +137,9 @@ struct Workspace {
     uint32_t* ub_best;               // [B]
     int32_t* seed_cnt;               // [B]
     int64_t ub_cap;
-    float* qt32;                     // band front end: queries, matrix-core tile layout
+    float* qt32;                     // band front end (Dq > 128): queries, matrix-core tile layout
+    uint32_t* qtb;                   // band front end (Dq <= 128): queries, bfloat16 split layout
+    uint32_t* cmtb;                  // band front end (Dq <= 128): centroids, bfloat16 split layout
     float* qn32;                     // [B] their squared norms
     float* cm32;                     // [nlist, Dq] centroid-major zero-padded centroids
     float* cmt32;                    // the centroids in the matrix-core tile layout
@@ -224,7 +226,10 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.ub_best = c.take<uint32_t>(B);
     w.seed_cnt = c.take<int32_t>(B);
     const int64_t Dq = band_dq(ix->D);
-    w.qt32 = c.take<float>((B + 15) / 16 * 16 * Dq);
+    const int64_t Dpb = Dq <= 128 ? 32 * band_steps_bf16((int)Dq) : 0;  // bfloat16 split dims
+    w.qt32 = c.take<float>(Dq > 128 ? (B + 15) / 16 * 16 * Dq : 0);
+    w.qtb = c.take<uint32_t>((B + 15) / 16 * 16 * Dpb);
+    w.cmtb = c.take<uint32_t>(((int64_t)ix->nlist + 15) / 16 * 16 * Dpb);
     w.qn32 = c.take<float>(B);
     w.cm32 = c.take<float>((int64_t)ix->nlist * Dq);
     w.cmt32 = c.take<float>(((int64_t)ix->nlist + 15) / 16 * 16 * Dq);
@@ -664,40 +669,49 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
             cn = w.cn32;
             cmax_dev = w.cmax2;
         }
+        const bool split = Dq <= 128;  // bfloat16 split operands, else float32
+        const int NS = split ? band_steps_bf16(Dq) : 0;
         pad_queries_kernel<<<(unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock), kBlock, 0,
-                             st>>>(xq, B, ix->D, Dq, w.qt32, w.qn32);
+                             st>>>(xq, B, ix->D, Dq, split ? nullptr : w.qt32, w.qn32, NS,
+                                   split ? reinterpret_cast<uint16_t*>(w.qtb) : nullptr);
         if ((rc = check_launch("pad_queries_kernel"))) return rc;
         float* a32 = reinterpret_cast<float*>(w.cd64);  // [B, nlist] approximations
-        if (Dq <= 128) {
+        if (split) {
+            const int64_t npair = ((int64_t)ix->nlist + 15) / 16 * 16 * 16 * NS;
+            centroid_bf16_kernel<<<(unsigned)std::min<int64_t>((npair + 255) / 256, 4096), 256, 0,
+                                   st>>>(cm, ix->nlist, Dq, NS, w.cmtb);
+            if ((rc = check_launch("centroid_bf16_kernel"))) return rc;
             const int64_t nst = ((ix->nlist + 15) / 16 + kStageTiles - 1) / kStageTiles;
             const int64_t spx = (nst + 7) / 8, nqb = (B + 63) / 64;
             const int64_t want = std::min<int64_t>(spx, std::max<int64_t>(1, kStreamBlocks / (8 * nqb)));
             const int64_t run_stages = (spx + want - 1) / want, nrun = (spx + run_stages - 1) / run_stages;
             const dim3 sgrid((unsigned)(8 * nqb * nrun));
-            switch (Dq >> 4) {
-#define TRIDENT_GEMM_CASE(NF)                                                                   \
-    case NF:                                                                                    \
-        coarse_gemm_stream_kernel<NF><<<sgrid, kBlock, 0, st>>>(w.qt32, w.qn32, B, cmt, cn,        \
-                                                                ix->nlist, Dq, (int)run_stages, a32); \
+            switch (NS) {
+#define TRIDENT_GEMM_CASE(NSV)                                                                  \
+    case NSV:                                                                                   \
+        coarse_gemm_bf16_kernel<NSV><<<sgrid, kBlock, 0, st>>>(w.qtb, w.qn32, B, w.cmtb, cn,       \
+                                                               ix->nlist, (int)run_stages, a32);  \
         break;
                 TRIDENT_GEMM_CASE(1) TRIDENT_GEMM_CASE(2) TRIDENT_GEMM_CASE(3) TRIDENT_GEMM_CASE(4)
-                TRIDENT_GEMM_CASE(5) TRIDENT_GEMM_CASE(6) TRIDENT_GEMM_CASE(7) TRIDENT_GEMM_CASE(8)
 #undef TRIDENT_GEMM_CASE
                 default:
                     return fail(TRIDENT_ERR_INVALID_ARGUMENT, "coarse GEMM: Dq=%d", (int)Dq);
             }
-            if ((rc = check_launch("coarse_gemm_stream_kernel"))) return rc;
+            if ((rc = check_launch("coarse_gemm_bf16_kernel"))) return rc;
         } else {
             const int64_t ncg = (ix->nlist + 16 * kGemmTiles - 1) / (16 * kGemmTiles);
             coarse_gemm_kernel<<<(unsigned)(8 * ((B + 63) / 64) * ((ncg + 7) / 8)), kBlock, 0, st>>>(
                 w.qt32, w.qn32, B, cmt, cn, ix->nlist, Dq, a32);
             if ((rc = check_launch("coarse_gemm_kernel"))) return rc;
         }
+        const double kappa = split ? band_kappa_bf16(Dq) : band_kappa_f32(Dq);
+        const double kabs = split ? band_kabs_bf16(Dq) : 0.0;
         const unsigned grid = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
         const int V = ix->nlist <= 1024 ? 16 : ix->nlist <= kBandMaxNlist ? 32 : 0;
 #define TRIDENT_BAND_LAUNCH(KPV, VV, SS)                                                         \
     select_band_kernel<KPV, VV, SS><<<grid, kBlock, 0, st>>>(                                   \
-        a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, nprobe,          \
+        a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, kappa, kabs,     \
+        nprobe,                                                                                 \
         w.probe_cids,                                                                           \
         w.probe_dqcs, nprobe, probe_cids, probe_dqcs, ld)
         if (nprobe <= 64) {

@@ -700,6 +700,19 @@ __global__ __launch_bounds__(256) void scatter_pairs_lds_kernel(
 // d64 <= T + E, so the nprobe-th smallest d64 is <= T + E and every centroid of the true
 // (d, cid) top-nprobe -- ties included -- has a <= T + 2E.  Those are the band; their exact d64
 // decide the selection, exactly as a full float64 pass would.
+//
+// bfloat16 split form (Dq <= 128, coarse_gemm_bf16_kernel): every float32 value x is split as
+// x = h + l + r with h = bf16(x), l = bf16(x - h) (round to nearest even; x - h is exact in
+// float32), so |x - h| <= 2^-8 |x|, |l| <= 2^-8 (1 + 2^-8) |x| and |r| <= 2^-16 |x|.  The matrix
+// cores sum the exact float32 products h_q h_c, h_q l_c and l_q h_c over the Dp = 32 ceil(Dq / 32)
+// (zero-padded) dimensions; the dropped terms l_q l_c + (h_q + l_q) r_c + r_q (h_c + l_c) +
+// r_q r_c are at most 3.02 * 2^-16 |q_d c_d| per dimension.  The h h products (<= (1 + 2^-7)
+// |q_d c_d|) pass through at most Dp / 2 + 2 additions, the mixed ones (<= 2^-7 (1 + 2^-7)
+// |q_d c_d| per pair) through at most Dp + 2, each with relative error <= 2^-23, so
+//   kappa = (Dp + 4) 2^-23 (1 + 2^-5) + 3.125 * 2^-16
+// bounds |s' - q.c| / sum |q_d c_d| to first order (the margins cover the second-order terms).
+// Subnormal bfloat16 operands or float32 products that the matrix cores flush to zero add at
+// most 3 Dp 2^-126 (1 + |q|_inf + |c|_inf) <= Dp 2^-100 (1 + nq + nc) in absolute terms.
 
 // Matrix-core tile layout of zero-padded float32 rows (Dq = D rounded up to 16, S = Dq / 4):
 // for rows 16 t .. 16 t + 15, float4 number (t S/4 + j) 64 + lane holds, for row 16 t + lane % 16
@@ -712,11 +725,37 @@ __device__ __forceinline__ size_t mfma_tile_offset(int row, int d, int S) {
            (sd & 3);
 }
 
+// bfloat16 split tile layout (NS 32-dim steps): for rows 16 t .. 16 t + 15, step s and part p
+// (0: h, 1: l), the 16 bytes ((t NS + s) 2 + p) 64 + lane hold row 16 t + lane % 16, dimensions
+// 32 s + 8 g .. 32 s + 8 g + 7 (g = lane / 16) -- one v_mfma_f32_16x16x32_bf16 operand, read by
+// a wave as 1 KiB contiguous.  Returns the offset of (row, d, p) in bfloat16 units.
+__device__ __forceinline__ size_t bf16_tile_offset(int row, int d, int NS, int p) {
+    const int s = d >> 5, k = d & 31;
+    return ((((size_t)(row >> 4) * NS + s) * 2 + p) * kWave + (row & 15) + 16 * (k >> 3)) * 8 +
+           (k & 7);
+}
+
+// bfloat16 bits of x rounded to nearest even; a finite x that would round to infinity is
+// truncated instead (no larger than the float32 products could hold anyway).
+__device__ __forceinline__ uint16_t bf16_rne(float x) {
+    const uint32_t u = __float_as_uint(x);
+    const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const bool fin = (u & 0x7f800000u) != 0x7f800000u;
+    return (uint16_t)(fin && (r & 0x7f80u) == 0x7f80u ? (u >> 16) : r);
+}
+
+// x = h + l + r: h = bf16(x), l = bf16(x - h) (x - h is exact in float32)
+__device__ __forceinline__ void split_bf16(float x, uint16_t& h, uint16_t& l) {
+    h = bf16_rne(x);
+    l = bf16_rne(x - __uint_as_float((uint32_t)h << 16));
+}
+
 // Queries in the tile layout (qt32) and their squared norms (float64 sum, float32 copy).
 __global__ __launch_bounds__(256) void pad_queries_kernel(const float* __restrict__ xq, int B,
                                                           int D, int Dq,
                                                           float* __restrict__ qt32,
-                                                          float* __restrict__ qn32) {
+                                                          float* __restrict__ qn32, int NS,
+                                                          uint16_t* __restrict__ qtb) {
     const int lane = threadIdx.x & 63;
     const int q = blockIdx.x * kWavesPerBlock + (int)(threadIdx.x >> 6);
     if (q >= B) return;
@@ -724,8 +763,16 @@ __global__ __launch_bounds__(256) void pad_queries_kernel(const float* __restric
     double acc = 0.0;
     for (int d = lane; d < Dq; d += kWave) {
         const float v = d < D ? xq[(size_t)q * D + d] : 0.0f;
-        qt32[mfma_tile_offset(q, d, S)] = v;
+        if (qt32) qt32[mfma_tile_offset(q, d, S)] = v;
         acc = fma((double)v, (double)v, acc);
+    }
+    if (qtb) {  // the bfloat16 split layout (NS 32-dim steps, zero past D)
+        for (int d = lane; d < 32 * NS; d += kWave) {
+            uint16_t h, l;
+            split_bf16(d < D ? xq[(size_t)q * D + d] : 0.0f, h, l);
+            qtb[bf16_tile_offset(q, d, NS, 0)] = h;
+            qtb[bf16_tile_offset(q, d, NS, 1)] = l;
+        }
     }
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) acc += __shfl_xor(acc, o, kWave);
@@ -789,7 +836,7 @@ __global__ __launch_bounds__(256) void pad_centroids_kernel(const float* __restr
 // kGemmTiles)) centroid groups), block 256.  Blocks are dealt to the XCDs round-robin, so block
 // b runs on XCD b % 8: XCD x takes centroid groups [x cpx, (x + 1) cpx) (cpx = ceil(ncg / 8)) for
 // every query block, and its share of the centroid tiles stays in its L2.  Used for Dq > 128
-// (coarse_gemm_stream_kernel takes Dq <= 128).  Each wave 16 queries (one query tile), all four
+// (coarse_gemm_bf16_kernel takes Dq <= 128).  Each wave 16 queries (one query tile), all four
 // waves the same kGemmTiles centroid tiles in the same order.  v_mfma_f32_16x16x4f32 with query
 // rows as A (16 x 4) and centroids as B (4 x 16), operands straight from the tile layouts: a
 // chunk of 32 k-steps is 8 + 8 coalesced float4 loads, issued whole before its 32 MFMAs; steps
@@ -869,29 +916,56 @@ __global__ __launch_bounds__(256) void coarse_gemm_kernel(const float* __restric
     }
 }
 
-// Dq <= 128: the coarse pass with a block's query tiles kept for a run of centroid stages.
-// One-dimensional grid of 8 * ceil(B / 64) * nrun blocks: block b runs on XCD x = b % 8 and
-// takes query block bx and run r of XCD x's share of the stages (kStageTiles 16-centroid tiles
-// each; XCD x owns stages [x spx, (x + 1) spx), split into nrun runs of run_stages), so its
-// centroid tiles stay in its L2.  The four waves' query operands stay in registers for the
-// whole run; each stage's tiles are fetched into registers while the waves compute the
-// previous stage from LDS, then written to the other LDS buffer.
-template <int F>  // Dq / 16: float4 per lane and row tile; only the F k-groups that hold data run
-__global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
-                                                                 const float* __restrict__ qn32,
-                                                                 int B,
-                                                                 const float* __restrict__ cmt32,
-                                                                 const float* __restrict__ cn32,
-                                                                 int nlist, int Dq,
-                                                                 int run_stages,
-                                                                 float* __restrict__ a32) {
+
+// Centroid rows cm32 [nlist, Dq] -> the bfloat16 split tile layout (NS steps), rows up to the
+// next multiple of 16 and dimensions past Dq zero.  One thread per (row, dimension pair).
+__global__ __launch_bounds__(256) void centroid_bf16_kernel(const float* __restrict__ cm32,
+                                                            int nlist, int Dq, int NS,
+                                                            uint32_t* __restrict__ cmtb) {
+    const int npair = 16 * NS;  // dimension pairs per row
+    const int64_t n = (int64_t)((nlist + 15) & ~15) * npair;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int row = (int)(i / npair), d = 2 * (int)(i - (int64_t)row * npair);
+        const float* src = cm32 + (size_t)row * Dq;
+        uint16_t h0, l0, h1, l1;
+        split_bf16(row < nlist && d < Dq ? src[d] : 0.0f, h0, l0);
+        split_bf16(row < nlist && d + 1 < Dq ? src[d + 1] : 0.0f, h1, l1);
+        // d even: (d, d + 1) share one 32-bit word of each part
+        cmtb[bf16_tile_offset(row, d, NS, 0) >> 1] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        cmtb[bf16_tile_offset(row, d, NS, 1) >> 1] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    }
+}
+
+// Dq <= 128: the coarse pass on the bfloat16 matrix cores, with a block's query tiles kept for a
+// run of centroid stages.  One-dimensional grid of 8 * ceil(B / 64) * nrun blocks: block b runs
+// on XCD x = b % 8 and takes query block bx and run r of XCD x's share of the stages
+// (kStageTiles 16-centroid tiles each; XCD x owns stages [x spx, (x + 1) spx), split into nrun
+// runs of run_stages), so its centroid tiles stay in its L2.  The four waves' split query
+// operands (NS 32-dim steps, 2 NS 16-byte operands per lane and row tile) stay in registers for
+// the whole run; each stage's tiles are fetched into registers while the waves compute the
+// previous stage from LDS, then written to the other LDS buffer.  Per tile four independent
+// accumulator chains: h h products of even and odd steps, and h l, l h products;
+// a = fma(-2, (H0 + H1) + (L0 + L1), nq32 + nc32).
+template <int NS>
+__global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* __restrict__ qtb,
+                                                               const float* __restrict__ qn32,
+                                                               int B,
+                                                               const uint32_t* __restrict__ cmtb,
+                                                               const float* __restrict__ cn32,
+                                                               int nlist, int run_stages,
+                                                               float* __restrict__ a32) {
     typedef float f4 __attribute__((ext_vector_type(4)));
-    constexpr int PT = (kStageTiles * F * kWave + kBlock - 1) / kBlock;  // float4 per thread, stage
-    __shared__ float4 s_b[2][PT * kBlock];
+    typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    constexpr int U = 2 * NS;                                            // u4 per lane and tile
+    constexpr int PT = (kStageTiles * U * kWave + kBlock - 1) / kBlock;  // u4 per thread, stage
+    static_assert(NS >= 1 && NS <= 4, "Dq <= 128");
+    static_assert(PT >= 1 && PT <= 4, "at most four u4 per thread and stage");
+    __shared__ u4 s_b[2][PT * kBlock];
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, g = lane >> 4;
-    static_assert(F >= 1 && F <= 8, "Dq <= 128");
     const int ntl_all = (nlist + 15) / 16;
     const int nst = (ntl_all + kStageTiles - 1) / kStageTiles, spx = (nst + 7) >> 3;
     const int nrun = (spx + run_stages - 1) / run_stages;
@@ -904,66 +978,57 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
     const bool wave_live = qb0 < B;  // waves past the last query still load and wait
     const int qtile = wave_live ? qb0 / 16 : 0;
     const int qb = wave_live ? qb0 : 0;
-    float4 av[F];  // rows past B are never stored
+    u4 av[U];  // rows past B are never stored
     {
-        const float4* qt = reinterpret_cast<const float4*>(qt32) + (size_t)qtile * F * kWave + lane;
+        const u4* qt = reinterpret_cast<const u4*>(qtb) + (size_t)qtile * U * kWave + lane;
 #pragma unroll
-        for (int j = 0; j < F; ++j) av[j] = qt[(size_t)j * kWave];
+        for (int j = 0; j < U; ++j) av[j] = qt[(size_t)j * kWave];
     }
-    const float4* cb = reinterpret_cast<const float4*>(cmt32);
-    // thread i moves float4s i, i + 256, ... of a stage's contiguous run (named registers: an
-    // array indexed in a loop went to scratch)
-    static_assert(PT >= 1 && PT <= 4, "at most four float4 per thread and stage");
-    float4 r0, r1, r2, r3;
-#define TRIDENT_FETCH(st_)                                                                       \
-    {                                                                                           \
-        const int t0_ = (st_) * kStageTiles, n_ = min(kStageTiles, ntl_all - t0_) * F * kWave;  \
-        const float4* p_ = cb + (size_t)t0_ * F * kWave; /* element 0 exists */                  \
-        const int i_ = (int)threadIdx.x;                                                         \
-        /* slots past the stage's tiles are never read: they load element 0 again */            \
-        r0 = p_[i_ < n_ ? i_ : 0];                                                               \
-        if constexpr (PT > 1) r1 = p_[i_ + kBlock < n_ ? i_ + kBlock : 0];                       \
-        if constexpr (PT > 2) r2 = p_[i_ + 2 * kBlock < n_ ? i_ + 2 * kBlock : 0];               \
-        if constexpr (PT > 3) r3 = p_[i_ + 3 * kBlock < n_ ? i_ + 3 * kBlock : 0];               \
-    }
-#define TRIDENT_PUT(b_)                                                                          \
-    {                                                                                           \
-        s_b[b_][threadIdx.x] = r0;                                                               \
-        if constexpr (PT > 1) s_b[b_][threadIdx.x + kBlock] = r1;                                \
-        if constexpr (PT > 2) s_b[b_][threadIdx.x + 2 * kBlock] = r2;                            \
-        if constexpr (PT > 3) s_b[b_][threadIdx.x + 3 * kBlock] = r3;                            \
-    }
-    TRIDENT_FETCH(s_beg)
-    TRIDENT_PUT(0)
+    const u4* cb = reinterpret_cast<const u4*>(cmtb);
+    // thread i moves u4s i, i + 256, ... of a stage's contiguous run (slots past the stage's
+    // tiles are never read: they load element 0 again)
+    u4 r[PT];
+    auto fetch = [&](int st) __attribute__((always_inline)) {
+        const int t0 = st * kStageTiles, n = min(kStageTiles, ntl_all - t0) * U * kWave;
+        const u4* p = cb + (size_t)t0 * U * kWave;
+#pragma unroll
+        for (int k = 0; k < PT; ++k) {
+            const int i = (int)threadIdx.x + k * kBlock;
+            r[k] = p[i < n ? i : 0];
+        }
+    };
+    auto put = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < PT; ++k) s_b[b][threadIdx.x + k * kBlock] = r[k];
+    };
+    fetch(s_beg);
+    put(0);
     __syncthreads();
     for (int st = s_beg; st < s_end; ++st) {
         const int buf = (st - s_beg) & 1;
-        if (st + 1 < s_end) TRIDENT_FETCH(st + 1)
+        if (st + 1 < s_end) fetch(st + 1);
         if (wave_live) {
             const int t0 = st * kStageTiles, ntl = min(kStageTiles, ntl_all - t0);
 #pragma unroll 1
             for (int t = 0; t < ntl; ++t) {
-                float4 bv[F];
+                u4 bv[U];
 #pragma unroll
-                for (int j = 0; j < F; ++j) bv[j] = s_b[buf][(t * F + j) * kWave + lane];
-                f4 acc4[4];
+                for (int j = 0; j < U; ++j) bv[j] = s_b[buf][(t * U + j) * kWave + lane];
+                // centroids are the A operand, queries the B operand
+                f4 h0 = {0.0f, 0.0f, 0.0f, 0.0f}, h1 = h0, l0 = h0, l1 = h0;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) acc4[u] = f4{0.0f, 0.0f, 0.0f, 0.0f};
-                // centroids are the A operand, queries the B operand; consecutive MFMAs go to
-                // different accumulators (k-step 4 j + u -> chain u)
-#pragma unroll
-                for (int j = 0; j < F; ++j) {
-                    acc4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].x, av[j].x, acc4[0], 0, 0, 0);
-                    acc4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].y, av[j].y, acc4[1], 0, 0, 0);
-                    acc4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, av[j].z, acc4[2], 0, 0, 0);
-                    acc4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].w, av[j].w, acc4[3], 0, 0, 0);
+                for (int s = 0; s < NS; ++s) {
+                    const bf8 cH = __builtin_bit_cast(bf8, bv[2 * s]),
+                              cL = __builtin_bit_cast(bf8, bv[2 * s + 1]);
+                    const bf8 qH = __builtin_bit_cast(bf8, av[2 * s]),
+                              qL = __builtin_bit_cast(bf8, av[2 * s + 1]);
+                    if (s & 1) h1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cH, qH, h1, 0, 0, 0);
+                    else h0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cH, qH, h0, 0, 0, 0);
+                    l0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cH, qL, l0, 0, 0, 0);
+                    l1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(cL, qH, l1, 0, 0, 0);
                 }
-                // matrix-core results: wait states before the first VALU read, fenced
-                __builtin_amdgcn_sched_barrier(0);
-                asm volatile("s_nop 7\n\ts_nop 7");
-                __builtin_amdgcn_sched_barrier(0);
-                const f4 acc = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
-                // lane (m, g) holds centroids n0 + 4 g .. + 3 of query qb + m
+                const f4 acc = (h0 + h1) + (l0 + l1);
+                // lane (m, g) holds centroids 16 (t0 + t) + 4 g .. + 3 of query qb + m
                 const int q = qb + m, c0 = 16 * (t0 + t) + 4 * g;
                 if (q < B) {
                     const float nq = qn32[q];
@@ -981,26 +1046,19 @@ __global__ __launch_bounds__(256) void coarse_gemm_stream_kernel(const float* __
                 }
             }
         }
-        if (st + 1 < s_end) TRIDENT_PUT(buf ^ 1)
+        if (st + 1 < s_end) put(buf ^ 1);
         __syncthreads();
     }
-#undef TRIDENT_FETCH
-#undef TRIDENT_PUT
 }
 
-#define TRIDENT_GEMM_STREAM(NF)                                                                 \
-    template __global__ void coarse_gemm_stream_kernel<NF>(const float*, const float*, int,      \
-                                                           const float*, const float*, int, int, \
-                                                           int, float*);
-TRIDENT_GEMM_STREAM(1)
-TRIDENT_GEMM_STREAM(2)
-TRIDENT_GEMM_STREAM(3)
-TRIDENT_GEMM_STREAM(4)
-TRIDENT_GEMM_STREAM(5)
-TRIDENT_GEMM_STREAM(6)
-TRIDENT_GEMM_STREAM(7)
-TRIDENT_GEMM_STREAM(8)
-#undef TRIDENT_GEMM_STREAM
+template __global__ void coarse_gemm_bf16_kernel<1>(const uint32_t*, const float*, int,
+                                                    const uint32_t*, const float*, int, int, float*);
+template __global__ void coarse_gemm_bf16_kernel<2>(const uint32_t*, const float*, int,
+                                                    const uint32_t*, const float*, int, int, float*);
+template __global__ void coarse_gemm_bf16_kernel<3>(const uint32_t*, const float*, int,
+                                                    const uint32_t*, const float*, int, int, float*);
+template __global__ void coarse_gemm_bf16_kernel<4>(const uint32_t*, const float*, int,
+                                                    const uint32_t*, const float*, int, int, float*);
 
 // One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM (any nlist), the
 // row streamed through a running filter.  T is any value with count(a <= T) >= nprobe over the
@@ -1022,7 +1080,7 @@ template <int KP, int V, bool STREAM>
 __global__ __launch_bounds__(256) void select_band_kernel(
     const float* __restrict__ a32, const double* __restrict__ xq64, const float* __restrict__ cm32,
     const unsigned long long* __restrict__ cmax_dev, double cmax_host, int B, int nlist, int D,
-    int Dq, int nprobe,
+    int Dq, double kappa, double kabs, int nprobe,
     int32_t* __restrict__ out_cids, float* __restrict__ out_dqcs, int ld,
     int32_t* __restrict__ out2_cids, float* __restrict__ out2_dqcs, int ld2) {
     // the band's centroids (up to 8 per lane); STREAM: the filter's list (up to 16 per lane),
@@ -1043,10 +1101,11 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     for (int d = lane; d < D; d += kWave) nq = fma(qrow[d], qrow[d], nq);
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) nq += __shfl_xor(nq, o, kWave);
-    const double kappa = (double)(Dq + 2) * 0x1p-23;
+    // kappa: the dot product's relative bound of the pass that wrote a32, kabs its absolute
+    // term per unit of 1 + nq + nc (float32 operands: (Dq + 2) 2^-23 and 0; bfloat16 split)
     const double cmax2 = cmax_dev ? __longlong_as_double((long long)*cmax_dev) : cmax_host;
-    const double E = (kappa + 0x1p-21) * (nq + cmax2) *
-                         (1.0 + 0x1p-10) + 1e-30;
+    const double E = (kappa + 0x1p-21) * (nq + cmax2) * (1.0 + 0x1p-10) +
+                     kabs * (1.0 + nq + cmax2) + 1e-30;
     const float Ef = __double2float_ru(E);
     // E carries a 2^-10 relative margin, which covers the float64 rounding of this sum
     auto cut_of = [&](float t) { return __double2float_ru((double)t + 2.0 * E); };
@@ -1127,7 +1186,17 @@ __global__ __launch_bounds__(256) void select_band_kernel(
             wave_sync();
             n = m;
         };
-        // eight of the lane's values per round, all loaded before the first is filtered
+        // eight of the lane's values per round, all loaded before the first is filtered, and the
+        // next round's loaded before this round is filtered
+        auto load8 = [&](float (&x)[8], int c0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * kWave + lane;
+                x[u] = c < nlist ? arow[c] : INFINITY;
+            }
+        };
+        float xn[8];
+        load8(xn, 0);
         for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
             if (n > kListCap - 8 * kWave) {  // the round could overflow the list: tighten T
                 float w[kListPer];
@@ -1143,10 +1212,8 @@ __global__ __launch_bounds__(256) void select_band_kernel(
             }
             float xs[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = c0 + u * kWave + lane;
-                xs[u] = c < nlist ? arow[c] : INFINITY;
-            }
+            for (int u = 0; u < 8; ++u) xs[u] = xn[u];
+            if (c0 + 8 * kWave < nlist) load8(xn, c0 + 8 * kWave);
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const bool take = c0 + u * kWave + lane < nlist && xs[u] <= cut;
@@ -1390,7 +1457,7 @@ __global__ __launch_bounds__(256) void select_band_kernel(
 #define TRIDENT_SELECT_BAND(KP, V, S)                                                           \
     template __global__ void select_band_kernel<KP, V, S>(                                      \
         const float*, const double*, const float*, const unsigned long long*, double, int, int,  \
-        int, int, int, int32_t*, float*, int, int32_t*, float*, int);
+        int, int, double, double, int, int32_t*, float*, int, int32_t*, float*, int);
 TRIDENT_SELECT_BAND(64, 16, false)
 TRIDENT_SELECT_BAND(64, 32, false)
 TRIDENT_SELECT_BAND(128, 16, false)

@@ -254,7 +254,10 @@ __global__ void scatter_pairs_kernel(const int32_t* __restrict__ probe_cids,
 constexpr int kGroupChunk = 2048;  // (query, probe) entries per block of the LDS grouping
 // band front end (frontend.hip)
 __global__ void pad_queries_kernel(const float* __restrict__ xq, int B, int D, int Dq,
-                                   float* __restrict__ qt32, float* __restrict__ qn32);
+                                   float* __restrict__ qt32, float* __restrict__ qn32, int NS,
+                                   uint16_t* __restrict__ qtb);
+__global__ void centroid_bf16_kernel(const float* __restrict__ cm32, int nlist, int Dq, int NS,
+                                     uint32_t* __restrict__ cmtb);
 __global__ void pad_centroids_kernel(const float* __restrict__ W, int ldw, int nlist, int D,
                                      int Dq, float* __restrict__ cm32, float* __restrict__ cmt32,
                                      float* __restrict__ cn32,
@@ -267,22 +270,31 @@ template <int KP, int V, bool STREAM>
 __global__ void select_band_kernel(const float* __restrict__ a32, const double* __restrict__ xq64,
                                    const float* __restrict__ cm32,
                                    const unsigned long long* __restrict__ cmax_dev,
-                                   double cmax_host, int B, int nlist, int D, int Dq, int nprobe,
+                                   double cmax_host, int B, int nlist, int D, int Dq,
+                                   double kappa, double kabs, int nprobe,
                                    int32_t* __restrict__ out_cids,
                                    float* __restrict__ out_dqcs, int ld,
                                    int32_t* __restrict__ out2_cids,
                                    float* __restrict__ out2_dqcs, int ld2);
 constexpr int kGemmTiles = 4;  // coarse_gemm_kernel: 16-centroid tiles per wave
-// coarse_gemm_stream_kernel (Dq <= 128): 16-centroid tiles per stage; the run of stages per
+// coarse_gemm_bf16_kernel (Dq <= 128): 16-centroid tiles per stage; the run of stages per
 // block is the longest that still gives a grid of about kStreamBlocks blocks
 constexpr int kStageTiles = 2;
 constexpr int kStreamBlocks = 5120;
-template <int F>
-__global__ void coarse_gemm_stream_kernel(const float* __restrict__ qt32,
-                                          const float* __restrict__ qn32, int B,
-                                          const float* __restrict__ cmt32,
-                                          const float* __restrict__ cn32, int nlist, int Dq,
-                                          int run_stages, float* __restrict__ a32);
+// Dq <= 128 on the bfloat16 matrix cores (NS = ceil(Dq / 32) steps of the split operands)
+template <int NS>
+__global__ void coarse_gemm_bf16_kernel(const uint32_t* __restrict__ qtb,
+                                        const float* __restrict__ qn32, int B,
+                                        const uint32_t* __restrict__ cmtb,
+                                        const float* __restrict__ cn32, int nlist, int run_stages,
+                                        float* __restrict__ a32);
+// relative and absolute dot-product bounds of the two coarse passes (select_band_kernel's E)
+inline double band_kappa_f32(int Dq) { return (double)(Dq + 2) * 0x1p-23; }
+inline int band_steps_bf16(int Dq) { return (Dq + 31) / 32; }
+inline double band_kappa_bf16(int Dq) {
+    return (double)(32 * band_steps_bf16(Dq) + 4) * 0x1p-23 * (1.0 + 0x1p-5) + 3.125 * 0x1p-16;
+}
+inline double band_kabs_bf16(int Dq) { return (double)(32 * band_steps_bf16(Dq)) * 0x1p-100; }
 // band front end: up to 32 x 64 approximations in registers (16 or 32 per lane); past that
 // each wave filters its streamed row through an LDS list (faster from nlist 4096 on than 64
 // values per lane in registers)
