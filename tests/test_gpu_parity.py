@@ -115,13 +115,16 @@ def test_band_front_end_split_adversarial(dev, low):
         _check_probes(b, xq, dev, nprobe)
 
 
-@pytest.mark.parametrize("offset", [3.0e3, 3.0e4])
-def test_band_front_end_stream_wide_band(dev, offset):
+@pytest.mark.parametrize("nlist,offset", [(4500, 3.0e3), (4500, 3.0e4), (8195, 0.0),
+                                          (8195, 3.0e3), (8195, 3.0e4)])
+def test_band_front_end_stream_wide_band(dev, nlist, offset):
     """Past 2048 centroids each wave filters its row through an LDS list tightened by
-    bisection.  Offsets from the origin widen the error band: to a few hundred centroids (the
-    band refined from the list 64 at a time) and to nearly all of them (the list cannot shrink,
-    the band is taken from the row again); the probes must still be the oracle's."""
-    nlist = 4500
+    bisection; from 8192 on it filters the row's 16-centroid tile minima first and reads only
+    the listed tiles (8195: rows padded to 8196 floats, a last tile of three centroids).
+    Offsets from the origin widen the error band: to a few hundred centroids (the band refined
+    from the list 64 at a time; more than 512 listed tiles stream the whole row) and to nearly
+    all of them (the list cannot shrink, the band is taken from the row again); the probes
+    must still be the oracle's."""
     xb, xq = datagen.cfg1(N=3 * nlist, D=64, B=48, n_centers=nlist, seed=45)
     b = build_index(xb + offset, nlist, dev, max_batch=64, max_nprobe=128)
     xq = (xq + offset).numpy()
@@ -129,6 +132,16 @@ def test_band_front_end_stream_wide_band(dev, offset):
     xq = np.concatenate([xq, dup]).astype(np.float32)
     for nprobe in (5, 64, 128):
         _check_probes(b, xq, dev, nprobe)
+
+
+def test_band_front_end_stream_wide_rows(dev):
+    """Rows wider than 128 dims (the float32 coarse pass) past 2048 centroids: the streaming
+    selector starts from the tile minima that pass writes; the probes must be the oracle's."""
+    nlist = 2500
+    xb, xq = datagen.cfg1(N=3 * nlist, D=200, B=48, n_centers=nlist, seed=48)
+    b = build_index(xb, nlist, dev, max_batch=64, max_nprobe=128)
+    for nprobe in (5, 64, 128):
+        _check_probes(b, xq.numpy(), dev, nprobe)
 
 
 @pytest.mark.parametrize("D", [12, 72, 100, 112])

@@ -29,12 +29,14 @@ CSRC = os.path.join(PKG, "csrc")
 OUT_DIR = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libtrident_hip.so")
 SOURCES = ["frontend.hip", "scan.hip", "batch.hip", "cm.hip", "capi.hip"]
-# Per-source flags.  batch.hip: matrix-core results in VGPRs (no accumulator-register reads in
-# the per-tile epilogue); no atomic optimizer (it turns the one-lane work-counter atomic into a
-# wave-wide one whose result is waited for at once, which would undo taking the next unit early).
+# Per-source flags.  batch.hip, cm.hip, frontend.hip: matrix-core results in VGPRs (no
+# accumulator-register reads in the per-tile epilogues; the coarse pass gains 13 us at configs[4]);
+# batch.hip: no atomic optimizer (it turns the one-lane work-counter atomic into a wave-wide one
+# whose result is waited for at once, which would undo taking the next unit early).
 EXTRA = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1",
                        "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
-         "cm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+         "cm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+         "frontend.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 HEADERS = ["common.hpp", "kernels.hpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -140,6 +140,7 @@ struct Workspace {
     float* qt32;                     // band front end (Dq > 128): queries, matrix-core tile layout
     uint32_t* qtb;                   // band front end (Dq <= 128): queries, bfloat16 split layout
     uint32_t* cmtb;                  // band front end (Dq <= 128): centroids, bfloat16 split layout
+    float* tmin;                     // [B, ceil(nlist / 16)] tile minima (nlist >= kTileMinNlist)
     float* qn32;                     // [B] their squared norms
     float* cm32;                     // [nlist, Dq] centroid-major zero-padded centroids
     float* cmt32;                    // the centroids in the matrix-core tile layout
@@ -230,6 +231,7 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.qt32 = c.take<float>(Dq > 128 ? (B + 15) / 16 * 16 * Dq : 0);
     w.qtb = c.take<uint32_t>((B + 15) / 16 * 16 * Dpb);
     w.cmtb = c.take<uint32_t>(((int64_t)ix->nlist + 15) / 16 * 16 * Dpb);
+    w.tmin = c.take<float>(ix->nlist >= kTileMinNlist && Dq <= 128 ? B * (((int64_t)ix->nlist + 15) / 16) : 0);
     w.qn32 = c.take<float>(B);
     w.cm32 = c.take<float>((int64_t)ix->nlist * Dq);
     w.cmt32 = c.take<float>(((int64_t)ix->nlist + 15) / 16 * 16 * Dq);
@@ -676,6 +678,8 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
                                    split ? reinterpret_cast<uint16_t*>(w.qtb) : nullptr);
         if ((rc = check_launch("pad_queries_kernel"))) return rc;
         float* a32 = reinterpret_cast<float*>(w.cd64);  // [B, nlist] approximations
+        // the streaming selector's tile minima (bfloat16 pass, from kTileMinNlist centroids)
+        float* tmin = ix->nlist >= kTileMinNlist && split ? w.tmin : nullptr;
         if (split) {
             const int64_t npair = ((int64_t)ix->nlist + 15) / 16 * 16 * 16 * NS;
             centroid_bf16_kernel<<<(unsigned)std::min<int64_t>((npair + 255) / 256, 4096), 256, 0,
@@ -690,7 +694,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
 #define TRIDENT_GEMM_CASE(NSV)                                                                  \
     case NSV:                                                                                   \
         coarse_gemm_bf16_kernel<NSV><<<sgrid, kBlock, 0, st>>>(w.qtb, w.qn32, B, w.cmtb, cn,       \
-                                                               ix->nlist, (int)run_stages, a32);  \
+                                                               ix->nlist, (int)run_stages, a32, tmin); \
         break;
                 TRIDENT_GEMM_CASE(1) TRIDENT_GEMM_CASE(2) TRIDENT_GEMM_CASE(3) TRIDENT_GEMM_CASE(4)
 #undef TRIDENT_GEMM_CASE
@@ -711,7 +715,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
 #define TRIDENT_BAND_LAUNCH(KPV, VV, SS)                                                         \
     select_band_kernel<KPV, VV, SS><<<grid, kBlock, 0, st>>>(                                   \
         a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, kappa, kabs,     \
-        nprobe,                                                                                 \
+        SS ? tmin : nullptr, split ? (ix->nlist + 3) & ~3 : ix->nlist, nprobe,                   \
         w.probe_cids,                                                                           \
         w.probe_dqcs, nprobe, probe_cids, probe_dqcs, ld)
         if (nprobe <= 64) {

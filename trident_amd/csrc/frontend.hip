@@ -946,7 +946,8 @@ __global__ __launch_bounds__(256) void centroid_bf16_kernel(const float* __restr
 // the whole run; each stage's tiles are fetched into registers while the waves compute the
 // previous stage from LDS, then written to the other LDS buffer.  Per tile four independent
 // accumulator chains: h h products of even and odd steps, and h l, l h products;
-// a = fma(-2, (H0 + H1) + (L0 + L1), nq32 + nc32).
+// a = fma(-2, (H0 + H1) + (L0 + L1), nq32 + nc32), in rows of lda = nlist rounded up to 4 floats
+// (the padding is never read); with tmin, also each query's 16-centroid tile minima.
 template <int NS>
 __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* __restrict__ qtb,
                                                                const float* __restrict__ qn32,
@@ -954,7 +955,8 @@ __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* _
                                                                const uint32_t* __restrict__ cmtb,
                                                                const float* __restrict__ cn32,
                                                                int nlist, int run_stages,
-                                                               float* __restrict__ a32) {
+                                                               float* __restrict__ a32,
+                                                               float* __restrict__ tmin) {
     typedef float f4 __attribute__((ext_vector_type(4)));
     typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
     typedef uint32_t u4 __attribute__((ext_vector_type(4)));
@@ -967,6 +969,7 @@ __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* _
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, g = lane >> 4;
     const int ntl_all = (nlist + 15) / 16;
+    const int lda = (nlist + 3) & ~3;
     const int nst = (ntl_all + kStageTiles - 1) / kStageTiles, spx = (nst + 7) >> 3;
     const int nrun = (spx + run_stages - 1) / run_stages;
     const int xcd = (int)(blockIdx.x & 7), local = (int)(blockIdx.x >> 3);
@@ -1001,6 +1004,26 @@ __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* _
 #pragma unroll
         for (int k = 0; k < PT; ++k) s_b[b][threadIdx.x + k * kBlock] = r[k];
     };
+    // tile minima (tmin, when not null: [B, ceil(nlist / 16)]) of the current 16-tile chunk:
+    // lane (m, g) holds tiles 16 ch + 4 g + [0, 4) of query qb + m, written as one 16-byte store
+    // per lane when the chunk moves on (tiles outside this block's run are left to the blocks
+    // that run them)
+    const int tile_lo = s_beg * kStageTiles, tile_hi = min(s_end * kStageTiles, ntl_all);
+    float mt0 = INFINITY, mt1 = INFINITY, mt2 = INFINITY, mt3 = INFINITY;
+    int chunk = -1;
+    auto flush_mt = [&]() __attribute__((always_inline)) {
+        const int q = qb + m, tb = 16 * chunk + 4 * g;
+        if (!tmin || chunk < 0 || q >= B) return;
+        float* dst = tmin + (size_t)q * ntl_all + tb;
+        if ((ntl_all & 3) == 0 && tb >= tile_lo && tb + 4 <= tile_hi) {
+            *reinterpret_cast<float4*>(dst) = make_float4(mt0, mt1, mt2, mt3);
+        } else {
+            const float mv[4] = {mt0, mt1, mt2, mt3};
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (tb + i >= tile_lo && tb + i < tile_hi) dst[i] = mv[i];
+        }
+    };
     fetch(s_beg);
     put(0);
     __syncthreads();
@@ -1030,18 +1053,44 @@ __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* _
                 const f4 acc = (h0 + h1) + (l0 + l1);
                 // lane (m, g) holds centroids 16 (t0 + t) + 4 g .. + 3 of query qb + m
                 const int q = qb + m, c0 = 16 * (t0 + t) + 4 * g;
-                if (q < B) {
-                    const float nq = qn32[q];
-                    float* dst = a32 + (size_t)q * nlist + c0;
-                    if ((nlist & 3) == 0 && c0 + 4 <= nlist) {
-                        const float4 nc = *reinterpret_cast<const float4*>(cn32 + c0);
-                        *reinterpret_cast<float4*>(dst) =
-                            make_float4(fmaf(-2.0f, acc[0], nq + nc.x), fmaf(-2.0f, acc[1], nq + nc.y),
-                                        fmaf(-2.0f, acc[2], nq + nc.z), fmaf(-2.0f, acc[3], nq + nc.w));
-                    } else {
+                const float nq = q < B ? qn32[q] : 0.0f;
+                float4 nc;
+                if ((nlist & 3) == 0 && c0 + 4 <= nlist) {
+                    nc = *reinterpret_cast<const float4*>(cn32 + c0);
+                } else {
+                    nc.x = c0 < nlist ? cn32[c0] : 0.0f;
+                    nc.y = c0 + 1 < nlist ? cn32[c0 + 1] : 0.0f;
+                    nc.z = c0 + 2 < nlist ? cn32[c0 + 2] : 0.0f;
+                    nc.w = c0 + 3 < nlist ? cn32[c0 + 3] : 0.0f;
+                }
+                const float ncv[4] = {nc.x, nc.y, nc.z, nc.w};
+                float o[4], mn = INFINITY;
 #pragma unroll
-                        for (int i = 0; i < 4; ++i)
-                            if (c0 + i < nlist) dst[i] = fmaf(-2.0f, acc[i], nq + cn32[c0 + i]);
+                for (int i = 0; i < 4; ++i) {
+                    o[i] = fmaf(-2.0f, acc[i], nq + ncv[i]);
+                    if (c0 + i < nlist) mn = fminf(mn, o[i]);
+                }
+                // rows of lda = nlist rounded up to 4 floats: one aligned 16-byte store
+                // (c0 < nlist: c0 and lda are multiples of 4, so c0 + 4 <= lda)
+                if (q < B && c0 < nlist)
+                    *reinterpret_cast<float4*>(a32 + (size_t)q * lda + c0) = make_float4(o[0], o[1], o[2], o[3]);
+                if (tmin) {
+                    // the tile's minimum for query q (lanes m, m + 16, m + 32, m + 48), kept by lane
+                    // group (tile / 4) % 4 in slot tile % 4
+                    mn = fminf(mn, __shfl_xor(mn, 16, kWave));
+                    mn = fminf(mn, __shfl_xor(mn, 32, kWave));
+                    const int tt = t0 + t;
+                    if ((tt >> 4) != chunk) {
+                        flush_mt();
+                        chunk = tt >> 4;
+                        mt0 = mt1 = mt2 = mt3 = INFINITY;
+                    }
+                    if (g == ((tt >> 2) & 3)) {
+                        const int sl = tt & 3;
+                        mt0 = sl == 0 ? mn : mt0;
+                        mt1 = sl == 1 ? mn : mt1;
+                        mt2 = sl == 2 ? mn : mt2;
+                        mt3 = sl == 3 ? mn : mt3;
                     }
                 }
             }
@@ -1049,16 +1098,17 @@ __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* _
         if (st + 1 < s_end) put(buf ^ 1);
         __syncthreads();
     }
+    if (wave_live) flush_mt();
 }
 
 template __global__ void coarse_gemm_bf16_kernel<1>(const uint32_t*, const float*, int,
-                                                    const uint32_t*, const float*, int, int, float*);
+                                                    const uint32_t*, const float*, int, int, float*, float*);
 template __global__ void coarse_gemm_bf16_kernel<2>(const uint32_t*, const float*, int,
-                                                    const uint32_t*, const float*, int, int, float*);
+                                                    const uint32_t*, const float*, int, int, float*, float*);
 template __global__ void coarse_gemm_bf16_kernel<3>(const uint32_t*, const float*, int,
-                                                    const uint32_t*, const float*, int, int, float*);
+                                                    const uint32_t*, const float*, int, int, float*, float*);
 template __global__ void coarse_gemm_bf16_kernel<4>(const uint32_t*, const float*, int,
-                                                    const uint32_t*, const float*, int, int, float*);
+                                                    const uint32_t*, const float*, int, int, float*, float*);
 
 // One wave per query: V approximations per lane (nlist <= 64 V), or, STREAM (any nlist), the
 // row streamed through a running filter.  T is any value with count(a <= T) >= nprobe over the
@@ -1075,12 +1125,13 @@ template __global__ void coarse_gemm_bf16_kernel<4>(const uint32_t*, const float
 // the filter: the band is then taken from the row again with cut = T + 2E for the T reached.
 // A band of <= 128 (the usual case: a few more than nprobe) is ranked by counting, each entry
 // against all others in (d, cid) order; a wider one streams through the (d, cid) register list
-// 64 centroids at a time.  Outputs as select_probes_wave_kernel.
+// 64 centroids at a time.  Outputs as select_probes_wave_kernel.  Row q of a32 starts at
+// q lda; STREAM with tmin first filters the row's tile minima (below).
 template <int KP, int V, bool STREAM>
 __global__ __launch_bounds__(256) void select_band_kernel(
     const float* __restrict__ a32, const double* __restrict__ xq64, const float* __restrict__ cm32,
     const unsigned long long* __restrict__ cmax_dev, double cmax_host, int B, int nlist, int D,
-    int Dq, double kappa, double kabs, int nprobe,
+    int Dq, double kappa, double kabs, const float* __restrict__ tmin, int lda, int nprobe,
     int32_t* __restrict__ out_cids, float* __restrict__ out_dqcs, int ld,
     int32_t* __restrict__ out2_cids, float* __restrict__ out2_dqcs, int ld2) {
     // the band's centroids (up to 8 per lane); STREAM: the filter's list (up to 16 per lane),
@@ -1094,7 +1145,7 @@ __global__ __launch_bounds__(256) void select_band_kernel(
     const int q = blockIdx.x * kWavesPerBlock + wid;
     if (q >= B) return;
     const double* qrow = xq64 + (size_t)q * D;
-    const float* arow = a32 + (size_t)q * nlist;
+    const float* arow = a32 + (size_t)q * lda;
     int32_t* band = s_band[wid];
     // the error bound E (float64, then rounded up to float32)
     double nq = 0.0;
@@ -1186,47 +1237,121 @@ __global__ __launch_bounds__(256) void select_band_kernel(
             wave_sync();
             n = m;
         };
-        // eight of the lane's values per round, all loaded before the first is filtered, and the
-        // next round's loaded before this round is filtered
-        auto load8 = [&](float (&x)[8], int c0) __attribute__((always_inline)) {
+        // before a round that can add `room` entries: tighten T over the list (bisection, then
+        // the entries above the new cut dropped); false when the list cannot shrink below
+        // kListCap - room (the filter closes)
+        auto tighten = [&](int room) __attribute__((always_inline)) {
+            if (n <= kListCap - room) return true;
+            float w[kListPer];
+            wave_sync();
+            load_list(w);
+            T = bisect(w, std::integral_constant<int, kListPer>{}, T, 32);
+            cut = cut_of(T);
+            compact(w, cut);
+            if (n <= kListCap - room) return true;
+            open = false;
+            return false;
+        };
+        // streams src[0, len) through the list (entry ids: the indices): eight of the lane's
+        // values per round, all loaded before the first is filtered, and the next round's loaded
+        // before this round is filtered
+        auto stream = [&](const float* src, int len) __attribute__((always_inline)) {
+            auto load8 = [&](float (&x)[8], int c0) __attribute__((always_inline)) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int c = c0 + u * kWave + lane;
-                x[u] = c < nlist ? arow[c] : INFINITY;
+                for (int u = 0; u < 8; ++u) {
+                    const int c = c0 + u * kWave + lane;
+                    x[u] = c < len ? src[c] : INFINITY;
+                }
+            };
+            float xn[8];
+            load8(xn, 0);
+            for (int c0 = 0; c0 < len; c0 += 8 * kWave) {
+                if (!tighten(8 * kWave)) break;
+                float xs[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) xs[u] = xn[u];
+                if (c0 + 8 * kWave < len) load8(xn, c0 + 8 * kWave);
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const bool take = c0 + u * kWave + lane < len && xs[u] <= cut;
+                    const uint64_t mk = __ballot(take);
+                    if (mk == 0ull) continue;
+                    if (take) {
+                        const int at = n + mask_rank(mk);
+                        lval[at] = xs[u];
+                        band[at] = c0 + u * kWave + lane;
+                    }
+                    n += __popcll(mk);
+                }
             }
         };
-        float xn[8];
-        load8(xn, 0);
-        for (int c0 = 0; c0 < nlist; c0 += 8 * kWave) {
-            if (n > kListCap - 8 * kWave) {  // the round could overflow the list: tighten T
+        // With the coarse pass's 16-centroid tile minima (tmin), those first: T with
+        // count(tile minimum <= T) >= nprobe over them has count(a <= T) >= nprobe over the row
+        // (one centroid per tile at least) and sits near the row's nprobe-th value.  Every
+        // approximation a <= cut lies in a tile whose minimum is <= cut, and the filter over the
+        // minima ends with all of those tiles listed: only their 16 values each are read (one
+        // listed tile per lane at a time).  More than 512 such tiles (a wide band) fall back to
+        // streaming the whole row from the T reached, a closed tile filter from T = +inf.
+        const int ntl = (nlist + 15) >> 4;
+        bool whole_row = true;
+        if (tmin && ntl >= nprobe) {
+            stream(tmin + (size_t)q * ntl, ntl);
+            if (open) {
                 float w[kListPer];
                 wave_sync();
                 load_list(w);
-                T = bisect(w, std::integral_constant<int, kListPer>{}, T, 32);
+                T = bisect(w, std::integral_constant<int, kListPer>{}, T, 2);
                 cut = cut_of(T);
                 compact(w, cut);
-                if (n > kListCap - 8 * kWave) {
-                    open = false;
-                    break;
-                }
-            }
-            float xs[8];
+                if (n <= 8 * kWave) {
+                    whole_row = false;
+                    int tl[8];  // listed tile lane + 64 k (-1 past the list)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) xs[u] = xn[u];
-            if (c0 + 8 * kWave < nlist) load8(xn, c0 + 8 * kWave);
+                    for (int k = 0; k < 8; ++k) tl[k] = k * kWave + lane < n ? band[k * kWave + lane] : -1;
+                    const int n1 = n;
+                    n = 0;
+                    wave_sync();
+#pragma unroll 1
+                    for (int k = 0; k < 8; ++k) {
+                        if (k * kWave >= n1) break;
+                        int tk = tl[0];  // tl[k] by a select chain (no indexed register array)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const bool take = c0 + u * kWave + lane < nlist && xs[u] <= cut;
-                const uint64_t mk = __ballot(take);
-                if (mk == 0ull) continue;
-                if (take) {
-                    const int at = n + mask_rank(mk);
-                    lval[at] = xs[u];
-                    band[at] = c0 + u * kWave + lane;
+                        for (int j = 1; j < 8; ++j) tk = k == j ? tl[j] : tk;
+                        const int c0 = 16 * tk;
+                        float xv[16];
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) xv[i] = tk >= 0 && c0 + i < nlist ? arow[c0 + i] : INFINITY;
+                        auto filter8 = [&](auto off_c) __attribute__((always_inline)) {
+                            constexpr int O = decltype(off_c)::value;
+#pragma unroll
+                            for (int i = O; i < O + 8; ++i) {
+                                const bool take = xv[i] <= cut;
+                                const uint64_t mk = __ballot(take);
+                                if (take) {
+                                    const int at = n + mask_rank(mk);
+                                    lval[at] = xv[i];
+                                    band[at] = c0 + i;
+                                }
+                                n += __popcll(mk);
+                            }
+                        };
+                        if (!tighten(8 * kWave)) break;
+                        filter8(std::integral_constant<int, 0>{});
+                        if (!tighten(8 * kWave)) break;
+                        filter8(std::integral_constant<int, 8>{});
+                    }
+                } else {
+                    n = 0;
+                    wave_sync();
                 }
-                n += __popcll(mk);
+            } else {
+                T = cut = INFINITY;
+                open = true;
+                n = 0;
+                wave_sync();
             }
         }
+        if (whole_row) stream(arow, nlist);
         if (open) {
             float w[kListPer];
             wave_sync();
@@ -1457,7 +1582,7 @@ __global__ __launch_bounds__(256) void select_band_kernel(
 #define TRIDENT_SELECT_BAND(KP, V, S)                                                           \
     template __global__ void select_band_kernel<KP, V, S>(                                      \
         const float*, const double*, const float*, const unsigned long long*, double, int, int,  \
-        int, int, double, double, int, int32_t*, float*, int, int32_t*, float*, int);
+        int, int, double, double, const float*, int, int, int32_t*, float*, int, int32_t*, float*, int);
 TRIDENT_SELECT_BAND(64, 16, false)
 TRIDENT_SELECT_BAND(64, 32, false)
 TRIDENT_SELECT_BAND(128, 16, false)

@@ -271,7 +271,8 @@ __global__ void select_band_kernel(const float* __restrict__ a32, const double* 
                                    const float* __restrict__ cm32,
                                    const unsigned long long* __restrict__ cmax_dev,
                                    double cmax_host, int B, int nlist, int D, int Dq,
-                                   double kappa, double kabs, int nprobe,
+                                   double kappa, double kabs, const float* __restrict__ tmin,
+                                   int lda, int nprobe,
                                    int32_t* __restrict__ out_cids,
                                    float* __restrict__ out_dqcs, int ld,
                                    int32_t* __restrict__ out2_cids,
@@ -287,7 +288,7 @@ __global__ void coarse_gemm_bf16_kernel(const uint32_t* __restrict__ qtb,
                                         const float* __restrict__ qn32, int B,
                                         const uint32_t* __restrict__ cmtb,
                                         const float* __restrict__ cn32, int nlist, int run_stages,
-                                        float* __restrict__ a32);
+                                        float* __restrict__ a32, float* __restrict__ tmin);
 // relative and absolute dot-product bounds of the two coarse passes (select_band_kernel's E)
 inline double band_kappa_f32(int Dq) { return (double)(Dq + 2) * 0x1p-23; }
 inline int band_steps_bf16(int Dq) { return (Dq + 31) / 32; }
@@ -299,6 +300,9 @@ inline double band_kabs_bf16(int Dq) { return (double)(32 * band_steps_bf16(Dq))
 // each wave filters its streamed row through an LDS list (faster from nlist 4096 on than 64
 // values per lane in registers)
 constexpr int kBandMaxNlist = 2048;
+// from this many centroids on, the bfloat16 coarse pass also writes each query's 16-centroid
+// tile minima and the streaming selector reads only the tiles that can hold band members
+constexpr int kTileMinNlist = 8192;
 inline int band_dq(int D) { return (D + 15) & ~15; }
 
 constexpr int kCoarseQW = 4;       // queries per wave of coarse_dist_kernel
