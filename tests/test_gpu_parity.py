@@ -134,6 +134,17 @@ def test_band_front_end_stream_wide_band(dev, nlist, offset):
         _check_probes(b, xq, dev, nprobe)
 
 
+@pytest.mark.parametrize("nlist", [1, 2, 3, 5])
+def test_band_front_end_tiny_nlist(dev, nlist):
+    """A handful of centroids: the approximation rows are padded to 4 floats, more than the
+    nlist doubles of the coarse-distance buffer they share below 3 centroids; every query must
+    still get the oracle's probes (and no row may spill into the next query's)."""
+    xb, xq = datagen.cfg1(N=2_000, D=40, B=300, n_centers=8, seed=49)
+    b = build_index(xb, nlist, dev, max_batch=512, max_nprobe=8)
+    for nprobe in sorted({1, nlist}):
+        _check_probes(b, xq.numpy(), dev, nprobe)
+
+
 def test_band_front_end_stream_wide_rows(dev):
     """Rows wider than 128 dims (the float32 coarse pass) past 2048 centroids: the streaming
     selector starts from the tile minima that pass writes; the probes must be the oracle's."""

@@ -190,7 +190,10 @@ Workspace carve(const TridentIndexView* ix, void* base, int64_t B, int64_t nprob
     w.xrot64 = c.take<double>(B * ix->D_pad);
     w.xrot32 = c.take<float>(B * ix->D_pad);
     w.qerr = c.take<double>(B * ix->D_pad);
-    w.cd64 = c.take<double>(B * ix->nlist);
+    // float64 coarse distances [B, nlist], or the band path's float32 approximations in rows of
+    // band_lda(nlist) floats (never more bytes: band_lda(n) <= n + 3 floats <= 2 n for n >= 3,
+    // and the rows of smaller n get the extra room here)
+    w.cd64 = c.take<double>(B * std::max<int64_t>(ix->nlist, (band_lda(ix->nlist) + 1) / 2));
     w.probe_cids = c.take<int32_t>(B * nprobe);
     w.probe_dqcs = c.take<float>(B * nprobe);
     w.counts = c.take<int32_t>(2 * ((int64_t)ix->nlist + 1));
@@ -715,7 +718,7 @@ int run_front_end(const TridentIndexView* ix, const float* xq, int B, int nprobe
 #define TRIDENT_BAND_LAUNCH(KPV, VV, SS)                                                         \
     select_band_kernel<KPV, VV, SS><<<grid, kBlock, 0, st>>>(                                   \
         a32, w.xq64, cm, cmax_dev, ix->cent_norm_max, B, ix->nlist, ix->D, Dq, kappa, kabs,     \
-        SS ? tmin : nullptr, split ? (ix->nlist + 3) & ~3 : ix->nlist, nprobe,                   \
+        SS ? tmin : nullptr, split ? band_lda(ix->nlist) : ix->nlist, nprobe,                    \
         w.probe_cids,                                                                           \
         w.probe_dqcs, nprobe, probe_cids, probe_dqcs, ld)
         if (nprobe <= 64) {

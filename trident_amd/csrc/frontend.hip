@@ -969,7 +969,7 @@ __global__ __launch_bounds__(256) void coarse_gemm_bf16_kernel(const uint32_t* _
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int m = lane & 15, g = lane >> 4;
     const int ntl_all = (nlist + 15) / 16;
-    const int lda = (nlist + 3) & ~3;
+    const int lda = band_lda(nlist);
     const int nst = (ntl_all + kStageTiles - 1) / kStageTiles, spx = (nst + 7) >> 3;
     const int nrun = (spx + run_stages - 1) / run_stages;
     const int xcd = (int)(blockIdx.x & 7), local = (int)(blockIdx.x >> 3);

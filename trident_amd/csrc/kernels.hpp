@@ -292,6 +292,9 @@ __global__ void coarse_gemm_bf16_kernel(const uint32_t* __restrict__ qtb,
 // relative and absolute dot-product bounds of the two coarse passes (select_band_kernel's E)
 inline double band_kappa_f32(int Dq) { return (double)(Dq + 2) * 0x1p-23; }
 inline int band_steps_bf16(int Dq) { return (Dq + 31) / 32; }
+// row length (floats) of the bfloat16 coarse pass's approximations: nlist rounded up to 4, so
+// that each tile's results are one aligned 16-byte store
+__host__ __device__ inline int band_lda(int nlist) { return (nlist + 3) & ~3; }
 inline double band_kappa_bf16(int Dq) {
     return (double)(32 * band_steps_bf16(Dq) + 4) * 0x1p-23 * (1.0 + 0x1p-5) + 3.125 * 0x1p-16;
 }
