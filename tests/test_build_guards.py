@@ -91,7 +91,7 @@ def kernel_resources(code_objects):
 
 # The hot kernels of the batched route: each must keep its working set in registers (a scratch
 # reload inside their loops serialises the loads in flight).
-HOT = ("lb_scan_kernelILi1E", "ub_scan_kernelILi2ELi4E", "coarse_gemm_bf16_kernelILi4E",
+HOT = ("lb_scan_kernelILi1E", "lb_scan_kernelILi2E", "ub_scan_kernelILi2ELi4E", "coarse_gemm_bf16_kernelILi4E",
        "select_band_kernel", "refine_survivors_kernelILb1ELi256E", "cm_scan_kernelILi32E")
 
 

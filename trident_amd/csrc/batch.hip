@@ -1684,7 +1684,8 @@ void lb_scan_kernel(BatchArgs a) {
                 const bool hv = lane < nq;
                 const LbRec L = a.lbr[pb + (hv ? lane : 0)];
                 s_kq[wid][lane] = hv ? L.kq : INT_MIN;
-                s_qf[wid][lane] = hv ? make_float4(L.c1f, L.c2f, L.H32, 0.0f)
+                // .w: the slot's query id, for the survivor flush (no global reads there)
+                s_qf[wid][lane] = hv ? make_float4(L.c1f, L.c2f, L.H32, __int_as_float(a.pair_qid[pb + lane]))
                                      : make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // never passes
             }
         }
@@ -1706,7 +1707,7 @@ void lb_scan_kernel(BatchArgs a) {
             __builtin_amdgcn_wave_barrier();
             if (lane < QW) {
                 const int c = s_scnt[wid][lane];
-                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[a.pair_qid[pb + lane]], c) : 0;
+                s_sbase[wid][lane] = c ? atomicAdd(&a.cand_cnt[__float_as_int(s_qf[wid][lane].w)], c) : 0;
                 s_scnt[wid][lane] = 0;
             }
             __builtin_amdgcn_wave_barrier();
@@ -1715,7 +1716,7 @@ void lb_scan_kernel(BatchArgs a) {
                 const int jj = (int)(ent & 31u);
                 const int slot = s_sbase[wid][jj] + atomicAdd(&s_scnt[wid][jj], 1);
                 if (slot < a.cap)
-                    a.cand_id[(size_t)a.pair_qid[pb + jj] * a.cap + slot] = v0 + (int)(ent >> 5);
+                    a.cand_id[(size_t)__float_as_int(s_qf[wid][jj].w) * a.cap + slot] = v0 + (int)(ent >> 5);
             }
             __builtin_amdgcn_wave_barrier();
             if (lane < QW) s_scnt[wid][lane] = 0;
@@ -1733,8 +1734,8 @@ void lb_scan_kernel(BatchArgs a) {
                 for (int r = 0; r < 4; ++r) {
                     const bool ps = pass(h, r);
                     const uint64_t pm = __ballot(ps);
-                    if (pm == 0ull) continue;
-                    if (nsq + __popcll(pm) > kLbQ) flush();
+                    if (__builtin_expect(pm == 0ull, 1)) continue;
+                    if (__builtin_expect(nsq + __popcll(pm) > kLbQ, 0)) flush();
                     if (ps) {
                         const int idx = __builtin_amdgcn_mbcnt_hi(
                             (uint32_t)(pm >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)pm, 0u));
@@ -1780,12 +1781,15 @@ void lb_scan_kernel(BatchArgs a) {
                 }
                 int mh = max(max(h0[0], h0[1]), max(h0[2], h0[3]));
                 if constexpr (TWO) mh = max(mh, max(max(h1[0], h1[1]), max(h1[2], h1[3])));
-                if (__ballot(mh >= thh) == 0ull) return;
+                if (__builtin_expect(__ballot(mh >= thh) == 0ull, 1)) return;
                 // the lo plane continues from 256 (plain hi sum) + kq in the same registers
                 {
-                    const v4i k0 = *reinterpret_cast<const v4i*>(&s_kq[wid][4 * g]);
+                    // the LDS address formed here (hoisted, it would stay live for the unit)
+                    int gl = g;
+                    asm volatile("" : "+v"(gl));
+                    const v4i k0 = *reinterpret_cast<const v4i*>(&s_kq[wid][4 * gl]);
                     v4i k1 = {0, 0, 0, 0};
-                    if constexpr (TWO) k1 = *reinterpret_cast<const v4i*>(&s_kq[wid][16 + 4 * g]);
+                    if constexpr (TWO) k1 = *reinterpret_cast<const v4i*>(&s_kq[wid][16 + 4 * gl]);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         h0[r] = ((h0[r] - hq4[0][r]) << 8) + k0[r];
@@ -1822,7 +1826,7 @@ void lb_scan_kernel(BatchArgs a) {
                     __builtin_amdgcn_ds_bpermute(src, SB == 1 || (t >> 2) == 0 ? thr_r[0] : thr_r[SB - 1]);
                 int m = max(max(S[0][0], S[0][1]), max(S[0][2], S[0][3]));
                 if constexpr (TWO) m = max(m, max(max(S[1][0], S[1][1]), max(S[1][2], S[1][3])));
-                if (__ballot(m >= th) == 0ull) return;
+                if (__builtin_expect(__ballot(m >= th) == 0ull, 1)) return;
                 queue([&](int h, int r) __attribute__((always_inline)) { return S[h][r] >= th; }, TWO, li);
             } else {
                 const float Av = s_A[buf][t * 16 + j], rv = s_r[buf][t * 16 + j];
@@ -1837,7 +1841,7 @@ void lb_scan_kernel(BatchArgs a) {
                 for (int h = 0; h < (TWO ? 2 : 1); ++h)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) any |= pass(h, r);
-                if (__ballot(any) == 0ull) return;
+                if (__builtin_expect(__ballot(any) == 0ull, 1)) return;
                 queue(pass, TWO, li);
             }
         };
