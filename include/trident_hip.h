@@ -120,8 +120,9 @@ typedef struct TridentIndexView {
 } TridentIndexView;
 
 /* How modes 2 and 10 are executed.  Both routes are exact; they differ in speed only.  Mode 10
- * batched is the float32 matrix-core cluster-major scan: it needs the base in device memory,
- * K <= 128 and D_pad <= 256 (AUTO takes it from 4 queries per probed cluster on average). */
+ * batched is the float32 matrix-core cluster-major scan: it needs K <= 128 and D_pad <= 1024
+ * (AUTO takes it from 4 queries per probed cluster on average, and always for a base in mapped
+ * host memory, where it reads each probed row once per unit instead of once per pair). */
 enum TridentRoute {
     TRIDENT_ROUTE_AUTO = 0,     /* batched when clusters are shared by enough queries */
     TRIDENT_ROUTE_PAIR = 1,     /* one workgroup per (cluster, query): Stage X / Y / Z per pair

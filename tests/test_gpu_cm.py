@@ -173,15 +173,23 @@ def test_cm_route_requirements(cm_sets, dev):
         run_search(b, xqd, 4, 129, mode=10, route=2)
 
 
-def test_cm_host_base_is_rejected_on_the_batched_route(dev):
+def test_cm_host_base_matrix_route(dev):
+    """Mode 10 on the matrix cores with the FP32 base in mapped host memory: exact on the
+    explicit and the automatic route (which takes the matrix cores for a host base), and a probed
+    row crosses PCIe once per unit, not once per (query, probe) pair as on the per-pair route."""
     xb, xq = datagen.cfg2(N=10_000, D=128, B=64, n_centers=16, seed=68)
     b = build_index(xb, 16, dev, xb_placement="host", max_batch=64)
     try:
-        with pytest.raises(TridentError, match="device memory"):
-            run_search(b, _q(xq.numpy(), dev), 4, 10, mode=10, route=2)
+        xqd = _q(xq.numpy(), dev)
         _, rd, ri = oracle_search(b, xq.numpy(), 4, 10)
-        d, i = run_search(b, _q(xq.numpy(), dev), 4, 10, mode=10, route=0)
-        assert_exact(d, i, rd, ri, "cm host base auto")
+        rows = {}
+        for route in (2, 0, 1):
+            hrows = torch.zeros(2, dtype=torch.int64, device=dev)
+            d, i, _ = b.ix.search(xqd, 4, mode=10, k=10, route=route, host_rows_buf=hrows)
+            torch.cuda.synchronize()
+            assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"cm host base route={route}")
+            rows[route] = int(hrows[0])
+        assert 0 < rows[2] < rows[1] and 0 < rows[0] < rows[1], rows
     finally:
         torch.cuda.synchronize()
         b.ix.storage._host_buf.free()

@@ -450,13 +450,15 @@ inline int seed_slice_count(int K, bool xb_host, bool fine) {
 }
 
 // Mode 10: the matrix-core cluster-major scan (cm_scan_kernel, cm_scan_wide_kernel past 256
-// dims) or the per-pair float64 scan.  The matrix-core route reads every probed row from the
-// base, so it needs the base in HBM; D_pad <= 1024 (the refine's query row in LDS) and K <= 128
-// (the merge's lists).  AUTO takes it when clusters are shared by at least 4 queries on average
-// (16-row tiles with fewer rows leave most of each matrix instruction idle).
+// dims) or the per-pair float64 scan.  Both read every probed row from the base; the matrix-core
+// route reads a row once per unit (up to 64 queries of its cluster) instead of once per (query,
+// probe) pair.  It needs D_pad <= 1024 (the refine's query row in LDS) and K <= 128 (the
+// merge's lists).  AUTO takes it when clusters are shared by at least 4 queries on average
+// (16-row tiles with fewer rows leave most of each matrix instruction idle), and always for a
+// base in mapped host memory (every row read crosses PCIe, and this route reads fewer).
 int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, int B, int K,
                     int nprobe, bool xb_host, bool* cm) {
-    const bool ok = ix->orig_ids_sorted && !xb_host && K <= 128 && ix->D_pad <= 1024 &&
+    const bool ok = ix->orig_ids_sorted && K <= 128 && ix->D_pad <= 1024 &&
                     ix->nlist <= kMaxBatchedNlist && ix->N < (1 << 27) &&
                     max_units_of((int64_t)B * nprobe, ix->nlist) < 0x7fffffff;
     switch (sp->route) {
@@ -466,14 +468,13 @@ int choose_cm_route(const TridentIndexView* ix, const TridentSearchParams* sp, i
         case TRIDENT_ROUTE_BATCHED:
             if (!ok)
                 return fail(TRIDENT_ERR_UNSUPPORTED,
-                            "mode 10 batched route needs orig_ids_sorted, the base in device "
-                            "memory, K <= 128, D_pad <= 1024, nlist <= %d and N < 2^27 (K=%d, "
-                            "D_pad=%d, nlist=%d, N=%d)",
+                            "mode 10 batched route needs orig_ids_sorted, K <= 128, D_pad <= "
+                            "1024, nlist <= %d and N < 2^27 (K=%d, D_pad=%d, nlist=%d, N=%d)",
                             kMaxBatchedNlist, K, ix->D_pad, ix->nlist, ix->N);
             *cm = true;
             return TRIDENT_OK;
         case TRIDENT_ROUTE_AUTO:
-            *cm = ok && (double)B * nprobe >= 4.0 * ix->nlist;
+            *cm = ok && (xb_host || (double)B * nprobe >= 4.0 * ix->nlist);
             return TRIDENT_OK;
         default:
             return fail(TRIDENT_ERR_INVALID_ARGUMENT, "route=%d outside {0,1,2}", sp->route);
@@ -1110,6 +1111,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.qerr = w.qerr;
         b.tau = w.tau64;
         b.B = B;
+        b.xb_host = xb_host ? 1 : 0;
         b.host_rows = host_rows;
         b.cand_key = w.cand_key;
         b.cand_id = w.cand_id;
@@ -1181,8 +1183,13 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         else fine_tau_kernel<128><<<qg, kBlock, 0, st>>>(b, B);
         if ((rc = check_launch("fine_tau_kernel"))) return rc;
         const dim3 rgrid(qg, (unsigned)std::min<int64_t>((cap + kWave - 1) / kWave, 16));
-        if (ix->D <= 256) refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);
-        else refine_survivors_kernel<false, 1024><<<rgrid, kBlock, 0, st>>>(b, B);
+        if (ix->D <= 256) {
+            if (xb_host) refine_survivors_kernel<true, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+            else refine_survivors_kernel<false, 256><<<rgrid, kBlock, 0, st>>>(b, B);
+        } else {
+            if (xb_host) refine_survivors_kernel<true, 1024><<<rgrid, kBlock, 0, st>>>(b, B);
+            else refine_survivors_kernel<false, 1024><<<rgrid, kBlock, 0, st>>>(b, B);
+        }
         if ((rc = check_launch("refine_survivors_kernel"))) return rc;
         m.use_prev = 0;
         m.tau_sq_out = out->tau_sq;

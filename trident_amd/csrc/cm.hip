@@ -200,6 +200,8 @@ __global__ __launch_bounds__(256) void cm_scan_kernel(BatchArgs a) {
         const int gq = wid / R, rr = wid - gq * R;
         const bool active = gq < G;
         const int nq = active ? min(kCmQW, cnt - gq * kCmQW) : 0;
+        // rows this unit reads from a host-mapped base: its slice, once
+        if (a.host_rows && a.xb_host && tid == 0) atomicAdd(a.host_rows, (unsigned long long)(ve - vb));
 
         // ---- this wave's queries: A operands (row j, dims g D4 .. g D4 + D4 - 1) and norms ----
         // (initialised on every path: nothing is carried from the previous unit)
@@ -395,6 +397,8 @@ __global__ __launch_bounds__(256) void cm_scan_wide_kernel(BatchArgs a) {
         const int gq = wid / R, rr = wid - gq * R;
         const bool active = gq < G;
         const int nq = active ? min(kCmQW, cnt - gq * kCmQW) : 0;
+        // rows this unit reads from a host-mapped base: its slice, once
+        if (a.host_rows && a.xb_host && tid == 0) atomicAdd(a.host_rows, (unsigned long long)(ve - vb));
         const bool qv = j < nq;
         const int qid = active && qv ? a.pair_qid[start + gq * kCmQW + j] : 0;
         const float* qrow = a.xq + (size_t)qid * D;
