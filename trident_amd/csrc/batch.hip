@@ -81,11 +81,11 @@ __device__ __forceinline__ int seed_slices(int S, int seed_sl) { return min(S, s
 // lower-bound units of cluster c (all its queries, <= uqB per unit, every slice).
 __device__ __forceinline__ int units_of_entry(const int32_t* seg, const int32_t* vec_off,
                                               int nlist, int uqB, int seed_all, int seed_sl, int sv,
-                                              int e) {
+                                              int svb, int e) {
     const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
     const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
     const int uq = p ? uqB : kUnitQ0;
-    const int S = splits_of(vec_off[c + 1] - vec_off[c], sv);
+    const int S = splits_of(vec_off[c + 1] - vec_off[c], p ? svb : sv);
     return q > 0 ? ((q + uq - 1) / uq) * (p ? S : seed_slices(S, seed_sl)) : 0;
 }
 
@@ -100,12 +100,12 @@ __device__ __forceinline__ int groups_of_cluster(const int32_t* seg, int c) {
 __global__ __launch_bounds__(256) void unit_scan_local_kernel(const int32_t* seg,
                                                               const int32_t* vec_off, int nlist,
                                                               int uqB, int seed_all, int seed_sl,
-                                                              int sv, int32_t* unit_off,
+                                                              int sv, int svb, int32_t* unit_off,
                                                               int32_t* grp_off, int32_t* blk_tot) {
     __shared__ uint32_t s_wtot[kWavesPerBlock];
     const int i = blockIdx.x * kBlock + threadIdx.x;
     const uint32_t nu =
-        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, seed_sl, sv, i)
+        i < 2 * nlist ? (uint32_t)units_of_entry(seg, vec_off, nlist, uqB, seed_all, seed_sl, sv, svb, i)
                       : 0u;
     const uint32_t ng = i < nlist ? (uint32_t)groups_of_cluster(seg, i) : 0u;
     uint32_t tu = 0, tg = 0;
@@ -158,7 +158,7 @@ __device__ __forceinline__ int seg_search(const int32_t* off, int n, int x) {
 // vector slice and query block.  Slices start on 64-vector blocks and are never empty (n > 64 S
 // (S - 1) whenever S = ceil(n / sv) > 1, for sv >= 512).
 __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off,
-                                                        int nlist, int uqB, int seed_all, int sv,
+                                                        int nlist, int uqB, int seed_all, int sv, int svb,
                                                         const int32_t* unit_off,
                                                         int4* units, int max_units,
                                                         const int32_t* grp_off, int2* groups,
@@ -176,7 +176,7 @@ __global__ __launch_bounds__(256) void unit_fill_kernel(const int32_t* seg, cons
         const int e = seg_search(unit_off, E, u);
         const int p = e >= nlist ? 1 : 0, c = e - p * nlist;
         const int n = vec_off[c + 1] - vec_off[c];
-        const int S = splits_of(n, sv);
+        const int S = splits_of(n, p ? svb : sv);
         const int local = u - unit_off[e];
         const int q = (p || seed_all ? seg[c + 1] : seg[nlist + 1 + c]) - seg[c];
         const int uq = p ? uqB : kUnitQ0;
@@ -1683,7 +1683,12 @@ void lb_scan_kernel(BatchArgs a) {
             if (lane < QW) {
                 const bool hv = lane < nq;
                 const LbRec L = a.lbr[pb + (hv ? lane : 0)];
-                s_kq[wid][lane] = hv ? L.kq : INT_MIN;
+                // integer groups: kq - 256 ceil(kq_pre / 256), the lo plane's start after the
+                // row's hi-plane sum (which began at ceil(kq_pre / 256)) is shifted left by 8
+                // (mod 2^32: the true sum 256 acc_hi + kq fits in int32)
+                s_kq[wid][lane] = !hv ? INT_MIN
+                                : int_ok ? (int)((uint32_t)L.kq - ((uint32_t)((L.kq_pre + 255) >> 8) << 8))
+                                         : L.kq;
                 // .w: the slot's query id, for the survivor flush (no global reads there)
                 s_qf[wid][lane] = hv ? make_float4(L.c1f, L.c2f, L.H32, __int_as_float(a.pair_qid[pb + lane]))
                                      : make_float4(0.0f, 0.0f, -INFINITY, 0.0f);  // never passes
@@ -1792,8 +1797,8 @@ void lb_scan_kernel(BatchArgs a) {
                     if constexpr (TWO) k1 = *reinterpret_cast<const v4i*>(&s_kq[wid][16 + 4 * gl]);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        h0[r] = ((h0[r] - hq4[0][r]) << 8) + k0[r];
-                        if constexpr (TWO) h1[r] = ((h1[r] - hq4[1][r]) << 8) + k1[r];
+                        h0[r] = (int)(((uint32_t)h0[r] << 8) + (uint32_t)k0[r]);
+                        if constexpr (TWO) h1[r] = (int)(((uint32_t)h1[r] << 8) + (uint32_t)k1[r]);
                     }
                 }
 #pragma unroll

@@ -1142,7 +1142,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
                                                             ix->nlist, b.unit_q, 0,
                                                             seed_slice_count(K, false, false),
-                                                            kSplitVec, w.unit_off, w.grp_off,
+                                                            kSplitVec, kSplitVec, w.unit_off, w.grp_off,
                                                             w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
             unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
@@ -1151,7 +1151,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, 0,
-                                 kSplitVec, w.unit_off, w.units, (int)w.max_units, w.grp_off,
+                                 kSplitVec, kSplitVec, w.unit_off, w.units, (int)w.max_units, w.grp_off,
                                  w.groups, (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         const unsigned qg = (unsigned)((B + kWavesPerBlock - 1) / kWavesPerBlock);
@@ -1288,12 +1288,15 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         // TRIDENT_UB_SEED 2 seeds from every probe, 0 and 1 from the first p_init
         const int seed_all = sp->ub_seed == 2 ? 1 : 0;
         const int split_vec = ix->D_pad <= 256 ? kSplitVecNarrow : kSplitVec;
+        const int split_vec_b =
+            ix->D_pad <= 256 && (int64_t)ix->N >= (int64_t)kLongSliceRows * ix->nlist ? 2 * kSplitVecNarrow
+                                                                                  : split_vec;
         const int seed_sl = seed_slice_count(K, xb_host, b.fine_mode != 0);
         {
             const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= kBlock (kMaxBatchedNlist)
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
                                                             ix->nlist, b.unit_q, seed_all, seed_sl,
-                                                            split_vec, w.unit_off, w.grp_off,
+                                                            split_vec, split_vec_b, w.unit_off, w.grp_off,
                                                             w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
             unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
@@ -1302,7 +1305,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, seed_all,
-                                 split_vec, w.unit_off, w.units, (int)w.max_units, w.grp_off,
+                                 split_vec, split_vec_b, w.unit_off, w.units, (int)w.max_units, w.grp_off,
                                  w.groups, (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if ((rc = launch_pair_prep(b, st))) return rc;

@@ -389,6 +389,11 @@ constexpr int kUnitQ0 = 16;
 // more work per vector, so shorter slices balance the workgroups better).
 constexpr int kSplitVecNarrow = 2048;
 constexpr int kSplitVec = 1024;
+// Lower-bound units of the narrow layout over clusters of >= kLongSliceRows rows on average take
+// slices twice as long: half the units' fixed costs (prologue, survivor flush) at configs[4]
+// (6,100 rows per cluster: pass B -3 %); shorter searches keep the shorter slices, whose units
+// balance the workgroups better near the end of the launch.
+constexpr int kLongSliceRows = 4096;
 constexpr int kMaxSplit = 8;
 constexpr int kCtrStride = 32;  // int32 between per-XCD counters (one 128-byte line each)
 
@@ -421,14 +426,15 @@ inline int64_t max_groups_of(int64_t pairs, int64_t nlist) {
 // seed_all: the seeding units cover every pair of a cluster (TRIDENT_UB_SEED 2), not only its
 // pass-1 pairs; seed_sl: the seeding units scan the first seed_sl slices of each cluster.
 // Two launches of ceil(2 nlist / kBlock) blocks; blk_tot holds 2 * kBlock block totals.
+// sv: the seeding units' slice length, svb: the lower-bound units'.
 __global__ void unit_scan_local_kernel(const int32_t* seg, const int32_t* vec_off, int nlist,
-                                       int uqB, int seed_all, int seed_sl, int sv,
+                                       int uqB, int seed_all, int seed_sl, int sv, int svb,
                                        int32_t* unit_off, int32_t* grp_off, int32_t* blk_tot);
 __global__ void unit_scan_carry_kernel(int nlist, const int32_t* blk_tot, int nblk,
                                        int32_t* unit_off, int32_t* grp_off);
 
 __global__ void unit_fill_kernel(const int32_t* seg, const int32_t* vec_off, int nlist, int uqB,
-                                 int seed_all, int sv, const int32_t* unit_off, int4* units, int max_units,
+                                 int seed_all, int sv, int svb, const int32_t* unit_off, int4* units, int max_units,
                                  const int32_t* grp_off, int2* groups, int max_groups);
 
 __global__ void fill_u64_kernel(unsigned long long* p, unsigned long long v, int64_t n);
