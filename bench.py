@@ -165,7 +165,8 @@ class Workload:
         if cached:
             log(f"index loaded from {index_cache} in {self.build_s:.1f}s")
         else:
-            log(f"k-means {t_train:.1f}s, index build {self.ix.build_time_s:.1f}s, total {self.build_s:.1f}s")
+            log(f"k-means {t_train:.1f}s, index build {self.ix.build_time_s:.1f}s, total {self.build_s:.1f}s; "
+                f"rows within a cluster by {getattr(self.st, 'within', 'id')}")
             if index_cache:
                 t2 = time.perf_counter()
                 persist.save_index(self.ix, index_cache, include_base=False, mean64=mean64, R64=R64,
@@ -452,6 +453,7 @@ def measure_primary(cfg_id, cfg, args, dev):
            "pruning": {"candidates": tot, "dims_scanned_frac": round(dims / max(tot * ix.D_pad, 1), 4),
                        "survivors_frac": round(surv / max(tot, 1), 6), "refined_kept": ins},
            "nprobe": nprobe, "K": K, "B": B, "N": N, "D": D, "nlist": cfg["nlist"],
+           "row_order": getattr(w.st, "within", "id"),
            "hbm_footprint": ix.hbm_footprint(),
            "host_bytes": int(w.st.xb_sorted.numel() * 4) if w.xb_host else 0}
     if w.xb_host:
@@ -631,7 +633,8 @@ def main():
         "config": {"workload": f"BASELINE {cfg['desc']}, N={r['N']}, D={r['D']}, nlist={r['nlist']}, "
                                f"nprobe={r['nprobe']}, K={r['K']}, B={r['B']}",
                    "route": ("batched" if r["route"] == _lib.ROUTE_BATCHED else "pair") if args.mode == 2 else "cm_exact",
-                   "ub_seed": args.ub, "p_init": r["p_init"], "tile_size": cfg["T"], "parallelism": "single GPU",
+                   "ub_seed": args.ub, "p_init": r["p_init"], "tile_size": cfg["T"], "row_order": r["row_order"],
+                   "parallelism": "single GPU",
                    "xb_placement": "host (mapped, out of core)" if cfg["host"] else "device"},
         "roofline": roof,
         "cpu_baseline": r["cpu"],

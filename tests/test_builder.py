@@ -381,3 +381,52 @@ def test_row_code_norms(which, hist_ix, gmm_ix, wide_ix):
         lo = rng.integers(-128, 128, size=(len(loc), D_pad))
         dots = np.abs(((codes - 128) * lo).sum(1)).astype(np.float64)
         assert np.all(dots <= got * np.sqrt((lo * lo).sum(1).astype(np.float64)))
+
+
+def _two_shapes(seed=0):
+    """Blob clusters (isotropic Gaussians, 32 dims) and elongated ones (a uniform segment per
+    cluster with small noise), 12 clusters of 4,000 rows each, with each cluster's mean."""
+    g = np.random.default_rng(seed)
+    n, k, D = 4000, 12, 32
+    lid = np.repeat(np.arange(k), n).astype(np.int64)
+    centers = g.uniform(0, 100, size=(k, D)).astype(np.float32)
+    blob = centers[lid] + g.normal(0, 4.0, size=(n * k, D)).astype(np.float32)
+    direction = g.normal(size=(k, D)).astype(np.float32)
+    direction /= np.linalg.norm(direction, axis=1, keepdims=True)
+    t = g.uniform(-30, 30, size=(n * k, 1)).astype(np.float32)
+    line = centers[lid] + t * direction[lid] + g.normal(0, 0.05, size=(n * k, D)).astype(np.float32)
+    out = {}
+    for name, x in (("blob", blob), ("line", line)):
+        mean = np.stack([x[lid == c].mean(0) for c in range(k)])
+        r = np.linalg.norm(x - mean[lid], axis=1).astype(np.float32)
+        out[name] = (x, lid, r, k)
+    return out
+
+
+def test_within_cluster_order_follows_the_seeding_score():
+    """Rows ordered by residual norm seed tighter thresholds on blob clusters (the first slice is
+    the core, near every query of the cluster) and far looser ones on elongated clusters (the
+    core is far from a query at either end); 'auto' takes the better order, and either order is
+    a cluster-sorted permutation with the same clusters."""
+    from trident_amd.index import seed_order_scores
+    sets = _two_shapes()
+    for name, (x, lid, r, k) in sets.items():
+        sc = seed_order_scores(torch.as_tensor(x), torch.as_tensor(lid), torch.as_tensor(r), k, sv=1024)
+        if name == "blob":
+            assert sc["residual"] < 0.99 * sc["id"], sc
+        else:
+            assert sc["id"] < 0.99 * sc["residual"], sc
+    for name, (x, lid, r, k) in sets.items():
+        st = {w: SharedClusterStorage(x, lid, r, k, device="cpu", within=w) for w in ("id", "residual")}
+        for w, s in st.items():
+            perm = s.sort_perm.astype(np.int64)
+            assert np.array_equal(np.sort(perm), np.arange(len(lid)))
+            assert np.all(np.diff(lid[perm]) >= 0)
+            np.testing.assert_array_equal(s.cluster_vec_off.cpu().numpy(), st["id"].cluster_vec_off.cpu().numpy())
+            np.testing.assert_array_equal(s.xb_sorted.cpu().numpy(), x[perm])
+        pr = st["residual"].sort_perm.astype(np.int64)
+        for c in range(k):
+            rc = r[pr[lid[pr] == c]]
+            assert np.all(np.diff(rc) >= 0)
+        assert np.array_equal(st["id"].sort_perm, np.argsort(lid, kind="stable").astype(np.int32))
+        assert SharedClusterStorage(x, lid, r, k, device="cpu").within == ("residual" if name == "blob" else "id")
