@@ -166,7 +166,8 @@ class Workload:
             log(f"index loaded from {index_cache} in {self.build_s:.1f}s")
         else:
             log(f"k-means {t_train:.1f}s, index build {self.ix.build_time_s:.1f}s, total {self.build_s:.1f}s; "
-                f"rows within a cluster by {getattr(self.st, 'within', 'id')}")
+                f"rows within a cluster by {getattr(self.st, 'within', 'id')} "
+                f"(seeding scores {getattr(self.st, 'seed_scores', None)})")
             if index_cache:
                 t2 = time.perf_counter()
                 persist.save_index(self.ix, index_cache, include_base=False, mean64=mean64, R64=R64,

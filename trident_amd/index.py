@@ -283,10 +283,11 @@ class SharedClusterStorage:
             raise ValueError(f"within={within!r}: 'auto', 'residual' or 'id'")
         xb = xb_raw if isinstance(xb_raw, torch.Tensor) else torch.as_tensor(np.ascontiguousarray(xb_raw))
         rv = None if r_vec is None else _as_tensor(r_vec, self.dev, torch.float32)
+        self.seed_scores = None
         if rv is None:
             within = "id"
         elif within == "auto":
-            sc = seed_order_scores(xb, lid, rv, self.nlist)
+            sc = self.seed_scores = seed_order_scores(xb, lid, rv, self.nlist)
             within = "residual" if sc["residual"] < 0.99 * sc["id"] else "id"
         self.within = within
         if within == "residual":
