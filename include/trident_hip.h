@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-#define TRIDENT_ABI_VERSION 5
+#define TRIDENT_ABI_VERSION 6
 
 enum TridentStatus {
     TRIDENT_OK = 0,
@@ -117,6 +117,12 @@ typedef struct TridentIndexView {
      * Cauchy-Schwarz (the row's norm times the query block's largest lo-plane norm) instead of
      * 128 sum |lo|, so fewer tiles need the lo plane; NULL keeps the per-query bound. */
     const float* vec_cn;
+    /* Rows of each seeding cluster the batched route's seeding pass scans (no counterpart in the
+     * reference): 0 = one slice of up to 2048 rows (two slices past K = 64, or for a host base
+     * without a fine level); a positive value caps each slice at max(512, seed_rows) rows (before
+     * rounding up to 64), for an index whose rows within a cluster are ordered by residual norm,
+     * so that a cluster's first rows are its best seeds.  Results do not depend on it. */
+    int32_t seed_rows;
 } TridentIndexView;
 
 /* How modes 2 and 10 are executed.  Both routes are exact; they differ in speed only.  Mode 10

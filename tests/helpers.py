@@ -13,7 +13,7 @@ class Built:
 
 def build_index(xb, nlist, device, tile_size=None, seed=0, niter=6, per_cluster_sq8=1, var_block=0,
                 max_batch=1024, max_nprobe=128, k=10, xb_placement="device", list_ids=None,
-                centroids=None, use_pca=1):
+                centroids=None, use_pca=1, within="auto"):
     """Cluster (unless lists are given) and build a TridentV4Index on ``device``."""
     xb = xb.float().contiguous()
     if list_ids is None:
@@ -23,7 +23,8 @@ def build_index(xb, nlist, device, tile_size=None, seed=0, niter=6, per_cluster_
         lid = np.asarray(list_ids, np.int32)
         r = clustering.residual_norms(xb, torch.as_tensor(cen), torch.as_tensor(lid, dtype=torch.int64)).numpy()
         mean64, R64 = clustering.residual_pca(xb, torch.as_tensor(cen), torch.as_tensor(lid, dtype=torch.int64))
-    st = SharedClusterStorage(xb.cpu().numpy(), lid, r, nlist, device=device, xb_placement=xb_placement)
+    st = SharedClusterStorage(xb.cpu().numpy(), lid, r, nlist, device=device, xb_placement=xb_placement,
+                              within=within)
     T = tile_size or choose_tile(xb.shape[1])
     ix = TridentV4Index(st, cen, mean64, R64, tile_size=T, per_cluster_sq8=per_cluster_sq8,
                         var_block=var_block, max_batch=max_batch, max_nprobe=max_nprobe, device=device, k=k,

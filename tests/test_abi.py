@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
     exported = set(re.findall(r"\bT (trident_[a-z0-9_]+)", out))
     assert exported == set(names), f"undeclared exports: {exported - set(names)}"
-    assert L.trident_abi_version() == _lib.ABI_VERSION == 5
+    assert L.trident_abi_version() == _lib.ABI_VERSION == 6
 
 
 def test_struct_layout_matches_header(tmp_path):

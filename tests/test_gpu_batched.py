@@ -8,7 +8,7 @@ import pytest
 import torch
 
 from tests.helpers import assert_exact, build_index, oracle_search, run_search
-from trident_amd import datagen
+from trident_amd import datagen, ext
 
 pytestmark = pytest.mark.gpu
 
@@ -133,6 +133,31 @@ def test_batched_large_clusters_split_into_slices(dev, K):
         _, rd, ri = oracle_search(b, xq.numpy(), nprobe, K)
         d, i = run_search(b, _q(xq.numpy(), dev), nprobe, K, mode=2, ub=1, route=2)
         assert_exact(d, i, rd, ri, f"slices K={K} nprobe={nprobe}")
+
+
+@pytest.mark.parametrize("seed_rows", [0, 100, 1024, 4096])
+def test_seed_rows_changes_no_result(dev, seed_rows):
+    """TridentIndexView.seed_rows caps the seeding slices (0: 2048 rows; else max(512, seed_rows),
+    at most 2048): ~3750 rows per cluster in residual-norm order are seeded from their first
+    ~1920, 960 or 512 rows.  Only the threshold's tightness changes: every seeded threshold stays
+    >= the query's exact K-th distance and the results equal the oracle's."""
+    xb, xq = datagen.cfg2(N=60_000, D=128, B=300, n_centers=16, seed=31)
+    b = build_index(xb, 16, dev, max_batch=512, within="residual")
+    assert b.ix.storage.within == "residual" and b.ix.seed_rows > 0
+    assert np.diff(b.vec_off).max() > 2048
+    v = b.ix.view()
+    v.seed_rows = seed_rows
+    q = _q(xq.numpy(), dev)
+    for nprobe, K in ((3, 10), (8, 64)):
+        _, rd, ri = oracle_search(b, xq.numpy(), nprobe, K)
+        d = torch.empty((q.shape[0], K), dtype=torch.float32, device=dev)
+        i = torch.empty((q.shape[0], K), dtype=torch.int64, device=dev)
+        tau = torch.empty(q.shape[0], dtype=torch.float32, device=dev)
+        ext.search_view(v, q, nprobe, d, i, mode=2, ub_seed=1, route=2, tau_sq=tau)
+        torch.cuda.synchronize()
+        assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"seed_rows={seed_rows} K={K}")
+        t = tau.cpu().numpy().astype(np.float64)
+        assert (t >= rd[:, K - 1]).all(), f"seeded threshold below the K-th distance (K={K})"
 
 
 def test_batched_many_units_per_workgroup(dev):

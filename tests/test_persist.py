@@ -31,8 +31,9 @@ def cpu_index():
 
 def _same_index(a, b):
     for n in ("N", "D", "D_pad", "nlist", "tile_size", "per_cluster_sq8", "total_tiles", "rot_sq_min",
-              "rot_sq_max"):
+              "rot_sq_max", "seed_rows"):
         assert getattr(a, n) == getattr(b, n), n
+    assert a.storage.within == b.storage.within
     for n in _TENSORS:
         ta, tb = getattr(a, n), getattr(b, n)
         assert ta.dtype == tb.dtype and torch.equal(ta.cpu(), tb.cpu()), n
@@ -57,6 +58,20 @@ def test_round_trip_with_base(cpu_index, tmp_path):
     _same_index(ix, got)
     with np.load(tmp_path / "meta.npz", allow_pickle=False) as z:
         assert np.array_equal(z["mean64"], mean64) and np.array_equal(z["R64"], R64)
+
+
+def test_round_trip_keeps_the_row_order(tmp_path):
+    """A layout ordered by residual norm within clusters is reloaded as such (the seeding pass
+    then scans TridentIndexView.seed_rows rows per seeding slice)."""
+    xb, _ = datagen.cfg2(N=4000, D=64, B=8, n_centers=16, seed=9)
+    cen, lid, r, mean64, R64, _ = clustering.train_clustering(xb, 12, seed=0, niter=4)
+    st = SharedClusterStorage(xb.numpy(), lid, r, 12, device="cpu", within="residual")
+    ix = TridentV4Index(st, cen, mean64, R64, tile_size=64, device="cpu", max_batch=8, max_nprobe=8)
+    assert ix.seed_rows > 0
+    persist.save_index(ix, str(tmp_path))
+    got = persist.load_index(str(tmp_path), device="cpu", max_batch=8, max_nprobe=8)
+    assert got.storage.within == "residual"
+    _same_index(ix, got)
 
 
 def test_round_trip_without_base(cpu_index, tmp_path):

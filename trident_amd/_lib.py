@@ -10,7 +10,7 @@ _PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG, "libtrident_hip.so")
 
 TRIDENT_OK = 0
-ABI_VERSION = 5  # TRIDENT_ABI_VERSION
+ABI_VERSION = 6  # TRIDENT_ABI_VERSION
 MODE_SQ8_RERANK = 0
 MODE_SQ8 = 1
 MODE_CASCADE = 2
@@ -37,7 +37,7 @@ class TridentIndexView(ctypes.Structure):
         ("sq8_cells", _P),
         ("cent_rows", _P), ("cent_tiles", _P), ("cent_norms", _P), ("cent_norm_max", _f64),
         ("r_vec_sorted", _P), ("fine_codes", _P), ("fine_qp", _P), ("cluster_bounds", _P),
-        ("vec_cn", _P),
+        ("vec_cn", _P), ("seed_rows", _i32),
     ]
 
 

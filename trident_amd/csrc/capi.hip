@@ -259,6 +259,8 @@ int validate_index(const TridentIndexView* ix) {
     if (ix->D_pad < ix->D || ix->D_pad % 32 != 0)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "D_pad=%d must be a multiple of 32 >= D=%d",
                     ix->D_pad, ix->D);
+    if (ix->seed_rows < 0)
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT, "seed_rows=%d must be >= 0", ix->seed_rows);
     if (ix->tile_size < 64 || ix->tile_size % 64 != 0)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "tile_size=%d must be a positive multiple of 64",
                     ix->tile_size);
@@ -1292,11 +1294,15 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
             ix->D_pad <= 256 && (int64_t)ix->N >= (int64_t)kLongSliceRows * ix->nlist ? 2 * kSplitVecNarrow
                                                                                   : split_vec;
         const int seed_sl = seed_slice_count(K, xb_host, b.fine_mode != 0);
+        // seeding slices: split_vec rows, or the index's seed_rows (at least 512, so that no
+        // slice is empty) when its rows within a cluster put the best seeds first
+        const int split_vec_a =
+            ix->seed_rows > 0 ? std::max(512, std::min(split_vec, (int)ix->seed_rows)) : split_vec;
         {
             const int nblk = (2 * ix->nlist + kBlock - 1) / kBlock;  // <= kBlock (kMaxBatchedNlist)
             unit_scan_local_kernel<<<nblk, kBlock, 0, st>>>(w.seg_off, ix->cluster_vec_off,
                                                             ix->nlist, b.unit_q, seed_all, seed_sl,
-                                                            split_vec, split_vec_b, w.unit_off, w.grp_off,
+                                                            split_vec_a, split_vec_b, w.unit_off, w.grp_off,
                                                             w.blk_tot);
             if ((rc = check_launch("unit_scan_local_kernel"))) return rc;
             unit_scan_carry_kernel<<<nblk, kBlock, 0, st>>>(ix->nlist, w.blk_tot, nblk,
@@ -1305,7 +1311,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         }
         unit_fill_kernel<<<(unsigned)std::min<int64_t>((w.max_units + 255) / 256, 2048), 256, 0,
                            st>>>(w.seg_off, ix->cluster_vec_off, ix->nlist, b.unit_q, seed_all,
-                                 split_vec, split_vec_b, w.unit_off, w.units, (int)w.max_units, w.grp_off,
+                                 split_vec_a, split_vec_b, w.unit_off, w.units, (int)w.max_units, w.grp_off,
                                  w.groups, (int)w.max_groups);
         if ((rc = check_launch("unit_fill_kernel"))) return rc;
         if ((rc = launch_pair_prep(b, st))) return rc;

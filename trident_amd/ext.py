@@ -163,7 +163,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
                     eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
                     cent_band=None, r_vec_sorted=None, fine_codes=None, fine_qp=None,
-                    cluster_bounds=None, vec_cn=None) -> TridentIndexView:
+                    cluster_bounds=None, vec_cn=None, seed_rows=0) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -189,6 +189,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.fine_qp = _ptr(fine_qp)
     v.cluster_bounds = _ptr(cluster_bounds)
     v.vec_cn = _ptr(vec_cn)
+    v.seed_rows = int(seed_rows)
     if cent_band is not None:
         rows, tiles, norms, nmax = cent_band
         v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
@@ -361,9 +362,11 @@ def launch_trident_v4_search(
     host_rows: Optional[torch.Tensor] = None,
     cluster_bounds: Optional[torch.Tensor] = None,
     vec_cn: Optional[torch.Tensor] = None,
+    seed_rows: int = 0,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
+    _need(int(seed_rows) >= 0, "seed_rows must be >= 0")
     _need(mode in (0, 1, 2, 10, 11), f"unknown mode {mode} (0, 1, 2, 10 or 11)")
     _need(int(rerank_m) >= 0, "rerank_m must be >= 0")
     sq8 = mode in (0, 1, 2)  # modes reading the SQ8 codes
@@ -495,7 +498,8 @@ def launch_trident_v4_search(
         blk_bounds4=blk_bounds4, vec_Ar=vec_Ar if mode == 2 else None,
         sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted,
         fine_codes=fine_codes if mode == 2 else None, fine_qp=fine_qp if mode == 2 else None,
-        cluster_bounds=cluster_bounds if mode == 2 else None, vec_cn=vec_cn if mode == 2 else None)
+        cluster_bounds=cluster_bounds if mode == 2 else None, vec_cn=vec_cn if mode == 2 else None,
+        seed_rows=seed_rows)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route,

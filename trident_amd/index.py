@@ -56,6 +56,11 @@ def _as_tensor(x, device, dtype):
 # Slice length of the seeding pass's units on the narrow layout (kSplitVecNarrow in
 # csrc/kernels.hpp): the seeding pass scans the first slice of each seeding cluster.
 SEED_SLICE_ROWS = 2048
+# Rows per seeding slice for rows ordered by residual norm (TridentIndexView.seed_rows): on
+# histogram-like data with ~6,100 rows per cluster (configs[4]'s shape) the first 1024 rows of a
+# cluster seed a threshold 1.044x the K-th distance within the whole cluster (seed_order_scores)
+# against 1.032x for 2048 rows, and the seeding pass reads half the codes.
+SEED_ROWS_RESIDUAL = 1024
 
 
 def seed_order_scores(xb, lid: torch.Tensor, r: torch.Tensor, nlist: int, sv: int = SEED_SLICE_ROWS,
@@ -324,9 +329,11 @@ class SharedClusterStorage:
                     xb_raw=None, chunk_rows: int = 1 << 22):
         """Storage of an already sorted layout (a saved index): rows come from ``xb_sorted``
         ([N, D], e.g. a memmap) or, when it is None, from ``xb_raw[sort_perm]``; nothing is
-        re-sorted.  ``sort_perm`` [N] holds the original id of each sorted row."""
+        re-sorted.  ``sort_perm`` [N] holds the original id of each sorted row.  ``within`` is
+        "id" (set it to "residual" for a layout ordered by residual norm within clusters)."""
         self = cls.__new__(cls)
         self.dev = torch.device(device)
+        self.within, self.seed_scores = "id", None
         perm = np.ascontiguousarray(sort_perm, np.int64)
         voff = np.ascontiguousarray(vec_off, np.int64)
         self.N, self.nlist = int(perm.shape[0]), int(voff.shape[0]) - 1
@@ -715,7 +722,8 @@ class TridentV4Index:
             p_init=p_init,
             vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band,
             r_vec_sorted=self.r_vec_sorted, fine_codes=self.fine_codes, fine_qp=self.fine_qp,
-            host_rows=host_rows_buf, cluster_bounds=self.cluster_bounds, vec_cn=getattr(self, "vec_cn", None))
+            host_rows=host_rows_buf, cluster_bounds=self.cluster_bounds, vec_cn=getattr(self, "vec_cn", None),
+            seed_rows=self.seed_rows)
         return topk_d, topk_i, kern_ms
 
     def view(self):
@@ -733,7 +741,16 @@ class TridentV4Index:
             delta=self.delta_pad, eps_dim=self.eps_pad, blk_bounds4=self.blk_bounds4, vec_Ar=self.vec_Ar,
             sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted,
             fine_codes=self.fine_codes, fine_qp=self.fine_qp,
-            cluster_bounds=getattr(self, "cluster_bounds", None), vec_cn=getattr(self, "vec_cn", None))
+            cluster_bounds=getattr(self, "cluster_bounds", None), vec_cn=getattr(self, "vec_cn", None),
+            seed_rows=self.seed_rows)
+
+    @property
+    def seed_rows(self) -> int:
+        """Rows per seeding slice the batched route scans (TridentIndexView.seed_rows): with rows
+        ordered by residual norm within each cluster a cluster's first rows are its best seeds,
+        so SEED_ROWS_RESIDUAL of them seed almost as tight a threshold as SEED_SLICE_ROWS; 0
+        (the library's 2048-row slices) for the id order."""
+        return SEED_ROWS_RESIDUAL if getattr(self.storage, "within", "id") == "residual" else 0
 
     def _fill_cluster_bounds(self):
         """The batched route's per-cluster constants (A_max, r_max, r_lo), once per index."""

@@ -100,6 +100,7 @@ def save_index(ix: TridentV4Index, path: str, include_base: bool = True, mean64=
     meta = {k: np.int64(getattr(ix, k)) for k in _SCALARS}
     meta.update(
         format=np.array(FORMAT), version=np.int64(VERSION),
+        within=np.array(getattr(st, "within", "id")),
         token=np.frombuffer(token, np.uint8).copy(),
         rot_sq_min=np.float64(ix.rot_sq_min), rot_sq_max=np.float64(ix.rot_sq_max),
         centroids=ix.centroids.cpu().numpy(),
@@ -234,6 +235,8 @@ def load_index(path: str, device="cuda:0", xb_placement: str = "device", xb_raw=
         xb_sorted = None
     st = SharedClusterStorage.from_sorted(xb_sorted, sort_perm, meta["vec_off"], device=dev,
                                           xb_placement=xb_placement, xb_raw=xb_raw)
+    # the row order within clusters (indexes saved before it was recorded are in id order)
+    st.within = str(meta["within"]) if "within" in meta else "id"
     ix = TridentV4Index.__new__(TridentV4Index)
     ix.storage, ix.dev = st, dev
     for k2, v in sc.items():
