@@ -377,11 +377,16 @@ def measure_variant(w, nprobe, K, mode, ub, route, steps, warmup, rounds, label=
            "pruning": {"candidates": stats[0], "survivors": stats[2], "refined_kept": stats[3]}}
     if w.xb_host:
         D = w.cfg["D"]
+        # the exact refines read the base's uint8 copy when it has one (the rescan of an
+        # overflowed candidate list reads float32 rows)
+        u8 = getattr(w.st, "xb_sorted_u8", None) is not None
+        rb = D if u8 else 4 * D
         out["pcie"] = {"host_rows_read": hrows[0], "seeding_pass_rows": hrows[1],
-                       "stage_z_rows": hrows[0] - hrows[1], "row_bytes": 4 * D,
-                       "bytes_per_query": round(hrows[0] * 4 * D / B, 1),
-                       "seeding_bytes_per_query": round(hrows[1] * 4 * D / B, 1),
-                       "stage_z_bytes_per_query": round((hrows[0] - hrows[1]) * 4 * D / B, 1)}
+                       "stage_z_rows": hrows[0] - hrows[1], "row_bytes": rb,
+                       "row_format": "uint8 copy of the float32 base" if u8 else "float32",
+                       "bytes_per_query": round(hrows[0] * rb / B, 1),
+                       "seeding_bytes_per_query": round(hrows[1] * rb / B, 1),
+                       "stage_z_bytes_per_query": round((hrows[0] - hrows[1]) * rb / B, 1)}
     log(f"{label} nprobe={nprobe} K={K} mode={mode} ub={ub}: {ms:.3f} ms/step, {B / ms * 1e3:,.0f} QPS; "
         f"exact ids {ex['ids_identical']}/{B}, distances {ex['distances_identical']}/{B}; "
         f"{roof['kernel'].split(' ')[0]} {roof['frac']:.3f} of peak in {roof['launch_ms']} ms")
@@ -456,7 +461,9 @@ def measure_primary(cfg_id, cfg, args, dev):
            "nprobe": nprobe, "K": K, "B": B, "N": N, "D": D, "nlist": cfg["nlist"],
            "row_order": getattr(w.st, "within", "id"),
            "hbm_footprint": ix.hbm_footprint(),
-           "host_bytes": int(w.st.xb_sorted.numel() * 4) if w.xb_host else 0}
+           "host_bytes": (int(w.st.xb_sorted.numel() * 4) + (0 if getattr(w.st, "xb_sorted_u8", None) is None
+                                                             else int(w.st.xb_sorted_u8.numel())))
+                         if w.xb_host else 0}
     if w.xb_host:
         out["out_of_core"] = dict(v["pcie"], fine_level=ix.fine_codes is not None,
                                   pass_b_survivors=surv, stage_z_ms=round(stage["pass2_merge_ms"], 4))
@@ -494,6 +501,17 @@ def measure_primary(cfg_id, cfg, args, dev):
                 f"({sec * 1e3 / nb:.3f} ms per batch of {B}), results identical {same}")
         out["pipelined_from_host"] = dict(batches=nb, batch=B, **pipe_out)
         out["two_streams_resident"] = two_streams_resident(w, nprobe, K, mode, ub, args.route, nb, gpu_d, gpu_i)
+
+    if w.xb_host and mode == 2 and getattr(w.st, "xb_sorted_u8", None) is not None:
+        # the same search with every exact refine reading the float32 rows (uint8 copy unset)
+        u8_saved = w.st.xb_sorted_u8
+        w.st.xb_sorted_u8 = None
+        try:
+            sv, _ = measure_variant(w, nprobe, K, mode, ub, args.route, args.extra_steps, 3, 2,
+                                    label=f"cfg{cfg_id} float32 refine rows")
+        finally:
+            w.st.xb_sorted_u8 = u8_saved
+        out["float32_refine_rows"] = sv
 
     if args.sweep:
         sweep = {}
@@ -636,7 +654,8 @@ def main():
                    "route": ("batched" if r["route"] == _lib.ROUTE_BATCHED else "pair") if args.mode == 2 else "cm_exact",
                    "ub_seed": args.ub, "p_init": r["p_init"], "tile_size": cfg["T"], "row_order": r["row_order"],
                    "parallelism": "single GPU",
-                   "xb_placement": "host (mapped, out of core)" if cfg["host"] else "device"},
+                   "xb_placement": "host (mapped, out of core)" if cfg["host"] else "device",
+                   "host_rows": (r["out_of_core"]["row_format"] if "out_of_core" in r else None)},
         "roofline": roof,
         "cpu_baseline": r["cpu"],
         "rounds": {"n": len(r["round_qps"]), "qps_mean": round(statistics.mean(r["round_qps"]), 1),
@@ -654,6 +673,8 @@ def main():
     extra = {}
     if "sq8_only" in r:
         extra[f"cfg{args.cfg}_sq8_only"] = r["sq8_only"]
+    if "float32_refine_rows" in r:
+        extra[f"cfg{args.cfg}_float32_refine_rows"] = r["float32_refine_rows"]
     if args.cfg == 5 and not args.no_extra:
         cids = [int(c) for c in args.extra_cfgs.split(",") if c.strip()]
         extra["configs"] = measure_sweeps(args, dev, cids)

@@ -123,6 +123,13 @@ typedef struct TridentIndexView {
      * rounding up to 64), for an index whose rows within a cluster are ordered by residual norm,
      * so that a cluster's first rows are its best seeds.  Results do not depend on it. */
     int32_t seed_rows;
+    /* The rows of xb_sorted as uint8 (optional; no counterpart in the reference): [N, D], for a
+     * base whose every value is an integer in [0, 255] (the float32 values exactly), in the same
+     * kind of memory as xb_sorted; needs D a multiple of 16 and a 16-byte aligned pointer.  The
+     * batched route's and mode 10's exact refines (seeds and Stage Z) read these rows instead of
+     * xb_sorted's: the same distances from a quarter of the bytes, which for a base in mapped
+     * host memory are the bytes crossing PCIe.  NULL: every refine reads xb_sorted. */
+    const uint8_t* xb_sorted_u8;
 } TridentIndexView;
 
 /* How modes 2 and 10 are executed.  Both routes are exact; they differ in speed only.  Mode 10

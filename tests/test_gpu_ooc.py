@@ -97,6 +97,44 @@ def test_fine_mode_is_exact_and_refines_fewer_rows(host_sets, dev, name):
         assert kept[True] <= kept[False] and rows[True] < rows[False], (rows, kept)
 
 
+def test_uint8_copy_of_the_host_base(dev):
+    """A host base of integers in [0, 255] (D a multiple of 16) gets an exact uint8 copy that
+    the exact refines (seeds, Stage Z; batched route and mode 10) read instead of its float32
+    rows: results equal the oracle's and the same index's without the copy, from the same host
+    rows (128 instead of 512 bytes each).  Non-integer values, values past 255 and D not a
+    multiple of 16 get no copy."""
+    xb, xq = datagen.cfg2(N=30_000, D=128, B=500, n_centers=48, seed=95)
+    b = build_index(xb, 48, dev, xb_placement="host", max_batch=512)
+    st = b.ix.storage
+    try:
+        assert st.xb_sorted_u8 is not None
+        assert torch.equal(st.xb_sorted_u8.to(torch.float32), st.xb_sorted)
+        q = _q(xq.numpy(), dev)
+        for K, nprobe, mode in ((10, 16, 2), (64, 8, 2), (10, 16, 10)):
+            _, rd, ri = oracle_search(b, xq.numpy(), nprobe, K)
+            rows = {}
+            for u8 in (True, False):
+                saved = st.xb_sorted_u8
+                if not u8:
+                    st.xb_sorted_u8 = None
+                hr = torch.zeros(2, dtype=torch.int64, device=dev)
+                d, i, _ = b.ix.search(q, nprobe, mode=mode, k=K, route=2, host_rows_buf=hr)
+                torch.cuda.synchronize()
+                st.xb_sorted_u8 = saved
+                assert_exact(d.cpu().numpy(), i.cpu().numpy(), rd, ri, f"u8={u8} K={K} mode={mode}")
+                rows[u8] = int(hr[0])
+            assert rows[True] == rows[False] > 0, rows
+    finally:
+        st._host_buf.free()
+    assert st.xb_sorted_u8 is None and st.xb_sorted is None
+    for xb2 in (datagen.cfg1(N=3000, D=128, B=8, n_centers=8, seed=96)[0],   # not integers
+                datagen.cfg2(N=3000, D=128, B=8, n_centers=8, seed=97)[0] * 2,  # past 255
+                datagen.cfg2(N=3000, D=72, B=8, n_centers=8, seed=98)[0]):      # D % 16 != 0
+        b2 = build_index(xb2, 8, dev, xb_placement="host", max_batch=8)
+        assert b2.ix.storage.xb_sorted_u8 is None
+        b2.ix.storage._host_buf.free()
+
+
 def test_host_rows_is_zero_for_a_device_base(dev):
     xb, xq = datagen.cfg2(N=20_000, D=64, B=200, n_centers=32, seed=94)
     b = build_index(xb, 32, dev, max_batch=256)

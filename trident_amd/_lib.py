@@ -37,7 +37,7 @@ class TridentIndexView(ctypes.Structure):
         ("sq8_cells", _P),
         ("cent_rows", _P), ("cent_tiles", _P), ("cent_norms", _P), ("cent_norm_max", _f64),
         ("r_vec_sorted", _P), ("fine_codes", _P), ("fine_qp", _P), ("cluster_bounds", _P),
-        ("vec_cn", _P), ("seed_rows", _i32),
+        ("vec_cn", _P), ("seed_rows", _i32), ("xb_sorted_u8", _P),
     ]
 
 

@@ -452,7 +452,7 @@ __global__ __launch_bounds__(256) void refine_survivors_kernel(BatchArgs a, int 
             if (need) s_pos[wid][rk] = pos;
             wave_sync();
             double acc = 0.0;
-            if (nq > 0) acc = refine_rows(a.xb, D, s_pos[wid], nq, s_stage[wid], s_q64[wid]);
+            if (nq > 0) acc = refine_rows(a.xb, a.xb8, D, s_pos[wid], nq, s_stage[wid], s_q64[wid]);
             if (a.host_rows && lane == 0 && nq > 0) atomicAdd(a.host_rows, (unsigned long long)nq);
             wave_sync();
             const double d = shfl_f64(acc, rk);
@@ -1424,7 +1424,7 @@ __global__ __launch_bounds__(256) void ub_kth_kernel(BatchArgs a) {
                 const int nr = min(kWave, K - h * kWave);
                 dv[h] = 0.0;
                 if (nr > 0) {
-                    dv[h] = refine_rows(a.xb, a.D, s_pos[wid] + h * kWave, nr, s_stage[wid],
+                    dv[h] = refine_rows(a.xb, a.xb8, a.D, s_pos[wid] + h * kWave, nr, s_stage[wid],
                                             s_q64[wid]);
                     if (lane < nr) mx = fmax(mx, dv[h]);
                 }

@@ -261,6 +261,9 @@ int validate_index(const TridentIndexView* ix) {
                     ix->D_pad, ix->D);
     if (ix->seed_rows < 0)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "seed_rows=%d must be >= 0", ix->seed_rows);
+    if (ix->xb_sorted_u8 && (ix->D % 16 != 0 || (reinterpret_cast<uintptr_t>(ix->xb_sorted_u8) & 15) != 0))
+        return fail(TRIDENT_ERR_INVALID_ARGUMENT,
+                    "xb_sorted_u8 needs D a multiple of 16 (D=%d) and a 16-byte aligned pointer", ix->D);
     if (ix->tile_size < 64 || ix->tile_size % 64 != 0)
         return fail(TRIDENT_ERR_INVALID_ARGUMENT, "tile_size=%d must be a positive multiple of 64",
                     ix->tile_size);
@@ -1106,6 +1109,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         BatchArgs b{};
         b.vec_off = ix->cluster_vec_off;
         b.xb = ix->xb_sorted;
+        b.xb8 = ix->xb_sorted_u8;
         b.orig_ids = ix->orig_ids_sorted;
         b.D = ix->D;
         b.D_pad = ix->D_pad;
@@ -1222,6 +1226,7 @@ int trident_search(const TridentIndexView* ix, const TridentSearchParams* sp, co
         b.tile_off = ix->cluster_tile_off;
         b.vec_off = ix->cluster_vec_off;
         b.xb = ix->xb_sorted;
+        b.xb8 = ix->xb_sorted_u8;
         b.vmin = ix->vmin;
         b.delta = ix->delta;
         b.eps = ix->eps_dim;

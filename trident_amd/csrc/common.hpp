@@ -307,7 +307,10 @@ static_assert(kStageRows * (kStageDims + 1) <= kStageCh * (kWave + 1), "staging 
 // (row stride 129 floats: the lanes' reads of their rows fall in distinct banks).  Whole
 // 512-byte runs in flight matter for a base in mapped host memory: random rows cross PCIe at
 // ~51 GB/s read this way against ~40 GB/s as 128-byte pieces one 32-dim chunk at a time.
-__device__ __forceinline__ double refine_rows(const float* __restrict__ xb, int D,
+// With xb8 (the same rows as uint8, exact; D a multiple of 16, rows 16-byte aligned) the rows
+// are read from it instead: 128 bytes per 128 dims, converted to float32 exactly when staged.
+__device__ __forceinline__ double refine_rows(const float* __restrict__ xb,
+                                              const uint8_t* __restrict__ xb8, int D,
                                               const int32_t* q_spos, int nq,
                                               float (*stage)[kWave + 1],
                                               const double* s_q64) {
@@ -322,7 +325,30 @@ __device__ __forceinline__ double refine_rows(const float* __restrict__ xb, int 
         const bool mine = lane >= g0 && lane < g0 + ng;
         for (int d0 = 0; d0 < D; d0 += kStageDims) {
             const int ch = min(kStageDims, D - d0);
-            if (vec4) {
+            if (xb8) {
+                // the group's rows as 16-byte pieces (16 dims each, ch / 16 per row), two per
+                // lane: piece j = lane + 64 m is piece j % per of row j / per; pieces past the
+                // group's rows reload its last row and are not staged
+                const int per = ch >> 4;
+                uint4 v8[2];
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const int j = lane + kWave * m, r = j / per, p = j - r * per;
+                    v8[m] = *reinterpret_cast<const uint4*>(
+                        xb8 + (size_t)q_spos[g0 + min(r, ng - 1)] * D + d0 + 16 * p);
+                }
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    const int j = lane + kWave * m, r = j / per, p = j - r * per;
+                    if (r < ng) {
+                        float* dst = st + r * RS + 16 * p;
+                        const uint32_t w4[4] = {v8[m].x, v8[m].y, v8[m].z, v8[m].w};
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            dst[e] = (float)((w4[e >> 2] >> (8 * (e & 3))) & 0xffu);
+                    }
+                }
+            } else if (vec4) {
                 // lane (half, kk): float4 kk of rows g0 + 2 k + half; rows past the group and
                 // float4s past the chunk reload the last ones (never staged)
                 const int c4 = min(kk, (ch >> 2) - 1);

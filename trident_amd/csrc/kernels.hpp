@@ -133,6 +133,8 @@ struct BatchArgs {
     const int32_t* tile_off;
     const int32_t* vec_off;
     const float* xb;
+    const uint8_t* xb8;         // [N, D] the rows of xb as uint8 (exact), or null: read by the
+                                // exact refines instead of xb (a quarter of the bytes)
     const float* vmin;
     const float* delta;
     const float* eps;           // per-dim |x_rot - x_hat| bound (bounds r_x for the f32 slack)

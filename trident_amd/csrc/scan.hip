@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void pair_scan_kernel(ScanArgs a) {
     float(*my_stage)[kWave + 1] = s_stage[wid];
 
     auto flush = [&](int cnt) {
-        const double d64 = refine_rows(a.xb, D, my_qspos, cnt, my_stage, s_q64);
+        const double d64 = refine_rows(a.xb, nullptr, D, my_qspos, cnt, my_stage, s_q64);
         if (a.host_rows && lane == 0) atomicAdd(a.host_rows, (unsigned long long)cnt);
         const bool ok = lane < cnt && d64 <= thr;
         if (a.stats) st_ins += __popcll(__ballot(ok));
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(256) void rerank_kernel(RerankArgs a) {
     s_spos[wid][lane] = spos;
     wave_sync();
     double d64 = 0.0;
-    if (nv > 0) d64 = refine_rows(a.xb, a.D, s_spos[wid], nv, s_stage[wid], s_q64);
+    if (nv > 0) d64 = refine_rows(a.xb, nullptr, a.D, s_spos[wid], nv, s_stage[wid], s_q64);
     if (a.host_rows && lane == 0 && nv > 0) atomicAdd(a.host_rows, (unsigned long long)nv);
     WaveList<KO> L;
     L.init();

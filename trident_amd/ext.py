@@ -163,7 +163,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
                     cluster_tile_off, cluster_vec_off, xb_sorted, orig_ids_sorted, vmin, delta,
                     eps_dim, blk_bounds4, vec_Ar=None, sq8_cells=None,
                     cent_band=None, r_vec_sorted=None, fine_codes=None, fine_qp=None,
-                    cluster_bounds=None, vec_cn=None, seed_rows=0) -> TridentIndexView:
+                    cluster_bounds=None, vec_cn=None, seed_rows=0, xb_sorted_u8=None) -> TridentIndexView:
     v = TridentIndexView()
     v.N, v.D, v.D_pad, v.nlist = int(N), int(D), int(D_pad), int(nlist)
     v.tile_size = int(tile_size)
@@ -190,6 +190,7 @@ def make_index_view(*, N, D, D_pad, nlist, tile_size, per_cluster_sq8, W_combine
     v.cluster_bounds = _ptr(cluster_bounds)
     v.vec_cn = _ptr(vec_cn)
     v.seed_rows = int(seed_rows)
+    v.xb_sorted_u8 = device_pointer(xb_sorted_u8) if xb_sorted_u8 is not None else None
     if cent_band is not None:
         rows, tiles, norms, nmax = cent_band
         v.cent_rows, v.cent_tiles, v.cent_norms = _ptr(rows), _ptr(tiles), _ptr(norms)
@@ -363,6 +364,7 @@ def launch_trident_v4_search(
     cluster_bounds: Optional[torch.Tensor] = None,
     vec_cn: Optional[torch.Tensor] = None,
     seed_rows: int = 0,
+    xb_sorted_u8: Optional[torch.Tensor] = None,
 ):
     """Batched lossless IVF search; signature of the reference extension (see module doc)."""
     mode, nprobe = int(mode), int(nprobe)
@@ -438,6 +440,10 @@ def launch_trident_v4_search(
     if vec_cn is not None:
         _check_tensor("vec_cn", vec_cn, torch.float32, dev, 1)
         _need(vec_cn.numel() == N, f"vec_cn must hold N={N} floats")
+    if xb_sorted_u8 is not None:
+        _check_tensor("xb_sorted_u8", xb_sorted_u8, torch.uint8, dev, 2, allow_host=True)
+        _need(tuple(xb_sorted_u8.shape) == (N, D) and D % 16 == 0,
+              "xb_sorted_u8 must be [N, D] uint8 with D a multiple of 16")
     if sq8_cells is not None:
         _check_tensor("sq8_cells", sq8_cells, torch.int32, dev)
         _need(sq8_cells.numel() == tiles * (D_pad // 16) * int(tile_size) * 4,
@@ -499,7 +505,7 @@ def launch_trident_v4_search(
         sq8_cells=sq8_cells if mode == 2 else None, cent_band=cent_band, r_vec_sorted=r_vec_sorted,
         fine_codes=fine_codes if mode == 2 else None, fine_qp=fine_qp if mode == 2 else None,
         cluster_bounds=cluster_bounds if mode == 2 else None, vec_cn=vec_cn if mode == 2 else None,
-        seed_rows=seed_rows)
+        seed_rows=seed_rows, xb_sorted_u8=xb_sorted_u8 if mode in (2, 10) else None)
     ub = env_ub_seed() if ub_seed is None else int(ub_seed)
     return search_view(view, xq_orig, nprobe, topk_d, topk_i, mode=mode, ub_seed=ub,
                        use_l1=int(use_l1), p_init=p_init, route=route,

@@ -232,7 +232,8 @@ class PinnedHostBuffer:
     """
 
     def __init__(self, shape, dtype=torch.float32, owner=None):
-        self._owner = owner  # object whose xb_sorted is this buffer's tensor (cleared by free)
+        self._owner = owner  # object whose xb_sorted / xb_sorted_u8 is this buffer's tensor
+        self.children = []   # buffers freed with this one
         nbytes = int(np.prod(shape)) * torch.empty(0, dtype=dtype).element_size()
         ptr = ctypes.c_void_p()
         _lib.check(_lib.lib().trident_host_alloc_mapped(ctypes.c_size_t(max(nbytes, 1)), ctypes.byref(ptr)),
@@ -248,9 +249,13 @@ class PinnedHostBuffer:
         """Releases the host memory.  The owning storage's ``xb_sorted`` (a view of it) is
         cleared first, so nothing keeps a tensor over freed memory; every search using that
         storage must have completed (synchronise its stream before freeing)."""
+        for c in self.children:
+            c.free()
+        self.children = []
         if self._ptr:
-            if self._owner is not None and getattr(self._owner, "xb_sorted", None) is self.tensor:
-                self._owner.xb_sorted = None
+            for attr in ("xb_sorted", "xb_sorted_u8"):
+                if self._owner is not None and getattr(self._owner, attr, None) is self.tensor:
+                    setattr(self._owner, attr, None)
             self.tensor = None
             _lib.lib().trident_host_free(ctypes.c_void_p(self._ptr))
             self._ptr = None
@@ -260,7 +265,12 @@ class SharedClusterStorage:
     """Cluster-sorted base (reference benchmarks/phase4a_suite.py:75-92).
 
     ``xb_placement="device"`` keeps the FP32 base in HBM; ``"host"`` puts it in device-mapped
-    pinned host memory (the out-of-core mode) while ids and offsets stay on the device.
+    pinned host memory (the out-of-core mode) while ids and offsets stay on the device.  With
+    ``host_u8`` (the default) a host base whose every value is an integer in [0, 255] (u8
+    descriptors such as SIFT / BIGANN stored as float32) and D a multiple of 16 also gets an
+    exact uint8 copy in host memory, ``xb_sorted_u8`` (N * D more bytes, freed with the base):
+    the exact refines read their rows from it, a quarter of the PCIe bytes for the same
+    distances.
 
     Within a cluster, rows follow one of two orders; search results do not depend on it, but
     the seeding pass scans the first slice of each seeding cluster, so the order decides how
@@ -279,7 +289,7 @@ class SharedClusterStorage:
     """
 
     def __init__(self, xb_raw, list_ids, r_vec, nlist: int, device="cuda:0", xb_placement: str = "device",
-                 within: str = "auto"):
+                 within: str = "auto", host_u8: bool = True):
         self.dev = torch.device(device)
         lid = _as_tensor(list_ids, self.dev, torch.int64)
         self.N = int(lid.numel())
@@ -307,12 +317,17 @@ class SharedClusterStorage:
         if xb_placement == "host":
             self._host_buf = PinnedHostBuffer((self.N, self.D), torch.float32, owner=self)
             self.xb_sorted = self._host_buf.tensor
+            u8 = self._u8_start(host_u8)
             step = 1 << 22
             perm_cpu = sort_perm.cpu()
             for s in range(0, self.N, step):
                 idx = perm_cpu[s:s + step]
-                self.xb_sorted[s:s + step] = xb[idx.to(xb.device)].to("cpu", torch.float32)
+                rows = xb[idx.to(xb.device)]
+                u8 = self._u8_put(u8, s, rows)
+                self.xb_sorted[s:s + step] = rows.to("cpu", torch.float32)
+            self._u8_finish(u8)
         else:
+            self.xb_sorted_u8 = None
             self.xb_sorted = xb.to(self.dev, torch.float32)[sort_perm].contiguous()
         self.orig_ids_sorted = sort_perm.to(torch.int32).contiguous()
         counts = torch.bincount(lid, minlength=nlist).to(torch.int32)
@@ -324,9 +339,35 @@ class SharedClusterStorage:
         self.list_ids_sorted = lid[sort_perm].to(torch.int32).contiguous()
         self.r_vec_sorted = None if r_vec is None else _as_tensor(r_vec, self.dev, torch.float32)[sort_perm].contiguous()
 
+    def _u8_start(self, host_u8: bool):
+        """The buffer of the base's uint8 copy (xb_sorted_u8), or None: kept for a base in host
+        memory with D a multiple of 16 while every value is an integer in [0, 255]."""
+        self.xb_sorted_u8 = None
+        if not host_u8 or self.placement != "host" or self.D % 16 != 0 or self.N == 0:
+            return None
+        return PinnedHostBuffer((self.N, self.D), torch.uint8, owner=self)
+
+    @staticmethod
+    def _u8_put(buf, s: int, rows: torch.Tensor):
+        """Writes sorted rows [s, s + len(rows)) into the uint8 copy; at the first value that
+        uint8 does not hold exactly the copy is freed (returns None)."""
+        if buf is None:
+            return None
+        r = rows.to(torch.float32)
+        if not bool(((r >= 0) & (r <= 255) & (r == torch.round(r))).all()):
+            buf.free()
+            return None
+        buf.tensor[s:s + r.shape[0]] = r.to(torch.uint8).cpu()
+        return buf
+
+    def _u8_finish(self, buf):
+        if buf is not None:
+            self._host_buf.children.append(buf)  # freed with the FP32 base
+            self.xb_sorted_u8 = buf.tensor
+
     @classmethod
     def from_sorted(cls, xb_sorted, sort_perm, vec_off, device="cuda:0", xb_placement: str = "device",
-                    xb_raw=None, chunk_rows: int = 1 << 22):
+                    xb_raw=None, chunk_rows: int = 1 << 22, host_u8: bool = True):
         """Storage of an already sorted layout (a saved index): rows come from ``xb_sorted``
         ([N, D], e.g. a memmap) or, when it is None, from ``xb_raw[sort_perm]``; nothing is
         re-sorted.  ``sort_perm`` [N] holds the original id of each sorted row.  ``within`` is
@@ -346,6 +387,7 @@ class SharedClusterStorage:
             self.xb_sorted = self._host_buf.tensor
         else:
             self.xb_sorted = torch.empty((self.N, self.D), device=self.dev, dtype=torch.float32)
+        u8 = self._u8_start(host_u8)
         for s in range(0, self.N, chunk_rows):
             e = min(self.N, s + chunk_rows)
             if xb_sorted is not None:
@@ -353,7 +395,9 @@ class SharedClusterStorage:
             else:
                 xr = xb_raw if isinstance(xb_raw, torch.Tensor) else torch.as_tensor(np.asarray(xb_raw))
                 rows = xr[torch.as_tensor(perm[s:e]).to(xr.device)].to(torch.float32)
+            u8 = self._u8_put(u8, s, rows)
             self.xb_sorted[s:e] = rows.to(self.xb_sorted.device)
+        self._u8_finish(u8)
         self.orig_ids_sorted = torch.as_tensor(perm.astype(np.int32)).to(self.dev)
         self.cluster_vec_off = torch.as_tensor(voff.astype(np.int32)).to(self.dev)
         counts = (voff[1:] - voff[:-1]).astype(np.int32)
@@ -723,7 +767,7 @@ class TridentV4Index:
             vec_Ar=self.vec_Ar, route=route, sq8_cells=self.sq8_cells, cent_band=self.cent_band,
             r_vec_sorted=self.r_vec_sorted, fine_codes=self.fine_codes, fine_qp=self.fine_qp,
             host_rows=host_rows_buf, cluster_bounds=self.cluster_bounds, vec_cn=getattr(self, "vec_cn", None),
-            seed_rows=self.seed_rows)
+            seed_rows=self.seed_rows, xb_sorted_u8=getattr(st, "xb_sorted_u8", None))
         return topk_d, topk_i, kern_ms
 
     def view(self):
@@ -742,7 +786,7 @@ class TridentV4Index:
             sq8_cells=self.sq8_cells, cent_band=self.cent_band, r_vec_sorted=self.r_vec_sorted,
             fine_codes=self.fine_codes, fine_qp=self.fine_qp,
             cluster_bounds=getattr(self, "cluster_bounds", None), vec_cn=getattr(self, "vec_cn", None),
-            seed_rows=self.seed_rows)
+            seed_rows=self.seed_rows, xb_sorted_u8=getattr(st, "xb_sorted_u8", None))
 
     @property
     def seed_rows(self) -> int:
