@@ -502,7 +502,7 @@ def measure_primary(cfg_id, cfg, args, dev):
         out["pipelined_from_host"] = dict(batches=nb, batch=B, **pipe_out)
         out["two_streams_resident"] = two_streams_resident(w, nprobe, K, mode, ub, args.route, nb, gpu_d, gpu_i)
 
-    if w.xb_host and mode == 2 and getattr(w.st, "xb_sorted_u8", None) is not None:
+    if w.xb_host and mode == 2 and not args.no_float32_rows and getattr(w.st, "xb_sorted_u8", None) is not None:
         # the same search with every exact refine reading the float32 rows (uint8 copy unset)
         u8_saved = w.st.xb_sorted_u8
         w.st.xb_sorted_u8 = None
@@ -598,6 +598,8 @@ def main():
     ap.add_argument("--xb-device", action="store_true", help="FP32 base in HBM (cfg 5 defaults to host)")
     ap.add_argument("--no-extra", action="store_true", help="skip the config sweeps after cfg 5")
     ap.add_argument("--no-sq8-only", action="store_true", help="skip the SQ8-only out-of-core lines")
+    ap.add_argument("--no-float32-rows", action="store_true",
+                    help="skip the out-of-core line whose refines read float32 rows instead of the uint8 copy")
     ap.add_argument("--extra-cfgs", default="1,2,3,4", help="configs swept after cfg 5")
     ap.add_argument("--pipeline-batches", type=int, default=12,
                     help="batches of B host queries for the pipelined end-to-end line (0 = skip)")
